@@ -1,0 +1,267 @@
+"""Benchmark of the Q4_K GEMV op on one MI355X.
+
+Headline workload: the Mistral-7B FFN gate/up projection, Q4_K weight
+14336 x 4096 times one F32 activation column (batch 1) -- the shape the
+metric is quoted on.  One step = one q4k_mul_mat_vec_q call through the C ABI
+(F32 activation in, quantised to Q8_1 inside the launch, F32 out) on inputs
+already resident in HBM.  The weight rotates through copies totalling more
+than 1 GiB so every step streams it from HBM rather than from the 256 MB
+Infinity Cache.
+
+Timing: W untimed eager warm-up steps; the K timed steps are captured into one
+HIP graph (the way ggml launches decode), which is replayed once untimed and
+then once between two HIP events recorded on the stream the kernels run on.
+value = algorithmic bytes per step / seconds per step (GB/s); the roofline
+object prices the same bytes against the 8 TB/s HBM peak.  The CPU baseline is
+the oracle's restatement of ggml's CPU path (Q8_K activations +
+vec_dot_q4_K_q8_K, AVX2, a thread per core) timed on a bounded sample on the
+host cores of the same machine.
+
+--sweep prints one line per (workload, shape, ncols) of the five workloads
+instead of the headline JSON.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+METRIC = "Q4_K GEMV µs/call + achieved HBM GB/s (% of 8 TB/s), 14336x4096 b=1"
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_14336x4096_b1_traffic.txt")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(M: int, K: int, N: int) -> int:
+    """Bytes the fused op must move: the Q4_K weight once, the F32
+    activation once and the F32 result once."""
+    return M * (K // 256) * 144 + 4 * N * K + 4 * M * N
+
+
+def make_inputs(Q, M, K, N, seed=0):
+    import _common
+    W = _common.weights(M, K, seed)
+    wq = Q.quantize_rows_q4_K(W, nthreads=min(16, len(os.sched_getaffinity(0))))
+    del W
+    x = _common.activations(N, K, seed)
+    return wq, x
+
+
+class OpRunner:
+    """Pre-resolved ctypes call of q4k_mul_mat_vec_q over rotating weights."""
+
+    def __init__(self, Q, wq, x, min_pool_bytes=1 << 30):
+        import ctypes
+        import torch
+        self.Q = Q
+        self.dev = torch.device("cuda:0")
+        self.M, self.rb = wq.shape
+        self.K = self.rb // 144 * 256
+        self.N = x.shape[0]
+        w0 = torch.from_numpy(wq).to(self.dev)
+        self.ncopies = max(2, math.ceil(min_pool_bytes / wq.nbytes))
+        self.copies = [w0] + [w0.clone() for _ in range(self.ncopies - 1)]
+        self.x = torch.from_numpy(x).to(self.dev)
+        self.out = torch.empty((self.N, self.M), dtype=torch.float32, device=self.dev)
+        self.fn = Q.lib().q4k_mul_mat_vec_q
+        self.wptr = [ctypes.c_void_p(c.data_ptr()) for c in self.copies]
+        self.args = (self.K, self.M, self.rb, ctypes.c_void_p(self.x.data_ptr()), self.N, self.K * 4,
+                     ctypes.c_void_p(self.out.data_ptr()), self.M * 4, None, 0)
+        self.i = 0
+
+    def step(self, stream):
+        st = self.fn(self.wptr[self.i % self.ncopies], *self.args, stream)
+        self.i += 1
+        if st != 0:
+            raise self.Q.Q4KError(st, "q4k_mul_mat_vec_q")
+
+
+def time_gpu(runner: OpRunner, steps: int, warmup: int):
+    """Returns dict with graph-launched and eager seconds per step."""
+    import ctypes
+    import torch
+    stream = torch.cuda.Stream()
+    res = {}
+    with torch.cuda.stream(stream):
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        for _ in range(warmup):
+            runner.step(sp)
+        torch.cuda.synchronize()
+        # eager: K back-to-back launches from the host
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            runner.step(sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res["eager_s"] = e0.elapsed_time(e1) * 1e-3 / steps
+        # graph: the same K calls captured once, replayed
+        g = torch.cuda.CUDAGraph()
+        runner.i = 0
+        with torch.cuda.graph(g, stream=stream):
+            for _ in range(steps):
+                runner.step(sp)
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res["graph_s"] = e0.elapsed_time(e1) * 1e-3 / steps
+    return res
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 PMC summary."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(wq, x, target_s=12.0):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    if not os.path.exists(O.LIB_PATH):
+        O.build()
+    cores = min(16, len(os.sched_getaffinity(0)))
+    K = wq.shape[1] // 144 * 256
+    t1 = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, 2)
+    per = float(np.median(t1))
+    reps = int(max(3, min(5000, target_s / max(per, 1e-6))))
+    t = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, reps)
+    isa = "avx2" if O.lib().orc_cpu_has_avx2() else "scalar"
+    med = float(np.median(t))
+    M, N = wq.shape[0], x.shape[0]
+    return {"value": algorithmic_bytes(M, K, N) / med / 1e9, "unit": "GB/s", "cores": cores,
+            "kind": "port", "us_per_call": med * 1e6,
+            "sample": f"{reps} calls of the full {M}x{K} N={N} product (Q8_K quantisation + "
+                      f"vec_dot_q4_K_q8_K, {isa}, {cores} threads, row chunks of 16), "
+                      f"{float(np.sum(t)):.1f} s total, median reported"}
+
+
+def headline(args):
+    import torch
+    Q = _pkg()
+    M, K, N = 14336, 4096, 1
+    log(f"[bench] preparing {M}x{K} N={N} inputs")
+    wq, x = make_inputs(Q, M, K, N)
+    runner = OpRunner(Q, wq, x)
+    log(f"[bench] {runner.ncopies} weight copies ({runner.ncopies * wq.nbytes / 2**30:.2f} GiB); "
+        f"geometry {Q.geometry(K, M, N)}")
+    torch.cuda.synchronize()
+    t = time_gpu(runner, args.steps, args.warmup)
+    sec = t["graph_s"]
+    nbytes = algorithmic_bytes(M, K, N)
+    achieved = nbytes / sec / 1e9
+    log(f"[bench] graph {sec * 1e6:.2f} us/call ({achieved:.0f} GB/s), eager {t['eager_s'] * 1e6:.2f} us/call")
+    rec = {
+        "metric": METRIC, "value": round(achieved, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": sec * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4_K x q8_1: int8 dot4 -> int32, f32 scale/accumulate",
+        "data": "synthetic: W ~ N(0,0.02) -> Q4_K (quantize_row_q4_K_ref arithmetic), x ~ N(0,1); seed 0",
+        "config": {"workload": "mistral7b_ffn_gate_14336x4096_b1", "M": M, "K": K, "ncols": N,
+                   "launch": "hipGraph of the K timed calls", "weight_copies": runner.ncopies,
+                   "geometry": Q.geometry(K, M, N)},
+        "us_per_call": round(sec * 1e6, 3),
+        "us_per_call_eager": round(t["eager_s"] * 1e6, 3),
+        "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(), "algorithmic_bytes_per_launch": nbytes},
+    }
+    if not args.no_cpu:
+        log("[bench] CPU baseline (bounded sample)")
+        rec["cpu_baseline"] = cpu_baseline(wq, x)
+    print(json.dumps(rec), flush=True)
+
+
+def sweep(args):
+    import _common
+    import torch
+    Q = _pkg()
+    rows = []
+    seen = set()
+    for wl, items in _common.WORKLOADS.items():
+        for M, K, ns in items:
+            wq = None
+            for N in ns:
+                if (M, K, N) in seen:
+                    continue
+                seen.add((M, K, N))
+                if wq is None:
+                    log(f"[sweep] inputs {M}x{K}")
+                    wq, _ = make_inputs(Q, M, K, 1)
+                x = _common.activations(N, K, 0)
+                runner = OpRunner(Q, wq, x)
+                t = time_gpu(runner, args.steps, args.warmup)
+                sec = t["graph_s"]
+                gbs = algorithmic_bytes(M, K, N) / sec / 1e9
+                r = {"workload": wl, "M": M, "K": K, "N": N, "us_per_call": round(sec * 1e6, 3),
+                     "us_eager": round(t["eager_s"] * 1e6, 3), "GBps": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "geometry": Q.geometry(K, M, N)}
+                rows.append(r)
+                print(json.dumps(r), flush=True)
+                del runner
+                torch.cuda.empty_cache()
+
+
+def profile_mode(args):
+    """Only the GEMV launches of the headline workload (for rocprofv3)."""
+    import ctypes
+    import torch
+    Q = _pkg()
+    M, K, N = args.shape
+    wq, x = make_inputs(Q, M, K, N)
+    runner = OpRunner(Q, wq, x)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for _ in range(args.warmup + args.steps):
+        runner.step(s)
+    torch.cuda.synchronize()
+    log(f"[profile] {args.warmup + args.steps} launches of {M}x{K} N={N} done")
+
+
+def _pkg():
+    import _common
+    return _common.pkg()
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--profile", action="store_true", help="plain launches only, for rocprofv3")
+    ap.add_argument("--shape", type=int, nargs=3, default=[14336, 4096, 1], metavar=("M", "K", "N"))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(row sharding across GPUs is described in DESIGN.md); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.sweep:
+        sweep(args)
+    elif args.profile:
+        profile_mode(args)
+    else:
+        headline(args)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,205 @@
+"""Python binding of libq4k_gemv.so (the C ABI in include/q4k_gemv.h).
+
+The product is the C ABI; this module is plumbing for tests and the
+benchmark: it passes torch device tensors and torch's current HIP stream to
+the library and turns status codes into exceptions.  It never computes on the
+CPU: if the library is missing, loading it raises.
+
+torch is imported before the library is loaded so that the library binds to
+the HIP runtime torch already loaded (one runtime per process).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libq4k_gemv.so")
+
+Q4K_OK, Q4K_EUNSUPPORTED, Q4K_EINVAL, Q4K_EHIP, Q4K_ENOMEM = 0, 1, 2, 3, 4
+GGML_TYPE_F32, GGML_TYPE_Q8_1, GGML_TYPE_Q4_K = 0, 9, 12
+QK_K = 256
+BLOCK_Q4_K_BYTES = 144
+BLOCK_Q8_1_BYTES = 36
+MATRIX_ROW_PADDING = 512
+
+# Every symbol include/q4k_gemv.h declares: (restype, argtypes)
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+SIGNATURES = {
+    "q4k_version": (ctypes.c_int32, []),
+    "q4k_strerror": (ctypes.c_char_p, [_I]),
+    "q4k_last_hip_error": (ctypes.c_int32, []),
+    "q4k_q8_1_bytes": (ctypes.c_size_t, [_I64, _I64]),
+    "q4k_quantize_row_q8_1": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P]),
+    "q4k_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, ctypes.c_size_t, _P]),
+    "q4k_op_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "q4k_ggml_mul_mat_vec_q": (_I, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),
+    "q4k_subblock_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P]),
+    "q4k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
+    "q4k_quantize_rows_q4_K": (_I, [_P, _P, _I64, _I64, _I]),
+}
+
+
+class q4k_tensor(ctypes.Structure):
+    """The ggml_tensor subset of include/q4k_gemv.h."""
+    _fields_ = [("type", ctypes.c_int32), ("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_size_t * 4),
+                ("data", ctypes.c_void_p)]
+
+
+class Q4KError(RuntimeError):
+    def __init__(self, status: int, where: str):
+        self.status = status
+        msg = f"{where}: {lib().q4k_strerror(status).decode()} (status {status}"
+        if status == Q4K_EHIP:
+            msg += f", hipError {lib().q4k_last_hip_error()}"
+        super().__init__(msg + ")")
+
+
+_lib = None
+
+
+def lib():
+    """Loads libq4k_gemv.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        import torch  # noqa: F401  -- bind to torch's HIP runtime
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(status: int, where: str):
+    if status != Q4K_OK:
+        raise Q4KError(status, where)
+
+
+def _stream(stream=None):
+    """torch's current HIP stream (or `stream`); the null stream when no GPU
+    is visible, where only the host-side argument checks can run."""
+    import torch
+    if stream is None:
+        if not torch.cuda.is_available():
+            return None
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def pad_k(K: int) -> int:
+    return (K + MATRIX_ROW_PADDING - 1) // MATRIX_ROW_PADDING * MATRIX_ROW_PADDING
+
+
+def q8_1_bytes(K: int, ncols: int) -> int:
+    return int(lib().q4k_q8_1_bytes(K, ncols))
+
+
+# ------------------------------------------------------------------ host ----
+def quantize_rows_q4_K(w: np.ndarray, nthreads: int = 8) -> np.ndarray:
+    """Host F32 [M, K] -> Q4_K bytes [M, K/256*144]."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    M, K = w.shape
+    out = np.empty((M, K // QK_K * BLOCK_Q4_K_BYTES), dtype=np.uint8)
+    _check(lib().q4k_quantize_rows_q4_K(w.ctypes.data_as(_P), out.ctypes.data_as(_P), M, K, nthreads),
+           "q4k_quantize_rows_q4_K")
+    return out
+
+
+# ---------------------------------------------------------------- device ----
+def quantize_row_q8_1(x, K: int | None = None, out=None, stream=None):
+    """x: float32 cuda [N, K] (row = one activation column) -> uint8 cuda
+    [N, pad(K)/32*36] block_q8_1."""
+    import torch
+    N, Kx = x.shape
+    K = Kx if K is None else K
+    kp = pad_k(K)
+    if out is None:
+        out = torch.empty((N, kp // 32 * BLOCK_Q8_1_BYTES), dtype=torch.uint8, device=x.device)
+    _check(lib().q4k_quantize_row_q8_1(_ptr(x), _ptr(out), K, x.stride(0), kp, N, _stream(stream)),
+           "q4k_quantize_row_q8_1")
+    return out
+
+
+def mul_mat_vec_q(w_q, K: int, x, out=None, workspace=None, stream=None):
+    """ggml_cuda_mul_mat_vec_q: Q4_K [M, K/256*144] (uint8 cuda) x F32 [N, K]
+    -> F32 [N, M] (row c of the result = column c of ggml's dst)."""
+    import torch
+    M = w_q.shape[0]
+    N = x.shape[0]
+    if out is None:
+        out = torch.empty((N, M), dtype=torch.float32, device=x.device)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(lib().q4k_mul_mat_vec_q(_ptr(w_q), K, M, w_q.stride(0), _ptr(x), N, x.stride(0) * 4,
+                                   _ptr(out), out.stride(0) * 4, _ptr(workspace), ws_bytes,
+                                   _stream(stream)), "q4k_mul_mat_vec_q")
+    return out
+
+
+def op_mul_mat_vec_q(w_q, K: int, q8, ncols: int, row_low: int = 0, row_high: int | None = None,
+                     out=None, nrows_dst: int | None = None, stream=None):
+    """ggml_cuda_op_mul_mat_vec_q: rows [row_low, row_high) of a contiguous
+    Q4_K weight (w_q holds exactly those rows) x pre-quantised Q8_1 columns."""
+    import torch
+    if row_high is None:
+        row_high = row_low + w_q.shape[0]
+    rows = row_high - row_low
+    nrows_dst = rows if nrows_dst is None else nrows_dst
+    if out is None:
+        out = torch.empty((ncols, nrows_dst), dtype=torch.float32, device=q8.device)
+    padded = q8.shape[1] // BLOCK_Q8_1_BYTES * 32
+    _check(lib().q4k_op_mul_mat_vec_q(_ptr(w_q), K, row_low, row_high, _ptr(q8), ncols, padded,
+                                      _ptr(out), nrows_dst, _stream(stream)), "q4k_op_mul_mat_vec_q")
+    return out
+
+
+def make_tensor(type_id: int, ne, nb, data_ptr: int) -> q4k_tensor:
+    t = q4k_tensor()
+    t.type = type_id
+    for i in range(4):
+        t.ne[i] = ne[i] if i < len(ne) else 1
+    last = nb[-1] * (ne[len(nb) - 1] if len(nb) else 1)
+    for i in range(4):
+        t.nb[i] = nb[i] if i < len(nb) else last
+    t.data = data_ptr
+    return t
+
+
+def ggml_mul_mat_vec_q(src0: q4k_tensor, src1: q4k_tensor, dst: q4k_tensor, ids=None, fusion=None,
+                       workspace=None, stream=None) -> int:
+    """Descriptor form; returns the status (Q4K_EUNSUPPORTED means: fall back)."""
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    return int(lib().q4k_ggml_mul_mat_vec_q(ctypes.byref(src0), ctypes.byref(src1),
+                                            ctypes.byref(ids) if ids is not None else None,
+                                            ctypes.byref(dst), fusion, _ptr(workspace), ws_bytes,
+                                            _stream(stream)))
+
+
+def subblock_sums(w_q, K: int, q8, ncols: int, stream=None):
+    """Returns (sqq int32 [N, M, K/32], sq int32 [N, K/32]) on the device."""
+    import torch
+    M = w_q.shape[0]
+    sqq = torch.empty((ncols, M, K // 32), dtype=torch.int32, device=q8.device)
+    sq = torch.empty((ncols, K // 32), dtype=torch.int32, device=q8.device)
+    _check(lib().q4k_subblock_sums(_ptr(w_q), K, M, w_q.stride(0), _ptr(q8), ncols,
+                                   q8.shape[1] // BLOCK_Q8_1_BYTES, _ptr(sqq), _ptr(sq),
+                                   _stream(stream)), "q4k_subblock_sums")
+    return sqq, sq
+
+
+def geometry(K: int, M: int, N: int) -> dict:
+    out = (ctypes.c_int32 * 6)()
+    _check(lib().q4k_gemv_geometry(K, M, N, ctypes.cast(out, _P)), "q4k_gemv_geometry")
+    keys = ("rows_per_tile", "waves_per_wg", "workgroups", "lds_bytes", "cols_per_launch", "fused")
+    return dict(zip(keys, list(out)))

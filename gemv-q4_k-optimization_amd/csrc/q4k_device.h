@@ -1,0 +1,190 @@
+// q4k_device.h -- device building blocks of the gfx950 Q4_K GEMV.
+//
+// Wave64 lane map used by every kernel here.  A wave consumes one "group" of
+// 8 consecutive Q4_K super-blocks of one weight row per load instruction:
+//
+//   lane = 8*g + p        g = block within the group (0..7)
+//                         p = 16-byte part of the block's 128 qs bytes (0..7)
+//   qs bytes [16p, 16p+16) of block kb = 8*i + g
+//     low  nibbles -> elements 64*(p/2) + 16*(p%2) + [0,16)      (sub-block 2*(p/2))
+//     high nibbles -> elements 64*(p/2) + 32 + 16*(p%2) + [0,16) (sub-block 2*(p/2)+1)
+//
+// so the 64 lanes of a wave read 8 x 128 contiguous qs bytes (one 16-byte
+// load each, no idle lanes) and the 16-byte block header (d, dmin, scales)
+// once per lane with a second load that the 8 lanes of a block share.  The
+// nibble order and sub-block pairing are those of kernels/vecdotq.cuh:785-794;
+// the (sc, m) unpack is kernels/vecdotq.cuh:796-807 done with byte permutes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q4k {
+
+constexpr int kQK = 256;          // weights per super-block
+constexpr int kBlockBytes = 144;  // block_q4_K
+constexpr int kQ81Bytes = 36;     // block_q8_1
+constexpr int kWave = 64;
+constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that is always out of range
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// gfx9 buffer descriptor word 3: 32-bit data format, no swizzle.
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             kBufferWord3);
+}
+
+// 16-byte buffer load; offsets at or beyond the descriptor's size return 0.
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __builtin_bit_cast(float, dpp<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+constexpr int kDppXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppRor4 = 0x124;  // row_ror:4
+constexpr int kDppRor8 = 0x128;  // row_ror:8
+
+template <int XOR_MASK>
+__device__ __forceinline__ float swizzle_xor(float v) {
+    // ds_swizzle bit mode inside 32-lane halves: and_mask 0x1f, xor_mask
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (XOR_MASK << 10)));
+}
+
+// Sum over the 64 lanes; the result is wave-uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dppf<kDppXor1>(v);
+    v += dppf<kDppXor2>(v);
+    v += dppf<kDppRor4>(v);
+    v += dppf<kDppRor8>(v);
+    v += swizzle_xor<16>(v);
+    const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    return lo + hi;
+}
+
+// Per-lane constants of the scale/min unpack for sub-block pair jp = p/2.
+struct ScaleSel {
+    uint32_t sel_x;  // bytes (2j', 2j'+1) of scales[0..3] and of scales[4..7]
+    uint32_t sel_y;  // bytes (2j', 2j'+1) of scales[8..11], twice
+    bool high;       // jp >= 2: 4+2 bit split fields
+};
+
+__device__ __forceinline__ ScaleSel make_scale_sel(int jp) {
+    const uint32_t j = (uint32_t)(jp & 1) * 2u;
+    ScaleSel s;
+    s.sel_x = j | ((j + 1u) << 8) | ((j + 4u) << 16) | ((j + 5u) << 24);
+    s.sel_y = j | ((j + 1u) << 8) | (j << 16) | ((j + 1u) << 24);
+    s.high = jp >= 2;
+    return s;
+}
+
+// Header dwords: h[0] = d | dmin << 16, h[1..3] = scales[0..11].
+// Returns bytes {sc[2jp], sc[2jp+1], m[2jp], m[2jp+1]} (each 0..63).
+__device__ __forceinline__ uint32_t unpack_scale_min(u32x4 h, const ScaleSel &s) {
+    const uint32_t x = __builtin_amdgcn_perm(h[2], h[1], s.sel_x);
+    const uint32_t y = __builtin_amdgcn_perm(h[3], h[3], s.sel_y);
+    const uint32_t low = x & 0x3f3f3f3fu;
+    const uint32_t split = (y & 0x00000f0fu) | ((y >> 4) & 0x0f0f0000u) | ((x >> 2) & 0x30303030u);
+    return s.high ? split : low;
+}
+
+// The lane's 16 q4 x q8 products for each of its two sub-blocks.
+__device__ __forceinline__ void lane_qdot(u32x4 w, u32x4 alo, u32x4 ahi, int &sa, int &sb) {
+    int a = 0, b = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        a = __builtin_amdgcn_sdot4((int)(w[k] & 0x0f0f0f0fu), (int)alo[k], a, false);
+        b = __builtin_amdgcn_sdot4((int)((w[k] >> 4) & 0x0f0f0f0fu), (int)ahi[k], b, false);
+    }
+    sa = a;
+    sb = b;
+}
+
+__device__ __forceinline__ int byte_sum16(u32x4 a) {
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s = __builtin_amdgcn_sdot4((int)a[k], 0x01010101, s, false);
+    return s;
+}
+
+// ------------------------------------------------------------------------
+// Activation staging into LDS: q8[c*K + e] (int8) and d8[c*K/32 + b] (f32).
+// ------------------------------------------------------------------------
+
+// F32 activation -> Q8_1 values with ggml-cuda's quantize_q8_1 arithmetic
+// (call site kernels/mmvq.cu:734): per 32 values d = amax/127,
+// q = amax == 0 ? 0 : roundf(x/d), and the kernel consumes half(d).
+// Four lanes per 32-value block, 8 values per lane.
+__device__ __forceinline__ void stage_from_f32(const float *__restrict__ x, int64_t ldx, int K,
+                                               int ncols, bool vec_ok, int8_t *q8s, float *d8s) {
+    const int nblk = K / 32;
+    const int total = ncols * nblk;
+    const int quarter = threadIdx.x & 3;
+    for (int qb = threadIdx.x >> 2; qb < total; qb += blockDim.x >> 2) {
+        const int c = qb / nblk;
+        const int b = qb - c * nblk;
+        const float *src = x + c * ldx + b * 32 + quarter * 8;
+        float v[8];
+        if (vec_ok) {
+            const float4 a0 = *reinterpret_cast<const float4 *>(src);
+            const float4 a1 = *reinterpret_cast<const float4 *>(src + 4);
+            v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+            v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = src[k];
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+        amax = fmaxf(amax, dppf<kDppXor1>(amax));
+        amax = fmaxf(amax, dppf<kDppXor2>(amax));
+        const float d = amax / 127.0f;
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int q = amax == 0.0f ? 0 : (int)roundf(v[k] / d);
+            const uint32_t byte = (uint32_t)(q & 0xff);
+            if (k < 4) lo |= byte << (8 * k);
+            else hi |= byte << (8 * (k - 4));
+        }
+        *reinterpret_cast<uint2 *>(q8s + c * K + b * 32 + quarter * 8) = make_uint2(lo, hi);
+        if (quarter == 0) d8s[qb] = (float)(_Float16)d;
+    }
+}
+
+// Already-quantised AoS block_q8_1 (column stride stride_col_y blocks) -> LDS.
+__device__ __forceinline__ void stage_from_q8_1(const uint8_t *__restrict__ y, int64_t stride_col_y,
+                                                int K, int ncols, int8_t *q8s, float *d8s) {
+    const int nblk = K / 32;
+    const int total = ncols * nblk;
+    const int quarter = threadIdx.x & 3;
+    for (int qb = threadIdx.x >> 2; qb < total; qb += blockDim.x >> 2) {
+        const int c = qb / nblk;
+        const int b = qb - c * nblk;
+        const uint8_t *blk = y + ((int64_t)c * stride_col_y + b) * kQ81Bytes;
+        const uint32_t w0 = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t *>(blk + 8 + quarter * 8);
+        *reinterpret_cast<uint2 *>(q8s + c * K + b * 32 + quarter * 8) = make_uint2(w0, w1);
+        if (quarter == 0) d8s[qb] = half_bits_to_float(*reinterpret_cast<const uint16_t *>(blk));
+    }
+}
+
+}  // namespace q4k

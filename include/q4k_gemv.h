@@ -1,0 +1,170 @@
+/*
+ * q4k_gemv.h -- C ABI of the MI355X (gfx950) Q4_K matrix-vector product.
+ *
+ * Drop-in for ggml's "mmvq" path of GGML_OP_MUL_MAT with a Q4_K weight
+ * (src0), an F32 activation of 1..8 columns (src1) and an F32 result (dst).
+ * Every entry point takes plain pointers and sizes, returns a q4k_status and
+ * never throws or aborts.  All device work is enqueued on the caller's HIP
+ * stream (passed as void *, NULL = the null stream) with no host
+ * synchronisation, like the reference, which runs on ctx.stream().
+ *
+ * Memory: src0, src1 and dst are caller-owned device buffers.  The library
+ * allocates nothing on the hot path; q4k_mul_mat_vec_q only falls back to a
+ * stream-ordered temporary (hipMallocAsync/hipFreeAsync, the counterpart of
+ * ggml's ctx.pool()) for shapes whose activation does not fit one
+ * workgroup's LDS when no workspace is passed.
+ *
+ * Threading: entry points may be called from any host thread; per-device
+ * state is initialised once under a lock.  Calls that share a stream are
+ * ordered by it.
+ */
+#ifndef Q4K_GEMV_H
+#define Q4K_GEMV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+typedef enum q4k_status {
+    Q4K_OK = 0,
+    /* The shape or layout is outside what this path implements; the caller
+     * falls back to another implementation.  Counterpart of the reference's
+     * simple_ok gate, which routes such cases to the generic kernel
+     * (kernels/mmvq.cu:540-545, :585-591). */
+    Q4K_EUNSUPPORTED = 1,
+    /* Invalid argument (null pointer, K not a multiple of 256, more than 8
+     * columns, inconsistent strides).  The reference aborts on these with
+     * GGML_ASSERT (kernels/mmvq.cu:393-394, :669-684). */
+    Q4K_EINVAL = 2,
+    /* A HIP runtime call or kernel launch failed; q4k_last_hip_error() gives
+     * the hipError_t.  The reference leaves launches unchecked
+     * (kernels/mmvq.cu:563-584). */
+    Q4K_EHIP = 3,
+    /* The stream-ordered temporary could not be allocated. */
+    Q4K_ENOMEM = 4
+} q4k_status;
+
+/* ggml type ids used in descriptors (values of ggml's enum ggml_type) */
+#define Q4K_GGML_TYPE_F32 0
+#define Q4K_GGML_TYPE_Q8_1 9
+#define Q4K_GGML_TYPE_Q4_K 12
+
+#define Q4K_QK_K 256            /* weights per Q4_K super-block */
+#define Q4K_BLOCK_Q4_K_BYTES 144 /* d, dmin (fp16), scales[12], qs[128]; kernels/2pack.cu:6 */
+#define Q4K_BLOCK_Q8_1_BYTES 36  /* ds (half2), qs[32]; kernels/2pack.cu:7 */
+#define Q4K_MATRIX_ROW_PADDING 512 /* K padding of the Q8_1 temp; kernels/mmvq.cu:728 */
+#define Q4K_MAX_BATCH 8         /* MMVQ_MAX_BATCH_SIZE; kernels/mmvq.cu:394 */
+
+/* The subset of ggml_tensor the op reads: type, ne[4] (elements per dim),
+ * nb[4] (bytes per step in each dim), data (device pointer). */
+typedef struct q4k_tensor {
+    int32_t type;
+    int64_t ne[4];
+    size_t nb[4];
+    void *data;
+} q4k_tensor;
+
+/* ----------------------------------------------------------------- misc */
+int32_t q4k_version(void);
+const char *q4k_strerror(int status);
+/* hipError_t of the most recent Q4K_EHIP on the calling thread (0 if none) */
+int32_t q4k_last_hip_error(void);
+
+/* Bytes of the Q8_1 activation buffer for ne11 columns of ne10 values:
+ * ne11 * pad(ne10, 512) / 32 * 36.  Same size as the reference's pool
+ * allocation (kernels/mmvq.cu:728-729). */
+size_t q4k_q8_1_bytes(int64_t ne10, int64_t ne11);
+
+/* ------------------------------------------------------------ entry points */
+
+/* F32 -> Q8_1 activation quantiser for the 2-D case.  Replaces
+ * quantize_row_q8_1_cuda(x, NULL, vy, type, ne00, s01, s02, s03, ne0,
+ * ne1, 1, 1, stream) as called at kernels/mmvq.cu:734.
+ *   x:    ne1 columns of ne00 floats, column stride s01 floats
+ *   vy:   ne1 * ne0/32 block_q8_1, column after column; values at index
+ *         >= ne00 quantise as 0 (ne0 = padded length, multiple of 32)
+ * Per 32 values: d = amax/127, q = round(x/d) (0 if amax == 0),
+ * ds = (half(d), half(sum x)). */
+int q4k_quantize_row_q8_1(const float *x, void *vy, int64_t ne00, int64_t s01, int64_t ne0,
+                          int64_t ne1, void *stream);
+
+/* dst = src0 (Q4_K, ne01 x ne00) * src1 (F32, ne00 x ne11).  Replaces
+ * ggml_cuda_mul_mat_vec_q(ctx, src0, src1, ids=NULL, dst, fusion=NULL)
+ * (kernels/mmvq.cu:666-762) for the 2-D case.
+ *   src0: ne01 rows, row stride nb01 bytes (multiple of 144), 16-B aligned
+ *   src1: ne11 columns of ne00 floats, column stride nb11 bytes
+ *   dst:  ne11 columns of ne01 floats, column stride nb1 bytes
+ * ne00 must be a multiple of 256 and 1 <= ne11 <= 8 (ne01 == 0 or ne11 == 0
+ * is an empty product and returns Q4K_OK).  The activation is quantised to
+ * Q8_1 inside the GEMV launch when it fits one workgroup's LDS; otherwise
+ * through a Q8_1 buffer: `workspace` (at least q4k_q8_1_bytes(ne00, ne11)
+ * bytes, 4-B aligned) or, when NULL, a stream-ordered temporary. */
+int q4k_mul_mat_vec_q(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
+                      const float *src1, int64_t ne11, int64_t nb11, float *dst, int64_t nb1,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/* Row-slice GEMV on an already-quantised activation.  Replaces
+ * ggml_cuda_op_mul_mat_vec_q(ctx, src0, src1, dst, src0_dd_i, src1_ddf_i,
+ * src1_ddq_i, dst_dd_i, row_low, row_high, src1_ncols,
+ * src1_padded_row_size, stream) (kernels/mmvq.cu:764-793), the per-device
+ * call of ggml's split-mode-row multi-GPU matmul.
+ *   src0_dd_i:   rows [row_low, row_high) of the Q4_K weight, contiguous
+ *                (ne00/256 blocks per row), 16-B aligned
+ *   src1_ddq_i:  src1_ncols columns of block_q8_1, column stride
+ *                src1_padded_row_size/32 blocks
+ *   dst_dd_i:    dst_dd_i[c*nrows_dst + r] for r < row_high-row_low
+ * As in the reference, nrows_dst is ne0 on the device that holds the whole
+ * result and row_high-row_low elsewhere (kernels/mmvq.cu:780-782). */
+int q4k_op_mul_mat_vec_q(const void *src0_dd_i, int64_t ne00, int64_t row_low, int64_t row_high,
+                         const void *src1_ddq_i, int64_t src1_ncols,
+                         int64_t src1_padded_row_size, float *dst_dd_i, int64_t nrows_dst,
+                         void *stream);
+
+/* ggml-descriptor form of q4k_mul_mat_vec_q: the signature of
+ * ggml_cuda_mul_mat_vec_q (kernels/mmvq.cu:666-668) with ggml_tensor
+ * replaced by q4k_tensor and the backend context by (workspace, stream).
+ * Checks the reference's assertions: src1/dst F32 (:669-670), nb00 == 144,
+ * nb10 == 4, nb0 == 4 (:681-683), ne10 == ne00, ne0 == ne01, ne1 == ne11.
+ * Returns Q4K_EUNSUPPORTED for what this path does not implement: ids
+ * (MUL_MAT_ID), fusion (gate/bias/GLU), more than one channel or sample
+ * (ne2/ne3 > 1) -- the cases the reference's simple_ok gate also excludes. */
+int q4k_ggml_mul_mat_vec_q(const q4k_tensor *src0, const q4k_tensor *src1, const q4k_tensor *ids,
+                           q4k_tensor *dst, const void *fusion, void *workspace,
+                           size_t workspace_bytes, void *stream);
+
+/* Parity probe: the int32 sub-block sums of the product, computed with the
+ * GEMV kernel's own lane mapping and dot routines.
+ *   sqq[(c*ne01 + r)*(ne00/32) + s] = sum over sub-block s of q4 * q8
+ *   sq[c*(ne00/32) + s]            = sum over sub-block s of q8
+ * q8_1 holds ncols columns of block_q8_1 with column stride stride_col_y
+ * blocks.  These are the quantities of kernels/vecdotq.cuh:469-478 summed
+ * over the lanes that share a sub-block. */
+int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
+                      const void *q8_1, int64_t ncols, int64_t stride_col_y, int32_t *sqq,
+                      int32_t *sq, void *stream);
+
+/* Launch geometry q4k_mul_mat_vec_q would use on the current device:
+ * out[0] rows per wave tile, out[1] waves per workgroup, out[2] workgroups,
+ * out[3] LDS bytes per workgroup, out[4] columns per launch, out[5] 1 when
+ * the activation is quantised inside the GEMV launch. */
+int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[6]);
+
+/* ------------------------------------------------------------ host side */
+
+/* Host Q4_K quantiser: nrows rows of n_per_row floats (multiple of 256)
+ * into nrows * n_per_row/256 block_q4_K, using up to nthreads threads.
+ * Replaces quantize_row_q4_K_ref row by row (ggml-quants.c, the weight
+ * format the reference consumes); the byte layout is fixed by
+ * kernels/vecdotq.cuh:785-807. */
+int q4k_quantize_rows_q4_K(const float *src, void *dst, int64_t nrows, int64_t n_per_row,
+                           int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q4K_GEMV_H */

@@ -1,0 +1,209 @@
+"""numpy bindings of the CPU oracle (oracle/q4k_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP product path and the CPU
+baseline the benchmark times beside it.  Only tests/, the smoke entry point and
+the benchmark's CPU-baseline leg may import this module.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libq4k_oracle.so")
+
+QK_K = 256
+QK8_1 = 32
+Q4K_BYTES = 144
+Q81_BYTES = 36
+Q8K_BYTES = 292
+MATRIX_ROW_PADDING = 512  # kernels/mmvq.cu:728 pads K to this for the Q8_1 temp
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compiles the oracle with its Makefile (gcc); returns the library path."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE, "-B" if force else "all"], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        I64 = ctypes.c_int64
+        I = ctypes.c_int
+        sig = {
+            "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+            "orc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "orc_f32_to_f16_array": (None, [P, P, I64]),
+            "orc_f16_to_f32_array": (None, [P, P, I64]),
+            "orc_nearest_int": (I, [ctypes.c_float]),
+            "orc_nearest_int_array": (None, [P, P, I64]),
+            "orc_scale_min_k4": (None, [I, P, P, P]),
+            "orc_vecdot_scale_pair": (None, [I, P, P]),
+            "orc_pack_scales_k4": (None, [P, P, P]),
+            "orc_selftest_scale_unpack": (I64, []),
+            "orc_selftest_scale_pack": (I64, []),
+            "orc_quantize_q4_K": (None, [P, P, I64]),
+            "orc_quantize_q4_K_rows": (None, [P, P, I64, I64, I]),
+            "orc_dequantize_q4_K": (None, [P, P, I64]),
+            "orc_quantize_q8_1": (None, [P, I64, I64, P]),
+            "orc_quantize_q8_1_cols": (None, [P, I64, I64, I64, I64, P]),
+            "orc_gemv_q4K_q8_1": (None, [P, I64, I64, I64, P, I64, I64, P, P, P, P]),
+            "orc_quantize_q8_K": (None, [P, P, I64]),
+            "orc_vec_dot_q4_K_q8_K_scalar": (ctypes.c_float, [I64, P, P]),
+            "orc_vec_dot_q4_K_q8_K_avx2": (ctypes.c_float, [I64, P, P]),
+            "orc_cpu_has_avx2": (I, []),
+            "orc_cpu_mul_mat_q4_K": (I, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I]),
+            "orc_time_cpu_mul_mat_q4_K": (None, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I, I, P]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def pad_k(K: int) -> int:
+    return (K + MATRIX_ROW_PADDING - 1) // MATRIX_ROW_PADDING * MATRIX_ROW_PADDING
+
+
+# ---------------------------------------------------------------- fp16 ----
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_f16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().orc_f16_to_f32_array(_p(h), _p(out), h.size)
+    return out
+
+
+def nearest_int(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.int32)
+    lib().orc_nearest_int_array(_p(x), _p(out), x.size)
+    return out
+
+
+# ------------------------------------------------------------ quantisers ----
+def quantize_q4_K(w: np.ndarray, nthreads: int = 1) -> np.ndarray:
+    """F32 [M, K] -> Q4_K bytes [M, K/256*144] (quantize_row_q4_K_ref per row)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    M, K = w.shape
+    assert K % QK_K == 0
+    out = np.empty((M, K // QK_K * Q4K_BYTES), dtype=np.uint8)
+    lib().orc_quantize_q4_K_rows(_p(w), _p(out), M, K, nthreads)
+    return out
+
+
+def dequantize_q4_K(q: np.ndarray, K: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    M = q.size // (K // QK_K * Q4K_BYTES)
+    out = np.empty((M, K), dtype=np.float32)
+    for r in range(M):
+        lib().orc_dequantize_q4_K(_p(q[r]), _p(out[r]), K)
+    return out
+
+
+def quantize_q8_1(x: np.ndarray, k_padded: int | None = None) -> np.ndarray:
+    """F32 [N, K] -> Q8_1 bytes [N, K_pad/32*36] with ggml-cuda semantics."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    N, K = x.shape
+    kp = pad_k(K) if k_padded is None else k_padded
+    out = np.empty((N, kp // QK8_1 * Q81_BYTES), dtype=np.uint8)
+    lib().orc_quantize_q8_1_cols(_p(x), K, K, N, kp, _p(out))
+    return out
+
+
+def quantize_q8_K(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    N, K = x.shape
+    out = np.empty((N, K // QK_K * Q8K_BYTES), dtype=np.uint8)
+    for c in range(N):
+        lib().orc_quantize_q8_K(_p(x[c]), _p(out[c]), K)
+    return out
+
+
+# ------------------------------------------------------------------ GEMV ----
+def gemv_q4K_q8_1(w_q: np.ndarray, K: int, q8: np.ndarray, want_sums: bool = True):
+    """Q4_K [M, K/256*144] x Q8_1 [N, Kp/32*36] -> dict(y64 [N,M], l1 [N,M],
+    sqq [N,M,K/32] int32, sq [N,K/32] int32)."""
+    w_q = np.ascontiguousarray(w_q, dtype=np.uint8)
+    q8 = np.ascontiguousarray(np.atleast_2d(q8), dtype=np.uint8)
+    row_bytes = K // QK_K * Q4K_BYTES
+    M = w_q.size // row_bytes
+    N = q8.shape[0]
+    stride_col_y = q8.shape[1] // Q81_BYTES
+    y64 = np.empty((N, M), dtype=np.float64)
+    l1 = np.empty((N, M), dtype=np.float64)
+    sqq = np.empty((N, M, K // 32), dtype=np.int32) if want_sums else None
+    sq = np.empty((N, K // 32), dtype=np.int32) if want_sums else None
+    lib().orc_gemv_q4K_q8_1(_p(w_q), M, K, row_bytes, _p(q8), N, stride_col_y, _p(y64), _p(l1),
+                            _p(sqq) if want_sums else None, _p(sq) if want_sums else None)
+    return {"y64": y64, "l1": l1, "sqq": sqq, "sq": sq}
+
+
+def vec_dot_q4_K_q8_K(w_row: np.ndarray, y_row: np.ndarray, K: int, isa: str = "avx2") -> float:
+    f = lib().orc_vec_dot_q4_K_q8_K_avx2 if isa == "avx2" else lib().orc_vec_dot_q4_K_q8_K_scalar
+    return float(f(K, _p(np.ascontiguousarray(w_row)), _p(np.ascontiguousarray(y_row))))
+
+
+def cpu_mul_mat_q4_K(w_q: np.ndarray, K: int, x: np.ndarray, nthreads: int = 1, isa: str = "avx2"):
+    """ggml CPU path: x [N, K] f32 -> Q8_K, then vec_dot per (row, column);
+    returns (dst [N, M] float32, isa_used)."""
+    w_q = np.ascontiguousarray(w_q, dtype=np.uint8)
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    N = x.shape[0]
+    row_bytes = K // QK_K * Q4K_BYTES
+    M = w_q.size // row_bytes
+    yq = np.empty((N, K // QK_K * Q8K_BYTES), dtype=np.uint8)
+    dst = np.empty((N, M), dtype=np.float32)
+    used = lib().orc_cpu_mul_mat_q4_K(_p(w_q), M, K, row_bytes, _p(x), N, K, _p(yq), _p(dst), M,
+                                      nthreads, 1 if isa == "avx2" else 0, 1)
+    return dst, ("avx2" if used else "scalar")
+
+
+def time_cpu_mul_mat_q4_K(w_q: np.ndarray, K: int, x: np.ndarray, nthreads: int, reps: int,
+                          isa: str = "avx2", quantize: bool = True) -> np.ndarray:
+    """Wall time (s) of each of `reps` calls of the threaded CPU path."""
+    w_q = np.ascontiguousarray(w_q, dtype=np.uint8)
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    N = x.shape[0]
+    row_bytes = K // QK_K * Q4K_BYTES
+    M = w_q.size // row_bytes
+    yq = quantize_q8_K(x)
+    dst = np.empty((N, M), dtype=np.float32)
+    t = np.empty(reps, dtype=np.float64)
+    lib().orc_time_cpu_mul_mat_q4_K(_p(w_q), M, K, row_bytes, _p(x), N, K, _p(yq), _p(dst), M,
+                                    nthreads, 1 if isa == "avx2" else 0, 1 if quantize else 0,
+                                    reps, _p(t))
+    return t
+
+
+# -------------------------------------------------------------- tolerance ----
+def parity_tolerance(y64: np.ndarray, l1: np.ndarray) -> np.ndarray:
+    """Per-output F32 tolerance against the f64 result: 1e-5 relative, or 4 ulp
+    of the result, or, where the row's terms cancel, 8 f32 epsilons of the sum
+    of |term| over its per-sub-block terms (the scale of a reordered f32 sum)."""
+    ulp = np.spacing(np.abs(y64).astype(np.float32)).astype(np.float64)
+    return np.maximum(np.maximum(1e-5 * np.abs(y64), 4.0 * ulp), 8.0 * np.finfo(np.float32).eps * l1)

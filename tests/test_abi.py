@@ -1,0 +1,89 @@
+"""The C-ABI library builds, loads and exports every entry point its header
+declares; argument checks that need no GPU return the documented status."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import _common
+
+HEADER = os.path.join(_common.ROOT, "include", "q4k_gemv.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(q4k_[A-Za-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for n in ("q4k_mul_mat_vec_q", "q4k_op_mul_mat_vec_q", "q4k_ggml_mul_mat_vec_q",
+              "q4k_quantize_row_q8_1", "q4k_subblock_sums", "q4k_quantize_rows_q4_K"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(Q):
+    L = ctypes.CDLL(Q.LIB_PATH)
+    for n in declared_functions():
+        assert hasattr(L, n), n
+        assert n in Q.SIGNATURES, n
+
+
+def test_misc_entry_points(Q):
+    L = Q.lib()
+    assert L.q4k_version() >= 100
+    assert L.q4k_strerror(Q.Q4K_EUNSUPPORTED).decode().startswith("unsupported")
+    assert L.q4k_q8_1_bytes(4096, 1) == 4096 // 32 * 36
+    assert L.q4k_q8_1_bytes(4100, 2) == 2 * 4608 // 32 * 36
+    assert L.q4k_q8_1_bytes(14336, 8) == 8 * 14336 // 32 * 36
+
+
+FAKE = ctypes.c_void_p(0x10000)     # never dereferenced by the host checks
+FAKE_ODD = ctypes.c_void_p(0x10004)
+
+
+@pytest.mark.parametrize("args,status", [
+    ((FAKE, 4000, 16, 4000 // 256 * 144, FAKE, 1, 16000, FAKE, 64), 2),   # K % 256
+    ((FAKE, 4096, 16, 2304, FAKE, 9, 16384, FAKE, 64), 2),                  # 9 columns
+    ((FAKE, 4096, 16, 2300, FAKE, 1, 16384, FAKE, 64), 2),                  # row stride
+    ((FAKE, 4096, 16, 2304, None, 1, 16384, FAKE, 64), 2),                  # null src1
+    ((FAKE, 4096, 16, 2304, FAKE, 2, 1000, FAKE, 64), 2),                   # column stride
+    ((FAKE_ODD, 4096, 16, 2304, FAKE, 1, 16384, FAKE, 64), 1),              # src0 alignment
+    ((FAKE, 4096, 0, 2304, FAKE, 1, 16384, FAKE, 64), 0),                   # empty: no rows
+    ((FAKE, 4096, 16, 2304, FAKE, 0, 16384, FAKE, 64), 0),                  # empty: no columns
+])
+def test_mul_mat_vec_q_argument_checks(Q, args, status):
+    assert Q.lib().q4k_mul_mat_vec_q(*args, None, 0, None) == status
+
+
+def test_op_and_descriptor_checks(Q):
+    L = Q.lib()
+    assert L.q4k_op_mul_mat_vec_q(FAKE, 4096, 10, 5, FAKE, 1, 4096, FAKE, 5, None) == Q.Q4K_EINVAL
+    assert L.q4k_op_mul_mat_vec_q(FAKE, 4096, 0, 8, FAKE, 1, 4000, FAKE, 8, None) == Q.Q4K_EINVAL
+    assert L.q4k_op_mul_mat_vec_q(FAKE, 4096, 0, 8, FAKE, 1, 4096, FAKE, 4, None) == Q.Q4K_EINVAL
+    assert L.q4k_op_mul_mat_vec_q(FAKE, 4096, 3, 3, FAKE, 1, 4096, FAKE, 4, None) == Q.Q4K_OK
+    s0 = Q.make_tensor(Q.GGML_TYPE_Q4_K, [4096, 16], [144, 2304], 0x10000)
+    s1 = Q.make_tensor(Q.GGML_TYPE_F32, [4096, 1], [4, 16384], 0x20000)
+    d = Q.make_tensor(Q.GGML_TYPE_F32, [16, 1], [4, 64], 0x30000)
+    f16 = Q.make_tensor(1, [4096, 1], [2, 8192], 0x20000)
+    assert Q.ggml_mul_mat_vec_q(s0, f16, d) == Q.Q4K_EINVAL
+    assert Q.ggml_mul_mat_vec_q(s0, s1, d, ids=s1) == Q.Q4K_EUNSUPPORTED
+    L2 = Q.lib()
+    st = L2.q4k_ggml_mul_mat_vec_q(ctypes.byref(s0), ctypes.byref(s1), None, ctypes.byref(d),
+                                   ctypes.c_void_p(0x40000), None, 0, None)
+    assert st == Q.Q4K_EUNSUPPORTED                                          # fusion
+    q6 = Q.make_tensor(14, [4096, 16], [210, 3360], 0x10000)
+    assert Q.ggml_mul_mat_vec_q(q6, s1, d) == Q.Q4K_EUNSUPPORTED             # other types
+    s3 = Q.make_tensor(Q.GGML_TYPE_F32, [4096, 1, 2], [4, 16384, 16384], 0x20000)
+    assert Q.ggml_mul_mat_vec_q(s0, s3, d) == Q.Q4K_EUNSUPPORTED             # batched 3-D
+    assert L.q4k_quantize_row_q8_1(FAKE, FAKE, 100, 100, 96, 1, None) == Q.Q4K_EINVAL
+    assert L.q4k_quantize_row_q8_1(FAKE, FAKE, 100, 100, 130, 1, None) == Q.Q4K_EINVAL
+    assert L.q4k_quantize_rows_q4_K(None, None, 4, 300, 1) == Q.Q4K_EINVAL
+
+
+def test_host_quantiser_rejects_bad_shapes(Q):
+    import numpy as np
+    with pytest.raises(Q.Q4KError):
+        Q.quantize_rows_q4_K(np.zeros((2, 300), np.float32))

@@ -1,0 +1,233 @@
+"""GPU parity of the HIP path (called through the C ABI) against the oracle.
+
+Bar: Q8_1 bytes and int32 sub-block sums bit-exact; F32 outputs within the
+parity tolerance of the oracle's f64 result (1e-5 relative, or 4 ulp, or 8
+f32 epsilons of the row's sum of |term| where terms cancel).  Full-size
+workloads check every output against the oracle on a row sample (rows are
+independent) and all outputs through size-independent properties: the fused
+and pre-quantised launches agree bit for bit, and row-split calls reassemble
+the full result exactly.
+"""
+import numpy as np
+import pytest
+
+import _common
+
+pytestmark = pytest.mark.gpu
+
+_cache = {}
+
+
+def inputs(Q, M, K, N, seed=0):
+    key = (M, K, N, seed)
+    if key not in _cache:
+        if len(_cache) > 6:
+            _cache.clear()
+        W = _common.weights(M, K, seed)
+        wq = Q.quantize_rows_q4_K(W, nthreads=16)
+        del W
+        x = _common.activations(N, K, seed)
+        _cache[key] = (wq, x)
+    return _cache[key]
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def oracle_rows(O, wq, K, q8, rows):
+    ref = O.gemv_q4K_q8_1(wq[rows], K, q8, want_sums=False)
+    return ref
+
+
+# --------------------------------------------------------------- Q8_1 ----
+@pytest.mark.parametrize("N,K,kpad,ld", [(1, 4096, 4096, 4096), (3, 4096, 4096, 4160),
+                                         (2, 14336, 14336, 14336), (1, 300, 512, 320),
+                                         (8, 8192, 8192, 8192)])
+def test_quantize_q8_1_bytes_exact(Q, O, gpu, N, K, kpad, ld):
+    import torch
+    x = np.zeros((N, ld), np.float32)
+    x[:, :K] = _common.activations(N, K, seed=K)
+    x[0, :32] = 0.0  # one all-zero block
+    xd = to_dev(x, gpu)
+    out = torch.empty((N, kpad // 32 * 36), dtype=torch.uint8, device=gpu)
+    Q._check(Q.lib().q4k_quantize_row_q8_1(Q._ptr(xd), Q._ptr(out), K, ld, kpad, N, Q._stream()), "q8_1")
+    ref = np.stack([O.quantize_q8_1(x[c:c + 1, :K], k_padded=kpad)[0] for c in range(N)])
+    assert np.array_equal(out.cpu().numpy(), ref)
+
+
+# ---------------------------------------------------------- int sums ----
+@pytest.mark.parametrize("M,K,N", [(5, 256, 1), (33, 768, 2), (64, 2304, 3), (4096, 4096, 1),
+                                   (96, 14336, 2), (40, 28672, 1)])
+def test_subblock_sums_exact(Q, O, gpu, M, K, N):
+    wq, x = inputs(Q, M, K, N)
+    q8 = O.quantize_q8_1(x)
+    sqq, sq = Q.subblock_sums(to_dev(wq, gpu), K, to_dev(q8, gpu), N)
+    ref = O.gemv_q4K_q8_1(wq, K, q8)
+    assert np.array_equal(sq.cpu().numpy(), ref["sq"])
+    assert np.array_equal(sqq.cpu().numpy(), ref["sqq"])
+
+
+# ------------------------------------------------------ small shapes ----
+EDGE_SHAPES = [(1, 256, 1), (3, 768, 2), (5, 2304, 3), (17, 4352, 5), (64, 8192, 8),
+               (129, 1024, 7), (1000, 4096, 4), (7, 2048, 6), (2, 512, 8)]
+
+
+@pytest.mark.parametrize("M,K,N", EDGE_SHAPES)
+def test_gemv_edge_shapes(Q, O, gpu, M, K, N):
+    wq, x = inputs(Q, M, K, N, seed=1)
+    q8 = O.quantize_q8_1(x)
+    ref = O.gemv_q4K_q8_1(wq, K, q8, want_sums=False)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    _common.assert_within_tolerance(O, y, ref, f"fused {M}x{K} N={N}")
+    y2 = Q.op_mul_mat_vec_q(wd, K, to_dev(q8, gpu), N).cpu().numpy()
+    _common.assert_within_tolerance(O, y2, ref, f"q8_1 {M}x{K} N={N}")
+    assert np.array_equal(y, y2)
+
+
+def test_zero_activation_and_zero_weight(Q, O, gpu):
+    M, K, N = 40, 1024, 3
+    wq, x = inputs(Q, M, K, N, seed=2)
+    x = x.copy()
+    x[1] = 0.0
+    wq = wq.copy()
+    wq[5] = 0
+    q8 = O.quantize_q8_1(x)
+    ref = O.gemv_q4K_q8_1(wq, K, q8, want_sums=False)
+    y = Q.mul_mat_vec_q(to_dev(wq, gpu), K, to_dev(x, gpu)).cpu().numpy()
+    _common.assert_within_tolerance(O, y, ref, "zeros")
+    assert (y[1] == 0).all() and (y[:, 5] == 0).all()
+
+
+def test_strides_and_no_out_of_bounds_writes(Q, O, gpu):
+    """Padded weight rows, padded activation columns and a dst column stride
+    larger than M; the padding of dst must stay untouched."""
+    import torch
+    M, K, N = 37, 2048, 3
+    wq, x = inputs(Q, M, K, N, seed=3)
+    rb = wq.shape[1]
+    wpad = np.full((M, rb + 144 * 2), 0xAB, np.uint8)
+    wpad[:, :rb] = wq
+    xpad = np.full((N, K + 64), np.nan, np.float32)
+    xpad[:, :K] = x
+    ld = M + 11
+    dst = torch.full((N, ld), -7.0, dtype=torch.float32, device=gpu)
+    wd, xd = to_dev(wpad, gpu), to_dev(xpad, gpu)
+    st = Q.lib().q4k_mul_mat_vec_q(Q._ptr(wd), K, M, wpad.shape[1], Q._ptr(xd), N, (K + 64) * 4,
+                                   Q._ptr(dst), ld * 4, None, 0, Q._stream())
+    assert st == Q.Q4K_OK
+    out = dst.cpu().numpy()
+    assert (out[:, M:] == -7.0).all()
+    ref = O.gemv_q4K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, out[:, :M], ref, "strided")
+
+
+def test_unquantised_path_for_large_activation(Q, O, gpu):
+    """K=28672 with 8 columns does not fit one workgroup's LDS: the op
+    quantises to a Q8_1 buffer (caller workspace or stream-ordered temporary)
+    and runs the GEMV in column chunks."""
+    import torch
+    M, K, N = 96, 28672, 8
+    geo = Q.geometry(K, M, N)
+    wq, x = inputs(Q, M, K, N, seed=4)
+    ref = O.gemv_q4K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    _common.assert_within_tolerance(O, y, ref, f"large K ({geo})")
+    ws = torch.empty(Q.q8_1_bytes(K, N), dtype=torch.uint8, device=gpu)
+    y2 = Q.mul_mat_vec_q(wd, K, xd, workspace=ws).cpu().numpy()
+    assert np.array_equal(y, y2)
+
+
+def test_ggml_descriptor_entry(Q, O, gpu):
+    import torch
+    M, K, N = 300, 4096, 2
+    wq, x = inputs(Q, M, K, N, seed=5)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    dst = torch.empty((N, M), dtype=torch.float32, device=gpu)
+    s0 = Q.make_tensor(Q.GGML_TYPE_Q4_K, [K, M], [144, wq.shape[1]], wd.data_ptr())
+    s1 = Q.make_tensor(Q.GGML_TYPE_F32, [K, N], [4, K * 4], xd.data_ptr())
+    d = Q.make_tensor(Q.GGML_TYPE_F32, [M, N], [4, M * 4], dst.data_ptr())
+    assert Q.ggml_mul_mat_vec_q(s0, s1, d) == Q.Q4K_OK
+    y = Q.mul_mat_vec_q(wd, K, xd)
+    assert torch.equal(dst, y)
+    # what the path leaves to the caller's fallback
+    assert Q.ggml_mul_mat_vec_q(s0, s1, d, ids=s1) == Q.Q4K_EUNSUPPORTED
+    s3 = Q.make_tensor(Q.GGML_TYPE_Q4_K, [K, M, 2], [144, wq.shape[1], wq.nbytes], wd.data_ptr())
+    assert Q.ggml_mul_mat_vec_q(s3, s1, d) == Q.Q4K_EUNSUPPORTED
+    bad = Q.make_tensor(Q.GGML_TYPE_F32, [K + 256, N], [4, (K + 256) * 4], xd.data_ptr())
+    assert Q.ggml_mul_mat_vec_q(s0, bad, d) == Q.Q4K_EINVAL
+
+
+def test_golden_fixture_on_gpu(Q, O, gpu):
+    g = np.load(_common.GOLDEN_DIR + "/q4k_golden.npz")
+    for name in sorted({k.split("/")[0] for k in g.files if k.endswith("/wq")}):
+        wq, x, K = g[name + "/wq"], g[name + "/x"], int(g[name + "/K"])
+        N = x.shape[0]
+        ref = {"y64": g[name + "/y64"], "l1": g[name + "/l1"]}
+        y = Q.mul_mat_vec_q(to_dev(wq, gpu), K, to_dev(x, gpu)).cpu().numpy()
+        _common.assert_within_tolerance(O, y, ref, "golden " + name)
+        q8d = Q.quantize_row_q8_1(to_dev(x, gpu))
+        assert np.array_equal(q8d.cpu().numpy(), g[name + "/q8"])
+        sqq, sq = Q.subblock_sums(to_dev(wq, gpu), K, q8d, N)
+        assert np.array_equal(sqq.cpu().numpy(), g[name + "/sqq"])
+        assert np.array_equal(sq.cpu().numpy(), g[name + "/sq"])
+
+
+def test_golden_4096x4096_b1_on_gpu(Q, O, gpu):
+    """The 4096x4096 b=1 workload regenerated from its seeds (digests must
+    match the fixture) and run on the GPU against the fixture's result."""
+    import hashlib
+    g = np.load(_common.GOLDEN_DIR + "/q4k_golden.npz")
+    W = _common.weights(4096, 4096, 0)
+    wq = Q.quantize_rows_q4_K(W, nthreads=16)
+    x = _common.activations(1, 4096, 0)
+    assert hashlib.sha256(wq.tobytes()).hexdigest() == str(g["cfg_4096x4096_b1/sha256_wq"])
+    assert hashlib.sha256(x.tobytes()).hexdigest() == str(g["cfg_4096x4096_b1/sha256_x_f32"])
+    ref = {"y64": g["cfg_4096x4096_b1/y64"], "l1": g["cfg_4096x4096_b1/l1"]}
+    y = Q.mul_mat_vec_q(to_dev(wq, gpu), 4096, to_dev(x, gpu)).cpu().numpy()
+    _common.assert_within_tolerance(O, y, ref, "4096x4096 b=1")
+
+
+# ---------------------------------------------------- full workloads ----
+def _cases():
+    out = []
+    for wl, items in _common.WORKLOADS.items():
+        for M, K, ns in items:
+            for N in ns:
+                out.append(pytest.param(M, K, N, id=f"{wl}-{M}x{K}-N{N}"))
+    # de-duplicate identical shapes across workloads
+    seen, uniq = set(), []
+    for p in out:
+        if p.values not in seen:
+            seen.add(p.values)
+            uniq.append(p)
+    return uniq
+
+
+@pytest.mark.parametrize("M,K,N", _cases())
+def test_workload_parity(Q, O, gpu, M, K, N):
+    wq, x = inputs(Q, M, K, N)
+    q8 = O.quantize_q8_1(x)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    # oracle on all rows for small products, else on a row sample
+    if M * K * N <= 4096 * 4096 * 2:
+        rows = np.arange(M)
+    else:
+        rng = np.random.default_rng(M + K + N)
+        rows = np.unique(np.concatenate([[0, 1, M - 2, M - 1], rng.choice(M, 380, replace=False)]))
+    ref = oracle_rows(O, wq, K, q8, rows)
+    _common.assert_within_tolerance(O, y[:, rows], ref, f"{M}x{K} N={N}")
+    # pre-quantised launch: identical bits
+    q8d = Q.quantize_row_q8_1(xd)
+    y2 = Q.op_mul_mat_vec_q(wd, K, q8d, N).cpu().numpy()
+    assert np.array_equal(y, y2)
+    # split-mode row slices reassemble the full result exactly
+    cut = (M // 3) // 16 * 16 + 5
+    top = Q.op_mul_mat_vec_q(wd[:cut], K, q8d, N, row_low=0, row_high=cut).cpu().numpy()
+    bot = Q.op_mul_mat_vec_q(wd[cut:], K, q8d, N, row_low=cut, row_high=M).cpu().numpy()
+    assert np.array_equal(np.concatenate([top, bot], axis=1), y)
+    assert np.isfinite(y).all()

@@ -1,0 +1,61 @@
+"""Pins the oracle's F32 -> Q8_1 quantiser (ggml-cuda quantize_q8_1
+arithmetic) by its invariants and exact special cases."""
+import numpy as np
+
+
+def _split(q8, nblk):
+    b = q8.reshape(-1, nblk, 36)
+    d = b[..., 0:2].copy().view(np.uint16)[..., 0]
+    s = b[..., 2:4].copy().view(np.uint16)[..., 0]
+    qs = b[..., 4:].view(np.int8)
+    return d, s, qs
+
+
+def test_invariants(O):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((3, 4096)) * rng.uniform(0.01, 100, size=(3, 1))).astype(np.float32)
+    q8 = O.quantize_q8_1(x)
+    d16, s16, qs = _split(q8, 4096 // 32)
+    d = O.f16_bits_to_f32(d16)
+    xb = x.reshape(3, -1, 32)
+    amax = np.abs(xb).max(-1)
+    assert np.abs(qs.astype(np.int32)).max() <= 127
+    # d is half(amax/127) with the f32 quotient
+    assert (d16 == O.f32_to_f16_bits((amax / np.float32(127)).astype(np.float32))).all()
+    # the largest-magnitude value maps to +-127
+    imax = np.abs(xb).argmax(-1)
+    top = np.take_along_axis(qs.astype(np.int32), imax[..., None], -1)[..., 0]
+    sign = np.sign(np.take_along_axis(xb, imax[..., None], -1)[..., 0])
+    assert (top == 127 * sign).all()
+    # rounding error at most half a step of the f32 scale
+    d32 = (amax / np.float32(127)).astype(np.float64)
+    err = np.abs(xb.astype(np.float64) - d32[..., None] * qs)
+    assert (err <= d32[..., None] * 0.5 * (1 + 1e-6)).all()
+    # ds.y is half of the block sum
+    ssum = xb.astype(np.float64).sum(-1)
+    s = O.f16_bits_to_f32(s16).astype(np.float64)
+    assert (np.abs(s - ssum) <= np.abs(ssum) * 2.0 ** -10 + 1e-6).all()
+
+
+def test_zero_blocks_and_padding(O):
+    x = np.zeros((1, 1024), dtype=np.float32)
+    x[0, 100] = 3.0
+    q8 = O.quantize_q8_1(x, k_padded=2048)
+    assert q8.shape == (1, 2048 // 32 * 36)
+    d16, s16, qs = _split(q8, 64)
+    # block 3 holds the only non-zero value
+    nz = [i for i in range(64) if d16[0, i] != 0]
+    assert nz == [3]
+    assert (qs[0, [i for i in range(64) if i != 3]] == 0).all()
+    assert (s16[0, 32:] == 0).all() and (d16[0, 32:] == 0).all()
+
+
+def test_exact_multiples_roundtrip(O):
+    rng = np.random.default_rng(9)
+    q = rng.integers(-127, 128, size=(2, 512)).astype(np.int32)
+    q[:, ::32] = 127  # every block reaches amax = 127 * 2^-e
+    for e in (0, 3, 10):
+        x = (q * 2.0 ** -e).astype(np.float32)
+        d16, _, qs = _split(O.quantize_q8_1(x), 16)
+        assert (qs.reshape(2, -1) == q).all()
+        assert (O.f16_bits_to_f32(d16) == np.float32(2.0 ** -e)).all()
