@@ -40,6 +40,7 @@ SIGNATURES = {
     "q4k_ggml_mul_mat_vec_q": (_I, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "q4k_subblock_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P]),
     "q4k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
+    "q4k_set_geometry_override": (_I, [ctypes.c_int32] * 4),
     "q4k_quantize_rows_q4_K": (_I, [_P, _P, _I64, _I64, _I]),
 }
 
@@ -198,8 +199,15 @@ def subblock_sums(w_q, K: int, q8, ncols: int, stream=None):
     return sqq, sq
 
 
+def set_geometry_override(rows_per_tile: int = 0, waves_per_wg: int = 0, workgroups: int = 0,
+                          kernel: int = 0):
+    _check(lib().q4k_set_geometry_override(rows_per_tile, waves_per_wg, workgroups, kernel),
+           "q4k_set_geometry_override")
+
+
 def geometry(K: int, M: int, N: int) -> dict:
-    out = (ctypes.c_int32 * 6)()
+    out = (ctypes.c_int32 * 8)()
     _check(lib().q4k_gemv_geometry(K, M, N, ctypes.cast(out, _P)), "q4k_gemv_geometry")
-    keys = ("rows_per_tile", "waves_per_wg", "workgroups", "lds_bytes", "cols_per_launch", "fused")
+    keys = ("rows_per_tile", "waves_per_wg", "workgroups", "lds_bytes", "cols_per_launch", "fused",
+            "kernel", "rows_per_step")
     return dict(zip(keys, list(out)))

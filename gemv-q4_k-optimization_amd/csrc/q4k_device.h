@@ -128,56 +128,174 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 // Activation staging into LDS: q8[c*K + e] (int8) and d8[c*K/32 + b] (f32).
 // ------------------------------------------------------------------------
 
+// n / d for n < 2^31 as (umulhi(n, mul) + n) >> shift, with mul and shift
+// from fastdiv_init on the host (Granlund-Montgomery round-up method).
+struct FastDiv {
+    uint32_t d, mul, shift;
+};
+
+__host__ __device__ inline FastDiv fastdiv_init(uint32_t d) {
+    uint32_t l = 0;
+    while (l < 32 && (1ull << l) < d) ++l;
+    FastDiv f;
+    f.d = d;
+    f.shift = l;
+    f.mul = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    return f;
+}
+
+__device__ __forceinline__ uint32_t fastdiv(uint32_t n, const FastDiv &f) {
+    return (__umulhi(n, f.mul) + n) >> f.shift;
+}
+
+// roundf(x / d) with the correctly rounded quotient x/d, as ggml-cuda's
+// quantize_q8_1 computes it.  y = x * rcp(d) is within 2^-15 of the quotient
+// for |x/d| <= 128 (v_rcp_f32 is 1-ulp accurate), so unless y lies within
+// 2^-12 of a half-integer both round to the same integer and rint(y) is the
+// answer; the rare lanes near a tie (and any out-of-range y) divide exactly.
+__device__ __forceinline__ int quantize_value(float x, float d, float rd) {
+    const float y = x * rd;
+    const float f = fabsf(y - truncf(y));
+    if (!(fabsf(f - 0.5f) >= 0x1p-12f && fabsf(y) <= 128.0f)) return (int)roundf(x / d);
+    return (int)rintf(y);
+}
+
 // F32 activation -> Q8_1 values with ggml-cuda's quantize_q8_1 arithmetic
 // (call site kernels/mmvq.cu:734): per 32 values d = amax/127,
 // q = amax == 0 ? 0 : roundf(x/d), and the kernel consumes half(d).
-// Four lanes per 32-value block, 8 values per lane.
-__device__ __forceinline__ void stage_from_f32(const float *__restrict__ x, int64_t ldx, int K,
-                                               int ncols, bool vec_ok, int8_t *q8s, float *d8s) {
-    const int nblk = K / 32;
-    const int total = ncols * nblk;
-    const int quarter = threadIdx.x & 3;
-    for (int qb = threadIdx.x >> 2; qb < total; qb += blockDim.x >> 2) {
-        const int c = qb / nblk;
-        const int b = qb - c * nblk;
-        const float *src = x + c * ldx + b * 32 + quarter * 8;
-        float v[8];
-        if (vec_ok) {
-            const float4 a0 = *reinterpret_cast<const float4 *>(src);
-            const float4 a1 = *reinterpret_cast<const float4 *>(src + 4);
-            v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-            v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-        } else {
+// Four lanes per 32-value block, 8 values per lane.  Staging is split in
+// two: issue() loads the first kPre rounds of values into registers, to be
+// called before the kernel's first weight loads (vector loads complete in
+// issue order, so values loaded after the weights would wait for them);
+// finish() quantises them into LDS and handles any further rounds.
+constexpr int kPre = 4;
+
+struct ActStage {
+    float v[kPre][8];
+};
+
+__device__ __forceinline__ void quantize_block_part(const float (&v)[8], int quarter, int K, int c,
+                                                    int b, int qb, int8_t *q8s, float *d8s) {
+    float amax = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = src[k];
-        }
-        float amax = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
-        amax = fmaxf(amax, dppf<kDppXor1>(amax));
-        amax = fmaxf(amax, dppf<kDppXor2>(amax));
-        const float d = amax / 127.0f;
-        uint32_t lo = 0, hi = 0;
+    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    amax = fmaxf(amax, dppf<kDppXor1>(amax));
+    amax = fmaxf(amax, dppf<kDppXor2>(amax));
+    const float d = amax / 127.0f;
+    const float rd = __builtin_amdgcn_rcpf(d);
+    uint32_t lo = 0, hi = 0;
+    if (amax != 0.0f) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const int q = amax == 0.0f ? 0 : (int)roundf(v[k] / d);
-            const uint32_t byte = (uint32_t)(q & 0xff);
+            const uint32_t byte = (uint32_t)(quantize_value(v[k], d, rd) & 0xff);
             if (k < 4) lo |= byte << (8 * k);
             else hi |= byte << (8 * (k - 4));
         }
-        *reinterpret_cast<uint2 *>(q8s + c * K + b * 32 + quarter * 8) = make_uint2(lo, hi);
-        if (quarter == 0) d8s[qb] = (float)(_Float16)d;
+    }
+    *reinterpret_cast<uint2 *>(q8s + c * K + b * 32 + quarter * 8) = make_uint2(lo, hi);
+    if (quarter == 0) d8s[qb] = (float)(_Float16)d;
+}
+
+__device__ __forceinline__ void load_x8(const float *src, bool vec_ok, float (&v)[8]) {
+    if (vec_ok) {
+        const float4 a0 = *reinterpret_cast<const float4 *>(src);
+        const float4 a1 = *reinterpret_cast<const float4 *>(src + 4);
+        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+        v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = src[k];
     }
 }
 
-// Already-quantised AoS block_q8_1 (column stride stride_col_y blocks) -> LDS.
-__device__ __forceinline__ void stage_from_q8_1(const uint8_t *__restrict__ y, int64_t stride_col_y,
-                                                int K, int ncols, int8_t *q8s, float *d8s) {
+__device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int64_t ldx, int K,
+                                                int ncols, bool vec_ok, const FastDiv &fd,
+                                                ActStage &st) {
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int quarter = threadIdx.x & 3;
-    for (int qb = threadIdx.x >> 2; qb < total; qb += blockDim.x >> 2) {
-        const int c = qb / nblk;
+    const int step = blockDim.x >> 2;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const int qb = (threadIdx.x >> 2) + j * step;
+        if (qb < total) {
+            const int c = (int)fastdiv((uint32_t)qb, fd);
+            const int b = qb - c * nblk;
+            load_x8(x + c * ldx + b * 32 + quarter * 8, vec_ok, st.v[j]);
+        }
+    }
+}
+
+__device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, int64_t ldx, int K,
+                                                 int ncols, bool vec_ok, const FastDiv &fd,
+                                                 const ActStage &st, int8_t *q8s, float *d8s) {
+    const int nblk = K / 32;
+    const int total = ncols * nblk;
+    const int quarter = threadIdx.x & 3;
+    const int step = blockDim.x >> 2;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const int qb = (threadIdx.x >> 2) + j * step;
+        if (qb < total) {
+            const int c = (int)fastdiv((uint32_t)qb, fd);
+            quantize_block_part(st.v[j], quarter, K, c, qb - c * nblk, qb, q8s, d8s);
+        }
+    }
+    for (int qb = (threadIdx.x >> 2) + kPre * step; qb < total; qb += step) {
+        const int c = (int)fastdiv((uint32_t)qb, fd);
+        const int b = qb - c * nblk;
+        float v[8];
+        load_x8(x + c * ldx + b * 32 + quarter * 8, vec_ok, v);
+        quantize_block_part(v, quarter, K, c, b, qb, q8s, d8s);
+    }
+}
+
+// Already-quantised AoS block_q8_1 (column stride stride_col_y blocks) -> LDS,
+// in the same two phases: the first kPre rounds' bytes are loaded by issue().
+struct Q81Stage {
+    uint32_t w[kPre][2];
+    uint32_t ds[kPre];
+};
+
+__device__ __forceinline__ void stage_q81_issue(const uint8_t *__restrict__ y, int64_t stride_col_y,
+                                                int K, int ncols, const FastDiv &fd, Q81Stage &st) {
+    const int nblk = K / 32;
+    const int total = ncols * nblk;
+    const int quarter = threadIdx.x & 3;
+    const int step = blockDim.x >> 2;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const int qb = (threadIdx.x >> 2) + j * step;
+        if (qb < total) {
+            const int c = (int)fastdiv((uint32_t)qb, fd);
+            const uint8_t *blk = y + ((int64_t)c * stride_col_y + (qb - c * nblk)) * kQ81Bytes;
+            st.w[j][0] = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
+            st.w[j][1] = *reinterpret_cast<const uint32_t *>(blk + 8 + quarter * 8);
+            st.ds[j] = *reinterpret_cast<const uint32_t *>(blk);
+        }
+    }
+}
+
+__device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, int64_t stride_col_y,
+                                                 int K, int ncols, const FastDiv &fd,
+                                                 const Q81Stage &st, int8_t *q8s, float *d8s) {
+    const int nblk = K / 32;
+    const int total = ncols * nblk;
+    const int quarter = threadIdx.x & 3;
+    const int step = blockDim.x >> 2;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const int qb = (threadIdx.x >> 2) + j * step;
+        if (qb < total) {
+            const int c = (int)fastdiv((uint32_t)qb, fd);
+            const int b = qb - c * nblk;
+            *reinterpret_cast<uint2 *>(q8s + c * K + b * 32 + quarter * 8) =
+                make_uint2(st.w[j][0], st.w[j][1]);
+            if (quarter == 0) d8s[qb] = half_bits_to_float(st.ds[j]);
+        }
+    }
+    for (int qb = (threadIdx.x >> 2) + kPre * step; qb < total; qb += step) {
+        const int c = (int)fastdiv((uint32_t)qb, fd);
         const int b = qb - c * nblk;
         const uint8_t *blk = y + ((int64_t)c * stride_col_y + b) * kQ81Bytes;
         const uint32_t w0 = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
@@ -185,6 +303,15 @@ __device__ __forceinline__ void stage_from_q8_1(const uint8_t *__restrict__ y, i
         *reinterpret_cast<uint2 *>(q8s + c * K + b * 32 + quarter * 8) = make_uint2(w0, w1);
         if (quarter == 0) d8s[qb] = half_bits_to_float(*reinterpret_cast<const uint16_t *>(blk));
     }
+}
+
+// One-call form (issue + finish) for kernels with no loads to overlap.
+__device__ __forceinline__ void stage_from_q8_1(const uint8_t *__restrict__ y, int64_t stride_col_y,
+                                                int K, int ncols, const FastDiv &fd, int8_t *q8s,
+                                                float *d8s) {
+    Q81Stage st;
+    stage_q81_issue(y, stride_col_y, K, ncols, fd, st);
+    stage_q81_finish(y, stride_col_y, K, ncols, fd, st, q8s, d8s);
 }
 
 }  // namespace q4k

@@ -40,15 +40,20 @@ struct GemvParams {
     int K;                   // values per row
     int nb;                  // super-blocks per row (K/256)
     int G;                   // groups of 8 super-blocks per row
-    int ntiles;              // ceil(M / R)
+    int ntiles;              // ceil(M / R) (ceil(M / rpw) for the block-per-lane kernel)
     int vec_ok;              // F32 activation 16-B aligned with ldx % 4 == 0
+    int rpw;                 // block-per-lane kernel: rows per wave pass (64/nb or 1)
+    int rows_base;           // tile kernel: each wave owns rows_base rows,
+    int rows_extra;          //   the first rows_extra waves one more
+    int prologue;            // tile kernel: prologue order (see gemv_q4k_kernel)
+    FastDiv nblk32;          // division by K/32 (Q8_1 blocks per column)
 };
 
+// Loads group i (8 super-blocks) of rows [row0, row0 + nrows), nrows <= R;
+// the rows past nrows and blocks past the row's end read as 0.
 template <int R>
-__device__ __forceinline__ void load_group(const GemvParams &p, int tile, int i, int g, int part,
-                                           u32x4 (&wq)[R], u32x4 (&wh)[R]) {
-    const int row0 = tile * R;
-    const int nrows = min(R, p.M - row0);
+__device__ __forceinline__ void load_group(const GemvParams &p, int row0, int nrows, int i, int g,
+                                           int part, u32x4 (&wq)[R], u32x4 (&wh)[R]) {
     const uint8_t *base = p.w + (int64_t)row0 * p.row_stride;
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nrows * p.row_stride));
     const int kb = 8 * i + g;
@@ -61,113 +66,435 @@ __device__ __forceinline__ void load_group(const GemvParams &p, int tile, int i,
     }
 }
 
+// Position of a wave in its sequence of (row tile, group) steps.
+struct Step {
+    int tile;
+    int i;
+};
+
+__device__ __forceinline__ Step next_step(Step s, int G) {
+    return s.i + 1 == G ? Step{s.tile + 1, 0} : Step{s.tile, s.i + 1};
+}
+
+// Per-lane constants of the lane map.
+struct Lane {
+    int lane, g, part, jp, h;
+    ScaleSel sel;
+};
+
+// The contiguous rows [beg, end) a wave owns: M rows split as evenly as
+// possible over all waves of the grid.
+struct WaveRows {
+    int beg, end;
+};
+
+__device__ __forceinline__ WaveRows wave_rows(const GemvParams &p, int gw) {
+    const int beg = gw * p.rows_base + min(gw, p.rows_extra);
+    return WaveRows{beg, beg + p.rows_base + (gw < p.rows_extra ? 1 : 0)};
+}
+
+template <int R>
+__device__ __forceinline__ void load_step(const GemvParams &p, const Lane &ln, const WaveRows &wr,
+                                          Step st, u32x4 (&wq)[R], u32x4 (&wh)[R]) {
+    const int row0 = wr.beg + st.tile * R;
+    load_group<R>(p, row0, min(R, wr.end - row0), st.i, ln.g, ln.part, wq, wh);
+}
+
+// Consumes one group (8 super-blocks of R rows) held in wq/wh; on the last
+// group of a tile reduces the R x NC sums over the wave and stores them.
+template <int NC, int R>
+__device__ __forceinline__ void process_group(const GemvParams &p, const Lane &ln,
+                                              const WaveRows &wr, Step st, const int8_t *q8s,
+                                              const float *d8s, const u32x4 (&wq)[R],
+                                              const u32x4 (&wh)[R], float (&acc)[R][NC]) {
+    const int K = p.K;
+    const int kb = 8 * st.i + ln.g;
+    const int kbc = kb < p.nb ? kb : 0;
+    u32x4 alo[NC], ahi[NC];
+    float d8a[NC], d8b[NC], ka[NC], kbv[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int8_t *qa = q8s + c * K + kbc * kQK + ln.jp * 64 + ln.h * 16;
+        alo[c] = *reinterpret_cast<const u32x4 *>(qa);
+        ahi[c] = *reinterpret_cast<const u32x4 *>(qa + 32);
+        const float2 dd = *reinterpret_cast<const float2 *>(d8s + c * (K / 32) + kbc * 8 + ln.jp * 2);
+        d8a[c] = dd.x;
+        d8b[c] = dd.y;
+        ka[c] = dd.x * (float)byte_sum16(alo[c]);
+        kbv[c] = dd.y * (float)byte_sum16(ahi[c]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t scm = unpack_scale_min(wh[r], ln.sel);
+        const int sca = (int)(scm & 0xffu);
+        const int scb = (int)((scm >> 8) & 0xffu);
+        const float maf = (float)((scm >> 16) & 0xffu);
+        const float mbf = (float)(scm >> 24);
+        const float d = half_bits_to_float(wh[r][0]);
+        const float dmin = half_bits_to_float(wh[r][0] >> 16);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            int sa, sb;
+            lane_qdot(wq[r], alo[c], ahi[c], sa, sb);
+            // |sa|, |sb| <= 16*15*127 and sc <= 63: 24-bit products are exact
+            const float xs = d8a[c] * (float)__mul24(sa, sca) + d8b[c] * (float)__mul24(sb, scb);
+            const float ms = ka[c] * maf + kbv[c] * mbf;
+            acc[r][c] = fmaf(d, xs, acc[r][c]);
+            acc[r][c] = fmaf(-dmin, ms, acc[r][c]);
+        }
+    }
+    if (st.i == p.G - 1) {
+        float out = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float s = wave_sum(acc[r][c]);
+                if (ln.lane == r * NC + c) out = s;
+                acc[r][c] = 0.0f;
+            }
+        const int r = ln.lane / NC;
+        const int c = ln.lane - r * NC;
+        const int row = wr.beg + st.tile * R + r;
+        if (ln.lane < R * NC && row < wr.end) p.dst[(int64_t)c * p.ld_dst + row] = out;
+    }
+}
+
+// Tile kernel: any K, 1..8 columns.  One workgroup per CU (the launch asks
+// for enough LDS to keep a second one off the CU); each wave owns a
+// contiguous range of rows and walks it R rows x one group at a time, two
+// groups in flight.  Every wave issues its activation loads, the workgroup
+// passes a barrier, and only then are weight loads issued: a CU serves
+// vector memory requests in order, so an activation load queued behind the
+// weight stream would stall the whole workgroup's prologue.
 template <int NC, int R, int WAVES>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float *d8s = reinterpret_cast<float *>(lds + NC * p.K);
 
-    if (p.x) {
-        stage_from_f32(p.x, p.ldx, p.K, NC, p.vec_ok != 0, q8s, d8s);
-    } else {
-        stage_from_q8_1(p.y, p.stride_col_y, p.K, NC, q8s, d8s);
-    }
-    __syncthreads();
-
-    const int lane = threadIdx.x & (kWave - 1);
-    const int g = lane >> 3;
-    const int part = lane & 7;
-    const int jp = part >> 1;
-    const int h = part & 1;
-    const ScaleSel sel = make_scale_sel(jp);
-    const int K = p.K;
-    const int nblk32 = K / 32;
+    Lane ln;
+    ln.lane = threadIdx.x & (kWave - 1);
+    ln.g = ln.lane >> 3;
+    ln.part = ln.lane & 7;
+    ln.jp = ln.part >> 1;
+    ln.h = ln.part & 1;
+    ln.sel = make_scale_sel(ln.jp);
 
     // the wave index is wave-uniform; readfirstlane lets the compiler keep
-    // tile numbers and buffer descriptors in scalar registers
-    int tile = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int tstride = gridDim.x * WAVES;
-    if (tile >= p.ntiles) return;  // no barrier below this point
+    // row numbers and buffer descriptors in scalar registers
+    const int gw = blockIdx.x * (int)(blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const WaveRows wr = wave_rows(p, gw);
+    const int ntiles = (wr.end - wr.beg + R - 1) / R;
+    const bool active = ntiles > 0;
 
-    u32x4 wq[R], wh[R];
-    load_group<R>(p, tile, 0, g, part, wq, wh);
-    int i = 0;
+    ActStage xs;
+    Q81Stage ys;
+    if (p.x) stage_f32_issue(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+    else stage_q81_issue(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+    __syncthreads();  // all activation loads of this CU are queued first
+
+    // Prologue order (p.prologue): 0 -- the first two groups' weight loads
+    // go out before the activation is quantised; 1 -- the activation is
+    // quantised first and the weight loads follow (it then never waits
+    // behind the weight stream); 2 -- one group goes out first, the second
+    // after quantisation.
+    Step a{0, 0};
+    Step b = next_step(a, p.G);
+    bool vb = active && b.tile < ntiles;
+    u32x4 qa[R], ha[R], qb[R], hb[R];
+    if (p.prologue != 1) {
+        if (active) load_step<R>(p, ln, wr, a, qa, ha);
+        if (vb && p.prologue == 0) load_step<R>(p, ln, wr, b, qb, hb);
+    }
+    if (p.x) stage_f32_finish(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, q8s, d8s);
+    else stage_q81_finish(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, q8s, d8s);
+    __syncthreads();
+    if (!active) return;  // no barrier below this point
+    if (p.prologue == 1) load_step<R>(p, ln, wr, a, qa, ha);
+    if (vb && p.prologue != 0) load_step<R>(p, ln, wr, b, qb, hb);
+
     float acc[R][NC];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
 
+    // two register slots: while one group is consumed the next is in flight
     for (;;) {
-        int ni = i + 1, ntile = tile;
-        if (ni == p.G) {
-            ni = 0;
-            ntile += tstride;
-        }
-        const bool more = ntile < p.ntiles;
-        u32x4 nq[R], nh[R];
-        if (more) load_group<R>(p, ntile, ni, g, part, nq, nh);
+        process_group<NC, R>(p, ln, wr, a, q8s, d8s, qa, ha, acc);
+        if (!vb) break;
+        const Step a2 = next_step(b, p.G);
+        const bool va2 = a2.tile < ntiles;
+        if (va2) load_step<R>(p, ln, wr, a2, qa, ha);
+        process_group<NC, R>(p, ln, wr, b, q8s, d8s, qb, hb, acc);
+        if (!va2) break;
+        const Step b2 = next_step(a2, p.G);
+        vb = b2.tile < ntiles;
+        if (vb) load_step<R>(p, ln, wr, b2, qb, hb);
+        a = a2;
+        b = b2;
+    }
+}
 
-        // activation slice of this lane for group i
-        const int kb = 8 * i + g;
-        const int kbc = kb < p.nb ? kb : 0;
-        u32x4 alo[NC], ahi[NC];
-        float d8a[NC], d8b[NC], ka[NC], kbv[NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int8_t *qa = q8s + c * K + kbc * kQK + jp * 64 + h * 16;
-            alo[c] = *reinterpret_cast<const u32x4 *>(qa);
-            ahi[c] = *reinterpret_cast<const u32x4 *>(qa + 32);
-            const float2 dd = *reinterpret_cast<const float2 *>(d8s + c * nblk32 + kbc * 8 + jp * 2);
-            d8a[c] = dd.x;
-            d8b[c] = dd.y;
-            ka[c] = dd.x * (float)byte_sum16(alo[c]);
-            kbv[c] = dd.y * (float)byte_sum16(ahi[c]);
-        }
+// ------------------------------------------------------------------------
+// Block-per-lane kernel (one activation column, nb <= 64 super-blocks per row)
+//
+// Lane l owns super-block kb = l % nb of row l / nb in each "pass" of rpw
+// rows (rpw = 64/nb for nb = 16 or 32, else 1 with lanes >= nb idle).  Its
+// 144 weight bytes arrive as nine 16-byte loads and the matching 256-value
+// activation slice stays in registers for the whole kernel, so the per-block
+// work -- scale/min unpack, eight sub-block scalings, the min term -- is paid
+// once per 144 bytes instead of once per 16.
+// ------------------------------------------------------------------------
 
+__device__ __forceinline__ void load_pass(const GemvParams &p, int pass, int rr, int kb, bool lane_on,
+                                          u32x4 (&w)[9]) {
+    const int row0 = pass * p.rpw;
+    const int nrows = min(p.rpw, p.M - row0);
+    const uint8_t *base = p.w + (int64_t)row0 * p.row_stride;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nrows * p.row_stride));
+    const uint32_t off = lane_on ? (uint32_t)(rr * p.row_stride) + (uint32_t)kb * kBlockBytes : kOOB;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint32_t scm = unpack_scale_min(wh[r], sel);
-            const int sca = (int)(scm & 0xffu);
-            const int scb = (int)((scm >> 8) & 0xffu);
-            const float maf = (float)((scm >> 16) & 0xffu);
-            const float mbf = (float)(scm >> 24);
-            const float d = half_bits_to_float(wh[r][0]);
-            const float dmin = half_bits_to_float(wh[r][0] >> 16);
+    for (int t = 0; t < 9; ++t) w[t] = load16(rs, off + 16u * t);
+}
+
+// Sum over the nb lanes of each row segment (nb = 16, 32 or the whole wave);
+// the result is valid in the segment's first lane.
+__device__ __forceinline__ float segment_sum(float v, int nb) {
+    v += dppf<kDppXor1>(v);
+    v += dppf<kDppXor2>(v);
+    v += dppf<kDppRor4>(v);
+    v += dppf<kDppRor8>(v);
+    if (nb == 16) return v;
+    v += swizzle_xor<16>(v);
+    if (nb == 32) return v;
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    return v + hi;
+}
+
+struct BlockAct {
+    u32x4 q[16];   // 256 int8 activation values of the lane's super-block
+    float d8[8];   // per sub-block scale
+    float km[8];   // d8 * sum of the sub-block's q8 (the min term's factor)
+};
+
+__device__ __forceinline__ float block_dot(const u32x4 (&w)[9], const BlockAct &a) {
+    const u32x4 h = w[0];
+    const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+    const uint32_t m03 = h[2] & 0x3f3f3f3fu;
+    const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+    const uint32_t m47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+    float xs = 0.0f, ys = 0.0f;
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                int sa, sb;
-                lane_qdot(wq[r], alo[c], ahi[c], sa, sb);
-                const float xs = d8a[c] * (float)(sa * sca) + d8b[c] * (float)(sb * scb);
-                const float ms = ka[c] * maf + kbv[c] * mbf;
-                acc[r][c] = fmaf(d, xs, acc[r][c]);
-                acc[r][c] = fmaf(-dmin, ms, acc[r][c]);
+    for (int c = 0; c < 4; ++c) {  // 32-byte chunk c: sub-blocks 2c (low) and 2c+1 (high)
+        int slo = 0, shi = 0;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const u32x4 wv = w[1 + 2 * c + hh];
+            const u32x4 alo = a.q[4 * c + hh];
+            const u32x4 ahi = a.q[4 * c + 2 + hh];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                slo = __builtin_amdgcn_sdot4((int)(wv[k] & 0x0f0f0f0fu), (int)alo[k], slo, false);
+                shi = __builtin_amdgcn_sdot4((int)((wv[k] >> 4) & 0x0f0f0f0fu), (int)ahi[k], shi, false);
             }
         }
+        const int s0 = 2 * c, s1 = 2 * c + 1;
+        const uint32_t scw = s0 < 4 ? sc03 : sc47;
+        const uint32_t mw = s0 < 4 ? m03 : m47;
+        const int sh0 = 8 * (s0 & 3), sh1 = 8 * (s1 & 3);
+        const int sc0 = (int)((scw >> sh0) & 0xffu), sc1 = (int)((scw >> sh1) & 0xffu);
+        xs = fmaf(a.d8[s0], (float)__mul24(slo, sc0), xs);
+        xs = fmaf(a.d8[s1], (float)__mul24(shi, sc1), xs);
+        ys = fmaf(a.km[s0], (float)((mw >> sh0) & 0xffu), ys);
+        ys = fmaf(a.km[s1], (float)((mw >> sh1) & 0xffu), ys);
+    }
+    const float d = half_bits_to_float(h[0]);
+    const float dmin = half_bits_to_float(h[0] >> 16);
+    return fmaf(d, xs, -dmin * ys);
+}
 
-        if (i == p.G - 1) {
-            float out = 0.0f;
+__device__ __forceinline__ void finish_pass(const GemvParams &p, int pass, int rr, int kb, bool lane_on,
+                                            float part) {
+    const float s = segment_sum(part, p.nb);
+    const int row = pass * p.rpw + rr;
+    if (lane_on && kb == 0 && row < p.M) p.dst[row] = s;
+}
+
+template <int WAVES>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(GemvParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    int8_t *q8s = reinterpret_cast<int8_t *>(lds);
+    float *d8s = reinterpret_cast<float *>(lds + p.K);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int rr = lane / p.nb;
+    const int kb = lane - rr * p.nb;
+    const bool lane_on = rr < p.rpw;
+
+    const int tstride = gridDim.x * WAVES;
+    int pa = blockIdx.x * WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool active = pa < p.ntiles;
+    int pb = pa + tstride;
+    bool vb = active && pb < p.ntiles;
+
+    // activation loads first (the whole workgroup), then the weight loads of
+    // each wave's first two passes
+    ActStage xs;
+    Q81Stage ys;
+    if (p.x) stage_f32_issue(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
+    else stage_q81_issue(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
+    __syncthreads();
+    u32x4 wa[9], wb[9];
+    if (active) load_pass(p, pa, rr, kb, lane_on, wa);
+    if (vb) load_pass(p, pb, rr, kb, lane_on, wb);
+    if (p.x) stage_f32_finish(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, q8s, d8s);
+    else stage_q81_finish(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, q8s, d8s);
+    __syncthreads();
+    if (!active) return;  // no barrier below this point
+
+    BlockAct act;
+    {
+        const int8_t *src = q8s + kb * kQK;
 #pragma unroll
-            for (int r = 0; r < R; ++r)
+        for (int t = 0; t < 16; ++t) act.q[t] = *reinterpret_cast<const u32x4 *>(src + 16 * t);
 #pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    const float s = wave_sum(acc[r][c]);
-                    if (lane == r * NC + c) out = s;
-                    acc[r][c] = 0.0f;
-                }
-            const int r = lane / NC;
-            const int c = lane - r * NC;
-            const int row = tile * R + r;
-            if (lane < R * NC && row < p.M) p.dst[(int64_t)c * p.ld_dst + row] = out;
+        for (int s = 0; s < 8; ++s) {
+            act.d8[s] = d8s[kb * 8 + s];
+            act.km[s] = act.d8[s] * (float)(byte_sum16(act.q[2 * s]) + byte_sum16(act.q[2 * s + 1]));
         }
-        if (!more) break;
+    }
+
+    for (;;) {
+        finish_pass(p, pa, rr, kb, lane_on, block_dot(wa, act));
+        if (!vb) break;
+        const int pa2 = pb + tstride;
+        const bool va2 = pa2 < p.ntiles;
+        if (va2) load_pass(p, pa2, rr, kb, lane_on, wa);
+        finish_pass(p, pb, rr, kb, lane_on, block_dot(wb, act));
+        if (!va2) break;
+        const int pb2 = pa2 + tstride;
+        vb = pb2 < p.ntiles;
+        if (vb) load_pass(p, pb2, rr, kb, lane_on, wb);
+        pa = pa2;
+        pb = pb2;
+    }
+}
+
+// ------------------------------------------------------------------------
+// Block kernel: the block-per-lane arithmetic with coalesced loads.
+//
+// A pass (rpw rows x nb super-blocks, at most 64 blocks = 9216 bytes) is
+// loaded with nine fully coalesced 16-byte loads -- lane l gets bytes
+// [1024t + 16l, +16) of the pass -- written unchanged into a wave-private LDS
+// slot, and read back by each lane as its own 144-byte block (stride 144 B
+// is free of bank conflicts for 16-byte LDS reads).  Two passes are in
+// flight per wave.
+// ------------------------------------------------------------------------
+
+constexpr int kSlotBytes = 64 * kBlockBytes;  // 9216
+
+struct PassOffsets {
+    uint32_t o[9];  // buffer offset of each of the lane's nine loads
+};
+
+__device__ __forceinline__ PassOffsets pass_offsets(const GemvParams &p, int lane) {
+    const int row_bytes = p.nb * kBlockBytes;
+    const int span = p.rpw * row_bytes;
+    PassOffsets po;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            wq[r] = nq[r];
-            wh[r] = nh[r];
+    for (int t = 0; t < 9; ++t) {
+        const int lin = 1024 * t + 16 * lane;
+        int r = 0;
+        while (r + 1 < p.rpw && lin >= (r + 1) * row_bytes) ++r;
+        po.o[t] = lin < span ? (uint32_t)(r * p.row_stride + (lin - r * row_bytes)) : kOOB;
+    }
+    return po;
+}
+
+__device__ __forceinline__ void load_pass_coalesced(const GemvParams &p, int pass, const PassOffsets &po,
+                                                    u32x4 (&w)[9]) {
+    const int row0 = pass * p.rpw;
+    const int nrows = min(p.rpw, p.M - row0);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(p.w + (int64_t)row0 * p.row_stride, (uint32_t)(nrows * p.row_stride));
+#pragma unroll
+    for (int t = 0; t < 9; ++t) w[t] = load16(rs, po.o[t]);
+}
+
+// landing registers -> LDS slot (pass order) -> this lane's 144-byte block
+__device__ __forceinline__ void transpose_pass(uint8_t *slot, int lane, const u32x4 (&w)[9],
+                                               u32x4 (&blk)[9]) {
+#pragma unroll
+    for (int t = 0; t < 9; ++t) *reinterpret_cast<u32x4 *>(slot + 1024 * t + 16 * lane) = w[t];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) blk[t] = *reinterpret_cast<const u32x4 *>(slot + kBlockBytes * lane + 16 * t);
+}
+
+template <int WAVES>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(GemvParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    int8_t *q8s = reinterpret_cast<int8_t *>(lds);
+    float *d8s = reinterpret_cast<float *>(lds + p.K);
+    const int act_bytes = (p.K + p.K / 8 + 15) & ~15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint8_t *slot = lds + act_bytes + wave * kSlotBytes;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int rr = lane / p.nb;
+    const int kb = lane - rr * p.nb;
+    const bool lane_on = rr < p.rpw;
+
+    const int tstride = gridDim.x * (int)(blockDim.x >> 6);
+    int pa = blockIdx.x * (int)(blockDim.x >> 6) + wave;
+    const bool active = pa < p.ntiles;
+    int pb = pa + tstride;
+    bool vb = active && pb < p.ntiles;
+    const PassOffsets po = pass_offsets(p, lane);
+
+    // activation loads first (the whole workgroup), then the weight loads of
+    // each wave's first two passes
+    ActStage xs;
+    Q81Stage ys;
+    if (p.x) stage_f32_issue(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
+    else stage_q81_issue(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
+    __syncthreads();
+    u32x4 wa[9], wb[9];
+    if (active) load_pass_coalesced(p, pa, po, wa);
+    if (vb) load_pass_coalesced(p, pb, po, wb);
+    if (p.x) stage_f32_finish(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, q8s, d8s);
+    else stage_q81_finish(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, q8s, d8s);
+    __syncthreads();
+    if (!active) return;  // no barrier below this point
+
+    BlockAct act;
+    {
+        const int8_t *src = q8s + kb * kQK;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) act.q[t] = *reinterpret_cast<const u32x4 *>(src + 16 * t);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            act.d8[s] = d8s[kb * 8 + s];
+            act.km[s] = act.d8[s] * (float)(byte_sum16(act.q[2 * s]) + byte_sum16(act.q[2 * s + 1]));
         }
-        tile = ntile;
-        i = ni;
+    }
+
+    u32x4 blk[9];
+    for (;;) {
+        transpose_pass(slot, lane, wa, blk);
+        const int pa2 = pb + tstride;
+        const bool va2 = vb && pa2 < p.ntiles;
+        if (va2) load_pass_coalesced(p, pa2, po, wa);
+        finish_pass(p, pa, rr, kb, lane_on, block_dot(blk, act));
+        if (!vb) break;
+        transpose_pass(slot, lane, wb, blk);
+        const int pb2 = pa2 + tstride;
+        const bool vb2 = va2 && pb2 < p.ntiles;
+        if (vb2) load_pass_coalesced(p, pb2, po, wb);
+        finish_pass(p, pb, rr, kb, lane_on, block_dot(blk, act));
+        if (!va2) break;
+        pa = pa2;
+        pb = pb2;
+        vb = vb2;
     }
 }
 
@@ -207,6 +534,7 @@ struct SumsParams {
     int32_t *sqq;      // [M][K/32] for this column
     int32_t *sq;       // [K/32] for this column
     int M, K, nb, G;
+    FastDiv nblk32;
 };
 
 // One wave per (row, group): the GEMV's lane map and lane_qdot, then the two
@@ -215,7 +543,7 @@ __global__ __launch_bounds__(256) void subblock_sums_kernel(SumsParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float *d8s = reinterpret_cast<float *>(lds + p.K);
-    stage_from_q8_1(p.y, 0, p.K, 1, q8s, d8s);
+    stage_from_q8_1(p.y, 0, p.K, 1, p.nblk32, q8s, d8s);
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int g = lane >> 3, part = lane & 7, jp = part >> 1, h = part & 1;
@@ -230,7 +558,7 @@ __global__ __launch_bounds__(256) void subblock_sums_kernel(SumsParams p) {
         gp.row_stride = p.row_stride;
         gp.M = p.M;
         gp.nb = p.nb;
-        load_group<1>(gp, row, i, g, part, wq, wh);
+        load_group<1>(gp, row, 1, i, g, part, wq, wh);
         const int kb = 8 * i + g;
         const int kbc = kb < p.nb ? kb : 0;
         const int8_t *qa = q8s + kbc * kQK + jp * 64 + h * 16;
@@ -319,43 +647,125 @@ static int env_int(const char *name, int dflt) {
     return v && *v ? std::atoi(v) : dflt;
 }
 
+// Geometry overrides for tuning sweeps (0 = automatic): set through
+// q4k_set_geometry_override or, as start-up defaults, the environment
+// variables Q4K_ROWS, Q4K_WAVES and Q4K_WGS.
+static std::atomic<int> g_ovr_rows{-1}, g_ovr_waves{-1}, g_ovr_wgs{-1}, g_ovr_kernel{-1};
+static std::atomic<int> g_ovr_prologue{-1};
+
+static void load_env_overrides() {
+    static std::once_flag once;
+    std::call_once(once, []() {
+        int expect = -1;
+        g_ovr_rows.compare_exchange_strong(expect, env_int("Q4K_ROWS", 0));
+        expect = -1;
+        g_ovr_waves.compare_exchange_strong(expect, env_int("Q4K_WAVES", 0));
+        expect = -1;
+        g_ovr_wgs.compare_exchange_strong(expect, env_int("Q4K_WGS", 0));
+        expect = -1;
+        g_ovr_kernel.compare_exchange_strong(expect, env_int("Q4K_KERNEL", 0));
+        expect = -1;
+        g_ovr_prologue.compare_exchange_strong(expect, env_int("Q4K_PROLOGUE", -1));
+    });
+}
+
 struct Geometry {
-    int R = 4;
-    int waves = 4;
-    int grid = 0;
-    int lds = 0;
-    int nc_chunk = 1;
-    int ntiles = 0;
+    int R = 2;          // tile kernel: rows per wave tile
+    int waves = 16;     // waves per workgroup
+    int grid = 0;       // workgroups
+    int lds = 0;        // LDS bytes the activation needs
+    int lds_launch = 0; // LDS bytes requested at launch (>= lds)
+    int nc_chunk = 1;   // columns per launch
+    int ntiles = 0;     // block-per-lane kernel: passes
+    int bpl = 0;        // 1: block-per-lane kernel
+    int rpw = 0;        // block-per-lane kernel: rows per pass
+    int rows_base = 0;  // tile kernel: rows per wave (first rows_extra waves +1)
+    int rows_extra = 0;
+    int prologue = 0;   // tile kernel prologue order
 };
+
+// Rows per pass of the block-per-lane kernel, 0 when it does not apply.
+static int bpl_rows_per_pass(int64_t nb) {
+    if (nb == 16) return 4;
+    if (nb == 32) return 2;
+    if (nb > 32 && nb <= 64) return 1;
+    return 0;
+}
 
 static int lds_bytes(int K, int nc) { return nc * (K + K / 8); }
 
-// Rows per wave tile, waves per workgroup and grid for an (M, K, N) product.
-// Environment overrides for sweeps: Q4K_ROWS (1, 2, 4), Q4K_WAVES (4, 8),
-// Q4K_WGS (workgroups), Q4K_WGS_PER_CU.
+// Launch geometry for an (M, K, N) product.
+//  tile kernel: one workgroup per CU (requesting just over half the CU's LDS
+//    keeps a second one away), 16 waves (8 when 5+ columns need more
+//    registers), the M rows split evenly over all waves, 2 rows per tile
+//    once waves own 2 or more rows.
+//  block-per-lane kernel (one column, 16..64 super-blocks per row): 4-wave
+//    workgroups, 2 per CU, two passes per wave in flight.
 static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N) {
+    load_env_overrides();
     Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
+    const int cus = di.cus > 0 ? di.cus : 1;
     int nc = (int)N;
     while (nc > 1 && lds_bytes((int)K, nc) > max_lds) nc = (nc + 1) / 2;
     g.nc_chunk = nc;
     g.lds = lds_bytes((int)K, nc);
-    g.R = nc == 1 ? 4 : 2;
-    g.waves = g.lds > 40 * 1024 ? 8 : 4;
-    g.R = env_int("Q4K_ROWS", g.R);
-    if (g.R != 1 && g.R != 2 && g.R != 4) g.R = 2;
-    g.waves = env_int("Q4K_WAVES", g.waves);
-    if (g.waves != 4 && g.waves != 8) g.waves = 4;
-    g.ntiles = (int)((M + g.R - 1) / g.R);
-    const int wg_needed = (g.ntiles + g.waves - 1) / g.waves;
-    int per_cu = max_lds / (g.lds > 0 ? g.lds : 1);
-    if (per_cu < 1) per_cu = 1;
-    if (per_cu > 8) per_cu = 8;
-    per_cu = env_int("Q4K_WGS_PER_CU", per_cu);
-    int wgs = di.cus * per_cu;
-    wgs = env_int("Q4K_WGS", wgs);
-    if (wgs < 1) wgs = 1;
-    g.grid = wg_needed < wgs ? wg_needed : wgs;
+    const int orows = g_ovr_rows.load(), owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load();
+    const int okern = g_ovr_kernel.load();
+    const int rpw = bpl_rows_per_pass(K / kQK);
+    if (N == 1 && rpw > 0 && okern == 3) {
+        // block kernel: ~2 waves per SIMD; activation + one 9216-byte LDS
+        // slot per wave
+        g.bpl = 2;
+        g.rpw = rpw;
+        g.waves = (owaves >= 1 && owaves <= 8) ? owaves : 8;
+        g.ntiles = (int)((M + rpw - 1) / rpw);
+        const int wg_needed = (g.ntiles + g.waves - 1) / g.waves;
+        int wgs = cus;
+        if (owgs > 0) wgs = owgs;
+        g.grid = wg_needed < wgs ? wg_needed : wgs;
+        g.lds_launch = ((g.lds + 15) & ~15) + g.waves * kSlotBytes;
+        return g;
+    }
+    // Large single-column products stream long enough for the block-per-lane
+    // kernel's lower instruction count to win; short ones are bound by the
+    // activation prologue and the launch, where the tile kernel's 16 waves
+    // per CU do better (measured on MI355X).
+    const int64_t weight_bytes = M * (K / kQK) * kBlockBytes;
+    const bool auto_bpl = okern == 0 && weight_bytes >= (48ll << 20);
+    if (N == 1 && rpw > 0 && (okern == 2 || auto_bpl)) {
+        // ~173 VGPRs: two waves per SIMD; 4-wave workgroups, two per CU
+        g.bpl = 1;
+        g.rpw = rpw;
+        g.waves = (owaves == 4 || owaves == 8) ? owaves : 4;
+        g.ntiles = (int)((M + rpw - 1) / rpw);
+        const int wg_needed = (g.ntiles + g.waves - 1) / g.waves;
+        int wgs = cus * (8 / g.waves);
+        if (owgs > 0) wgs = owgs;
+        g.grid = wg_needed < wgs ? wg_needed : wgs;
+        g.lds_launch = g.lds;
+        return g;
+    }
+    g.waves = nc <= 4 ? 16 : 8;
+    if (owaves >= 1 && owaves <= 16) g.waves = owaves;
+    g.grid = owgs > 0 ? owgs : cus;
+    const int64_t total_waves = (int64_t)g.grid * g.waves;
+    g.rows_base = (int)(M / total_waves);
+    g.rows_extra = (int)(M % total_waves);
+    g.R = g.rows_base >= 2 ? 2 : 1;
+    if (orows == 1 || orows == 2 || orows == 4) g.R = orows;
+    // 16-wave launch bounds cap a lane at 128 VGPRs: only these variants fit
+    const bool fits16 = g.R == 1 || (g.R == 2 && nc <= 4) || (g.R == 4 && nc <= 2);
+    if (g.waves > 8 && !fits16) {
+        g.waves = 8;
+        const int64_t tw = (int64_t)g.grid * g.waves;
+        g.rows_base = (int)(M / tw);
+        g.rows_extra = (int)(M % tw);
+    }
+    g.lds_launch = g.lds;
+    if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
+    const int opro = g_ovr_prologue.load();
+    if (opro >= 0 && opro <= 2) g.prologue = opro;
     return g;
 }
 
@@ -381,25 +791,39 @@ static const void *gemv_sym_nc(int nc) {
     }
 }
 
+// Instantiations: R in {1, 2, 4}; launch bounds of 8 or 16 waves.
 static const void *gemv_kernel_for(int nc, int R, int waves) {
-    if (waves == 4) {
-        if (R == 1) return gemv_sym_nc<1, 4>(nc);
-        if (R == 2) return gemv_sym_nc<2, 4>(nc);
-        return gemv_sym_nc<4, 4>(nc);
+    if (waves <= 8) {
+        if (R == 1) return gemv_sym_nc<1, 8>(nc);
+        if (R == 2) return gemv_sym_nc<2, 8>(nc);
+        return gemv_sym_nc<4, 8>(nc);
     }
-    if (R == 1) return gemv_sym_nc<1, 8>(nc);
-    if (R == 2) return gemv_sym_nc<2, 8>(nc);
-    return gemv_sym_nc<4, 8>(nc);
+    if (R == 1) return gemv_sym_nc<1, 16>(nc);
+    if (R == 2) return gemv_sym_nc<2, 16>(nc);
+    return gemv_sym_nc<4, 16>(nc);
 }
 
 static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc, hipStream_t stream) {
-    const void *fn = gemv_kernel_for(nc, geo.R, geo.waves);
+    const void *fn = nullptr;
+    if (geo.bpl == 2 && nc == 1) {
+        fn = reinterpret_cast<const void *>(&gemv_q4k_blk_kernel<8>);
+        p.rpw = geo.rpw;
+    } else if (geo.bpl == 1 && nc == 1) {
+        fn = geo.waves == 8 ? reinterpret_cast<const void *>(&gemv_q4k_bpl_kernel<8>)
+                            : reinterpret_cast<const void *>(&gemv_q4k_bpl_kernel<4>);
+        p.rpw = geo.rpw;
+    } else {
+        fn = gemv_kernel_for(nc, geo.R, geo.waves);
+        p.rows_base = geo.rows_base;
+        p.rows_extra = geo.rows_extra;
+        p.prologue = geo.prologue;
+    }
     if (!fn) return Q4K_EINVAL;
-    int st = ensure_lds(di, fn, geo.lds);
+    int st = ensure_lds(di, fn, geo.lds_launch);
     if (st != Q4K_OK) return st;
     void *args[] = {&p};
-    hipError_t e = hipLaunchKernel(fn, dim3(geo.grid), dim3(kWave * geo.waves), args, (size_t)geo.lds,
-                                   stream);
+    hipError_t e = hipLaunchKernel(fn, dim3(geo.grid), dim3(kWave * geo.waves), args,
+                                   (size_t)geo.lds_launch, stream);
     if (e != hipSuccess) return hip_fail(e);
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e);
@@ -434,6 +858,7 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
         g2.lds = lds_bytes((int)ne00, nc);
+        if (g2.lds_launch < g2.lds) g2.lds_launch = g2.lds;
         GemvParams p{};
         p.w = static_cast<const uint8_t *>(src0);
         p.row_stride = nb01;
@@ -449,6 +874,7 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
         p.G = (p.nb + 7) / 8;
         p.ntiles = geo.ntiles;
         p.vec_ok = x && aligned(p.x, 16) && (ldx % 4 == 0);
+        p.nblk32 = fastdiv_init((uint32_t)(ne00 / 32));
         st = launch_gemv(di, g2, p, nc, stream);
         if (st != Q4K_OK) return st;
     }
@@ -609,6 +1035,7 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
         p.K = (int)ne00;
         p.nb = nb;
         p.G = (nb + 7) / 8;
+        p.nblk32 = fastdiv_init((uint32_t)(ne00 / 32));
         const int64_t items = ne01 * p.G;
         int grid = (int)((items + 3) / 4);
         if (grid > di->cus * 8) grid = di->cus * 8;
@@ -620,7 +1047,22 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
     return Q4K_OK;
 }
 
-int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[6]) {
+int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32_t workgroups,
+                              int32_t kernel) {
+    if (rows_per_tile < 0 || waves_per_wg < 0 || workgroups < 0) return Q4K_EINVAL;
+    if (kernel < 0 || kernel > 3) return Q4K_EINVAL;
+    if (rows_per_tile != 0 && rows_per_tile != 1 && rows_per_tile != 2 && rows_per_tile != 4)
+        return Q4K_EINVAL;
+    if (waves_per_wg < 0 || waves_per_wg > 16) return Q4K_EINVAL;
+    load_env_overrides();
+    g_ovr_rows.store(rows_per_tile);
+    g_ovr_waves.store(waves_per_wg);
+    g_ovr_wgs.store(workgroups);
+    g_ovr_kernel.store(kernel);
+    return Q4K_OK;
+}
+
+int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) {
     if (!out || ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0 || ne11 < 1 || ne11 > Q4K_MAX_BATCH)
         return Q4K_EINVAL;
     DeviceInfo *di = nullptr;
@@ -630,9 +1072,11 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[6]) 
     out[0] = g.R;
     out[1] = g.waves;
     out[2] = g.grid;
-    out[3] = g.lds;
+    out[3] = g.lds_launch;
     out[4] = g.nc_chunk;
     out[5] = g.nc_chunk >= ne11 ? 1 : 0;
+    out[6] = g.bpl == 2 ? 3 : (g.bpl ? 2 : 1);
+    out[7] = g.bpl ? g.rpw : g.R;
     return Q4K_OK;
 }
 

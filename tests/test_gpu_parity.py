@@ -71,7 +71,9 @@ def test_subblock_sums_exact(Q, O, gpu, M, K, N):
 
 # ------------------------------------------------------ small shapes ----
 EDGE_SHAPES = [(1, 256, 1), (3, 768, 2), (5, 2304, 3), (17, 4352, 5), (64, 8192, 8),
-               (129, 1024, 7), (1000, 4096, 4), (7, 2048, 6), (2, 512, 8)]
+               (129, 1024, 7), (1000, 4096, 4), (7, 2048, 6), (2, 512, 8),
+               # block-per-lane kernel: 16, 32 and 33..64 super-blocks per row
+               (1001, 4096, 1), (3, 8192, 1), (5, 12288, 1), (130, 16384, 1), (2, 14336, 1)]
 
 
 @pytest.mark.parametrize("M,K,N", EDGE_SHAPES)
@@ -85,6 +87,52 @@ def test_gemv_edge_shapes(Q, O, gpu, M, K, N):
     y2 = Q.op_mul_mat_vec_q(wd, K, to_dev(q8, gpu), N).cpu().numpy()
     _common.assert_within_tolerance(O, y2, ref, f"q8_1 {M}x{K} N={N}")
     assert np.array_equal(y, y2)
+
+
+@pytest.mark.parametrize("M,K", [(999, 4096), (258, 8192), (97, 14336), (64, 16384), (3001, 4096),
+                                 (5, 12288)])
+def test_kernel_variants_against_oracle(Q, O, gpu, M, K):
+    """Every GEMV kernel (tile, block-per-lane, block with coalesced loads) on
+    shapes where each can run, forced through the geometry override."""
+    wq, x = inputs(Q, M, K, 1, seed=7)
+    ref = O.gemv_q4K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    try:
+        for kern in (1, 2, 3):
+            Q.set_geometry_override(kernel=kern)
+            assert Q.geometry(K, M, 1)["kernel"] == kern
+            y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+            _common.assert_within_tolerance(O, y, ref, f"kernel {kern} {M}x{K}")
+    finally:
+        Q.set_geometry_override()
+
+
+def test_fused_quantisation_at_ties(Q, O, gpu):
+    """Activations whose x/d falls exactly on, or one ulp beside, a half-integer:
+    round-half-away (ggml's roundf) and round-half-even differ there, so the
+    in-launch quantiser must take its exact path.  The fused launch must match
+    the standalone quantiser (bytes checked against the oracle) bit for bit."""
+    M, K, N = 64, 4096, 3
+    wq, _ = inputs(Q, M, K, 1, seed=6)
+    rng = np.random.default_rng(6)
+    x = np.zeros((N, K), np.float32)
+    blocks = x.reshape(N, -1, 32)
+    blocks[:, :, 0] = 127.0                      # amax = 127 -> d = 1 exactly
+    halves = (rng.integers(-127, 127, size=blocks[:, :, 1:].shape) + 0.5).astype(np.float32)
+    blocks[:, :, 1:] = halves
+    blocks[1, :, 1:] = np.nextafter(halves[1], np.float32(0))             # one ulp inside
+    blocks[2, ::2, 0] = 100.0                    # d = 100/127: generic quotients
+    blocks[2, ::2, 1:] = rng.uniform(-100, 100, size=blocks[2, ::2, 1:].shape)
+    x = x.reshape(N, K)
+    q8 = O.quantize_q8_1(x)
+    ref = O.gemv_q4K_q8_1(wq, K, q8, want_sums=False)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    q8d = Q.quantize_row_q8_1(xd)
+    assert np.array_equal(q8d.cpu().numpy(), q8)
+    y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    y2 = Q.op_mul_mat_vec_q(wd, K, q8d, N).cpu().numpy()
+    assert np.array_equal(y, y2)
+    _common.assert_within_tolerance(O, y, ref, "ties")
 
 
 def test_zero_activation_and_zero_weight(Q, O, gpu):
@@ -225,9 +273,16 @@ def test_workload_parity(Q, O, gpu, M, K, N):
     q8d = Q.quantize_row_q8_1(xd)
     y2 = Q.op_mul_mat_vec_q(wd, K, q8d, N).cpu().numpy()
     assert np.array_equal(y, y2)
-    # split-mode row slices reassemble the full result exactly
+    # split-mode row slices reassemble the full result: bit for bit when the
+    # slices run the same kernel as the whole product (kernels differ only in
+    # summation order), else each slice within tolerance of the oracle
     cut = (M // 3) // 16 * 16 + 5
     top = Q.op_mul_mat_vec_q(wd[:cut], K, q8d, N, row_low=0, row_high=cut).cpu().numpy()
     bot = Q.op_mul_mat_vec_q(wd[cut:], K, q8d, N, row_low=cut, row_high=M).cpu().numpy()
-    assert np.array_equal(np.concatenate([top, bot], axis=1), y)
+    kern = {Q.geometry(K, m, N)["kernel"] for m in (M, cut, M - cut)}
+    if len(kern) == 1:
+        assert np.array_equal(np.concatenate([top, bot], axis=1), y)
+    else:
+        both = np.concatenate([top, bot], axis=1)
+        _common.assert_within_tolerance(O, both[:, rows], ref, f"split {M}x{K} N={N}")
     assert np.isfinite(y).all()
