@@ -313,8 +313,8 @@ def main():
                     help="run only a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(row sharding across GPUs is described in DESIGN.md); run with --gpus 1.",
+        print("bench.py measures one GPU only: the Q4_K GEMV has no multi-GPU path here "
+              "(rows would shard across GPUs through q4k_op_mul_mat_vec_q); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
     if args.stream_probe:
