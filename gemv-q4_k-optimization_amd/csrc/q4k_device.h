@@ -1,19 +1,21 @@
 // q4k_device.h -- device building blocks of the gfx950 Q4_K GEMV.
 //
-// Wave64 lane map used by every kernel here.  A wave consumes one "group" of
-// 8 consecutive Q4_K super-blocks of one weight row per load instruction:
+// Wave64 lane map of the tile kernel.  A wave consumes one "group" of 16
+// consecutive Q4_K super-blocks of a weight row per step, four lanes per
+// super-block:
 //
-//   lane = 8*g + p        g = block within the group (0..7)
-//                         p = 16-byte part of the block's 128 qs bytes (0..7)
-//   qs bytes [16p, 16p+16) of block kb = 8*i + g
-//     low  nibbles -> elements 64*(p/2) + 16*(p%2) + [0,16)      (sub-block 2*(p/2))
-//     high nibbles -> elements 64*(p/2) + 32 + 16*(p%2) + [0,16) (sub-block 2*(p/2)+1)
+//   lane = 4*g + j        g = super-block within the group (0..15)
+//                         j = 32-byte chunk of the block's 128 qs bytes (0..3)
+//   qs bytes [32j, 32j+32) of block kb = 16*i + g, as two 16-byte loads:
+//     low  nibbles -> elements 64j + [0,32)       (sub-block 2j)
+//     high nibbles -> elements 64j + 32 + [0,32)  (sub-block 2j+1)
 //
-// so the 64 lanes of a wave read 8 x 128 contiguous qs bytes (one 16-byte
-// load each, no idle lanes) and the 16-byte block header (d, dmin, scales)
-// once per lane with a second load that the 8 lanes of a block share.  The
-// nibble order and sub-block pairing are those of kernels/vecdotq.cuh:785-794;
-// the (sc, m) unpack is kernels/vecdotq.cuh:796-807 done with byte permutes.
+// so each lane holds two whole sub-blocks: its integer dot products are the
+// complete sub-block sums and the scale/min unpack and float scaling are paid
+// once per 32 bytes.  The 16-byte block header (d, dmin, scales) is a third
+// load per lane, shared by the block's four lanes.  Nibble order and
+// sub-block pairing are those of kernels/vecdotq.cuh:785-794; the (sc, m)
+// unpack is kernels/vecdotq.cuh:796-807 done with byte permutes.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -79,7 +81,7 @@ __device__ __forceinline__ float wave_sum(float v) {
     return lo + hi;
 }
 
-// Per-lane constants of the scale/min unpack for sub-block pair jp = p/2.
+// Per-lane constants of the scale/min unpack for sub-block pair jp.
 struct ScaleSel {
     uint32_t sel_x;  // bytes (2j', 2j'+1) of scales[0..3] and of scales[4..7]
     uint32_t sel_y;  // bytes (2j', 2j'+1) of scales[8..11], twice
@@ -105,13 +107,20 @@ __device__ __forceinline__ uint32_t unpack_scale_min(u32x4 h, const ScaleSel &s)
     return s.high ? split : low;
 }
 
-// The lane's 16 q4 x q8 products for each of its two sub-blocks.
-__device__ __forceinline__ void lane_qdot(u32x4 w, u32x4 alo, u32x4 ahi, int &sa, int &sb) {
+// The int32 sums over the lane's two whole sub-blocks: w0/w1 = its 32 qs
+// bytes, a0/a1 = the 32 q8 of sub-block 2j, b0/b1 = those of sub-block 2j+1.
+__device__ __forceinline__ void lane_qdot(u32x4 w0, u32x4 w1, u32x4 a0, u32x4 a1, u32x4 b0, u32x4 b1,
+                                          int &sa, int &sb) {
     int a = 0, b = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        a = __builtin_amdgcn_sdot4((int)(w[k] & 0x0f0f0f0fu), (int)alo[k], a, false);
-        b = __builtin_amdgcn_sdot4((int)((w[k] >> 4) & 0x0f0f0f0fu), (int)ahi[k], b, false);
+        a = __builtin_amdgcn_sdot4((int)(w0[k] & 0x0f0f0f0fu), (int)a0[k], a, false);
+        b = __builtin_amdgcn_sdot4((int)((w0[k] >> 4) & 0x0f0f0f0fu), (int)b0[k], b, false);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        a = __builtin_amdgcn_sdot4((int)(w1[k] & 0x0f0f0f0fu), (int)a1[k], a, false);
+        b = __builtin_amdgcn_sdot4((int)((w1[k] >> 4) & 0x0f0f0f0fu), (int)b1[k], b, false);
     }
     sa = a;
     sb = b;
@@ -125,8 +134,28 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 }
 
 // ------------------------------------------------------------------------
-// Activation staging into LDS: q8[c*K + e] (int8) and d8[c*K/32 + b] (f32).
+// Activation staging into LDS.  Per column c (qcol bytes apart) the int8 q8
+// values, and after all columns, per 32-value block b,
+// dk[c*K/32 + b] = (d8, d8 * sum of the block's q8) as a float2 -- the
+// second term is the factor of the Q4_K min correction, so the GEMV needs no
+// per-lane byte sums.
+//
+// Two q8 layouts:
+//   linear   element e at c*qcol + e (qcol = K)
+//   swizzled the tile kernel's read order: element e of super-block
+//            kb = 16i + g, position 64j + 16k + t in the block, at
+//            c*qcol + 4096i + 1024k + 16(4g + j) + t (qcol = 4096*ceil(K/4096)),
+//            so that the 64 lanes of a wave reading chunk k of their blocks
+//            read one contiguous, bank-conflict-free 1 KB.
 // ------------------------------------------------------------------------
+
+template <bool SWZ>
+__device__ __forceinline__ int q8_offset(int c, int qcol, int b, int quarter) {
+    if (!SWZ) return c * qcol + b * 32 + quarter * 8;
+    const int kb = b >> 3, s = b & 7;
+    return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (quarter >> 1)) * 1024 +
+           ((kb & 15) * 4 + (s >> 1)) * 16 + (quarter & 1) * 8;
+}
 
 // n / d for n < 2^31 as (umulhi(n, mul) + n) >> shift, with mul and shift
 // from fastdiv_init on the host (Granlund-Montgomery round-up method).
@@ -174,8 +203,16 @@ struct ActStage {
     float v[kPre][8];
 };
 
-__device__ __forceinline__ void quantize_block_part(const float (&v)[8], int quarter, int K, int c,
-                                                    int b, int qb, int8_t *q8s, float *d8s) {
+// Sum of the four lanes of a quad (lanes 4k..4k+3).
+__device__ __forceinline__ int quad_sum(int v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    return v;
+}
+
+template <bool SWZ>
+__device__ __forceinline__ void quantize_block_part(const float (&v)[8], int quarter, int qcol, int c,
+                                                    int b, int qb, int8_t *q8s, float2 *dks) {
     float amax = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
@@ -184,16 +221,21 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[8], int qua
     const float d = amax / 127.0f;
     const float rd = __builtin_amdgcn_rcpf(d);
     uint32_t lo = 0, hi = 0;
+    int qsum = 0;
     if (amax != 0.0f) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const uint32_t byte = (uint32_t)(quantize_value(v[k], d, rd) & 0xff);
+            const int q = quantize_value(v[k], d, rd);
+            qsum += q;
+            const uint32_t byte = (uint32_t)(q & 0xff);
             if (k < 4) lo |= byte << (8 * k);
             else hi |= byte << (8 * (k - 4));
         }
     }
-    *reinterpret_cast<uint2 *>(q8s + c * K + b * 32 + quarter * 8) = make_uint2(lo, hi);
-    if (quarter == 0) d8s[qb] = (float)(_Float16)d;
+    qsum = quad_sum(qsum);
+    *reinterpret_cast<uint2 *>(q8s + q8_offset<SWZ>(c, qcol, b, quarter)) = make_uint2(lo, hi);
+    const float d8 = (float)(_Float16)d;
+    if (quarter == 0) dks[qb] = make_float2(d8, d8 * (float)qsum);
 }
 
 __device__ __forceinline__ void load_x8(const float *src, bool vec_ok, float (&v)[8]) {
@@ -226,9 +268,11 @@ __device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int
     }
 }
 
+template <bool SWZ>
 __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, int64_t ldx, int K,
                                                  int ncols, bool vec_ok, const FastDiv &fd,
-                                                 const ActStage &st, int8_t *q8s, float *d8s) {
+                                                 const ActStage &st, int qcol, int8_t *q8s,
+                                                 float2 *dks) {
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int quarter = threadIdx.x & 3;
@@ -238,7 +282,7 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
         const int qb = (threadIdx.x >> 2) + j * step;
         if (qb < total) {
             const int c = (int)fastdiv((uint32_t)qb, fd);
-            quantize_block_part(st.v[j], quarter, K, c, qb - c * nblk, qb, q8s, d8s);
+            quantize_block_part<SWZ>(st.v[j], quarter, qcol, c, qb - c * nblk, qb, q8s, dks);
         }
     }
     for (int qb = (threadIdx.x >> 2) + kPre * step; qb < total; qb += step) {
@@ -246,7 +290,7 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
         const int b = qb - c * nblk;
         float v[8];
         load_x8(x + c * ldx + b * 32 + quarter * 8, vec_ok, v);
-        quantize_block_part(v, quarter, K, c, b, qb, q8s, d8s);
+        quantize_block_part<SWZ>(v, quarter, qcol, c, b, qb, q8s, dks);
     }
 }
 
@@ -276,9 +320,22 @@ __device__ __forceinline__ void stage_q81_issue(const uint8_t *__restrict__ y, i
     }
 }
 
+template <bool SWZ>
+__device__ __forceinline__ void store_q81_part(uint32_t w0, uint32_t w1, uint32_t ds, int quarter,
+                                               int qcol, int c, int b, int qb, int8_t *q8s, float2 *dks) {
+    const int qsum = quad_sum(__builtin_amdgcn_sdot4((int)w0, 0x01010101,
+                                                     __builtin_amdgcn_sdot4((int)w1, 0x01010101, 0, false),
+                                                     false));
+    *reinterpret_cast<uint2 *>(q8s + q8_offset<SWZ>(c, qcol, b, quarter)) = make_uint2(w0, w1);
+    const float d8 = half_bits_to_float(ds);
+    if (quarter == 0) dks[qb] = make_float2(d8, d8 * (float)qsum);
+}
+
+template <bool SWZ>
 __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                  int K, int ncols, const FastDiv &fd,
-                                                 const Q81Stage &st, int8_t *q8s, float *d8s) {
+                                                 const Q81Stage &st, int qcol, int8_t *q8s,
+                                                 float2 *dks) {
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int quarter = threadIdx.x & 3;
@@ -288,10 +345,8 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
         const int qb = (threadIdx.x >> 2) + j * step;
         if (qb < total) {
             const int c = (int)fastdiv((uint32_t)qb, fd);
-            const int b = qb - c * nblk;
-            *reinterpret_cast<uint2 *>(q8s + c * K + b * 32 + quarter * 8) =
-                make_uint2(st.w[j][0], st.w[j][1]);
-            if (quarter == 0) d8s[qb] = half_bits_to_float(st.ds[j]);
+            store_q81_part<SWZ>(st.w[j][0], st.w[j][1], st.ds[j], quarter, qcol, c, qb - c * nblk, qb,
+                                q8s, dks);
         }
     }
     for (int qb = (threadIdx.x >> 2) + kPre * step; qb < total; qb += step) {
@@ -300,18 +355,19 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
         const uint8_t *blk = y + ((int64_t)c * stride_col_y + b) * kQ81Bytes;
         const uint32_t w0 = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
         const uint32_t w1 = *reinterpret_cast<const uint32_t *>(blk + 8 + quarter * 8);
-        *reinterpret_cast<uint2 *>(q8s + c * K + b * 32 + quarter * 8) = make_uint2(w0, w1);
-        if (quarter == 0) d8s[qb] = half_bits_to_float(*reinterpret_cast<const uint16_t *>(blk));
+        store_q81_part<SWZ>(w0, w1, *reinterpret_cast<const uint32_t *>(blk), quarter, qcol, c, b, qb,
+                            q8s, dks);
     }
 }
 
 // One-call form (issue + finish) for kernels with no loads to overlap.
+template <bool SWZ>
 __device__ __forceinline__ void stage_from_q8_1(const uint8_t *__restrict__ y, int64_t stride_col_y,
-                                                int K, int ncols, const FastDiv &fd, int8_t *q8s,
-                                                float *d8s) {
+                                                int K, int ncols, const FastDiv &fd, int qcol,
+                                                int8_t *q8s, float2 *dks) {
     Q81Stage st;
     stage_q81_issue(y, stride_col_y, K, ncols, fd, st);
-    stage_q81_finish(y, stride_col_y, K, ncols, fd, st, q8s, d8s);
+    stage_q81_finish<SWZ>(y, stride_col_y, K, ncols, fd, st, qcol, q8s, dks);
 }
 
 }  // namespace q4k

@@ -9,9 +9,10 @@
 //                          it from F32 itself (one launch per op) or copying an
 //                          already-quantised AoS Q8_1 buffer.  Each wave then
 //                          owns tiles of R rows and streams them group by group
-//                          (8 super-blocks x 144 B per row per step) with
-//                          16-byte buffer loads, the next step's loads issued
-//                          before the current step's arithmetic.
+//                          (16 super-blocks x 144 B per row per step, four
+//                          lanes per super-block) with 16-byte buffer loads,
+//                          the next step's loads issued before the current
+//                          step's arithmetic.
 //   subblock_sums_kernel   parity probe: the int32 sub-block sums computed with
 //                          the GEMV's lane map and dot routines.
 #include <hip/hip_runtime.h>
@@ -39,7 +40,8 @@ struct GemvParams {
     int M;                   // rows
     int K;                   // values per row
     int nb;                  // super-blocks per row (K/256)
-    int G;                   // groups of 8 super-blocks per row
+    int G;                   // groups of 16 super-blocks per row
+    int qcol;                // LDS bytes between the staged q8 columns
     int ntiles;              // ceil(M / R) (ceil(M / rpw) for the block-per-lane kernel)
     int vec_ok;              // F32 activation 16-B aligned with ldx % 4 == 0
     int rpw;                 // block-per-lane kernel: rows per wave pass (64/nb or 1)
@@ -49,20 +51,27 @@ struct GemvParams {
     FastDiv nblk32;          // division by K/32 (Q8_1 blocks per column)
 };
 
-// Loads group i (8 super-blocks) of rows [row0, row0 + nrows), nrows <= R;
+// One row's share of a group in a lane's registers: the block header and the
+// lane's 32 qs bytes.
+struct RowRegs {
+    u32x4 h, q0, q1;
+};
+
+// Loads group i (16 super-blocks) of rows [row0, row0 + nrows), nrows <= R;
 // the rows past nrows and blocks past the row's end read as 0.
 template <int R>
 __device__ __forceinline__ void load_group(const GemvParams &p, int row0, int nrows, int i, int g,
-                                           int part, u32x4 (&wq)[R], u32x4 (&wh)[R]) {
+                                           int j, RowRegs (&w)[R]) {
     const uint8_t *base = p.w + (int64_t)row0 * p.row_stride;
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nrows * p.row_stride));
-    const int kb = 8 * i + g;
+    const int kb = 16 * i + g;
     const uint32_t off = kb < p.nb ? (uint32_t)kb * kBlockBytes : kOOB;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t ro = off + (uint32_t)(r * p.row_stride);
-        wh[r] = load16(rs, ro);
-        wq[r] = load16(rs, ro + 16u + 16u * (uint32_t)part);
+        w[r].h = load16(rs, ro);
+        w[r].q0 = load16(rs, ro + 16u + 32u * (uint32_t)j);
+        w[r].q1 = load16(rs, ro + 32u + 32u * (uint32_t)j);
     }
 }
 
@@ -76,9 +85,9 @@ __device__ __forceinline__ Step next_step(Step s, int G) {
     return s.i + 1 == G ? Step{s.tile + 1, 0} : Step{s.tile, s.i + 1};
 }
 
-// Per-lane constants of the lane map.
+// Per-lane constants of the lane map (lane = 4g + j).
 struct Lane {
-    int lane, g, part, jp, h;
+    int lane, g, j;
     ScaleSel sel;
 };
 
@@ -95,52 +104,63 @@ __device__ __forceinline__ WaveRows wave_rows(const GemvParams &p, int gw) {
 
 template <int R>
 __device__ __forceinline__ void load_step(const GemvParams &p, const Lane &ln, const WaveRows &wr,
-                                          Step st, u32x4 (&wq)[R], u32x4 (&wh)[R]) {
+                                          Step st, RowRegs (&w)[R]) {
     const int row0 = wr.beg + st.tile * R;
-    load_group<R>(p, row0, min(R, wr.end - row0), st.i, ln.g, ln.part, wq, wh);
+    load_group<R>(p, row0, min(R, wr.end - row0), st.i, ln.g, ln.j, w);
 }
 
-// Consumes one group (8 super-blocks of R rows) held in wq/wh; on the last
-// group of a tile reduces the R x NC sums over the wave and stores them.
+// The activation a lane needs for one group and column: the q8 of sub-blocks
+// 2j (a0, a1) and 2j+1 (b0, b1) of its super-block, and their (d8, d8*sum q8).
+struct LaneAct {
+    u32x4 a0, a1, b0, b1;
+    float4 dk;  // d8a, kma, d8b, kmb
+};
+
+__device__ __forceinline__ LaneAct lane_act(const GemvParams &p, const Lane &ln, int i, int c,
+                                            const int8_t *q8s, const float2 *dks) {
+    const int kb = 16 * i + ln.g;
+    const int kbc = kb < p.nb ? kb : 0;  // blocks past the row's end: weights read as 0
+    const int8_t *qa = q8s + c * p.qcol + i * 4096 + ln.lane * 16;
+    LaneAct a;
+    a.a0 = *reinterpret_cast<const u32x4 *>(qa);
+    a.a1 = *reinterpret_cast<const u32x4 *>(qa + 1024);
+    a.b0 = *reinterpret_cast<const u32x4 *>(qa + 2048);
+    a.b1 = *reinterpret_cast<const u32x4 *>(qa + 3072);
+    a.dk = *reinterpret_cast<const float4 *>(dks + c * (p.K / 32) + kbc * 8 + ln.j * 2);
+    return a;
+}
+
+// Consumes one group (16 super-blocks of R rows) held in w; on the last group
+// of a tile reduces the R x NC sums over the wave and stores them.
 template <int NC, int R>
 __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &ln,
                                               const WaveRows &wr, Step st, const int8_t *q8s,
-                                              const float *d8s, const u32x4 (&wq)[R],
-                                              const u32x4 (&wh)[R], float (&acc)[R][NC]) {
-    const int K = p.K;
-    const int kb = 8 * st.i + ln.g;
-    const int kbc = kb < p.nb ? kb : 0;
-    u32x4 alo[NC], ahi[NC];
-    float d8a[NC], d8b[NC], ka[NC], kbv[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const int8_t *qa = q8s + c * K + kbc * kQK + ln.jp * 64 + ln.h * 16;
-        alo[c] = *reinterpret_cast<const u32x4 *>(qa);
-        ahi[c] = *reinterpret_cast<const u32x4 *>(qa + 32);
-        const float2 dd = *reinterpret_cast<const float2 *>(d8s + c * (K / 32) + kbc * 8 + ln.jp * 2);
-        d8a[c] = dd.x;
-        d8b[c] = dd.y;
-        ka[c] = dd.x * (float)byte_sum16(alo[c]);
-        kbv[c] = dd.y * (float)byte_sum16(ahi[c]);
-    }
+                                              const float2 *dks, const RowRegs (&w)[R],
+                                              float (&acc)[R][NC]) {
+    int sca[R], scb[R];
+    float maf[R], mbf[R], d[R], dmin[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t scm = unpack_scale_min(wh[r], ln.sel);
-        const int sca = (int)(scm & 0xffu);
-        const int scb = (int)((scm >> 8) & 0xffu);
-        const float maf = (float)((scm >> 16) & 0xffu);
-        const float mbf = (float)(scm >> 24);
-        const float d = half_bits_to_float(wh[r][0]);
-        const float dmin = half_bits_to_float(wh[r][0] >> 16);
+        const uint32_t scm = unpack_scale_min(w[r].h, ln.sel);
+        sca[r] = (int)(scm & 0xffu);
+        scb[r] = (int)((scm >> 8) & 0xffu);
+        maf[r] = (float)((scm >> 16) & 0xffu);
+        mbf[r] = (float)(scm >> 24);
+        d[r] = half_bits_to_float(w[r].h[0]);
+        dmin[r] = half_bits_to_float(w[r].h[0] >> 16);
+    }
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
+    for (int c = 0; c < NC; ++c) {
+        const LaneAct a = lane_act(p, ln, st.i, c, q8s, dks);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
             int sa, sb;
-            lane_qdot(wq[r], alo[c], ahi[c], sa, sb);
-            // |sa|, |sb| <= 16*15*127 and sc <= 63: 24-bit products are exact
-            const float xs = d8a[c] * (float)__mul24(sa, sca) + d8b[c] * (float)__mul24(sb, scb);
-            const float ms = ka[c] * maf + kbv[c] * mbf;
-            acc[r][c] = fmaf(d, xs, acc[r][c]);
-            acc[r][c] = fmaf(-dmin, ms, acc[r][c]);
+            lane_qdot(w[r].q0, w[r].q1, a.a0, a.a1, a.b0, a.b1, sa, sb);
+            // |sa|, |sb| <= 32*15*127 and sc <= 63: 24-bit products are exact
+            const float xs = a.dk.x * (float)__mul24(sa, sca[r]) + a.dk.z * (float)__mul24(sb, scb[r]);
+            const float ms = a.dk.y * maf[r] + a.dk.w * mbf[r];
+            acc[r][c] = fmaf(d[r], xs, acc[r][c]);
+            acc[r][c] = fmaf(-dmin[r], ms, acc[r][c]);
         }
     }
     if (st.i == p.G - 1) {
@@ -171,15 +191,13 @@ template <int NC, int R, int WAVES>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
-    float *d8s = reinterpret_cast<float *>(lds + NC * p.K);
+    float2 *dks = reinterpret_cast<float2 *>(lds + NC * p.qcol);
 
     Lane ln;
     ln.lane = threadIdx.x & (kWave - 1);
-    ln.g = ln.lane >> 3;
-    ln.part = ln.lane & 7;
-    ln.jp = ln.part >> 1;
-    ln.h = ln.part & 1;
-    ln.sel = make_scale_sel(ln.jp);
+    ln.g = ln.lane >> 2;
+    ln.j = ln.lane & 3;
+    ln.sel = make_scale_sel(ln.j);
 
     // the wave index is wave-uniform; readfirstlane lets the compiler keep
     // row numbers and buffer descriptors in scalar registers
@@ -202,17 +220,17 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
     Step a{0, 0};
     Step b = next_step(a, p.G);
     bool vb = active && b.tile < ntiles;
-    u32x4 qa[R], ha[R], qb[R], hb[R];
+    RowRegs wa[R], wb[R];
     if (p.prologue != 1) {
-        if (active) load_step<R>(p, ln, wr, a, qa, ha);
-        if (vb && p.prologue == 0) load_step<R>(p, ln, wr, b, qb, hb);
+        if (active) load_step<R>(p, ln, wr, a, wa);
+        if (vb && p.prologue == 0) load_step<R>(p, ln, wr, b, wb);
     }
-    if (p.x) stage_f32_finish(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, q8s, d8s);
-    else stage_q81_finish(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, q8s, d8s);
+    if (p.x) stage_f32_finish<true>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks);
+    else stage_q81_finish<true>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
-    if (p.prologue == 1) load_step<R>(p, ln, wr, a, qa, ha);
-    if (vb && p.prologue != 0) load_step<R>(p, ln, wr, b, qb, hb);
+    if (p.prologue == 1) load_step<R>(p, ln, wr, a, wa);
+    if (vb && p.prologue != 0) load_step<R>(p, ln, wr, b, wb);
 
     float acc[R][NC];
 #pragma unroll
@@ -222,16 +240,16 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
 
     // two register slots: while one group is consumed the next is in flight
     for (;;) {
-        process_group<NC, R>(p, ln, wr, a, q8s, d8s, qa, ha, acc);
+        process_group<NC, R>(p, ln, wr, a, q8s, dks, wa, acc);
         if (!vb) break;
         const Step a2 = next_step(b, p.G);
         const bool va2 = a2.tile < ntiles;
-        if (va2) load_step<R>(p, ln, wr, a2, qa, ha);
-        process_group<NC, R>(p, ln, wr, b, q8s, d8s, qb, hb, acc);
+        if (va2) load_step<R>(p, ln, wr, a2, wa);
+        process_group<NC, R>(p, ln, wr, b, q8s, dks, wb, acc);
         if (!va2) break;
         const Step b2 = next_step(a2, p.G);
         vb = b2.tile < ntiles;
-        if (vb) load_step<R>(p, ln, wr, b2, qb, hb);
+        if (vb) load_step<R>(p, ln, wr, b2, wb);
         a = a2;
         b = b2;
     }
@@ -326,7 +344,7 @@ template <int WAVES>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
-    float *d8s = reinterpret_cast<float *>(lds + p.K);
+    float2 *dks = reinterpret_cast<float2 *>(lds + p.K);
     const int lane = threadIdx.x & (kWave - 1);
     const int rr = lane / p.nb;
     const int kb = lane - rr * p.nb;
@@ -348,8 +366,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(GemvParams p
     u32x4 wa[9], wb[9];
     if (active) load_pass(p, pa, rr, kb, lane_on, wa);
     if (vb) load_pass(p, pb, rr, kb, lane_on, wb);
-    if (p.x) stage_f32_finish(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, q8s, d8s);
-    else stage_q81_finish(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, q8s, d8s);
+    if (p.x) stage_f32_finish<false>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
+    else stage_q81_finish<false>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
 
@@ -360,8 +378,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(GemvParams p
         for (int t = 0; t < 16; ++t) act.q[t] = *reinterpret_cast<const u32x4 *>(src + 16 * t);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            act.d8[s] = d8s[kb * 8 + s];
-            act.km[s] = act.d8[s] * (float)(byte_sum16(act.q[2 * s]) + byte_sum16(act.q[2 * s + 1]));
+            const float2 dk = dks[kb * 8 + s];
+            act.d8[s] = dk.x;
+            act.km[s] = dk.y;
         }
     }
 
@@ -435,8 +454,8 @@ template <int WAVES>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(GemvParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
-    float *d8s = reinterpret_cast<float *>(lds + p.K);
-    const int act_bytes = (p.K + p.K / 8 + 15) & ~15;
+    float2 *dks = reinterpret_cast<float2 *>(lds + p.K);
+    const int act_bytes = p.K + p.K / 4;  // a multiple of 16: K % 256 == 0
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint8_t *slot = lds + act_bytes + wave * kSlotBytes;
     const int lane = threadIdx.x & (kWave - 1);
@@ -461,8 +480,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(GemvParams p
     u32x4 wa[9], wb[9];
     if (active) load_pass_coalesced(p, pa, po, wa);
     if (vb) load_pass_coalesced(p, pb, po, wb);
-    if (p.x) stage_f32_finish(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, q8s, d8s);
-    else stage_q81_finish(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, q8s, d8s);
+    if (p.x) stage_f32_finish<false>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
+    else stage_q81_finish<false>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
 
@@ -473,8 +492,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(GemvParams p
         for (int t = 0; t < 16; ++t) act.q[t] = *reinterpret_cast<const u32x4 *>(src + 16 * t);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            act.d8[s] = d8s[kb * 8 + s];
-            act.km[s] = act.d8[s] * (float)(byte_sum16(act.q[2 * s]) + byte_sum16(act.q[2 * s + 1]));
+            const float2 dk = dks[kb * 8 + s];
+            act.d8[s] = dk.x;
+            act.km[s] = dk.y;
         }
     }
 
@@ -533,51 +553,48 @@ struct SumsParams {
     const uint8_t *y;  // one column of AoS Q8_1
     int32_t *sqq;      // [M][K/32] for this column
     int32_t *sq;       // [K/32] for this column
-    int M, K, nb, G;
+    int M, K, nb, G, qcol;
     FastDiv nblk32;
 };
 
-// One wave per (row, group): the GEMV's lane map and lane_qdot, then the two
-// lanes that share a sub-block (p and p^1) are added.
+// One wave per (row, group): the GEMV's lane map, swizzled activation layout,
+// loads and lane_qdot; each lane's two sums are whole sub-blocks.
 __global__ __launch_bounds__(256) void subblock_sums_kernel(SumsParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
-    float *d8s = reinterpret_cast<float *>(lds + p.K);
-    stage_from_q8_1(p.y, 0, p.K, 1, p.nblk32, q8s, d8s);
+    float2 *dks = reinterpret_cast<float2 *>(lds + p.qcol);
+    stage_from_q8_1<true>(p.y, 0, p.K, 1, p.nblk32, p.qcol, q8s, dks);
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 3, part = lane & 7, jp = part >> 1, h = part & 1;
+    GemvParams gp{};
+    gp.w = p.w;
+    gp.row_stride = p.row_stride;
+    gp.M = p.M;
+    gp.K = p.K;
+    gp.nb = p.nb;
+    gp.qcol = p.qcol;
+    Lane ln;
+    ln.lane = threadIdx.x & 63;
+    ln.g = ln.lane >> 2;
+    ln.j = ln.lane & 3;
+    ln.sel = make_scale_sel(ln.j);
     const int nitems = p.M * p.G;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     for (int item = blockIdx.x * 4 + wave; item < nitems; item += gridDim.x * 4) {
         const int row = item / p.G;
         const int i = item - row * p.G;
-        u32x4 wq[1], wh[1];
-        GemvParams gp{};
-        gp.w = p.w;
-        gp.row_stride = p.row_stride;
-        gp.M = p.M;
-        gp.nb = p.nb;
-        load_group<1>(gp, row, 1, i, g, part, wq, wh);
-        const int kb = 8 * i + g;
-        const int kbc = kb < p.nb ? kb : 0;
-        const int8_t *qa = q8s + kbc * kQK + jp * 64 + h * 16;
-        const u32x4 alo = *reinterpret_cast<const u32x4 *>(qa);
-        const u32x4 ahi = *reinterpret_cast<const u32x4 *>(qa + 32);
+        RowRegs w[1];
+        load_group<1>(gp, row, 1, i, ln.g, ln.j, w);
+        const LaneAct a = lane_act(gp, ln, i, 0, q8s, dks);
         int sa, sb;
-        lane_qdot(wq[0], alo, ahi, sa, sb);
-        int qa_sum = byte_sum16(alo), qb_sum = byte_sum16(ahi);
-        sa += dpp<kDppXor1>(sa);
-        sb += dpp<kDppXor1>(sb);
-        qa_sum += dpp<kDppXor1>(qa_sum);
-        qb_sum += dpp<kDppXor1>(qb_sum);
-        if (h == 0 && kb < p.nb) {
-            int32_t *o = p.sqq + (int64_t)row * (p.K / 32) + kb * 8 + jp * 2;
+        lane_qdot(w[0].q0, w[0].q1, a.a0, a.a1, a.b0, a.b1, sa, sb);
+        const int kb = 16 * i + ln.g;
+        if (kb < p.nb) {
+            int32_t *o = p.sqq + (int64_t)row * (p.K / 32) + kb * 8 + ln.j * 2;
             o[0] = sa;
             o[1] = sb;
             if (row == 0) {
-                p.sq[kb * 8 + jp * 2] = qa_sum;
-                p.sq[kb * 8 + jp * 2 + 1] = qb_sum;
+                p.sq[kb * 8 + ln.j * 2] = byte_sum16(a.a0) + byte_sum16(a.a1);
+                p.sq[kb * 8 + ln.j * 2 + 1] = byte_sum16(a.b0) + byte_sum16(a.b1);
             }
         }
     }
@@ -684,6 +701,13 @@ struct Geometry {
     int prologue = 0;   // tile kernel prologue order
 };
 
+// Tile kernel variants that are instantiated: those whose registers fit the
+// launch bounds without spilling (16 waves per workgroup leave 128 VGPRs per
+// lane, 8 waves 256).
+static constexpr bool tile_fits(int nc, int R, int waves) {
+    return waves > 8 ? (R == 1 || (R == 2 && nc <= 3)) : (R <= 2 || (R == 4 && nc <= 5));
+}
+
 // Rows per pass of the block-per-lane kernel, 0 when it does not apply.
 static int bpl_rows_per_pass(int64_t nb) {
     if (nb == 16) return 4;
@@ -692,13 +716,18 @@ static int bpl_rows_per_pass(int64_t nb) {
     return 0;
 }
 
-static int lds_bytes(int K, int nc) { return nc * (K + K / 8); }
+// LDS bytes of the staged activation: q8 columns (swizzled, padded to whole
+// 16-block groups, for the tile kernel; linear for the one-column block
+// kernels) followed by the per-32-value (d8, d8*sum q8) pairs.
+static int q8_col_bytes(int K) { return (K + 4095) / 4096 * 4096; }
+static int lds_bytes(int K, int nc) { return nc * (q8_col_bytes(K) + K / 4); }
+static int lds_bytes_linear(int K) { return K + K / 4; }
 
 // Launch geometry for an (M, K, N) product.
 //  tile kernel: one workgroup per CU (requesting just over half the CU's LDS
-//    keeps a second one away), 16 waves (8 when 5+ columns need more
-//    registers), the M rows split evenly over all waves, 2 rows per tile
-//    once waves own 2 or more rows.
+//    keeps a second one away), 16 waves, the M rows split evenly over all
+//    waves, 2 rows per tile once waves own 2 or more rows and the variant
+//    fits the registers (up to 3 columns).
 //  block-per-lane kernel (one column, 16..64 super-blocks per row): 4-wave
 //    workgroups, 2 per CU, two passes per wave in flight.
 static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N) {
@@ -724,7 +753,8 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         int wgs = cus;
         if (owgs > 0) wgs = owgs;
         g.grid = wg_needed < wgs ? wg_needed : wgs;
-        g.lds_launch = ((g.lds + 15) & ~15) + g.waves * kSlotBytes;
+        g.lds = lds_bytes_linear((int)K);
+        g.lds_launch = g.lds + g.waves * kSlotBytes;
         return g;
     }
     // Large single-column products stream long enough for the block-per-lane
@@ -743,25 +773,21 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         int wgs = cus * (8 / g.waves);
         if (owgs > 0) wgs = owgs;
         g.grid = wg_needed < wgs ? wg_needed : wgs;
+        g.lds = lds_bytes_linear((int)K);
         g.lds_launch = g.lds;
         return g;
     }
-    g.waves = nc <= 4 ? 16 : 8;
+    g.waves = 16;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves;
     g.grid = owgs > 0 ? owgs : cus;
+    g.R = (M >= (int64_t)g.grid * g.waves * 2 && tile_fits(nc, 2, g.waves)) ? 2 : 1;
+    if (orows == 1 || orows == 2 || orows == 4) g.R = orows;
+    // only the variants that fit the register file without spilling exist
+    if (!tile_fits(nc, g.R, g.waves)) g.waves = 8;
+    if (!tile_fits(nc, g.R, g.waves)) g.R = 2;
     const int64_t total_waves = (int64_t)g.grid * g.waves;
     g.rows_base = (int)(M / total_waves);
     g.rows_extra = (int)(M % total_waves);
-    g.R = g.rows_base >= 2 ? 2 : 1;
-    if (orows == 1 || orows == 2 || orows == 4) g.R = orows;
-    // 16-wave launch bounds cap a lane at 128 VGPRs: only these variants fit
-    const bool fits16 = g.R == 1 || (g.R == 2 && nc <= 4) || (g.R == 4 && nc <= 2);
-    if (g.waves > 8 && !fits16) {
-        g.waves = 8;
-        const int64_t tw = (int64_t)g.grid * g.waves;
-        g.rows_base = (int)(M / tw);
-        g.rows_extra = (int)(M % tw);
-    }
     g.lds_launch = g.lds;
     if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
     const int opro = g_ovr_prologue.load();
@@ -769,11 +795,12 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     return g;
 }
 
-typedef void (*gemv_fn_t)(GemvParams);
-
 template <int NC, int R, int WAVES>
 static const void *gemv_sym() {
-    return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES>);
+    if constexpr (tile_fits(NC, R, WAVES))
+        return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES>);
+    else
+        return nullptr;
 }
 
 template <int R, int WAVES>
@@ -791,7 +818,7 @@ static const void *gemv_sym_nc(int nc) {
     }
 }
 
-// Instantiations: R in {1, 2, 4}; launch bounds of 8 or 16 waves.
+// Instantiations: R in {1, 2, 4}; launch bounds of 8 or 16 waves (see tile_fits).
 static const void *gemv_kernel_for(int nc, int R, int waves) {
     if (waves <= 8) {
         if (R == 1) return gemv_sym_nc<1, 8>(nc);
@@ -854,11 +881,14 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     int st = device_info(&di);
     if (st != Q4K_OK) return st;
     const Geometry geo = pick_geometry(*di, ne00, ne01, ncols);
+    if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
-        g2.lds = lds_bytes((int)ne00, nc);
-        if (g2.lds_launch < g2.lds) g2.lds_launch = g2.lds;
+        if (!geo.bpl) {
+            g2.lds = lds_bytes((int)ne00, nc);
+            if (g2.lds_launch < g2.lds) g2.lds_launch = g2.lds;
+        }
         GemvParams p{};
         p.w = static_cast<const uint8_t *>(src0);
         p.row_stride = nb01;
@@ -871,7 +901,8 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
         p.M = (int)ne01;
         p.K = (int)ne00;
         p.nb = (int)(ne00 / kQK);
-        p.G = (p.nb + 7) / 8;
+        p.G = (p.nb + 15) / 16;
+        p.qcol = q8_col_bytes((int)ne00);
         p.ntiles = geo.ntiles;
         p.vec_ok = x && aligned(p.x, 16) && (ldx % 4 == 0);
         p.nblk32 = fastdiv_init((uint32_t)(ne00 / 32));
@@ -1021,6 +1052,7 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
     st = device_info(&di);
     if (st != Q4K_OK) return st;
     const int lds = lds_bytes((int)ne00, 1);
+    if (lds > di->max_lds) return Q4K_EUNSUPPORTED;
     st = ensure_lds(di, reinterpret_cast<const void *>(&subblock_sums_kernel), lds);
     if (st != Q4K_OK) return st;
     const int nb = (int)(ne00 / kQK);
@@ -1034,7 +1066,8 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
         p.M = (int)ne01;
         p.K = (int)ne00;
         p.nb = nb;
-        p.G = (nb + 7) / 8;
+        p.G = (nb + 15) / 16;
+        p.qcol = q8_col_bytes((int)ne00);
         p.nblk32 = fastdiv_init((uint32_t)(ne00 / 32));
         const int64_t items = ne01 * p.G;
         int grid = (int)((items + 3) / 4);
