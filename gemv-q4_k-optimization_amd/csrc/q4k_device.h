@@ -61,6 +61,7 @@ constexpr int kDppXor1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;   // quad_perm [2,3,0,1]
 constexpr int kDppRor4 = 0x124;  // row_ror:4
 constexpr int kDppRor8 = 0x128;  // row_ror:8
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror: lane i <-> 7-i within 8 lanes
 
 template <int XOR_MASK>
 __device__ __forceinline__ float swizzle_xor(float v) {
@@ -149,12 +150,13 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 //            read one contiguous, bank-conflict-free 1 KB.
 // ------------------------------------------------------------------------
 
+// LDS offset of values [4e, 4e+4) of 32-value block b of column c.
 template <bool SWZ>
-__device__ __forceinline__ int q8_offset(int c, int qcol, int b, int quarter) {
-    if (!SWZ) return c * qcol + b * 32 + quarter * 8;
+__device__ __forceinline__ int q8_offset(int c, int qcol, int b, int e) {
+    if (!SWZ) return c * qcol + b * 32 + e * 4;
     const int kb = b >> 3, s = b & 7;
-    return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (quarter >> 1)) * 1024 +
-           ((kb & 15) * 4 + (s >> 1)) * 16 + (quarter & 1) * 8;
+    return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (e >> 2)) * 1024 +
+           ((kb & 15) * 4 + (s >> 1)) * 16 + (e & 3) * 4;
 }
 
 // n / d for n < 2^31 as (umulhi(n, mul) + n) >> shift, with mul and shift
@@ -192,106 +194,145 @@ __device__ __forceinline__ int quantize_value(float x, float d, float rd) {
 // F32 activation -> Q8_1 values with ggml-cuda's quantize_q8_1 arithmetic
 // (call site kernels/mmvq.cu:734): per 32 values d = amax/127,
 // q = amax == 0 ? 0 : roundf(x/d), and the kernel consumes half(d).
-// Four lanes per 32-value block, 8 values per lane.  Staging is split in
-// two: issue() loads the first kPre rounds of values into registers, to be
-// called before the kernel's first weight loads (vector loads complete in
-// issue order, so values loaded after the weights would wait for them);
-// finish() quantises them into LDS and handles any further rounds.
+// LPB lanes per 32-value block (8 or 4), 32/LPB values per lane: 8 lets a
+// 16-wave workgroup cover a 4096-value column in one round, 4 halves the
+// per-block overhead when several columns need several rounds.  Staging is
+// split in two: issue() loads the first kPre rounds of values into
+// registers, to be called before the kernel's first weight loads (vector
+// loads complete in issue order, so values loaded after the weights would
+// wait for them); finish() quantises them into LDS and handles any further
+// rounds.  issue() loads unconditionally (lanes past the end re-read the
+// last block): with no branches around them the compiler's wait for these
+// values counts exactly the weight loads issued after them instead of
+// waiting for all loads.
 constexpr int kPre = 4;
 
+template <int LPB>
 struct ActStage {
-    float v[kPre][8];
+    float v[kPre][32 / LPB];
 };
+
+// amax / 127 rounded to nearest, as the IEEE division: the product with
+// the rounded reciprocal corrected by one exact fma residual.  Equal to
+// amax / 127.0f for every finite non-negative float (checked exhaustively).
+__device__ __forceinline__ float div127(float a) {
+    constexpr float kRcp127 = (float)(1.0 / 127.0);
+    const float q0 = a * kRcp127;
+    const float r = __builtin_fmaf(-q0, 127.0f, a);
+    return __builtin_fmaf(r, kRcp127, q0);
+}
+
+// Reductions over the LPB lanes of a 32-value block (aligned lane groups).
+template <int LPB>
+__device__ __forceinline__ float block_max(float v) {
+    v = fmaxf(v, dppf<kDppXor1>(v));
+    v = fmaxf(v, dppf<kDppXor2>(v));
+    if (LPB == 8) v = fmaxf(v, dppf<kDppHalfMirror>(v));
+    return v;
+}
+
+template <int LPB>
+__device__ __forceinline__ int block_sum(int v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    if (LPB == 8) v += dpp<kDppHalfMirror>(v);
+    return v;
+}
+
+template <bool SWZ, int LPB>
+__device__ __forceinline__ void quantize_block_part(const float (&v)[32 / LPB], int e, int qcol, int c,
+                                                    int b, int qb, int8_t *q8s, float2 *dks) {
+    constexpr int V = 32 / LPB;
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < V; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    amax = block_max<LPB>(amax);
+    const float d = div127(amax);
+    const float rd = __builtin_amdgcn_rcpf(d);
+    uint32_t word[V / 4];
+    int qsum = 0;
+#pragma unroll
+    for (int w = 0; w < V / 4; ++w) word[w] = 0;
+    if (amax != 0.0f) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            const int q = quantize_value(v[k], d, rd);
+            qsum += q;
+            word[k / 4] |= (uint32_t)(q & 0xff) << (8 * (k % 4));
+        }
+    }
+    qsum = block_sum<LPB>(qsum);
+    int8_t *dst = q8s + q8_offset<SWZ>(c, qcol, b, e * (V / 4));
+    if (V == 4) *reinterpret_cast<uint32_t *>(dst) = word[0];
+    else *reinterpret_cast<uint2 *>(dst) = make_uint2(word[0], word[V / 4 - 1]);
+    const float d8 = (float)(_Float16)d;
+    if (e == 0) dks[qb] = make_float2(d8, d8 * (float)qsum);
+}
+
+template <int V>
+__device__ __forceinline__ void load_xv(const float *src, bool vec_ok, float (&v)[V]) {
+    if (vec_ok) {
+#pragma unroll
+        for (int k = 0; k < V; k += 4) {
+            const float4 a = *reinterpret_cast<const float4 *>(src + k);
+            v[k] = a.x; v[k + 1] = a.y; v[k + 2] = a.z; v[k + 3] = a.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) v[k] = src[k];
+    }
+}
+
+template <int LPB>
+__device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int64_t ldx, int K,
+                                                int ncols, bool vec_ok, const FastDiv &fd,
+                                                ActStage<LPB> &st) {
+    constexpr int V = 32 / LPB;
+    const int nblk = K / 32;
+    const int total = ncols * nblk;
+    const int e = threadIdx.x & (LPB - 1);
+    const int step = blockDim.x / LPB;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const int qb = min((int)(threadIdx.x / LPB) + j * step, total - 1);
+        const int c = (int)fastdiv((uint32_t)qb, fd);
+        const int b = qb - c * nblk;
+        load_xv<V>(x + c * ldx + b * 32 + e * V, vec_ok, st.v[j]);
+    }
+}
+
+template <bool SWZ, int LPB>
+__device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, int64_t ldx, int K,
+                                                 int ncols, bool vec_ok, const FastDiv &fd,
+                                                 const ActStage<LPB> &st, int qcol, int8_t *q8s,
+                                                 float2 *dks) {
+    constexpr int V = 32 / LPB;
+    const int nblk = K / 32;
+    const int total = ncols * nblk;
+    const int e = threadIdx.x & (LPB - 1);
+    const int step = blockDim.x / LPB;
+#pragma unroll
+    for (int j = 0; j < kPre; ++j) {
+        const int qb = (int)(threadIdx.x / LPB) + j * step;
+        if (qb < total) {
+            const int c = (int)fastdiv((uint32_t)qb, fd);
+            quantize_block_part<SWZ, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, q8s, dks);
+        }
+    }
+    for (int qb = (int)(threadIdx.x / LPB) + kPre * step; qb < total; qb += step) {
+        const int c = (int)fastdiv((uint32_t)qb, fd);
+        const int b = qb - c * nblk;
+        float v[V];
+        load_xv<V>(x + c * ldx + b * 32 + e * V, vec_ok, v);
+        quantize_block_part<SWZ, LPB>(v, e, qcol, c, b, qb, q8s, dks);
+    }
+}
 
 // Sum of the four lanes of a quad (lanes 4k..4k+3).
 __device__ __forceinline__ int quad_sum(int v) {
     v += dpp<kDppXor1>(v);
     v += dpp<kDppXor2>(v);
     return v;
-}
-
-template <bool SWZ>
-__device__ __forceinline__ void quantize_block_part(const float (&v)[8], int quarter, int qcol, int c,
-                                                    int b, int qb, int8_t *q8s, float2 *dks) {
-    float amax = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
-    amax = fmaxf(amax, dppf<kDppXor1>(amax));
-    amax = fmaxf(amax, dppf<kDppXor2>(amax));
-    const float d = amax / 127.0f;
-    const float rd = __builtin_amdgcn_rcpf(d);
-    uint32_t lo = 0, hi = 0;
-    int qsum = 0;
-    if (amax != 0.0f) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int q = quantize_value(v[k], d, rd);
-            qsum += q;
-            const uint32_t byte = (uint32_t)(q & 0xff);
-            if (k < 4) lo |= byte << (8 * k);
-            else hi |= byte << (8 * (k - 4));
-        }
-    }
-    qsum = quad_sum(qsum);
-    *reinterpret_cast<uint2 *>(q8s + q8_offset<SWZ>(c, qcol, b, quarter)) = make_uint2(lo, hi);
-    const float d8 = (float)(_Float16)d;
-    if (quarter == 0) dks[qb] = make_float2(d8, d8 * (float)qsum);
-}
-
-__device__ __forceinline__ void load_x8(const float *src, bool vec_ok, float (&v)[8]) {
-    if (vec_ok) {
-        const float4 a0 = *reinterpret_cast<const float4 *>(src);
-        const float4 a1 = *reinterpret_cast<const float4 *>(src + 4);
-        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-        v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-    } else {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = src[k];
-    }
-}
-
-__device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int64_t ldx, int K,
-                                                int ncols, bool vec_ok, const FastDiv &fd,
-                                                ActStage &st) {
-    const int nblk = K / 32;
-    const int total = ncols * nblk;
-    const int quarter = threadIdx.x & 3;
-    const int step = blockDim.x >> 2;
-#pragma unroll
-    for (int j = 0; j < kPre; ++j) {
-        const int qb = (threadIdx.x >> 2) + j * step;
-        if (qb < total) {
-            const int c = (int)fastdiv((uint32_t)qb, fd);
-            const int b = qb - c * nblk;
-            load_x8(x + c * ldx + b * 32 + quarter * 8, vec_ok, st.v[j]);
-        }
-    }
-}
-
-template <bool SWZ>
-__device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, int64_t ldx, int K,
-                                                 int ncols, bool vec_ok, const FastDiv &fd,
-                                                 const ActStage &st, int qcol, int8_t *q8s,
-                                                 float2 *dks) {
-    const int nblk = K / 32;
-    const int total = ncols * nblk;
-    const int quarter = threadIdx.x & 3;
-    const int step = blockDim.x >> 2;
-#pragma unroll
-    for (int j = 0; j < kPre; ++j) {
-        const int qb = (threadIdx.x >> 2) + j * step;
-        if (qb < total) {
-            const int c = (int)fastdiv((uint32_t)qb, fd);
-            quantize_block_part<SWZ>(st.v[j], quarter, qcol, c, qb - c * nblk, qb, q8s, dks);
-        }
-    }
-    for (int qb = (threadIdx.x >> 2) + kPre * step; qb < total; qb += step) {
-        const int c = (int)fastdiv((uint32_t)qb, fd);
-        const int b = qb - c * nblk;
-        float v[8];
-        load_x8(x + c * ldx + b * 32 + quarter * 8, vec_ok, v);
-        quantize_block_part<SWZ>(v, quarter, qcol, c, b, qb, q8s, dks);
-    }
 }
 
 // Already-quantised AoS block_q8_1 (column stride stride_col_y blocks) -> LDS,
@@ -309,14 +350,12 @@ __device__ __forceinline__ void stage_q81_issue(const uint8_t *__restrict__ y, i
     const int step = blockDim.x >> 2;
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
-        const int qb = (threadIdx.x >> 2) + j * step;
-        if (qb < total) {
-            const int c = (int)fastdiv((uint32_t)qb, fd);
-            const uint8_t *blk = y + ((int64_t)c * stride_col_y + (qb - c * nblk)) * kQ81Bytes;
-            st.w[j][0] = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
-            st.w[j][1] = *reinterpret_cast<const uint32_t *>(blk + 8 + quarter * 8);
-            st.ds[j] = *reinterpret_cast<const uint32_t *>(blk);
-        }
+        const int qb = min((int)(threadIdx.x >> 2) + j * step, total - 1);  // unconditional, as above
+        const int c = (int)fastdiv((uint32_t)qb, fd);
+        const uint8_t *blk = y + ((int64_t)c * stride_col_y + (qb - c * nblk)) * kQ81Bytes;
+        st.w[j][0] = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
+        st.w[j][1] = *reinterpret_cast<const uint32_t *>(blk + 8 + quarter * 8);
+        st.ds[j] = *reinterpret_cast<const uint32_t *>(blk);
     }
 }
 
@@ -326,7 +365,7 @@ __device__ __forceinline__ void store_q81_part(uint32_t w0, uint32_t w1, uint32_
     const int qsum = quad_sum(__builtin_amdgcn_sdot4((int)w0, 0x01010101,
                                                      __builtin_amdgcn_sdot4((int)w1, 0x01010101, 0, false),
                                                      false));
-    *reinterpret_cast<uint2 *>(q8s + q8_offset<SWZ>(c, qcol, b, quarter)) = make_uint2(w0, w1);
+    *reinterpret_cast<uint2 *>(q8s + q8_offset<SWZ>(c, qcol, b, 2 * quarter)) = make_uint2(w0, w1);
     const float d8 = half_bits_to_float(ds);
     if (quarter == 0) dks[qb] = make_float2(d8, d8 * (float)qsum);
 }

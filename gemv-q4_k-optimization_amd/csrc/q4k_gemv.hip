@@ -47,7 +47,7 @@ struct GemvParams {
     int rpw;                 // block-per-lane kernel: rows per wave pass (64/nb or 1)
     int rows_base;           // tile kernel: each wave owns rows_base rows,
     int rows_extra;          //   the first rows_extra waves one more
-    int prologue;            // tile kernel: prologue order (see gemv_q4k_kernel)
+    int ring_off;            // tile kernel: LDS byte offset of the per-wave result rings
     FastDiv nblk32;          // division by K/32 (Q8_1 blocks per column)
 };
 
@@ -58,12 +58,13 @@ struct RowRegs {
 };
 
 // Loads group i (16 super-blocks) of rows [row0, row0 + nrows), nrows <= R;
-// the rows past nrows and blocks past the row's end read as 0.
+// the rows past nrows (all rows when nrows <= 0) and blocks past the row's
+// end read as 0 and cost no memory traffic.
 template <int R>
 __device__ __forceinline__ void load_group(const GemvParams &p, int row0, int nrows, int i, int g,
                                            int j, RowRegs (&w)[R]) {
     const uint8_t *base = p.w + (int64_t)row0 * p.row_stride;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, (uint32_t)(nrows * p.row_stride));
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, nrows > 0 ? (uint32_t)(nrows * p.row_stride) : 0u);
     const int kb = 16 * i + g;
     const uint32_t off = kb < p.nb ? (uint32_t)kb * kBlockBytes : kOOB;
 #pragma unroll
@@ -130,13 +131,38 @@ __device__ __forceinline__ LaneAct lane_act(const GemvParams &p, const Lane &ln,
     return a;
 }
 
+// Results of a wave, buffered in LDS and written to dst in coalesced runs:
+// entry e is column e % NC of row beg + e / NC.
+constexpr int kRing = 256;  // floats per wave
+
+struct ResultRing {
+    float *buf;   // this wave's kRing floats of LDS
+    int beg;      // first row of the wave
+    int end;      // one past its last row
+    int base;     // entries already written out
+    int n;        // entries buffered
+};
+
+// Writes the buffered entries to dst (entries of rows >= end are dropped).
+template <int NC>
+__device__ __forceinline__ void ring_flush(const GemvParams &p, int lane, ResultRing &rr) {
+    for (int k = lane; k < rr.n; k += kWave) {
+        const int idx = rr.base + k;
+        const int row = rr.beg + idx / NC;
+        const int c = idx - (idx / NC) * NC;
+        if (row < rr.end) p.dst[(int64_t)c * p.ld_dst + row] = rr.buf[k];
+    }
+    rr.base += rr.n;
+    rr.n = 0;
+}
+
 // Consumes one group (16 super-blocks of R rows) held in w; on the last group
-// of a tile reduces the R x NC sums over the wave and stores them.
+// of a tile reduces the R x NC sums over the wave into the result ring.
 template <int NC, int R>
-__device__ __forceinline__ void process_group(const GemvParams &p, const Lane &ln,
-                                              const WaveRows &wr, Step st, const int8_t *q8s,
-                                              const float2 *dks, const RowRegs (&w)[R],
-                                              float (&acc)[R][NC]) {
+__device__ __forceinline__ void process_group(const GemvParams &p, const Lane &ln, Step st,
+                                              const int8_t *q8s, const float2 *dks,
+                                              const RowRegs (&w)[R], float (&acc)[R][NC],
+                                              ResultRing &rr) {
     int sca[R], scb[R];
     float maf[R], mbf[R], d[R], dmin[R];
 #pragma unroll
@@ -173,22 +199,37 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
                 if (ln.lane == r * NC + c) out = s;
                 acc[r][c] = 0.0f;
             }
-        const int r = ln.lane / NC;
-        const int c = ln.lane - r * NC;
-        const int row = wr.beg + st.tile * R + r;
-        if (ln.lane < R * NC && row < wr.end) p.dst[(int64_t)c * p.ld_dst + row] = out;
+        if (ln.lane < R * NC) rr.buf[rr.n + ln.lane] = out;
+        rr.n += R * NC;
+        // rare (a wave's rows x NC above kRing): global stores inside the
+        // loop make the compiler's load waits conservative
+        if (rr.n + R * NC > kRing) ring_flush<NC>(p, ln.lane, rr);
     }
 }
 
 // Tile kernel: any K, 1..8 columns.  One workgroup per CU (the launch asks
 // for enough LDS to keep a second one off the CU); each wave owns a
-// contiguous range of rows and walks it R rows x one group at a time, two
-// groups in flight.  Every wave issues its activation loads, the workgroup
-// passes a barrier, and only then are weight loads issued: a CU serves
-// vector memory requests in order, so an activation load queued behind the
-// weight stream would stall the whole workgroup's prologue.
-template <int NC, int R, int WAVES>
+// contiguous range of rows and walks it R rows x one group at a time, with S
+// groups in flight in S register slots.  Every wave issues its activation
+// loads and the workgroup passes a barrier before any weight load is
+// issued: a CU serves vector memory requests in order, so an activation load
+// queued behind the weight stream would stall the whole workgroup's
+// prologue.  PRO selects when the weight loads start: 0 -- the first two
+// slots before the activation is quantised (it needs at most kPre staging
+// rounds, so no activation load is issued after them) and the rest after,
+// 1 -- all after, 2 -- all before.  Weight requests issued early overlap the quantisation
+// but queue in the memory system ahead of other CUs' activation loads, so
+// only part of the pipeline goes out early.
+//
+// Every weight load is issued unconditionally (steps past the wave's last
+// one read zeros from outside the buffer) and results go to LDS, not
+// memory, inside the loop: with no branch around a vector memory
+// instruction, the compiler waits for exactly the group being consumed
+// while the others stay in flight.
+template <int NC, int R, int WAVES, int PRO, int S>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
+    // slots loaded before quantisation
+    constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : (PRO == 2 ? S : 0);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float2 *dks = reinterpret_cast<float2 *>(lds + NC * p.qcol);
@@ -201,58 +242,55 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
 
     // the wave index is wave-uniform; readfirstlane lets the compiler keep
     // row numbers and buffer descriptors in scalar registers
-    const int gw = blockIdx.x * (int)(blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int gw = blockIdx.x * (int)(blockDim.x >> 6) + wave;
     const WaveRows wr = wave_rows(p, gw);
     const int ntiles = (wr.end - wr.beg + R - 1) / R;
-    const bool active = ntiles > 0;
+    int remaining = ntiles * p.G;  // steps of this wave
 
-    ActStage xs;
+    constexpr int kLPB = NC == 1 ? 8 : 4;  // activation lanes per 32-value block
+    ActStage<kLPB> xs;
     Q81Stage ys;
-    if (p.x) stage_f32_issue(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+    if (p.x) stage_f32_issue<kLPB>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
     else stage_q81_issue(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
     __syncthreads();  // all activation loads of this CU are queued first
 
-    // Prologue order (p.prologue): 0 -- the first two groups' weight loads
-    // go out before the activation is quantised; 1 -- the activation is
-    // quantised first and the weight loads follow (it then never waits
-    // behind the weight stream); 2 -- one group goes out first, the second
-    // after quantisation.
-    Step a{0, 0};
-    Step b = next_step(a, p.G);
-    bool vb = active && b.tile < ntiles;
-    RowRegs wa[R], wb[R];
-    if (p.prologue != 1) {
-        if (active) load_step<R>(p, ln, wr, a, wa);
-        if (vb && p.prologue == 0) load_step<R>(p, ln, wr, b, wb);
-    }
-    if (p.x) stage_f32_finish<true>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks);
+    Step st[S];
+    RowRegs w[S][R];
+    st[0] = Step{0, 0};
+#pragma unroll
+    for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], p.G);
+#pragma unroll
+    for (int k = 0; k < kEarly; ++k) load_step<R>(p, ln, wr, st[k], w[k]);
+    if (p.x) stage_f32_finish<true, kLPB>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks);
     else stage_q81_finish<true>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks);
     __syncthreads();
-    if (!active) return;  // no barrier below this point
-    if (p.prologue == 1) load_step<R>(p, ln, wr, a, wa);
-    if (vb && p.prologue != 0) load_step<R>(p, ln, wr, b, wb);
+    if (remaining == 0) return;  // no barrier below this point
+#pragma unroll
+    for (int k = kEarly; k < S; ++k) load_step<R>(p, ln, wr, st[k], w[k]);
 
     float acc[R][NC];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
+    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * kRing, wr.beg, wr.end, 0, 0};
 
-    // two register slots: while one group is consumed the next is in flight
+    // Slot k is consumed, then reloaded with the step after the newest one in
+    // flight.  Steps go S at a time with one exit test; a count that is not a
+    // multiple of S ends with steps past the wave's rows, whose zeros add
+    // nothing and whose results the final flush drops.
     for (;;) {
-        process_group<NC, R>(p, ln, wr, a, q8s, dks, wa, acc);
-        if (!vb) break;
-        const Step a2 = next_step(b, p.G);
-        const bool va2 = a2.tile < ntiles;
-        if (va2) load_step<R>(p, ln, wr, a2, wa);
-        process_group<NC, R>(p, ln, wr, b, q8s, dks, wb, acc);
-        if (!va2) break;
-        const Step b2 = next_step(a2, p.G);
-        vb = b2.tile < ntiles;
-        if (vb) load_step<R>(p, ln, wr, b2, wb);
-        a = a2;
-        b = b2;
+#pragma unroll
+        for (int k = 0; k < S; ++k) {
+            process_group<NC, R>(p, ln, st[k], q8s, dks, w[k], acc, rr);
+            st[k] = next_step(st[(k + S - 1) % S], p.G);
+            load_step<R>(p, ln, wr, st[k], w[k]);
+        }
+        remaining -= S;
+        if (remaining <= 0) break;
     }
+    ring_flush<NC>(p, ln.lane, rr);
 }
 
 // ------------------------------------------------------------------------
@@ -358,15 +396,15 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(GemvParams p
 
     // activation loads first (the whole workgroup), then the weight loads of
     // each wave's first two passes
-    ActStage xs;
+    ActStage<8> xs;
     Q81Stage ys;
-    if (p.x) stage_f32_issue(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
+    if (p.x) stage_f32_issue<8>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
     else stage_q81_issue(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
     __syncthreads();
     u32x4 wa[9], wb[9];
     if (active) load_pass(p, pa, rr, kb, lane_on, wa);
     if (vb) load_pass(p, pb, rr, kb, lane_on, wb);
-    if (p.x) stage_f32_finish<false>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
+    if (p.x) stage_f32_finish<false, 8>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
     else stage_q81_finish<false>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
@@ -472,15 +510,15 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(GemvParams p
 
     // activation loads first (the whole workgroup), then the weight loads of
     // each wave's first two passes
-    ActStage xs;
+    ActStage<8> xs;
     Q81Stage ys;
-    if (p.x) stage_f32_issue(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
+    if (p.x) stage_f32_issue<8>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
     else stage_q81_issue(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
     __syncthreads();
     u32x4 wa[9], wb[9];
     if (active) load_pass_coalesced(p, pa, po, wa);
     if (vb) load_pass_coalesced(p, pb, po, wb);
-    if (p.x) stage_f32_finish<false>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
+    if (p.x) stage_f32_finish<false, 8>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
     else stage_q81_finish<false>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
@@ -668,7 +706,7 @@ static int env_int(const char *name, int dflt) {
 // q4k_set_geometry_override or, as start-up defaults, the environment
 // variables Q4K_ROWS, Q4K_WAVES and Q4K_WGS.
 static std::atomic<int> g_ovr_rows{-1}, g_ovr_waves{-1}, g_ovr_wgs{-1}, g_ovr_kernel{-1};
-static std::atomic<int> g_ovr_prologue{-1};
+static std::atomic<int> g_ovr_prologue{-1}, g_ovr_slots{-1};
 
 static void load_env_overrides() {
     static std::once_flag once;
@@ -683,6 +721,8 @@ static void load_env_overrides() {
         g_ovr_kernel.compare_exchange_strong(expect, env_int("Q4K_KERNEL", 0));
         expect = -1;
         g_ovr_prologue.compare_exchange_strong(expect, env_int("Q4K_PROLOGUE", -1));
+        expect = -1;
+        g_ovr_slots.compare_exchange_strong(expect, env_int("Q4K_SLOTS", 0));
     });
 }
 
@@ -698,14 +738,18 @@ struct Geometry {
     int rpw = 0;        // block-per-lane kernel: rows per pass
     int rows_base = 0;  // tile kernel: rows per wave (first rows_extra waves +1)
     int rows_extra = 0;
-    int prologue = 0;   // tile kernel prologue order
+    int prologue = 0;   // tile kernel: when the first weight loads go out (PRO)
+    int slots = 2;      // tile kernel: groups in flight per wave (S)
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
 // launch bounds without spilling (16 waves per workgroup leave 128 VGPRs per
-// lane, 8 waves 256).
-static constexpr bool tile_fits(int nc, int R, int waves) {
-    return waves > 8 ? (R == 1 || (R == 2 && nc <= 3)) : (R <= 2 || (R == 4 && nc <= 5));
+// lane, 8 waves 256), with 2 or 4 groups in flight.
+static constexpr bool tile_fits(int nc, int R, int waves, int slots) {
+    if (slots == 8) return waves <= 8 && R == 1 && nc <= 2;
+    if (slots == 4)
+        return waves > 8 ? (R == 1 && nc <= 4) : (R == 1 || (R == 2 && nc <= 4));
+    return waves > 8 ? (R == 1 || (R == 2 && nc <= 2)) : (R <= 2 || (R == 4 && nc <= 5));
 }
 
 // Rows per pass of the block-per-lane kernel, 0 when it does not apply.
@@ -721,13 +765,17 @@ static int bpl_rows_per_pass(int64_t nb) {
 // kernels) followed by the per-32-value (d8, d8*sum q8) pairs.
 static int q8_col_bytes(int K) { return (K + 4095) / 4096 * 4096; }
 static int lds_bytes(int K, int nc) { return nc * (q8_col_bytes(K) + K / 4); }
+// The tile kernel adds a kRing-float result ring per wave after the activation.
+static int tile_lds_bytes(int K, int nc, int waves) { return lds_bytes(K, nc) + waves * kRing * 4; }
 static int lds_bytes_linear(int K) { return K + K / 4; }
 
 // Launch geometry for an (M, K, N) product.
 //  tile kernel: one workgroup per CU (requesting just over half the CU's LDS
-//    keeps a second one away), 16 waves, the M rows split evenly over all
-//    waves, 2 rows per tile once waves own 2 or more rows and the variant
-//    fits the registers (up to 3 columns).
+//    keeps a second one away), 8 or 16 waves, the M rows split evenly over
+//    all waves, one row per tile and two groups in flight per wave (larger
+//    tiles and deeper pipelines measured slower on MI355X: the activation
+//    prologue is the critical path and more weight requests in flight delay
+//    its loads).
 //  block-per-lane kernel (one column, 16..64 super-blocks per row): 4-wave
 //    workgroups, 2 per CU, two passes per wave in flight.
 static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N) {
@@ -736,9 +784,9 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
     int nc = (int)N;
-    while (nc > 1 && lds_bytes((int)K, nc) > max_lds) nc = (nc + 1) / 2;
+    while (nc > 1 && tile_lds_bytes((int)K, nc, 16) > max_lds) nc = (nc + 1) / 2;
     g.nc_chunk = nc;
-    g.lds = lds_bytes((int)K, nc);
+    g.lds = tile_lds_bytes((int)K, nc, 16);
     const int orows = g_ovr_rows.load(), owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load();
     const int okern = g_ovr_kernel.load();
     const int rpw = bpl_rows_per_pass(K / kQK);
@@ -777,57 +825,77 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         g.lds_launch = g.lds;
         return g;
     }
-    g.waves = 16;
-    if (owaves >= 1 && owaves <= 16) g.waves = owaves;
     g.grid = owgs > 0 ? owgs : cus;
-    g.R = (M >= (int64_t)g.grid * g.waves * 2 && tile_fits(nc, 2, g.waves)) ? 2 : 1;
+    // 16 waves per CU when each still gets a few groups to stream; 8 for
+    // small products, where a second wave per SIMD mostly adds prologue
+    const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
+    g.waves = steps_per_wg >= 48 ? 16 : 8;
+    if (owaves >= 1 && owaves <= 16) g.waves = owaves;
+    g.R = 1;
     if (orows == 1 || orows == 2 || orows == 4) g.R = orows;
+    const int oslots = g_ovr_slots.load();
+    if (oslots == 2 || oslots == 4 || oslots == 8) g.slots = oslots;
     // only the variants that fit the register file without spilling exist
-    if (!tile_fits(nc, g.R, g.waves)) g.waves = 8;
-    if (!tile_fits(nc, g.R, g.waves)) g.R = 2;
+    if (!tile_fits(nc, g.R, g.waves, g.slots)) g.waves = 8;
+    if (!tile_fits(nc, g.R, g.waves, g.slots)) g.slots = g.slots == 8 ? 4 : 2;
+    if (!tile_fits(nc, g.R, g.waves, g.slots)) g.slots = 2;
+    if (!tile_fits(nc, g.R, g.waves, g.slots)) g.R = 2;
     const int64_t total_waves = (int64_t)g.grid * g.waves;
     g.rows_base = (int)(M / total_waves);
     g.rows_extra = (int)(M % total_waves);
+    g.lds = tile_lds_bytes((int)K, nc, g.waves);
     g.lds_launch = g.lds;
     if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
+    // weight loads before quantisation only when every activation load fits
+    // the kPre staging rounds issued ahead of them
+    const int lpb = nc == 1 ? 8 : 4;  // the kernel's activation lanes per block
+    const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)kPre * g.waves * (kWave / lpb);
+    g.prologue = pro0_ok ? 0 : 1;
     const int opro = g_ovr_prologue.load();
-    if (opro >= 0 && opro <= 2) g.prologue = opro;
+    if (opro == 1 || ((opro == 0 || (opro == 2 && g.slots >= 4)) && pro0_ok)) g.prologue = opro;
     return g;
 }
 
-template <int NC, int R, int WAVES>
-static const void *gemv_sym() {
-    if constexpr (tile_fits(NC, R, WAVES))
-        return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES>);
-    else
-        return nullptr;
+template <int NC, int R, int WAVES, int S>
+static const void *gemv_sym(int pro) {
+    if constexpr (tile_fits(NC, R, WAVES, S)) {
+        if (pro == 0) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 0, S>);
+        if (pro == 1) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 1, S>);
+        if constexpr (S >= 4) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 2, S>);
+    }
+    return nullptr;
 }
 
-template <int R, int WAVES>
-static const void *gemv_sym_nc(int nc) {
+template <int R, int WAVES, int S>
+static const void *gemv_sym_nc(int nc, int pro) {
     switch (nc) {
-        case 1: return gemv_sym<1, R, WAVES>();
-        case 2: return gemv_sym<2, R, WAVES>();
-        case 3: return gemv_sym<3, R, WAVES>();
-        case 4: return gemv_sym<4, R, WAVES>();
-        case 5: return gemv_sym<5, R, WAVES>();
-        case 6: return gemv_sym<6, R, WAVES>();
-        case 7: return gemv_sym<7, R, WAVES>();
-        case 8: return gemv_sym<8, R, WAVES>();
+        case 1: return gemv_sym<1, R, WAVES, S>(pro);
+        case 2: return gemv_sym<2, R, WAVES, S>(pro);
+        case 3: return gemv_sym<3, R, WAVES, S>(pro);
+        case 4: return gemv_sym<4, R, WAVES, S>(pro);
+        case 5: return gemv_sym<5, R, WAVES, S>(pro);
+        case 6: return gemv_sym<6, R, WAVES, S>(pro);
+        case 7: return gemv_sym<7, R, WAVES, S>(pro);
+        case 8: return gemv_sym<8, R, WAVES, S>(pro);
         default: return nullptr;
     }
 }
 
-// Instantiations: R in {1, 2, 4}; launch bounds of 8 or 16 waves (see tile_fits).
-static const void *gemv_kernel_for(int nc, int R, int waves) {
+template <int WAVES, int S>
+static const void *gemv_sym_r(int nc, int R, int pro) {
+    if (R == 1) return gemv_sym_nc<1, WAVES, S>(nc, pro);
+    if (R == 2) return gemv_sym_nc<2, WAVES, S>(nc, pro);
+    return gemv_sym_nc<4, WAVES, S>(nc, pro);
+}
+
+// Instantiations: R in {1, 2, 4}; launch bounds of 8 or 16 waves; 2 or 4
+// slots (see tile_fits); both prologue orders.
+static const void *gemv_kernel_for(int nc, int R, int waves, int pro, int slots) {
     if (waves <= 8) {
-        if (R == 1) return gemv_sym_nc<1, 8>(nc);
-        if (R == 2) return gemv_sym_nc<2, 8>(nc);
-        return gemv_sym_nc<4, 8>(nc);
+        if (slots == 8) return gemv_sym_r<8, 8>(nc, R, pro);
+        return slots == 4 ? gemv_sym_r<8, 4>(nc, R, pro) : gemv_sym_r<8, 2>(nc, R, pro);
     }
-    if (R == 1) return gemv_sym_nc<1, 16>(nc);
-    if (R == 2) return gemv_sym_nc<2, 16>(nc);
-    return gemv_sym_nc<4, 16>(nc);
+    return slots == 4 ? gemv_sym_r<16, 4>(nc, R, pro) : gemv_sym_r<16, 2>(nc, R, pro);
 }
 
 static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc, hipStream_t stream) {
@@ -840,10 +908,10 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
                             : reinterpret_cast<const void *>(&gemv_q4k_bpl_kernel<4>);
         p.rpw = geo.rpw;
     } else {
-        fn = gemv_kernel_for(nc, geo.R, geo.waves);
+        fn = gemv_kernel_for(nc, geo.R, geo.waves, geo.prologue, geo.slots);
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
-        p.prologue = geo.prologue;
+        p.ring_off = lds_bytes(p.K, nc);
     }
     if (!fn) return Q4K_EINVAL;
     int st = ensure_lds(di, fn, geo.lds_launch);
@@ -886,7 +954,7 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
         if (!geo.bpl) {
-            g2.lds = lds_bytes((int)ne00, nc);
+            g2.lds = tile_lds_bytes((int)ne00, nc, geo.waves);
             if (g2.lds_launch < g2.lds) g2.lds_launch = g2.lds;
         }
         GemvParams p{};

@@ -53,6 +53,7 @@ def lib():
             "orc_pack_scales_k4": (None, [P, P, P]),
             "orc_selftest_scale_unpack": (I64, []),
             "orc_selftest_scale_pack": (I64, []),
+            "orc_check_div127": (I64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
             "orc_quantize_q4_K": (None, [P, P, I64]),
             "orc_quantize_q4_K_rows": (None, [P, P, I64, I64, I]),
             "orc_dequantize_q4_K": (None, [P, P, I64]),

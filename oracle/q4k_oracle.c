@@ -207,6 +207,29 @@ int64_t orc_selftest_scale_unpack(void) {
     return bad;
 }
 
+/* The GPU quantiser computes d = amax/127 without a division instruction:
+ * q0 = amax*RN(1/127), r = fma(-q0, 127, amax) (exact), d = fma(r, RN(1/127), q0).
+ * Counts the float bit patterns lo, lo+stride, ... < hi (non-negative finite
+ * floats: hi <= 0x7f800000) where that differs from the IEEE quotient
+ * amax / 127.0f that ggml-cuda's quantize_q8_1 computes.  stride = 1 over
+ * [0, 0x7f800000) is the exhaustive check. */
+int64_t orc_check_div127(uint32_t lo, uint32_t hi, uint32_t stride) {
+    const float rcp = (float)(1.0 / 127.0);
+    int64_t bad = 0;
+    if (stride == 0) stride = 1;
+    for (uint64_t u = lo; u < hi; u += stride) {
+        const uint32_t bits = (uint32_t)u;
+        float a;
+        memcpy(&a, &bits, 4);
+        const float ref = a / 127.0f;
+        const float q0 = a * rcp;
+        const float r = fmaf(-q0, 127.0f, a);
+        const float q1 = fmaf(r, rcp, q0);
+        if (memcmp(&q1, &ref, 4) != 0) bad++;
+    }
+    return bad;
+}
+
 /* pack -> unpack identity for all 64x64 (sc, m) at every sub-block position */
 int64_t orc_selftest_scale_pack(void) {
     int64_t bad = 0;

@@ -59,3 +59,20 @@ def test_exact_multiples_roundtrip(O):
         d16, _, qs = _split(O.quantize_q8_1(x), 16)
         assert (qs.reshape(2, -1) == q).all()
         assert (O.f16_bits_to_f32(d16) == np.float32(2.0 ** -e)).all()
+
+
+def test_division_by_127_identity(O):
+    """The GPU quantiser's division-free d = amax/127 (product with the
+    rounded reciprocal plus one fma correction) must equal the IEEE quotient.
+    Every 61st float bit pattern here (35M values, a few seconds); the
+    same function run with stride 1 over [0, 0x7f800000) is the exhaustive
+    check and reports no mismatch either.  A planted error -- the correction
+    step dropped -- is caught by the same sample."""
+    L = O.lib()
+    assert L.orc_check_div127(0, 0x7F800000, 61) == 0
+    # the first 2^20 patterns (zero and the subnormals) exhaustively
+    assert L.orc_check_div127(0, 1 << 20, 1) == 0
+    # without the correction (q0 alone) many quotients are off by one ulp
+    rcp = np.float32(1.0 / 127.0)
+    a = np.random.default_rng(0).uniform(1e-3, 1e3, 100000).astype(np.float32)
+    assert ((a * rcp).astype(np.float32) != a / np.float32(127)).sum() > 1000
