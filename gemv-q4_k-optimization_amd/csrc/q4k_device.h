@@ -70,16 +70,27 @@ __device__ __forceinline__ float swizzle_xor(float v) {
         float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (XOR_MASK << 10)));
 }
 
-// Sum over the 64 lanes; the result is wave-uniform.
+constexpr int kDppBcast15 = 0x142;  // row_bcast:15 -- lane 15 of each row to the next row
+constexpr int kDppBcast31 = 0x143;  // row_bcast:31 -- lane 31 to rows 2 and 3
+
+// DPP move into the rows of ROW_MASK only; the other rows read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dppf_rows(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes, all in DPP (no LDS round trip); the result is
+// wave-uniform.  After the four row steps every lane holds its 16-lane row's
+// sum; the two broadcasts accumulate rows 0..3 into lane 63.
 __device__ __forceinline__ float wave_sum(float v) {
     v += dppf<kDppXor1>(v);
     v += dppf<kDppXor2>(v);
     v += dppf<kDppRor4>(v);
     v += dppf<kDppRor8>(v);
-    v += swizzle_xor<16>(v);
-    const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    return lo + hi;
+    v += dppf_rows<kDppBcast15, 0xa>(v);
+    v += dppf_rows<kDppBcast31, 0xc>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Per-lane constants of the scale/min unpack for sub-block pair jp.
@@ -179,16 +190,25 @@ __device__ __forceinline__ uint32_t fastdiv(uint32_t n, const FastDiv &f) {
     return (__umulhi(n, f.mul) + n) >> f.shift;
 }
 
-// roundf(x / d) with the correctly rounded quotient x/d, as ggml-cuda's
-// quantize_q8_1 computes it.  y = x * rcp(d) is within 2^-15 of the quotient
-// for |x/d| <= 128 (v_rcp_f32 is 1-ulp accurate), so unless y lies within
-// 2^-12 of a half-integer both round to the same integer and rint(y) is the
-// answer; the rare lanes near a tie (and any out-of-range y) divide exactly.
-__device__ __forceinline__ int quantize_value(float x, float d, float rd) {
-    const float y = x * rd;
-    const float f = fabsf(y - truncf(y));
-    if (!(fabsf(f - 0.5f) >= 0x1p-12f && fabsf(y) <= 128.0f)) return (int)roundf(x / d);
-    return (int)rintf(y);
+// q[k] = roundf(v[k] / d) with the correctly rounded quotient, as ggml-cuda's
+// quantize_q8_1 computes it.  y = v * rcp(d) is within 2^-15 of that
+// quotient (|v/d| <= 127 and v_rcp_f32 is 1-ulp accurate), so rint(y) is the
+// answer unless y lies within 2^-12 of a half-integer; a lane with such a
+// value (or a NaN) recomputes all its values with the exact division.  One
+// branch per lane instead of one per value.
+template <int V>
+__device__ __forceinline__ void quantize_values(const float (&v)[V], float d, float rd, int (&q)[V]) {
+    bool fast = true;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        const float y = v[k] * rd;
+        q[k] = (int)rintf(y);
+        fast = fast && fabsf(fabsf(y - truncf(y)) - 0.5f) >= 0x1p-12f;
+    }
+    if (!fast) {
+#pragma unroll
+        for (int k = 0; k < V; ++k) q[k] = (int)roundf(v[k] / d);
+    }
 }
 
 // F32 activation -> Q8_1 values with ggml-cuda's quantize_q8_1 arithmetic
@@ -254,11 +274,12 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[32 / LPB], 
 #pragma unroll
     for (int w = 0; w < V / 4; ++w) word[w] = 0;
     if (amax != 0.0f) {
+        int q[V];
+        quantize_values<V>(v, d, rd, q);
 #pragma unroll
         for (int k = 0; k < V; ++k) {
-            const int q = quantize_value(v[k], d, rd);
-            qsum += q;
-            word[k / 4] |= (uint32_t)(q & 0xff) << (8 * (k % 4));
+            qsum += q[k];
+            word[k / 4] |= (uint32_t)(q[k] & 0xff) << (8 * (k % 4));
         }
     }
     qsum = block_sum<LPB>(qsum);
@@ -295,7 +316,7 @@ __device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
         const int qb = min((int)(threadIdx.x / LPB) + j * step, total - 1);
-        const int c = (int)fastdiv((uint32_t)qb, fd);
+        const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
         const int b = qb - c * nblk;
         load_xv<V>(x + c * ldx + b * 32 + e * V, vec_ok, st.v[j]);
     }
@@ -315,12 +336,12 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
     for (int j = 0; j < kPre; ++j) {
         const int qb = (int)(threadIdx.x / LPB) + j * step;
         if (qb < total) {
-            const int c = (int)fastdiv((uint32_t)qb, fd);
+            const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
             quantize_block_part<SWZ, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, q8s, dks);
         }
     }
     for (int qb = (int)(threadIdx.x / LPB) + kPre * step; qb < total; qb += step) {
-        const int c = (int)fastdiv((uint32_t)qb, fd);
+        const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
         const int b = qb - c * nblk;
         float v[V];
         load_xv<V>(x + c * ldx + b * 32 + e * V, vec_ok, v);

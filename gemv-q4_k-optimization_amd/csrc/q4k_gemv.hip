@@ -103,11 +103,38 @@ __device__ __forceinline__ WaveRows wave_rows(const GemvParams &p, int gw) {
     return WaveRows{beg, beg + p.rows_base + (gw < p.rows_extra ? 1 : 0)};
 }
 
+// A wave's rows as one buffer (the host keeps them under 2^31 bytes): a load
+// past them or past a row's last block reads 0 without memory traffic.
+struct WaveStream {
+    __amdgpu_buffer_rsrc_t rs;
+    int ntiles;
+    uint32_t lh, lq;  // the lane's byte offsets of its header and qs loads in a group
+};
+
+__device__ __forceinline__ WaveStream wave_stream(const GemvParams &p, const Lane &ln,
+                                                  const WaveRows &wr, int R) {
+    WaveStream ws;
+    ws.rs = make_rsrc(p.w + (int64_t)wr.beg * p.row_stride, (uint32_t)((wr.end - wr.beg) * p.row_stride));
+    ws.ntiles = (wr.end - wr.beg + R - 1) / R;
+    ws.lh = (uint32_t)ln.g * kBlockBytes;
+    ws.lq = ws.lh + 16u + 32u * (uint32_t)ln.j;
+    return ws;
+}
+
 template <int R>
-__device__ __forceinline__ void load_step(const GemvParams &p, const Lane &ln, const WaveRows &wr,
+__device__ __forceinline__ void load_step(const GemvParams &p, const Lane &ln, const WaveStream &ws,
                                           Step st, RowRegs (&w)[R]) {
-    const int row0 = wr.beg + st.tile * R;
-    load_group<R>(p, row0, min(R, wr.end - row0), st.i, ln.g, ln.j, w);
+    const uint32_t base = (uint32_t)(st.tile * R) * (uint32_t)p.row_stride + (uint32_t)st.i * (16 * kBlockBytes);
+    const bool ok = st.tile < ws.ntiles && 16 * st.i + ln.g < p.nb;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t ro = base + (uint32_t)(r * p.row_stride);
+        const uint32_t oh = ok ? ro + ws.lh : kOOB;
+        const uint32_t oq = ok ? ro + ws.lq : kOOB;
+        w[r].h = load16(ws.rs, oh);
+        w[r].q0 = load16(ws.rs, oq);
+        w[r].q1 = load16(ws.rs, oq + 16u);
+    }
 }
 
 // The activation a lane needs for one group and column: the q8 of sub-blocks
@@ -217,7 +244,7 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
 // prologue.  PRO selects when the weight loads start: 0 -- the first two
 // slots before the activation is quantised (it needs at most kPre staging
 // rounds, so no activation load is issued after them) and the rest after,
-// 1 -- all after, 2 -- all before.  Weight requests issued early overlap the quantisation
+// 1 -- all after, 2 -- all before, 3 -- one slot before.  Weight requests issued early overlap the quantisation
 // but queue in the memory system ahead of other CUs' activation loads, so
 // only part of the pipeline goes out early.
 //
@@ -229,7 +256,7 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
 template <int NC, int R, int WAVES, int PRO, int S>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
     // slots loaded before quantisation
-    constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : (PRO == 2 ? S : 0);
+    constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : (PRO == 2 ? S : (PRO == 3 ? 1 : 0));
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float2 *dks = reinterpret_cast<float2 *>(lds + NC * p.qcol);
@@ -245,8 +272,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int gw = blockIdx.x * (int)(blockDim.x >> 6) + wave;
     const WaveRows wr = wave_rows(p, gw);
-    const int ntiles = (wr.end - wr.beg + R - 1) / R;
-    int remaining = ntiles * p.G;  // steps of this wave
+    const WaveStream ws = wave_stream(p, ln, wr, R);
+    int remaining = ws.ntiles * p.G;  // steps of this wave
 
     constexpr int kLPB = NC == 1 ? 8 : 4;  // activation lanes per 32-value block
     ActStage<kLPB> xs;
@@ -261,13 +288,13 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
 #pragma unroll
     for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], p.G);
 #pragma unroll
-    for (int k = 0; k < kEarly; ++k) load_step<R>(p, ln, wr, st[k], w[k]);
+    for (int k = 0; k < kEarly; ++k) load_step<R>(p, ln, ws, st[k], w[k]);
     if (p.x) stage_f32_finish<true, kLPB>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks);
     else stage_q81_finish<true>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks);
     __syncthreads();
     if (remaining == 0) return;  // no barrier below this point
 #pragma unroll
-    for (int k = kEarly; k < S; ++k) load_step<R>(p, ln, wr, st[k], w[k]);
+    for (int k = kEarly; k < S; ++k) load_step<R>(p, ln, ws, st[k], w[k]);
 
     float acc[R][NC];
 #pragma unroll
@@ -285,7 +312,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
         for (int k = 0; k < S; ++k) {
             process_group<NC, R>(p, ln, st[k], q8s, dks, w[k], acc, rr);
             st[k] = next_step(st[(k + S - 1) % S], p.G);
-            load_step<R>(p, ln, wr, st[k], w[k]);
+            load_step<R>(p, ln, ws, st[k], w[k]);
         }
         remaining -= S;
         if (remaining <= 0) break;
@@ -747,6 +774,7 @@ struct Geometry {
 // lane, 8 waves 256), with 2 or 4 groups in flight.
 static constexpr bool tile_fits(int nc, int R, int waves, int slots) {
     if (slots == 8) return waves <= 8 && R == 1 && nc <= 2;
+    if (slots == 1) return R == 1;
     if (slots == 4)
         return waves > 8 ? (R == 1 && nc <= 4) : (R == 1 || (R == 2 && nc <= 4));
     return waves > 8 ? (R == 1 || (R == 2 && nc <= 2)) : (R <= 2 || (R == 4 && nc <= 5));
@@ -805,12 +833,11 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         g.lds_launch = g.lds + g.waves * kSlotBytes;
         return g;
     }
-    // Large single-column products stream long enough for the block-per-lane
-    // kernel's lower instruction count to win; short ones are bound by the
-    // activation prologue and the launch, where the tile kernel's 16 waves
-    // per CU do better (measured on MI355X).
+    // Large single-column products with 4096-value rows stream long enough
+    // for the block-per-lane kernel's lower instruction count to win; the
+    // tile kernel does better on everything else (measured on MI355X).
     const int64_t weight_bytes = M * (K / kQK) * kBlockBytes;
-    const bool auto_bpl = okern == 0 && weight_bytes >= (48ll << 20);
+    const bool auto_bpl = okern == 0 && K == 4096 && weight_bytes >= (48ll << 20);
     if (N == 1 && rpw > 0 && (okern == 2 || auto_bpl)) {
         // ~173 VGPRs: two waves per SIMD; 4-wave workgroups, two per CU
         g.bpl = 1;
@@ -826,15 +853,17 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         return g;
     }
     g.grid = owgs > 0 ? owgs : cus;
-    // 16 waves per CU when each still gets a few groups to stream; 8 for
-    // small products, where a second wave per SIMD mostly adds prologue
+    // 16 waves per CU unless the product is small; two groups in flight per
+    // wave once a wave has four or more to stream, else one (a second slot
+    // would mostly run past the wave's rows).  Measured on MI355X.
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
-    g.waves = steps_per_wg >= 48 ? 16 : 8;
+    g.waves = steps_per_wg >= 16 ? 16 : 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves;
+    g.slots = steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
     g.R = 1;
     if (orows == 1 || orows == 2 || orows == 4) g.R = orows;
     const int oslots = g_ovr_slots.load();
-    if (oslots == 2 || oslots == 4 || oslots == 8) g.slots = oslots;
+    if (oslots == 1 || oslots == 2 || oslots == 4 || oslots == 8) g.slots = oslots;
     // only the variants that fit the register file without spilling exist
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.waves = 8;
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.slots = g.slots == 8 ? 4 : 2;
@@ -852,7 +881,8 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)kPre * g.waves * (kWave / lpb);
     g.prologue = pro0_ok ? 0 : 1;
     const int opro = g_ovr_prologue.load();
-    if (opro == 1 || ((opro == 0 || (opro == 2 && g.slots >= 4)) && pro0_ok)) g.prologue = opro;
+    if (opro == 1 || ((opro == 0 || (opro == 2 && g.slots >= 4) || (opro == 3 && g.slots == 2)) && pro0_ok))
+        g.prologue = opro;
     return g;
 }
 
@@ -861,7 +891,12 @@ static const void *gemv_sym(int pro) {
     if constexpr (tile_fits(NC, R, WAVES, S)) {
         if (pro == 0) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 0, S>);
         if (pro == 1) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 1, S>);
-        if constexpr (S >= 4) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 2, S>);
+        if constexpr (S >= 4) {
+            if (pro == 2) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 2, S>);
+        }
+        if constexpr (S == 2) {
+            if (pro == 3) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 3, S>);
+        }
     }
     return nullptr;
 }
@@ -893,8 +928,10 @@ static const void *gemv_sym_r(int nc, int R, int pro) {
 static const void *gemv_kernel_for(int nc, int R, int waves, int pro, int slots) {
     if (waves <= 8) {
         if (slots == 8) return gemv_sym_r<8, 8>(nc, R, pro);
+        if (slots == 1) return gemv_sym_r<8, 1>(nc, R, pro);
         return slots == 4 ? gemv_sym_r<8, 4>(nc, R, pro) : gemv_sym_r<8, 2>(nc, R, pro);
     }
+    if (slots == 1) return gemv_sym_r<16, 1>(nc, R, pro);
     return slots == 4 ? gemv_sym_r<16, 4>(nc, R, pro) : gemv_sym_r<16, 2>(nc, R, pro);
 }
 
@@ -950,6 +987,8 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     if (st != Q4K_OK) return st;
     const Geometry geo = pick_geometry(*di, ne00, ne01, ncols);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
+    // the tile kernel addresses a wave's rows with 31-bit offsets
+    if (!geo.bpl && (int64_t)(geo.rows_base + 1) * nb01 >= ((int64_t)1 << 31)) return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
