@@ -304,7 +304,10 @@ __device__ __forceinline__ void load_xv(const float *src, bool vec_ok, float (&v
     }
 }
 
-template <int LPB>
+// NT: threads per workgroup, a compile-time constant of every kernel (reading
+// blockDim would put a dependent kernel-argument load ahead of the first
+// activation load).
+template <int LPB, int NT>
 __device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int64_t ldx, int K,
                                                 int ncols, bool vec_ok, const FastDiv &fd,
                                                 ActStage<LPB> &st) {
@@ -312,7 +315,7 @@ __device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int e = threadIdx.x & (LPB - 1);
-    const int step = blockDim.x / LPB;
+    constexpr int step = NT / LPB;
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
         const int qb = min((int)(threadIdx.x / LPB) + j * step, total - 1);
@@ -322,7 +325,7 @@ __device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int
     }
 }
 
-template <bool SWZ, int LPB>
+template <bool SWZ, int LPB, int NT>
 __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, int64_t ldx, int K,
                                                  int ncols, bool vec_ok, const FastDiv &fd,
                                                  const ActStage<LPB> &st, int qcol, int8_t *q8s,
@@ -331,7 +334,7 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int e = threadIdx.x & (LPB - 1);
-    const int step = blockDim.x / LPB;
+    constexpr int step = NT / LPB;
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
         const int qb = (int)(threadIdx.x / LPB) + j * step;
@@ -363,12 +366,13 @@ struct Q81Stage {
     uint32_t ds[kPre];
 };
 
+template <int NT>
 __device__ __forceinline__ void stage_q81_issue(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                 int K, int ncols, const FastDiv &fd, Q81Stage &st) {
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int quarter = threadIdx.x & 3;
-    const int step = blockDim.x >> 2;
+    constexpr int step = NT / 4;
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
         const int qb = min((int)(threadIdx.x >> 2) + j * step, total - 1);  // unconditional, as above
@@ -391,7 +395,7 @@ __device__ __forceinline__ void store_q81_part(uint32_t w0, uint32_t w1, uint32_
     if (quarter == 0) dks[qb] = make_float2(d8, d8 * (float)qsum);
 }
 
-template <bool SWZ>
+template <bool SWZ, int NT>
 __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                  int K, int ncols, const FastDiv &fd,
                                                  const Q81Stage &st, int qcol, int8_t *q8s,
@@ -399,7 +403,7 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int quarter = threadIdx.x & 3;
-    const int step = blockDim.x >> 2;
+    constexpr int step = NT / 4;
 #pragma unroll
     for (int j = 0; j < kPre; ++j) {
         const int qb = (threadIdx.x >> 2) + j * step;
@@ -421,13 +425,13 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
 }
 
 // One-call form (issue + finish) for kernels with no loads to overlap.
-template <bool SWZ>
+template <bool SWZ, int NT>
 __device__ __forceinline__ void stage_from_q8_1(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                 int K, int ncols, const FastDiv &fd, int qcol,
                                                 int8_t *q8s, float2 *dks) {
     Q81Stage st;
-    stage_q81_issue(y, stride_col_y, K, ncols, fd, st);
-    stage_q81_finish<SWZ>(y, stride_col_y, K, ncols, fd, st, qcol, q8s, dks);
+    stage_q81_issue<NT>(y, stride_col_y, K, ncols, fd, st);
+    stage_q81_finish<SWZ, NT>(y, stride_col_y, K, ncols, fd, st, qcol, q8s, dks);
 }
 
 }  // namespace q4k

@@ -45,8 +45,8 @@ struct GemvParams {
     int ntiles;              // ceil(M / R) (ceil(M / rpw) for the block-per-lane kernel)
     int vec_ok;              // F32 activation 16-B aligned with ldx % 4 == 0
     int rpw;                 // block-per-lane kernel: rows per wave pass (64/nb or 1)
-    int rows_base;           // tile kernel: each wave owns rows_base rows,
-    int rows_extra;          //   the first rows_extra waves one more
+    int rows_base;           // tile kernel: each workgroup owns rows_base rows,
+    int rows_extra;          //   the first rows_extra workgroups one more
     int ring_off;            // tile kernel: LDS byte offset of the per-wave result rings
     FastDiv nblk32;          // division by K/32 (Q8_1 blocks per column)
 };
@@ -92,15 +92,22 @@ struct Lane {
     ScaleSel sel;
 };
 
-// The contiguous rows [beg, end) a wave owns: M rows split as evenly as
-// possible over all waves of the grid.
+// The contiguous rows [beg, end) a wave owns: the M rows split as evenly as
+// possible over the workgroups (rows_base each, the first rows_extra one
+// more), and each workgroup's share as evenly over its waves.  Every CU gets
+// the same work to within one row and reads one contiguous range.
 struct WaveRows {
     int beg, end;
 };
 
-__device__ __forceinline__ WaveRows wave_rows(const GemvParams &p, int gw) {
-    const int beg = gw * p.rows_base + min(gw, p.rows_extra);
-    return WaveRows{beg, beg + p.rows_base + (gw < p.rows_extra ? 1 : 0)};
+template <int WAVES>
+__device__ __forceinline__ WaveRows wave_rows(const GemvParams &p, int wave) {
+    const int b = (int)blockIdx.x;
+    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
+    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int q = n / WAVES, rem = n - q * WAVES;
+    const int beg = wg_beg + wave * q + min(wave, rem);
+    return WaveRows{beg, beg + q + (wave < rem ? 1 : 0)};
 }
 
 // A wave's rows as one buffer (the host keeps them under 2^31 bytes): a load
@@ -209,9 +216,11 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
         for (int r = 0; r < R; ++r) {
             int sa, sb;
             lane_qdot(w[r].q0, w[r].q1, a.a0, a.a1, a.b0, a.b1, sa, sb);
-            // |sa|, |sb| <= 32*15*127 and sc <= 63: 24-bit products are exact
-            const float xs = a.dk.x * (float)__mul24(sa, sca[r]) + a.dk.z * (float)__mul24(sb, scb[r]);
-            const float ms = a.dk.y * maf[r] + a.dk.w * mbf[r];
+            // |sa|, |sb| <= 32*15*127 and sc <= 63: 24-bit products are exact.
+            // Explicit fmas: every kernel variant rounds identically, so the
+            // result does not depend on the launch geometry.
+            const float xs = __builtin_fmaf(a.dk.x, (float)__mul24(sa, sca[r]), a.dk.z * (float)__mul24(sb, scb[r]));
+            const float ms = __builtin_fmaf(a.dk.y, maf[r], a.dk.w * mbf[r]);
             acc[r][c] = fmaf(d[r], xs, acc[r][c]);
             acc[r][c] = fmaf(-dmin[r], ms, acc[r][c]);
         }
@@ -270,16 +279,15 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
     // the wave index is wave-uniform; readfirstlane lets the compiler keep
     // row numbers and buffer descriptors in scalar registers
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int gw = blockIdx.x * (int)(blockDim.x >> 6) + wave;
-    const WaveRows wr = wave_rows(p, gw);
+    const WaveRows wr = wave_rows<WAVES>(p, wave);
     const WaveStream ws = wave_stream(p, ln, wr, R);
     int remaining = ws.ntiles * p.G;  // steps of this wave
 
     constexpr int kLPB = NC == 1 ? 8 : 4;  // activation lanes per 32-value block
     ActStage<kLPB> xs;
     Q81Stage ys;
-    if (p.x) stage_f32_issue<kLPB>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
-    else stage_q81_issue(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+    if (p.x) stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+    else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
     __syncthreads();  // all activation loads of this CU are queued first
 
     Step st[S];
@@ -289,8 +297,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
     for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], p.G);
 #pragma unroll
     for (int k = 0; k < kEarly; ++k) load_step<R>(p, ln, ws, st[k], w[k]);
-    if (p.x) stage_f32_finish<true, kLPB>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks);
-    else stage_q81_finish<true>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks);
+    if (p.x) stage_f32_finish<true, kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks);
+    else stage_q81_finish<true, kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks);
     __syncthreads();
     if (remaining == 0) return;  // no barrier below this point
 #pragma unroll
@@ -425,14 +433,14 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(GemvParams p
     // each wave's first two passes
     ActStage<8> xs;
     Q81Stage ys;
-    if (p.x) stage_f32_issue<8>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
-    else stage_q81_issue(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
+    if (p.x) stage_f32_issue<8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
+    else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
     __syncthreads();
     u32x4 wa[9], wb[9];
     if (active) load_pass(p, pa, rr, kb, lane_on, wa);
     if (vb) load_pass(p, pb, rr, kb, lane_on, wb);
-    if (p.x) stage_f32_finish<false, 8>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
-    else stage_q81_finish<false>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
+    if (p.x) stage_f32_finish<false, 8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
+    else stage_q81_finish<false, kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
 
@@ -528,8 +536,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(GemvParams p
     const int kb = lane - rr * p.nb;
     const bool lane_on = rr < p.rpw;
 
-    const int tstride = gridDim.x * (int)(blockDim.x >> 6);
-    int pa = blockIdx.x * (int)(blockDim.x >> 6) + wave;
+    const int tstride = gridDim.x * WAVES;
+    int pa = blockIdx.x * WAVES + wave;
     const bool active = pa < p.ntiles;
     int pb = pa + tstride;
     bool vb = active && pb < p.ntiles;
@@ -539,14 +547,14 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(GemvParams p
     // each wave's first two passes
     ActStage<8> xs;
     Q81Stage ys;
-    if (p.x) stage_f32_issue<8>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
-    else stage_q81_issue(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
+    if (p.x) stage_f32_issue<8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
+    else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
     __syncthreads();
     u32x4 wa[9], wb[9];
     if (active) load_pass_coalesced(p, pa, po, wa);
     if (vb) load_pass_coalesced(p, pb, po, wb);
-    if (p.x) stage_f32_finish<false, 8>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
-    else stage_q81_finish<false>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
+    if (p.x) stage_f32_finish<false, 8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
+    else stage_q81_finish<false, kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
 
@@ -628,7 +636,7 @@ __global__ __launch_bounds__(256) void subblock_sums_kernel(SumsParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float2 *dks = reinterpret_cast<float2 *>(lds + p.qcol);
-    stage_from_q8_1<true>(p.y, 0, p.K, 1, p.nblk32, p.qcol, q8s, dks);
+    stage_from_q8_1<true, 256>(p.y, 0, p.K, 1, p.nblk32, p.qcol, q8s, dks);
     __syncthreads();
     GemvParams gp{};
     gp.w = p.w;
@@ -763,7 +771,7 @@ struct Geometry {
     int ntiles = 0;     // block-per-lane kernel: passes
     int bpl = 0;        // 1: block-per-lane kernel
     int rpw = 0;        // block-per-lane kernel: rows per pass
-    int rows_base = 0;  // tile kernel: rows per wave (first rows_extra waves +1)
+    int rows_base = 0;  // tile kernel: rows per workgroup (first rows_extra +1)
     int rows_extra = 0;
     int prologue = 0;   // tile kernel: when the first weight loads go out (PRO)
     int slots = 2;      // tile kernel: groups in flight per wave (S)
@@ -823,7 +831,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         // slot per wave
         g.bpl = 2;
         g.rpw = rpw;
-        g.waves = (owaves >= 1 && owaves <= 8) ? owaves : 8;
+        g.waves = 8;  // the kernel's compile-time workgroup size
         g.ntiles = (int)((M + rpw - 1) / rpw);
         const int wg_needed = (g.ntiles + g.waves - 1) / g.waves;
         int wgs = cus;
@@ -858,20 +866,20 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // would mostly run past the wave's rows).  Measured on MI355X.
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
     g.waves = steps_per_wg >= 16 ? 16 : 8;
-    if (owaves >= 1 && owaves <= 16) g.waves = owaves;
+    if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;  // the instantiated sizes
     g.slots = steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
     g.R = 1;
     if (orows == 1 || orows == 2 || orows == 4) g.R = orows;
     const int oslots = g_ovr_slots.load();
     if (oslots == 1 || oslots == 2 || oslots == 4 || oslots == 8) g.slots = oslots;
     // only the variants that fit the register file without spilling exist
-    if (!tile_fits(nc, g.R, g.waves, g.slots)) g.waves = 8;
+    if (!tile_fits(nc, g.R, g.waves, g.slots)) g.waves = 8;  // (8 fits every R, slots <= 4 variant)
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.slots = g.slots == 8 ? 4 : 2;
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.slots = 2;
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.R = 2;
-    const int64_t total_waves = (int64_t)g.grid * g.waves;
-    g.rows_base = (int)(M / total_waves);
-    g.rows_extra = (int)(M % total_waves);
+    // rows per workgroup (the kernel splits each share over its waves)
+    g.rows_base = (int)(M / g.grid);
+    g.rows_extra = (int)(M % g.grid);
     g.lds = tile_lds_bytes((int)K, nc, g.waves);
     g.lds_launch = g.lds;
     if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
@@ -988,7 +996,7 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     const Geometry geo = pick_geometry(*di, ne00, ne01, ncols);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // the tile kernel addresses a wave's rows with 31-bit offsets
-    if (!geo.bpl && (int64_t)(geo.rows_base + 1) * nb01 >= ((int64_t)1 << 31)) return Q4K_EUNSUPPORTED;
+    if (!geo.bpl && (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31)) return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;

@@ -151,17 +151,21 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
  * out[0] rows per wave tile (tile kernel), out[1] waves per workgroup,
  * out[2] workgroups, out[3] LDS bytes requested per workgroup, out[4] columns per
  * launch, out[5] 1 when the activation is quantised inside the GEMV launch,
- * out[6] kernel (1 tile, 2 block-per-lane), out[7] rows per wave step. */
+ * out[6] kernel (1 tile, 2 block-per-lane, 3 coalesced block kernel),
+ * out[7] rows per wave step. */
 int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
 
 /* Tuning override of the launch geometry for every later call in the
  * process: rows per wave tile of the tile kernel (1, 2, 4), waves per
- * workgroup (1..16; reduced to 8 where 16 would not fit the registers),
- * the number of workgroups and the kernel (1 tile kernel, 2 block-per-lane
- * kernel where it applies); 0 restores the automatic choice.  The environment variables Q4K_ROWS, Q4K_WAVES, Q4K_WGS and
- * Q4K_KERNEL give start-up values.  Not part of the reference interface: a
- * benchmarking knob (ggml's counterpart is editing the compile-time tables
- * of kernels/mmvq.cu:95-147). */
+ * workgroup (tile kernel: 1..8 selects the 8-wave, 9..16 the 16-wave
+ * variant; reduced to 8 where 16 would not fit the registers), the number
+ * of workgroups and the kernel (1 tile kernel, 2 block-per-lane, 3
+ * coalesced block kernel where they apply); 0 restores the automatic
+ * choice.  The environment variables Q4K_ROWS, Q4K_WAVES, Q4K_WGS and
+ * Q4K_KERNEL give start-up values (Q4K_SLOTS and Q4K_PROLOGUE select the
+ * tile kernel's pipeline depth and prologue order).  Not part of the
+ * reference interface: a benchmarking knob (ggml's counterpart is editing
+ * the compile-time tables of kernels/mmvq.cu:95-147). */
 int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32_t workgroups,
                               int32_t kernel);
 
