@@ -57,6 +57,38 @@ struct RowRegs {
     u32x4 h, q0, q1;
 };
 
+// The GEMV kernels take the fields their first memory requests need as
+// leading scalar arguments (16 dwords), ahead of the GemvParams block, so
+// they arrive in one kernel-argument fetch and can be preloaded into scalar
+// registers (-mllvm -amdgpu-kernarg-preload-count=16; measured neutral to
+// slightly slower on MI355X for the 14336 x 4096 product, so not enabled).
+#define Q4K_GEMV_KERNEL_ARGS                                                                      \
+    const float *x_, const uint8_t *y_, const uint8_t *w_, int64_t row_stride_, int ldx_,        \
+        int stride_col_y_, int K_, int vec_ok_, int rows_base_, int rows_extra_, int nb_, int qcol_, \
+        GemvParams p
+#define Q4K_GEMV_HEAD_VALUES \
+    x_, y_, w_, row_stride_, ldx_, stride_col_y_, K_, vec_ok_, rows_base_, rows_extra_, nb_, qcol_
+
+__device__ __forceinline__ GemvParams with_head(GemvParams p, const float *x, const uint8_t *y,
+                                                const uint8_t *w, int64_t row_stride, int ldx,
+                                                int stride_col_y, int K, int vec_ok, int rows_base,
+                                                int rows_extra, int nb, int qcol) {
+    p.x = x;
+    p.y = y;
+    p.w = w;
+    p.row_stride = row_stride;
+    p.ldx = ldx;
+    p.stride_col_y = stride_col_y;
+    p.K = K;
+    p.vec_ok = vec_ok;
+    p.rows_base = rows_base;
+    p.rows_extra = rows_extra;
+    p.nb = nb;
+    p.G = (nb + 15) >> 4;
+    p.qcol = qcol;
+    return p;
+}
+
 // Loads group i (16 super-blocks) of rows [row0, row0 + nrows), nrows <= R;
 // the rows past nrows (all rows when nrows <= 0) and blocks past the row's
 // end read as 0 and cost no memory traffic.
@@ -263,7 +295,8 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
 // instruction, the compiler waits for exactly the group being consumed
 // while the others stay in flight.
 template <int NC, int R, int WAVES, int PRO, int S>
-__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(GemvParams p) {
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     // slots loaded before quantisation
     constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : (PRO == 2 ? S : (PRO == 3 ? 1 : 0));
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -414,7 +447,8 @@ __device__ __forceinline__ void finish_pass(const GemvParams &p, int pass, int r
 }
 
 template <int WAVES>
-__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(GemvParams p) {
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float2 *dks = reinterpret_cast<float2 *>(lds + p.K);
@@ -524,7 +558,8 @@ __device__ __forceinline__ void transpose_pass(uint8_t *slot, int lane, const u3
 }
 
 template <int WAVES>
-__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(GemvParams p) {
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float2 *dks = reinterpret_cast<float2 *>(lds + p.K);
@@ -961,7 +996,10 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
     if (!fn) return Q4K_EINVAL;
     int st = ensure_lds(di, fn, geo.lds_launch);
     if (st != Q4K_OK) return st;
-    void *args[] = {&p};
+    // leading arguments: column strides as 32-bit values (run_gemv checks the range)
+    int32_t ldx32 = (int32_t)p.ldx, scy32 = (int32_t)p.stride_col_y;
+    void *args[] = {&p.x, &p.y, &p.w, &p.row_stride, &ldx32, &scy32, &p.K, &p.vec_ok,
+                    &p.rows_base, &p.rows_extra, &p.nb, &p.qcol, &p};
     hipError_t e = hipLaunchKernel(fn, dim3(geo.grid), dim3(kWave * geo.waves), args,
                                    (size_t)geo.lds_launch, stream);
     if (e != hipSuccess) return hip_fail(e);
@@ -995,8 +1033,10 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     if (st != Q4K_OK) return st;
     const Geometry geo = pick_geometry(*di, ne00, ne01, ncols);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
-    // the tile kernel addresses a wave's rows with 31-bit offsets
+    // the tile kernel addresses a wave's rows with 31-bit offsets; column
+    // strides travel as 32-bit kernel arguments
     if (!geo.bpl && (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31)) return Q4K_EUNSUPPORTED;
+    if (ldx > INT32_MAX || stride_col_y > INT32_MAX) return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
