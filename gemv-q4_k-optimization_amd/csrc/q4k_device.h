@@ -195,15 +195,22 @@ __device__ __forceinline__ uint32_t fastdiv(uint32_t n, const FastDiv &f) {
 // quotient (|v/d| <= 127 and v_rcp_f32 is 1-ulp accurate), so rint(y) is the
 // answer unless y lies within 2^-12 of a half-integer; a lane with such a
 // value (or a NaN) recomputes all its values with the exact division.  One
-// branch per lane instead of one per value.
+// branch per lane instead of one per value.  rint(y) comes from adding
+// 1.5 * 2^23: the sum is exact in its integer part for |y| < 2^22, so its low
+// mantissa bits hold rint(y) (round-to-nearest-even, like the add itself)
+// and subtracting the constant back gives it as a float.  Contraction is off
+// so y is rounded on its own before the add.
 template <int V>
 __device__ __forceinline__ void quantize_values(const float (&v)[V], float d, float rd, int (&q)[V]) {
+#pragma clang fp contract(off)
+    constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
     bool fast = true;
 #pragma unroll
     for (int k = 0; k < V; ++k) {
         const float y = v[k] * rd;
-        q[k] = (int)rintf(y);
-        fast = fast && fabsf(fabsf(y - truncf(y)) - 0.5f) >= 0x1p-12f;
+        const float m = y + kMagic;
+        q[k] = __builtin_bit_cast(int, m) - 0x4B400000;
+        fast = fast && fabsf(y - (m - kMagic)) <= 0.5f - 0x1p-12f;
     }
     if (!fast) {
 #pragma unroll
