@@ -18,7 +18,8 @@ vec_dot_q4_K_q8_K, AVX2, a thread per core) timed on a bounded sample on the
 host cores of the same machine.
 
 --sweep prints one line per (workload, shape, ncols) of the five workloads
-instead of the headline JSON.
+instead of the headline JSON; with --wtype q6_K, of the Q6_K tensors of a
+Q4_K_M model (ffn_down, attn_v, output projection).
 """
 from __future__ import annotations
 
@@ -43,38 +44,44 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(M: int, K: int, N: int) -> int:
-    """Bytes the fused op must move: the Q4_K weight once, the F32
+BLOCK_BYTES = {"q4_K": 144, "q6_K": 210}
+
+
+def algorithmic_bytes(M: int, K: int, N: int, wtype: str = "q4_K") -> int:
+    """Bytes the fused op must move: the quantised weight once, the F32
     activation once and the F32 result once."""
-    return M * (K // 256) * 144 + 4 * N * K + 4 * M * N
+    return M * (K // 256) * BLOCK_BYTES[wtype] + 4 * N * K + 4 * M * N
 
 
-def make_inputs(Q, M, K, N, seed=0):
+def make_inputs(Q, M, K, N, seed=0, wtype="q4_K"):
     import _common
     W = _common.weights(M, K, seed)
-    wq = Q.quantize_rows_q4_K(W, nthreads=min(16, len(os.sched_getaffinity(0))))
+    quant = Q.quantize_rows_q4_K if wtype == "q4_K" else Q.quantize_rows_q6_K
+    wq = quant(W, nthreads=min(16, len(os.sched_getaffinity(0))))
     del W
     x = _common.activations(N, K, seed)
     return wq, x
 
 
 class OpRunner:
-    """Pre-resolved ctypes call of q4k_mul_mat_vec_q over rotating weights."""
+    """Pre-resolved ctypes call of q4k_mul_mat_vec_q (q6k_mul_mat_vec_q for
+    Q6_K) over rotating weights."""
 
-    def __init__(self, Q, wq, x, min_pool_bytes=1 << 30):
+    def __init__(self, Q, wq, x, min_pool_bytes=1 << 30, wtype="q4_K"):
         import ctypes
         import torch
         self.Q = Q
         self.dev = torch.device("cuda:0")
         self.M, self.rb = wq.shape
-        self.K = self.rb // 144 * 256
+        self.K = self.rb // BLOCK_BYTES[wtype] * 256
         self.N = x.shape[0]
         w0 = torch.from_numpy(wq).to(self.dev)
         self.ncopies = max(2, math.ceil(min_pool_bytes / wq.nbytes))
         self.copies = [w0] + [w0.clone() for _ in range(self.ncopies - 1)]
         self.x = torch.from_numpy(x).to(self.dev)
         self.out = torch.empty((self.N, self.M), dtype=torch.float32, device=self.dev)
-        self.fn = Q.lib().q4k_mul_mat_vec_q
+        self.name = "q4k_mul_mat_vec_q" if wtype == "q4_K" else "q6k_mul_mat_vec_q"
+        self.fn = getattr(Q.lib(), self.name)
         self.wptr = [ctypes.c_void_p(c.data_ptr()) for c in self.copies]
         self.args = (self.K, self.M, self.rb, ctypes.c_void_p(self.x.data_ptr()), self.N, self.K * 4,
                      ctypes.c_void_p(self.out.data_ptr()), self.M * 4, None, 0)
@@ -84,7 +91,7 @@ class OpRunner:
         st = self.fn(self.wptr[self.i % self.ncopies], *self.args, stream)
         self.i += 1
         if st != 0:
-            raise self.Q.Q4KError(st, "q4k_mul_mat_vec_q")
+            raise self.Q.Q4KError(st, self.name)
 
 
 def time_gpu(runner: OpRunner, steps: int, warmup: int):
@@ -196,7 +203,10 @@ def sweep(args):
     Q = _pkg()
     rows = []
     seen = set()
-    for wl, items in _common.WORKLOADS.items():
+    wt = args.wtype
+    gtype = Q.GGML_TYPE_Q4_K if wt == "q4_K" else Q.GGML_TYPE_Q6_K
+    table = _common.WORKLOADS if wt == "q4_K" else _common.Q6K_WORKLOADS
+    for wl, items in table.items():
         for M, K, ns in items:
             wq = None
             for N in ns:
@@ -204,16 +214,16 @@ def sweep(args):
                     continue
                 seen.add((M, K, N))
                 if wq is None:
-                    log(f"[sweep] inputs {M}x{K}")
-                    wq, _ = make_inputs(Q, M, K, 1)
+                    log(f"[sweep] inputs {wt} {M}x{K}")
+                    wq, _ = make_inputs(Q, M, K, 1, wtype=wt)
                 x = _common.activations(N, K, 0)
-                runner = OpRunner(Q, wq, x)
+                runner = OpRunner(Q, wq, x, wtype=wt)
                 t = time_gpu(runner, args.steps, args.warmup)
                 sec = t["graph_s"]
-                gbs = algorithmic_bytes(M, K, N) / sec / 1e9
-                r = {"workload": wl, "M": M, "K": K, "N": N, "us_per_call": round(sec * 1e6, 3),
+                gbs = algorithmic_bytes(M, K, N, wt) / sec / 1e9
+                r = {"workload": wl, "wtype": wt, "M": M, "K": K, "N": N, "us_per_call": round(sec * 1e6, 3),
                      "us_eager": round(t["eager_s"] * 1e6, 3), "GBps": round(gbs, 1),
-                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "geometry": Q.geometry(K, M, N)}
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "geometry": Q.geometry(K, M, N, gtype)}
                 rows.append(r)
                 print(json.dumps(r), flush=True)
                 del runner
@@ -226,8 +236,8 @@ def profile_mode(args):
     import torch
     Q = _pkg()
     M, K, N = args.shape
-    wq, x = make_inputs(Q, M, K, N)
-    runner = OpRunner(Q, wq, x)
+    wq, x = make_inputs(Q, M, K, N, wtype=args.wtype)
+    runner = OpRunner(Q, wq, x, wtype=args.wtype)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for _ in range(args.warmup + args.steps):
         runner.step(s)
@@ -307,6 +317,8 @@ def main():
     ap.add_argument("--profile", action="store_true", help="plain launches only, for rocprofv3")
     ap.add_argument("--shape", type=int, nargs=3, default=[14336, 4096, 1], metavar=("M", "K", "N"))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--wtype", choices=sorted(BLOCK_BYTES), default="q4_K",
+                    help="weight format of --sweep and --profile (the headline is Q4_K)")
     ap.add_argument("--stream-probe", action="store_true",
                     help="time a plain streaming read of the GEMV byte counts (ceiling)")
     ap.add_argument("--copy-cal", type=int, default=0, metavar="BYTES",

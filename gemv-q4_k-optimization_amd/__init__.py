@@ -19,9 +19,10 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libq4k_gemv.so")
 
 Q4K_OK, Q4K_EUNSUPPORTED, Q4K_EINVAL, Q4K_EHIP, Q4K_ENOMEM = 0, 1, 2, 3, 4
-GGML_TYPE_F32, GGML_TYPE_Q8_1, GGML_TYPE_Q4_K = 0, 9, 12
+GGML_TYPE_F32, GGML_TYPE_Q8_1, GGML_TYPE_Q4_K, GGML_TYPE_Q6_K = 0, 9, 12, 14
 QK_K = 256
 BLOCK_Q4_K_BYTES = 144
+BLOCK_Q6_K_BYTES = 210
 BLOCK_Q8_1_BYTES = 36
 MATRIX_ROW_PADDING = 512
 
@@ -42,6 +43,11 @@ SIGNATURES = {
     "q4k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
     "q4k_set_geometry_override": (_I, [ctypes.c_int32] * 4),
     "q4k_quantize_rows_q4_K": (_I, [_P, _P, _I64, _I64, _I]),
+    "q6k_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, ctypes.c_size_t, _P]),
+    "q6k_op_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "q6k_group_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P]),
+    "q6k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
+    "q4k_quantize_rows_q6_K": (_I, [_P, _P, _I64, _I64, _I]),
 }
 
 
@@ -118,6 +124,16 @@ def quantize_rows_q4_K(w: np.ndarray, nthreads: int = 8) -> np.ndarray:
     return out
 
 
+def quantize_rows_q6_K(w: np.ndarray, nthreads: int = 8) -> np.ndarray:
+    """Host F32 [M, K] -> Q6_K bytes [M, K/256*210]."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    M, K = w.shape
+    out = np.empty((M, K // QK_K * BLOCK_Q6_K_BYTES), dtype=np.uint8)
+    _check(lib().q4k_quantize_rows_q6_K(w.ctypes.data_as(_P), out.ctypes.data_as(_P), M, K, nthreads),
+           "q4k_quantize_rows_q6_K")
+    return out
+
+
 # ---------------------------------------------------------------- device ----
 def quantize_row_q8_1(x, K: int | None = None, out=None, stream=None):
     """x: float32 cuda [N, K] (row = one activation column) -> uint8 cuda
@@ -133,25 +149,35 @@ def quantize_row_q8_1(x, K: int | None = None, out=None, stream=None):
     return out
 
 
-def mul_mat_vec_q(w_q, K: int, x, out=None, workspace=None, stream=None):
-    """ggml_cuda_mul_mat_vec_q: Q4_K [M, K/256*144] (uint8 cuda) x F32 [N, K]
-    -> F32 [N, M] (row c of the result = column c of ggml's dst)."""
+def _entry(wtype: int, q4k_name: str, q6k_name: str):
+    if wtype == GGML_TYPE_Q4_K:
+        return q4k_name, getattr(lib(), q4k_name)
+    if wtype == GGML_TYPE_Q6_K:
+        return q6k_name, getattr(lib(), q6k_name)
+    raise ValueError(f"weight type {wtype} has no GEMV here")
+
+
+def mul_mat_vec_q(w_q, K: int, x, out=None, workspace=None, stream=None, wtype: int = GGML_TYPE_Q4_K):
+    """ggml_cuda_mul_mat_vec_q: Q4_K [M, K/256*144] or (wtype GGML_TYPE_Q6_K)
+    Q6_K [M, K/256*210] (uint8 cuda) x F32 [N, K] -> F32 [N, M] (row c of the
+    result = column c of ggml's dst)."""
     import torch
     M = w_q.shape[0]
     N = x.shape[0]
     if out is None:
         out = torch.empty((N, M), dtype=torch.float32, device=x.device)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    _check(lib().q4k_mul_mat_vec_q(_ptr(w_q), K, M, w_q.stride(0), _ptr(x), N, x.stride(0) * 4,
-                                   _ptr(out), out.stride(0) * 4, _ptr(workspace), ws_bytes,
-                                   _stream(stream)), "q4k_mul_mat_vec_q")
+    name, fn = _entry(wtype, "q4k_mul_mat_vec_q", "q6k_mul_mat_vec_q")
+    _check(fn(_ptr(w_q), K, M, w_q.stride(0), _ptr(x), N, x.stride(0) * 4, _ptr(out), out.stride(0) * 4,
+              _ptr(workspace), ws_bytes, _stream(stream)), name)
     return out
 
 
 def op_mul_mat_vec_q(w_q, K: int, q8, ncols: int, row_low: int = 0, row_high: int | None = None,
-                     out=None, nrows_dst: int | None = None, stream=None):
+                     out=None, nrows_dst: int | None = None, stream=None, wtype: int = GGML_TYPE_Q4_K):
     """ggml_cuda_op_mul_mat_vec_q: rows [row_low, row_high) of a contiguous
-    Q4_K weight (w_q holds exactly those rows) x pre-quantised Q8_1 columns."""
+    Q4_K (or Q6_K) weight (w_q holds exactly those rows) x pre-quantised Q8_1
+    columns."""
     import torch
     if row_high is None:
         row_high = row_low + w_q.shape[0]
@@ -160,8 +186,9 @@ def op_mul_mat_vec_q(w_q, K: int, q8, ncols: int, row_low: int = 0, row_high: in
     if out is None:
         out = torch.empty((ncols, nrows_dst), dtype=torch.float32, device=q8.device)
     padded = q8.shape[1] // BLOCK_Q8_1_BYTES * 32
-    _check(lib().q4k_op_mul_mat_vec_q(_ptr(w_q), K, row_low, row_high, _ptr(q8), ncols, padded,
-                                      _ptr(out), nrows_dst, _stream(stream)), "q4k_op_mul_mat_vec_q")
+    name, fn = _entry(wtype, "q4k_op_mul_mat_vec_q", "q6k_op_mul_mat_vec_q")
+    _check(fn(_ptr(w_q), K, row_low, row_high, _ptr(q8), ncols, padded, _ptr(out), nrows_dst,
+              _stream(stream)), name)
     return out
 
 
@@ -199,15 +226,28 @@ def subblock_sums(w_q, K: int, q8, ncols: int, stream=None):
     return sqq, sq
 
 
+def group_sums_q6_K(w_q, K: int, q8, ncols: int, stream=None):
+    """Q6_K parity probe: int32 [N, M, K/16] sums of (q - 32) * q8 per
+    16-weight scale group, on the device."""
+    import torch
+    M = w_q.shape[0]
+    s16 = torch.empty((ncols, M, K // 16), dtype=torch.int32, device=q8.device)
+    _check(lib().q6k_group_sums(_ptr(w_q), K, M, w_q.stride(0), _ptr(q8), ncols,
+                                q8.shape[1] // BLOCK_Q8_1_BYTES, _ptr(s16), _stream(stream)),
+           "q6k_group_sums")
+    return s16
+
+
 def set_geometry_override(rows_per_tile: int = 0, waves_per_wg: int = 0, workgroups: int = 0,
                           kernel: int = 0):
     _check(lib().q4k_set_geometry_override(rows_per_tile, waves_per_wg, workgroups, kernel),
            "q4k_set_geometry_override")
 
 
-def geometry(K: int, M: int, N: int) -> dict:
+def geometry(K: int, M: int, N: int, wtype: int = GGML_TYPE_Q4_K) -> dict:
     out = (ctypes.c_int32 * 8)()
-    _check(lib().q4k_gemv_geometry(K, M, N, ctypes.cast(out, _P)), "q4k_gemv_geometry")
+    name, fn = _entry(wtype, "q4k_gemv_geometry", "q6k_gemv_geometry")
+    _check(fn(K, M, N, ctypes.cast(out, _P)), name)
     keys = ("rows_per_tile", "waves_per_wg", "workgroups", "lds_bytes", "cols_per_launch", "fused",
             "kernel", "rows_per_step")
     return dict(zip(keys, list(out)))

@@ -35,20 +35,31 @@ def _run(cmd, verbose):
 def build(verbose: bool = False, save_temps: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     hipcc = _hipcc()
-    dev_obj = os.path.join(BUILD, "q4k_gemv.o")
     host_obj = os.path.join(BUILD, "q4k_quantize_host.o")
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
-           # no packed-FP32 instructions in device code
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-Wall", "-Wno-unused-function",
-           "-c", os.path.join(CSRC, "q4k_gemv.hip"), "-o", dev_obj]
-    if save_temps:
-        cmd.insert(1, f"--save-temps={'obj'}")
-    _run(cmd, verbose)
+    # the device sources compile in parallel (each instantiates many kernels)
+    dev_objs, procs = [], []
+    for src in ("q4k_gemv.hip", "q6k_gemv.hip"):
+        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        cmd = [hipcc, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+               # no packed-FP32 instructions in device code
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               "-Wall", "-Wno-unused-function",
+               "-c", os.path.join(CSRC, src), "-o", obj]
+        if save_temps:
+            cmd.insert(1, "--save-temps=obj")
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+        dev_objs.append(obj)
+    for cmd, pr in procs:
+        out, _ = pr.communicate()
+        if pr.returncode != 0:
+            sys.stderr.write(out)
+            raise RuntimeError(f"build step failed: {' '.join(cmd)}")
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-Wall",
           "-c", os.path.join(CSRC, "q4k_quantize_host.cpp"), "-o", host_obj], verbose)
     tmp = LIB + ".tmp"
-    _run([hipcc, "-shared", "-fPIC", "-o", tmp, dev_obj, host_obj, "-lpthread"], verbose)
+    _run([hipcc, "-shared", "-fPIC", "-o", tmp, *dev_objs, host_obj, "-lpthread"], verbose)
     os.replace(tmp, LIB)
     # measurement aid for bench.py --stream-probe (not part of the library)
     probe_obj = os.path.join(BUILD, "stream_probe.o")

@@ -147,27 +147,66 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 
 // ------------------------------------------------------------------------
 // Activation staging into LDS.  Per column c (qcol bytes apart) the int8 q8
-// values, and after all columns, per 32-value block b,
-// dk[c*K/32 + b] = (d8, d8 * sum of the block's q8) as a float2 -- the
-// second term is the factor of the Q4_K min correction, so the GEMV needs no
-// per-lane byte sums.
+// values, followed after all columns by per-block auxiliary terms whose form
+// depends on the weight type (LAYOUT):
 //
-// Two q8 layouts:
-//   linear   element e at c*qcol + e (qcol = K)
-//   swizzled the tile kernel's read order: element e of super-block
-//            kb = 16i + g, position 64j + 16k + t in the block, at
-//            c*qcol + 4096i + 1024k + 16(4g + j) + t (qcol = 4096*ceil(K/4096)),
-//            so that the 64 lanes of a wave reading chunk k of their blocks
-//            read one contiguous, bank-conflict-free 1 KB.
+//   linear    element e at c*qcol + e (qcol = K)
+//   Q4K tile  the Q4_K tile kernel's read order: element e of super-block
+//             kb = 16i + g, position 64j + 16k + t in the block, at
+//             c*qcol + 4096i + 1024k + 16(4g + j) + t (qcol = 4096*ceil(K/4096)),
+//             so that the 64 lanes of a wave reading chunk k of their blocks
+//             read one contiguous, bank-conflict-free 1 KB.
+//   Q6K tile  the Q6_K tile kernel's read order: position 128h + 32m + 16j' + t
+//             of super-block kb = 16i + g at c*qcol + 4096i + 1024m +
+//             16(4g + 2h + j') + t -- lane 4g + 2h + j' reads, for each m, the 16
+//             values that share one Q6_K scale.
+//
+// Auxiliary terms for the linear and Q4K layouts: per 32-value block b of
+// column c, dk[c*K/32 + b] = (d8, d8 * sum of the block's q8) as a float2 --
+// the second term is the factor of the Q4_K min correction, so the GEMV needs
+// no per-lane byte sums.  For the Q6K layout: d8 as a float per 32-value
+// block (float d8f[ncols*K/32]), then one int per 16-value half block,
+// -32 * (sum of its q8) -- the Q6_K offset correction, the starting value of
+// the lane's dot product -- at sq[ncols*K/32 + c*K/16 + 16kb + 4(2h + j') + m]
+// (int units from the start of the auxiliary area), so a lane's four values
+// are one 16-byte read.
 // ------------------------------------------------------------------------
+constexpr int kLayoutLinear = 0;
+constexpr int kLayoutQ4K = 1;
+constexpr int kLayoutQ6K = 2;
 
 // LDS offset of values [4e, 4e+4) of 32-value block b of column c.
-template <bool SWZ>
+template <int LAYOUT>
 __device__ __forceinline__ int q8_offset(int c, int qcol, int b, int e) {
-    if (!SWZ) return c * qcol + b * 32 + e * 4;
+    if (LAYOUT == kLayoutLinear) return c * qcol + b * 32 + e * 4;
     const int kb = b >> 3, s = b & 7;
-    return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (e >> 2)) * 1024 +
-           ((kb & 15) * 4 + (s >> 1)) * 16 + (e & 3) * 4;
+    if (LAYOUT == kLayoutQ4K)
+        return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (e >> 2)) * 1024 +
+               ((kb & 15) * 4 + (s >> 1)) * 16 + (e & 3) * 4;
+    // Q6K: s = 4h + m, values 16j' + 4(e & 3) + [0, 4) with j' = e >> 2
+    return c * qcol + (kb >> 4) * 4096 + (s & 3) * 1024 + ((kb & 15) * 4 + (s >> 2) * 2 + (e >> 2)) * 16 +
+           (e & 3) * 4;
+}
+
+// Int index (from the start of the auxiliary area) of the Q6K offset
+// correction of half `half` of 32-value block b of column c; total = ncols*K/32.
+__device__ __forceinline__ int q6_sq_index(int total, int nblk, int c, int b, int half) {
+    const int kb = b >> 3, s = b & 7;
+    return total + c * 2 * nblk + kb * 16 + ((s >> 2) * 2 + half) * 4 + (s & 3);
+}
+
+// Stores the auxiliary terms of 32-value block b (qb = c*nblk + b) from the
+// lane holding values 16*half.. of it: d8 = half(d) widened, qsum = sum of
+// all 32 q8 (Q4K/linear), hsum = sum of the lane's 16-value half (Q6K).
+template <int LAYOUT>
+__device__ __forceinline__ void store_aux(void *aux, int total, int nblk, int c, int b, int qb, int half,
+                                          float d8, int qsum, int hsum) {
+    if (LAYOUT == kLayoutQ6K) {
+        if (half == 0) reinterpret_cast<float *>(aux)[qb] = d8;
+        reinterpret_cast<int *>(aux)[q6_sq_index(total, nblk, c, b, half)] = -32 * hsum;
+    } else if (half == 0) {
+        reinterpret_cast<float2 *>(aux)[qb] = make_float2(d8, d8 * (float)qsum);
+    }
 }
 
 // n / d for n < 2^31 as (umulhi(n, mul) + n) >> shift, with mul and shift
@@ -258,17 +297,21 @@ __device__ __forceinline__ float block_max(float v) {
     return v;
 }
 
+// Integer sums over the LPB lanes of a 32-value block: `half` over the lanes
+// holding the lane's 16-value half of the block, `full` over all 32 values.
 template <int LPB>
-__device__ __forceinline__ int block_sum(int v) {
+__device__ __forceinline__ void block_sums(int v, int &half, int &full) {
     v += dpp<kDppXor1>(v);
-    v += dpp<kDppXor2>(v);
-    if (LPB == 8) v += dpp<kDppHalfMirror>(v);
-    return v;
+    if (LPB == 8) v += dpp<kDppXor2>(v);
+    half = v;
+    v += LPB == 8 ? dpp<kDppHalfMirror>(v) : dpp<kDppXor2>(v);
+    full = v;
 }
 
-template <bool SWZ, int LPB>
+template <int LAYOUT, int LPB>
 __device__ __forceinline__ void quantize_block_part(const float (&v)[32 / LPB], int e, int qcol, int c,
-                                                    int b, int qb, int8_t *q8s, float2 *dks) {
+                                                    int b, int qb, int total, int nblk, int8_t *q8s,
+                                                    void *aux) {
     constexpr int V = 32 / LPB;
     float amax = 0.0f;
 #pragma unroll
@@ -289,12 +332,13 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[32 / LPB], 
             word[k / 4] |= (uint32_t)(q[k] & 0xff) << (8 * (k % 4));
         }
     }
-    qsum = block_sum<LPB>(qsum);
-    int8_t *dst = q8s + q8_offset<SWZ>(c, qcol, b, e * (V / 4));
+    int hsum, fsum;
+    block_sums<LPB>(qsum, hsum, fsum);
+    int8_t *dst = q8s + q8_offset<LAYOUT>(c, qcol, b, e * (V / 4));
     if (V == 4) *reinterpret_cast<uint32_t *>(dst) = word[0];
     else *reinterpret_cast<uint2 *>(dst) = make_uint2(word[0], word[V / 4 - 1]);
     const float d8 = (float)(_Float16)d;
-    if (e == 0) dks[qb] = make_float2(d8, d8 * (float)qsum);
+    if ((e & (LPB / 2 - 1)) == 0) store_aux<LAYOUT>(aux, total, nblk, c, b, qb, e / (LPB / 2), d8, fsum, hsum);
 }
 
 template <int V>
@@ -332,11 +376,11 @@ __device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int
     }
 }
 
-template <bool SWZ, int LPB, int NT>
+template <int LAYOUT, int LPB, int NT>
 __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, int64_t ldx, int K,
                                                  int ncols, bool vec_ok, const FastDiv &fd,
                                                  const ActStage<LPB> &st, int qcol, int8_t *q8s,
-                                                 float2 *dks) {
+                                                 void *aux) {
     constexpr int V = 32 / LPB;
     const int nblk = K / 32;
     const int total = ncols * nblk;
@@ -347,7 +391,7 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
         const int qb = (int)(threadIdx.x / LPB) + j * step;
         if (qb < total) {
             const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
-            quantize_block_part<SWZ, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, q8s, dks);
+            quantize_block_part<LAYOUT, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, total, nblk, q8s, aux);
         }
     }
     for (int qb = (int)(threadIdx.x / LPB) + kPre * step; qb < total; qb += step) {
@@ -355,15 +399,8 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
         const int b = qb - c * nblk;
         float v[V];
         load_xv<V>(x + c * ldx + b * 32 + e * V, vec_ok, v);
-        quantize_block_part<SWZ, LPB>(v, e, qcol, c, b, qb, q8s, dks);
+        quantize_block_part<LAYOUT, LPB>(v, e, qcol, c, b, qb, total, nblk, q8s, aux);
     }
-}
-
-// Sum of the four lanes of a quad (lanes 4k..4k+3).
-__device__ __forceinline__ int quad_sum(int v) {
-    v += dpp<kDppXor1>(v);
-    v += dpp<kDppXor2>(v);
-    return v;
 }
 
 // Already-quantised AoS block_q8_1 (column stride stride_col_y blocks) -> LDS,
@@ -391,22 +428,24 @@ __device__ __forceinline__ void stage_q81_issue(const uint8_t *__restrict__ y, i
     }
 }
 
-template <bool SWZ>
+template <int LAYOUT>
 __device__ __forceinline__ void store_q81_part(uint32_t w0, uint32_t w1, uint32_t ds, int quarter,
-                                               int qcol, int c, int b, int qb, int8_t *q8s, float2 *dks) {
-    const int qsum = quad_sum(__builtin_amdgcn_sdot4((int)w0, 0x01010101,
-                                                     __builtin_amdgcn_sdot4((int)w1, 0x01010101, 0, false),
-                                                     false));
-    *reinterpret_cast<uint2 *>(q8s + q8_offset<SWZ>(c, qcol, b, 2 * quarter)) = make_uint2(w0, w1);
-    const float d8 = half_bits_to_float(ds);
-    if (quarter == 0) dks[qb] = make_float2(d8, d8 * (float)qsum);
+                                               int qcol, int c, int b, int qb, int total, int nblk,
+                                               int8_t *q8s, void *aux) {
+    int hsum, fsum;
+    block_sums<4>(__builtin_amdgcn_sdot4((int)w0, 0x01010101, __builtin_amdgcn_sdot4((int)w1, 0x01010101, 0, false),
+                                         false),
+                  hsum, fsum);
+    *reinterpret_cast<uint2 *>(q8s + q8_offset<LAYOUT>(c, qcol, b, 2 * quarter)) = make_uint2(w0, w1);
+    if ((quarter & 1) == 0)
+        store_aux<LAYOUT>(aux, total, nblk, c, b, qb, quarter >> 1, half_bits_to_float(ds), fsum, hsum);
 }
 
-template <bool SWZ, int NT>
+template <int LAYOUT, int NT>
 __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                  int K, int ncols, const FastDiv &fd,
                                                  const Q81Stage &st, int qcol, int8_t *q8s,
-                                                 float2 *dks) {
+                                                 void *aux) {
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int quarter = threadIdx.x & 3;
@@ -416,8 +455,8 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
         const int qb = (threadIdx.x >> 2) + j * step;
         if (qb < total) {
             const int c = (int)fastdiv((uint32_t)qb, fd);
-            store_q81_part<SWZ>(st.w[j][0], st.w[j][1], st.ds[j], quarter, qcol, c, qb - c * nblk, qb,
-                                q8s, dks);
+            store_q81_part<LAYOUT>(st.w[j][0], st.w[j][1], st.ds[j], quarter, qcol, c, qb - c * nblk, qb,
+                                   total, nblk, q8s, aux);
         }
     }
     for (int qb = (threadIdx.x >> 2) + kPre * step; qb < total; qb += step) {
@@ -426,19 +465,19 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
         const uint8_t *blk = y + ((int64_t)c * stride_col_y + b) * kQ81Bytes;
         const uint32_t w0 = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
         const uint32_t w1 = *reinterpret_cast<const uint32_t *>(blk + 8 + quarter * 8);
-        store_q81_part<SWZ>(w0, w1, *reinterpret_cast<const uint32_t *>(blk), quarter, qcol, c, b, qb,
-                            q8s, dks);
+        store_q81_part<LAYOUT>(w0, w1, *reinterpret_cast<const uint32_t *>(blk), quarter, qcol, c, b, qb,
+                               total, nblk, q8s, aux);
     }
 }
 
 // One-call form (issue + finish) for kernels with no loads to overlap.
-template <bool SWZ, int NT>
+template <int LAYOUT, int NT>
 __device__ __forceinline__ void stage_from_q8_1(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                 int K, int ncols, const FastDiv &fd, int qcol,
-                                                int8_t *q8s, float2 *dks) {
+                                                int8_t *q8s, void *aux) {
     Q81Stage st;
     stage_q81_issue<NT>(y, stride_col_y, K, ncols, fd, st);
-    stage_q81_finish<SWZ, NT>(y, stride_col_y, K, ncols, fd, st, qcol, q8s, dks);
+    stage_q81_finish<LAYOUT, NT>(y, stride_col_y, K, ncols, fd, st, qcol, q8s, aux);
 }
 
 }  // namespace q4k

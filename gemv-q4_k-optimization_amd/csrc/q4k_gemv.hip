@@ -24,70 +24,16 @@
 #include <vector>
 
 #include "../../include/q4k_gemv.h"
-#include "q4k_device.h"
+#include "q4k_runtime.h"
+#include "q4k_tile.h"
 
 namespace q4k {
-
-struct GemvParams {
-    const uint8_t *w;        // weight rows (Q4_K)
-    int64_t row_stride;      // bytes between rows
-    const float *x;          // F32 activation (staged with quantisation) or null
-    int64_t ldx;             // floats between activation columns
-    const uint8_t *y;        // AoS Q8_1 activation when x is null
-    int64_t stride_col_y;    // blocks between Q8_1 columns
-    float *dst;
-    int64_t ld_dst;          // floats between output columns
-    int M;                   // rows
-    int K;                   // values per row
-    int nb;                  // super-blocks per row (K/256)
-    int G;                   // groups of 16 super-blocks per row
-    int qcol;                // LDS bytes between the staged q8 columns
-    int ntiles;              // ceil(M / R) (ceil(M / rpw) for the block-per-lane kernel)
-    int vec_ok;              // F32 activation 16-B aligned with ldx % 4 == 0
-    int rpw;                 // block-per-lane kernel: rows per wave pass (64/nb or 1)
-    int rows_base;           // tile kernel: each workgroup owns rows_base rows,
-    int rows_extra;          //   the first rows_extra workgroups one more
-    int ring_off;            // tile kernel: LDS byte offset of the per-wave result rings
-    FastDiv nblk32;          // division by K/32 (Q8_1 blocks per column)
-};
 
 // One row's share of a group in a lane's registers: the block header and the
 // lane's 32 qs bytes.
 struct RowRegs {
     u32x4 h, q0, q1;
 };
-
-// The GEMV kernels take the fields their first memory requests need as
-// leading scalar arguments (16 dwords), ahead of the GemvParams block, so
-// they arrive in one kernel-argument fetch and can be preloaded into scalar
-// registers (-mllvm -amdgpu-kernarg-preload-count=16; measured neutral to
-// slightly slower on MI355X for the 14336 x 4096 product, so not enabled).
-#define Q4K_GEMV_KERNEL_ARGS                                                                      \
-    const float *x_, const uint8_t *y_, const uint8_t *w_, int64_t row_stride_, int ldx_,        \
-        int stride_col_y_, int K_, int vec_ok_, int rows_base_, int rows_extra_, int nb_, int qcol_, \
-        GemvParams p
-#define Q4K_GEMV_HEAD_VALUES \
-    x_, y_, w_, row_stride_, ldx_, stride_col_y_, K_, vec_ok_, rows_base_, rows_extra_, nb_, qcol_
-
-__device__ __forceinline__ GemvParams with_head(GemvParams p, const float *x, const uint8_t *y,
-                                                const uint8_t *w, int64_t row_stride, int ldx,
-                                                int stride_col_y, int K, int vec_ok, int rows_base,
-                                                int rows_extra, int nb, int qcol) {
-    p.x = x;
-    p.y = y;
-    p.w = w;
-    p.row_stride = row_stride;
-    p.ldx = ldx;
-    p.stride_col_y = stride_col_y;
-    p.K = K;
-    p.vec_ok = vec_ok;
-    p.rows_base = rows_base;
-    p.rows_extra = rows_extra;
-    p.nb = nb;
-    p.G = (nb + 15) >> 4;
-    p.qcol = qcol;
-    return p;
-}
 
 // Loads group i (16 super-blocks) of rows [row0, row0 + nrows), nrows <= R;
 // the rows past nrows (all rows when nrows <= 0) and blocks past the row's
@@ -108,39 +54,11 @@ __device__ __forceinline__ void load_group(const GemvParams &p, int row0, int nr
     }
 }
 
-// Position of a wave in its sequence of (row tile, group) steps.
-struct Step {
-    int tile;
-    int i;
-};
-
-__device__ __forceinline__ Step next_step(Step s, int G) {
-    return s.i + 1 == G ? Step{s.tile + 1, 0} : Step{s.tile, s.i + 1};
-}
-
 // Per-lane constants of the lane map (lane = 4g + j).
 struct Lane {
     int lane, g, j;
     ScaleSel sel;
 };
-
-// The contiguous rows [beg, end) a wave owns: the M rows split as evenly as
-// possible over the workgroups (rows_base each, the first rows_extra one
-// more), and each workgroup's share as evenly over its waves.  Every CU gets
-// the same work to within one row and reads one contiguous range.
-struct WaveRows {
-    int beg, end;
-};
-
-template <int WAVES>
-__device__ __forceinline__ WaveRows wave_rows(const GemvParams &p, int wave) {
-    const int b = (int)blockIdx.x;
-    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
-    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
-    const int q = n / WAVES, rem = n - q * WAVES;
-    const int beg = wg_beg + wave * q + min(wave, rem);
-    return WaveRows{beg, beg + q + (wave < rem ? 1 : 0)};
-}
 
 // A wave's rows as one buffer (the host keeps them under 2^31 bytes): a load
 // past them or past a row's last block reads 0 without memory traffic.
@@ -197,31 +115,6 @@ __device__ __forceinline__ LaneAct lane_act(const GemvParams &p, const Lane &ln,
     return a;
 }
 
-// Results of a wave, buffered in LDS and written to dst in coalesced runs:
-// entry e is column e % NC of row beg + e / NC.
-constexpr int kRing = 256;  // floats per wave
-
-struct ResultRing {
-    float *buf;   // this wave's kRing floats of LDS
-    int beg;      // first row of the wave
-    int end;      // one past its last row
-    int base;     // entries already written out
-    int n;        // entries buffered
-};
-
-// Writes the buffered entries to dst (entries of rows >= end are dropped).
-template <int NC>
-__device__ __forceinline__ void ring_flush(const GemvParams &p, int lane, ResultRing &rr) {
-    for (int k = lane; k < rr.n; k += kWave) {
-        const int idx = rr.base + k;
-        const int row = rr.beg + idx / NC;
-        const int c = idx - (idx / NC) * NC;
-        if (row < rr.end) p.dst[(int64_t)c * p.ld_dst + row] = rr.buf[k];
-    }
-    rr.base += rr.n;
-    rr.n = 0;
-}
-
 // Consumes one group (16 super-blocks of R rows) held in w; on the last group
 // of a tile reduces the R x NC sums over the wave into the result ring.
 template <int NC, int R>
@@ -257,22 +150,7 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
             acc[r][c] = fmaf(-dmin[r], ms, acc[r][c]);
         }
     }
-    if (st.i == p.G - 1) {
-        float out = 0.0f;
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const float s = wave_sum(acc[r][c]);
-                if (ln.lane == r * NC + c) out = s;
-                acc[r][c] = 0.0f;
-            }
-        if (ln.lane < R * NC) rr.buf[rr.n + ln.lane] = out;
-        rr.n += R * NC;
-        // rare (a wave's rows x NC above kRing): global stores inside the
-        // loop make the compiler's load waits conservative
-        if (rr.n + R * NC > kRing) ring_flush<NC>(p, ln.lane, rr);
-    }
+    if (st.i == p.G - 1) tile_to_ring<NC, R>(p, ln.lane, acc, rr);
 }
 
 // Tile kernel: any K, 1..8 columns.  One workgroup per CU (the launch asks
@@ -330,8 +208,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], p.G);
 #pragma unroll
     for (int k = 0; k < kEarly; ++k) load_step<R>(p, ln, ws, st[k], w[k]);
-    if (p.x) stage_f32_finish<true, kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks);
-    else stage_q81_finish<true, kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks);
+    if (p.x) stage_f32_finish<kLayoutQ4K, kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks);
+    else stage_q81_finish<kLayoutQ4K, kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks);
     __syncthreads();
     if (remaining == 0) return;  // no barrier below this point
 #pragma unroll
@@ -473,8 +351,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(Q4K_GEMV_KER
     u32x4 wa[9], wb[9];
     if (active) load_pass(p, pa, rr, kb, lane_on, wa);
     if (vb) load_pass(p, pb, rr, kb, lane_on, wb);
-    if (p.x) stage_f32_finish<false, 8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
-    else stage_q81_finish<false, kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
+    if (p.x) stage_f32_finish<kLayoutLinear, 8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
+    else stage_q81_finish<kLayoutLinear, kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
 
@@ -588,8 +466,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(Q4K_GEMV_KER
     u32x4 wa[9], wb[9];
     if (active) load_pass_coalesced(p, pa, po, wa);
     if (vb) load_pass_coalesced(p, pb, po, wb);
-    if (p.x) stage_f32_finish<false, 8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
-    else stage_q81_finish<false, kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
+    if (p.x) stage_f32_finish<kLayoutLinear, 8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
+    else stage_q81_finish<kLayoutLinear, kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
 
@@ -671,7 +549,7 @@ __global__ __launch_bounds__(256) void subblock_sums_kernel(SumsParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float2 *dks = reinterpret_cast<float2 *>(lds + p.qcol);
-    stage_from_q8_1<true, 256>(p.y, 0, p.K, 1, p.nblk32, p.qcol, q8s, dks);
+    stage_from_q8_1<kLayoutQ4K, 256>(p.y, 0, p.K, 1, p.nblk32, p.qcol, q8s, dks);
     __syncthreads();
     GemvParams gp{};
     gp.w = p.w;
@@ -712,28 +590,16 @@ __global__ __launch_bounds__(256) void subblock_sums_kernel(SumsParams p) {
 // host side
 // ------------------------------------------------------------------------
 
-static thread_local int32_t g_last_hip_error = 0;
+thread_local int32_t g_last_hip_error = 0;
 
-static int hip_fail(hipError_t e) {
+int hip_fail(hipError_t e) {
     g_last_hip_error = (int32_t)e;
     return Q4K_EHIP;
 }
 
-struct DeviceInfo {
-    bool ok = false;
-    bool supported = false;
-    int cus = 0;
-    int max_lds = 0;
-    std::once_flag once;
-    // dynamic-LDS attribute already raised for a kernel (by address)
-    std::mutex attr_mu;
-    std::vector<const void *> attr_done;
-};
-
-static constexpr int kMaxDevices = 64;
 static DeviceInfo g_dev[kMaxDevices];
 
-static int device_info(DeviceInfo **out) {
+int device_info(DeviceInfo **out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e);
@@ -756,7 +622,7 @@ static int device_info(DeviceInfo **out) {
     return Q4K_OK;
 }
 
-static int ensure_lds(DeviceInfo *di, const void *fn, int bytes) {
+int ensure_lds(DeviceInfo *di, const void *fn, int bytes) {
     if (bytes <= 65536) return Q4K_OK;
     std::lock_guard<std::mutex> lk(di->attr_mu);
     for (const void *f : di->attr_done)
@@ -775,10 +641,10 @@ static int env_int(const char *name, int dflt) {
 // Geometry overrides for tuning sweeps (0 = automatic): set through
 // q4k_set_geometry_override or, as start-up defaults, the environment
 // variables Q4K_ROWS, Q4K_WAVES and Q4K_WGS.
-static std::atomic<int> g_ovr_rows{-1}, g_ovr_waves{-1}, g_ovr_wgs{-1}, g_ovr_kernel{-1};
-static std::atomic<int> g_ovr_prologue{-1}, g_ovr_slots{-1};
+std::atomic<int> g_ovr_rows{-1}, g_ovr_waves{-1}, g_ovr_wgs{-1}, g_ovr_kernel{-1};
+std::atomic<int> g_ovr_prologue{-1}, g_ovr_slots{-1};
 
-static void load_env_overrides() {
+void load_env_overrides() {
     static std::once_flag once;
     std::call_once(once, []() {
         int expect = -1;
@@ -834,7 +700,6 @@ static int bpl_rows_per_pass(int64_t nb) {
 // LDS bytes of the staged activation: q8 columns (swizzled, padded to whole
 // 16-block groups, for the tile kernel; linear for the one-column block
 // kernels) followed by the per-32-value (d8, d8*sum q8) pairs.
-static int q8_col_bytes(int K) { return (K + 4095) / 4096 * 4096; }
 static int lds_bytes(int K, int nc) { return nc * (q8_col_bytes(K) + K / 4); }
 // The tile kernel adds a kRing-float result ring per wave after the activation.
 static int tile_lds_bytes(int K, int nc, int waves) { return lds_bytes(K, nc) + waves * kRing * 4; }
@@ -1008,10 +873,6 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
     return Q4K_OK;
 }
 
-static bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
-
-static int64_t pad512(int64_t k) { return (k + 511) / 512 * 512; }
-
 // Shared checks of the weight operand.
 static int check_weight(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01) {
     if (ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0) return Q4K_EINVAL;
@@ -1182,15 +1043,17 @@ int q4k_ggml_mul_mat_vec_q(const q4k_tensor *src0, const q4k_tensor *src1, const
                            size_t workspace_bytes, void *stream) {
     if (!src0 || !src1 || !dst) return Q4K_EINVAL;
     if (src1->type != Q4K_GGML_TYPE_F32 || dst->type != Q4K_GGML_TYPE_F32) return Q4K_EINVAL;
-    if (src0->type != Q4K_GGML_TYPE_Q4_K) return Q4K_EUNSUPPORTED;
-    if (src0->nb[0] != (size_t)kBlockBytes || src1->nb[0] != 4 || dst->nb[0] != 4) return Q4K_EINVAL;
+    if (src0->type != Q4K_GGML_TYPE_Q4_K && src0->type != Q4K_GGML_TYPE_Q6_K) return Q4K_EUNSUPPORTED;
+    const bool q6 = src0->type == Q4K_GGML_TYPE_Q6_K;
+    const size_t block_bytes = q6 ? Q4K_BLOCK_Q6_K_BYTES : (size_t)kBlockBytes;
+    if (src0->nb[0] != block_bytes || src1->nb[0] != 4 || dst->nb[0] != 4) return Q4K_EINVAL;
     if (ids || fusion) return Q4K_EUNSUPPORTED;
     for (int d = 2; d < 4; ++d)
         if (src0->ne[d] != 1 || src1->ne[d] != 1 || dst->ne[d] != 1) return Q4K_EUNSUPPORTED;
     if (src1->ne[0] != src0->ne[0] || dst->ne[0] != src0->ne[1] || dst->ne[1] != src1->ne[1])
         return Q4K_EINVAL;
     // ggml's nb00 is the block size: ne00 counts values, ne00/256 blocks per row
-    return q4k_mul_mat_vec_q(src0->data, src0->ne[0], src0->ne[1], (int64_t)src0->nb[1],
+    return (q6 ? q6k_mul_mat_vec_q : q4k_mul_mat_vec_q)(src0->data, src0->ne[0], src0->ne[1], (int64_t)src0->nb[1],
                              static_cast<const float *>(src1->data), src1->ne[1],
                              (int64_t)src1->nb[1], static_cast<float *>(dst->data),
                              (int64_t)dst->nb[1], workspace, workspace_bytes, stream);

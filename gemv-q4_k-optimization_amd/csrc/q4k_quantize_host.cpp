@@ -1,8 +1,10 @@
-// q4k_quantize_host.cpp -- host F32 -> Q4_K weight quantiser.
+// q4k_quantize_host.cpp -- host F32 -> Q4_K and Q6_K weight quantisers.
 //
-// Produces the weight format the GEMV consumes, with the arithmetic of ggml's
-// quantize_row_q4_K_ref (ggml-quants.c; the reference consumes its output and
-// does not vendor it).  Per 256-value super-block:
+// Produce the weight formats the GEMVs consume, with the arithmetic of
+// ggml's quantize_row_q4_K_ref and quantize_row_q6_K_ref (ggml-quants.c; the
+// reference consumes their output and does not vendor them).
+//
+// Q4_K, per 256-value super-block:
 //   1. each 32-value sub-block gets a weighted least-squares fit
 //      x ~ scale*L + min, L in [0,15], min <= 0 (weights sqrt(mean x^2)+|x|,
 //      21 candidate inverse scales (15 + -1 + 0.1*k)/(max-min));
@@ -10,6 +12,15 @@
 //      d = fp16(max_scale/63), dmin = fp16(max_min/63);
 //   3. every value is re-quantised against the fp16 (d*sc, dmin*m) it will be
 //      decoded with, and the nibbles are packed 32 low + 32 high per 32 bytes.
+// Q6_K, per 256-value super-block:
+//   1. each 16-value group gets a fit x ~ scale*l, l in [-32, 31], weighted by
+//      x^2, over 19 candidate inverse scales -(32 + 0.1*k)/x_m (k = -9..9,
+//      x_m the value of largest magnitude), keeping the best by sum(wxl)^2/sum(wl^2);
+//   2. the group scales are quantised to int8 against the one of largest
+//      magnitude s_m: iscale = -128/s_m, sc = min(127, round(iscale*scale)),
+//      d = fp16(1/iscale);
+//   3. every value is re-quantised against fp16(d)*sc, and l + 32 is split
+//      into ql (low nibbles) and qh (2-bit fields).
 // Built with -ffp-contract=off: every float expression rounds as written,
 // which the byte-for-byte agreement with ggml's reference code relies on.
 #include <cmath>
@@ -193,15 +204,109 @@ void quantize_block(const float *x, uint8_t *out) {
             qs[32 * c + i] = (uint8_t)(levels[64 * c + i] | (levels[64 * c + 32 + i] << 4));
 }
 
-}  // namespace
+// ---------------------------------------------------------------- Q6_K ----
 
-extern "C" int q4k_quantize_rows_q4_K(const float *src, void *dst, int64_t nrows, int64_t n_per_row,
-                                      int nthreads) {
+constexpr int kQ6Bytes = 210;
+constexpr float kGroupEps = 1e-15f;  // ggml's GROUP_MAX_EPS
+
+inline int clamp_q6(int v) { return v < -32 ? -32 : (v > 31 ? 31 : v); }
+
+// Fit of one 16-value group (ggml's make_qx_quants with nmax 32, weights
+// x^2): returns the scale and writes the levels l + 32.
+float fit_group16(const float *x, int8_t *levels) {
+    float amax = 0.0f, xm = 0.0f;
+    for (int i = 0; i < 16; ++i) {
+        const float ax = std::fabs(x[i]);
+        if (ax > amax) {
+            amax = ax;
+            xm = x[i];
+        }
+    }
+    if (amax < kGroupEps) {
+        for (int i = 0; i < 16; ++i) levels[i] = 0;
+        return 0.0f;
+    }
+    float iscale = -32.0f / xm;
+    float sumlx = 0.0f, suml2 = 0.0f;
+    for (int i = 0; i < 16; ++i) {
+        const int l = clamp_q6(round_half_even(iscale * x[i]));
+        levels[i] = (int8_t)(l + 32);
+        const float w = x[i] * x[i];
+        sumlx += w * x[i] * (float)l;
+        suml2 += w * (float)l * (float)l;
+    }
+    float scale = suml2 != 0.0f ? sumlx / suml2 : 0.0f;
+    float best = scale * sumlx;
+    for (int k = -9; k <= 9; ++k) {
+        if (k == 0) continue;
+        iscale = -(32.0f + 0.1f * (float)k) / xm;
+        sumlx = suml2 = 0.0f;
+        for (int i = 0; i < 16; ++i) {
+            const int l = clamp_q6(round_half_even(iscale * x[i]));
+            const float w = x[i] * x[i];
+            sumlx += w * x[i] * (float)l;
+            suml2 += w * (float)l * (float)l;
+        }
+        if (suml2 > 0.0f && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < 16; ++i) levels[i] = (int8_t)(clamp_q6(round_half_even(iscale * x[i])) + 32);
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+        }
+    }
+    return scale;
+}
+
+void quantize_block_q6(const float *x, uint8_t *out) {
+    int8_t levels[kBlock];
+    float scales[16];
+    float max_scale = 0.0f, max_abs = 0.0f;
+    for (int g = 0; g < 16; ++g) {
+        scales[g] = fit_group16(x + 16 * g, levels + 16 * g);
+        const float a = std::fabs(scales[g]);
+        if (a > max_abs) {
+            max_abs = a;
+            max_scale = scales[g];
+        }
+    }
+    if (max_abs < kGroupEps) {
+        std::memset(out, 0, kQ6Bytes);
+        return;
+    }
+    const float iscale = -128.0f / max_scale;
+    const uint16_t dh = to_half(1.0f / iscale);
+    int8_t *sc = reinterpret_cast<int8_t *>(out + 192);
+    for (int g = 0; g < 16; ++g) {
+        const int v = round_half_even(iscale * scales[g]);
+        sc[g] = (int8_t)(v < 127 ? v : 127);
+    }
+    const float d = from_half(dh);
+    for (int g = 0; g < 16; ++g) {
+        const float dg = d * (float)sc[g];
+        if (dg == 0.0f) continue;
+        for (int i = 0; i < 16; ++i)
+            levels[16 * g + i] = (int8_t)(clamp_q6(round_half_even(x[16 * g + i] / dg)) + 32);
+    }
+    uint8_t *ql = out, *qh = out + 128;
+    for (int h = 0; h < 2; ++h) {
+        const int8_t *L = levels + 128 * h;
+        for (int l = 0; l < 32; ++l) {
+            ql[64 * h + l] = (uint8_t)((L[l] & 0xf) | ((L[l + 64] & 0xf) << 4));
+            ql[64 * h + 32 + l] = (uint8_t)((L[l + 32] & 0xf) | ((L[l + 96] & 0xf) << 4));
+            qh[32 * h + l] = (uint8_t)((L[l] >> 4) | ((L[l + 32] >> 4) << 2) | ((L[l + 64] >> 4) << 4) |
+                                       ((L[l + 96] >> 4) << 6));
+        }
+    }
+    out[208] = (uint8_t)(dh & 0xff);
+    out[209] = (uint8_t)(dh >> 8);
+}
+
+// nrows x n_per_row floats -> blocks of `bytes` each, on up to nthreads threads.
+int quantize_rows(const float *src, void *dst, int64_t nrows, int64_t n_per_row, int nthreads, int bytes,
+                  void (*block_fn)(const float *, uint8_t *)) {
     if (nrows < 0 || n_per_row <= 0 || n_per_row % kBlock != 0) return Q4K_EINVAL;
     if (nrows == 0) return Q4K_OK;
     if (!src || !dst) return Q4K_EINVAL;
-    const int64_t nb = n_per_row / kBlock;
-    const int64_t total = nrows * nb;
+    const int64_t total = nrows * (n_per_row / kBlock);
     uint8_t *out = static_cast<uint8_t *>(dst);
     if (nthreads < 1) nthreads = 1;
     std::atomic<int64_t> next{0};
@@ -211,7 +316,7 @@ extern "C" int q4k_quantize_rows_q4_K(const float *src, void *dst, int64_t nrows
             const int64_t b0 = next.fetch_add(chunk);
             if (b0 >= total) break;
             const int64_t b1 = b0 + chunk < total ? b0 + chunk : total;
-            for (int64_t b = b0; b < b1; ++b) quantize_block(src + b * kBlock, out + b * kBytes);
+            for (int64_t b = b0; b < b1; ++b) block_fn(src + b * kBlock, out + b * bytes);
         }
     };
     std::vector<std::thread> pool;
@@ -219,4 +324,16 @@ extern "C" int q4k_quantize_rows_q4_K(const float *src, void *dst, int64_t nrows
     work();
     for (auto &t : pool) t.join();
     return Q4K_OK;
+}
+
+}  // namespace
+
+extern "C" int q4k_quantize_rows_q4_K(const float *src, void *dst, int64_t nrows, int64_t n_per_row,
+                                      int nthreads) {
+    return quantize_rows(src, dst, nrows, n_per_row, nthreads, kBytes, quantize_block);
+}
+
+extern "C" int q4k_quantize_rows_q6_K(const float *src, void *dst, int64_t nrows, int64_t n_per_row,
+                                      int nthreads) {
+    return quantize_rows(src, dst, nrows, n_per_row, nthreads, kQ6Bytes, quantize_block_q6);
 }

@@ -1,0 +1,53 @@
+// q4k_runtime.h -- host-side state and helpers shared by the K-quant GEMV
+// entry points (Q4_K in q4k_gemv.hip, Q6_K in q6k_gemv.hip): per-device
+// properties, the dynamic-LDS attribute, the last HIP error, the tuning
+// overrides and small layout helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <mutex>
+#include <vector>
+
+#include "../../include/q4k_gemv.h"
+
+namespace q4k {
+
+// hipError_t of the most recent Q4K_EHIP on this thread
+extern thread_local int32_t g_last_hip_error;
+// records e and returns Q4K_EHIP
+int hip_fail(hipError_t e);
+
+struct DeviceInfo {
+    bool ok = false;
+    bool supported = false;
+    int cus = 0;
+    int max_lds = 0;
+    std::once_flag once;
+    // dynamic-LDS attribute already raised for a kernel (by address)
+    std::mutex attr_mu;
+    std::vector<const void *> attr_done;
+};
+
+constexpr int kMaxDevices = 64;
+
+// The current device's properties, read once per device; Q4K_EUNSUPPORTED on
+// anything but gfx950.
+int device_info(DeviceInfo **out);
+// Raises a kernel's dynamic-LDS limit once when it asks for more than 64 KB.
+int ensure_lds(DeviceInfo *di, const void *fn, int bytes);
+
+// Geometry overrides for tuning sweeps (0 = automatic, -1 = not yet read from
+// the environment).
+extern std::atomic<int> g_ovr_rows, g_ovr_waves, g_ovr_wgs, g_ovr_kernel;
+extern std::atomic<int> g_ovr_prologue, g_ovr_slots;
+void load_env_overrides();
+
+inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+inline int64_t pad512(int64_t k) { return (k + 511) / 512 * 512; }
+// LDS bytes of one staged q8 column in a tile layout (whole 16-block groups)
+inline int q8_col_bytes(int K) { return (K + 4095) / 4096 * 4096; }
+
+}  // namespace q4k

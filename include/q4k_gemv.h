@@ -52,10 +52,12 @@ typedef enum q4k_status {
 #define Q4K_GGML_TYPE_F32 0
 #define Q4K_GGML_TYPE_Q8_1 9
 #define Q4K_GGML_TYPE_Q4_K 12
+#define Q4K_GGML_TYPE_Q6_K 14
 
 #define Q4K_QK_K 256            /* weights per Q4_K super-block */
 #define Q4K_BLOCK_Q4_K_BYTES 144 /* d, dmin (fp16), scales[12], qs[128]; kernels/2pack.cu:6 */
 #define Q4K_BLOCK_Q8_1_BYTES 36  /* ds (half2), qs[32]; kernels/2pack.cu:7 */
+#define Q4K_BLOCK_Q6_K_BYTES 210 /* ql[128], qh[64], scales[16] (int8), d (fp16) */
 #define Q4K_MATRIX_ROW_PADDING 512 /* K padding of the Q8_1 temp; kernels/mmvq.cu:728 */
 #define Q4K_MAX_BATCH 8         /* MMVQ_MAX_BATCH_SIZE; kernels/mmvq.cu:394 */
 
@@ -124,11 +126,14 @@ int q4k_op_mul_mat_vec_q(const void *src0_dd_i, int64_t ne00, int64_t row_low, i
                          int64_t src1_padded_row_size, float *dst_dd_i, int64_t nrows_dst,
                          void *stream);
 
-/* ggml-descriptor form of q4k_mul_mat_vec_q: the signature of
- * ggml_cuda_mul_mat_vec_q (kernels/mmvq.cu:666-668) with ggml_tensor
- * replaced by q4k_tensor and the backend context by (workspace, stream).
- * Checks the reference's assertions: src1/dst F32 (:669-670), nb00 == 144,
- * nb10 == 4, nb0 == 4 (:681-683), ne10 == ne00, ne0 == ne01, ne1 == ne11.
+/* ggml-descriptor form of q4k_mul_mat_vec_q / q6k_mul_mat_vec_q: the
+ * signature of ggml_cuda_mul_mat_vec_q (kernels/mmvq.cu:666-668) with
+ * ggml_tensor replaced by q4k_tensor and the backend context by (workspace,
+ * stream).  src0->type selects the weight format (Q4K_GGML_TYPE_Q4_K or
+ * Q4K_GGML_TYPE_Q6_K, the reference's type switch at kernels/mmvq.cu:536,
+ * :600-605; any other type returns Q4K_EUNSUPPORTED).
+ * Checks the reference's assertions: src1/dst F32 (:669-670), nb00 == block
+ * size, nb10 == 4, nb0 == 4 (:681-683), ne10 == ne00, ne0 == ne01, ne1 == ne11.
  * Returns Q4K_EUNSUPPORTED for what this path does not implement: ids
  * (MUL_MAT_ID), fusion (gate/bias/GLU), more than one channel or sample
  * (ne2/ne3 > 1) -- the cases the reference's simple_ok gate also excludes. */
@@ -146,6 +151,41 @@ int q4k_ggml_mul_mat_vec_q(const q4k_tensor *src0, const q4k_tensor *src1, const
 int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
                       const void *q8_1, int64_t ncols, int64_t stride_col_y, int32_t *sqq,
                       int32_t *sq, void *stream);
+
+/* ------------------------------------------------------------- Q6_K ---- */
+
+/* dst = src0 (Q6_K, ne01 x ne00) * src1 (F32, ne00 x ne11): the Q6_K case of
+ * ggml_cuda_mul_mat_vec_q (kernels/mmvq.cu:600-605 dispatches
+ * mul_mat_vec_q<GGML_TYPE_Q6_K>, whose per-block dot product is
+ * kernels/vecdotq.cuh:867-891 with :580-600).  Arguments, layout rules and
+ * statuses as q4k_mul_mat_vec_q, except: src0 rows are block_q6_K (210 bytes
+ * per 256 weights, nb01 a multiple of 210) and src0 needs 2-byte alignment.
+ * Per block the product is d * sum over 16-weight groups g of
+ * d8(g/2) * scales[g] * S_g, S_g = sum of (q - 32) * q8 (int32, exact). */
+int q6k_mul_mat_vec_q(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
+                      const float *src1, int64_t ne11, int64_t nb11, float *dst, int64_t nb1,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/* Row-slice Q6_K GEMV on an already-quantised activation: the Q6_K case of
+ * ggml_cuda_op_mul_mat_vec_q (kernels/mmvq.cu:764-793); arguments as
+ * q4k_op_mul_mat_vec_q with src0_dd_i holding ne00/256 block_q6_K per row. */
+int q6k_op_mul_mat_vec_q(const void *src0_dd_i, int64_t ne00, int64_t row_low, int64_t row_high,
+                         const void *src1_ddq_i, int64_t src1_ncols,
+                         int64_t src1_padded_row_size, float *dst_dd_i, int64_t nrows_dst,
+                         void *stream);
+
+/* Parity probe of the Q6_K GEMV: the int32 sums S_g over every 16-weight
+ * scale group g of (q - 32) * q8, computed with the GEMV kernel's lane map,
+ * activation staging and dot routine:
+ *   s16[(c*ne01 + r)*(ne00/16) + g]
+ * These are the dp4a sums of kernels/vecdotq.cuh:589-593 (vi - 32 against
+ * u) summed over the four lanes that share a scale. */
+int q6k_group_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const void *q8_1,
+                   int64_t ncols, int64_t stride_col_y, int32_t *s16, void *stream);
+
+/* Launch geometry q6k_mul_mat_vec_q would use (the out[] fields of
+ * q4k_gemv_geometry; out[7] = weight groups in flight per wave). */
+int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
 
 /* Launch geometry q4k_mul_mat_vec_q would use on the current device:
  * out[0] rows per wave tile (tile kernel), out[1] waves per workgroup,
@@ -177,6 +217,13 @@ int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32
  * format the reference consumes); the byte layout is fixed by
  * kernels/vecdotq.cuh:785-807. */
 int q4k_quantize_rows_q4_K(const float *src, void *dst, int64_t nrows, int64_t n_per_row,
+                           int nthreads);
+
+/* Host Q6_K quantiser: nrows rows of n_per_row floats (multiple of 256) into
+ * nrows * n_per_row/256 block_q6_K, using up to nthreads threads.  Replaces
+ * quantize_row_q6_K_ref row by row (ggml-quants.c); the byte layout is fixed
+ * by kernels/vecdotq.cuh:867-891. */
+int q4k_quantize_rows_q6_K(const float *src, void *dst, int64_t nrows, int64_t n_per_row,
                            int nthreads);
 
 #ifdef __cplusplus

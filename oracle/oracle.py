@@ -1,4 +1,4 @@
-"""numpy bindings of the CPU oracle (oracle/q4k_oracle.c).
+"""numpy bindings of the CPU oracle (oracle/q4k_oracle.c, oracle/q6k_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: the checker for the HIP product path and the CPU
 baseline the benchmark times beside it.  Only tests/, the smoke entry point and
@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(HERE, "libq4k_oracle.so")
 QK_K = 256
 QK8_1 = 32
 Q4K_BYTES = 144
+Q6K_BYTES = 210
 Q81_BYTES = 36
 Q8K_BYTES = 292
 MATRIX_ROW_PADDING = 512  # kernels/mmvq.cu:728 pads K to this for the Q8_1 temp
@@ -66,6 +67,9 @@ def lib():
             "orc_cpu_has_avx2": (I, []),
             "orc_cpu_mul_mat_q4_K": (I, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I]),
             "orc_time_cpu_mul_mat_q4_K": (None, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I, I, P]),
+            "orc_quantize_q6_K": (None, [P, P, I64]),
+            "orc_dequantize_q6_K": (None, [P, P, I64]),
+            "orc_gemv_q6K_q8_1": (I64, [P, I64, I64, I64, P, I64, I64, P, P, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -126,6 +130,27 @@ def dequantize_q4_K(q: np.ndarray, K: int) -> np.ndarray:
     return out
 
 
+def quantize_q6_K(w: np.ndarray) -> np.ndarray:
+    """F32 [M, K] -> Q6_K bytes [M, K/256*210] (quantize_row_q6_K_ref per row)."""
+    w = np.ascontiguousarray(np.atleast_2d(w), dtype=np.float32)
+    M, K = w.shape
+    assert K % QK_K == 0
+    out = np.empty((M, K // QK_K * Q6K_BYTES), dtype=np.uint8)
+    for r in range(M):
+        lib().orc_quantize_q6_K(_p(w[r]), _p(out[r]), K)
+    return out
+
+
+def dequantize_q6_K(q: np.ndarray, K: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    M = q.size // (K // QK_K * Q6K_BYTES)
+    q = q.reshape(M, -1)
+    out = np.empty((M, K), dtype=np.float32)
+    for r in range(M):
+        lib().orc_dequantize_q6_K(_p(q[r]), _p(out[r]), K)
+    return out
+
+
 def quantize_q8_1(x: np.ndarray, k_padded: int | None = None) -> np.ndarray:
     """F32 [N, K] -> Q8_1 bytes [N, K_pad/32*36] with ggml-cuda semantics."""
     x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
@@ -162,6 +187,24 @@ def gemv_q4K_q8_1(w_q: np.ndarray, K: int, q8: np.ndarray, want_sums: bool = Tru
     lib().orc_gemv_q4K_q8_1(_p(w_q), M, K, row_bytes, _p(q8), N, stride_col_y, _p(y64), _p(l1),
                             _p(sqq) if want_sums else None, _p(sq) if want_sums else None)
     return {"y64": y64, "l1": l1, "sqq": sqq, "sq": sq}
+
+
+def gemv_q6K_q8_1(w_q: np.ndarray, K: int, q8: np.ndarray, want_sums: bool = True):
+    """Q6_K [M, K/256*210] x Q8_1 [N, Kp/32*36] -> dict(y64 [N,M], l1 [N,M],
+    s16 [N,M,K/16] int32 sums of (q - 32) * q8 per 16-weight group,
+    mismatches: scale-index / group-index disagreements (0 expected))."""
+    w_q = np.ascontiguousarray(w_q, dtype=np.uint8)
+    q8 = np.ascontiguousarray(np.atleast_2d(q8), dtype=np.uint8)
+    row_bytes = K // QK_K * Q6K_BYTES
+    M = w_q.size // row_bytes
+    N = q8.shape[0]
+    stride_col_y = q8.shape[1] // Q81_BYTES
+    y64 = np.empty((N, M), dtype=np.float64)
+    l1 = np.empty((N, M), dtype=np.float64)
+    s16 = np.empty((N, M, K // 16), dtype=np.int32) if want_sums else None
+    mism = lib().orc_gemv_q6K_q8_1(_p(w_q), M, K, row_bytes, _p(q8), N, stride_col_y, _p(y64), _p(l1),
+                                   _p(s16) if want_sums else None)
+    return {"y64": y64, "l1": l1, "s16": s16, "mismatches": int(mism)}
 
 
 def vec_dot_q4_K_q8_K(w_row: np.ndarray, y_row: np.ndarray, K: int, isa: str = "avx2") -> float:

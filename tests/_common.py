@@ -24,6 +24,13 @@ WORKLOADS = {
     "lm_head_128256": [(128256, 4096, [1, 8])],
 }
 
+# Q6_K tensors of a Q4_K_M Mistral-7B (v0.3 vocabulary) / Llama-3-8B:
+# ffn_down and attn_v of half the layers, and the output projection
+Q6K_WORKLOADS = {
+    "q4km_q6k_tensors": [(4096, 14336, [1, 2, 4, 8]), (1024, 4096, [1, 4, 8]), (32768, 4096, [1, 8]),
+                         (128256, 4096, [1, 8])],
+}
+
 STREAM_W, STREAM_X = 1, 2
 
 

@@ -14,13 +14,14 @@ HEADER = os.path.join(_common.ROOT, "include", "q4k_gemv.h")
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(q4k_[A-Za-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(q[46]k_[A-Za-z0-9_]+)\s*\(", text)))
 
 
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("q4k_mul_mat_vec_q", "q4k_op_mul_mat_vec_q", "q4k_ggml_mul_mat_vec_q",
-              "q4k_quantize_row_q8_1", "q4k_subblock_sums", "q4k_quantize_rows_q4_K"):
+              "q4k_quantize_row_q8_1", "q4k_subblock_sums", "q4k_quantize_rows_q4_K",
+              "q6k_mul_mat_vec_q", "q6k_op_mul_mat_vec_q", "q6k_group_sums", "q4k_quantize_rows_q6_K"):
         assert n in names
 
 
@@ -74,8 +75,10 @@ def test_op_and_descriptor_checks(Q):
     st = L2.q4k_ggml_mul_mat_vec_q(ctypes.byref(s0), ctypes.byref(s1), None, ctypes.byref(d),
                                    ctypes.c_void_p(0x40000), None, 0, None)
     assert st == Q.Q4K_EUNSUPPORTED                                          # fusion
-    q6 = Q.make_tensor(14, [4096, 16], [210, 3360], 0x10000)
-    assert Q.ggml_mul_mat_vec_q(q6, s1, d) == Q.Q4K_EUNSUPPORTED             # other types
+    q5 = Q.make_tensor(13, [4096, 16], [176, 2816], 0x10000)
+    assert Q.ggml_mul_mat_vec_q(q5, s1, d) == Q.Q4K_EUNSUPPORTED             # other types
+    q6 = Q.make_tensor(Q.GGML_TYPE_Q6_K, [4096, 16], [144, 3360], 0x10000)
+    assert Q.ggml_mul_mat_vec_q(q6, s1, d) == Q.Q4K_EINVAL                   # nb00 != 210
     s3 = Q.make_tensor(Q.GGML_TYPE_F32, [4096, 1, 2], [4, 16384, 16384], 0x20000)
     assert Q.ggml_mul_mat_vec_q(s0, s3, d) == Q.Q4K_EUNSUPPORTED             # batched 3-D
     assert L.q4k_quantize_row_q8_1(FAKE, FAKE, 100, 100, 96, 1, None) == Q.Q4K_EINVAL
@@ -87,3 +90,30 @@ def test_host_quantiser_rejects_bad_shapes(Q):
     import numpy as np
     with pytest.raises(Q.Q4KError):
         Q.quantize_rows_q4_K(np.zeros((2, 300), np.float32))
+
+
+FAKE_2 = ctypes.c_void_p(0x10002)   # 2-byte aligned: enough for Q6_K rows
+FAKE_1 = ctypes.c_void_p(0x10001)
+
+
+@pytest.mark.parametrize("args,status", [
+    ((FAKE, 4000, 16, 4000 // 256 * 210, FAKE, 1, 16000, FAKE, 64), 2),   # K % 256
+    ((FAKE, 4096, 16, 3360, FAKE, 9, 16384, FAKE, 64), 2),                  # 9 columns
+    ((FAKE, 4096, 16, 3364, FAKE, 1, 16384, FAKE, 64), 2),                  # row stride % 210
+    ((FAKE, 4096, 16, 3150, FAKE, 1, 16384, FAKE, 64), 2),                  # row stride < row
+    ((FAKE, 4096, 16, 3360, None, 1, 16384, FAKE, 64), 2),                  # null src1
+    ((FAKE_1, 4096, 16, 3360, FAKE, 1, 16384, FAKE, 64), 2),                # src0 alignment
+    ((FAKE_2, 4096, 0, 3360, FAKE, 1, 16384, FAKE, 64), 0),                 # empty: no rows
+    ((FAKE, 4096, 16, 3360, FAKE, 0, 16384, FAKE, 64), 0),                  # empty: no columns
+])
+def test_q6k_mul_mat_vec_q_argument_checks(Q, args, status):
+    assert Q.lib().q6k_mul_mat_vec_q(*args, None, 0, None) == status
+
+
+def test_q6k_op_and_probe_checks(Q):
+    L = Q.lib()
+    assert L.q6k_op_mul_mat_vec_q(FAKE, 4096, 10, 5, FAKE, 1, 4096, FAKE, 5, None) == Q.Q4K_EINVAL
+    assert L.q6k_op_mul_mat_vec_q(FAKE, 4096, 0, 8, FAKE, 1, 4000, FAKE, 8, None) == Q.Q4K_EINVAL
+    assert L.q6k_op_mul_mat_vec_q(FAKE, 4096, 3, 3, FAKE, 1, 4096, FAKE, 4, None) == Q.Q4K_OK
+    assert L.q6k_group_sums(FAKE, 4096, 4, 3360, FAKE, 1, 100, FAKE, None) == Q.Q4K_EINVAL
+    assert L.q6k_group_sums(FAKE, 4096, 0, 3360, FAKE, 1, 128, FAKE, None) == Q.Q4K_OK
