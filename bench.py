@@ -94,6 +94,57 @@ class OpRunner:
             raise self.Q.Q4KError(st, self.name)
 
 
+class FusedRunner(OpRunner):
+    """q4k_mul_mat_vec_q_fused with a gate weight and SWIGLU over rotating
+    (weight, gate) pairs: one launch computes silu(gate . x) * (up . x)."""
+
+    def __init__(self, Q, wq, gq, x, min_pool_bytes=1 << 30, wtype="q4_K", glu_op=2):
+        import ctypes
+        super().__init__(Q, wq, x, min_pool_bytes=min_pool_bytes // 2, wtype=wtype)
+        import torch
+        g0 = torch.from_numpy(gq).to(self.dev)
+        self.gcopies = [g0] + [g0.clone() for _ in range(self.ncopies - 1)]
+        self.fusions = [Q.q4k_fusion(None, ctypes.c_void_p(g.data_ptr()), None, glu_op) for g in self.gcopies]
+        self.type_id = Q.GGML_TYPE_Q4_K if wtype == "q4_K" else Q.GGML_TYPE_Q6_K
+        self.name = "q4k_mul_mat_vec_q_fused"
+        self.fn = Q.lib().q4k_mul_mat_vec_q_fused
+        self.fargs = (self.K, self.M, self.rb, ctypes.c_void_p(self.x.data_ptr()))
+        self.outp = ctypes.c_void_p(self.out.data_ptr())
+
+    def step(self, stream):
+        import ctypes
+        k = self.i % self.ncopies
+        st = self.fn(self.type_id, self.wptr[k], *self.fargs, ctypes.byref(self.fusions[k]), self.outp, stream)
+        self.i += 1
+        if st != 0:
+            raise self.Q.Q4KError(st, self.name)
+
+
+def fused_sweep(args):
+    """Gate+up with SWIGLU in one launch against the two plain launches, on
+    the FFN shapes (batch 1, the only fused case)."""
+    import _common
+    import torch
+    Q = _pkg()
+    wt = args.wtype
+    for M, K in ((14336, 4096), (4096, 4096), (28672, 8192)):
+        wu, x = make_inputs(Q, M, K, 1, seed=0, wtype=wt)
+        wg, _ = make_inputs(Q, M, K, 1, seed=1, wtype=wt)
+        fr = FusedRunner(Q, wu, wg, x, wtype=wt)
+        tf = time_gpu(fr, args.steps, args.warmup)["graph_s"]
+        del fr
+        torch.cuda.empty_cache()
+        pr = OpRunner(Q, wu, x, wtype=wt)
+        tp = time_gpu(pr, args.steps, args.warmup)["graph_s"]
+        del pr
+        torch.cuda.empty_cache()
+        nbytes = 2 * M * (K // 256) * BLOCK_BYTES[wt] + 4 * K + 4 * M
+        r = {"workload": "ffn_gate_up_swiglu_b1", "wtype": wt, "M": M, "K": K, "N": 1,
+             "us_fused": round(tf * 1e6, 3), "us_two_plain": round(2 * tp * 1e6, 3),
+             "GBps_fused": round(nbytes / tf / 1e9, 1), "hbm_frac": round(nbytes / tf / 1e9 / HBM_PEAK_GBS, 4)}
+        print(json.dumps(r), flush=True)
+
+
 def time_gpu(runner: OpRunner, steps: int, warmup: int):
     """Returns dict with graph-launched and eager seconds per step."""
     import ctypes
@@ -317,6 +368,8 @@ def main():
     ap.add_argument("--profile", action="store_true", help="plain launches only, for rocprofv3")
     ap.add_argument("--shape", type=int, nargs=3, default=[14336, 4096, 1], metavar=("M", "K", "N"))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--fused", action="store_true",
+                    help="time the gate+up SWIGLU launch against two plain launches")
     ap.add_argument("--wtype", choices=sorted(BLOCK_BYTES), default="q4_K",
                     help="weight format of --sweep and --profile (the headline is Q4_K)")
     ap.add_argument("--stream-probe", action="store_true",
@@ -333,6 +386,8 @@ def main():
         stream_probe(args)
     elif args.copy_cal:
         copy_calibration(args)
+    elif args.fused:
+        fused_sweep(args)
     elif args.sweep:
         sweep(args)
     elif args.profile:

@@ -42,6 +42,8 @@ SIGNATURES = {
     "q4k_subblock_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P]),
     "q4k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
     "q4k_set_geometry_override": (_I, [ctypes.c_int32] * 4),
+    "q4k_set_pipeline_override": (_I, [ctypes.c_int32] * 2),
+    "q4k_mul_mat_vec_q_fused": (_I, [ctypes.c_int32, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
     "q4k_quantize_rows_q4_K": (_I, [_P, _P, _I64, _I64, _I]),
     "q6k_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, ctypes.c_size_t, _P]),
     "q6k_op_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
@@ -55,6 +57,21 @@ class q4k_tensor(ctypes.Structure):
     """The ggml_tensor subset of include/q4k_gemv.h."""
     _fields_ = [("type", ctypes.c_int32), ("ne", ctypes.c_int64 * 4), ("nb", ctypes.c_size_t * 4),
                 ("data", ctypes.c_void_p)]
+
+
+class q4k_fusion(ctypes.Structure):
+    """Fused epilogue, device pointers (include/q4k_gemv.h)."""
+    _fields_ = [("x_bias", ctypes.c_void_p), ("gate", ctypes.c_void_p), ("gate_bias", ctypes.c_void_p),
+                ("glu_op", ctypes.c_int32)]
+
+
+class q4k_fusion_args(ctypes.Structure):
+    """Fused epilogue, tensor descriptors (ggml_cuda_mm_fusion_args_host)."""
+    _fields_ = [("x_bias", ctypes.POINTER(q4k_tensor)), ("gate", ctypes.POINTER(q4k_tensor)),
+                ("gate_bias", ctypes.POINTER(q4k_tensor)), ("glu_op", ctypes.c_int32)]
+
+
+GLU_OP_GEGLU, GLU_OP_SWIGLU, GLU_OP_SWIGLU_OAI = 1, 2, 3
 
 
 class Q4KError(RuntimeError):
@@ -173,6 +190,20 @@ def mul_mat_vec_q(w_q, K: int, x, out=None, workspace=None, stream=None, wtype: 
     return out
 
 
+def mul_mat_vec_q_fused(w_q, K: int, x, gate=None, x_bias=None, gate_bias=None, glu_op: int = GLU_OP_SWIGLU,
+                        out=None, stream=None, wtype: int = GGML_TYPE_Q4_K):
+    """One column with the fused epilogue: dst = x_bias + w_q . x, or with a
+    gate weight glu(w_q . x + x_bias, gate . x + gate_bias) -> F32 [1, M]."""
+    import torch
+    M = w_q.shape[0]
+    if out is None:
+        out = torch.empty((1, M), dtype=torch.float32, device=x.device)
+    f = q4k_fusion(_ptr(x_bias), _ptr(gate), _ptr(gate_bias), glu_op)
+    _check(lib().q4k_mul_mat_vec_q_fused(wtype, _ptr(w_q), K, M, w_q.stride(0), _ptr(x), ctypes.byref(f),
+                                         _ptr(out), _stream(stream)), "q4k_mul_mat_vec_q_fused")
+    return out
+
+
 def op_mul_mat_vec_q(w_q, K: int, q8, ncols: int, row_low: int = 0, row_high: int | None = None,
                      out=None, nrows_dst: int | None = None, stream=None, wtype: int = GGML_TYPE_Q4_K):
     """ggml_cuda_op_mul_mat_vec_q: rows [row_low, row_high) of a contiguous
@@ -210,8 +241,9 @@ def ggml_mul_mat_vec_q(src0: q4k_tensor, src1: q4k_tensor, dst: q4k_tensor, ids=
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     return int(lib().q4k_ggml_mul_mat_vec_q(ctypes.byref(src0), ctypes.byref(src1),
                                             ctypes.byref(ids) if ids is not None else None,
-                                            ctypes.byref(dst), fusion, _ptr(workspace), ws_bytes,
-                                            _stream(stream)))
+                                            ctypes.byref(dst),
+                                            ctypes.byref(fusion) if fusion is not None else None,
+                                            _ptr(workspace), ws_bytes, _stream(stream)))
 
 
 def subblock_sums(w_q, K: int, q8, ncols: int, stream=None):
@@ -242,6 +274,10 @@ def set_geometry_override(rows_per_tile: int = 0, waves_per_wg: int = 0, workgro
                           kernel: int = 0):
     _check(lib().q4k_set_geometry_override(rows_per_tile, waves_per_wg, workgroups, kernel),
            "q4k_set_geometry_override")
+
+
+def set_pipeline_override(slots: int = 0, prologue: int = -1):
+    _check(lib().q4k_set_pipeline_override(slots, prologue), "q4k_set_pipeline_override")
 
 
 def geometry(K: int, M: int, N: int, wtype: int = GGML_TYPE_Q4_K) -> dict:

@@ -78,19 +78,24 @@ __device__ __forceinline__ WaveStream wave_stream(const GemvParams &p, const Lan
     return ws;
 }
 
-template <int R>
+// Loads one step: R rows of the tile, or with GLU (R = 2) one row of the
+// weight (w[0]) and the same row of the gate weight (w[1], buffer rs_gate).
+template <int R, bool GLU>
 __device__ __forceinline__ void load_step(const GemvParams &p, const Lane &ln, const WaveStream &ws,
-                                          Step st, RowRegs (&w)[R]) {
-    const uint32_t base = (uint32_t)(st.tile * R) * (uint32_t)p.row_stride + (uint32_t)st.i * (16 * kBlockBytes);
+                                          __amdgpu_buffer_rsrc_t rs_gate, Step st, RowRegs (&w)[R]) {
+    constexpr int kRowsPerTile = GLU ? 1 : R;
+    const uint32_t base =
+        (uint32_t)(st.tile * kRowsPerTile) * (uint32_t)p.row_stride + (uint32_t)st.i * (16 * kBlockBytes);
     const bool ok = st.tile < ws.ntiles && 16 * st.i + ln.g < p.nb;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t ro = base + (uint32_t)(r * p.row_stride);
+        const uint32_t ro = GLU ? base : base + (uint32_t)(r * p.row_stride);
+        const __amdgpu_buffer_rsrc_t rs = GLU && r == 1 ? rs_gate : ws.rs;
         const uint32_t oh = ok ? ro + ws.lh : kOOB;
         const uint32_t oq = ok ? ro + ws.lq : kOOB;
-        w[r].h = load16(ws.rs, oh);
-        w[r].q0 = load16(ws.rs, oq);
-        w[r].q1 = load16(ws.rs, oq + 16u);
+        w[r].h = load16(rs, oh);
+        w[r].q0 = load16(rs, oq);
+        w[r].q1 = load16(rs, oq + 16u);
     }
 }
 
@@ -117,7 +122,7 @@ __device__ __forceinline__ LaneAct lane_act(const GemvParams &p, const Lane &ln,
 
 // Consumes one group (16 super-blocks of R rows) held in w; on the last group
 // of a tile reduces the R x NC sums over the wave into the result ring.
-template <int NC, int R>
+template <int NC, int R, bool GLU>
 __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &ln, Step st,
                                               const int8_t *q8s, const float2 *dks,
                                               const RowRegs (&w)[R], float (&acc)[R][NC],
@@ -150,7 +155,7 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
             acc[r][c] = fmaf(-dmin[r], ms, acc[r][c]);
         }
     }
-    if (st.i == p.G - 1) tile_to_ring<NC, R>(p, ln.lane, acc, rr);
+    if (st.i == p.G - 1) tile_to_ring<NC, R, GLU>(p, ln.lane, acc, rr);
 }
 
 // Tile kernel: any K, 1..8 columns.  One workgroup per CU (the launch asks
@@ -172,8 +177,14 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
 // memory, inside the loop: with no branch around a vector memory
 // instruction, the compiler waits for exactly the group being consumed
 // while the others stay in flight.
-template <int NC, int R, int WAVES, int PRO, int S>
+//
+// GLU (one column, R = 2): each tile is one row of the weight and the same
+// row of the gate weight (kernels/mmvq.cu:254-262 computes both products
+// from the same activation); the ring holds the pair and its flush applies
+// the biases and the GLU.
+template <int NC, int R, int WAVES, int PRO, int S, bool GLU>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    static_assert(!GLU || (NC == 1 && R == 2), "the fused epilogue pairs one row of each weight");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     // slots loaded before quantisation
     constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : (PRO == 2 ? S : (PRO == 3 ? 1 : 0));
@@ -191,7 +202,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     // row numbers and buffer descriptors in scalar registers
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WaveRows wr = wave_rows<WAVES>(p, wave);
-    const WaveStream ws = wave_stream(p, ln, wr, R);
+    const WaveStream ws = wave_stream(p, ln, wr, GLU ? 1 : R);
+    const __amdgpu_buffer_rsrc_t rs_gate =
+        GLU ? make_rsrc(p.gate + (int64_t)wr.beg * p.row_stride, (uint32_t)((wr.end - wr.beg) * p.row_stride))
+            : ws.rs;
     int remaining = ws.ntiles * p.G;  // steps of this wave
 
     constexpr int kLPB = NC == 1 ? 8 : 4;  // activation lanes per 32-value block
@@ -207,13 +221,13 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
 #pragma unroll
     for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], p.G);
 #pragma unroll
-    for (int k = 0; k < kEarly; ++k) load_step<R>(p, ln, ws, st[k], w[k]);
+    for (int k = 0; k < kEarly; ++k) load_step<R, GLU>(p, ln, ws, rs_gate, st[k], w[k]);
     if (p.x) stage_f32_finish<kLayoutQ4K, kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks);
     else stage_q81_finish<kLayoutQ4K, kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks);
     __syncthreads();
     if (remaining == 0) return;  // no barrier below this point
 #pragma unroll
-    for (int k = kEarly; k < S; ++k) load_step<R>(p, ln, ws, st[k], w[k]);
+    for (int k = kEarly; k < S; ++k) load_step<R, GLU>(p, ln, ws, rs_gate, st[k], w[k]);
 
     float acc[R][NC];
 #pragma unroll
@@ -229,14 +243,14 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     for (;;) {
 #pragma unroll
         for (int k = 0; k < S; ++k) {
-            process_group<NC, R>(p, ln, st[k], q8s, dks, w[k], acc, rr);
+            process_group<NC, R, GLU>(p, ln, st[k], q8s, dks, w[k], acc, rr);
             st[k] = next_step(st[(k + S - 1) % S], p.G);
-            load_step<R>(p, ln, ws, st[k], w[k]);
+            load_step<R, GLU>(p, ln, ws, rs_gate, st[k], w[k]);
         }
         remaining -= S;
         if (remaining <= 0) break;
     }
-    ring_flush<NC>(p, ln.lane, rr);
+    ring_flush<NC, GLU>(p, ln.lane, rr);
 }
 
 // ------------------------------------------------------------------------
@@ -714,7 +728,10 @@ static int lds_bytes_linear(int K) { return K + K / 4; }
 //    its loads).
 //  block-per-lane kernel (one column, 16..64 super-blocks per row): 4-wave
 //    workgroups, 2 per CU, two passes per wave in flight.
-static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N) {
+//  fused epilogue (bias and/or gate, one column): the tile kernel only; with
+//    a gate each tile pairs one row of both weights (R = 2, one or two
+//    groups in flight).
+static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int fused = 0) {
     load_env_overrides();
     Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
@@ -726,7 +743,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const int orows = g_ovr_rows.load(), owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load();
     const int okern = g_ovr_kernel.load();
     const int rpw = bpl_rows_per_pass(K / kQK);
-    if (N == 1 && rpw > 0 && okern == 3) {
+    if (N == 1 && rpw > 0 && okern == 3 && !fused) {
         // block kernel: ~2 waves per SIMD; activation + one 9216-byte LDS
         // slot per wave
         g.bpl = 2;
@@ -746,7 +763,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // tile kernel does better on everything else (measured on MI355X).
     const int64_t weight_bytes = M * (K / kQK) * kBlockBytes;
     const bool auto_bpl = okern == 0 && K == 4096 && weight_bytes >= (48ll << 20);
-    if (N == 1 && rpw > 0 && (okern == 2 || auto_bpl)) {
+    if (N == 1 && rpw > 0 && (okern == 2 || auto_bpl) && !fused) {
         // ~173 VGPRs: two waves per SIMD; 4-wave workgroups, two per CU
         g.bpl = 1;
         g.rpw = rpw;
@@ -777,6 +794,11 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.slots = g.slots == 8 ? 4 : 2;
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.slots = 2;
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.R = 2;
+    if (fused == kFusedGate) {
+        g.R = 2;  // the weight row and the gate row
+        if (g.slots > 2) g.slots = 2;
+    }
+    const bool glu = fused == kFusedGate;
     // rows per workgroup (the kernel splits each share over its waves)
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
@@ -789,7 +811,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)kPre * g.waves * (kWave / lpb);
     g.prologue = pro0_ok ? 0 : 1;
     const int opro = g_ovr_prologue.load();
-    if (opro == 1 || ((opro == 0 || (opro == 2 && g.slots >= 4) || (opro == 3 && g.slots == 2)) && pro0_ok))
+    if (opro == 1 || ((opro == 0 || (opro == 2 && g.slots >= 4) || (opro == 3 && g.slots == 2 && !glu)) && pro0_ok))
         g.prologue = opro;
     return g;
 }
@@ -797,13 +819,13 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
 template <int NC, int R, int WAVES, int S>
 static const void *gemv_sym(int pro) {
     if constexpr (tile_fits(NC, R, WAVES, S)) {
-        if (pro == 0) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 0, S>);
-        if (pro == 1) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 1, S>);
+        if (pro == 0) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 0, S, false>);
+        if (pro == 1) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 1, S, false>);
         if constexpr (S >= 4) {
-            if (pro == 2) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 2, S>);
+            if (pro == 2) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 2, S, false>);
         }
         if constexpr (S == 2) {
-            if (pro == 3) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 3, S>);
+            if (pro == 3) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 3, S, false>);
         }
     }
     return nullptr;
@@ -833,6 +855,20 @@ static const void *gemv_sym_r(int nc, int R, int pro) {
 
 // Instantiations: R in {1, 2, 4}; launch bounds of 8 or 16 waves; 2 or 4
 // slots (see tile_fits); both prologue orders.
+template <int WAVES, int S>
+static const void *gemv_sym_glu(int pro) {
+    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q4k_kernel<1, 2, WAVES, 0, S, true>)
+                    : reinterpret_cast<const void *>(&gemv_q4k_kernel<1, 2, WAVES, 1, S, true>);
+}
+
+// The gate-fused variants: one column, 8 or 16 waves, 1 or 2 slots, both
+// prologue orders.
+static const void *gemv_kernel_glu(int waves, int pro, int slots) {
+    if (pro != 0 && pro != 1) return nullptr;
+    if (waves <= 8) return slots == 1 ? gemv_sym_glu<8, 1>(pro) : gemv_sym_glu<8, 2>(pro);
+    return slots == 1 ? gemv_sym_glu<16, 1>(pro) : gemv_sym_glu<16, 2>(pro);
+}
+
 static const void *gemv_kernel_for(int nc, int R, int waves, int pro, int slots) {
     if (waves <= 8) {
         if (slots == 8) return gemv_sym_r<8, 8>(nc, R, pro);
@@ -845,7 +881,13 @@ static const void *gemv_kernel_for(int nc, int R, int waves, int pro, int slots)
 
 static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc, hipStream_t stream) {
     const void *fn = nullptr;
-    if (geo.bpl == 2 && nc == 1) {
+    if (p.gate) {
+        if (nc != 1 || geo.bpl) return Q4K_EINVAL;
+        fn = gemv_kernel_glu(geo.waves, geo.prologue, geo.slots);
+        p.rows_base = geo.rows_base;
+        p.rows_extra = geo.rows_extra;
+        p.ring_off = lds_bytes(p.K, nc);
+    } else if (geo.bpl == 2 && nc == 1) {
         fn = reinterpret_cast<const void *>(&gemv_q4k_blk_kernel<8>);
         p.rpw = geo.rpw;
     } else if (geo.bpl == 1 && nc == 1) {
@@ -888,11 +930,13 @@ static int check_weight(const void *src0, int64_t ne00, int64_t ne01, int64_t nb
 
 static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x,
                     int64_t ldx, const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst,
-                    int64_t ld_dst, hipStream_t stream) {
+                    int64_t ld_dst, hipStream_t stream, const Epilogue *ep = nullptr) {
     DeviceInfo *di = nullptr;
     int st = device_info(&di);
     if (st != Q4K_OK) return st;
-    const Geometry geo = pick_geometry(*di, ne00, ne01, ncols);
+    const int fused = fused_kind(ep);
+    if (fused && ncols != 1) return Q4K_EINVAL;
+    const Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // the tile kernel addresses a wave's rows with 31-bit offsets; column
     // strides travel as 32-bit kernel arguments
@@ -922,6 +966,12 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
         p.ntiles = geo.ntiles;
         p.vec_ok = x && aligned(p.x, 16) && (ldx % 4 == 0);
         p.nblk32 = fastdiv_init((uint32_t)(ne00 / 32));
+        if (fused) {
+            p.gate = ep->gate;
+            p.bias = ep->bias;
+            p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
+            p.glu_op = ep->glu_op;
+        }
         st = launch_gemv(di, g2, p, nc, stream);
         if (st != Q4K_OK) return st;
     }
@@ -1038,8 +1088,42 @@ int q4k_op_mul_mat_vec_q(const void *src0_dd_i, int64_t ne00, int64_t row_low, i
                     dst_dd_i, nrows_dst, (hipStream_t)stream);
 }
 
+int q4k_mul_mat_vec_q_fused(int32_t src0_type, const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
+                            const float *src1, const q4k_fusion *fusion, float *dst, void *stream) {
+    const bool q6 = src0_type == Q4K_GGML_TYPE_Q6_K;
+    if (!q6 && src0_type != Q4K_GGML_TYPE_Q4_K) return Q4K_EUNSUPPORTED;
+    int st = q6 ? check_weight_q6(src0, ne00, ne01, nb01) : check_weight(src0, ne00, ne01, nb01);
+    if (st != Q4K_OK) return st;
+    if (ne01 == 0) return Q4K_OK;
+    if (!src1 || !dst || !aligned(src1, 4) || !aligned(dst, 4)) return Q4K_EINVAL;
+    Epilogue ep;
+    if (fusion) {
+        ep.gate = static_cast<const uint8_t *>(fusion->gate);
+        ep.bias = fusion->x_bias;
+        ep.gate_bias = fusion->gate ? fusion->gate_bias : nullptr;  // kernels/mmvq.cu:191
+        ep.glu_op = fusion->glu_op;
+    }
+    if (ep.gate) {
+        if (ep.glu_op != kGluGeglu && ep.glu_op != kGluSwiglu && ep.glu_op != kGluSwigluOai)
+            return Q4K_EUNSUPPORTED;
+        if (!aligned(ep.gate, q6 ? 2 : 16)) return q6 ? Q4K_EINVAL : Q4K_EUNSUPPORTED;
+    }
+    if (!aligned(ep.bias, 4) || !aligned(ep.gate_bias, 4)) return Q4K_EINVAL;
+    const hipStream_t s = (hipStream_t)stream;
+    const Epilogue *e = fused_kind(&ep) ? &ep : nullptr;
+    return q6 ? run_gemv_q6(src0, ne00, ne01, nb01, src1, ne00, nullptr, 0, 1, dst, ne01, s, e)
+              : run_gemv(src0, ne00, ne01, nb01, src1, ne00, nullptr, 0, 1, dst, ne01, s, e);
+}
+
+// Same shape and strides (ggml_are_same_stride for the 2-D case).
+static bool same_layout(const q4k_tensor *a, const q4k_tensor *b) {
+    for (int d = 0; d < 4; ++d)
+        if (a->ne[d] != b->ne[d] || a->nb[d] != b->nb[d]) return false;
+    return true;
+}
+
 int q4k_ggml_mul_mat_vec_q(const q4k_tensor *src0, const q4k_tensor *src1, const q4k_tensor *ids,
-                           q4k_tensor *dst, const void *fusion, void *workspace,
+                           q4k_tensor *dst, const q4k_fusion_args *fusion, void *workspace,
                            size_t workspace_bytes, void *stream) {
     if (!src0 || !src1 || !dst) return Q4K_EINVAL;
     if (src1->type != Q4K_GGML_TYPE_F32 || dst->type != Q4K_GGML_TYPE_F32) return Q4K_EINVAL;
@@ -1047,11 +1131,33 @@ int q4k_ggml_mul_mat_vec_q(const q4k_tensor *src0, const q4k_tensor *src1, const
     const bool q6 = src0->type == Q4K_GGML_TYPE_Q6_K;
     const size_t block_bytes = q6 ? Q4K_BLOCK_Q6_K_BYTES : (size_t)kBlockBytes;
     if (src0->nb[0] != block_bytes || src1->nb[0] != 4 || dst->nb[0] != 4) return Q4K_EINVAL;
-    if (ids || fusion) return Q4K_EUNSUPPORTED;
+    if (ids) return Q4K_EUNSUPPORTED;
     for (int d = 2; d < 4; ++d)
         if (src0->ne[d] != 1 || src1->ne[d] != 1 || dst->ne[d] != 1) return Q4K_EUNSUPPORTED;
     if (src1->ne[0] != src0->ne[0] || dst->ne[0] != src0->ne[1] || dst->ne[1] != src1->ne[1])
         return Q4K_EINVAL;
+    if (fusion && (fusion->x_bias || fusion->gate)) {
+        // the reference's fusion checks (kernels/mmvq.cu:696-714)
+        if (dst->ne[1] != 1) return Q4K_EINVAL;
+        q4k_fusion f{};
+        if (fusion->x_bias) {
+            if (fusion->x_bias->type != Q4K_GGML_TYPE_F32 || fusion->x_bias->ne[0] != dst->ne[0]) return Q4K_EINVAL;
+            f.x_bias = static_cast<const float *>(fusion->x_bias->data);
+        }
+        if (fusion->gate) {
+            if (fusion->gate->type != src0->type || !same_layout(fusion->gate, src0)) return Q4K_EINVAL;
+            f.gate = fusion->gate->data;
+            if (fusion->gate_bias) {
+                if (fusion->gate_bias->type != Q4K_GGML_TYPE_F32 || fusion->gate_bias->ne[0] != dst->ne[0])
+                    return Q4K_EINVAL;
+                f.gate_bias = static_cast<const float *>(fusion->gate_bias->data);
+            }
+            f.glu_op = fusion->glu_op;
+        }
+        return q4k_mul_mat_vec_q_fused(src0->type, src0->data, src0->ne[0], src0->ne[1], (int64_t)src0->nb[1],
+                                       static_cast<const float *>(src1->data), &f,
+                                       static_cast<float *>(dst->data), stream);
+    }
     // ggml's nb00 is the block size: ne00 counts values, ne00/256 blocks per row
     return (q6 ? q6k_mul_mat_vec_q : q4k_mul_mat_vec_q)(src0->data, src0->ne[0], src0->ne[1], (int64_t)src0->nb[1],
                              static_cast<const float *>(src1->data), src1->ne[1],
@@ -1110,6 +1216,15 @@ int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32
     g_ovr_waves.store(waves_per_wg);
     g_ovr_wgs.store(workgroups);
     g_ovr_kernel.store(kernel);
+    return Q4K_OK;
+}
+
+int q4k_set_pipeline_override(int32_t slots, int32_t prologue) {
+    if (slots != 0 && slots != 1 && slots != 2 && slots != 4 && slots != 8) return Q4K_EINVAL;
+    if (prologue < -1 || prologue > 3) return Q4K_EINVAL;
+    load_env_overrides();
+    g_ovr_slots.store(slots);
+    g_ovr_prologue.store(prologue);
     return Q4K_OK;
 }
 

@@ -45,7 +45,31 @@ extern std::atomic<int> g_ovr_rows, g_ovr_waves, g_ovr_wgs, g_ovr_kernel;
 extern std::atomic<int> g_ovr_prologue, g_ovr_slots;
 void load_env_overrides();
 
+// Fused epilogue of a one-column product (the fields of ggml's
+// ggml_cuda_mm_fusion_args_device, kernels/mmvq.cu:692-715): an optional
+// gate weight with the layout of the weight, optional biases of the two
+// products, and the GLU op that combines them.
+struct Epilogue {
+    const uint8_t *gate = nullptr;
+    const float *bias = nullptr;
+    const float *gate_bias = nullptr;
+    int glu_op = 0;
+};
+constexpr int kFusedNone = 0;
+constexpr int kFusedBias = 1;  // bias only
+constexpr int kFusedGate = 2;  // gate weight (+ biases) and GLU
+inline int fused_kind(const Epilogue *e) {
+    return !e ? kFusedNone : (e->gate ? kFusedGate : (e->bias ? kFusedBias : kFusedNone));
+}
+
 inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// Q6_K weight checks and launch (q6k_gemv.hip), for the type-dispatching
+// entry points of q4k_gemv.hip.
+int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01);
+int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x, int64_t ldx,
+                const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst, int64_t ld_dst,
+                hipStream_t stream, const Epilogue *ep = nullptr);
 inline int64_t pad512(int64_t k) { return (k + 511) / 512 * 512; }
 // LDS bytes of one staged q8 column in a tile layout (whole 16-block groups)
 inline int q8_col_bytes(int K) { return (K + 4095) / 4096 * 4096; }

@@ -29,6 +29,12 @@ struct GemvParams {
     int rows_extra;          //   the first rows_extra workgroups one more
     int ring_off;            // tile kernel: LDS byte offset of the per-wave result rings
     FastDiv nblk32;          // division by K/32 (Q8_1 blocks per column)
+    // fused epilogue (one column): gate weight rows (same layout as w), the
+    // biases of the two products (indexed like dst) and the GLU op
+    const uint8_t *gate;
+    const float *bias;
+    const float *gate_bias;
+    int glu_op;
 };
 
 // The GEMV kernels take the fields their first memory requests need as
@@ -91,8 +97,33 @@ __device__ __forceinline__ WaveRows wave_rows(const GemvParams &p, int wave) {
     return WaveRows{beg, beg + q + (wave < rem ? 1 : 0)};
 }
 
+// GLU ops of the fused epilogue (values of ggml's enum ggml_glu_op).
+constexpr int kGluGeglu = 1;
+constexpr int kGluSwiglu = 2;
+constexpr int kGluSwigluOai = 3;
+
+// The epilogue of kernels/mmvq.cu:309-336 for one output: `up` (the product
+// with the weight, bias added) gated by `g` (the product with the gate
+// weight, its bias added): SWIGLU up * silu(g), GEGLU up * gelu(g) (tanh
+// form), SWIGLU_OAI with alpha 1.702 and limit 7 (ggml's
+// ggml_cuda_op_*_single formulas; expf and tanhf are the device library's).
+__device__ __forceinline__ float glu_apply(int op, float up, float g) {
+    if (op == kGluSwiglu) return up * (g / (1.0f + expf(-g)));
+    if (op == kGluGeglu) {
+        const float kSqrt2OverPi = 0.79788456080286535588f;
+        return up * (0.5f * g * (1.0f + tanhf(kSqrt2OverPi * g * (1.0f + 0.044715f * g * g))));
+    }
+    if (op == kGluSwigluOai) {
+        const float x = fminf(g, 7.0f);
+        const float u = fmaxf(fminf(up, 7.0f), -7.0f);
+        return x / (1.0f + expf(-x * 1.702f)) * (1.0f + u);
+    }
+    return up * g;
+}
+
 // Results of a wave, buffered in LDS and written to dst in coalesced runs:
-// entry e is column e % NC of row beg + e / NC.
+// entry e is column e % NC of row beg + e / NC; with a gate (GLU), entries
+// 2t and 2t + 1 are the products of row beg + t with the weight and the gate.
 constexpr int kRing = 256;  // floats per wave
 
 struct ResultRing {
@@ -103,14 +134,30 @@ struct ResultRing {
     int n;        // entries buffered
 };
 
-// Writes the buffered entries to dst (entries of rows >= end are dropped).
-template <int NC>
+// Writes the buffered entries to dst (entries of rows >= end are dropped),
+// adding the bias and applying the GLU when the launch carries them.
+template <int NC, bool GLU>
 __device__ __forceinline__ void ring_flush(const GemvParams &p, int lane, ResultRing &rr) {
-    for (int k = lane; k < rr.n; k += kWave) {
-        const int idx = rr.base + k;
-        const int row = rr.beg + idx / NC;
-        const int c = idx - (idx / NC) * NC;
-        if (row < rr.end) p.dst[(int64_t)c * p.ld_dst + row] = rr.buf[k];
+    if (GLU) {
+        for (int k = lane; 2 * k < rr.n; k += kWave) {
+            const int row = rr.beg + rr.base / 2 + k;
+            if (row < rr.end) {
+                const float2 v = *reinterpret_cast<const float2 *>(rr.buf + 2 * k);
+                const float up = p.bias ? v.x + p.bias[row] : v.x;
+                const float g = p.gate_bias ? v.y + p.gate_bias[row] : v.y;
+                p.dst[row] = glu_apply(p.glu_op, up, g);
+            }
+        }
+    } else {
+        for (int k = lane; k < rr.n; k += kWave) {
+            const int idx = rr.base + k;
+            const int row = rr.beg + idx / NC;
+            const int c = idx - (idx / NC) * NC;
+            if (row < rr.end) {
+                const int64_t o = (int64_t)c * p.ld_dst + row;
+                p.dst[o] = p.bias ? rr.buf[k] + p.bias[o] : rr.buf[k];
+            }
+        }
     }
     rr.base += rr.n;
     rr.n = 0;
@@ -118,7 +165,7 @@ __device__ __forceinline__ void ring_flush(const GemvParams &p, int lane, Result
 
 // End of a row tile: the R x NC lane partials of the tile, reduced over the
 // wave, go to the result ring (lane r*NC + c writes entry r*NC + c).
-template <int NC, int R>
+template <int NC, int R, bool GLU>
 __device__ __forceinline__ void tile_to_ring(const GemvParams &p, int lane, float (&acc)[R][NC],
                                              ResultRing &rr) {
     float out = 0.0f;
@@ -134,7 +181,7 @@ __device__ __forceinline__ void tile_to_ring(const GemvParams &p, int lane, floa
     rr.n += R * NC;
     // rare (a wave's rows x NC above kRing): global stores inside the
     // loop make the compiler's load waits conservative
-    if (rr.n + R * NC > kRing) ring_flush<NC>(p, lane, rr);
+    if (rr.n + R * NC > kRing) ring_flush<NC, GLU>(p, lane, rr);
 }
 
 }  // namespace q4k

@@ -147,52 +147,69 @@ __device__ __forceinline__ void q6_lane_sums(const uint32_t (&v)[4][4], const Q6
         for (int k = 0; k < 4; ++k) s[m] = __builtin_amdgcn_sdot4((int)v[m][k], (int)a.a[m][k], s[m], false);
 }
 
-// A wave's rows as one buffer, as for Q4_K.
+// A wave's rows as one buffer, as for Q4_K (and the same rows of the gate
+// weight when the launch fuses one).
 struct Q6Stream {
-    __amdgpu_buffer_rsrc_t rs;
+    __amdgpu_buffer_rsrc_t rs, rs_gate;
     int ntiles;
 };
 
+// Loads one step: the row's group into w[0] and, with GLU, the gate row's
+// group into w[1].
+template <int R>
 __device__ __forceinline__ void q6_load_step(const GemvParams &p, const Q6Lane &ln, const Q6Stream &ws,
-                                             Step st, Q6Regs &w) {
+                                             Step st, Q6Regs (&w)[R]) {
     const uint32_t row = (uint32_t)st.tile * (uint32_t)p.row_stride + (uint32_t)st.i * (16 * kQ6Bytes);
-    q6_load(ws.rs, ln, row, st.tile < ws.ntiles && 16 * st.i + ln.g < p.nb, w);
+    const bool ok = st.tile < ws.ntiles && 16 * st.i + ln.g < p.nb;
+    q6_load(ws.rs, ln, row, ok, w[0]);
+    if (R == 2) q6_load(ws.rs_gate, ln, row, ok, w[R - 1]);
 }
 
-// Consumes one group held in w (one row); at the tile's last group moves the
-// NC sums to the result ring.
-template <int NC>
+// Consumes one group held in w (one row, or the row and its gate row); at
+// the tile's last group moves the R x NC sums to the result ring.
+template <int NC, int R, bool GLU>
 __device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6Lane &ln, Step st,
-                                                 const int8_t *q8s, const uint8_t *aux, const Q6Regs &w,
-                                                 float (&acc)[1][NC], ResultRing &rr) {
-    uint32_t v[4][4];
-    q6_values(w, v);
-    int sc[4];
-    q6_scales(w, ln.jp, sc);
-    const float d = half_bits_to_float(w.dw >> 16);
+                                                 const int8_t *q8s, const uint8_t *aux, const Q6Regs (&w)[R],
+                                                 float (&acc)[R][NC], ResultRing &rr) {
+    uint32_t v[R][4][4];
+    int sc[R][4];
+    float d[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        q6_values(w[r], v[r]);
+        q6_scales(w[r], ln.jp, sc[r]);
+        d[r] = half_bits_to_float(w[r].dw >> 16);
+    }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const Q6Act a = q6_act(p, ln, st.i, c, NC, q8s, aux);
-        int s[4];
-        q6_lane_sums(v, a, s);
-        // |s| <= 16*32*127 and |sc| <= 128: the 24-bit products are exact in
-        // f32.  Explicit fmas fix the rounding for every launch geometry.
-        float f = a.d8.x * (float)__mul24(s[0], sc[0]);
-        f = __builtin_fmaf(a.d8.y, (float)__mul24(s[1], sc[1]), f);
-        f = __builtin_fmaf(a.d8.z, (float)__mul24(s[2], sc[2]), f);
-        f = __builtin_fmaf(a.d8.w, (float)__mul24(s[3], sc[3]), f);
-        acc[0][c] = __builtin_fmaf(d, f, acc[0][c]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            int s[4];
+            q6_lane_sums(v[r], a, s);
+            // |s| <= 16*32*127 and |sc| <= 128: the 24-bit products are exact
+            // in f32.  Explicit fmas fix the rounding for every launch geometry.
+            float f = a.d8.x * (float)__mul24(s[0], sc[r][0]);
+            f = __builtin_fmaf(a.d8.y, (float)__mul24(s[1], sc[r][1]), f);
+            f = __builtin_fmaf(a.d8.z, (float)__mul24(s[2], sc[r][2]), f);
+            f = __builtin_fmaf(a.d8.w, (float)__mul24(s[3], sc[r][3]), f);
+            acc[r][c] = __builtin_fmaf(d[r], f, acc[r][c]);
+        }
     }
-    if (st.i == p.G - 1) tile_to_ring<NC, 1>(p, ln.lane, acc, rr);
+    if (st.i == p.G - 1) tile_to_ring<NC, R, GLU>(p, ln.lane, acc, rr);
 }
 
 // Tile kernel: any K, 1..8 columns; one row per tile.  The structure of the
 // Q4_K tile kernel: one workgroup per CU, activation loads first, then the
 // barrier, the early weight slots (PRO 0: min(S, 2) slots before the
 // activation is quantised, 1: none), quantisation into LDS, the barrier, and
-// the S-slot stream with unconditional loads and the result ring.
-template <int NC, int WAVES, int PRO, int S>
+// the S-slot stream with unconditional loads and the result ring.  GLU (one
+// column): each tile also streams the same row of the gate weight, and the
+// ring flush applies the biases and the GLU.
+template <int NC, int WAVES, int PRO, int S, bool GLU>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    static_assert(!GLU || NC == 1, "the fused epilogue is one-column");
+    constexpr int R = GLU ? 2 : 1;
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : 0;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -203,7 +220,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WaveRows wr = wave_rows<WAVES>(p, wave);
     Q6Stream ws;
-    ws.rs = make_rsrc(p.w + (int64_t)wr.beg * p.row_stride, (uint32_t)((wr.end - wr.beg) * p.row_stride));
+    const uint32_t wave_bytes = (uint32_t)((wr.end - wr.beg) * p.row_stride);
+    ws.rs = make_rsrc(p.w + (int64_t)wr.beg * p.row_stride, wave_bytes);
+    ws.rs_gate = GLU ? make_rsrc(p.gate + (int64_t)wr.beg * p.row_stride, wave_bytes) : ws.rs;
     ws.ntiles = wr.end - wr.beg;
     int remaining = ws.ntiles * p.G;
 
@@ -215,12 +234,12 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     __syncthreads();  // all activation loads of this CU are queued first
 
     Step st[S];
-    Q6Regs w[S];
+    Q6Regs w[S][R];
     st[0] = Step{0, 0};
 #pragma unroll
     for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], p.G);
 #pragma unroll
-    for (int k = 0; k < kEarly; ++k) q6_load_step(p, ln, ws, st[k], w[k]);
+    for (int k = 0; k < kEarly; ++k) q6_load_step<R>(p, ln, ws, st[k], w[k]);
     if (p.x)
         stage_f32_finish<kLayoutQ6K, kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs,
                                                           p.qcol, q8s, aux);
@@ -230,24 +249,26 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     __syncthreads();
     if (remaining == 0) return;  // no barrier below this point
 #pragma unroll
-    for (int k = kEarly; k < S; ++k) q6_load_step(p, ln, ws, st[k], w[k]);
+    for (int k = kEarly; k < S; ++k) q6_load_step<R>(p, ln, ws, st[k], w[k]);
 
-    float acc[1][NC];
+    float acc[R][NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) acc[0][c] = 0.0f;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
     ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * kRing, wr.beg, wr.end, 0, 0};
 
     for (;;) {
 #pragma unroll
         for (int k = 0; k < S; ++k) {
-            q6_process_group<NC>(p, ln, st[k], q8s, aux, w[k], acc, rr);
+            q6_process_group<NC, R, GLU>(p, ln, st[k], q8s, aux, w[k], acc, rr);
             st[k] = next_step(st[(k + S - 1) % S], p.G);
-            q6_load_step(p, ln, ws, st[k], w[k]);
+            q6_load_step<R>(p, ln, ws, st[k], w[k]);
         }
         remaining -= S;
         if (remaining <= 0) break;
     }
-    ring_flush<NC>(p, ln.lane, rr);
+    ring_flush<NC, GLU>(p, ln.lane, rr);
 }
 
 // Parity probe: the int32 sums over every 16-weight scale group of
@@ -317,10 +338,13 @@ struct Q6Geometry {
     int slots = 2;
 };
 
-// The Q4_K tile kernel's choices (measured on MI355X for that kernel): one
-// workgroup per CU, 16 waves when a workgroup has 16 or more steps, two
-// groups in flight per wave from four steps per wave on, weight loads before
-// quantisation when the activation fits the kPre staging rounds.
+// One workgroup per CU; one group (3360 bytes per wave) in flight per wave;
+// 8 waves unless the activation is long (more than 8192 values over all
+// columns: 16 waves quantise it in half the rounds) and the workgroup has 16
+// or more steps; weight loads before quantisation when the activation fits
+// the kPre staging rounds.  Measured on MI355X: with 210-byte blocks, more
+// weight requests in flight (16 waves x 2 groups, 27.5 MB over the chip)
+// delay the activation loads more than they hide latency.
 static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N) {
     load_env_overrides();
     Q6Geometry g;
@@ -332,9 +356,9 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     const int owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load(), oslots = g_ovr_slots.load();
     g.grid = owgs > 0 ? owgs : cus;
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
-    g.waves = steps_per_wg >= 16 ? 16 : 8;
+    g.waves = steps_per_wg >= 16 && (int64_t)nc * K > 8192 ? 16 : 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;
-    g.slots = steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
+    g.slots = 1;
     if (oslots == 1 || oslots == 2) g.slots = oslots;
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
@@ -349,10 +373,10 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     return g;
 }
 
-template <int NC, int WAVES, int S>
+template <int NC, int WAVES, int S, bool GLU = false>
 static const void *q6_sym(int pro) {
-    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 0, S>)
-                    : reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 1, S>);
+    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 0, S, GLU>)
+                    : reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 1, S, GLU>);
 }
 
 template <int WAVES, int S>
@@ -370,12 +394,17 @@ static const void *q6_sym_nc(int nc, int pro) {
     }
 }
 
-static const void *q6_kernel_for(int nc, int waves, int pro, int slots) {
+static const void *q6_kernel_for(int nc, int waves, int pro, int slots, bool glu) {
+    if (glu) {
+        if (nc != 1) return nullptr;
+        if (waves <= 8) return slots == 1 ? q6_sym<1, 8, 1, true>(pro) : q6_sym<1, 8, 2, true>(pro);
+        return slots == 1 ? q6_sym<1, 16, 1, true>(pro) : q6_sym<1, 16, 2, true>(pro);
+    }
     if (waves <= 8) return slots == 1 ? q6_sym_nc<8, 1>(nc, pro) : q6_sym_nc<8, 2>(nc, pro);
     return slots == 1 ? q6_sym_nc<16, 1>(nc, pro) : q6_sym_nc<16, 2>(nc, pro);
 }
 
-static int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01) {
+int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01) {
     if (ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0) return Q4K_EINVAL;
     const int64_t row_bytes = ne00 / kQK * kQ6Bytes;
     if (nb01 < row_bytes || nb01 % kQ6Bytes != 0) return Q4K_EINVAL;
@@ -386,12 +415,14 @@ static int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t
     return Q4K_OK;
 }
 
-static int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x,
-                       int64_t ldx, const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst,
-                       int64_t ld_dst, hipStream_t stream) {
+int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x, int64_t ldx,
+                const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst, int64_t ld_dst,
+                hipStream_t stream, const Epilogue *ep) {
     DeviceInfo *di = nullptr;
     int st = device_info(&di);
     if (st != Q4K_OK) return st;
+    const int fused = fused_kind(ep);
+    if (fused && ncols != 1) return Q4K_EINVAL;
     const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // a wave's rows are addressed with 31-bit offsets; column strides travel
@@ -422,7 +453,13 @@ static int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb0
         p.rows_extra = geo.rows_extra;
         p.ring_off = q6_act_bytes(p.K, nc);
         p.nblk32 = fastdiv_init((uint32_t)(ne00 / 32));
-        const void *fn = q6_kernel_for(nc, geo.waves, geo.prologue, geo.slots);
+        if (fused) {
+            p.gate = ep->gate;
+            p.bias = ep->bias;
+            p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
+            p.glu_op = ep->glu_op;
+        }
+        const void *fn = q6_kernel_for(nc, geo.waves, geo.prologue, geo.slots, fused == kFusedGate);
         if (!fn) return Q4K_EINVAL;
         st = ensure_lds(di, fn, lds_launch);
         if (st != Q4K_OK) return st;

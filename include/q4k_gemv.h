@@ -70,6 +70,32 @@ typedef struct q4k_tensor {
     void *data;
 } q4k_tensor;
 
+/* GLU ops of the fused epilogue (values of ggml's enum ggml_glu_op) */
+#define Q4K_GLU_OP_GEGLU 1      /* up * gelu(gate), tanh form */
+#define Q4K_GLU_OP_SWIGLU 2     /* up * silu(gate) */
+#define Q4K_GLU_OP_SWIGLU_OAI 3 /* silu_1.702(min(gate, 7)) * (1 + clamp(up, -7, 7)) */
+
+/* Fused epilogue of a one-column product, device pointers: the counterpart
+ * of ggml_cuda_mm_fusion_args_device (kernels/mmvq.cu:692-715).  With it,
+ * dst[r] = up + x_bias[r], where up = row r of src0 times src1; with a gate
+ * weight, dst[r] = glu(up + x_bias[r], g + gate_bias[r]) where g = row r of
+ * the gate times src1 (kernels/mmvq.cu:309-336).  NULL members are absent. */
+typedef struct q4k_fusion {
+    const float *x_bias;    /* ne01 floats */
+    const void *gate;       /* same type, shape and row stride as src0 */
+    const float *gate_bias; /* ne01 floats, used only with a gate */
+    int32_t glu_op;         /* Q4K_GLU_OP_*, used only with a gate */
+} q4k_fusion;
+
+/* ggml-descriptor form (ggml_cuda_mm_fusion_args_host): F32 bias tensors of
+ * ne[0] == dst->ne[0], a gate tensor of src0's type and strides. */
+typedef struct q4k_fusion_args {
+    const q4k_tensor *x_bias;
+    const q4k_tensor *gate;
+    const q4k_tensor *gate_bias;
+    int32_t glu_op;
+} q4k_fusion_args;
+
 /* ----------------------------------------------------------------- misc */
 int32_t q4k_version(void);
 const char *q4k_strerror(int status);
@@ -134,12 +160,27 @@ int q4k_op_mul_mat_vec_q(const void *src0_dd_i, int64_t ne00, int64_t row_low, i
  * :600-605; any other type returns Q4K_EUNSUPPORTED).
  * Checks the reference's assertions: src1/dst F32 (:669-670), nb00 == block
  * size, nb10 == 4, nb0 == 4 (:681-683), ne10 == ne00, ne0 == ne01, ne1 == ne11.
- * Returns Q4K_EUNSUPPORTED for what this path does not implement: ids
- * (MUL_MAT_ID), fusion (gate/bias/GLU), more than one channel or sample
- * (ne2/ne3 > 1) -- the cases the reference's simple_ok gate also excludes. */
+ * fusion (may be NULL) adds the bias / gate + GLU epilogue of
+ * q4k_mul_mat_vec_q_fused under the reference's checks (:696-714): dst with
+ * one column, F32 biases of dst->ne[0] values, a gate of src0's type and
+ * strides.  Returns Q4K_EUNSUPPORTED for what this path does not implement:
+ * ids (MUL_MAT_ID), more than one channel or sample (ne2/ne3 > 1). */
 int q4k_ggml_mul_mat_vec_q(const q4k_tensor *src0, const q4k_tensor *src1, const q4k_tensor *ids,
-                           q4k_tensor *dst, const void *fusion, void *workspace,
+                           q4k_tensor *dst, const q4k_fusion_args *fusion, void *workspace,
                            size_t workspace_bytes, void *stream);
+
+/* One-column product with the fused epilogue (bias, gate + GLU): the
+ * has_fusion instantiation of the reference's mul_mat_vec_q
+ * (kernels/mmvq.cu:150-344, launched with fusion for ncols_dst == 1,
+ * :697-698).  src0_type is Q4K_GGML_TYPE_Q4_K or Q4K_GGML_TYPE_Q6_K; src0
+ * as for q4k_mul_mat_vec_q / q6k_mul_mat_vec_q (the gate with the same
+ * alignment), src1 one column of ne00 floats, dst ne01 floats, biases 4-byte
+ * aligned.  The gate is streamed beside src0 in the same launch, so both
+ * products share one pass over the activation.  GLU ops other than
+ * Q4K_GLU_OP_* return Q4K_EUNSUPPORTED (ggml runs those unfused). */
+int q4k_mul_mat_vec_q_fused(int32_t src0_type, const void *src0, int64_t ne00, int64_t ne01,
+                            int64_t nb01, const float *src1, const q4k_fusion *fusion, float *dst,
+                            void *stream);
 
 /* Parity probe: the int32 sub-block sums of the product, computed with the
  * GEMV kernel's own lane mapping and dot routines.
@@ -208,6 +249,16 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * the compile-time tables of kernels/mmvq.cu:95-147). */
 int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32_t workgroups,
                               int32_t kernel);
+
+/* Tuning override of the tile kernels' pipeline for every later call in the
+ * process: weight groups in flight per wave (1, 2, 4 or 8; Q6_K uses 1 or 2;
+ * 0 = automatic) and when the first weight loads are issued relative to the
+ * activation quantisation (0 = the first two groups before it, 1 = all
+ * after, 2 = all before, 3 = one before; -1 = automatic).  Values a kernel
+ * has no variant for fall back to the automatic choice.  Start-up values
+ * come from Q4K_SLOTS and Q4K_PROLOGUE.  Not part of the reference
+ * interface: a benchmarking knob. */
+int q4k_set_pipeline_override(int32_t slots, int32_t prologue);
 
 /* ------------------------------------------------------------ host side */
 

@@ -251,3 +251,47 @@ def parity_tolerance(y64: np.ndarray, l1: np.ndarray) -> np.ndarray:
     of |term| over its per-sub-block terms (the scale of a reordered f32 sum)."""
     ulp = np.spacing(np.abs(y64).astype(np.float32)).astype(np.float64)
     return np.maximum(np.maximum(1e-5 * np.abs(y64), 4.0 * ulp), 8.0 * np.finfo(np.float32).eps * l1)
+
+
+# ------------------------------------------------------ fused epilogue ----
+GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI = 1, 2, 3  # ggml_glu_op values
+
+
+def glu(op: int, up, g):
+    """The epilogue of kernels/mmvq.cu:316-333 in f64: SWIGLU up*silu(g),
+    GEGLU up*gelu(g) (tanh form, ggml's constants 0.044715 and sqrt(2/pi)),
+    SWIGLU_OAI silu_1.702(min(g, 7)) * (1 + clamp(up, -7, 7)); other ops up*g."""
+    up = np.asarray(up, np.float64)
+    g = np.asarray(g, np.float64)
+    if op == GLU_SWIGLU:
+        return up * (g / (1.0 + np.exp(-g)))
+    if op == GLU_GEGLU:
+        return up * (0.5 * g * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * g * (1.0 + 0.044715 * g * g))))
+    if op == GLU_SWIGLU_OAI:
+        x = np.minimum(g, 7.0)
+        u = np.clip(up, -7.0, 7.0)
+        return x / (1.0 + np.exp(-1.702 * x)) * (1.0 + u)
+    return up * g
+
+
+def glu_tolerance(op: int, up, g, tol_up, tol_g):
+    """Bound on the F32 fused result against glu(up, g) in f64 when the two
+    products carry errors up to tol_up and tol_g: twice the largest change of
+    glu over the corners of that box, plus 16 f32 epsilons of the epilogue's
+    own magnitude (device expf/tanhf and the float operations, including the
+    cancellation in 1 + tanh and 1 + up)."""
+    f0 = glu(op, up, g)
+    dev = np.zeros_like(f0)
+    for su in (-1.0, 1.0):
+        for sg in (-1.0, 1.0):
+            dev = np.maximum(dev, np.abs(glu(op, up + su * tol_up, g + sg * tol_g) - f0))
+    up = np.asarray(up, np.float64)
+    g = np.asarray(g, np.float64)
+    if op == GLU_GEGLU:
+        scale = np.abs(up * g)
+    elif op == GLU_SWIGLU_OAI:
+        x = np.minimum(g, 7.0)
+        scale = np.abs(x / (1.0 + np.exp(-1.702 * x))) * (1.0 + np.abs(np.clip(up, -7.0, 7.0)))
+    else:
+        scale = np.abs(f0)
+    return 2.0 * dev + 16.0 * np.finfo(np.float32).eps * scale + 1e-30

@@ -71,10 +71,20 @@ def test_op_and_descriptor_checks(Q):
     f16 = Q.make_tensor(1, [4096, 1], [2, 8192], 0x20000)
     assert Q.ggml_mul_mat_vec_q(s0, f16, d) == Q.Q4K_EINVAL
     assert Q.ggml_mul_mat_vec_q(s0, s1, d, ids=s1) == Q.Q4K_EUNSUPPORTED
-    L2 = Q.lib()
-    st = L2.q4k_ggml_mul_mat_vec_q(ctypes.byref(s0), ctypes.byref(s1), None, ctypes.byref(d),
-                                   ctypes.c_void_p(0x40000), None, 0, None)
-    assert st == Q.Q4K_EUNSUPPORTED                                          # fusion
+    # fusion under the reference's checks (host-side, no device call)
+    gate = Q.make_tensor(Q.GGML_TYPE_Q4_K, [4096, 16], [144, 2304], 0x50000)
+    bad_bias = Q.make_tensor(1, [16], [2], 0x60000)
+    fa = Q.q4k_fusion_args(None, ctypes.pointer(gate), None, 0)              # REGLU: not fused
+    assert Q.ggml_mul_mat_vec_q(s0, s1, d, fusion=fa) == Q.Q4K_EUNSUPPORTED
+    fa = Q.q4k_fusion_args(ctypes.pointer(bad_bias), None, None, 2)          # F16 bias
+    assert Q.ggml_mul_mat_vec_q(s0, s1, d, fusion=fa) == Q.Q4K_EINVAL
+    gate6 = Q.make_tensor(Q.GGML_TYPE_Q6_K, [4096, 16], [210, 3360], 0x50000)
+    fa = Q.q4k_fusion_args(None, ctypes.pointer(gate6), None, 2)             # gate of another type
+    assert Q.ggml_mul_mat_vec_q(s0, s1, d, fusion=fa) == Q.Q4K_EINVAL
+    s1b = Q.make_tensor(Q.GGML_TYPE_F32, [4096, 2], [4, 16384], 0x20000)
+    d2 = Q.make_tensor(Q.GGML_TYPE_F32, [16, 2], [4, 64], 0x30000)
+    fa = Q.q4k_fusion_args(None, ctypes.pointer(gate), None, 2)              # fusion needs one column
+    assert Q.ggml_mul_mat_vec_q(s0, s1b, d2, fusion=fa) == Q.Q4K_EINVAL
     q5 = Q.make_tensor(13, [4096, 16], [176, 2816], 0x10000)
     assert Q.ggml_mul_mat_vec_q(q5, s1, d) == Q.Q4K_EUNSUPPORTED             # other types
     q6 = Q.make_tensor(Q.GGML_TYPE_Q6_K, [4096, 16], [144, 3360], 0x10000)
@@ -117,3 +127,15 @@ def test_q6k_op_and_probe_checks(Q):
     assert L.q6k_op_mul_mat_vec_q(FAKE, 4096, 3, 3, FAKE, 1, 4096, FAKE, 4, None) == Q.Q4K_OK
     assert L.q6k_group_sums(FAKE, 4096, 4, 3360, FAKE, 1, 100, FAKE, None) == Q.Q4K_EINVAL
     assert L.q6k_group_sums(FAKE, 4096, 0, 3360, FAKE, 1, 128, FAKE, None) == Q.Q4K_OK
+
+
+def test_fused_entry_checks(Q):
+    L = Q.lib()
+    f = Q.q4k_fusion(None, FAKE, None, 0)
+    assert L.q4k_mul_mat_vec_q_fused(13, FAKE, 4096, 16, 2304, FAKE, ctypes.byref(f), FAKE, None) == 1
+    assert L.q4k_mul_mat_vec_q_fused(12, FAKE, 4096, 16, 2304, FAKE, ctypes.byref(f), FAKE, None) == 1
+    f = Q.q4k_fusion(ctypes.c_void_p(0x60002), None, None, 0)               # misaligned bias
+    assert L.q4k_mul_mat_vec_q_fused(12, FAKE, 4096, 16, 2304, FAKE, ctypes.byref(f), FAKE, None) == 2
+    f = Q.q4k_fusion(None, FAKE_2, None, 2)                                  # Q4_K gate alignment
+    assert L.q4k_mul_mat_vec_q_fused(12, FAKE, 4096, 16, 2304, FAKE, ctypes.byref(f), FAKE, None) == 1
+    assert L.q4k_mul_mat_vec_q_fused(14, FAKE, 4096, 0, 3360, FAKE, ctypes.byref(f), FAKE, None) == 0
