@@ -69,9 +69,10 @@ struct WaveStream {
 };
 
 __device__ __forceinline__ WaveStream wave_stream(const GemvParams &p, const Lane &ln,
-                                                  const WaveRows &wr, int R) {
+                                                  const WaveRows &wr, int R, bool absent = false) {
     WaveStream ws;
-    ws.rs = make_rsrc(p.w + (int64_t)wr.beg * p.row_stride, (uint32_t)((wr.end - wr.beg) * p.row_stride));
+    ws.rs = make_rsrc(p.w + (int64_t)wr.beg * p.row_stride,
+                      absent ? 0u : (uint32_t)((wr.end - wr.beg) * p.row_stride));
     ws.ntiles = (wr.end - wr.beg + R - 1) / R;
     ws.lh = (uint32_t)ln.g * kBlockBytes;
     ws.lq = ws.lh + 16u + 32u * (uint32_t)ln.j;
@@ -122,7 +123,7 @@ __device__ __forceinline__ LaneAct lane_act(const GemvParams &p, const Lane &ln,
 
 // Consumes one group (16 super-blocks of R rows) held in w; on the last group
 // of a tile reduces the R x NC sums over the wave into the result ring.
-template <int NC, int R, bool GLU>
+template <int NC, int R, int EPI>
 __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &ln, Step st,
                                               const int8_t *q8s, const float2 *dks,
                                               const RowRegs (&w)[R], float (&acc)[R][NC],
@@ -155,7 +156,7 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
             acc[r][c] = fmaf(-dmin[r], ms, acc[r][c]);
         }
     }
-    if (st.i == p.G - 1) tile_to_ring<NC, R, GLU>(p, ln.lane, acc, rr);
+    if (st.i == p.G - 1) tile_to_ring<NC, R, EPI>(p, ln.lane, acc, rr);
 }
 
 // Tile kernel: any K, 1..8 columns.  One workgroup per CU (the launch asks
@@ -182,10 +183,20 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
 // row of the gate weight (kernels/mmvq.cu:254-262 computes both products
 // from the same activation); the ring holds the pair and its flush applies
 // the biases and the GLU.
-template <int NC, int R, int WAVES, int PRO, int S, bool GLU>
+//
+// BATCH: one launch over dst channels (grid y) and samples (grid z); each
+// workgroup first selects its activation channel and dst slice, and, after
+// its activation loads are issued, its weight matrix (batch_weights).
+//
+// EPI: the epilogue (kEpiNone, kEpiBias, kEpiGlu; the fused ones are one
+// column).
+template <int NC, int R, int WAVES, int PRO, int S, int EPI = kEpiNone, bool BATCH = false>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    constexpr bool GLU = EPI == kEpiGlu;
     static_assert(!GLU || (NC == 1 && R == 2), "the fused epilogue pairs one row of each weight");
+    static_assert(EPI != kEpiBias || (NC == 1 && R == 1), "the bias epilogue is one column, one row per tile");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    if constexpr (BATCH) batch_activation(p);
     // slots loaded before quantisation
     constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : (PRO == 2 ? S : (PRO == 3 ? 1 : 0));
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -202,17 +213,26 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     // row numbers and buffer descriptors in scalar registers
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WaveRows wr = wave_rows<WAVES>(p, wave);
-    const WaveStream ws = wave_stream(p, ln, wr, GLU ? 1 : R);
-    const __amdgpu_buffer_rsrc_t rs_gate =
-        GLU ? make_rsrc(p.gate + (int64_t)wr.beg * p.row_stride, (uint32_t)((wr.end - wr.beg) * p.row_stride))
-            : ws.rs;
-    int remaining = ws.ntiles * p.G;  // steps of this wave
-
     constexpr int kLPB = NC == 1 ? 8 : 4;  // activation lanes per 32-value block
     ActStage<kLPB> xs;
     Q81Stage ys;
-    if (p.x) stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
-    else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+    if constexpr (BATCH) {
+        if (p.x) stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+        else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+        batch_weights(p);
+    }
+    const bool absent = BATCH && p.w_absent;
+    const WaveStream ws = wave_stream(p, ln, wr, GLU ? 1 : R, absent);
+    const __amdgpu_buffer_rsrc_t rs_gate =
+        GLU ? make_rsrc(p.gate + (int64_t)wr.beg * p.row_stride,
+                        absent ? 0u : (uint32_t)((wr.end - wr.beg) * p.row_stride))
+            : ws.rs;
+    int remaining = ws.ntiles * p.G;  // steps of this wave
+
+    if constexpr (!BATCH) {
+        if (p.x) stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+        else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+    }
     __syncthreads();  // all activation loads of this CU are queued first
 
     Step st[S];
@@ -243,14 +263,14 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     for (;;) {
 #pragma unroll
         for (int k = 0; k < S; ++k) {
-            process_group<NC, R, GLU>(p, ln, st[k], q8s, dks, w[k], acc, rr);
+            process_group<NC, R, EPI>(p, ln, st[k], q8s, dks, w[k], acc, rr);
             st[k] = next_step(st[(k + S - 1) % S], p.G);
             load_step<R, GLU>(p, ln, ws, rs_gate, st[k], w[k]);
         }
         remaining -= S;
         if (remaining <= 0) break;
     }
-    ring_flush<NC, GLU>(p, ln.lane, rr);
+    ring_flush<NC, EPI>(p, ln.lane, rr);
 }
 
 // ------------------------------------------------------------------------
@@ -731,7 +751,8 @@ static int lds_bytes_linear(int K) { return K + K / 4; }
 //  fused epilogue (bias and/or gate, one column): the tile kernel only; with
 //    a gate each tile pairs one row of both weights (R = 2, one or two
 //    groups in flight).
-static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int fused = 0) {
+static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int fused = 0,
+                              int64_t mats = 1) {
     load_env_overrides();
     Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
@@ -743,7 +764,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const int orows = g_ovr_rows.load(), owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load();
     const int okern = g_ovr_kernel.load();
     const int rpw = bpl_rows_per_pass(K / kQK);
-    if (N == 1 && rpw > 0 && okern == 3 && !fused) {
+    if (N == 1 && rpw > 0 && okern == 3 && !fused && mats == 1) {
         // block kernel: ~2 waves per SIMD; activation + one 9216-byte LDS
         // slot per wave
         g.bpl = 2;
@@ -763,7 +784,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // tile kernel does better on everything else (measured on MI355X).
     const int64_t weight_bytes = M * (K / kQK) * kBlockBytes;
     const bool auto_bpl = okern == 0 && K == 4096 && weight_bytes >= (48ll << 20);
-    if (N == 1 && rpw > 0 && (okern == 2 || auto_bpl) && !fused) {
+    if (N == 1 && rpw > 0 && (okern == 2 || auto_bpl) && !fused && mats == 1) {
         // ~173 VGPRs: two waves per SIMD; 4-wave workgroups, two per CU
         g.bpl = 1;
         g.rpw = rpw;
@@ -777,7 +798,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         g.lds_launch = g.lds;
         return g;
     }
-    g.grid = owgs > 0 ? owgs : cus;
+    g.grid = owgs > 0 ? owgs : grid_per_matrix(cus, mats, M);
     // 16 waves per CU unless the product is small; two groups in flight per
     // wave once a wave has four or more to stream, else one (a second slot
     // would mostly run past the wave's rows).  Measured on MI355X.
@@ -794,11 +815,11 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.slots = g.slots == 8 ? 4 : 2;
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.slots = 2;
     if (!tile_fits(nc, g.R, g.waves, g.slots)) g.R = 2;
-    if (fused == kFusedGate) {
-        g.R = 2;  // the weight row and the gate row
+    if (fused) {
+        g.R = fused == kFusedGate ? 2 : 1;  // with a gate: the weight row and the gate row
         if (g.slots > 2) g.slots = 2;
     }
-    const bool glu = fused == kFusedGate;
+    const bool glu = fused != kFusedNone;
     // rows per workgroup (the kernel splits each share over its waves)
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
@@ -819,13 +840,13 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
 template <int NC, int R, int WAVES, int S>
 static const void *gemv_sym(int pro) {
     if constexpr (tile_fits(NC, R, WAVES, S)) {
-        if (pro == 0) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 0, S, false>);
-        if (pro == 1) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 1, S, false>);
+        if (pro == 0) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 0, S, kEpiNone>);
+        if (pro == 1) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 1, S, kEpiNone>);
         if constexpr (S >= 4) {
-            if (pro == 2) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 2, S, false>);
+            if (pro == 2) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 2, S, kEpiNone>);
         }
         if constexpr (S == 2) {
-            if (pro == 3) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 3, S, false>);
+            if (pro == 3) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, R, WAVES, 3, S, kEpiNone>);
         }
     }
     return nullptr;
@@ -855,18 +876,49 @@ static const void *gemv_sym_r(int nc, int R, int pro) {
 
 // Instantiations: R in {1, 2, 4}; launch bounds of 8 or 16 waves; 2 or 4
 // slots (see tile_fits); both prologue orders.
-template <int WAVES, int S>
-static const void *gemv_sym_glu(int pro) {
-    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q4k_kernel<1, 2, WAVES, 0, S, true>)
-                    : reinterpret_cast<const void *>(&gemv_q4k_kernel<1, 2, WAVES, 1, S, true>);
+template <int EPI, int WAVES, int S, bool BATCH>
+static const void *gemv_sym_epi(int pro) {
+    constexpr int R = EPI == kEpiGlu ? 2 : 1;
+    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q4k_kernel<1, R, WAVES, 0, S, EPI, BATCH>)
+                    : reinterpret_cast<const void *>(&gemv_q4k_kernel<1, R, WAVES, 1, S, EPI, BATCH>);
 }
 
-// The gate-fused variants: one column, 8 or 16 waves, 1 or 2 slots, both
-// prologue orders.
-static const void *gemv_kernel_glu(int waves, int pro, int slots) {
+// The fused-epilogue variants (bias, or gate + GLU): one column, 8 or 16
+// waves, 1 or 2 slots, both prologue orders, plain or batched.
+template <int EPI, bool BATCH>
+static const void *gemv_kernel_epi(int waves, int pro, int slots) {
     if (pro != 0 && pro != 1) return nullptr;
-    if (waves <= 8) return slots == 1 ? gemv_sym_glu<8, 1>(pro) : gemv_sym_glu<8, 2>(pro);
-    return slots == 1 ? gemv_sym_glu<16, 1>(pro) : gemv_sym_glu<16, 2>(pro);
+    if (waves <= 8) return slots == 1 ? gemv_sym_epi<EPI, 8, 1, BATCH>(pro) : gemv_sym_epi<EPI, 8, 2, BATCH>(pro);
+    return slots == 1 ? gemv_sym_epi<EPI, 16, 1, BATCH>(pro) : gemv_sym_epi<EPI, 16, 2, BATCH>(pro);
+}
+
+template <int NC, int WAVES, int S>
+static const void *gemv_sym_batch(int pro) {
+    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, 1, WAVES, 0, S, kEpiNone, true>)
+                    : reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, 1, WAVES, 1, S, kEpiNone, true>);
+}
+
+template <int WAVES, int S>
+static const void *gemv_sym_batch_nc(int nc, int pro) {
+    switch (nc) {
+        case 1: return gemv_sym_batch<1, WAVES, S>(pro);
+        case 2: return gemv_sym_batch<2, WAVES, S>(pro);
+        case 3: return gemv_sym_batch<3, WAVES, S>(pro);
+        case 4: return gemv_sym_batch<4, WAVES, S>(pro);
+        case 5: return gemv_sym_batch<5, WAVES, S>(pro);
+        case 6: return gemv_sym_batch<6, WAVES, S>(pro);
+        case 7: return gemv_sym_batch<7, WAVES, S>(pro);
+        case 8: return gemv_sym_batch<8, WAVES, S>(pro);
+        default: return nullptr;
+    }
+}
+
+// Batched variants (channels/samples, MUL_MAT_ID): one row per tile, 8 or
+// 16 waves, 1 or 2 slots, both prologue orders.
+static const void *gemv_kernel_batch(int nc, int waves, int pro, int slots) {
+    if (pro != 0 && pro != 1) return nullptr;
+    if (waves <= 8) return slots == 1 ? gemv_sym_batch_nc<8, 1>(nc, pro) : gemv_sym_batch_nc<8, 2>(nc, pro);
+    return slots == 1 ? gemv_sym_batch_nc<16, 1>(nc, pro) : gemv_sym_batch_nc<16, 2>(nc, pro);
 }
 
 static const void *gemv_kernel_for(int nc, int R, int waves, int pro, int slots) {
@@ -879,11 +931,25 @@ static const void *gemv_kernel_for(int nc, int R, int waves, int pro, int slots)
     return slots == 4 ? gemv_sym_r<16, 4>(nc, R, pro) : gemv_sym_r<16, 2>(nc, R, pro);
 }
 
-static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc, hipStream_t stream) {
+static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc, hipStream_t stream,
+                       const BatchLaunch *bl = nullptr) {
     const void *fn = nullptr;
-    if (p.gate) {
-        if (nc != 1 || geo.bpl) return Q4K_EINVAL;
-        fn = gemv_kernel_glu(geo.waves, geo.prologue, geo.slots);
+    const bool batch = bl != nullptr;
+    if (batch && geo.bpl) return Q4K_EINVAL;
+    if (p.gate || p.bias) {
+        if (nc != 1 || geo.bpl || geo.R != (p.gate ? 2 : 1)) return Q4K_EINVAL;
+        if (p.gate)
+            fn = batch ? gemv_kernel_epi<kEpiGlu, true>(geo.waves, geo.prologue, geo.slots)
+                       : gemv_kernel_epi<kEpiGlu, false>(geo.waves, geo.prologue, geo.slots);
+        else
+            fn = batch ? gemv_kernel_epi<kEpiBias, true>(geo.waves, geo.prologue, geo.slots)
+                       : gemv_kernel_epi<kEpiBias, false>(geo.waves, geo.prologue, geo.slots);
+        p.rows_base = geo.rows_base;
+        p.rows_extra = geo.rows_extra;
+        p.ring_off = lds_bytes(p.K, nc);
+    } else if (batch) {
+        if (geo.R != 1) return Q4K_EINVAL;
+        fn = gemv_kernel_batch(nc, geo.waves, geo.prologue, geo.slots);
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
         p.ring_off = lds_bytes(p.K, nc);
@@ -907,8 +973,9 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
     int32_t ldx32 = (int32_t)p.ldx, scy32 = (int32_t)p.stride_col_y;
     void *args[] = {&p.x, &p.y, &p.w, &p.row_stride, &ldx32, &scy32, &p.K, &p.vec_ok,
                     &p.rows_base, &p.rows_extra, &p.nb, &p.qcol, &p};
-    hipError_t e = hipLaunchKernel(fn, dim3(geo.grid), dim3(kWave * geo.waves), args,
-                                   (size_t)geo.lds_launch, stream);
+    if (batch) p.bt = bl->bt;
+    const dim3 grid((unsigned)geo.grid, batch ? (unsigned)bl->nch : 1u, batch ? (unsigned)bl->nsmp : 1u);
+    hipError_t e = hipLaunchKernel(fn, grid, dim3(kWave * geo.waves), args, (size_t)geo.lds_launch, stream);
     if (e != hipSuccess) return hip_fail(e);
     e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e);
@@ -930,13 +997,21 @@ static int check_weight(const void *src0, int64_t ne00, int64_t ne01, int64_t nb
 
 static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x,
                     int64_t ldx, const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst,
-                    int64_t ld_dst, hipStream_t stream, const Epilogue *ep = nullptr) {
+                    int64_t ld_dst, hipStream_t stream, const Epilogue *ep = nullptr,
+                    const BatchLaunch *bl = nullptr) {
     DeviceInfo *di = nullptr;
     int st = device_info(&di);
     if (st != Q4K_OK) return st;
     const int fused = fused_kind(ep);
     if (fused && ncols != 1) return Q4K_EINVAL;
-    const Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused);
+    if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
+    const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
+    Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused, mats);
+    if (bl || fused) {  // the batched and fused variants: 1 or 2 slots, prologue 0 or 1
+        if (fused != kFusedGate) geo.R = 1;
+        if (geo.slots > 2) geo.slots = 2;
+        if (geo.prologue > 1) geo.prologue = 0;
+    }
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // the tile kernel addresses a wave's rows with 31-bit offsets; column
     // strides travel as 32-bit kernel arguments
@@ -972,7 +1047,7 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
             p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
             p.glu_op = ep->glu_op;
         }
-        st = launch_gemv(di, g2, p, nc, stream);
+        st = launch_gemv(di, g2, p, nc, stream, bl);
         if (st != Q4K_OK) return st;
     }
     return Q4K_OK;
@@ -1115,11 +1190,27 @@ int q4k_mul_mat_vec_q_fused(int32_t src0_type, const void *src0, int64_t ne00, i
               : run_gemv(src0, ne00, ne01, nb01, src1, ne00, nullptr, 0, 1, dst, ne01, s, e);
 }
 
-// Same shape and strides (ggml_are_same_stride for the 2-D case).
+// Same shape and strides (ggml_are_same_shape and ggml_are_same_stride).
 static bool same_layout(const q4k_tensor *a, const q4k_tensor *b) {
     for (int d = 0; d < 4; ++d)
         if (a->ne[d] != b->ne[d] || a->nb[d] != b->nb[d]) return false;
     return true;
+}
+
+// A bias of the fused epilogue: F32, dst->ne[0] values per row, and (the
+// kernel indexes it with dst's strides, as kernels/mmvq.cu:201-218 does) the
+// strides of dst in every further dimension the launch walks.
+static int check_bias(const q4k_tensor *b, const q4k_tensor *dst, const q4k_tensor *src0, bool ids) {
+    if (b->type != Q4K_GGML_TYPE_F32 || b->ne[0] != dst->ne[0] || b->nb[0] != 4) return Q4K_EINVAL;
+    if (ids) {
+        if (b->ne[1] != src0->ne[2]) return Q4K_EINVAL;  // one bias row per weight matrix
+        if (b->ne[1] > 1 && b->nb[1] != dst->nb[1]) return Q4K_EUNSUPPORTED;
+        if (dst->ne[3] > 1 && (b->ne[3] != dst->ne[3] || b->nb[3] != dst->nb[3])) return Q4K_EUNSUPPORTED;
+        return Q4K_OK;
+    }
+    for (int d = 2; d < 4; ++d)
+        if (dst->ne[d] > 1 && (b->ne[d] != dst->ne[d] || b->nb[d] != dst->nb[d])) return Q4K_EUNSUPPORTED;
+    return Q4K_OK;
 }
 
 int q4k_ggml_mul_mat_vec_q(const q4k_tensor *src0, const q4k_tensor *src1, const q4k_tensor *ids,
@@ -1131,38 +1222,99 @@ int q4k_ggml_mul_mat_vec_q(const q4k_tensor *src0, const q4k_tensor *src1, const
     const bool q6 = src0->type == Q4K_GGML_TYPE_Q6_K;
     const size_t block_bytes = q6 ? Q4K_BLOCK_Q6_K_BYTES : (size_t)kBlockBytes;
     if (src0->nb[0] != block_bytes || src1->nb[0] != 4 || dst->nb[0] != 4) return Q4K_EINVAL;
-    if (ids) return Q4K_EUNSUPPORTED;
-    for (int d = 2; d < 4; ++d)
-        if (src0->ne[d] != 1 || src1->ne[d] != 1 || dst->ne[d] != 1) return Q4K_EUNSUPPORTED;
-    if (src1->ne[0] != src0->ne[0] || dst->ne[0] != src0->ne[1] || dst->ne[1] != src1->ne[1])
-        return Q4K_EINVAL;
-    if (fusion && (fusion->x_bias || fusion->gate)) {
-        // the reference's fusion checks (kernels/mmvq.cu:696-714)
-        if (dst->ne[1] != 1) return Q4K_EINVAL;
-        q4k_fusion f{};
+    if (ids && (ids->type != Q4K_GGML_TYPE_I32 || ids->nb[0] != 4)) return Q4K_EINVAL;  // :671, :685
+    if (src1->ne[0] != src0->ne[0] || dst->ne[0] != src0->ne[1]) return Q4K_EINVAL;
+    for (int d = 1; d < 4; ++d)
+        if (src0->nb[d] % 2 || src1->nb[d] % 4 || dst->nb[d] % 4) return Q4K_EINVAL;
+    const int64_t ne00 = src0->ne[0], ne01 = src0->ne[1], ne02 = src0->ne[2], ne03 = src0->ne[3];
+    const int64_t ne11 = src1->ne[1], ne12 = src1->ne[2], ne13 = src1->ne[3];
+    if (ne02 < 1 || ne03 < 1) return Q4K_EINVAL;
+
+    // fused epilogue, under the reference's checks (kernels/mmvq.cu:694-715)
+    const bool want_fusion = fusion && (fusion->x_bias || fusion->gate);
+    Epilogue ep;
+    if (want_fusion) {
+        if (ids ? dst->ne[2] != 1 : dst->ne[1] != 1) return Q4K_EINVAL;
+        int st;
         if (fusion->x_bias) {
-            if (fusion->x_bias->type != Q4K_GGML_TYPE_F32 || fusion->x_bias->ne[0] != dst->ne[0]) return Q4K_EINVAL;
-            f.x_bias = static_cast<const float *>(fusion->x_bias->data);
+            if ((st = check_bias(fusion->x_bias, dst, src0, ids != nullptr)) != Q4K_OK) return st;
+            ep.bias = static_cast<const float *>(fusion->x_bias->data);
         }
         if (fusion->gate) {
             if (fusion->gate->type != src0->type || !same_layout(fusion->gate, src0)) return Q4K_EINVAL;
-            f.gate = fusion->gate->data;
+            if (fusion->glu_op != kGluGeglu && fusion->glu_op != kGluSwiglu && fusion->glu_op != kGluSwigluOai)
+                return Q4K_EUNSUPPORTED;
+            ep.gate = static_cast<const uint8_t *>(fusion->gate->data);
+            ep.glu_op = fusion->glu_op;
             if (fusion->gate_bias) {
-                if (fusion->gate_bias->type != Q4K_GGML_TYPE_F32 || fusion->gate_bias->ne[0] != dst->ne[0])
-                    return Q4K_EINVAL;
-                f.gate_bias = static_cast<const float *>(fusion->gate_bias->data);
+                if ((st = check_bias(fusion->gate_bias, dst, src0, ids != nullptr)) != Q4K_OK) return st;
+                ep.gate_bias = static_cast<const float *>(fusion->gate_bias->data);
             }
-            f.glu_op = fusion->glu_op;
         }
-        return q4k_mul_mat_vec_q_fused(src0->type, src0->data, src0->ne[0], src0->ne[1], (int64_t)src0->nb[1],
-                                       static_cast<const float *>(src1->data), &f,
-                                       static_cast<float *>(dst->data), stream);
+        if (!aligned(ep.gate, q6 ? 2 : 16)) return q6 ? Q4K_EINVAL : Q4K_EUNSUPPORTED;
     }
-    // ggml's nb00 is the block size: ne00 counts values, ne00/256 blocks per row
-    return (q6 ? q6k_mul_mat_vec_q : q4k_mul_mat_vec_q)(src0->data, src0->ne[0], src0->ne[1], (int64_t)src0->nb[1],
-                             static_cast<const float *>(src1->data), src1->ne[1],
-                             (int64_t)src1->nb[1], static_cast<float *>(dst->data),
-                             (int64_t)dst->nb[1], workspace, workspace_bytes, stream);
+    const Epilogue *e = want_fusion ? &ep : nullptr;
+    const int64_t nb01 = (int64_t)src0->nb[1];
+    const float *x = static_cast<const float *>(src1->data);
+    float *d = static_cast<float *>(dst->data);
+
+    BatchLaunch bl;
+    int64_t ncols, ldx, ldd;
+    if (!ids) {
+        if (dst->ne[1] != ne11 || dst->ne[2] != ne12 || dst->ne[3] != ne13) return Q4K_EINVAL;
+        if (ne12 % ne02 != 0 || ne13 % ne03 != 0) return Q4K_EINVAL;  // broadcast (ggml_can_mul_mat)
+        if (ne12 == 1 && ne13 == 1) {
+            // the 2-D product
+            if (e) {
+                q4k_fusion f{ep.bias, ep.gate, ep.gate_bias, ep.glu_op};
+                return q4k_mul_mat_vec_q_fused(src0->type, src0->data, ne00, ne01, nb01, x, &f, d, stream);
+            }
+            return (q6 ? q6k_mul_mat_vec_q : q4k_mul_mat_vec_q)(src0->data, ne00, ne01, nb01, x, ne11,
+                                                                 (int64_t)src1->nb[1], d, (int64_t)dst->nb[1],
+                                                                 workspace, workspace_bytes, stream);
+        }
+        bl.nch = (int)ne12;
+        bl.nsmp = (int)ne13;
+        bl.bt.channel_ratio = (int)(ne12 / ne02);
+        bl.bt.sample_ratio = (int)(ne13 / ne03);
+        bl.bt.x_channel = (int64_t)src1->nb[2] / 4;
+        bl.bt.dst_channel = (int64_t)dst->nb[2] / 4;
+        ncols = ne11;
+        ldx = (int64_t)src1->nb[1] / 4;
+        ldd = (int64_t)dst->nb[1] / 4;
+    } else {
+        // MUL_MAT_ID: dst column j of token 0 = src0[ids[j]] . src1 column j % ne11
+        if (ne12 != 1) return Q4K_EINVAL;  // :675 (batch size 1)
+        if (ids->ne[0] != dst->ne[1] || ids->ne[1] != ne12 || dst->ne[2] != ne12 || dst->ne[3] != ne13)
+            return Q4K_EINVAL;
+        if (ne13 % ne03 != 0) return Q4K_EINVAL;
+        if (!aligned(ids->data, 4)) return Q4K_EINVAL;
+        bl.nch = (int)dst->ne[1];
+        bl.nsmp = (int)ne13;
+        bl.bt.ids = static_cast<const int32_t *>(ids->data);
+        bl.bt.nchannels_y = (int)ne11;
+        bl.bt.nexperts = (int)ne02;
+        bl.bt.channel_ratio = 1;
+        bl.bt.sample_ratio = (int)(ne13 / ne03);
+        bl.bt.x_channel = (int64_t)src1->nb[1] / 4;
+        bl.bt.dst_channel = (int64_t)dst->nb[1] / 4;
+        ncols = 1;
+        ldx = (int64_t)src1->nb[2] / 4;
+        ldd = (int64_t)dst->nb[2] / 4;
+    }
+    if (ne01 == 0 || ne11 == 0 || bl.nch == 0 || bl.nsmp == 0) return Q4K_OK;  // empty product
+    if (ncols > Q4K_MAX_BATCH) return Q4K_EINVAL;
+    if (!x || !d || !aligned(x, 4) || !aligned(d, 4)) return Q4K_EINVAL;
+    bl.bt.w_channel = (int64_t)src0->nb[2];
+    bl.bt.w_sample = (int64_t)src0->nb[3];
+    bl.bt.x_sample = (int64_t)src1->nb[3] / 4;
+    bl.bt.dst_sample = (int64_t)dst->nb[3] / 4;
+    int st = q6 ? check_weight_q6(src0->data, ne00, ne01, nb01) : check_weight(src0->data, ne00, ne01, nb01);
+    if (st != Q4K_OK) return st;
+    if (!q6 && ((bl.bt.w_channel % 16) || (bl.bt.w_sample % 16))) return Q4K_EUNSUPPORTED;
+    const hipStream_t s = (hipStream_t)stream;
+    return q6 ? run_gemv_q6(src0->data, ne00, ne01, nb01, x, ldx, nullptr, 0, ncols, d, ldd, s, e, &bl)
+              : run_gemv(src0->data, ne00, ne01, nb01, x, ldx, nullptr, 0, ncols, d, ldd, s, e, &bl);
 }
 
 int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const void *q8_1,

@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "../../include/q4k_gemv.h"
+#include "q4k_tile.h"
 
 namespace q4k {
 
@@ -69,7 +70,15 @@ inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)
 int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01);
 int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x, int64_t ldx,
                 const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst, int64_t ld_dst,
-                hipStream_t stream, const Epilogue *ep = nullptr);
+                hipStream_t stream, const Epilogue *ep = nullptr, const BatchLaunch *bl = nullptr);
+
+// Workgroups per weight matrix of a launch over `mats` matrices of M rows:
+// the CUs shared among the matrices, at least one, at most one per row.
+inline int grid_per_matrix(int cus, int64_t mats, int64_t M) {
+    int64_t g = mats > 1 ? cus / mats : cus;
+    if (mats > 1 && g > M) g = M;
+    return g < 1 ? 1 : (int)g;
+}
 inline int64_t pad512(int64_t k) { return (k + 511) / 512 * 512; }
 // LDS bytes of one staged q8 column in a tile layout (whole 16-block groups)
 inline int q8_col_bytes(int K) { return (K + 4095) / 4096 * 4096; }

@@ -8,6 +8,24 @@
 
 namespace q4k {
 
+// Channels and samples of a batched launch (grid y = dst channel, z = dst
+// sample; kernels/mmvq.cu:174-180): the weight matrix is ids[channel]
+// (MUL_MAT_ID) or channel / channel_ratio, the activation channel is
+// channel % nchannels_y (MUL_MAT_ID) or the channel itself.
+struct BatchParams {
+    const int32_t *ids;      // MUL_MAT_ID: weight matrix of each dst channel, or null
+    int64_t w_channel;       // bytes between weight matrices
+    int64_t w_sample;
+    int64_t x_channel;       // activation: floats (F32) or Q8_1 blocks
+    int64_t x_sample;
+    int64_t dst_channel;     // floats (biases are indexed like dst)
+    int64_t dst_sample;
+    int channel_ratio;       // dst channels per weight matrix (without ids)
+    int sample_ratio;        // dst samples per weight sample
+    int nchannels_y;         // MUL_MAT_ID: activation channels (1 or the number of ids)
+    int nexperts;            // MUL_MAT_ID: weight matrices; other ids read no weights
+};
+
 struct GemvParams {
     const uint8_t *w;        // weight rows (Q4_K)
     int64_t row_stride;      // bytes between rows
@@ -35,7 +53,59 @@ struct GemvParams {
     const float *bias;
     const float *gate_bias;
     int glu_op;
+    BatchParams bt;          // batched launches only
+    int w_absent;            // batched: this workgroup's weight matrix is absent (bad id)
 };
+
+// A batched launch: its BatchParams and the dst channels and samples (grid
+// y and z); nch = nsmp = 1 with bt.ids null is the plain 2-D product.
+struct BatchLaunch {
+    BatchParams bt{};
+    int nch = 1;
+    int nsmp = 1;
+};
+
+// Batched launches, step 1 (before the activation loads): this workgroup's
+// activation channel, dst and bias slices.  Only kernel arguments and the
+// block index: no memory access.
+__device__ __forceinline__ void batch_activation(GemvParams &p) {
+    const int ch = (int)blockIdx.y, smp = (int)blockIdx.z;
+    const int cy = p.bt.ids ? ch % p.bt.nchannels_y : ch;
+    const int64_t xo = (int64_t)smp * p.bt.x_sample + (int64_t)cy * p.bt.x_channel;
+    if (p.x) p.x += xo;
+    else p.y += xo * kQ81Bytes;
+    const int64_t dofs = (int64_t)smp * p.bt.dst_sample + (int64_t)ch * p.bt.dst_channel;
+    p.dst += dofs;
+    if (!p.bt.ids) {  // biases per dst channel; with ids per weight matrix (step 2)
+        if (p.bias) p.bias += dofs;
+        if (p.gate_bias) p.gate_bias += dofs;
+    }
+}
+
+// Batched launches, step 2 (after the activation loads are issued): the
+// weight matrix.  The expert id is read with a vector load, which returns
+// after the activation loads issued before it, then made wave-uniform.  An
+// id outside [0, nexperts) selects no matrix: the workgroup's weight loads
+// read zeros and its biases are dropped.
+__device__ __forceinline__ void batch_weights(GemvParams &p) {
+    const int ch = (int)blockIdx.y, smp = (int)blockIdx.z;
+    int cx;
+    if (p.bt.ids) {
+        const __amdgpu_buffer_rsrc_t ri = make_rsrc(p.bt.ids, (uint32_t)(ch + 1) * 4u);
+        cx = __builtin_amdgcn_readfirstlane((int)__builtin_amdgcn_raw_buffer_load_b32(ri, (uint32_t)ch * 4u, 0, 0));
+        const bool ok = cx >= 0 && cx < p.bt.nexperts;
+        p.w_absent = !ok;
+        const int64_t bo = (int64_t)smp * p.bt.dst_sample + (int64_t)cx * p.bt.dst_channel;
+        p.bias = p.bias && ok ? p.bias + bo : nullptr;
+        p.gate_bias = p.gate_bias && ok ? p.gate_bias + bo : nullptr;
+        if (!ok) cx = 0;
+    } else {
+        cx = ch / p.bt.channel_ratio;
+    }
+    const int64_t wo = (int64_t)(smp / p.bt.sample_ratio) * p.bt.w_sample + (int64_t)cx * p.bt.w_channel;
+    p.w += wo;
+    if (p.gate) p.gate += wo;
+}
 
 // The GEMV kernels take the fields their first memory requests need as
 // leading scalar arguments (16 dwords), ahead of the GemvParams block, so
@@ -97,6 +167,14 @@ __device__ __forceinline__ WaveRows wave_rows(const GemvParams &p, int wave) {
     return WaveRows{beg, beg + q + (wave < rem ? 1 : 0)};
 }
 
+// Epilogue of a tile kernel variant, a compile-time choice: the plain
+// kernels never read the epilogue's kernel arguments (a kernel-argument
+// cache line first touched at the loop's entry costs the whole launch a
+// memory round trip).
+constexpr int kEpiNone = 0;  // dst = product
+constexpr int kEpiBias = 1;  // dst = product + bias
+constexpr int kEpiGlu = 2;   // dst = glu(product + bias, gate product + gate bias)
+
 // GLU ops of the fused epilogue (values of ggml's enum ggml_glu_op).
 constexpr int kGluGeglu = 1;
 constexpr int kGluSwiglu = 2;
@@ -135,10 +213,10 @@ struct ResultRing {
 };
 
 // Writes the buffered entries to dst (entries of rows >= end are dropped),
-// adding the bias and applying the GLU when the launch carries them.
-template <int NC, bool GLU>
+// applying the variant's epilogue.
+template <int NC, int EPI>
 __device__ __forceinline__ void ring_flush(const GemvParams &p, int lane, ResultRing &rr) {
-    if (GLU) {
+    if (EPI == kEpiGlu) {
         for (int k = lane; 2 * k < rr.n; k += kWave) {
             const int row = rr.beg + rr.base / 2 + k;
             if (row < rr.end) {
@@ -155,7 +233,7 @@ __device__ __forceinline__ void ring_flush(const GemvParams &p, int lane, Result
             const int c = idx - (idx / NC) * NC;
             if (row < rr.end) {
                 const int64_t o = (int64_t)c * p.ld_dst + row;
-                p.dst[o] = p.bias ? rr.buf[k] + p.bias[o] : rr.buf[k];
+                p.dst[o] = EPI == kEpiBias ? rr.buf[k] + p.bias[o] : rr.buf[k];
             }
         }
     }
@@ -165,7 +243,7 @@ __device__ __forceinline__ void ring_flush(const GemvParams &p, int lane, Result
 
 // End of a row tile: the R x NC lane partials of the tile, reduced over the
 // wave, go to the result ring (lane r*NC + c writes entry r*NC + c).
-template <int NC, int R, bool GLU>
+template <int NC, int R, int EPI>
 __device__ __forceinline__ void tile_to_ring(const GemvParams &p, int lane, float (&acc)[R][NC],
                                              ResultRing &rr) {
     float out = 0.0f;
@@ -181,7 +259,7 @@ __device__ __forceinline__ void tile_to_ring(const GemvParams &p, int lane, floa
     rr.n += R * NC;
     // rare (a wave's rows x NC above kRing): global stores inside the
     // loop make the compiler's load waits conservative
-    if (rr.n + R * NC > kRing) ring_flush<NC, GLU>(p, lane, rr);
+    if (rr.n + R * NC > kRing) ring_flush<NC, EPI>(p, lane, rr);
 }
 
 }  // namespace q4k

@@ -167,7 +167,7 @@ __device__ __forceinline__ void q6_load_step(const GemvParams &p, const Q6Lane &
 
 // Consumes one group held in w (one row, or the row and its gate row); at
 // the tile's last group moves the R x NC sums to the result ring.
-template <int NC, int R, bool GLU>
+template <int NC, int R, int EPI>
 __device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6Lane &ln, Step st,
                                                  const int8_t *q8s, const uint8_t *aux, const Q6Regs (&w)[R],
                                                  float (&acc)[R][NC], ResultRing &rr) {
@@ -196,7 +196,7 @@ __device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6La
             acc[r][c] = __builtin_fmaf(d[r], f, acc[r][c]);
         }
     }
-    if (st.i == p.G - 1) tile_to_ring<NC, R, GLU>(p, ln.lane, acc, rr);
+    if (st.i == p.G - 1) tile_to_ring<NC, R, EPI>(p, ln.lane, acc, rr);
 }
 
 // Tile kernel: any K, 1..8 columns; one row per tile.  The structure of the
@@ -206,11 +206,16 @@ __device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6La
 // the S-slot stream with unconditional loads and the result ring.  GLU (one
 // column): each tile also streams the same row of the gate weight, and the
 // ring flush applies the biases and the GLU.
-template <int NC, int WAVES, int PRO, int S, bool GLU>
+// BATCH: channels and samples over grid y and z, as in the Q4_K kernel.
+// EPI: the epilogue (kEpiNone, kEpiBias, kEpiGlu; the fused ones are one
+// column).
+template <int NC, int WAVES, int PRO, int S, int EPI = kEpiNone, bool BATCH = false>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_ARGS) {
-    static_assert(!GLU || NC == 1, "the fused epilogue is one-column");
+    constexpr bool GLU = EPI == kEpiGlu;
+    static_assert(EPI == kEpiNone || NC == 1, "the fused epilogue is one-column");
     constexpr int R = GLU ? 2 : 1;
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    if constexpr (BATCH) batch_activation(p);
     constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : 0;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
@@ -219,18 +224,25 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     const Q6Lane ln = q6_lane(threadIdx.x & (kWave - 1));
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WaveRows wr = wave_rows<WAVES>(p, wave);
+    constexpr int kLPB = NC == 1 ? 8 : 4;
+    ActStage<kLPB> xs;
+    Q81Stage ys;
+    if constexpr (BATCH) {
+        if (p.x) stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+        else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+        batch_weights(p);
+    }
     Q6Stream ws;
-    const uint32_t wave_bytes = (uint32_t)((wr.end - wr.beg) * p.row_stride);
+    const uint32_t wave_bytes = BATCH && p.w_absent ? 0u : (uint32_t)((wr.end - wr.beg) * p.row_stride);
     ws.rs = make_rsrc(p.w + (int64_t)wr.beg * p.row_stride, wave_bytes);
     ws.rs_gate = GLU ? make_rsrc(p.gate + (int64_t)wr.beg * p.row_stride, wave_bytes) : ws.rs;
     ws.ntiles = wr.end - wr.beg;
     int remaining = ws.ntiles * p.G;
 
-    constexpr int kLPB = NC == 1 ? 8 : 4;
-    ActStage<kLPB> xs;
-    Q81Stage ys;
-    if (p.x) stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
-    else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+    if constexpr (!BATCH) {
+        if (p.x) stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+        else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+    }
     __syncthreads();  // all activation loads of this CU are queued first
 
     Step st[S];
@@ -261,14 +273,14 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     for (;;) {
 #pragma unroll
         for (int k = 0; k < S; ++k) {
-            q6_process_group<NC, R, GLU>(p, ln, st[k], q8s, aux, w[k], acc, rr);
+            q6_process_group<NC, R, EPI>(p, ln, st[k], q8s, aux, w[k], acc, rr);
             st[k] = next_step(st[(k + S - 1) % S], p.G);
             q6_load_step<R>(p, ln, ws, st[k], w[k]);
         }
         remaining -= S;
         if (remaining <= 0) break;
     }
-    ring_flush<NC, GLU>(p, ln.lane, rr);
+    ring_flush<NC, EPI>(p, ln.lane, rr);
 }
 
 // Parity probe: the int32 sums over every 16-weight scale group of
@@ -345,7 +357,7 @@ struct Q6Geometry {
 // the kPre staging rounds.  Measured on MI355X: with 210-byte blocks, more
 // weight requests in flight (16 waves x 2 groups, 27.5 MB over the chip)
 // delay the activation loads more than they hide latency.
-static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N) {
+static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int64_t mats = 1) {
     load_env_overrides();
     Q6Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
@@ -354,7 +366,7 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     while (nc > 1 && q6_tile_lds_bytes((int)K, nc, 16) > max_lds) nc = (nc + 1) / 2;
     g.nc_chunk = nc;
     const int owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load(), oslots = g_ovr_slots.load();
-    g.grid = owgs > 0 ? owgs : cus;
+    g.grid = owgs > 0 ? owgs : grid_per_matrix(cus, mats, M);
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
     g.waves = steps_per_wg >= 16 && (int64_t)nc * K > 8192 ? 16 : 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;
@@ -373,35 +385,43 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     return g;
 }
 
-template <int NC, int WAVES, int S, bool GLU = false>
+template <int NC, int WAVES, int S, int EPI, bool BATCH>
 static const void *q6_sym(int pro) {
-    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 0, S, GLU>)
-                    : reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 1, S, GLU>);
+    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 0, S, EPI, BATCH>)
+                    : reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 1, S, EPI, BATCH>);
 }
 
-template <int WAVES, int S>
+template <int WAVES, int S, bool BATCH>
 static const void *q6_sym_nc(int nc, int pro) {
     switch (nc) {
-        case 1: return q6_sym<1, WAVES, S>(pro);
-        case 2: return q6_sym<2, WAVES, S>(pro);
-        case 3: return q6_sym<3, WAVES, S>(pro);
-        case 4: return q6_sym<4, WAVES, S>(pro);
-        case 5: return q6_sym<5, WAVES, S>(pro);
-        case 6: return q6_sym<6, WAVES, S>(pro);
-        case 7: return q6_sym<7, WAVES, S>(pro);
-        case 8: return q6_sym<8, WAVES, S>(pro);
+        case 1: return q6_sym<1, WAVES, S, kEpiNone, BATCH>(pro);
+        case 2: return q6_sym<2, WAVES, S, kEpiNone, BATCH>(pro);
+        case 3: return q6_sym<3, WAVES, S, kEpiNone, BATCH>(pro);
+        case 4: return q6_sym<4, WAVES, S, kEpiNone, BATCH>(pro);
+        case 5: return q6_sym<5, WAVES, S, kEpiNone, BATCH>(pro);
+        case 6: return q6_sym<6, WAVES, S, kEpiNone, BATCH>(pro);
+        case 7: return q6_sym<7, WAVES, S, kEpiNone, BATCH>(pro);
+        case 8: return q6_sym<8, WAVES, S, kEpiNone, BATCH>(pro);
         default: return nullptr;
     }
 }
 
-static const void *q6_kernel_for(int nc, int waves, int pro, int slots, bool glu) {
-    if (glu) {
+template <int EPI, bool BATCH>
+static const void *q6_kernel_epi(int waves, int pro, int slots) {
+    if (waves <= 8) return slots == 1 ? q6_sym<1, 8, 1, EPI, BATCH>(pro) : q6_sym<1, 8, 2, EPI, BATCH>(pro);
+    return slots == 1 ? q6_sym<1, 16, 1, EPI, BATCH>(pro) : q6_sym<1, 16, 2, EPI, BATCH>(pro);
+}
+
+template <bool BATCH>
+static const void *q6_kernel_for(int nc, int waves, int pro, int slots, int fused) {
+    if (pro != 0 && pro != 1) return nullptr;
+    if (fused) {
         if (nc != 1) return nullptr;
-        if (waves <= 8) return slots == 1 ? q6_sym<1, 8, 1, true>(pro) : q6_sym<1, 8, 2, true>(pro);
-        return slots == 1 ? q6_sym<1, 16, 1, true>(pro) : q6_sym<1, 16, 2, true>(pro);
+        return fused == kFusedGate ? q6_kernel_epi<kEpiGlu, BATCH>(waves, pro, slots)
+                                   : q6_kernel_epi<kEpiBias, BATCH>(waves, pro, slots);
     }
-    if (waves <= 8) return slots == 1 ? q6_sym_nc<8, 1>(nc, pro) : q6_sym_nc<8, 2>(nc, pro);
-    return slots == 1 ? q6_sym_nc<16, 1>(nc, pro) : q6_sym_nc<16, 2>(nc, pro);
+    if (waves <= 8) return slots == 1 ? q6_sym_nc<8, 1, BATCH>(nc, pro) : q6_sym_nc<8, 2, BATCH>(nc, pro);
+    return slots == 1 ? q6_sym_nc<16, 1, BATCH>(nc, pro) : q6_sym_nc<16, 2, BATCH>(nc, pro);
 }
 
 int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01) {
@@ -417,13 +437,15 @@ int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01) 
 
 int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x, int64_t ldx,
                 const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst, int64_t ld_dst,
-                hipStream_t stream, const Epilogue *ep) {
+                hipStream_t stream, const Epilogue *ep, const BatchLaunch *bl) {
     DeviceInfo *di = nullptr;
     int st = device_info(&di);
     if (st != Q4K_OK) return st;
     const int fused = fused_kind(ep);
     if (fused && ncols != 1) return Q4K_EINVAL;
-    const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols);
+    if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
+    const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
+    const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // a wave's rows are addressed with 31-bit offsets; column strides travel
     // as 32-bit kernel arguments
@@ -459,15 +481,17 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
             p.glu_op = ep->glu_op;
         }
-        const void *fn = q6_kernel_for(nc, geo.waves, geo.prologue, geo.slots, fused == kFusedGate);
+        const void *fn = bl ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused)
+                            : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused);
+        if (bl) p.bt = bl->bt;
         if (!fn) return Q4K_EINVAL;
         st = ensure_lds(di, fn, lds_launch);
         if (st != Q4K_OK) return st;
         int32_t ldx32 = (int32_t)p.ldx, scy32 = (int32_t)p.stride_col_y;
         void *args[] = {&p.x, &p.y, &p.w, &p.row_stride, &ldx32, &scy32, &p.K, &p.vec_ok,
                         &p.rows_base, &p.rows_extra, &p.nb, &p.qcol, &p};
-        hipError_t e = hipLaunchKernel(fn, dim3(geo.grid), dim3(kWave * geo.waves), args, (size_t)lds_launch,
-                                       stream);
+        const dim3 grid((unsigned)geo.grid, bl ? (unsigned)bl->nch : 1u, bl ? (unsigned)bl->nsmp : 1u);
+        hipError_t e = hipLaunchKernel(fn, grid, dim3(kWave * geo.waves), args, (size_t)lds_launch, stream);
         if (e != hipSuccess) return hip_fail(e);
         e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(e);

@@ -53,6 +53,7 @@ typedef enum q4k_status {
 #define Q4K_GGML_TYPE_Q8_1 9
 #define Q4K_GGML_TYPE_Q4_K 12
 #define Q4K_GGML_TYPE_Q6_K 14
+#define Q4K_GGML_TYPE_I32 26  /* MUL_MAT_ID expert ids */
 
 #define Q4K_QK_K 256            /* weights per Q4_K super-block */
 #define Q4K_BLOCK_Q4_K_BYTES 144 /* d, dmin (fp16), scales[12], qs[128]; kernels/2pack.cu:6 */
@@ -160,11 +161,19 @@ int q4k_op_mul_mat_vec_q(const void *src0_dd_i, int64_t ne00, int64_t row_low, i
  * :600-605; any other type returns Q4K_EUNSUPPORTED).
  * Checks the reference's assertions: src1/dst F32 (:669-670), nb00 == block
  * size, nb10 == 4, nb0 == 4 (:681-683), ne10 == ne00, ne0 == ne01, ne1 == ne11.
+ * Channels and samples (dims 2 and 3) broadcast as in ggml's MUL_MAT:
+ * dst channel c, sample s uses src0 matrix (c / (ne12/ne02), s / (ne13/ne03))
+ * and src1 channel c, sample s (kernels/mmvq.cu:174-180, :739-755), all in
+ * one launch.  With ids (I32, GGML_OP_MUL_MAT_ID for one token, ne12 == 1,
+ * kernels/mmvq.cu:675): dst column j = src0 matrix ids[j] times src1 column
+ * j % ne11; the ids are read on the device, and an id outside [0, ne02)
+ * yields a zero column.
  * fusion (may be NULL) adds the bias / gate + GLU epilogue of
- * q4k_mul_mat_vec_q_fused under the reference's checks (:696-714): dst with
- * one column, F32 biases of dst->ne[0] values, a gate of src0's type and
- * strides.  Returns Q4K_EUNSUPPORTED for what this path does not implement:
- * ids (MUL_MAT_ID), more than one channel or sample (ne2/ne3 > 1). */
+ * q4k_mul_mat_vec_q_fused under the reference's checks (:694-714): one dst
+ * column per channel (dst->ne[1] == 1, or with ids dst->ne[2] == 1), F32
+ * biases of dst->ne[0] values (with ids one row per src0 matrix), a gate of
+ * src0's type, shape and strides; biases are indexed with dst's strides in
+ * the dimensions the launch walks (other layouts: Q4K_EUNSUPPORTED). */
 int q4k_ggml_mul_mat_vec_q(const q4k_tensor *src0, const q4k_tensor *src1, const q4k_tensor *ids,
                            q4k_tensor *dst, const q4k_fusion_args *fusion, void *workspace,
                            size_t workspace_bytes, void *stream);

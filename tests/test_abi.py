@@ -70,7 +70,7 @@ def test_op_and_descriptor_checks(Q):
     d = Q.make_tensor(Q.GGML_TYPE_F32, [16, 1], [4, 64], 0x30000)
     f16 = Q.make_tensor(1, [4096, 1], [2, 8192], 0x20000)
     assert Q.ggml_mul_mat_vec_q(s0, f16, d) == Q.Q4K_EINVAL
-    assert Q.ggml_mul_mat_vec_q(s0, s1, d, ids=s1) == Q.Q4K_EUNSUPPORTED
+    assert Q.ggml_mul_mat_vec_q(s0, s1, d, ids=s1) == Q.Q4K_EINVAL           # ids must be I32
     # fusion under the reference's checks (host-side, no device call)
     gate = Q.make_tensor(Q.GGML_TYPE_Q4_K, [4096, 16], [144, 2304], 0x50000)
     bad_bias = Q.make_tensor(1, [16], [2], 0x60000)
@@ -90,7 +90,15 @@ def test_op_and_descriptor_checks(Q):
     q6 = Q.make_tensor(Q.GGML_TYPE_Q6_K, [4096, 16], [144, 3360], 0x10000)
     assert Q.ggml_mul_mat_vec_q(q6, s1, d) == Q.Q4K_EINVAL                   # nb00 != 210
     s3 = Q.make_tensor(Q.GGML_TYPE_F32, [4096, 1, 2], [4, 16384, 16384], 0x20000)
-    assert Q.ggml_mul_mat_vec_q(s0, s3, d) == Q.Q4K_EUNSUPPORTED             # batched 3-D
+    assert Q.ggml_mul_mat_vec_q(s0, s3, d) == Q.Q4K_EINVAL                   # dst dims != src1's
+    s03 = Q.make_tensor(Q.GGML_TYPE_Q4_K, [4096, 16, 2], [144, 2304, 2304 * 16], 0x10000)
+    s13 = Q.make_tensor(Q.GGML_TYPE_F32, [4096, 1, 3], [4, 16384, 16384], 0x20000)
+    d3 = Q.make_tensor(Q.GGML_TYPE_F32, [16, 1, 3], [4, 64, 64], 0x30000)
+    assert Q.ggml_mul_mat_vec_q(s03, s13, d3) == Q.Q4K_EINVAL                # 3 channels over 2 matrices
+    ids2 = Q.make_tensor(26, [2, 2], [4, 8], 0x40000)
+    d2 = Q.make_tensor(Q.GGML_TYPE_F32, [16, 2, 2], [4, 64, 128], 0x30000)
+    s12 = Q.make_tensor(Q.GGML_TYPE_F32, [4096, 1, 2], [4, 16384, 16384], 0x20000)
+    assert Q.ggml_mul_mat_vec_q(s03, s12, d2, ids=ids2) == Q.Q4K_EINVAL      # MUL_MAT_ID: one token
     assert L.q4k_quantize_row_q8_1(FAKE, FAKE, 100, 100, 96, 1, None) == Q.Q4K_EINVAL
     assert L.q4k_quantize_row_q8_1(FAKE, FAKE, 100, 100, 130, 1, None) == Q.Q4K_EINVAL
     assert L.q4k_quantize_rows_q4_K(None, None, 4, 300, 1) == Q.Q4K_EINVAL

@@ -201,10 +201,12 @@ def test_ggml_descriptor_entry(Q, O, gpu):
     assert Q.ggml_mul_mat_vec_q(s0, s1, d) == Q.Q4K_OK
     y = Q.mul_mat_vec_q(wd, K, xd)
     assert torch.equal(dst, y)
-    # what the path leaves to the caller's fallback
-    assert Q.ggml_mul_mat_vec_q(s0, s1, d, ids=s1) == Q.Q4K_EUNSUPPORTED
+    # argument errors the reference asserts on
+    assert Q.ggml_mul_mat_vec_q(s0, s1, d, ids=s1) == Q.Q4K_EINVAL        # ids not I32
     s3 = Q.make_tensor(Q.GGML_TYPE_Q4_K, [K, M, 2], [144, wq.shape[1], wq.nbytes], wd.data_ptr())
-    assert Q.ggml_mul_mat_vec_q(s3, s1, d) == Q.Q4K_EUNSUPPORTED
+    assert Q.ggml_mul_mat_vec_q(s3, s1, d) == Q.Q4K_EINVAL                # 1 channel over 2 matrices
+    q5 = Q.make_tensor(13, [K, M], [176, K // 256 * 176], wd.data_ptr())
+    assert Q.ggml_mul_mat_vec_q(q5, s1, d) == Q.Q4K_EUNSUPPORTED          # left to the caller
     bad = Q.make_tensor(Q.GGML_TYPE_F32, [K + 256, N], [4, (K + 256) * 4], xd.data_ptr())
     assert Q.ggml_mul_mat_vec_q(s0, bad, d) == Q.Q4K_EINVAL
 
