@@ -18,7 +18,7 @@ import numpy as np
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libq4k_gemv.so")
 
-Q4K_OK, Q4K_EUNSUPPORTED, Q4K_EINVAL, Q4K_EHIP, Q4K_ENOMEM = 0, 1, 2, 3, 4
+Q4K_OK, Q4K_EUNSUPPORTED, Q4K_EINVAL, Q4K_EHIP, Q4K_ENOMEM, Q4K_EIO, Q4K_EFORMAT = 0, 1, 2, 3, 4, 5, 6
 GGML_TYPE_F32, GGML_TYPE_Q8_1, GGML_TYPE_Q4_K, GGML_TYPE_Q6_K = 0, 9, 12, 14
 QK_K = 256
 BLOCK_Q4_K_BYTES = 144
@@ -26,7 +26,14 @@ BLOCK_Q6_K_BYTES = 210
 BLOCK_Q8_1_BYTES = 36
 MATRIX_ROW_PADDING = 512
 
-# Every symbol include/q4k_gemv.h declares: (restype, argtypes)
+class q4k_gguf_tensor_info(ctypes.Structure):
+    """A GGUF tensor directory entry (include/q4k_gguf.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int32), ("n_dims", ctypes.c_int32),
+                ("ne", ctypes.c_int64 * 4), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64),
+                ("data", ctypes.c_void_p)]
+
+
+# Every symbol include/q4k_gemv.h and include/q4k_gguf.h declare: (restype, argtypes)
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
@@ -50,6 +57,26 @@ SIGNATURES = {
     "q6k_group_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P]),
     "q6k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
     "q4k_quantize_rows_q6_K": (_I, [_P, _P, _I64, _I64, _I]),
+    # include/q4k_gguf.h
+    "q4k_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "q4k_gguf_close": (None, [_P]),
+    "q4k_gguf_version": (ctypes.c_uint32, [_P]),
+    "q4k_gguf_alignment": (ctypes.c_uint64, [_P]),
+    "q4k_gguf_data_offset": (ctypes.c_uint64, [_P]),
+    "q4k_gguf_tensor_count": (_I64, [_P]),
+    "q4k_gguf_find_tensor": (_I64, [_P, ctypes.c_char_p]),
+    "q4k_gguf_get_tensor": (_I, [_P, _I64, ctypes.POINTER(q4k_gguf_tensor_info)]),
+    "q4k_ggml_row_size": (ctypes.c_uint64, [ctypes.c_int32, _I64]),
+    "q4k_gguf_kv_count": (_I64, [_P]),
+    "q4k_gguf_find_key": (_I64, [_P, ctypes.c_char_p]),
+    "q4k_gguf_key": (ctypes.c_char_p, [_P, _I64]),
+    "q4k_gguf_kv_type": (ctypes.c_int32, [_P, _I64]),
+    "q4k_gguf_get_int": (_I, [_P, _I64, ctypes.POINTER(_I64)]),
+    "q4k_gguf_get_float": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_double)]),
+    "q4k_gguf_get_str": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_char_p)]),
+    "q4k_gguf_get_arr": (_I, [_P, _I64, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_I64),
+                              ctypes.POINTER(_P)]),
+    "q4k_gguf_get_arr_str": (_I, [_P, _I64, _I64, ctypes.POINTER(ctypes.c_char_p)]),
 }
 
 
@@ -287,3 +314,88 @@ def geometry(K: int, M: int, N: int, wtype: int = GGML_TYPE_Q4_K) -> dict:
     keys = ("rows_per_tile", "waves_per_wg", "workgroups", "lds_bytes", "cols_per_launch", "fused",
             "kernel", "rows_per_step")
     return dict(zip(keys, list(out)))
+
+
+# ------------------------------------------------------------------ GGUF ----
+GGUF_ARRAY, GGUF_STRING = 9, 8
+_GGUF_NP = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32, 6: np.float32,
+            7: np.bool_, 10: np.uint64, 11: np.int64, 12: np.float64}
+
+
+class GGUFFile:
+    """A GGUF file opened with the library's reader (q4k_gguf_open).
+    tensors: {name: dict(type, ne, offset, nbytes)}; tensor_bytes(name) is a
+    zero-copy uint8 view of the mapped data, valid until close()."""
+
+    def __init__(self, path: str):
+        self._h = ctypes.c_void_p()
+        _check(lib().q4k_gguf_open(os.fsencode(path), ctypes.byref(self._h)), f"q4k_gguf_open({path})")
+        L = lib()
+        self.version = int(L.q4k_gguf_version(self._h))
+        self.alignment = int(L.q4k_gguf_alignment(self._h))
+        self.data_offset = int(L.q4k_gguf_data_offset(self._h))
+        self.tensors = {}
+        for i in range(L.q4k_gguf_tensor_count(self._h)):
+            ti = q4k_gguf_tensor_info()
+            _check(L.q4k_gguf_get_tensor(self._h, i, ctypes.byref(ti)), "q4k_gguf_get_tensor")
+            self.tensors[ti.name.decode()] = {"index": i, "type": ti.type, "ne": list(ti.ne)[:ti.n_dims],
+                                              "offset": int(ti.offset), "nbytes": int(ti.nbytes),
+                                              "data": ti.data}
+
+    def metadata(self) -> dict:
+        L = lib()
+        out = {}
+        for i in range(L.q4k_gguf_kv_count(self._h)):
+            key = L.q4k_gguf_key(self._h, i).decode()
+            t = L.q4k_gguf_kv_type(self._h, i)
+            if t == GGUF_STRING:
+                sp = ctypes.c_char_p()
+                _check(L.q4k_gguf_get_str(self._h, i, ctypes.byref(sp)), key)
+                out[key] = sp.value.decode()
+            elif t == GGUF_ARRAY:
+                et, n, dp = ctypes.c_int32(), ctypes.c_int64(), ctypes.c_void_p()
+                _check(L.q4k_gguf_get_arr(self._h, i, ctypes.byref(et), ctypes.byref(n), ctypes.byref(dp)), key)
+                if et.value == GGUF_STRING:
+                    vals = []
+                    for j in range(n.value):
+                        sp = ctypes.c_char_p()
+                        _check(L.q4k_gguf_get_arr_str(self._h, i, j, ctypes.byref(sp)), key)
+                        vals.append(sp.value.decode())
+                    out[key] = vals
+                else:
+                    dt = np.dtype(_GGUF_NP[et.value])
+                    buf = (ctypes.c_uint8 * (n.value * dt.itemsize)).from_address(dp.value) if n.value else b""
+                    out[key] = np.frombuffer(bytes(buf), dtype=dt).tolist()
+            elif t in (6, 12):
+                v = ctypes.c_double()
+                _check(L.q4k_gguf_get_float(self._h, i, ctypes.byref(v)), key)
+                out[key] = v.value
+            else:
+                v = ctypes.c_int64()
+                _check(L.q4k_gguf_get_int(self._h, i, ctypes.byref(v)), key)
+                out[key] = bool(v.value) if t == 7 else v.value
+        return out
+
+    def tensor_bytes(self, name: str) -> np.ndarray:
+        t = self.tensors[name]
+        if not t["nbytes"]:
+            raise ValueError(f"{name}: block size of ggml type {t['type']} unknown")
+        buf = (ctypes.c_uint8 * t["nbytes"]).from_address(t["data"])
+        return np.frombuffer(buf, dtype=np.uint8)
+
+    def weight_rows(self, name: str) -> np.ndarray:
+        """A 2-D quantised weight as [rows, row bytes] (zero-copy view)."""
+        t = self.tensors[name]
+        rb = int(lib().q4k_ggml_row_size(t["type"], t["ne"][0]))
+        return self.tensor_bytes(name).reshape(-1, rb)
+
+    def close(self):
+        if self._h:
+            lib().q4k_gguf_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

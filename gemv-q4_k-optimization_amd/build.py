@@ -1,5 +1,6 @@
-"""Builds libq4k_gemv.so in-tree: the gfx950 kernels + C ABI (hipcc) and the
-host Q4_K quantiser (g++), linked into one shared library."""
+"""Builds libq4k_gemv.so in-tree: the gfx950 kernels + C ABI (hipcc), the host
+Q4_K/Q6_K quantisers and the GGUF reader (g++), linked into one shared
+library."""
 from __future__ import annotations
 
 import os
@@ -58,8 +59,11 @@ def build(verbose: bool = False, save_temps: bool = False) -> str:
             raise RuntimeError(f"build step failed: {' '.join(cmd)}")
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-Wall",
           "-c", os.path.join(CSRC, "q4k_quantize_host.cpp"), "-o", host_obj], verbose)
+    gguf_obj = os.path.join(BUILD, "gguf_reader.o")
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra",
+          "-c", os.path.join(CSRC, "gguf_reader.cpp"), "-o", gguf_obj], verbose)
     tmp = LIB + ".tmp"
-    _run([hipcc, "-shared", "-fPIC", "-o", tmp, *dev_objs, host_obj, "-lpthread"], verbose)
+    _run([hipcc, "-shared", "-fPIC", "-o", tmp, *dev_objs, host_obj, gguf_obj, "-lpthread"], verbose)
     os.replace(tmp, LIB)
     # measurement aid for bench.py --stream-probe (not part of the library)
     probe_obj = os.path.join(BUILD, "stream_probe.o")

@@ -1067,7 +1067,9 @@ const char *q4k_strerror(int status) {
         case Q4K_EUNSUPPORTED: return "unsupported shape, layout or device (fall back)";
         case Q4K_EINVAL: return "invalid argument";
         case Q4K_EHIP: return "HIP runtime error";
-        case Q4K_ENOMEM: return "out of device memory";
+        case Q4K_ENOMEM: return "out of memory";
+        case Q4K_EIO: return "file could not be opened, read or mapped";
+        case Q4K_EFORMAT: return "not a valid GGUF v2/v3 file";
         default: return "unknown status";
     }
 }

@@ -44,8 +44,12 @@ typedef enum q4k_status {
      * the hipError_t.  The reference leaves launches unchecked
      * (kernels/mmvq.cu:563-584). */
     Q4K_EHIP = 3,
-    /* The stream-ordered temporary could not be allocated. */
-    Q4K_ENOMEM = 4
+    /* The stream-ordered temporary (or host memory) could not be allocated. */
+    Q4K_ENOMEM = 4,
+    /* A file could not be opened, read or mapped (GGUF reader). */
+    Q4K_EIO = 5,
+    /* A file is not a valid GGUF v2/v3 file (GGUF reader). */
+    Q4K_EFORMAT = 6
 } q4k_status;
 
 /* ggml type ids used in descriptors (values of ggml's enum ggml_type) */

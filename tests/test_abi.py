@@ -8,20 +8,24 @@ import pytest
 
 import _common
 
-HEADER = os.path.join(_common.ROOT, "include", "q4k_gemv.h")
+HEADERS = [os.path.join(_common.ROOT, "include", h) for h in sorted(os.listdir(os.path.join(_common.ROOT, "include")))
+           if h.endswith(".h")]
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(q[46]k_[A-Za-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(q[46]k_[A-Za-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_expected_entry_points():
     names = declared_functions()
     for n in ("q4k_mul_mat_vec_q", "q4k_op_mul_mat_vec_q", "q4k_ggml_mul_mat_vec_q",
               "q4k_quantize_row_q8_1", "q4k_subblock_sums", "q4k_quantize_rows_q4_K",
-              "q6k_mul_mat_vec_q", "q6k_op_mul_mat_vec_q", "q6k_group_sums", "q4k_quantize_rows_q6_K"):
+              "q6k_mul_mat_vec_q", "q6k_op_mul_mat_vec_q", "q6k_group_sums", "q4k_quantize_rows_q6_K",
+              "q4k_mul_mat_vec_q_fused", "q4k_gguf_open", "q4k_gguf_get_tensor"):
         assert n in names
 
 
