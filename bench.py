@@ -145,6 +145,86 @@ def fused_sweep(args):
         print(json.dumps(r), flush=True)
 
 
+class MoeRunner:
+    """GGML_OP_MUL_MAT_ID for one token through q4k_ggml_mul_mat_vec_q:
+    nexp expert matrices [nexp, M, K] (quantised), nused expert ids on the
+    device, activation columns ne11 (1: shared, nused: one per slot),
+    optionally the gate weight with SWIGLU fused.  The expert tensor rotates
+    over copies totalling >= 1 GiB."""
+
+    def __init__(self, Q, wq, nexp, M, K, ids, ne11, gq=None, wtype="q4_K", min_pool_bytes=1 << 30):
+        import ctypes
+        import _common
+        import torch
+        self.Q = Q
+        dev = torch.device("cuda:0")
+        gt = Q.GGML_TYPE_Q4_K if wtype == "q4_K" else Q.GGML_TYPE_Q6_K
+        bb = BLOCK_BYTES[wtype]
+        rb = K // 256 * bb
+        per = wq.nbytes * (2 if gq is not None else 1)
+        self.ncopies = max(2, math.ceil(min_pool_bytes / per))
+        w0 = torch.from_numpy(wq).to(dev)
+        self.w = [w0] + [w0.clone() for _ in range(self.ncopies - 1)]
+        self.g = None
+        if gq is not None:
+            g0 = torch.from_numpy(gq).to(dev)
+            self.g = [g0] + [g0.clone() for _ in range(self.ncopies - 1)]
+        nused = len(ids)
+        self.ids = torch.tensor(ids, dtype=torch.int32, device=dev)
+        self.x = torch.from_numpy(_common.activations(ne11, K, 0)).to(dev)
+        self.out = torch.empty((nused, M), dtype=torch.float32, device=dev)
+        self.s0 = [Q.make_tensor(gt, [K, M, nexp], [bb, rb, rb * M], t.data_ptr()) for t in self.w]
+        self.fus = []
+        if self.g is not None:
+            self.sg = [Q.make_tensor(gt, [K, M, nexp], [bb, rb, rb * M], t.data_ptr()) for t in self.g]
+            self.fus = [Q.q4k_fusion_args(None, ctypes.pointer(t), None, 2) for t in self.sg]
+        self.s1 = Q.make_tensor(0, [K, ne11, 1], [4, 4 * K, 4 * K * ne11], self.x.data_ptr())
+        self.ti = Q.make_tensor(26, [nused, 1], [4, 4 * nused], self.ids.data_ptr())
+        self.d = Q.make_tensor(0, [M, nused, 1], [4, 4 * M, 4 * M * nused], self.out.data_ptr())
+        self.fn = Q.lib().q4k_ggml_mul_mat_vec_q
+        self.i = 0
+
+    def step(self, stream):
+        import ctypes
+        k = self.i % self.ncopies
+        f = ctypes.byref(self.fus[k]) if self.fus else None
+        st = self.fn(ctypes.byref(self.s0[k]), ctypes.byref(self.s1), ctypes.byref(self.ti), ctypes.byref(self.d),
+                     f, None, 0, stream)
+        self.i += 1
+        if st != 0:
+            raise self.Q.Q4KError(st, "q4k_ggml_mul_mat_vec_q (MUL_MAT_ID)")
+
+
+# (name, experts, rows, K, ids, activation columns, weight type, fused gate)
+MOE_CASES = [
+    ("mixtral8x7b_ffn_gate_up_swiglu", 8, 14336, 4096, [2, 5], 1, "q4_K", True),
+    ("mixtral8x7b_ffn_down", 8, 4096, 14336, [2, 5], 2, "q6_K", False),
+    ("qwen3_30b_a3b_ffn_gate_up_swiglu", 128, 768, 2048, [3, 17, 40, 41, 77, 90, 100, 127], 1, "q4_K", True),
+    ("qwen3_30b_a3b_ffn_down", 128, 2048, 768, [3, 17, 40, 41, 77, 90, 100, 127], 8, "q6_K", False),
+]
+
+
+def moe_sweep(args):
+    import _common
+    import torch
+    Q = _pkg()
+    for name, nexp, M, K, ids, ne11, wt, fused in MOE_CASES:
+        quant = Q.quantize_rows_q4_K if wt == "q4_K" else Q.quantize_rows_q6_K
+        nthr = min(16, len(os.sched_getaffinity(0)))
+        wq = np.stack([quant(_common.weights(M, K, seed=e), nthreads=nthr) for e in range(nexp)])
+        gq = np.stack([quant(_common.weights(M, K, seed=1000 + e), nthreads=nthr) for e in range(nexp)]) if fused else None
+        r = MoeRunner(Q, wq, nexp, M, K, ids, ne11, gq=gq, wtype=wt)
+        t = time_gpu(r, args.steps, args.warmup)["graph_s"]
+        del r
+        torch.cuda.empty_cache()
+        nused = len(ids)
+        nbytes = nused * M * (K // 256) * BLOCK_BYTES[wt] * (2 if fused else 1) + 4 * ne11 * K + 4 * M * nused
+        print(json.dumps({"workload": name, "wtype": wt, "experts": nexp, "used": nused, "M": M, "K": K,
+                          "ncols_y": ne11, "fused_swiglu": fused, "us_per_call": round(t * 1e6, 3),
+                          "GBps": round(nbytes / t / 1e9, 1), "hbm_frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}),
+              flush=True)
+
+
 def time_gpu(runner: OpRunner, steps: int, warmup: int):
     """Returns dict with graph-launched and eager seconds per step."""
     import ctypes
@@ -288,7 +368,11 @@ def profile_mode(args):
     Q = _pkg()
     M, K, N = args.shape
     wq, x = make_inputs(Q, M, K, N, wtype=args.wtype)
-    runner = OpRunner(Q, wq, x, wtype=args.wtype)
+    if args.fused:  # gate + up with SWIGLU in one launch (one column)
+        gq, _ = make_inputs(Q, M, K, 1, seed=1, wtype=args.wtype)
+        runner = FusedRunner(Q, wq, gq, x[:1], wtype=args.wtype)
+    else:
+        runner = OpRunner(Q, wq, x, wtype=args.wtype)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for _ in range(args.warmup + args.steps):
         runner.step(s)
@@ -368,6 +452,8 @@ def main():
     ap.add_argument("--profile", action="store_true", help="plain launches only, for rocprofv3")
     ap.add_argument("--shape", type=int, nargs=3, default=[14336, 4096, 1], metavar=("M", "K", "N"))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--moe", action="store_true",
+                    help="time MUL_MAT_ID (one token) on expert-FFN shapes")
     ap.add_argument("--fused", action="store_true",
                     help="time the gate+up SWIGLU launch against two plain launches")
     ap.add_argument("--wtype", choices=sorted(BLOCK_BYTES), default="q4_K",
@@ -386,12 +472,14 @@ def main():
         stream_probe(args)
     elif args.copy_cal:
         copy_calibration(args)
-    elif args.fused:
-        fused_sweep(args)
-    elif args.sweep:
-        sweep(args)
     elif args.profile:
         profile_mode(args)
+    elif args.fused:
+        fused_sweep(args)
+    elif args.moe:
+        moe_sweep(args)
+    elif args.sweep:
+        sweep(args)
     else:
         headline(args)
 
