@@ -230,48 +230,79 @@ __device__ __forceinline__ uint32_t fastdiv(uint32_t n, const FastDiv &f) {
 }
 
 // q[k] = roundf(v[k] / d) with the correctly rounded quotient, as ggml-cuda's
-// quantize_q8_1 computes it.  y = v * rcp(d) is within 2^-15 of that
-// quotient (|v/d| <= 127 and v_rcp_f32 is 1-ulp accurate), so rint(y) is the
-// answer unless y lies within 2^-12 of a half-integer; a lane with such a
-// value (or a NaN) recomputes all its values with the exact division.  One
-// branch per lane instead of one per value.  rint(y) comes from adding
+// quantize_q8_1 computes it.  y = v * rcp(d) is within 127 (2^-23 + 2^-24) <
+// 2^-15.4 of v/d (|v/d| <= 127, v_rcp_f32 is 1-ulp accurate) and the rounded
+// quotient within 2^-17 of it, so rint(y) is the answer unless y lies within
+// 2^-15 of a half-integer; a lane with a value within 2^-14 of one (twice
+// the margin; or a NaN) recomputes all its values with the exact division.
+// One branch per lane instead of one per value.  rint(y) comes from adding
 // 1.5 * 2^23: the sum is exact in its integer part for |y| < 2^22, so its low
 // mantissa bits hold rint(y) (round-to-nearest-even, like the add itself)
 // and subtracting the constant back gives it as a float.  Contraction is off
 // so y is rounded on its own before the add.
-template <int V>
-__device__ __forceinline__ void quantize_values(const float (&v)[V], float d, float rd, int (&q)[V]) {
+template <int V, int H>
+__device__ __forceinline__ bool quantize_pack(const float (&v)[V], float d, float rd, bool exact,
+                                              uint32_t (&word)[V / 4], int (&hsum)[H]) {
 #pragma clang fp contract(off)
     constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
     bool fast = true;
 #pragma unroll
-    for (int k = 0; k < V; ++k) {
-        const float y = v[k] * rd;
-        const float m = y + kMagic;
-        q[k] = __builtin_bit_cast(int, m) - 0x4B400000;
-        fast = fast && fabsf(y - (m - kMagic)) <= 0.5f - 0x1p-12f;
-    }
-    if (!fast) {
+    for (int w = 0; w < V / 4; ++w) word[w] = 0;
 #pragma unroll
-        for (int k = 0; k < V; ++k) q[k] = (int)roundf(v[k] / d);
+    for (int h = 0; h < H; ++h) hsum[h] = 0;
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        int q;
+        if (exact) {
+            q = (int)roundf(v[k] / d);
+        } else {
+            const float y = v[k] * rd;
+            const float m = y + kMagic;
+            q = __builtin_bit_cast(int, m) - 0x4B400000;
+            fast = fast && fabsf(y - (m - kMagic)) <= 0.5f - 0x1p-14f;
+        }
+        hsum[k * H / V] += q;
+        word[k / 4] |= (uint32_t)(q & 0xff) << (8 * (k % 4));
     }
+    return fast;
+}
+
+// The q8 of one lane's V values packed four to a dword, and the sums over
+// its H halves of the block: the fast rounding, and the exact division when
+// the lane has a value near a tie.  The bytes are packed as they are
+// computed, so only the values, the packed words and the sums stay live.
+template <int V, int H>
+__device__ __forceinline__ void quantize_values(const float (&v)[V], float d, float rd,
+                                                uint32_t (&word)[V / 4], int (&hsum)[H]) {
+    if (!quantize_pack<V, H>(v, d, rd, false, word, hsum)) quantize_pack<V, H>(v, d, rd, true, word, hsum);
 }
 
 // F32 activation -> Q8_1 values with ggml-cuda's quantize_q8_1 arithmetic
 // (call site kernels/mmvq.cu:734): per 32 values d = amax/127,
 // q = amax == 0 ? 0 : roundf(x/d), and the kernel consumes half(d).
-// LPB lanes per 32-value block (8 or 4), 32/LPB values per lane: 8 lets a
+// LPB lanes per 32-value block (8 or 4), 32/LPB values per lane, consecutive
+// lanes reading consecutive 16 bytes (fewer lanes per block, each reading
+// 64-128 contiguous bytes, cut the quantisation's instructions but spread a
+// wave's loads over 4-8 times the cache lines and measured slower): 8 lets a
 // 16-wave workgroup cover a 4096-value column in one round, 4 halves the
-// per-block overhead when several columns need several rounds.  Staging is
-// split in two: issue() loads the first kPre rounds of values into
-// registers, to be called before the kernel's first weight loads (vector
-// loads complete in issue order, so values loaded after the weights would
-// wait for them); finish() quantises them into LDS and handles any further
-// rounds.  issue() loads unconditionally (lanes past the end re-read the
-// last block): with no branches around them the compiler's wait for these
-// values counts exactly the weight loads issued after them instead of
+// per-block overhead when several columns need several rounds (stage_lpb).
+// Staging is split in two: issue() loads the first kPre rounds of values
+// into registers, to be called before the kernel's first weight loads
+// (vector loads complete in issue order, so values loaded after the weights
+// would wait for them); finish() quantises them into LDS and handles any
+// further rounds.  issue() loads unconditionally (lanes past the end re-read
+// the last block): with no branches around them the compiler's wait for
+// these values counts exactly the weight loads issued after them instead of
 // waiting for all loads.
 constexpr int kPre = 4;
+__host__ __device__ constexpr int stage_lpb(int ncols) { return ncols == 1 ? 8 : 4; }
+// Blocks of 32 values the rounds issued ahead of the weight loads cover in a
+// workgroup of nt threads.
+__host__ __device__ constexpr int stage_capacity(int lpb, int nt) { return kPre * (nt / lpb); }
+// Weight slots a tile kernel issues before quantising the activation.
+__host__ __device__ constexpr int early_slots(int pro, int slots) {
+    return pro == 0 ? (slots < 2 ? slots : 2) : (pro == 2 ? slots : (pro == 3 ? 1 : 0));
+}
 
 template <int LPB>
 struct ActStage {
@@ -320,20 +351,16 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[32 / LPB], 
     const float d = div127(amax);
     const float rd = __builtin_amdgcn_rcpf(d);
     uint32_t word[V / 4];
-    int qsum = 0;
-#pragma unroll
-    for (int w = 0; w < V / 4; ++w) word[w] = 0;
+    int qsum[1];
     if (amax != 0.0f) {
-        int q[V];
-        quantize_values<V>(v, d, rd, q);
+        quantize_values<V, 1>(v, d, rd, word, qsum);
+    } else {
 #pragma unroll
-        for (int k = 0; k < V; ++k) {
-            qsum += q[k];
-            word[k / 4] |= (uint32_t)(q[k] & 0xff) << (8 * (k % 4));
-        }
+        for (int w = 0; w < V / 4; ++w) word[w] = 0;
+        qsum[0] = 0;
     }
     int hsum, fsum;
-    block_sums<LPB>(qsum, hsum, fsum);
+    block_sums<LPB>(qsum[0], hsum, fsum);
     int8_t *dst = q8s + q8_offset<LAYOUT>(c, qcol, b, e * (V / 4));
     if (V == 4) *reinterpret_cast<uint32_t *>(dst) = word[0];
     else *reinterpret_cast<uint2 *>(dst) = make_uint2(word[0], word[V / 4 - 1]);

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     if constexpr (BATCH) batch_activation(p);
     // slots loaded before quantisation
-    constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : (PRO == 2 ? S : (PRO == 3 ? 1 : 0));
+    constexpr int kEarly = early_slots(PRO, S);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float2 *dks = reinterpret_cast<float2 *>(lds + NC * p.qcol);
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     // row numbers and buffer descriptors in scalar registers
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WaveRows wr = wave_rows<WAVES>(p, wave);
-    constexpr int kLPB = NC == 1 ? 8 : 4;  // activation lanes per 32-value block
+    constexpr int kLPB = stage_lpb(NC);  // activation lanes per 32-value block
     ActStage<kLPB> xs;
     Q81Stage ys;
     if constexpr (BATCH) {
@@ -828,8 +828,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
     // weight loads before quantisation only when every activation load fits
     // the kPre staging rounds issued ahead of them
-    const int lpb = nc == 1 ? 8 : 4;  // the kernel's activation lanes per block
-    const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)kPre * g.waves * (kWave / lpb);
+    const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave);
     g.prologue = pro0_ok ? 0 : 1;
     const int opro = g_ovr_prologue.load();
     if (opro == 1 || ((opro == 0 || (opro == 2 && g.slots >= 4) || (opro == 3 && g.slots == 2 && !glu)) && pro0_ok))

@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     constexpr int R = GLU ? 2 : 1;
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     if constexpr (BATCH) batch_activation(p);
-    constexpr int kEarly = PRO == 0 ? (S < 2 ? S : 2) : 0;
+    constexpr int kEarly = early_slots(PRO, S);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     uint8_t *aux = lds + NC * p.qcol;
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     const Q6Lane ln = q6_lane(threadIdx.x & (kWave - 1));
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WaveRows wr = wave_rows<WAVES>(p, wave);
-    constexpr int kLPB = NC == 1 ? 8 : 4;
+    constexpr int kLPB = stage_lpb(NC);
     ActStage<kLPB> xs;
     Q81Stage ys;
     if constexpr (BATCH) {
@@ -354,10 +354,11 @@ struct Q6Geometry {
 // 8 waves unless the activation is long (more than 8192 values over all
 // columns: 16 waves quantise it in half the rounds) and the workgroup has 16
 // or more steps; weight loads before quantisation when the activation fits
-// the kPre staging rounds.  Measured on MI355X: with 210-byte blocks, more
+// the staging rounds issued ahead of them.  Measured on MI355X: with 210-byte blocks, more
 // weight requests in flight (16 waves x 2 groups, 27.5 MB over the chip)
 // delay the activation loads more than they hide latency.
-static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int64_t mats = 1) {
+static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int64_t mats = 1,
+                                   int fused = kFusedNone) {
     load_env_overrides();
     Q6Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
@@ -377,8 +378,7 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     g.lds = q6_tile_lds_bytes((int)K, nc, g.waves);
     g.lds_launch = g.lds;
     if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
-    const int lpb = nc == 1 ? 8 : 4;
-    const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)kPre * g.waves * (kWave / lpb);
+    const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave);
     g.prologue = pro0_ok ? 0 : 1;
     const int opro = g_ovr_prologue.load();
     if (opro == 1 || (opro == 0 && pro0_ok)) g.prologue = opro;
@@ -445,7 +445,7 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
     if (fused && ncols != 1) return Q4K_EINVAL;
     if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
     const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
-    const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats);
+    const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats, fused);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // a wave's rows are addressed with 31-bit offsets; column strides travel
     // as 32-bit kernel arguments

@@ -76,3 +76,49 @@ def test_division_by_127_identity(O):
     rcp = np.float32(1.0 / 127.0)
     a = np.random.default_rng(0).uniform(1e-3, 1e3, 100000).astype(np.float32)
     assert ((a * rcp).astype(np.float32) != a / np.float32(127)).sum() > 1000
+
+
+def _fast_round_agrees(d, xs, threshold):
+    """The in-launch quantiser's fast rounding: y = x * r with r any float
+    within one ulp of 1/d (the accuracy of v_rcp_f32), rint(y) accepted when
+    |y - rint(y)| <= threshold.  Returns the number of accepted values whose
+    rint(y) differs from ggml's roundf(x / d) (IEEE quotient)."""
+    d = np.float32(d)
+    r0 = np.float32(1.0) / d
+    bad = 0
+    q_ref = np.float32(xs / d)
+    q_ref = np.sign(q_ref) * np.floor(np.abs(q_ref) + np.float32(0.5))
+    for r in (r0, np.nextafter(r0, np.float32(0)), np.nextafter(r0, np.float32(np.inf))):
+        y = (xs * r).astype(np.float32)
+        ry = np.rint(y)
+        fast = np.abs(y - ry) <= threshold
+        bad += int(np.sum(fast & (ry != q_ref)))
+    return bad
+
+
+def _tie_adversaries(rng, d, n=4000):
+    """x whose x/d lies within a few units of 2^-20 of a half-integer."""
+    k = rng.integers(-127, 127, size=n) + 0.5
+    off = rng.integers(-64, 65, size=n) * 2.0 ** -20
+    return (np.float32(d) * (k + off)).astype(np.float32)
+
+
+def test_fast_rounding_threshold_is_safe():
+    """|y - x/d| <= 127 (2^-23 + 2^-24) < 2^-15.4 and |fl(x/d) - x/d| <= 2^-17,
+    so rint(y) = roundf(fl(x/d)) whenever y is more than 2^-15 from a
+    half-integer; the kernel accepts up to 0.5 - 2^-14 (twice that margin).
+    Checked over random and near-tie quotients with the three reciprocals a
+    one-ulp rcp can return; a threshold without the margin fails."""
+    rng = np.random.default_rng(42)
+    thr = np.float32(0.5 - 2.0 ** -14)
+    too_loose = np.float32(0.5 - 2.0 ** -19)
+    loose_bad = 0
+    for _ in range(300):
+        amax = np.float32(np.exp(rng.uniform(-40, 40)))
+        d = np.float32(amax / np.float32(127.0))
+        xs = np.concatenate([rng.uniform(-1, 1, 2000).astype(np.float32) * amax,
+                             _tie_adversaries(rng, d)]).astype(np.float32)
+        xs = xs[np.abs(xs) <= amax]
+        assert _fast_round_agrees(d, xs, thr) == 0
+        loose_bad += _fast_round_agrees(d, xs, too_loose)
+    assert loose_bad > 0
