@@ -241,21 +241,93 @@ __device__ __forceinline__ void ring_flush(const GemvParams &p, int lane, Result
     rr.n = 0;
 }
 
+// v_permlane32_swap_b32 a, b: lanes 32..63 of a trade places with lanes 0..31
+// of b; v_permlane16_swap_b32 a, b: the odd 16-lane rows of a trade places
+// with the even rows of b.  Inline assembly: clang's builtins for them keep
+// only the first of the two results.  The s_nop covers a VALU write of
+// either operand right before.
+__device__ __forceinline__ void permlane32_swap(float &a, float &b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane16_swap(float &a, float &b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// Sums of NC (2..8) lane values over the wave, reduce-scatter style: with P
+// the power of two >= NC, each lane-swap halves the values a lane holds
+// (lane bit 5, then 4, then 3 select which half it keeps), so that lane l
+// ends with the sum of value (l >> (6 - log2 P)) over the 64 lanes, and the
+// butterfly over the remaining low lane bits costs one step per bit for all
+// values together.  Every value is summed over a fixed tree, the same in
+// every workgroup and wave.
+template <int NC>
+__device__ __forceinline__ float column_sums(const float (&v)[NC], int lane) {
+    constexpr int P = NC <= 2 ? 2 : (NC <= 4 ? 4 : 8);
+    static_assert(NC >= 2 && NC <= 8, "two to eight values");
+    float u[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) u[i] = i < NC ? v[i] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < P / 2; ++i) {  // lane bit 5: lanes 0..31 keep value i, 32..63 value i + P/2
+        float a = u[i], b = u[i + P / 2];
+        permlane32_swap(a, b);
+        u[i] = a + b;
+    }
+    if constexpr (P >= 4) {
+#pragma unroll
+        for (int i = 0; i < P / 4; ++i) {  // lane bit 4: even rows keep u[i], odd rows u[i + P/4]
+            float a = u[i], b = u[i + P / 4];
+            permlane16_swap(a, b);
+            u[i] = a + b;
+        }
+    }
+    float s = u[0];
+    if constexpr (P == 8) {  // lane bit 3: the lane keeps u[bit3] and adds its partner's
+        const bool hi = (lane & 8) != 0;
+        const float keep = hi ? u[1] : u[0];
+        const float send = hi ? u[0] : u[1];
+        s = keep + dppf<kDppRor8>(send);
+    }
+    s += dppf<kDppXor1>(s);
+    s += dppf<kDppXor2>(s);
+    s += dppf<kDppHalfMirror>(s);
+    if constexpr (P <= 4) s += dppf<kDppRor8>(s);
+    if constexpr (P == 2) {  // lane bit 4: a + b = s + s(lane ^ 16) in every lane
+        float a = s, b = s;
+        permlane16_swap(a, b);
+        s = a + b;
+    }
+    return s;
+}
+
 // End of a row tile: the R x NC lane partials of the tile, reduced over the
-// wave, go to the result ring (lane r*NC + c writes entry r*NC + c).
+// wave, go to the result ring (entry r*NC + c; with one column lane r writes
+// entry r, with several the lanes of column_sums' map).
 template <int NC, int R, int EPI>
 __device__ __forceinline__ void tile_to_ring(const GemvParams &p, int lane, float (&acc)[R][NC],
                                              ResultRing &rr) {
-    float out = 0.0f;
+    if constexpr (NC == 1) {
+        float out = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const float s = wave_sum(acc[r][c]);
-            if (lane == r * NC + c) out = s;
-            acc[r][c] = 0.0f;
+        for (int r = 0; r < R; ++r) {
+            const float s = wave_sum(acc[r][0]);
+            if (lane == r) out = s;
+            acc[r][0] = 0.0f;
         }
-    if (lane < R * NC) rr.buf[rr.n + lane] = out;
+        if (lane < R) rr.buf[rr.n + lane] = out;
+    } else {
+        constexpr int P = NC <= 2 ? 2 : (NC <= 4 ? 4 : 8);
+        constexpr int kShift = P == 2 ? 5 : (P == 4 ? 4 : 3);
+        const int c = lane >> kShift;
+        const bool writer = (lane & ((1 << kShift) - 1)) == 0 && c < NC;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float s = column_sums<NC>(acc[r], lane);
+            if (writer) rr.buf[rr.n + r * NC + c] = s;
+#pragma unroll
+            for (int k = 0; k < NC; ++k) acc[r][k] = 0.0f;
+        }
+    }
     rr.n += R * NC;
     // rare (a wave's rows x NC above kRing): global stores inside the
     // loop make the compiler's load waits conservative
