@@ -44,6 +44,15 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
 
+// Signed 4 x int8 dot product starting a sum: the three-operand
+// v_dot4_i32_i8 with an inline 0 (the compiler otherwise emits v_dot4c with
+// the accumulator zeroed by a separate move).
+__device__ __forceinline__ int sdot4_first(uint32_t a, uint32_t b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
 }
@@ -123,9 +132,10 @@ __device__ __forceinline__ uint32_t unpack_scale_min(u32x4 h, const ScaleSel &s)
 // bytes, a0/a1 = the 32 q8 of sub-block 2j, b0/b1 = those of sub-block 2j+1.
 __device__ __forceinline__ void lane_qdot(u32x4 w0, u32x4 w1, u32x4 a0, u32x4 a1, u32x4 b0, u32x4 b1,
                                           int &sa, int &sb) {
-    int a = 0, b = 0;
+    int a = sdot4_first(w0[0] & 0x0f0f0f0fu, a0[0]);
+    int b = sdot4_first((w0[0] >> 4) & 0x0f0f0f0fu, b0[0]);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 1; k < 4; ++k) {
         a = __builtin_amdgcn_sdot4((int)(w0[k] & 0x0f0f0f0fu), (int)a0[k], a, false);
         b = __builtin_amdgcn_sdot4((int)((w0[k] >> 4) & 0x0f0f0f0fu), (int)b0[k], b, false);
     }
@@ -319,12 +329,31 @@ __device__ __forceinline__ float div127(float a) {
     return __builtin_fmaf(r, kRcp127, q0);
 }
 
+// max(v, v of the lane that the DPP control names), as one v_max_f32 with
+// the DPP source (through fmaxf the compiler inserts a canonicalising
+// v_max after each DPP move).  The s_nop covers a VALU write of v right
+// before.  NaN handling is v_max_f32's, as with fmaxf.
+#define Q4K_DPP_MAX(CTRL)                                                                        \
+    __device__ __forceinline__ float dpp_max_##CTRL(float v) {                                   \
+        float r;                                                                                 \
+        asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 " Q4K_DPP_##CTRL " row_mask:0xf bank_mask:0xf" \
+            : "=v"(r)                                                                            \
+            : "v"(v));                                                                           \
+        return r;                                                                                \
+    }
+#define Q4K_DPP_xor1 "quad_perm:[1,0,3,2]"
+#define Q4K_DPP_xor2 "quad_perm:[2,3,0,1]"
+#define Q4K_DPP_half_mirror "row_half_mirror"
+Q4K_DPP_MAX(xor1)
+Q4K_DPP_MAX(xor2)
+Q4K_DPP_MAX(half_mirror)
+
 // Reductions over the LPB lanes of a 32-value block (aligned lane groups).
 template <int LPB>
 __device__ __forceinline__ float block_max(float v) {
-    v = fmaxf(v, dppf<kDppXor1>(v));
-    v = fmaxf(v, dppf<kDppXor2>(v));
-    if (LPB == 8) v = fmaxf(v, dppf<kDppHalfMirror>(v));
+    v = dpp_max_xor1(v);
+    v = dpp_max_xor2(v);
+    if (LPB == 8) v = dpp_max_half_mirror(v);
     return v;
 }
 
