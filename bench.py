@@ -65,7 +65,8 @@ def make_inputs(Q, M, K, N, seed=0, wtype="q4_K"):
 
 class OpRunner:
     """Pre-resolved ctypes call of q4k_mul_mat_vec_q (q6k_mul_mat_vec_q for
-    Q6_K) over rotating weights."""
+    Q6_K) over rotating weights, with a Q8_1 workspace as ggml's pool would
+    hand it (the op uses it for several long columns)."""
 
     def __init__(self, Q, wq, x, min_pool_bytes=1 << 30, wtype="q4_K"):
         import ctypes
@@ -80,11 +81,13 @@ class OpRunner:
         self.copies = [w0] + [w0.clone() for _ in range(self.ncopies - 1)]
         self.x = torch.from_numpy(x).to(self.dev)
         self.out = torch.empty((self.N, self.M), dtype=torch.float32, device=self.dev)
+        self.ws = torch.empty(Q.q8_1_bytes(self.K, self.N), dtype=torch.uint8, device=self.dev)
         self.name = "q4k_mul_mat_vec_q" if wtype == "q4_K" else "q6k_mul_mat_vec_q"
         self.fn = getattr(Q.lib(), self.name)
         self.wptr = [ctypes.c_void_p(c.data_ptr()) for c in self.copies]
         self.args = (self.K, self.M, self.rb, ctypes.c_void_p(self.x.data_ptr()), self.N, self.K * 4,
-                     ctypes.c_void_p(self.out.data_ptr()), self.M * 4, None, 0)
+                     ctypes.c_void_p(self.out.data_ptr()), self.M * 4, ctypes.c_void_p(self.ws.data_ptr()),
+                     self.ws.numel())
         self.i = 0
 
     def step(self, stream):

@@ -1114,13 +1114,16 @@ int q4k_mul_mat_vec_q(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
     const hipStream_t s = (hipStream_t)stream;
     const Geometry geo = pick_geometry(*di, ne00, ne01, ne11);
     const int64_t ldx = nb11 / 4, ldd = nb1 / 4;
-    if (geo.nc_chunk >= ne11) {
+    const size_t need = q4k_q8_1_bytes(ne00, ne11);
+    const bool ws_fits = workspace && workspace_bytes >= need && aligned(workspace, 4);
+    if (geo.nc_chunk >= ne11 && !(ws_fits && prefer_prequantised(ne00, ne11))) {
         // quantisation inside the GEMV launch
         return run_gemv(src0, ne00, ne01, nb01, src1, ldx, nullptr, 0, ne11, dst, ldd, s);
     }
-    // activation too large for one workgroup's LDS at this column count:
-    // quantise once to a Q8_1 buffer and run the GEMV in column chunks.
-    const size_t need = q4k_q8_1_bytes(ne00, ne11);
+    // activation too large for one workgroup's LDS at this column count, or
+    // (with a workspace) too many values for every workgroup to quantise:
+    // quantise once to a Q8_1 buffer and run the GEMV on it (in column
+    // chunks when the columns do not fit the LDS together).
     void *buf = workspace;
     bool owned = false;
     if (buf) {

@@ -80,6 +80,14 @@ inline int grid_per_matrix(int cus, int64_t mats, int64_t M) {
     return g < 1 ? 1 : (int)g;
 }
 inline int64_t pad512(int64_t k) { return (k + 511) / 512 * 512; }
+// A 2-D product with a caller workspace quantises the activation in a
+// launch of its own and runs the GEMV on the Q8_1 buffer when every
+// workgroup's in-launch quantisation of all ncols x K values would cost
+// more than that launch (~2 us per call on MI355X): measured crossover
+// near 40,000 values (4096 x 14336 at 3 columns even, 4 columns 15.7 vs
+// 16.8 us, 8 columns 27.2 vs 35.5 us; 8192 x 28672 at 2 columns 32.0 vs
+// 33.2 us; 4096-value rows up to 8 columns stay in one launch).
+inline bool prefer_prequantised(int64_t K, int64_t ncols) { return K * ncols > 40960; }
 // LDS bytes of one staged q8 column in a tile layout (whole 16-block groups)
 inline int q8_col_bytes(int K) { return (K + 4095) / 4096 * 4096; }
 

@@ -12,7 +12,9 @@
  * allocates nothing on the hot path; q4k_mul_mat_vec_q only falls back to a
  * stream-ordered temporary (hipMallocAsync/hipFreeAsync, the counterpart of
  * ggml's ctx.pool()) for shapes whose activation does not fit one
- * workgroup's LDS when no workspace is passed.
+ * workgroup's LDS when no workspace is passed.  A caller with a pool (as
+ * ggml has) should pass a workspace: it also speeds up several long
+ * columns.
  *
  * Threading: entry points may be called from any host thread; per-device
  * state is initialised once under a lock.  Calls that share a stream are
@@ -135,7 +137,11 @@ int q4k_quantize_row_q8_1(const float *x, void *vy, int64_t ne00, int64_t s01, i
  * is an empty product and returns Q4K_OK).  The activation is quantised to
  * Q8_1 inside the GEMV launch when it fits one workgroup's LDS; otherwise
  * through a Q8_1 buffer: `workspace` (at least q4k_q8_1_bytes(ne00, ne11)
- * bytes, 4-B aligned) or, when NULL, a stream-ordered temporary. */
+ * bytes, 4-B aligned) or, when NULL, a stream-ordered temporary.  With a
+ * workspace of that size the buffer is also used, in a quantisation launch
+ * of its own as the reference does, when ne00 * ne11 > 40960 (several long
+ * columns, which every workgroup would otherwise quantise in full).  Both
+ * routes give the same bits. */
 int q4k_mul_mat_vec_q(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
                       const float *src1, int64_t ne11, int64_t nb11, float *dst, int64_t nb1,
                       void *workspace, size_t workspace_bytes, void *stream);

@@ -172,6 +172,33 @@ def test_strides_and_no_out_of_bounds_writes(Q, O, gpu):
     _common.assert_within_tolerance(O, out[:, :M], ref, "strided")
 
 
+@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("M,K,N", [(300, 14336, 4), (77, 28672, 2), (130, 8192, 8)])
+def test_workspace_route_for_long_columns(Q, O, gpu, wtype, M, K, N):
+    """With a workspace and K * N > 40960 the op quantises in a launch of its
+    own and runs the GEMV on the Q8_1 buffer; without one (or with one too
+    small) the GEMV quantises in-launch.  Both give the same bits, within
+    the oracle's tolerance."""
+    import torch
+    if wtype == 12:
+        wq, x = inputs(Q, M, K, N, seed=8)
+        ref = O.gemv_q4K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
+    else:
+        wq = Q.quantize_rows_q6_K(_common.weights(M, K, seed=8), nthreads=16)
+        x = _common.activations(N, K, seed=9)
+        ref = O.gemv_q6K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    need = Q.q8_1_bytes(K, N)
+    y = Q.mul_mat_vec_q(wd, K, xd, wtype=wtype).cpu().numpy()
+    _common.assert_within_tolerance(O, y, ref, f"in-launch {M}x{K} N={N}")
+    ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+    y2 = Q.mul_mat_vec_q(wd, K, xd, workspace=ws, wtype=wtype).cpu().numpy()
+    assert np.array_equal(y, y2)
+    small = torch.empty(need - 4, dtype=torch.uint8, device=gpu)
+    y3 = Q.mul_mat_vec_q(wd, K, xd, workspace=small, wtype=wtype).cpu().numpy()
+    assert np.array_equal(y, y3)
+
+
 def test_unquantised_path_for_large_activation(Q, O, gpu):
     """K=28672 with 8 columns does not fit one workgroup's LDS: the op
     quantises to a Q8_1 buffer (caller workspace or stream-ordered temporary)
