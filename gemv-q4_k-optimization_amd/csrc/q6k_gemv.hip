@@ -371,7 +371,12 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
     g.waves = steps_per_wg >= 16 && (int64_t)nc * K > 8192 ? 16 : 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;
-    g.slots = 1;
+    // One group in flight per wave, except in launches over several weight
+    // matrices (MUL_MAT_ID, broadcasting) whose waves stream four or more
+    // groups: there a second slot measured faster (Mixtral down 22.7 ->
+    // 21.9 us, 2048 x 768 x 8 experts 9.35 -> 8.2 us), while on every
+    // single-matrix shape it measured slower (1024 x 4096: 3.71 -> 4.71 us).
+    g.slots = mats > 1 && steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
     if (oslots == 1 || oslots == 2) g.slots = oslots;
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
