@@ -799,11 +799,21 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         return g;
     }
     g.grid = owgs > 0 ? owgs : grid_per_matrix(cus, mats, M);
+    // One column with rows of at most 8192 values and ~500 KB or more of
+    // weight per CU: four 8-wave workgroups per CU, all resident, keep
+    // twice the weight requests in flight of one 16-wave workgroup, which
+    // pays off once the stream is long enough to amortise the extra
+    // activation staging (measured on MI355X: 28672 x 8192 27.2 -> 25.2 us,
+    // 32768 x 8192 28.6 -> 27.5 us; 20480 x 8192 even, and slower for
+    // shorter streams, longer rows or several columns).
+    const bool four_per_cu = owgs == 0 && owaves == 0 && N == 1 && !fused && mats == 1 && K <= 8192 &&
+                             weight_bytes >= (int64_t)500000 * cus;
+    if (four_per_cu) g.grid = 4 * cus;
     // 16 waves per CU unless the product is small; two groups in flight per
     // wave once a wave has four or more to stream, else one (a second slot
     // would mostly run past the wave's rows).  Measured on MI355X.
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
-    g.waves = steps_per_wg >= 16 ? 16 : 8;
+    g.waves = steps_per_wg >= 16 && !four_per_cu ? 16 : 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;  // the instantiated sizes
     g.slots = steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
     g.R = 1;
@@ -825,7 +835,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     g.rows_extra = (int)(M % g.grid);
     g.lds = tile_lds_bytes((int)K, nc, g.waves);
     g.lds_launch = g.lds;
-    if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
+    if (owgs == 0 && !four_per_cu && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
     // weight loads before quantisation only when every activation load fits
     // the kPre staging rounds issued ahead of them
     const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave);
