@@ -459,6 +459,28 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
     }
 }
 
+// Rounds [J0, J1) of stage_f32_finish (J1 <= kPre: values already in
+// registers), for a caller that interleaves the rounds with other work.
+// With one column and NT / LPB = 128, round j is the 4096 values of
+// 16-block group j.
+template <int LAYOUT, int LPB, int NT, int J0, int J1>
+__device__ __forceinline__ void stage_f32_rounds(int K, int ncols, const FastDiv &fd, const ActStage<LPB> &st,
+                                                 int qcol, int8_t *q8s, void *aux) {
+    static_assert(0 <= J0 && J0 <= J1 && J1 <= kPre, "rounds held in registers");
+    const int nblk = K / 32;
+    const int total = ncols * nblk;
+    const int e = threadIdx.x & (LPB - 1);
+    constexpr int step = NT / LPB;
+#pragma unroll
+    for (int j = J0; j < J1; ++j) {
+        const int qb = (int)(threadIdx.x / LPB) + j * step;
+        if (qb < total) {
+            const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
+            quantize_block_part<LAYOUT, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, total, nblk, q8s, aux);
+        }
+    }
+}
+
 // Already-quantised AoS block_q8_1 (column stride stride_col_y blocks) -> LDS,
 // in the same two phases: the first kPre rounds' bytes are loaded by issue().
 struct Q81Stage {
