@@ -270,8 +270,6 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
         process_group<NC, R, EPI>(p, ln, st[1], q8s, dks, w[1], acc, rr);
         st[1] = next_step(st[0], p.G);
         load_step<R, GLU>(p, ln, ws, rs_gate, st[1], w[1]);
-        stage_f32_rounds<kLayoutQ4K, kLPB, kWave * WAVES, 2, kPre>(p.K, NC, p.nblk32, xs, p.qcol, q8s, dks);
-        __syncthreads();
         remaining -= 2;
         if (remaining <= 0) {  // no barrier below this point
             ring_flush<NC, EPI>(p, ln.lane, rr);
