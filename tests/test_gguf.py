@@ -159,3 +159,67 @@ def test_malformed_files_are_refused(Q, tmp_path, case):
 
 def test_missing_file(Q, tmp_path):
     assert open_status(Q, tmp_path / "nope.gguf") == Q.Q4K_EIO
+
+
+def _read_everything(Q, path):
+    """Opens the file and walks every accessor; returns the open status."""
+    import ctypes
+    L = Q.lib()
+    h = ctypes.c_void_p()
+    st = L.q4k_gguf_open(str(path).encode(), ctypes.byref(h))
+    if st != 0:
+        return st
+    try:
+        for i in range(L.q4k_gguf_kv_count(h)):
+            L.q4k_gguf_key(h, i)
+            t = L.q4k_gguf_kv_type(h, i)
+            iv, fv, sv = ctypes.c_int64(), ctypes.c_double(), ctypes.c_char_p()
+            L.q4k_gguf_get_int(h, i, ctypes.byref(iv))
+            L.q4k_gguf_get_float(h, i, ctypes.byref(fv))
+            L.q4k_gguf_get_str(h, i, ctypes.byref(sv))
+            if t == W.ARRAY:
+                et, n, data = ctypes.c_int32(), ctypes.c_int64(), ctypes.c_void_p()
+                assert L.q4k_gguf_get_arr(h, i, ctypes.byref(et), ctypes.byref(n), ctypes.byref(data)) == 0
+                if et.value == W.STRING:
+                    for j in range(min(n.value, 64)):
+                        assert L.q4k_gguf_get_arr_str(h, i, j, ctypes.byref(sv)) == 0
+        info = Q.q4k_gguf_tensor_info()
+        for i in range(L.q4k_gguf_tensor_count(h)):
+            assert L.q4k_gguf_get_tensor(h, i, ctypes.byref(info)) == 0
+            if info.nbytes:   # the mapped data is readable to its last byte
+                ctypes.string_at(info.data, 1)
+                ctypes.string_at(info.data + info.nbytes - 1, 1)
+    finally:
+        L.q4k_gguf_close(h)
+    return 0
+
+
+def test_mutated_files_never_crash(Q, tmp_path):
+    """Seeded byte-level corruption of a valid file (flips, overwrites with
+    extreme values, insertions, deletions): every open either succeeds, and
+    then every accessor and the mapped tensor bytes stay readable, or is
+    refused with Q4K_EFORMAT."""
+    raw = bytearray(_small_file())
+    rng = np.random.default_rng(1234)
+    p = tmp_path / "m.gguf"
+    opened = 0
+    for trial in range(3000):
+        b = bytearray(raw)
+        for _ in range(int(rng.integers(1, 6))):
+            kind = int(rng.integers(0, 4))
+            pos = int(rng.integers(0, len(b)))
+            if kind == 0:
+                b[pos] ^= 1 << int(rng.integers(0, 8))
+            elif kind == 1:
+                v = [0x00, 0xFF, 0x7F, 0x80][int(rng.integers(0, 4))]
+                for k in range(pos, min(len(b), pos + int(rng.integers(1, 9)))):
+                    b[k] = v
+            elif kind == 2:
+                b[pos:pos] = bytes(rng.integers(0, 256, int(rng.integers(1, 9)), dtype=np.uint8))
+            elif len(b) > 8:
+                del b[pos:pos + int(rng.integers(1, 9))]
+        p.write_bytes(bytes(b))
+        st = _read_everything(Q, p)
+        assert st in (0, Q.Q4K_EFORMAT), (trial, st)
+        opened += st == 0
+    assert 0 < opened < 3000   # both outcomes occur
