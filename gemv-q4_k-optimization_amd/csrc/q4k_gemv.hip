@@ -121,6 +121,32 @@ __device__ __forceinline__ LaneAct lane_act(const GemvParams &p, const Lane &ln,
     return a;
 }
 
+// The lane's scale and min fields of one row's block (sub-blocks 2j, 2j+1)
+// and the block's d and dmin.
+struct RowScales {
+    int sca, scb;
+    float maf, mbf, d, dmin;
+};
+
+__device__ __forceinline__ RowScales row_scales(const RowRegs &w, const Lane &ln) {
+    const uint32_t scm = unpack_scale_min(w.h, ln.sel);
+    return RowScales{(int)(scm & 0xffu), (int)((scm >> 8) & 0xffu), (float)((scm >> 16) & 0xffu),
+                     (float)(scm >> 24), half_bits_to_float(w.h[0]), half_bits_to_float(w.h[0] >> 16)};
+}
+
+// acc += the lane's share of one row's block times one activation column.
+__device__ __forceinline__ void accumulate(const RowRegs &w, const RowScales &s, const LaneAct &a, float &acc) {
+    int sa, sb;
+    lane_qdot(w.q0, w.q1, a.a0, a.a1, a.b0, a.b1, sa, sb);
+    // |sa|, |sb| <= 32*15*127 and sc <= 63: 24-bit products are exact.
+    // Explicit fmas: every kernel variant rounds identically, so the result
+    // does not depend on the launch geometry.
+    const float xs = __builtin_fmaf(a.dk.x, (float)__mul24(sa, s.sca), a.dk.z * (float)__mul24(sb, s.scb));
+    const float ms = __builtin_fmaf(a.dk.y, s.maf, a.dk.w * s.mbf);
+    acc = fmaf(s.d, xs, acc);
+    acc = fmaf(-s.dmin, ms, acc);
+}
+
 // Consumes one group (16 super-blocks of R rows) held in w; on the last group
 // of a tile reduces the R x NC sums over the wave into the result ring.
 template <int NC, int R, int EPI>
@@ -128,35 +154,26 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
                                               const int8_t *q8s, const float2 *dks,
                                               const RowRegs (&w)[R], float (&acc)[R][NC],
                                               ResultRing &rr) {
-    int sca[R], scb[R];
-    float maf[R], mbf[R], d[R], dmin[R];
+    RowScales sc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t scm = unpack_scale_min(w[r].h, ln.sel);
-        sca[r] = (int)(scm & 0xffu);
-        scb[r] = (int)((scm >> 8) & 0xffu);
-        maf[r] = (float)((scm >> 16) & 0xffu);
-        mbf[r] = (float)(scm >> 24);
-        d[r] = half_bits_to_float(w[r].h[0]);
-        dmin[r] = half_bits_to_float(w[r].h[0] >> 16);
-    }
+    for (int r = 0; r < R; ++r) sc[r] = row_scales(w[r], ln);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const LaneAct a = lane_act(p, ln, st.i, c, q8s, dks);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            int sa, sb;
-            lane_qdot(w[r].q0, w[r].q1, a.a0, a.a1, a.b0, a.b1, sa, sb);
-            // |sa|, |sb| <= 32*15*127 and sc <= 63: 24-bit products are exact.
-            // Explicit fmas: every kernel variant rounds identically, so the
-            // result does not depend on the launch geometry.
-            const float xs = __builtin_fmaf(a.dk.x, (float)__mul24(sa, sca[r]), a.dk.z * (float)__mul24(sb, scb[r]));
-            const float ms = __builtin_fmaf(a.dk.y, maf[r], a.dk.w * mbf[r]);
-            acc[r][c] = fmaf(d[r], xs, acc[r][c]);
-            acc[r][c] = fmaf(-dmin[r], ms, acc[r][c]);
-        }
+        for (int r = 0; r < R; ++r) accumulate(w[r], sc[r], a, acc[r][c]);
     }
     if (st.i == p.G - 1) tile_to_ring<NC, R, EPI>(p, ln.lane, acc, rr);
+}
+
+// The same for one column whose rows are one group long, with the lane's
+// activation slice (the same in every step) held in registers.
+template <int R, int EPI>
+__device__ __forceinline__ void process_row_tile(const GemvParams &p, const Lane &ln, const LaneAct &a,
+                                                 const RowRegs (&w)[R], float (&acc)[R][1], ResultRing &rr) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) accumulate(w[r], row_scales(w[r], ln), a, acc[r][0]);
+    tile_to_ring<1, R, EPI>(p, ln.lane, acc, rr);
 }
 
 // Tile kernel: any K, 1..8 columns.  One workgroup per CU (the launch asks
@@ -288,6 +305,23 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     // flight.  Steps go S at a time with one exit test; a count that is not a
     // multiple of S ends with steps past the wave's rows, whose zeros add
     // nothing and whose results the final flush drops.
+    if constexpr (NC == 1 && R == 1 && S <= 2) {  // (wider variants would spill registers)
+        if (p.G == 1) {  // every step reads the same activation slice: keep it in registers
+            const LaneAct a0 = lane_act(p, ln, 0, 0, q8s, dks);
+            for (;;) {
+#pragma unroll
+                for (int k = 0; k < S; ++k) {
+                    process_row_tile<R, EPI>(p, ln, a0, w[k], acc, rr);
+                    st[k] = next_step(st[(k + S - 1) % S], p.G);
+                    load_step<R, GLU>(p, ln, ws, rs_gate, st[k], w[k]);
+                }
+                remaining -= S;
+                if (remaining <= 0) break;
+            }
+            ring_flush<NC, EPI>(p, ln.lane, rr);
+            return;
+        }
+    }
     for (;;) {
 #pragma unroll
         for (int k = 0; k < S; ++k) {
