@@ -166,14 +166,18 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
     if (st.i == p.G - 1) tile_to_ring<NC, R, EPI>(p, ln.lane, acc, rr);
 }
 
-// The same for one column whose rows are one group long, with the lane's
-// activation slice (the same in every step) held in registers.
-template <int R, int EPI>
-__device__ __forceinline__ void process_row_tile(const GemvParams &p, const Lane &ln, const LaneAct &a,
-                                                 const RowRegs (&w)[R], float (&acc)[R][1], ResultRing &rr) {
+// The same for up to two columns whose rows are one group long, with the
+// lane's activation slices (the same in every step) held in registers.
+template <int NC, int R, int EPI>
+__device__ __forceinline__ void process_row_tile(const GemvParams &p, const Lane &ln, const LaneAct (&a)[NC],
+                                                 const RowRegs (&w)[R], float (&acc)[R][NC], ResultRing &rr) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) accumulate(w[r], row_scales(w[r], ln), a, acc[r][0]);
-    tile_to_ring<1, R, EPI>(p, ln.lane, acc, rr);
+    for (int r = 0; r < R; ++r) {
+        const RowScales sc = row_scales(w[r], ln);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) accumulate(w[r], sc, a[c], acc[r][c]);
+    }
+    tile_to_ring<NC, R, EPI>(p, ln.lane, acc, rr);
 }
 
 // Tile kernel: any K, 1..8 columns.  One workgroup per CU (the launch asks
@@ -305,13 +309,15 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     // flight.  Steps go S at a time with one exit test; a count that is not a
     // multiple of S ends with steps past the wave's rows, whose zeros add
     // nothing and whose results the final flush drops.
-    if constexpr (NC == 1 && R == 1 && S <= 2) {  // (wider variants would spill registers)
+    if constexpr (NC <= 2 && R == 1 && S <= 2) {  // (wider variants would spill registers)
         if (p.G == 1) {  // every step reads the same activation slice: keep it in registers
-            const LaneAct a0 = lane_act(p, ln, 0, 0, q8s, dks);
+            LaneAct a0[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) a0[c] = lane_act(p, ln, 0, c, q8s, dks);
             for (;;) {
 #pragma unroll
                 for (int k = 0; k < S; ++k) {
-                    process_row_tile<R, EPI>(p, ln, a0, w[k], acc, rr);
+                    process_row_tile<NC, R, EPI>(p, ln, a0, w[k], acc, rr);
                     st[k] = next_step(st[(k + S - 1) % S], p.G);
                     load_step<R, GLU>(p, ln, ws, rs_gate, st[k], w[k]);
                 }

@@ -199,6 +199,26 @@ __device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6La
     if (st.i == p.G - 1) tile_to_ring<NC, R, EPI>(p, ln.lane, acc, rr);
 }
 
+// One column whose rows are one group long: q6_process_group with the
+// lane's activation slice (the same in every step) held in registers.
+template <int EPI>
+__device__ __forceinline__ void q6_process_reg(const GemvParams &p, const Q6Lane &ln, const Q6Act &a,
+                                               const Q6Regs (&w)[1], float (&acc)[1][1], ResultRing &rr) {
+    uint32_t v[4][4];
+    int sc[4];
+    q6_values(w[0], v);
+    q6_scales(w[0], ln.jp, sc);
+    const float d = half_bits_to_float(w[0].dw >> 16);
+    int s[4];
+    q6_lane_sums(v, a, s);
+    float f = a.d8.x * (float)__mul24(s[0], sc[0]);
+    f = __builtin_fmaf(a.d8.y, (float)__mul24(s[1], sc[1]), f);
+    f = __builtin_fmaf(a.d8.z, (float)__mul24(s[2], sc[2]), f);
+    f = __builtin_fmaf(a.d8.w, (float)__mul24(s[3], sc[3]), f);
+    acc[0][0] = __builtin_fmaf(d, f, acc[0][0]);
+    tile_to_ring<1, 1, EPI>(p, ln.lane, acc, rr);
+}
+
 // Tile kernel: any K, 1..8 columns; one row per tile.  The structure of the
 // Q4_K tile kernel: one workgroup per CU, activation loads first, then the
 // barrier, the early weight slots (PRO 0: min(S, 2) slots before the
@@ -270,6 +290,23 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
     ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * kRing, wr.beg, wr.end, 0, 0};
 
+    if constexpr (NC == 1 && R == 1 && S <= 2) {  // (wider variants would spill registers)
+        if (p.G == 1) {  // every step reads the same activation slice: keep it in registers
+            const Q6Act a0 = q6_act(p, ln, 0, 0, NC, q8s, aux);
+            for (;;) {
+#pragma unroll
+                for (int k = 0; k < S; ++k) {
+                    q6_process_reg<EPI>(p, ln, a0, w[k], acc, rr);
+                    st[k] = next_step(st[(k + S - 1) % S], p.G);
+                    q6_load_step<R>(p, ln, ws, st[k], w[k]);
+                }
+                remaining -= S;
+                if (remaining <= 0) break;
+            }
+            ring_flush<NC, EPI>(p, ln.lane, rr);
+            return;
+        }
+    }
     for (;;) {
 #pragma unroll
         for (int k = 0; k < S; ++k) {
