@@ -119,7 +119,7 @@ def lib():
     if _lib is None:
         import torch  # noqa: F401  -- bind to torch's HIP runtime
         if not os.path.exists(LIB_PATH):
-            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with gemv-q4_k-optimization_amd/build.py")
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             f = getattr(L, name)

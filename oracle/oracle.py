@@ -1,7 +1,7 @@
 """numpy bindings of the CPU oracle (oracle/q4k_oracle.c, oracle/q6k_oracle.c).
 
-TEST INFRASTRUCTURE ONLY: the checker for the HIP product path and the CPU
-baseline the benchmark times beside it.  Only tests/, the smoke entry point and
+TEST INFRASTRUCTURE ONLY: the oracle the tests compare the HIP product path
+against, and the CPU baseline the benchmark times beside it.  Only tests/, the smoke entry point and
 the benchmark's CPU-baseline leg may import this module.
 """
 from __future__ import annotations

@@ -1,8 +1,8 @@
 /*
  * q4k_oracle.c -- CPU restatement of the Q4_K x Q8 arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY.  This is the checker for the HIP product path and
- * the CPU baseline that the benchmark times beside it.  Only tests/, the smoke
+ * TEST INFRASTRUCTURE ONLY.  This is the oracle the tests compare the HIP
+ * product path against, and the CPU baseline that the benchmark times beside it.  Only tests/, the smoke
  * entry point and the benchmark's CPU-baseline leg may load it; the product
  * library never links, loads or calls anything in this file.
  *

@@ -1,7 +1,7 @@
 /*
  * q6k_oracle.c -- CPU restatement of the Q6_K x Q8_1 arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY.  This is the checker for the HIP Q6_K path.  Only
+ * TEST INFRASTRUCTURE ONLY.  The oracle for the HIP Q6_K path.  Only
  * tests/, the smoke entry point and the benchmark's CPU-baseline leg may load
  * it; the product library never links, loads or calls anything in this file.
  *
