@@ -287,8 +287,14 @@ def cpu_baseline(wq, x, target_s=12.0):
     isa = "avx2" if O.lib().orc_cpu_has_avx2() else "scalar"
     med = float(np.median(t))
     M, N = wq.shape[0], x.shape[0]
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            model = next((ln.split(":", 1)[1].strip() for ln in fh if ln.startswith("model name")), model)
+    except OSError:
+        pass
     return {"value": algorithmic_bytes(M, K, N) / med / 1e9, "unit": "GB/s", "cores": cores,
-            "kind": "port", "us_per_call": med * 1e6,
+            "kind": "port", "us_per_call": med * 1e6, "cpu_model": model, "isa": isa,
             "sample": f"{reps} calls of the full {M}x{K} N={N} product (Q8_K quantisation + "
                       f"vec_dot_q4_K_q8_K, {isa}, {cores} threads, row chunks of 16), "
                       f"{float(np.sum(t)):.1f} s total, median reported"}
