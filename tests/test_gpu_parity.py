@@ -315,3 +315,41 @@ def test_workload_parity(Q, O, gpu, M, K, N):
         both = np.concatenate([top, bot], axis=1)
         _common.assert_within_tolerance(O, both[:, rows], ref, f"split {M}x{K} N={N}")
     assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("M", [8192, 14336])
+def test_two_group_rows_streamed_prologue(Q, O, gpu, M):
+    """Rows of two 4096-value groups with 16 waves and two slots per wave:
+    the one-column launch consumes its first steps between the quantisation
+    rounds.  Checked against the oracle on a row sample, bit for bit against
+    the pre-quantised launch (which stages the whole activation first), and
+    with the bias epilogue (same rows, bias added)."""
+    import torch
+    K = 8192
+    geo = Q.geometry(K, M, 1)
+    assert geo["kernel"] == 1 and geo["waves_per_wg"] == 16 and geo["workgroups"] <= 256, geo
+    wq, x = inputs(Q, M, K, 1, seed=9)
+    q8 = O.quantize_q8_1(x)
+    rng = np.random.default_rng(M)
+    rows = np.unique(np.concatenate([[0, 1, 31, 32, M - 2, M - 1], rng.choice(M, 250, replace=False)]))
+    ref = oracle_rows(O, wq, K, q8, rows)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    _common.assert_within_tolerance(O, y[:, rows], ref, f"{M}x{K} streamed")
+    y2 = Q.op_mul_mat_vec_q(wd, K, to_dev(q8, gpu), 1).cpu().numpy()
+    assert np.array_equal(y, y2)
+    b = rng.standard_normal(M).astype(np.float32)
+    yb = Q.mul_mat_vec_q_fused(wd, K, xd, x_bias=to_dev(b, gpu)).cpu().numpy()[0]
+    assert np.array_equal(yb, y[0] + b)
+    # the same rows as two broadcast channels of one batched launch
+    x2 = np.concatenate([x, x[:, ::-1].copy()])
+    s0 = Q.make_tensor(12, [K, M, 1, 1], [144, wq.shape[1], wq.shape[1] * M, wq.shape[1] * M], wd.data_ptr())
+    xd2 = to_dev(x2, gpu)
+    s1 = Q.make_tensor(0, [K, 1, 2, 1], [4, 4 * K, 4 * K, 8 * K], xd2.data_ptr())
+    dst = torch.empty((2, M), dtype=torch.float32, device=gpu)
+    d = Q.make_tensor(0, [M, 1, 2, 1], [4, 4 * M, 4 * M, 8 * M], dst.data_ptr())
+    assert Q.ggml_mul_mat_vec_q(s0, s1, d) == Q.Q4K_OK
+    out = dst.cpu().numpy()
+    assert np.array_equal(out[0], y[0])
+    ref2 = oracle_rows(O, wq, K, O.quantize_q8_1(x2[1:2]), rows)
+    _common.assert_within_tolerance(O, out[1:2, rows], ref2, f"{M}x{K} channel 1")
