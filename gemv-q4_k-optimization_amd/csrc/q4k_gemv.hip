@@ -1154,7 +1154,8 @@ const char *q4k_strerror(int status) {
 int32_t q4k_last_hip_error(void) { return g_last_hip_error; }
 
 size_t q4k_q8_1_bytes(int64_t ne10, int64_t ne11) {
-    if (ne10 < 0 || ne11 < 0) return 0;
+    // 0 also for sizes whose byte count would not fit 63 bits
+    if (ne10 < 0 || ne11 < 0 || ne10 > ((int64_t)1 << 40) || ne11 > ((int64_t)1 << 16)) return 0;
     return (size_t)(ne11 * (pad512(ne10) / 32) * kQ81Bytes);
 }
 
@@ -1163,6 +1164,7 @@ int q4k_quantize_row_q8_1(const float *x, void *vy, int64_t ne00, int64_t s01, i
     if (ne00 < 0 || ne1 < 0 || ne0 < ne00 || ne0 % 32 != 0) return Q4K_EINVAL;
     if (ne0 == 0 || ne1 == 0) return Q4K_OK;
     if (!x || !vy || (ne1 > 1 && s01 < ne00) || ne1 > 65535) return Q4K_EINVAL;
+    if (ne0 > ((int64_t)1 << 38)) return Q4K_EUNSUPPORTED;  // grid.x = ne0 / 256 < 2^31
     if (!aligned(vy, 4)) return Q4K_EINVAL;
     DeviceInfo *di = nullptr;
     int st = device_info(&di);

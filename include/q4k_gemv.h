@@ -111,7 +111,8 @@ int32_t q4k_last_hip_error(void);
 
 /* Bytes of the Q8_1 activation buffer for ne11 columns of ne10 values:
  * ne11 * pad(ne10, 512) / 32 * 36.  Same size as the reference's pool
- * allocation (kernels/mmvq.cu:728-729). */
+ * allocation (kernels/mmvq.cu:728-729).  0 for negative sizes and for
+ * ne10 > 2^40 or ne11 > 2^16, whose byte count could overflow. */
 size_t q4k_q8_1_bytes(int64_t ne10, int64_t ne11);
 
 /* ------------------------------------------------------------ entry points */

@@ -43,6 +43,12 @@ def test_misc_entry_points(Q):
     assert L.q4k_q8_1_bytes(4096, 1) == 4096 // 32 * 36
     assert L.q4k_q8_1_bytes(4100, 2) == 2 * 4608 // 32 * 36
     assert L.q4k_q8_1_bytes(14336, 8) == 8 * 14336 // 32 * 36
+    # sizes whose byte count could overflow report 0, as negative ones do
+    assert L.q4k_q8_1_bytes(-1, 1) == 0
+    assert L.q4k_q8_1_bytes(1 << 62, 1) == 0
+    assert L.q4k_q8_1_bytes(4096, 1 << 40) == 0
+    # a quantiser grid beyond 2^31 workgroups is refused before any HIP call
+    assert L.q4k_quantize_row_q8_1(FAKE, FAKE, 4096, 4096, 1 << 40, 1, None) == Q.Q4K_EUNSUPPORTED
 
 
 FAKE = ctypes.c_void_p(0x10000)     # never dereferenced by the host checks
