@@ -296,7 +296,7 @@ __device__ __forceinline__ void quantize_values(const float (&v)[V], float d, fl
 // wave's loads over 4-8 times the cache lines and measured slower): 8 lets a
 // 16-wave workgroup cover a 4096-value column in one round, 4 halves the
 // per-block overhead when several columns need several rounds (stage_lpb).
-// Staging is split in two: issue() loads the first kPre rounds of values
+// Staging is split in two: issue() loads the first PRE rounds of values
 // into registers, to be called before the kernel's first weight loads
 // (vector loads complete in issue order, so values loaded after the weights
 // would wait for them); finish() quantises them into LDS and handles any
@@ -304,19 +304,25 @@ __device__ __forceinline__ void quantize_values(const float (&v)[V], float d, fl
 // the last block): with no branches around them the compiler's wait for
 // these values counts exactly the weight loads issued after them instead of
 // waiting for all loads.
-constexpr int kPre = 4;
+// PRE is 4, or, for workgroups of fewer than 1024 threads staging three or
+// more columns, the rounds that 4096-value columns take (a round left to
+// finish() waits for its loads behind the weight stream; a round past the
+// values re-reads the last block, which measured slower too).
+__host__ __device__ constexpr int pre_rounds(int ncols, int nt) { return nt >= 1024 || ncols <= 2 ? 4 : ncols; }
 __host__ __device__ constexpr int stage_lpb(int ncols) { return ncols == 1 ? 8 : 4; }
 // Blocks of 32 values the rounds issued ahead of the weight loads cover in a
 // workgroup of nt threads.
-__host__ __device__ constexpr int stage_capacity(int lpb, int nt) { return kPre * (nt / lpb); }
+__host__ __device__ constexpr int stage_capacity(int lpb, int nt, int ncols) {
+    return pre_rounds(ncols, nt) * (nt / lpb);
+}
 // Weight slots a tile kernel issues before quantising the activation.
 __host__ __device__ constexpr int early_slots(int pro, int slots) {
     return pro == 0 ? (slots < 2 ? slots : 2) : (pro == 2 ? slots : (pro == 3 ? 1 : 0));
 }
 
-template <int LPB>
+template <int LPB, int PRE>
 struct ActStage {
-    float v[kPre][32 / LPB];
+    float v[PRE][32 / LPB];
 };
 
 // amax / 127 rounded to nearest, as the IEEE division: the product with
@@ -414,17 +420,18 @@ __device__ __forceinline__ void load_xv(const float *src, bool vec_ok, float (&v
 // NT: threads per workgroup, a compile-time constant of every kernel (reading
 // blockDim would put a dependent kernel-argument load ahead of the first
 // activation load).
-template <int LPB, int NT>
+template <int LPB, int NT, int PRE>
 __device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int64_t ldx, int K,
                                                 int ncols, bool vec_ok, const FastDiv &fd,
-                                                ActStage<LPB> &st) {
+                                                ActStage<LPB, PRE> &st) {
     constexpr int V = 32 / LPB;
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int e = threadIdx.x & (LPB - 1);
     constexpr int step = NT / LPB;
 #pragma unroll
-    for (int j = 0; j < kPre; ++j) {
+    for (int j = 0; j < PRE; ++j) {
+        if (j >= 4 && j * step >= total) break;  // uniform: rounds past the values are not loaded
         const int qb = min((int)(threadIdx.x / LPB) + j * step, total - 1);
         const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
         const int b = qb - c * nblk;
@@ -432,10 +439,10 @@ __device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int
     }
 }
 
-template <int LAYOUT, int LPB, int NT>
+template <int LAYOUT, int LPB, int NT, int PRE>
 __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, int64_t ldx, int K,
                                                  int ncols, bool vec_ok, const FastDiv &fd,
-                                                 const ActStage<LPB> &st, int qcol, int8_t *q8s,
+                                                 const ActStage<LPB, PRE> &st, int qcol, int8_t *q8s,
                                                  void *aux) {
     constexpr int V = 32 / LPB;
     const int nblk = K / 32;
@@ -443,14 +450,14 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
     const int e = threadIdx.x & (LPB - 1);
     constexpr int step = NT / LPB;
 #pragma unroll
-    for (int j = 0; j < kPre; ++j) {
+    for (int j = 0; j < PRE; ++j) {
         const int qb = (int)(threadIdx.x / LPB) + j * step;
         if (qb < total) {
             const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
             quantize_block_part<LAYOUT, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, total, nblk, q8s, aux);
         }
     }
-    for (int qb = (int)(threadIdx.x / LPB) + kPre * step; qb < total; qb += step) {
+    for (int qb = (int)(threadIdx.x / LPB) + PRE * step; qb < total; qb += step) {
         const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
         const int b = qb - c * nblk;
         float v[V];
@@ -459,14 +466,14 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
     }
 }
 
-// Rounds [J0, J1) of stage_f32_finish (J1 <= kPre: values already in
+// Rounds [J0, J1) of stage_f32_finish (J1 <= PRE: values already in
 // registers), for a caller that interleaves the rounds with other work.
 // With one column and NT / LPB = 128, round j is the 4096 values of
 // 16-block group j.
-template <int LAYOUT, int LPB, int NT, int J0, int J1>
-__device__ __forceinline__ void stage_f32_rounds(int K, int ncols, const FastDiv &fd, const ActStage<LPB> &st,
+template <int LAYOUT, int LPB, int NT, int J0, int J1, int PRE>
+__device__ __forceinline__ void stage_f32_rounds(int K, int ncols, const FastDiv &fd, const ActStage<LPB, PRE> &st,
                                                  int qcol, int8_t *q8s, void *aux) {
-    static_assert(0 <= J0 && J0 <= J1 && J1 <= kPre, "rounds held in registers");
+    static_assert(0 <= J0 && J0 <= J1 && J1 <= PRE, "rounds held in registers");
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int e = threadIdx.x & (LPB - 1);
@@ -482,21 +489,23 @@ __device__ __forceinline__ void stage_f32_rounds(int K, int ncols, const FastDiv
 }
 
 // Already-quantised AoS block_q8_1 (column stride stride_col_y blocks) -> LDS,
-// in the same two phases: the first kPre rounds' bytes are loaded by issue().
+// in the same two phases: the first PRE rounds' bytes are loaded by issue().
+template <int PRE>
 struct Q81Stage {
-    uint32_t w[kPre][2];
-    uint32_t ds[kPre];
+    uint32_t w[PRE][2];
+    uint32_t ds[PRE];
 };
 
-template <int NT>
+template <int NT, int PRE>
 __device__ __forceinline__ void stage_q81_issue(const uint8_t *__restrict__ y, int64_t stride_col_y,
-                                                int K, int ncols, const FastDiv &fd, Q81Stage &st) {
+                                                int K, int ncols, const FastDiv &fd, Q81Stage<PRE> &st) {
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int quarter = threadIdx.x & 3;
     constexpr int step = NT / 4;
 #pragma unroll
-    for (int j = 0; j < kPre; ++j) {
+    for (int j = 0; j < PRE; ++j) {
+        if (j >= 4 && j * step >= total) break;  // uniform, as above
         const int qb = min((int)(threadIdx.x >> 2) + j * step, total - 1);  // unconditional, as above
         const int c = (int)fastdiv((uint32_t)qb, fd);
         const uint8_t *blk = y + ((int64_t)c * stride_col_y + (qb - c * nblk)) * kQ81Bytes;
@@ -519,17 +528,17 @@ __device__ __forceinline__ void store_q81_part(uint32_t w0, uint32_t w1, uint32_
         store_aux<LAYOUT>(aux, total, nblk, c, b, qb, quarter >> 1, half_bits_to_float(ds), fsum, hsum);
 }
 
-template <int LAYOUT, int NT>
+template <int LAYOUT, int NT, int PRE>
 __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                  int K, int ncols, const FastDiv &fd,
-                                                 const Q81Stage &st, int qcol, int8_t *q8s,
+                                                 const Q81Stage<PRE> &st, int qcol, int8_t *q8s,
                                                  void *aux) {
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int quarter = threadIdx.x & 3;
     constexpr int step = NT / 4;
 #pragma unroll
-    for (int j = 0; j < kPre; ++j) {
+    for (int j = 0; j < PRE; ++j) {
         const int qb = (threadIdx.x >> 2) + j * step;
         if (qb < total) {
             const int c = (int)fastdiv((uint32_t)qb, fd);
@@ -537,7 +546,7 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
                                    total, nblk, q8s, aux);
         }
     }
-    for (int qb = (threadIdx.x >> 2) + kPre * step; qb < total; qb += step) {
+    for (int qb = (threadIdx.x >> 2) + PRE * step; qb < total; qb += step) {
         const int c = (int)fastdiv((uint32_t)qb, fd);
         const int b = qb - c * nblk;
         const uint8_t *blk = y + ((int64_t)c * stride_col_y + b) * kQ81Bytes;
@@ -553,7 +562,7 @@ template <int LAYOUT, int NT>
 __device__ __forceinline__ void stage_from_q8_1(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                 int K, int ncols, const FastDiv &fd, int qcol,
                                                 int8_t *q8s, void *aux) {
-    Q81Stage st;
+    Q81Stage<4> st;
     stage_q81_issue<NT>(y, stride_col_y, K, ncols, fd, st);
     stage_q81_finish<LAYOUT, NT>(y, stride_col_y, K, ncols, fd, st, qcol, q8s, aux);
 }

@@ -166,7 +166,7 @@ __device__ __forceinline__ void process_group(const GemvParams &p, const Lane &l
     if (st.i == p.G - 1) tile_to_ring<NC, R, EPI>(p, ln.lane, acc, rr);
 }
 
-// The same for up to two columns whose rows are one group long, with the
+// The same for rows that are one group long, with the
 // lane's activation slices (the same in every step) held in registers.
 template <int NC, int R, int EPI>
 __device__ __forceinline__ void process_row_tile(const GemvParams &p, const Lane &ln, const LaneAct (&a)[NC],
@@ -188,7 +188,7 @@ __device__ __forceinline__ void process_row_tile(const GemvParams &p, const Lane
 // issued: a CU serves vector memory requests in order, so an activation load
 // queued behind the weight stream would stall the whole workgroup's
 // prologue.  PRO selects when the weight loads start: 0 -- the first two
-// slots before the activation is quantised (it needs at most kPre staging
+// slots before the activation is quantised (it needs at most PRE staging
 // rounds, so no activation load is issued after them) and the rest after,
 // 1 -- all after, 2 -- all before, 3 -- one slot before.  Weight requests issued early overlap the quantisation
 // but queue in the memory system ahead of other CUs' activation loads, so
@@ -235,8 +235,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WaveRows wr = wave_rows<WAVES>(p, wave);
     constexpr int kLPB = stage_lpb(NC);  // activation lanes per 32-value block
-    ActStage<kLPB> xs;
-    Q81Stage ys;
+    constexpr int kPreR = pre_rounds(NC, kWave * WAVES);
+    ActStage<kLPB, kPreR> xs;
+    Q81Stage<kPreR> ys;
     if constexpr (BATCH) {
         if (p.x) stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
         else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
@@ -309,7 +310,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     // flight.  Steps go S at a time with one exit test; a count that is not a
     // multiple of S ends with steps past the wave's rows, whose zeros add
     // nothing and whose results the final flush drops.
-    if constexpr (NC <= 2 && R == 1 && S <= 2) {  // (wider variants would spill registers)
+    // (up to two columns at 16 waves, eight at 8 waves: wider variants would
+    // spill registers)
+    if constexpr ((NC <= 2 || WAVES == 8) && R == 1 && S <= 2) {
         if (p.G == 1) {  // every step reads the same activation slice: keep it in registers
             LaneAct a0[NC];
 #pragma unroll
@@ -445,8 +448,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(Q4K_GEMV_KER
 
     // activation loads first (the whole workgroup), then the weight loads of
     // each wave's first two passes
-    ActStage<8> xs;
-    Q81Stage ys;
+    ActStage<8, pre_rounds(1, kWave * WAVES)> xs;
+    Q81Stage<pre_rounds(1, kWave * WAVES)> ys;
     if (p.x) stage_f32_issue<8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
     else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
     __syncthreads();
@@ -560,8 +563,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(Q4K_GEMV_KER
 
     // activation loads first (the whole workgroup), then the weight loads of
     // each wave's first two passes
-    ActStage<8> xs;
-    Q81Stage ys;
+    ActStage<8, pre_rounds(1, kWave * WAVES)> xs;
+    Q81Stage<pre_rounds(1, kWave * WAVES)> ys;
     if (p.x) stage_f32_issue<8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs);
     else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys);
     __syncthreads();
@@ -882,6 +885,13 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // would mostly run past the wave's rows).  Measured on MI355X.
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
     g.waves = steps_per_wg >= 16 && !four_per_cu ? 16 : 8;
+    // Six or more columns with rows of one group and >= 48 rows per
+    // workgroup: 8 waves, whose registers hold the lane's activation slices
+    // of every column, so the step loop reads no LDS (at 16 waves it reads
+    // the whole activation from LDS once per row, ~14 bytes per weight byte
+    // at 8 columns).  Measured on MI355X: 128256 x 4096 N=8 96 -> 83 us,
+    // 14336 x 4096 N=8 16.5 -> 15.8 us; slower with fewer columns or rows.
+    if (N >= 6 && K <= 16 * kQK && !fused && mats == 1 && (M + g.grid - 1) / g.grid >= 48) g.waves = 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;  // the instantiated sizes
     g.slots = steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
     g.R = 1;
@@ -905,8 +915,8 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     g.lds_launch = g.lds;
     if (owgs == 0 && !four_per_cu && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
     // weight loads before quantisation only when every activation load fits
-    // the kPre staging rounds issued ahead of them
-    const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave);
+    // the staging rounds issued ahead of them
+    const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave, nc);
     g.prologue = pro0_ok ? 0 : 1;
     const int opro = g_ovr_prologue.load();
     if (opro == 1 || ((opro == 0 || (opro == 2 && g.slots >= 4) || (opro == 3 && g.slots == 2 && !glu)) && pro0_ok))

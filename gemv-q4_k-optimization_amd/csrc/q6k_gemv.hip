@@ -245,8 +245,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const WaveRows wr = wave_rows<WAVES>(p, wave);
     constexpr int kLPB = stage_lpb(NC);
-    ActStage<kLPB> xs;
-    Q81Stage ys;
+    constexpr int kPreR = pre_rounds(NC, kWave * WAVES);
+    ActStage<kLPB, kPreR> xs;
+    Q81Stage<kPreR> ys;
     if constexpr (BATCH) {
         if (p.x) stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
         else stage_q81_issue<kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
@@ -420,7 +421,7 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     g.lds = q6_tile_lds_bytes((int)K, nc, g.waves);
     g.lds_launch = g.lds;
     if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
-    const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave);
+    const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave, nc);
     g.prologue = pro0_ok ? 0 : 1;
     const int opro = g_ovr_prologue.load();
     if (opro == 1 || (opro == 0 && pro0_ok)) g.prologue = opro;

@@ -107,6 +107,30 @@ def test_kernel_variants_against_oracle(Q, O, gpu, M, K):
         Q.set_geometry_override()
 
 
+@pytest.mark.parametrize("M,K,N", [(2048, 2048, 8), (1024, 4096, 5), (1024, 4096, 7), (300, 3072, 8),
+                                   (768, 2048, 3), (12288, 4096, 6)])
+def test_eight_wave_register_path(Q, O, gpu, M, K, N):
+    """8-wave launches with three or more columns of one-group rows: the
+    activation slices of every column held in registers, and staging rounds
+    issued ahead of the weights up to the column count, of which only those
+    holding values are loaded (2048- and 3072-value rows need fewer).  Checked
+    against the oracle, and bit for bit against the pre-quantised launch."""
+    assert Q.geometry(K, M, N)["waves_per_wg"] == 8
+    wq, x = inputs(Q, M, K, N, seed=11)
+    q8 = O.quantize_q8_1(x)
+    if M <= 1024:
+        rows = np.arange(M)
+    else:
+        rng = np.random.default_rng(M)
+        rows = np.unique(np.concatenate([[0, 1, M - 2, M - 1], rng.choice(M, 380, replace=False)]))
+    ref = oracle_rows(O, wq, K, q8, rows)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    _common.assert_within_tolerance(O, y[:, rows], ref, f"8 waves {M}x{K} N={N}")
+    y2 = Q.op_mul_mat_vec_q(wd, K, Q.quantize_row_q8_1(xd), N).cpu().numpy()
+    assert np.array_equal(y, y2)
+
+
 def test_fused_quantisation_at_ties(Q, O, gpu):
     """Activations whose x/d falls exactly on, or one ulp beside, a half-integer:
     round-half-away (ggml's roundf) and round-half-even differ there, so the
