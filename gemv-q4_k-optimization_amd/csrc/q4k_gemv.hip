@@ -269,7 +269,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
-    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * kRing, wr.beg, wr.end, 0, 0};
+    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * ring_floats(NC), wr.beg, wr.end, 0, 0};
 
     // Rows of two groups (4096 < K <= 8192), one column and row, both slots
     // loaded early (the gate-weight variant would spill registers): each
@@ -806,8 +806,8 @@ static int bpl_rows_per_pass(int64_t nb) {
 // 16-block groups, for the tile kernel; linear for the one-column block
 // kernels) followed by the per-32-value (d8, d8*sum q8) pairs.
 static int lds_bytes(int K, int nc) { return nc * (q8_col_bytes(K) + K / 4); }
-// The tile kernel adds a kRing-float result ring per wave after the activation.
-static int tile_lds_bytes(int K, int nc, int waves) { return lds_bytes(K, nc) + waves * kRing * 4; }
+// The tile kernel adds a result ring per wave after the activation.
+static int tile_lds_bytes(int K, int nc, int waves) { return lds_bytes(K, nc) + waves * ring_floats(nc) * 4; }
 static int lds_bytes_linear(int K) { return K + K / 4; }
 
 // Launch geometry for an (M, K, N) product.

@@ -202,10 +202,13 @@ __device__ __forceinline__ float glu_apply(int op, float up, float g) {
 // Results of a wave, buffered in LDS and written to dst in coalesced runs:
 // entry e is column e % NC of row beg + e / NC; with a gate (GLU), entries
 // 2t and 2t + 1 are the products of row beg + t with the weight and the gate.
-constexpr int kRing = 256;  // floats per wave
+// Floats per wave: 256, or 64 (eight rows) from five columns on, which lets
+// eight 14336-value columns and the rings of 16 waves share one
+// workgroup's 160 KB of LDS.
+__host__ __device__ constexpr int ring_floats(int nc) { return nc <= 4 ? 256 : 64; }
 
 struct ResultRing {
-    float *buf;   // this wave's kRing floats of LDS
+    float *buf;   // this wave's ring_floats(NC) floats of LDS
     int beg;      // first row of the wave
     int end;      // one past its last row
     int base;     // entries already written out
@@ -329,9 +332,9 @@ __device__ __forceinline__ void tile_to_ring(const GemvParams &p, int lane, floa
         }
     }
     rr.n += R * NC;
-    // rare (a wave's rows x NC above kRing): global stores inside the
+    // rare (a wave's rows x NC above the ring): global stores inside the
     // loop make the compiler's load waits conservative
-    if (rr.n + R * NC > kRing) ring_flush<NC, EPI>(p, lane, rr);
+    if (rr.n + R * NC > ring_floats(NC)) ring_flush<NC, EPI>(p, lane, rr);
 }
 
 }  // namespace q4k

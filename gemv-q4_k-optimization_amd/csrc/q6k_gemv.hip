@@ -289,7 +289,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
-    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * kRing, wr.beg, wr.end, 0, 0};
+    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * ring_floats(NC), wr.beg, wr.end, 0, 0};
 
     if constexpr (NC == 1 && R == 1 && S <= 2) {  // (wider variants would spill registers)
         if (p.G == 1) {  // every step reads the same activation slice: keep it in registers
@@ -372,9 +372,9 @@ __global__ __launch_bounds__(256) void q6_group_sums_kernel(Q6SumsParams p) {
 
 // LDS of the staged activation: q8 columns in the Q6K layout, d8 per
 // 32-value block (K/8 bytes per column), the -32*sum(q8) terms per 16 values
-// (K/4 bytes per column), then a kRing-float result ring per wave.
+// (K/4 bytes per column), then a result ring per wave.
 static int q6_act_bytes(int K, int nc) { return nc * (q8_col_bytes(K) + K / 8 + K / 4); }
-static int q6_tile_lds_bytes(int K, int nc, int waves) { return q6_act_bytes(K, nc) + waves * kRing * 4; }
+static int q6_tile_lds_bytes(int K, int nc, int waves) { return q6_act_bytes(K, nc) + waves * ring_floats(nc) * 4; }
 
 struct Q6Geometry {
     int waves = 16;
