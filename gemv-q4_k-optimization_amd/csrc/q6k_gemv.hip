@@ -199,24 +199,27 @@ __device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6La
     if (st.i == p.G - 1) tile_to_ring<NC, R, EPI>(p, ln.lane, acc, rr);
 }
 
-// One column whose rows are one group long: q6_process_group with the
-// lane's activation slice (the same in every step) held in registers.
-template <int EPI>
-__device__ __forceinline__ void q6_process_reg(const GemvParams &p, const Q6Lane &ln, const Q6Act &a,
-                                               const Q6Regs (&w)[1], float (&acc)[1][1], ResultRing &rr) {
+// Rows that are one group long: q6_process_group with the lane's activation
+// slices (the same in every step) held in registers.
+template <int NC, int EPI>
+__device__ __forceinline__ void q6_process_reg(const GemvParams &p, const Q6Lane &ln, const Q6Act (&a)[NC],
+                                               const Q6Regs (&w)[1], float (&acc)[1][NC], ResultRing &rr) {
     uint32_t v[4][4];
     int sc[4];
     q6_values(w[0], v);
     q6_scales(w[0], ln.jp, sc);
     const float d = half_bits_to_float(w[0].dw >> 16);
-    int s[4];
-    q6_lane_sums(v, a, s);
-    float f = a.d8.x * (float)__mul24(s[0], sc[0]);
-    f = __builtin_fmaf(a.d8.y, (float)__mul24(s[1], sc[1]), f);
-    f = __builtin_fmaf(a.d8.z, (float)__mul24(s[2], sc[2]), f);
-    f = __builtin_fmaf(a.d8.w, (float)__mul24(s[3], sc[3]), f);
-    acc[0][0] = __builtin_fmaf(d, f, acc[0][0]);
-    tile_to_ring<1, 1, EPI>(p, ln.lane, acc, rr);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int s[4];
+        q6_lane_sums(v, a[c], s);
+        float f = a[c].d8.x * (float)__mul24(s[0], sc[0]);
+        f = __builtin_fmaf(a[c].d8.y, (float)__mul24(s[1], sc[1]), f);
+        f = __builtin_fmaf(a[c].d8.z, (float)__mul24(s[2], sc[2]), f);
+        f = __builtin_fmaf(a[c].d8.w, (float)__mul24(s[3], sc[3]), f);
+        acc[0][c] = __builtin_fmaf(d, f, acc[0][c]);
+    }
+    tile_to_ring<NC, 1, EPI>(p, ln.lane, acc, rr);
 }
 
 // Tile kernel: any K, 1..8 columns; one row per tile.  The structure of the
@@ -291,13 +294,17 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
     ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * ring_floats(NC), wr.beg, wr.end, 0, 0};
 
-    if constexpr (NC == 1 && R == 1 && S <= 2) {  // (wider variants would spill registers)
+    // (one column at 16 waves, eight at 8 waves: wider variants would spill
+    // registers)
+    if constexpr ((NC == 1 || WAVES == 8) && R == 1 && S <= 2) {
         if (p.G == 1) {  // every step reads the same activation slice: keep it in registers
-            const Q6Act a0 = q6_act(p, ln, 0, 0, NC, q8s, aux);
+            Q6Act a0[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) a0[c] = q6_act(p, ln, 0, c, NC, q8s, aux);
             for (;;) {
 #pragma unroll
                 for (int k = 0; k < S; ++k) {
-                    q6_process_reg<EPI>(p, ln, a0, w[k], acc, rr);
+                    q6_process_reg<NC, EPI>(p, ln, a0, w[k], acc, rr);
                     st[k] = next_step(st[(k + S - 1) % S], p.G);
                     q6_load_step<R>(p, ln, ws, st[k], w[k]);
                 }
@@ -408,6 +415,13 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     g.grid = owgs > 0 ? owgs : grid_per_matrix(cus, mats, M);
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
     g.waves = steps_per_wg >= 16 && (int64_t)nc * K > 8192 ? 16 : 8;
+    // Six or more columns with rows of one group and >= 256 rows per
+    // workgroup: 8 waves, whose registers hold every column's activation
+    // slices (the step loop then reads no LDS), as in the Q4_K kernel.
+    // Measured on MI355X: 128256 x 4096 N=8 126 -> 121 us; even at 128 rows
+    // per workgroup (32768 x 4096) and 2 % slower at 56 (14336 x 4096).
+    if (N >= 6 && K <= 16 * kQK && fused == kFusedNone && mats == 1 && (M + g.grid - 1) / g.grid >= 256)
+        g.waves = 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;
     // One group in flight per wave, except in launches over several weight
     // matrices (MUL_MAT_ID, broadcasting) whose waves stream four or more

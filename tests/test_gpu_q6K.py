@@ -154,6 +154,25 @@ def test_zero_weight_and_activation(Q, O, gpu):
     assert (y2 == 0).all()
 
 
+def test_eight_wave_register_path_long_products(Q, O, gpu):
+    """Six or more columns over >= 256 rows per workgroup run 8-wave launches
+    whose registers hold every column's activation slices: the oracle on a
+    row sample, and bit for bit the pre-quantised launch."""
+    M, K, N = 65536, 4096, 6
+    assert Q.geometry(K, M, N, wtype=Q.GGML_TYPE_Q6_K)["waves_per_wg"] == 8
+    rng = np.random.default_rng(12)
+    wq = random_q6_blocks(rng, M, K, extremes=False)
+    x = _common.activations(N, K, 12)
+    q8 = O.quantize_q8_1(x)
+    rows = np.unique(np.concatenate([[0, 1, M - 2, M - 1], rng.choice(M, 380, replace=False)]))
+    ref = O.gemv_q6K_q8_1(wq[rows], K, q8, want_sums=False)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    y = Q.mul_mat_vec_q(wd, K, xd, wtype=Q.GGML_TYPE_Q6_K).cpu().numpy()
+    _common.assert_within_tolerance(O, y[:, rows], ref, f"8 waves {M}x{K} N={N}")
+    y2 = Q.op_mul_mat_vec_q(wd, K, to_dev(q8, gpu), N, wtype=Q.GGML_TYPE_Q6_K).cpu().numpy()
+    assert np.array_equal(y, y2)
+
+
 # ------------------------------------------------------- workloads ----
 # Q6_K tensors of a Q4_K_M model: ffn_down (4096 x 14336), attn_v
 # (1024 x 4096) and the output projection (32000 x 4096, Mistral 7B).
