@@ -885,13 +885,17 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // would mostly run past the wave's rows).  Measured on MI355X.
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
     g.waves = steps_per_wg >= 16 && !four_per_cu ? 16 : 8;
-    // Six or more columns with rows of one group and >= 48 rows per
-    // workgroup: 8 waves, whose registers hold the lane's activation slices
-    // of every column, so the step loop reads no LDS (at 16 waves it reads
-    // the whole activation from LDS once per row, ~14 bytes per weight byte
-    // at 8 columns).  Measured on MI355X: 128256 x 4096 N=8 96 -> 83 us,
-    // 14336 x 4096 N=8 16.5 -> 15.8 us; slower with fewer columns or rows.
-    if (N >= 6 && K <= 16 * kQK && !fused && mats == 1 && (M + g.grid - 1) / g.grid >= 48) g.waves = 8;
+    // Three or more columns with rows of one group and >= 96 rows per
+    // workgroup (>= 48 from six columns on): 8 waves, whose registers hold
+    // the lane's activation slices of every column, so the step loop reads
+    // no LDS (at 16 waves it reads the whole activation from LDS once per
+    // row, ~14 bytes per weight byte at 8 columns).  Measured on MI355X:
+    // 128256 x 4096 N=8 96 -> 83 us, N=4 63.6 -> 59.3 us, 28672 x 4096 N=4
+    // 20.6 -> 16.9 us, 14336 x 4096 N=8 16.5 -> 15.8 us; N=3..5 at
+    // 14336 x 4096 (56 rows) even to 3 % slower.
+    const int64_t rows_per_wg = (M + g.grid - 1) / g.grid;
+    if (N >= 3 && K <= 16 * kQK && !fused && mats == 1 && (rows_per_wg >= 96 || (N >= 6 && rows_per_wg >= 48)))
+        g.waves = 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;  // the instantiated sizes
     g.slots = steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
     g.R = 1;

@@ -108,7 +108,7 @@ def test_kernel_variants_against_oracle(Q, O, gpu, M, K):
 
 
 @pytest.mark.parametrize("M,K,N", [(2048, 2048, 8), (1024, 4096, 5), (1024, 4096, 7), (300, 3072, 8),
-                                   (768, 2048, 3), (12288, 4096, 6)])
+                                   (768, 2048, 3), (12288, 4096, 6), (28672, 4096, 3)])
 def test_eight_wave_register_path(Q, O, gpu, M, K, N):
     """8-wave launches with three or more columns of one-group rows: the
     activation slices of every column held in registers, and staging rounds
