@@ -43,7 +43,7 @@ def to_dev(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-SHAPES = [(1, 256), (17, 4352), (1000, 4096), (14336, 4096), (300, 14336)]
+SHAPES = [(1, 256), (17, 4352), (1000, 4096), (14336, 4096), (300, 14336), (777, 768), (3000, 2048)]
 TYPES = [12, 14]
 
 

@@ -131,6 +131,30 @@ def test_eight_wave_register_path(Q, O, gpu, M, K, N):
     assert np.array_equal(y, y2)
 
 
+@pytest.mark.parametrize("M,K", [(1000, 2048), (37, 768), (4099, 1280), (513, 512), (3, 1024),
+                                 (2047, 256), (20000, 2048)])
+def test_short_rows(Q, O, gpu, M, K):
+    """Rows of at most 8 super-blocks (lanes past a row's end read zeros),
+    from one to thousands of rows per workgroup: against the oracle, with the
+    bias epilogue, and bit for bit against the pre-quantised launch."""
+    wq, x = inputs(Q, M, K, 1, seed=13)
+    q8 = O.quantize_q8_1(x)
+    if M <= 4099:
+        rows = np.arange(M)
+    else:
+        rng = np.random.default_rng(M)
+        rows = np.unique(np.concatenate([[0, 1, M - 2, M - 1], rng.choice(M, 380, replace=False)]))
+    ref = oracle_rows(O, wq, K, q8, rows)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    _common.assert_within_tolerance(O, y[:, rows], ref, f"short rows {M}x{K}")
+    y2 = Q.op_mul_mat_vec_q(wd, K, Q.quantize_row_q8_1(xd), 1).cpu().numpy()
+    assert np.array_equal(y, y2)
+    bias = np.random.default_rng(M + K).standard_normal(M).astype(np.float32)
+    yb = Q.mul_mat_vec_q_fused(wd, K, xd, x_bias=to_dev(bias, gpu)).cpu().numpy()
+    assert np.array_equal(yb, (y + bias).astype(np.float32))
+
+
 def test_fused_quantisation_at_ties(Q, O, gpu):
     """Activations whose x/d falls exactly on, or one ulp beside, a half-integer:
     round-half-away (ggml's roundf) and round-half-even differ there, so the
