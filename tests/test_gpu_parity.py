@@ -183,6 +183,46 @@ def test_fused_quantisation_at_ties(Q, O, gpu):
     _common.assert_within_tolerance(O, y, ref, "ties")
 
 
+def test_concurrent_calls_from_host_threads(Q, O, gpu):
+    """Four host threads, each with its own stream, calling the op at once
+    (ctypes releases the GIL): shapes whose launches need the large-LDS
+    attribute, the workspace route and the one-launch route.  Every result
+    must equal the same call made alone."""
+    import threading
+    import torch
+    shapes = [(300, 14336, 2), (999, 4096, 1), (64, 8192, 8), (513, 2048, 3)]
+    data = []
+    for M, K, N in shapes:
+        wq, x = inputs(Q, M, K, N, seed=21)
+        wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+        ws = torch.empty(Q.q8_1_bytes(K, N), dtype=torch.uint8, device=gpu)
+        alone = Q.mul_mat_vec_q(wd, K, xd, workspace=ws).cpu().numpy()
+        data.append((K, wd, xd, ws, alone))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(t):
+        K, wd, xd, ws, alone = data[t]
+        st = torch.cuda.Stream(device=gpu)
+        try:
+            with torch.cuda.stream(st):
+                outs = [Q.mul_mat_vec_q(wd, K, xd, workspace=ws, stream=st) for _ in range(20)]
+            st.synchronize()
+            for o in outs:
+                if not np.array_equal(o.cpu().numpy(), alone):
+                    errors.append(t)
+                    break
+        except Exception as e:  # reported below
+            errors.append((t, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(len(shapes))]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+
+
 def test_zero_activation_and_zero_weight(Q, O, gpu):
     M, K, N = 40, 1024, 3
     wq, x = inputs(Q, M, K, N, seed=2)
