@@ -1066,9 +1066,9 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
                     &p.rows_base, &p.rows_extra, &p.nb, &p.qcol, &p};
     if (batch) p.bt = bl->bt;
     const dim3 grid((unsigned)geo.grid, batch ? (unsigned)bl->nch : 1u, batch ? (unsigned)bl->nsmp : 1u);
-    hipError_t e = hipLaunchKernel(fn, grid, dim3(kWave * geo.waves), args, (size_t)geo.lds_launch, stream);
-    if (e != hipSuccess) return hip_fail(e);
-    e = hipGetLastError();
+    // the launch's own status (hipGetLastError would also report, and clear,
+    // an error a caller's earlier unrelated call left behind)
+    const hipError_t e = hipLaunchKernel(fn, grid, dim3(kWave * geo.waves), args, (size_t)geo.lds_launch, stream);
     if (e != hipSuccess) return hip_fail(e);
     return Q4K_OK;
 }

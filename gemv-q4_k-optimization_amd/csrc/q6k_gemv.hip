@@ -548,9 +548,8 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         void *args[] = {&p.x, &p.y, &p.w, &p.row_stride, &ldx32, &scy32, &p.K, &p.vec_ok,
                         &p.rows_base, &p.rows_extra, &p.nb, &p.qcol, &p};
         const dim3 grid((unsigned)geo.grid, bl ? (unsigned)bl->nch : 1u, bl ? (unsigned)bl->nsmp : 1u);
-        hipError_t e = hipLaunchKernel(fn, grid, dim3(kWave * geo.waves), args, (size_t)lds_launch, stream);
-        if (e != hipSuccess) return hip_fail(e);
-        e = hipGetLastError();
+        // the launch's own status, as in the Q4_K launch
+        const hipError_t e = hipLaunchKernel(fn, grid, dim3(kWave * geo.waves), args, (size_t)lds_launch, stream);
         if (e != hipSuccess) return hip_fail(e);
     }
     return Q4K_OK;
