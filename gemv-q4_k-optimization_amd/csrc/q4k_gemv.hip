@@ -880,6 +880,14 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const bool four_per_cu = owgs == 0 && owaves == 0 && N == 1 && !fused && mats == 1 && K <= 8192 &&
                              weight_bytes >= (int64_t)500000 * cus;
     if (four_per_cu) g.grid = 4 * cus;
+    // One column with rows of three or more groups and >= 192 steps per CU:
+    // two 16-wave workgroups per CU with one group in flight per wave
+    // (measured on MI355X: 8192 x 28672 30.0 -> 28.5 us, 14336 x 14336
+    // 23.4 -> 22.7 us; 8192 x 14336, 128 steps, 5 % slower).
+    const int64_t G = (K / kQK + 15) / 16;
+    const bool two_per_cu = owgs == 0 && owaves == 0 && N == 1 && !fused && mats == 1 && !four_per_cu && G >= 3 &&
+                            (M + cus - 1) / cus * G >= 192;
+    if (two_per_cu) g.grid = 2 * cus;
     // 16 waves per CU unless the product is small; two groups in flight per
     // wave once a wave has four or more to stream, else one (a second slot
     // would mostly run past the wave's rows).  Measured on MI355X.
@@ -898,6 +906,14 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         g.waves = 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;  // the instantiated sizes
     g.slots = steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
+    if (two_per_cu) g.slots = 1;
+    // One column, rows of two groups, at most 8 rows per workgroup: 8 waves
+    // with both of a row's groups in flight (2048 x 8192 5.21 -> 4.63 us,
+    // 1024 x 8192 4.72 -> 4.33 us; 16 rows, 4096 x 8192, 2 % slower).
+    if (N == 1 && !fused && mats == 1 && owaves == 0 && G == 2 && rows_per_wg <= 8) {
+        g.waves = 8;
+        g.slots = 2;
+    }
     g.R = 1;
     if (orows == 1 || orows == 2 || orows == 4) g.R = orows;
     const int oslots = g_ovr_slots.load();
@@ -917,7 +933,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     g.rows_extra = (int)(M % g.grid);
     g.lds = tile_lds_bytes((int)K, nc, g.waves);
     g.lds_launch = g.lds;
-    if (owgs == 0 && !four_per_cu && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
+    if (owgs == 0 && !four_per_cu && !two_per_cu && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
     // weight loads before quantisation only when every activation load fits
     // the staging rounds issued ahead of them
     const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave, nc);
