@@ -938,13 +938,13 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // the staging rounds issued ahead of them
     const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave, nc);
     g.prologue = pro0_ok ? 0 : 1;
-    // One column, two slots and rows of three or more groups, on streams of
-    // under 8 steps per wave: one early group instead of two (measured on
-    // MI355X: 4096 x 14336 9.06 -> 8.63 us, 5120 x 13824 10.13 -> 9.63,
-    // 20480 x 4096 11.16 -> 10.85; 8192 x 28672, 14 steps per wave, 1 %
-    // slower).  Two-group rows keep both for the streamed prologue.
-    if (pro0_ok && nc == 1 && g.slots == 2 && !glu && (K / kQK + 15) / 16 != 2 && steps_per_wg < 8 * g.waves)
-        g.prologue = 3;
+    // One column and two slots on streams of under 8 steps per wave: one
+    // early group instead of two (measured on MI355X: 4096 x 14336 9.06 ->
+    // 8.63 us, 5120 x 13824 10.13 -> 9.63, 20480 x 4096 11.16 -> 10.85,
+    // 8192 x 8192 9.61 -> 8.85 (against the streamed prologue below),
+    // 11008 x 8192 11.42 -> 11.18; 8192 x 28672, 14 steps per wave, 1 %
+    // slower).  Longer two-group streams keep the streamed prologue.
+    if (pro0_ok && nc == 1 && g.slots == 2 && !glu && steps_per_wg < 8 * g.waves) g.prologue = 3;
     const int opro = g_ovr_prologue.load();
     if (opro == 1 || ((opro == 0 || (opro == 2 && g.slots >= 4) || (opro == 3 && g.slots == 2 && !glu)) && pro0_ok))
         g.prologue = opro;

@@ -405,13 +405,14 @@ def test_workload_parity(Q, O, gpu, M, K, N):
     assert np.isfinite(y).all()
 
 
-@pytest.mark.parametrize("M", [8192, 14336])
+@pytest.mark.parametrize("M", [8192, 14336, 20480])
 def test_two_group_rows_streamed_prologue(Q, O, gpu, M):
     """Rows of two 4096-value groups with 16 waves and two slots per wave:
-    the one-column launch consumes its first steps between the quantisation
-    rounds.  Checked against the oracle on a row sample, bit for bit against
-    the pre-quantised launch (which stages the whole activation first), and
-    with the bias epilogue (same rows, bias added)."""
+    with 64 or more rows per workgroup (20480 rows) the one-column launch
+    consumes its first steps between the quantisation rounds; with fewer it
+    issues one early group.  Checked against the oracle on a row sample,
+    bit for bit against the pre-quantised launch (which stages the whole
+    activation first), and with the bias epilogue (same rows, bias added)."""
     import torch
     K = 8192
     geo = Q.geometry(K, M, 1)
