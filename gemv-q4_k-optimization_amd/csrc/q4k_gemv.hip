@@ -907,6 +907,11 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;  // the instantiated sizes
     g.slots = steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
     if (two_per_cu) g.slots = 1;
+    // One column with rows of one group: one slot up to 8 steps per wave
+    // (20480 x 4096 10.87 -> 10.53 us, 18944 x 3584 9.71 -> 9.52 us; rows of
+    // four groups keep two: 5120 x 13824 9.60 against 11.13 us).
+    if (N == 1 && !fused && mats == 1 && !four_per_cu && g.waves == 16 && G == 1 && steps_per_wg < 128)
+        g.slots = 1;
     // One column, rows of two groups, at most 8 rows per workgroup: 8 waves
     // with both of a row's groups in flight (2048 x 8192 5.21 -> 4.63 us,
     // 1024 x 8192 4.72 -> 4.33 us; 16 rows, 4096 x 8192, 2 % slower).
