@@ -888,11 +888,13 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const bool two_per_cu = owgs == 0 && owaves == 0 && N == 1 && !fused && mats == 1 && !four_per_cu && G >= 3 &&
                             (M + cus - 1) / cus * G >= 192;
     if (two_per_cu) g.grid = 2 * cus;
-    // 16 waves per CU unless the product is small; two groups in flight per
-    // wave once a wave has four or more to stream, else one (a second slot
-    // would mostly run past the wave's rows).  Measured on MI355X.
+    // 16 waves per CU unless the product is small (under 12 steps per
+    // workgroup; 12-15 steps measured 2-4 % faster at 16 than at 8, e.g.
+    // 3584 x 3584 4.38 -> 4.24 us, and 4 steps 6 % slower); two groups in
+    // flight per wave once a wave has four or more to stream, else one (a
+    // second slot would mostly run past the wave's rows).  Measured on MI355X.
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
-    g.waves = steps_per_wg >= 16 && !four_per_cu ? 16 : 8;
+    g.waves = steps_per_wg >= 12 && !four_per_cu ? 16 : 8;
     // Three or more columns with rows of one group and >= 96 rows per
     // workgroup (>= 48 from six columns on): 8 waves, whose registers hold
     // the lane's activation slices of every column, so the step loop reads
