@@ -56,6 +56,8 @@ def lib():
             "orc_selftest_scale_pack": (I64, []),
             "orc_check_div127": (I64, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]),
             "orc_quantize_q4_K": (None, [P, P, I64]),
+            "orc_q4K_fit_block": (None, [P, ctypes.c_float, ctypes.c_float, I, I, P, P, P]),
+            "orc_q6K_fit_block": (None, [P, ctypes.c_float, I, I, P, P]),
             "orc_quantize_q4_K_rows": (None, [P, P, I64, I64, I]),
             "orc_dequantize_q4_K": (None, [P, P, I64]),
             "orc_quantize_q8_1": (None, [P, I64, I64, P]),
@@ -119,6 +121,37 @@ def quantize_q4_K(w: np.ndarray, nthreads: int = 1) -> np.ndarray:
     out = np.empty((M, K // QK_K * Q4K_BYTES), dtype=np.uint8)
     lib().orc_quantize_q4_K_rows(_p(w), _p(out), M, K, nthreads)
     return out
+
+
+def q4K_fit(w: np.ndarray, rmin: float = -1.0, rdelta: float = 0.1, nstep: int = 20, weight_mode: int = 0):
+    """Stage 1 of quantize_row_q4_K_ref on every 256-value block of w (F32,
+    size a multiple of 256): the make_qkx2_quants fit of each 32-value
+    sub-block.  Returns (scales [nblk, 8], mins [nblk, 8] (= -min of the fit),
+    L [nblk, 256] levels 0..15).  The defaults are ggml's parameters;
+    weight_mode 1 (x^2 weights) and other rmin/rdelta/nstep values are
+    planted mistakes for the tests."""
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1, QK_K)
+    n = w.shape[0]
+    sc = np.empty((n, 8), np.float32)
+    mn = np.empty((n, 8), np.float32)
+    L = np.empty((n, QK_K), np.uint8)
+    for b in range(n):
+        lib().orc_q4K_fit_block(_p(w[b]), rmin, rdelta, nstep, weight_mode, _p(sc[b]), _p(mn[b]), _p(L[b]))
+    return sc, mn, L
+
+
+def q6K_fit(w: np.ndarray, rdelta: float = 0.1, nstep: int = 9, weight_mode: int = 0):
+    """Stage 1 of quantize_row_q6_K_ref on every 256-value block of w: the
+    make_qx_quants fit (nmax 32) of each 16-value group.  Returns (scales
+    [nblk, 16], L [nblk, 256] as l + 32).  Defaults are ggml's parameters;
+    weight_mode 1 (|x| weights) is a planted mistake for the tests."""
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1, QK_K)
+    n = w.shape[0]
+    sc = np.empty((n, 16), np.float32)
+    L = np.empty((n, QK_K), np.int8)
+    for b in range(n):
+        lib().orc_q6K_fit_block(_p(w[b]), rdelta, nstep, weight_mode, _p(sc[b]), _p(L[b]))
+    return sc, L
 
 
 def dequantize_q4_K(q: np.ndarray, K: int) -> np.ndarray:

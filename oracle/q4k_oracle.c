@@ -19,15 +19,21 @@
  *   orc_vecdot_scale_pair     exhaustive agreement of two independent unpackers
  *                             + pack/unpack identity over all 64x64 (sc, m)
  *   orc_quantize_q8_1         invariants (|q|<=127, amax -> +-127, zero blocks,
- *                             |x-d*q| <= d/2, exact multiples round-trip)
+ *                             |x-d*q| <= d/2, exact multiples round-trip) and
+ *                             exact ties rounding away from zero (roundf)
  *   orc_gemv_q4K_q8_1         brute force: naive dequantised f64 dot (numpy) and
  *                             nibble-by-position integer sums (numpy)
- *   orc_quantize_q4_K         dequantisation error bound, packing invariants;
- *                             byte-exactness against upstream: parity unpinned
- *   orc_quantize_q8_K /
+ *   orc_q4K_fit_block /
+ *   orc_quantize_q4_K         stage 1 against a numpy walk over ggml's candidate
+ *                             scales with f64 fits (agreement away from near-ties;
+ *                             planted rdelta/rmin/weight/nstep mistakes fail);
+ *                             stages 2-3 nearest-field and nearest-level
+ *                             properties; exact-grid blocks round-trip bit for bit
+ *   orc_quantize_q8_K         signed-max rule (x_max -> -127, first on ties),
+ *                             bsums, error bound
  *   orc_vec_dot_q4_K_q8_K_*   scalar vs AVX2 agreement, error bound against the
- *                             f64 dequantised product; byte/ulp-exactness
- *                             against upstream: parity unpinned
+ *                             f64 dequantised product; the f32 summation order
+ *                             of ggml's own AVX2 code: parity unpinned
  *
  * Build: oracle/Makefile (gcc, -ffp-contract=off so float expressions are
  * evaluated exactly as written).
@@ -332,20 +338,35 @@ static float orc_make_qkx2_quants(int n, int nmax, const float *x, const float *
     return scale;
 }
 
+/* Stage 1 of quantize_row_q4_K_ref for one 256-value block: the
+ * make_qkx2_quants fit of each 32-value sub-block, giving its scale, its
+ * -min and its levels L.  ggml's parameters are rmin = -1, rdelta = 0.1,
+ * nstep = 20 and the weights sqrt(mean(x^2)) + |x| (weight_mode 0); the
+ * parameters are arguments so that the tests can plant a wrong one (weight_mode
+ * 1: x^2) and see their brute-force check of the fit fail. */
+void orc_q4K_fit_block(const float *x, float rmin, float rdelta, int nstep, int weight_mode,
+                       float scales[8], float mins[8], uint8_t L[256]) {
+    uint8_t Laux[32];
+    float w[32];
+    for (int s = 0; s < 8; ++s) {
+        const float *xs = x + 32 * s;
+        float sum_x2 = 0;
+        for (int l = 0; l < 32; ++l) sum_x2 += xs[l] * xs[l];
+        const float av_x = sqrtf(sum_x2 / 32);
+        for (int l = 0; l < 32; ++l) w[l] = weight_mode == 1 ? xs[l] * xs[l] : av_x + fabsf(xs[l]);
+        scales[s] = orc_make_qkx2_quants(32, 15, xs, w, L + 32 * s, &mins[s], Laux, rmin, rdelta, nstep);
+    }
+}
+
 /* quantize_row_q4_K_ref: k floats (k % 256 == 0) -> k/256 blocks of 144 B. */
 void orc_quantize_q4_K(const float *x, uint8_t *y, int64_t k) {
     const int64_t nb = k / ORC_QK_K;
-    uint8_t L[ORC_QK_K], Laux[32];
-    float w[32], mins[8], scales[8];
+    uint8_t L[ORC_QK_K];
+    float mins[8], scales[8];
     for (int64_t i = 0; i < nb; ++i, x += ORC_QK_K, y += ORC_Q4K_BYTES) {
         float max_scale = 0, max_min = 0;
+        orc_q4K_fit_block(x, -1.0f, 0.1f, 20, 0, scales, mins, L);
         for (int s = 0; s < 8; ++s) {
-            const float *xs = x + 32 * s;
-            float sum_x2 = 0;
-            for (int l = 0; l < 32; ++l) sum_x2 += xs[l] * xs[l];
-            const float av_x = sqrtf(sum_x2 / 32);
-            for (int l = 0; l < 32; ++l) w[l] = av_x + fabsf(xs[l]);
-            scales[s] = orc_make_qkx2_quants(32, 15, xs, w, L + 32 * s, &mins[s], Laux, -1.0f, 0.1f, 20);
             if (scales[s] > max_scale) max_scale = scales[s];
             if (mins[s] > max_min) max_min = mins[s];
         }

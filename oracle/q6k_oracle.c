@@ -19,9 +19,13 @@
  *                        sums and the f64 dot, at the extremes q in {0, 63},
  *                        q8 in {-127, 127}, scales in {-128, 127}
  *   orc_dequantize_q6_K  the same numpy decode, bit for bit
- *   orc_quantize_q6_K    dequantisation error bound, level range, all-zero
- *                        blocks, exact multiples of a group scale; byte-
- *                        exactness against upstream: parity unpinned
+ *   orc_q6K_fit_block /
+ *   orc_quantize_q6_K    stage 1 against a numpy argmax over ggml's 19
+ *                        candidate scales with f64 objectives (agreement away
+ *                        from near-ties; planted rdelta/weight/nstep mistakes
+ *                        fail); int8 scales nearest to -128 * fit / max; every
+ *                        value on the nearest level; all-zero blocks;
+ *                        exact-grid blocks round-trip bit for bit
  *
  * Build: oracle/Makefile (gcc, -ffp-contract=off).
  */
@@ -44,8 +48,11 @@ static inline int orc_clamp(int v, int lo, int hi) { return v < lo ? lo : (v > h
 /* make_qx_quants(n, nmax, x, L, rmse_type = 1, qw = NULL): fit of x to
  * scale * l, l in [-nmax, nmax - 1], weights x^2; the inverse scale -nmax/x_m
  * (x_m the value of largest magnitude) and 18 neighbours -(nmax + 0.1 k)/x_m,
- * k = +-1..+-9, keeping the best sum(w x l)^2 / sum(w l^2).  Writes l + nmax. */
-static float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L) {
+ * k = +-1..+-9, keeping the best sum(w x l)^2 / sum(w l^2).  Writes l + nmax.
+ * ggml's rdelta = 0.1, nstep = 9 and weights x^2 (weight_mode 0) are
+ * arguments so that the tests can plant a wrong one (weight_mode 1: |x|). */
+static float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L, float rdelta, int nstep,
+                                int weight_mode) {
     float amax = 0.0f, xm = 0.0f;
     for (int i = 0; i < n; ++i) {
         const float ax = fabsf(x[i]);
@@ -63,19 +70,19 @@ static float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L) {
     for (int i = 0; i < n; ++i) {
         const int l = orc_clamp(orc_nearest_int(iscale * x[i]), -nmax, nmax - 1);
         L[i] = (int8_t)(l + nmax);
-        const float w = x[i] * x[i];
+        const float w = weight_mode == 1 ? fabsf(x[i]) : x[i] * x[i];
         sumlx += w * x[i] * l;
         suml2 += w * l * l;
     }
     float scale = suml2 != 0.0f ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx;
-    for (int is = -9; is <= 9; ++is) {
+    for (int is = -nstep; is <= nstep; ++is) {
         if (is == 0) continue;
-        iscale = -(nmax + 0.1f * is) / xm;
+        iscale = -(nmax + rdelta * is) / xm;
         sumlx = suml2 = 0.0f;
         for (int i = 0; i < n; ++i) {
             const int l = orc_clamp(orc_nearest_int(iscale * x[i]), -nmax, nmax - 1);
-            const float w = x[i] * x[i];
+            const float w = weight_mode == 1 ? fabsf(x[i]) : x[i] * x[i];
             sumlx += w * x[i] * l;
             suml2 += w * l * l;
         }
@@ -89,6 +96,15 @@ static float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L) {
     return scale;
 }
 
+/* Stage 1 of quantize_row_q6_K_ref for one 256-value block: the
+ * make_qx_quants fit (nmax 32) of each 16-value group, giving its scale and
+ * levels L (l + 32).  ggml's parameters: rdelta 0.1, nstep 9, weight_mode 0. */
+void orc_q6K_fit_block(const float *x, float rdelta, int nstep, int weight_mode, float scales[16],
+                       int8_t L[256]) {
+    for (int ib = 0; ib < 16; ++ib)
+        scales[ib] = orc_make_qx_quants(16, 32, x + 16 * ib, L + 16 * ib, rdelta, nstep, weight_mode);
+}
+
 /* quantize_row_q6_K_ref: k floats (k % 256 == 0) -> k/256 blocks of 210 B. */
 void orc_quantize_q6_K(const float *x, uint8_t *y, int64_t k) {
     const int64_t nb = k / ORC_QK_K;
@@ -96,9 +112,9 @@ void orc_quantize_q6_K(const float *x, uint8_t *y, int64_t k) {
     float scales[16];
     for (int64_t i = 0; i < nb; ++i, x += ORC_QK_K, y += ORC_Q6K_BYTES) {
         float max_scale = 0.0f, max_abs = 0.0f;
+        orc_q6K_fit_block(x, 0.1f, 9, 0, scales, L);
         for (int ib = 0; ib < 16; ++ib) {
-            const float s = orc_make_qx_quants(16, 32, x + 16 * ib, L + 16 * ib);
-            scales[ib] = s;
+            const float s = scales[ib];
             if (fabsf(s) > max_abs) {
                 max_abs = fabsf(s);
                 max_scale = s;

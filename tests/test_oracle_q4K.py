@@ -1,7 +1,7 @@
-"""Q4_K weight quantiser: the oracle's restatement of quantize_row_q4_K_ref is
-pinned by its invariants (byte-exactness against upstream ggml is unpinned:
-ggml is not available here); the product's host quantiser must equal it byte
-for byte."""
+"""Q4_K weight quantiser: invariants of the oracle's restatement of
+quantize_row_q4_K_ref (its stages are pinned against ggml's published
+algorithm in test_oracle_quantiser_pins.py); the product's host quantiser
+must equal it byte for byte."""
 import numpy as np
 import pytest
 
