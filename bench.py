@@ -389,51 +389,6 @@ def profile_mode(args):
     log(f"[profile] {args.warmup + args.steps} launches of {M}x{K} N={N} done")
 
 
-def stream_probe(args):
-    """Bandwidth a single streaming-read launch reaches on this device for the
-    GEMV's byte counts (same timing method as the GEMV): the practical ceiling
-    the roofline fraction is read against."""
-    import ctypes
-    import torch
-    lib = ctypes.CDLL(os.path.join(ROOT, "gemv-q4_k-optimization_amd", "libq4k_stream_probe.so"))
-    lib.q4k_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32,
-                                          ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    dev = torch.device("cuda:0")
-    for nbytes in (33030144, 132120576, 295501824):
-        ncopies = max(2, math.ceil((1 << 30) / nbytes))
-        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(i) for i in range(ncopies)]
-        out = torch.empty(1 << 20, dtype=torch.int32, device=dev)
-        for bpw, depth in ((4096, 4), (8192, 8), (16384, 8), (16384, 16), (32768, 16), (65536, 16)):
-            if nbytes // bpw > (1 << 20):
-                continue
-            stream = torch.cuda.Stream()
-            with torch.cuda.stream(stream):
-                sp = ctypes.c_void_p(stream.cuda_stream)
-                def launch(i):
-                    st = lib.q4k_probe_stream_read(ctypes.c_void_p(bufs[i % ncopies].data_ptr()), nbytes, bpw,
-                                                   depth, ctypes.c_void_p(out.data_ptr()), sp)
-                    assert st == 0
-                for i in range(args.warmup):
-                    launch(i)
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g, stream=stream):
-                    for i in range(args.steps):
-                        launch(i)
-                g.replay()
-                torch.cuda.synchronize()
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                g.replay()
-                e1.record(stream)
-                torch.cuda.synchronize()
-            sec = e0.elapsed_time(e1) * 1e-3 / args.steps
-            print(json.dumps({"probe": "stream_read", "bytes": nbytes, "bytes_per_wave": bpw, "depth": depth,
-                              "waves": -(-nbytes // bpw), "us": round(sec * 1e6, 3),
-                              "GBps": round(nbytes / sec / 1e9, 1)}), flush=True)
-        del bufs
-        torch.cuda.empty_cache()
-
-
 def copy_calibration(args):
     """A plain device copy of known size (read N bytes, write N bytes) whose
     FETCH_SIZE / WRITE_SIZE readings calibrate the GEMV's counter values."""
@@ -467,8 +422,6 @@ def main():
                     help="time the gate+up SWIGLU launch against two plain launches")
     ap.add_argument("--wtype", choices=sorted(BLOCK_BYTES), default="q4_K",
                     help="weight format of --sweep and --profile (the headline is Q4_K)")
-    ap.add_argument("--stream-probe", action="store_true",
-                    help="time a plain streaming read of the GEMV byte counts (ceiling)")
     ap.add_argument("--copy-cal", type=int, default=0, metavar="BYTES",
                     help="run only a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -477,9 +430,7 @@ def main():
               "(rows would shard across GPUs through q4k_op_mul_mat_vec_q); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
-    if args.stream_probe:
-        stream_probe(args)
-    elif args.copy_cal:
+    if args.copy_cal:
         copy_calibration(args)
     elif args.profile:
         profile_mode(args)

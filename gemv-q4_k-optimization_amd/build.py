@@ -12,7 +12,6 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libq4k_gemv.so")
-PROBE_LIB = os.path.join(PKG, "libq4k_stream_probe.so")
 ARCH = "gfx950"
 
 
@@ -65,13 +64,6 @@ def build(verbose: bool = False, save_temps: bool = False) -> str:
     tmp = LIB + ".tmp"
     _run([hipcc, "-shared", "-fPIC", "-o", tmp, *dev_objs, host_obj, gguf_obj, "-lpthread"], verbose)
     os.replace(tmp, LIB)
-    # measurement aid for bench.py --stream-probe (not part of the library)
-    probe_obj = os.path.join(BUILD, "stream_probe.o")
-    _run([hipcc, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
-          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-          "-c", os.path.join(CSRC, "stream_probe.hip"), "-o", probe_obj], verbose)
-    _run([hipcc, "-shared", "-fPIC", "-o", PROBE_LIB + ".tmp", probe_obj], verbose)
-    os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
     return LIB
 
 

@@ -207,6 +207,7 @@ int parse(q4k_gguf &g) {
         g.kvs.push_back(std::move(kv));
     }
     g.tensors.reserve((size_t)n_tensors);
+    uint64_t data_size = 0;  // running padded size of the tensors so far
     for (uint64_t i = 0; i < n_tensors; ++i) {
         Tensor t;
         t.name = c.str();
@@ -225,13 +226,18 @@ int parse(q4k_gguf &g) {
         t.rel_offset = c.get<uint64_t>();
         if (!c.ok) return Q4K_EFORMAT;
         const BlockSize bs = block_size(t.type);
-        if (bs.elems) {
-            if (t.ne[0] % bs.elems != 0) return Q4K_EFORMAT;  // rows are whole blocks
-            const uint64_t blocks = nel / bs.elems;
-            if (blocks > UINT64_MAX / bs.bytes) return Q4K_EFORMAT;
-            t.nbytes = blocks * bs.bytes;
-        }
-        if (t.rel_offset % g.alignment != 0) return Q4K_EFORMAT;
+        if (!bs.elems) return Q4K_EFORMAT;  // unknown or removed type: its size is unknown
+        if (t.ne[0] % bs.elems != 0) return Q4K_EFORMAT;  // rows are whole blocks
+        const uint64_t blocks = nel / bs.elems;
+        if (blocks > UINT64_MAX / bs.bytes) return Q4K_EFORMAT;
+        t.nbytes = blocks * bs.bytes;
+        // ggml's loader lays the tensors out back to back in directory
+        // order, each padded to the alignment, and refuses a file whose
+        // offsets differ from that layout (gaps, overlaps, reordering)
+        if (t.rel_offset != data_size) return Q4K_EFORMAT;
+        const uint64_t padded = t.nbytes + (g.alignment - t.nbytes % g.alignment) % g.alignment;
+        if (padded < t.nbytes || data_size > UINT64_MAX - padded) return Q4K_EFORMAT;
+        data_size += padded;
         if (!g.tensor_index.emplace(t.name, (int64_t)g.tensors.size()).second) return Q4K_EFORMAT;
         g.tensors.push_back(std::move(t));
     }
@@ -267,11 +273,14 @@ int q4k_gguf_open(const char *path, q4k_gguf **out) {
     q4k_gguf *g = new (std::nothrow) q4k_gguf();
     if (!g) return Q4K_ENOMEM;
     g->fd = open(path, O_RDONLY | O_CLOEXEC);
-    struct stat st;
-    if (g->fd < 0 || fstat(g->fd, &st) != 0 || st.st_size < 24) {
-        const bool short_file = g->fd >= 0 && st.st_size < 24;
+    struct stat st {};
+    if (g->fd < 0 || fstat(g->fd, &st) != 0) {
         delete g;
-        return short_file ? Q4K_EFORMAT : Q4K_EIO;
+        return Q4K_EIO;
+    }
+    if (st.st_size < 24) {  // shorter than the fixed header
+        delete g;
+        return Q4K_EFORMAT;
     }
     g->size = (size_t)st.st_size;
     void *m = mmap(nullptr, g->size, PROT_READ, MAP_PRIVATE, g->fd, 0);

@@ -609,32 +609,51 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(Q4K_GEMV_KER
     }
 }
 
-// ggml-cuda quantize_q8_1 arithmetic, one value per lane, 32 lanes per block:
-// amax and sum reduced over the 32 lanes with xor distances 16, 8, 4, 2, 1.
+// F32 -> AoS block_q8_1 with ggml-cuda's quantize_q8_1 arithmetic (call site
+// kernels/mmvq.cu:728-735): per 32 values d = amax/127 (div127, the IEEE
+// quotient), q = roundf(x/d) (quantize_values), ds = (half(d), half(sum x)).
+// Eight lanes per block, four values (one 16-byte load) per lane, 32 blocks
+// per 256-thread workgroup.  amax is order-free; the sum follows the tree of
+// ggml's 32-lane warp_reduce_sum (partners at element distance 16, 8, 4, 2,
+// 1), which with element 4e + k in lane e is lane distance 4, 2, 1 and then
+// k ^ 2, k ^ 1 inside the lane, so ds.y is bit for bit ggml's.
 __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float *__restrict__ x,
                                                             uint8_t *__restrict__ vy, int64_t ne00,
-                                                            int64_t s01, int64_t ne0) {
-    const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i0 >= ne0) return;  // ne0 % 32 == 0: whole 32-lane groups leave together
+                                                            int64_t s01, int64_t nblk_col, int vec_ok) {
+    const int64_t blk = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    if (blk >= nblk_col) return;  // whole 8-lane groups leave together
+    const int e = threadIdx.x & 7;
     const int64_t col = blockIdx.y;
-    const float xi = i0 < ne00 ? x[col * s01 + i0] : 0.0f;
-    float amax = fabsf(xi);
-    float sum = xi;
-    amax = fmaxf(amax, swizzle_xor<16>(amax)); sum += swizzle_xor<16>(sum);
-    amax = fmaxf(amax, swizzle_xor<8>(amax));  sum += swizzle_xor<8>(sum);
-    amax = fmaxf(amax, swizzle_xor<4>(amax));  sum += swizzle_xor<4>(sum);
-    amax = fmaxf(amax, swizzle_xor<2>(amax));  sum += swizzle_xor<2>(sum);
-    amax = fmaxf(amax, swizzle_xor<1>(amax));  sum += swizzle_xor<1>(sum);
-    const float d = amax / 127.0f;
-    const int q = amax == 0.0f ? 0 : (int)roundf(xi / d);
-    const int64_t ic = col * ne0 + i0;
-    uint8_t *blk = vy + (ic / 32) * kQ81Bytes;
-    const int iqs = (int)(ic & 31);
-    blk[4 + iqs] = (uint8_t)(int8_t)q;
-    if (iqs == 0) {
+    const int64_t i0 = blk * 32 + 4 * e;
+    const float *src = x + col * s01 + i0;
+    float v[4];
+    if (vec_ok && i0 + 4 <= ne00) {
+        const float4 a = *reinterpret_cast<const float4 *>(src);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = i0 + k < ne00 ? src[k] : 0.0f;
+    }
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = block_max<8>(amax);
+    float t[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) t[k] = v[k] + swizzle_xor<4>(v[k]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) t[k] += dppf<kDppXor2>(t[k]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) t[k] += dppf<kDppXor1>(t[k]);
+    const float sum = (t[0] + t[2]) + (t[1] + t[3]);
+    const float d = div127(amax);
+    uint32_t word[1] = {0u};
+    int qsum[1];
+    if (amax != 0.0f) quantize_values<4, 1>(v, d, __builtin_amdgcn_rcpf(d), word, qsum);
+    uint8_t *out = vy + (col * nblk_col + blk) * kQ81Bytes;
+    *reinterpret_cast<uint32_t *>(out + 4 + 4 * e) = word[0];
+    if (e == 0) {
         const uint16_t dh = __builtin_bit_cast(uint16_t, (_Float16)d);
         const uint16_t sh = __builtin_bit_cast(uint16_t, (_Float16)sum);
-        *reinterpret_cast<uint32_t *>(blk) = (uint32_t)dh | ((uint32_t)sh << 16);
+        *reinterpret_cast<uint32_t *>(out) = (uint32_t)dh | ((uint32_t)sh << 16);
     }
 }
 
@@ -738,34 +757,11 @@ int ensure_lds(DeviceInfo *di, const void *fn, int bytes) {
     return Q4K_OK;
 }
 
-static int env_int(const char *name, int dflt) {
-    const char *v = std::getenv(name);
-    return v && *v ? std::atoi(v) : dflt;
-}
-
-// Geometry overrides for tuning sweeps (0 = automatic): set through
-// q4k_set_geometry_override or, as start-up defaults, the environment
-// variables Q4K_ROWS, Q4K_WAVES and Q4K_WGS.
-std::atomic<int> g_ovr_rows{-1}, g_ovr_waves{-1}, g_ovr_wgs{-1}, g_ovr_kernel{-1};
-std::atomic<int> g_ovr_prologue{-1}, g_ovr_slots{-1};
-
-void load_env_overrides() {
-    static std::once_flag once;
-    std::call_once(once, []() {
-        int expect = -1;
-        g_ovr_rows.compare_exchange_strong(expect, env_int("Q4K_ROWS", 0));
-        expect = -1;
-        g_ovr_waves.compare_exchange_strong(expect, env_int("Q4K_WAVES", 0));
-        expect = -1;
-        g_ovr_wgs.compare_exchange_strong(expect, env_int("Q4K_WGS", 0));
-        expect = -1;
-        g_ovr_kernel.compare_exchange_strong(expect, env_int("Q4K_KERNEL", 0));
-        expect = -1;
-        g_ovr_prologue.compare_exchange_strong(expect, env_int("Q4K_PROLOGUE", -1));
-        expect = -1;
-        g_ovr_slots.compare_exchange_strong(expect, env_int("Q4K_SLOTS", 0));
-    });
-}
+// Geometry overrides for tuning sweeps (0 = automatic; prologue -1 =
+// automatic), set only through q4k_set_geometry_override and
+// q4k_set_pipeline_override: nothing is read from the environment.
+std::atomic<int> g_ovr_rows{0}, g_ovr_waves{0}, g_ovr_wgs{0}, g_ovr_kernel{0};
+std::atomic<int> g_ovr_prologue{-1}, g_ovr_slots{0};
 
 struct Geometry {
     int R = 2;          // tile kernel: rows per wave tile
@@ -824,7 +820,6 @@ static int lds_bytes_linear(int K) { return K + K / 4; }
 //    groups in flight).
 static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int fused = 0,
                               int64_t mats = 1) {
-    load_env_overrides();
     Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
@@ -1224,15 +1219,20 @@ int q4k_quantize_row_q8_1(const float *x, void *vy, int64_t ne00, int64_t s01, i
     if (ne00 < 0 || ne1 < 0 || ne0 < ne00 || ne0 % 32 != 0) return Q4K_EINVAL;
     if (ne0 == 0 || ne1 == 0) return Q4K_OK;
     if (!x || !vy || (ne1 > 1 && s01 < ne00) || ne1 > 65535) return Q4K_EINVAL;
-    if (ne0 > ((int64_t)1 << 38)) return Q4K_EUNSUPPORTED;  // grid.x = ne0 / 256 < 2^31
+    if (ne0 > ((int64_t)1 << 38)) return Q4K_EUNSUPPORTED;  // grid.x = ne0 / 1024 < 2^31
     if (!aligned(vy, 4)) return Q4K_EINVAL;
     DeviceInfo *di = nullptr;
     int st = device_info(&di);
     if (st != Q4K_OK) return st;
-    const dim3 grid((unsigned)((ne0 + 255) / 256), (unsigned)ne1);
-    hipLaunchKernelGGL(quantize_q8_1_kernel, grid, dim3(256), 0, (hipStream_t)stream, x,
-                       static_cast<uint8_t *>(vy), ne00, s01, ne0);
-    hipError_t e = hipGetLastError();
+    int64_t nblk_col = ne0 / 32;
+    int vec_ok = aligned(x, 16) && s01 % 4 == 0;
+    uint8_t *y = static_cast<uint8_t *>(vy);
+    void *args[] = {&x, &y, &ne00, &s01, &nblk_col, &vec_ok};
+    // the launch's own status (hipGetLastError would also report, and clear,
+    // an error a caller's earlier unrelated call left behind)
+    const hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(&quantize_q8_1_kernel),
+                                         dim3((unsigned)((nblk_col + 31) / 32), (unsigned)ne1), dim3(256), args,
+                                         0, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e);
     return Q4K_OK;
 }
@@ -1492,9 +1492,9 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
         const int64_t items = ne01 * p.G;
         int grid = (int)((items + 3) / 4);
         if (grid > di->cus * 8) grid = di->cus * 8;
-        hipLaunchKernelGGL(subblock_sums_kernel, dim3(grid), dim3(256), (size_t)lds,
-                           (hipStream_t)stream, p);
-        hipError_t e = hipGetLastError();
+        void *args[] = {&p};
+        const hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(&subblock_sums_kernel), dim3(grid),
+                                             dim3(256), args, (size_t)lds, (hipStream_t)stream);
         if (e != hipSuccess) return hip_fail(e);
     }
     return Q4K_OK;
@@ -1507,7 +1507,6 @@ int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32
     if (rows_per_tile != 0 && rows_per_tile != 1 && rows_per_tile != 2 && rows_per_tile != 4)
         return Q4K_EINVAL;
     if (waves_per_wg < 0 || waves_per_wg > 16) return Q4K_EINVAL;
-    load_env_overrides();
     g_ovr_rows.store(rows_per_tile);
     g_ovr_waves.store(waves_per_wg);
     g_ovr_wgs.store(workgroups);
@@ -1518,7 +1517,6 @@ int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32
 int q4k_set_pipeline_override(int32_t slots, int32_t prologue) {
     if (slots != 0 && slots != 1 && slots != 2 && slots != 4 && slots != 8) return Q4K_EINVAL;
     if (prologue < -1 || prologue > 3) return Q4K_EINVAL;
-    load_env_overrides();
     g_ovr_slots.store(slots);
     g_ovr_prologue.store(prologue);
     return Q4K_OK;

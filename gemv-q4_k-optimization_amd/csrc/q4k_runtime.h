@@ -40,11 +40,10 @@ int device_info(DeviceInfo **out);
 // Raises a kernel's dynamic-LDS limit once when it asks for more than 64 KB.
 int ensure_lds(DeviceInfo *di, const void *fn, int bytes);
 
-// Geometry overrides for tuning sweeps (0 = automatic, -1 = not yet read from
-// the environment).
+// Geometry overrides for tuning sweeps (0 = automatic, prologue -1 =
+// automatic), set through the q4k_set_*_override entry points only.
 extern std::atomic<int> g_ovr_rows, g_ovr_waves, g_ovr_wgs, g_ovr_kernel;
 extern std::atomic<int> g_ovr_prologue, g_ovr_slots;
-void load_env_overrides();
 
 // Fused epilogue of a one-column product (the fields of ggml's
 // ggml_cuda_mm_fusion_args_device, kernels/mmvq.cu:692-715): an optional

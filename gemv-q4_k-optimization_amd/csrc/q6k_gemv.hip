@@ -404,7 +404,6 @@ struct Q6Geometry {
 // delay the activation loads more than they hide latency.
 static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int64_t mats = 1,
                                    int fused = kFusedNone) {
-    load_env_overrides();
     Q6Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
@@ -659,8 +658,9 @@ int q6k_group_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, c
         const int64_t items = ne01 * p.G;
         int grid = (int)((items + 3) / 4);
         if (grid > di->cus * 8) grid = di->cus * 8;
-        hipLaunchKernelGGL(q6_group_sums_kernel, dim3(grid), dim3(256), (size_t)lds, (hipStream_t)stream, p);
-        hipError_t e = hipGetLastError();
+        void *args[] = {&p};
+        const hipError_t e = hipLaunchKernel(reinterpret_cast<const void *>(&q6_group_sums_kernel), dim3(grid),
+                                             dim3(256), args, (size_t)lds, (hipStream_t)stream);
         if (e != hipSuccess) return hip_fail(e);
     }
     return Q4K_OK;

@@ -8,13 +8,13 @@
  * stream (passed as void *, NULL = the null stream) with no host
  * synchronisation, like the reference, which runs on ctx.stream().
  *
- * Memory: src0, src1 and dst are caller-owned device buffers.  The library
- * allocates nothing on the hot path; q4k_mul_mat_vec_q only falls back to a
+ * Memory: src0, src1 and dst are caller-owned device buffers.  Most calls
+ * allocate nothing: the activation is quantised inside the GEMV launch.
+ * q4k_mul_mat_vec_q and q6k_mul_mat_vec_q do allocate when the activation
+ * does not fit one workgroup's LDS and no workspace is passed: a
  * stream-ordered temporary (hipMallocAsync/hipFreeAsync, the counterpart of
- * ggml's ctx.pool()) for shapes whose activation does not fit one
- * workgroup's LDS when no workspace is passed.  A caller with a pool (as
- * ggml has) should pass a workspace: it also speeds up several long
- * columns.
+ * ggml's ctx.pool()) for the Q8_1 copy.  A caller with a pool (as ggml has)
+ * should pass a workspace: it also speeds up several long columns.
  *
  * Threading: entry points may be called from any host thread; per-device
  * state is initialised once under a lock.  Calls that share a stream are
@@ -262,11 +262,10 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * variant; reduced to 8 where 16 would not fit the registers), the number
  * of workgroups and the kernel (1 tile kernel, 2 block-per-lane, 3
  * coalesced block kernel where they apply); 0 restores the automatic
- * choice.  The environment variables Q4K_ROWS, Q4K_WAVES, Q4K_WGS and
- * Q4K_KERNEL give start-up values (Q4K_SLOTS and Q4K_PROLOGUE select the
- * tile kernel's pipeline depth and prologue order).  Not part of the
- * reference interface: a benchmarking knob (ggml's counterpart is editing
- * the compile-time tables of kernels/mmvq.cu:95-147). */
+ * choice.  Nothing is read from the environment: until this is called the
+ * geometry is automatic.  Not part of the reference interface: a
+ * benchmarking knob (ggml's counterpart is editing the compile-time tables
+ * of kernels/mmvq.cu:95-147). */
 int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32_t workgroups,
                               int32_t kernel);
 
@@ -275,9 +274,8 @@ int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32
  * 0 = automatic) and when the first weight loads are issued relative to the
  * activation quantisation (0 = the first two groups before it, 1 = all
  * after, 2 = all before, 3 = one before; -1 = automatic).  Values a kernel
- * has no variant for fall back to the automatic choice.  Start-up values
- * come from Q4K_SLOTS and Q4K_PROLOGUE.  Not part of the reference
- * interface: a benchmarking knob. */
+ * has no variant for fall back to the automatic choice.  Not part of the
+ * reference interface: a benchmarking knob. */
 int q4k_set_pipeline_override(int32_t slots, int32_t prologue);
 
 /* ------------------------------------------------------------ host side */

@@ -50,14 +50,17 @@ typedef struct q4k_gguf_tensor_info {
     int32_t n_dims;     /* 1..4 */
     int64_t ne[4];      /* elements per dimension, ggml order (ne[0] = row length); 1 past n_dims */
     uint64_t offset;    /* byte offset of the data from the start of the file */
-    uint64_t nbytes;    /* bytes of the data; 0 for a type whose block size is unknown here */
+    uint64_t nbytes;    /* bytes of the data (whole blocks of its type) */
     const void *data;   /* the data in the read-only mapping of the file */
 } q4k_gguf_tensor_info;
 
-/* Opens and validates a GGUF file.  Q4K_EFORMAT: not a GGUF v2/v3 file, or
- * a count, length, dimension, type or offset that does not fit the file;
- * Q4K_EIO: the file cannot be opened or mapped; Q4K_ENOMEM; Q4K_EINVAL:
- * null arguments. */
+/* Opens and validates a GGUF file.  Q4K_EFORMAT: not a GGUF v2/v3 file, a
+ * count, length or dimension that does not fit the file, a tensor type
+ * whose block size is unknown (including the types ggml removed), or tensor
+ * offsets other than ggml's layout (each tensor right after the previous
+ * one, padded to the alignment, in directory order; ggml's loader refuses
+ * the same files); Q4K_EIO: the file cannot be opened, inspected or mapped;
+ * Q4K_ENOMEM; Q4K_EINVAL: null arguments. */
 int q4k_gguf_open(const char *path, q4k_gguf **out);
 void q4k_gguf_close(q4k_gguf *g);
 

@@ -116,7 +116,9 @@ def test_every_truncation_is_refused(Q, tmp_path):
 
 @pytest.mark.parametrize("case", ["magic", "version1", "version4", "ndims5", "ndims0", "offset_past_end",
                                   "misaligned", "dup_tensor", "dup_key", "partial_block", "bad_alignment",
-                                  "alignment_type", "bad_value_type", "huge_count", "huge_string"])
+                                  "alignment_type", "bad_value_type", "huge_count", "huge_string",
+                                  "unknown_type", "removed_type", "offset_gap", "offset_overlap",
+                                  "offset_order"])
 def test_malformed_files_are_refused(Q, tmp_path, case):
     tensors = [("w", 12, [256, 2], bytes(288))]
     kvs = [("a", W.UINT32, 7)]
@@ -148,6 +150,16 @@ def test_malformed_files_are_refused(Q, tmp_path, case):
     elif case == "bad_value_type":
         raw = W.gguf_bytes(kvs, tensors).replace(struct.pack("<Q", 1) + b"a" + struct.pack("<I", 4),
                                                  struct.pack("<Q", 1) + b"a" + struct.pack("<I", 13), 1)
+    elif case == "unknown_type":
+        raw = W.gguf_bytes(kvs, [("w", 99, [256, 2], bytes(288))])
+    elif case == "removed_type":   # 4 was Q4_2, removed from ggml
+        raw = W.gguf_bytes(kvs, [("w", 4, [32, 2], bytes(40))])
+    elif case == "offset_gap":     # aligned, in bounds, but not where ggml expects it
+        raw = W.gguf_bytes(kvs, tensors, offsets=[32]) + bytes(32)
+    elif case == "offset_overlap":
+        raw = W.gguf_bytes(kvs, tensors + [("x", 0, [8], bytes(32))], offsets=[0, 0])
+    elif case == "offset_order":   # both tensors present, in the opposite order of the directory
+        raw = W.gguf_bytes(kvs, [("x", 0, [8], bytes(32))] + tensors, offsets=[288, 0]) + bytes(32)
     elif case == "huge_count":
         raw = b"GGUF" + struct.pack("<IQQ", 3, 1 << 40, 0) + bytes(64)
     else:  # huge_string: a key length far past the end of the file

@@ -44,7 +44,7 @@ def oracle_rows(O, wq, K, q8, rows):
 # --------------------------------------------------------------- Q8_1 ----
 @pytest.mark.parametrize("N,K,kpad,ld", [(1, 4096, 4096, 4096), (3, 4096, 4096, 4160),
                                          (2, 14336, 14336, 14336), (1, 300, 512, 320),
-                                         (8, 8192, 8192, 8192)])
+                                         (8, 8192, 8192, 8192), (2, 301, 512, 301), (3, 1000, 1024, 1003)])
 def test_quantize_q8_1_bytes_exact(Q, O, gpu, N, K, kpad, ld):
     import torch
     x = np.zeros((N, ld), np.float32)
@@ -55,6 +55,83 @@ def test_quantize_q8_1_bytes_exact(Q, O, gpu, N, K, kpad, ld):
     Q._check(Q.lib().q4k_quantize_row_q8_1(Q._ptr(xd), Q._ptr(out), K, ld, kpad, N, Q._stream()), "q8_1")
     ref = np.stack([O.quantize_q8_1(x[c:c + 1, :K], k_padded=kpad)[0] for c in range(N)])
     assert np.array_equal(out.cpu().numpy(), ref)
+
+
+def test_quantize_q8_1_exact_ties(Q, O, gpu):
+    """Values on exact ties x/d = k + 1/2 (d = 2^e) and their one-ulp
+    neighbours: the standalone quantiser's bytes equal the oracle's
+    (roundf: ties away from zero)."""
+    import torch
+    rng = np.random.default_rng(78)
+    nblk = 128
+    e = rng.integers(-20, 10, size=nblk)
+    t = rng.integers(-127, 127, size=(nblk, 32)).astype(np.float64) + 0.5
+    t[:, 0] = 127.0
+    x = (t * 2.0 ** e[:, None]).astype(np.float32)
+    x[1::3, 2:] = np.nextafter(x[1::3, 2:], np.float32(np.inf))
+    x[2::3, 2:] = np.nextafter(x[2::3, 2:], np.float32(-np.inf))
+    x = x.reshape(2, -1)
+    K = x.shape[1]
+    xd = to_dev(x, gpu)
+    out = torch.empty((2, K // 32 * 36), dtype=torch.uint8, device=gpu)
+    Q._check(Q.lib().q4k_quantize_row_q8_1(Q._ptr(xd), Q._ptr(out), K, K, K, 2, Q._stream()), "q8_1")
+    assert np.array_equal(out.cpu().numpy(), O.quantize_q8_1(x, k_padded=K))
+
+
+def _hip_runtime():
+    """The HIP runtime this process already uses (the one torch loaded)."""
+    import ctypes
+    paths = sorted({ln.split()[-1] for ln in open("/proc/self/maps") if "libamdhip64" in ln})
+    assert len(paths) == 1, paths
+    hip = ctypes.CDLL(paths[0])
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMalloc.restype = ctypes.c_int
+    hip.hipGetLastError.restype = ctypes.c_int
+    hip.hipPeekAtLastError.restype = ctypes.c_int
+    hip.hipGetDevice.argtypes = [ctypes.POINTER(ctypes.c_int)]
+    return hip
+
+
+def test_caller_error_is_left_alone(Q, O, gpu):
+    """An error a caller's earlier HIP call left behind (a failed huge
+    hipMalloc) is neither returned nor cleared by successful calls of the
+    library: every launch checks its own status.  Covers the workspace route
+    (standalone quantiser + GEMV), the in-launch route and the probes."""
+    import ctypes
+    import torch
+    hip = _hip_runtime()
+    M, K, N = 300, 14336, 4
+    wq, x = inputs(Q, M, K, N, seed=8)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    ws = torch.empty(Q.q8_1_bytes(K, N), dtype=torch.uint8, device=gpu)
+    dst = torch.empty((N, M), dtype=torch.float32, device=gpu)
+    q8 = torch.empty((N, Q.q8_1_bytes(K, 1)), dtype=torch.uint8, device=gpu)
+    sqq = torch.empty((1, M, K // 32), dtype=torch.int32, device=gpu)
+    sq = torch.empty((1, K // 32), dtype=torch.int32, device=gpu)
+    torch.cuda.synchronize()
+    L, s = Q.lib(), Q._stream()
+    hip.hipGetLastError()
+    p = ctypes.c_void_p()
+    err = hip.hipMalloc(ctypes.byref(p), 1 << 62)
+    assert err != 0
+    dev = ctypes.c_int()
+    hip.hipGetDevice(ctypes.byref(dev))
+    if hip.hipPeekAtLastError() != err:
+        hip.hipGetLastError()
+        pytest.skip("this HIP runtime resets the last error on every successful call")
+    assert L.q4k_mul_mat_vec_q(Q._ptr(wd), K, M, K // 256 * 144, Q._ptr(xd), N, K * 4, Q._ptr(dst), M * 4,
+                               Q._ptr(ws), ws.numel(), s) == Q.Q4K_OK
+    assert L.q4k_mul_mat_vec_q(Q._ptr(wd), K, M, K // 256 * 144, Q._ptr(xd), 1, K * 4, Q._ptr(dst), M * 4,
+                               None, 0, s) == Q.Q4K_OK
+    assert L.q4k_quantize_row_q8_1(Q._ptr(xd), Q._ptr(q8), K, K, K, N, s) == Q.Q4K_OK
+    assert L.q4k_subblock_sums(Q._ptr(wd), K, M, K // 256 * 144, Q._ptr(q8), 1, K // 32, Q._ptr(sqq),
+                               Q._ptr(sq), s) == Q.Q4K_OK
+    assert hip.hipGetLastError() == err
+    assert hip.hipGetLastError() == 0
+    torch.cuda.synchronize()
+    ref = O.gemv_q4K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, dst.cpu().numpy()[:1], {k: v[:1] for k, v in ref.items() if v is not None},
+                                    "after error")
 
 
 # ---------------------------------------------------------- int sums ----
