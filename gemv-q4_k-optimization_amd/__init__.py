@@ -18,7 +18,8 @@ import numpy as np
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libq4k_gemv.so")
 
-Q4K_OK, Q4K_EUNSUPPORTED, Q4K_EINVAL, Q4K_EHIP, Q4K_ENOMEM, Q4K_EIO, Q4K_EFORMAT = 0, 1, 2, 3, 4, 5, 6
+Q4K_OK, Q4K_EUNSUPPORTED, Q4K_EINVAL, Q4K_EHIP, Q4K_ENOMEM, Q4K_EIO, Q4K_EFORMAT, Q4K_ESCRATCH = 0, 1, 2, 3, 4, 5, 6, 7
+NOALLOC_SCRATCH_BYTES = 1 << 20
 GGML_TYPE_F32, GGML_TYPE_Q8_1, GGML_TYPE_Q4_K, GGML_TYPE_Q6_K = 0, 9, 12, 14
 QK_K = 256
 BLOCK_Q4_K_BYTES = 144
@@ -44,6 +45,7 @@ SIGNATURES = {
     "q4k_q8_1_bytes": (ctypes.c_size_t, [_I64, _I64]),
     "q4k_quantize_row_q8_1": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "q4k_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, ctypes.c_size_t, _P]),
+    "q4k_mul_mat_vec_q_noalloc": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
     "q4k_op_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
     "q4k_ggml_mul_mat_vec_q": (_I, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "q4k_subblock_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P]),

@@ -1202,6 +1202,7 @@ const char *q4k_strerror(int status) {
         case Q4K_ENOMEM: return "out of memory";
         case Q4K_EIO: return "file could not be opened, read or mapped";
         case Q4K_EFORMAT: return "not a valid GGUF v2/v3 file";
+        case Q4K_ESCRATCH: return "the activation's Q8_1 copy exceeds the allocation-free entry point's 1 MiB scratch";
         default: return "unknown status";
     }
 }
@@ -1286,6 +1287,66 @@ int q4k_mul_mat_vec_q(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
         if (e != hipSuccess && st == Q4K_OK) st = hip_fail(e);
     }
     return st;
+}
+
+}  // extern "C"
+
+namespace q4k {
+
+// Scratch of the allocation-free entry point: the Q8_1 copy of the
+// activation, in a file-scope device array instead of a workspace or a
+// stream-ordered temporary.  Every device holds its own copy until the
+// process ends.  Host code never uses the array's name (a host-side stand-in,
+// not a device address) but the address hipGetSymbolAddress returns for the
+// current device, looked up once per device.
+constexpr size_t kNoAllocScratchBytes = (size_t)1 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+struct ScratchSlot {
+    std::once_flag once;
+    void *ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+static ScratchSlot g_scratch[kMaxDevices];
+
+static int scratch_for_current_device(void **out) {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e);
+    if (dev < 0 || dev >= kMaxDevices) return Q4K_EUNSUPPORTED;
+    ScratchSlot &sl = g_scratch[dev];
+    std::call_once(sl.once, [&sl]() {
+        void *p = nullptr;
+        sl.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (sl.err == hipSuccess) sl.ptr = p;
+    });
+    if (sl.err != hipSuccess) return hip_fail(sl.err);
+    if (!sl.ptr) return hip_fail(hipErrorInvalidSymbol);
+    *out = sl.ptr;
+    return Q4K_OK;
+}
+
+}  // namespace q4k
+
+extern "C" {
+
+int q4k_mul_mat_vec_q_noalloc(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *src1,
+                              int64_t ne11, int64_t nb11, float *dst, int64_t nb1, void *stream) {
+    int st = check_weight(src0, ne00, ne01, nb01);
+    if (st != Q4K_OK) return st;
+    if (ne11 < 0 || ne11 > Q4K_MAX_BATCH) return Q4K_EINVAL;
+    if (ne01 == 0 || ne11 == 0) return Q4K_OK;
+    if (q4k_q8_1_bytes(ne00, ne11) > kNoAllocScratchBytes) return Q4K_ESCRATCH;
+    DeviceInfo *di = nullptr;
+    st = device_info(&di);
+    if (st != Q4K_OK) return st;
+    void *ws = nullptr;
+    st = scratch_for_current_device(&ws);
+    if (st != Q4K_OK) return st;
+    // with a workspace that holds the Q8_1 copy, q4k_mul_mat_vec_q never
+    // allocates: it quantises in-launch or into the workspace
+    return q4k_mul_mat_vec_q(src0, ne00, ne01, nb01, src1, ne11, nb11, dst, nb1, ws, kNoAllocScratchBytes,
+                             stream);
 }
 
 int q4k_op_mul_mat_vec_q(const void *src0_dd_i, int64_t ne00, int64_t row_low, int64_t row_high,

@@ -51,7 +51,11 @@ typedef enum q4k_status {
     /* A file could not be opened, read or mapped (GGUF reader). */
     Q4K_EIO = 5,
     /* A file is not a valid GGUF v2/v3 file (GGUF reader). */
-    Q4K_EFORMAT = 6
+    Q4K_EFORMAT = 6,
+    /* q4k_mul_mat_vec_q_noalloc: q4k_q8_1_bytes(ne00, ne11) exceeds its
+     * fixed device scratch (Q4K_NOALLOC_SCRATCH_BYTES); nothing was
+     * launched. */
+    Q4K_ESCRATCH = 7
 } q4k_status;
 
 /* ggml type ids used in descriptors (values of ggml's enum ggml_type) */
@@ -146,6 +150,23 @@ int q4k_quantize_row_q8_1(const float *x, void *vy, int64_t ne00, int64_t s01, i
 int q4k_mul_mat_vec_q(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
                       const float *src1, int64_t ne11, int64_t nb11, float *dst, int64_t nb1,
                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* Allocation-free form of q4k_mul_mat_vec_q (same arguments without the
+ * workspace, same results bit for bit).  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory -- code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  It
+ * calls no hipMalloc/hipFree or allocating library routine; the Q8_1 copy
+ * of the activation, when the route needs one, goes to a file-scope device
+ * scratch of Q4K_NOALLOC_SCRATCH_BYTES that each GPU holds until the process
+ * ends.  Limit: q4k_q8_1_bytes(ne00, ne11) <= Q4K_NOALLOC_SCRATCH_BYTES
+ * (8 columns of up to 116224 values each, one column of up to 931840),
+ * otherwise Q4K_ESCRATCH.  All calls on one GPU share its scratch: calls
+ * that overlap in time on one GPU (different streams or host threads
+ * without ordering between them) race; serialise them. */
+#define Q4K_NOALLOC_SCRATCH_BYTES ((size_t)1 << 20)
+int q4k_mul_mat_vec_q_noalloc(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
+                              const float *src1, int64_t ne11, int64_t nb11, float *dst, int64_t nb1,
+                              void *stream);
 
 /* Row-slice GEMV on an already-quantised activation.  Replaces
  * ggml_cuda_op_mul_mat_vec_q(ctx, src0, src1, dst, src0_dd_i, src1_ddf_i,

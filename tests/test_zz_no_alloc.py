@@ -1,0 +1,67 @@
+"""The allocation-free entry point q4k_mul_mat_vec_q_noalloc (through the C
+ABI) against q4k_mul_mat_vec_q with a caller workspace, bit for bit, on calls
+in a row, each smaller than the one before, so that the scratch still holds
+the previous call's Q8_1 bytes.  The shapes take the routes that use the
+scratch (a quantisation launch of its own for several long columns; column
+chunks when the activation does not fit the LDS) and one that does not
+(quantisation inside the GEMV launch).  A request beyond the scratch is
+refused with Q4K_ESCRATCH before anything is launched."""
+import numpy as np
+import pytest
+
+import _common
+
+pytestmark = pytest.mark.gpu
+
+# (M, K, N), largest first: column chunks (28672 x 8 values do not fit the
+# LDS), the quantisation launch (14336 x 4 > 40960 values), then in-launch
+CALLS = [(300, 28672, 8), (150, 14336, 4), (64, 4096, 2)]
+
+
+def _noalloc(Q, wd, M, K, xd, N, dst):
+    return Q.lib().q4k_mul_mat_vec_q_noalloc(Q._ptr(wd), K, M, K // 256 * 144, Q._ptr(xd), N, K * 4,
+                                            Q._ptr(dst), M * 4, Q._stream())
+
+
+def test_noalloc_equals_workspace_route(Q, O, gpu):
+    import torch
+    for M, K, N in CALLS:
+        print(f"[noalloc] {M}x{K} N={N}", flush=True)
+        wq = Q.quantize_rows_q4_K(_common.weights(M, K, seed=M), nthreads=16)
+        x = _common.activations(N, K, seed=K)
+        wd = torch.from_numpy(wq).to(gpu)
+        xd = torch.from_numpy(x).to(gpu)
+        ws = torch.empty(Q.q8_1_bytes(K, N), dtype=torch.uint8, device=gpu)
+        ref = Q.mul_mat_vec_q(wd, K, xd, workspace=ws)
+        dst = torch.full((N, M), -7.0, dtype=torch.float32, device=gpu)
+        assert _noalloc(Q, wd, M, K, xd, N, dst) == Q.Q4K_OK
+        torch.cuda.synchronize()
+        got = dst.cpu().numpy()
+        assert np.array_equal(got, ref.cpu().numpy()), f"{M}x{K} N={N}"
+        # and the oracle's bar, on a row sample
+        rows = np.arange(0, M, 7)
+        oref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
+        _common.assert_within_tolerance(O, got[:, rows], oref, f"noalloc {M}x{K} N={N}")
+
+
+def test_noalloc_refuses_requests_beyond_the_scratch(Q, gpu):
+    import torch
+    M, K, N = 2, 131072, 8   # 8 x 4096 Q8_1 blocks = 1,179,648 bytes > 1 MiB
+    assert Q.q8_1_bytes(K, N) > Q.NOALLOC_SCRATCH_BYTES
+    wq = Q.quantize_rows_q4_K(_common.weights(M, K, seed=5), nthreads=16)
+    wd = torch.from_numpy(wq).to(gpu)
+    xd = torch.from_numpy(_common.activations(N, K, seed=5)).to(gpu)
+    dst = torch.full((N, M), -7.0, dtype=torch.float32, device=gpu)
+    assert _noalloc(Q, wd, M, K, xd, N, dst) == Q.Q4K_ESCRATCH
+    torch.cuda.synchronize()
+    assert (dst.cpu().numpy() == -7.0).all()
+    # two columns of 65536 values (589,824 Q8_1 bytes, beyond the LDS) fit and
+    # equal the allocating route (a stream-ordered temporary)
+    K2, N2 = 65536, 2
+    wq2 = Q.quantize_rows_q4_K(_common.weights(M, K2, seed=6), nthreads=16)
+    wd2 = torch.from_numpy(wq2).to(gpu)
+    xd2 = torch.from_numpy(_common.activations(N2, K2, seed=6)).to(gpu)
+    dst2 = torch.full((N2, M), -7.0, dtype=torch.float32, device=gpu)
+    assert _noalloc(Q, wd2, M, K2, xd2, N2, dst2) == Q.Q4K_OK
+    torch.cuda.synchronize()
+    assert np.array_equal(dst2.cpu().numpy(), Q.mul_mat_vec_q(wd2, K2, xd2).cpu().numpy())
