@@ -46,6 +46,10 @@ SIGNATURES = {
     "q4k_quantize_row_q8_1": (_I, [_P, _P, _I64, _I64, _I64, _I64, _P]),
     "q4k_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, ctypes.c_size_t, _P]),
     "q4k_mul_mat_vec_q_noalloc": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
+    "q4k_mul_mat_vec_q_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, ctypes.c_size_t,
+                                    _P, _P, _P]),
+    "q6k_mul_mat_vec_q_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, ctypes.c_size_t,
+                                    _P, _P]),
     "q4k_op_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
     "q4k_ggml_mul_mat_vec_q": (_I, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "q4k_subblock_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P]),
@@ -217,6 +221,31 @@ def mul_mat_vec_q(w_q, K: int, x, out=None, workspace=None, stream=None, wtype: 
     _check(fn(_ptr(w_q), K, M, w_q.stride(0), _ptr(x), N, x.stride(0) * 4, _ptr(out), out.stride(0) * 4,
               _ptr(workspace), ws_bytes, _stream(stream)), name)
     return out
+
+
+def mul_mat_vec_q_sums(w_q, K: int, x, workspace=None, stream=None, wtype: int = GGML_TYPE_Q4_K):
+    """The parity form of mul_mat_vec_q: the production launch's SUMS
+    variant.  Returns (dst F32 [N, M], sums int32, sq int32 or None): Q4_K
+    sums [N, M, K/32] of q4*q8 per sub-block and sq [N, K/32] of q8; Q6_K
+    sums [N, M, K/16] of (q - 32)*q8 per 16-weight group."""
+    import torch
+    M = w_q.shape[0]
+    N = x.shape[0]
+    dev = x.device
+    out = torch.empty((N, M), dtype=torch.float32, device=dev)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    args = (_ptr(w_q), K, M, w_q.stride(0), _ptr(x), N, x.stride(0) * 4, _ptr(out), out.stride(0) * 4,
+            _ptr(workspace), ws_bytes)
+    if wtype == GGML_TYPE_Q4_K:
+        sums = torch.empty((N, M, K // 32), dtype=torch.int32, device=dev)
+        sq = torch.empty((N, K // 32), dtype=torch.int32, device=dev)
+        _check(lib().q4k_mul_mat_vec_q_sums(*args, _ptr(sums), _ptr(sq), _stream(stream)), "q4k_mul_mat_vec_q_sums")
+        return out, sums, sq
+    if wtype == GGML_TYPE_Q6_K:
+        sums = torch.empty((N, M, K // 16), dtype=torch.int32, device=dev)
+        _check(lib().q6k_mul_mat_vec_q_sums(*args, _ptr(sums), _stream(stream)), "q6k_mul_mat_vec_q_sums")
+        return out, sums, None
+    raise ValueError(f"weight type {wtype} has no GEMV here")
 
 
 def mul_mat_vec_q_fused(w_q, K: int, x, gate=None, x_bias=None, gate_bias=None, glu_op: int = GLU_OP_SWIGLU,

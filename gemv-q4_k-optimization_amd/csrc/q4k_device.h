@@ -374,10 +374,12 @@ __device__ __forceinline__ void block_sums(int v, int &half, int &full) {
     full = v;
 }
 
+// sq_out (parity variants only; a literal null in the product kernels, so the
+// store compiles away): the int32 sum of the block's 32 q8 at sq_out[qb].
 template <int LAYOUT, int LPB>
 __device__ __forceinline__ void quantize_block_part(const float (&v)[32 / LPB], int e, int qcol, int c,
                                                     int b, int qb, int total, int nblk, int8_t *q8s,
-                                                    void *aux) {
+                                                    void *aux, int32_t *sq_out = nullptr) {
     constexpr int V = 32 / LPB;
     float amax = 0.0f;
 #pragma unroll
@@ -401,6 +403,7 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[32 / LPB], 
     else *reinterpret_cast<uint2 *>(dst) = make_uint2(word[0], word[V / 4 - 1]);
     const float d8 = (float)(_Float16)d;
     if ((e & (LPB / 2 - 1)) == 0) store_aux<LAYOUT>(aux, total, nblk, c, b, qb, e / (LPB / 2), d8, fsum, hsum);
+    if (sq_out && e == 0) sq_out[qb] = fsum;
 }
 
 template <int V>
@@ -443,7 +446,7 @@ template <int LAYOUT, int LPB, int NT, int PRE>
 __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, int64_t ldx, int K,
                                                  int ncols, bool vec_ok, const FastDiv &fd,
                                                  const ActStage<LPB, PRE> &st, int qcol, int8_t *q8s,
-                                                 void *aux) {
+                                                 void *aux, int32_t *sq_out = nullptr) {
     constexpr int V = 32 / LPB;
     const int nblk = K / 32;
     const int total = ncols * nblk;
@@ -454,7 +457,8 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
         const int qb = (int)(threadIdx.x / LPB) + j * step;
         if (qb < total) {
             const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
-            quantize_block_part<LAYOUT, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, total, nblk, q8s, aux);
+            quantize_block_part<LAYOUT, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, total, nblk, q8s, aux,
+                                             sq_out);
         }
     }
     for (int qb = (int)(threadIdx.x / LPB) + PRE * step; qb < total; qb += step) {
@@ -462,7 +466,7 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
         const int b = qb - c * nblk;
         float v[V];
         load_xv<V>(x + c * ldx + b * 32 + e * V, vec_ok, v);
-        quantize_block_part<LAYOUT, LPB>(v, e, qcol, c, b, qb, total, nblk, q8s, aux);
+        quantize_block_part<LAYOUT, LPB>(v, e, qcol, c, b, qb, total, nblk, q8s, aux, sq_out);
     }
 }
 
@@ -472,7 +476,7 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
 // 16-block group j.
 template <int LAYOUT, int LPB, int NT, int J0, int J1, int PRE>
 __device__ __forceinline__ void stage_f32_rounds(int K, int ncols, const FastDiv &fd, const ActStage<LPB, PRE> &st,
-                                                 int qcol, int8_t *q8s, void *aux) {
+                                                 int qcol, int8_t *q8s, void *aux, int32_t *sq_out = nullptr) {
     static_assert(0 <= J0 && J0 <= J1 && J1 <= PRE, "rounds held in registers");
     const int nblk = K / 32;
     const int total = ncols * nblk;
@@ -483,7 +487,8 @@ __device__ __forceinline__ void stage_f32_rounds(int K, int ncols, const FastDiv
         const int qb = (int)(threadIdx.x / LPB) + j * step;
         if (qb < total) {
             const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
-            quantize_block_part<LAYOUT, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, total, nblk, q8s, aux);
+            quantize_block_part<LAYOUT, LPB>(st.v[j], e, qcol, c, qb - c * nblk, qb, total, nblk, q8s, aux,
+                                             sq_out);
         }
     }
 }
@@ -518,7 +523,7 @@ __device__ __forceinline__ void stage_q81_issue(const uint8_t *__restrict__ y, i
 template <int LAYOUT>
 __device__ __forceinline__ void store_q81_part(uint32_t w0, uint32_t w1, uint32_t ds, int quarter,
                                                int qcol, int c, int b, int qb, int total, int nblk,
-                                               int8_t *q8s, void *aux) {
+                                               int8_t *q8s, void *aux, int32_t *sq_out = nullptr) {
     int hsum, fsum;
     block_sums<4>(__builtin_amdgcn_sdot4((int)w0, 0x01010101, __builtin_amdgcn_sdot4((int)w1, 0x01010101, 0, false),
                                          false),
@@ -526,13 +531,14 @@ __device__ __forceinline__ void store_q81_part(uint32_t w0, uint32_t w1, uint32_
     *reinterpret_cast<uint2 *>(q8s + q8_offset<LAYOUT>(c, qcol, b, 2 * quarter)) = make_uint2(w0, w1);
     if ((quarter & 1) == 0)
         store_aux<LAYOUT>(aux, total, nblk, c, b, qb, quarter >> 1, half_bits_to_float(ds), fsum, hsum);
+    if (sq_out && quarter == 0) sq_out[qb] = fsum;
 }
 
 template <int LAYOUT, int NT, int PRE>
 __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                  int K, int ncols, const FastDiv &fd,
                                                  const Q81Stage<PRE> &st, int qcol, int8_t *q8s,
-                                                 void *aux) {
+                                                 void *aux, int32_t *sq_out = nullptr) {
     const int nblk = K / 32;
     const int total = ncols * nblk;
     const int quarter = threadIdx.x & 3;
@@ -543,7 +549,7 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
         if (qb < total) {
             const int c = (int)fastdiv((uint32_t)qb, fd);
             store_q81_part<LAYOUT>(st.w[j][0], st.w[j][1], st.ds[j], quarter, qcol, c, qb - c * nblk, qb,
-                                   total, nblk, q8s, aux);
+                                   total, nblk, q8s, aux, sq_out);
         }
     }
     for (int qb = (threadIdx.x >> 2) + PRE * step; qb < total; qb += step) {
@@ -553,7 +559,7 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
         const uint32_t w0 = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
         const uint32_t w1 = *reinterpret_cast<const uint32_t *>(blk + 8 + quarter * 8);
         store_q81_part<LAYOUT>(w0, w1, *reinterpret_cast<const uint32_t *>(blk), quarter, qcol, c, b, qb,
-                               total, nblk, q8s, aux);
+                               total, nblk, q8s, aux, sq_out);
     }
 }
 

@@ -64,12 +64,28 @@ inline int fused_kind(const Epilogue *e) {
 
 inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Parity outputs of the *_sums entry points: launches with them run the
+// SUMS variants of the product kernels (same geometry, same results) that
+// also store the int32 sums.
+struct SumsOut {
+    int32_t *sums;  // Q4_K [N][M][K/32] sub-block sums; Q6_K [N][M][K/16] group sums
+    int32_t *sq;    // Q4_K [N][K/32] activation sums (Q6_K: unused)
+};
+
+// The SUMS kernels (q4k_sums.hip, q6k_sums.hip): the variant of the launch
+// shape given, or null when it is not instantiated (only the shapes the
+// automatic geometry picks for plain products are).
+const void *q4k_sums_kernel(int nc, int waves, int pro, int slots);
+const void *q4k_bpl_sums_kernel(int waves);
+const void *q6k_sums_kernel(int nc, int waves, int pro, int slots);
+
 // Q6_K weight checks and launch (q6k_gemv.hip), for the type-dispatching
 // entry points of q4k_gemv.hip.
 int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01);
 int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x, int64_t ldx,
                 const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst, int64_t ld_dst,
-                hipStream_t stream, const Epilogue *ep = nullptr, const BatchLaunch *bl = nullptr);
+                hipStream_t stream, const Epilogue *ep = nullptr, const BatchLaunch *bl = nullptr,
+                const SumsOut *so = nullptr);
 
 // Workgroups per weight matrix of a launch over `mats` matrices of M rows:
 // the CUs shared among the matrices, at least one, at most one per row.

@@ -1,0 +1,55 @@
+// q4k_sums.hip -- the parity variants (SUMS) of the Q4_K GEMV kernels: the
+// product kernels of q4k_gemv_kernels.h that also store every lane's int32
+// sub-block sums and the staging's int32 activation sums.  Instantiated in a
+// translation unit of their own for the launch shapes the automatic
+// geometry picks for plain products (one row per tile, 8 or 16 waves, 1 or 2
+// slots, prologue 0, 1 or 3; the block-per-lane kernel at 4 or 8 waves);
+// q4k_gemv.hip launches them with the product's own geometry.
+#include <hip/hip_runtime.h>
+
+#include "q4k_gemv_kernels.h"
+#include "q4k_runtime.h"
+
+namespace q4k {
+namespace {
+
+template <int NC, int WAVES, int S>
+const void *tile_sums(int pro) {
+    if (pro == 0) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, 1, WAVES, 0, S, kEpiNone, false, true>);
+    if (pro == 1) return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, 1, WAVES, 1, S, kEpiNone, false, true>);
+    if constexpr (S == 2) {
+        if (pro == 3)
+            return reinterpret_cast<const void *>(&gemv_q4k_kernel<NC, 1, WAVES, 3, S, kEpiNone, false, true>);
+    }
+    return nullptr;
+}
+
+template <int WAVES, int S>
+const void *tile_sums_nc(int nc, int pro) {
+    switch (nc) {
+        case 1: return tile_sums<1, WAVES, S>(pro);
+        case 2: return tile_sums<2, WAVES, S>(pro);
+        case 3: return tile_sums<3, WAVES, S>(pro);
+        case 4: return tile_sums<4, WAVES, S>(pro);
+        case 5: return tile_sums<5, WAVES, S>(pro);
+        case 6: return tile_sums<6, WAVES, S>(pro);
+        case 7: return tile_sums<7, WAVES, S>(pro);
+        case 8: return tile_sums<8, WAVES, S>(pro);
+        default: return nullptr;
+    }
+}
+
+}  // namespace
+
+const void *q4k_sums_kernel(int nc, int waves, int pro, int slots) {
+    if (slots != 1 && slots != 2) return nullptr;
+    if (waves <= 8) return slots == 1 ? tile_sums_nc<8, 1>(nc, pro) : tile_sums_nc<8, 2>(nc, pro);
+    return slots == 1 ? tile_sums_nc<16, 1>(nc, pro) : tile_sums_nc<16, 2>(nc, pro);
+}
+
+const void *q4k_bpl_sums_kernel(int waves) {
+    return waves == 8 ? reinterpret_cast<const void *>(&gemv_q4k_bpl_kernel<8, true>)
+                      : reinterpret_cast<const void *>(&gemv_q4k_bpl_kernel<4, true>);
+}
+
+}  // namespace q4k

@@ -55,6 +55,11 @@ struct GemvParams {
     int glu_op;
     BatchParams bt;          // batched launches only
     int w_absent;            // batched: this workgroup's weight matrix is absent (bad id)
+    // parity variants (SUMS) only: the int32 sums the kernel forms, where
+    // the oracle keeps them (Q4_K: sums[(c*M + row)*(K/32) + 8kb + s],
+    // sq[c*(K/32) + b]; Q6_K: sums[(c*M + row)*(K/16) + 16kb + t])
+    int32_t *sums;
+    int32_t *sq;
 };
 
 // A batched launch: its BatchParams and the dst channels and samples (grid

@@ -1,0 +1,43 @@
+// q6k_sums.hip -- the parity variants (SUMS) of the Q6_K GEMV kernel: the
+// product kernel of q6k_kernels.h that also stores every lane's int32 group
+// sums.  Instantiated for the launch shapes the automatic geometry picks for
+// plain products (8 or 16 waves, one slot, prologue 0 or 1); q6k_gemv.hip
+// launches them with the product's own geometry.
+#include <hip/hip_runtime.h>
+
+#include "q4k_runtime.h"
+#include "q6k_kernels.h"
+
+namespace q4k {
+namespace {
+
+template <int NC, int WAVES>
+const void *q6_sums(int pro) {
+    if (pro == 0) return reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 0, 1, kEpiNone, false, true>);
+    if (pro == 1) return reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 1, 1, kEpiNone, false, true>);
+    return nullptr;
+}
+
+template <int WAVES>
+const void *q6_sums_nc(int nc, int pro) {
+    switch (nc) {
+        case 1: return q6_sums<1, WAVES>(pro);
+        case 2: return q6_sums<2, WAVES>(pro);
+        case 3: return q6_sums<3, WAVES>(pro);
+        case 4: return q6_sums<4, WAVES>(pro);
+        case 5: return q6_sums<5, WAVES>(pro);
+        case 6: return q6_sums<6, WAVES>(pro);
+        case 7: return q6_sums<7, WAVES>(pro);
+        case 8: return q6_sums<8, WAVES>(pro);
+        default: return nullptr;
+    }
+}
+
+}  // namespace
+
+const void *q6k_sums_kernel(int nc, int waves, int pro, int slots) {
+    if (slots != 1) return nullptr;
+    return waves <= 8 ? q6_sums_nc<8>(nc, pro) : q6_sums_nc<16>(nc, pro);
+}
+
+}  // namespace q4k

@@ -234,6 +234,21 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
                       const void *q8_1, int64_t ncols, int64_t stride_col_y, int32_t *sqq,
                       int32_t *sq, void *stream);
 
+/* Parity form of q4k_mul_mat_vec_q: the same routes, geometry and kernels,
+ * in their variant that also stores the int32 sums it forms -- the
+ * quantities of kernels/vecdotq.cuh:469-478 (dot1 per sub-block, summed over
+ * the lanes that share it) and the activation sums the min term uses:
+ *   sums[(c*ne01 + r)*(ne00/32) + s] = sum over sub-block s of q4 * q8
+ *   sq[c*(ne00/32) + s]             = sum over sub-block s of q8
+ * dst receives the product, bit for bit what q4k_mul_mat_vec_q writes.
+ * Only launch shapes the automatic geometry picks have this variant (a
+ * geometry override can return Q4K_EUNSUPPORTED).  No counterpart in the
+ * reference; for parity tests. */
+int q4k_mul_mat_vec_q_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
+                           const float *src1, int64_t ne11, int64_t nb11, float *dst, int64_t nb1,
+                           void *workspace, size_t workspace_bytes, int32_t *sums, int32_t *sq,
+                           void *stream);
+
 /* ------------------------------------------------------------- Q6_K ---- */
 
 /* dst = src0 (Q6_K, ne01 x ne00) * src1 (F32, ne00 x ne11): the Q6_K case of
@@ -264,6 +279,16 @@ int q6k_op_mul_mat_vec_q(const void *src0_dd_i, int64_t ne00, int64_t row_low, i
  * u) summed over the four lanes that share a scale. */
 int q6k_group_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const void *q8_1,
                    int64_t ncols, int64_t stride_col_y, int32_t *s16, void *stream);
+
+/* Parity form of q6k_mul_mat_vec_q (as q4k_mul_mat_vec_q_sums): the
+ * production kernels' int32 group sums S_g of (q - 32) * q8,
+ *   s16[(c*ne01 + r)*(ne00/16) + g]
+ * (kernels/vecdotq.cuh:589-593 summed over the lanes sharing a scale), and
+ * dst bit for bit what q6k_mul_mat_vec_q writes.  No counterpart in the
+ * reference; for parity tests. */
+int q6k_mul_mat_vec_q_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
+                           const float *src1, int64_t ne11, int64_t nb11, float *dst, int64_t nb1,
+                           void *workspace, size_t workspace_bytes, int32_t *s16, void *stream);
 
 /* Launch geometry q6k_mul_mat_vec_q would use (the out[] fields of
  * q4k_gemv_geometry; out[7] = weight groups in flight per wave). */

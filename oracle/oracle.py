@@ -63,6 +63,8 @@ def lib():
             "orc_quantize_q8_1": (None, [P, I64, I64, P]),
             "orc_quantize_q8_1_cols": (None, [P, I64, I64, I64, I64, P]),
             "orc_gemv_q4K_q8_1": (None, [P, I64, I64, I64, P, I64, I64, P, P, P, P]),
+            "orc_gemv_q4K_q8_1_mt": (None, [P, I64, I64, I64, P, I64, I64, P, P, P, P, I]),
+            "orc_gemv_q6K_q8_1_mt": (I64, [P, I64, I64, I64, P, I64, I64, P, P, P, I]),
             "orc_quantize_q8_K": (None, [P, P, I64]),
             "orc_vec_dot_q4_K_q8_K_scalar": (ctypes.c_float, [I64, P, P]),
             "orc_vec_dot_q4_K_q8_K_avx2": (ctypes.c_float, [I64, P, P]),
@@ -204,9 +206,16 @@ def quantize_q8_K(x: np.ndarray) -> np.ndarray:
 
 
 # ------------------------------------------------------------------ GEMV ----
-def gemv_q4K_q8_1(w_q: np.ndarray, K: int, q8: np.ndarray, want_sums: bool = True):
+def _threads(nthreads):
+    if nthreads is not None:
+        return max(1, int(nthreads))
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def gemv_q4K_q8_1(w_q: np.ndarray, K: int, q8: np.ndarray, want_sums: bool = True, nthreads: int | None = None):
     """Q4_K [M, K/256*144] x Q8_1 [N, Kp/32*36] -> dict(y64 [N,M], l1 [N,M],
-    sqq [N,M,K/32] int32, sq [N,K/32] int32)."""
+    sqq [N,M,K/32] int32, sq [N,K/32] int32); rows split over nthreads
+    threads (default: the usable cores, at most 16)."""
     w_q = np.ascontiguousarray(w_q, dtype=np.uint8)
     q8 = np.ascontiguousarray(np.atleast_2d(q8), dtype=np.uint8)
     row_bytes = K // QK_K * Q4K_BYTES
@@ -217,12 +226,12 @@ def gemv_q4K_q8_1(w_q: np.ndarray, K: int, q8: np.ndarray, want_sums: bool = Tru
     l1 = np.empty((N, M), dtype=np.float64)
     sqq = np.empty((N, M, K // 32), dtype=np.int32) if want_sums else None
     sq = np.empty((N, K // 32), dtype=np.int32) if want_sums else None
-    lib().orc_gemv_q4K_q8_1(_p(w_q), M, K, row_bytes, _p(q8), N, stride_col_y, _p(y64), _p(l1),
-                            _p(sqq) if want_sums else None, _p(sq) if want_sums else None)
+    lib().orc_gemv_q4K_q8_1_mt(_p(w_q), M, K, row_bytes, _p(q8), N, stride_col_y, _p(y64), _p(l1),
+                               _p(sqq) if want_sums else None, _p(sq) if want_sums else None, _threads(nthreads))
     return {"y64": y64, "l1": l1, "sqq": sqq, "sq": sq}
 
 
-def gemv_q6K_q8_1(w_q: np.ndarray, K: int, q8: np.ndarray, want_sums: bool = True):
+def gemv_q6K_q8_1(w_q: np.ndarray, K: int, q8: np.ndarray, want_sums: bool = True, nthreads: int | None = None):
     """Q6_K [M, K/256*210] x Q8_1 [N, Kp/32*36] -> dict(y64 [N,M], l1 [N,M],
     s16 [N,M,K/16] int32 sums of (q - 32) * q8 per 16-weight group,
     mismatches: scale-index / group-index disagreements (0 expected))."""
@@ -235,8 +244,8 @@ def gemv_q6K_q8_1(w_q: np.ndarray, K: int, q8: np.ndarray, want_sums: bool = Tru
     y64 = np.empty((N, M), dtype=np.float64)
     l1 = np.empty((N, M), dtype=np.float64)
     s16 = np.empty((N, M, K // 16), dtype=np.int32) if want_sums else None
-    mism = lib().orc_gemv_q6K_q8_1(_p(w_q), M, K, row_bytes, _p(q8), N, stride_col_y, _p(y64), _p(l1),
-                                   _p(s16) if want_sums else None)
+    mism = lib().orc_gemv_q6K_q8_1_mt(_p(w_q), M, K, row_bytes, _p(q8), N, stride_col_y, _p(y64), _p(l1),
+                                      _p(s16) if want_sums else None, _threads(nthreads))
     return {"y64": y64, "l1": l1, "s16": s16, "mismatches": int(mism)}
 
 

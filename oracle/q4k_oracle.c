@@ -497,14 +497,15 @@ static inline int32_t orc_dp4a(int32_t a, int32_t b, int32_t c) {
  *   sqq[(c*M + r)*(K/32)+s]  int32 sum over the sub-block of q4*q8
  *   sq[c*(K/32) + s]         int32 sum over the sub-block of q8
  */
-void orc_gemv_q4K_q8_1(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride,
-                       const uint8_t *q8, int64_t N, int64_t stride_col_y,
-                       double *y64, double *l1, int32_t *sqq, int32_t *sq) {
+/* Rows [r0, r1) of orc_gemv_q4K_q8_1 (outputs indexed as there); sq is
+ * written by the range that holds row 0. */
+static void orc_gemv_q4K_rows(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const uint8_t *q8,
+                              int64_t N, int64_t stride_col_y, int64_t r0, int64_t r1, double *y64, double *l1,
+                              int32_t *sqq, int32_t *sq) {
     const int64_t nb = K / ORC_QK_K, ns = K / 32;
-    int32_t *dq = (int32_t *)malloc(sizeof(int32_t) * (size_t)ns * 2);
     for (int64_t c = 0; c < N; ++c) {
         const uint8_t *yc = q8 + c * stride_col_y * ORC_Q81_BYTES;
-        for (int64_t r = 0; r < M; ++r) {
+        for (int64_t r = r0; r < r1; ++r) {
             const uint8_t *wr = w + r * row_stride;
             double acc = 0.0, acc_l1 = 0.0;
             for (int64_t kb = 0; kb < nb; ++kb) {
@@ -543,17 +544,53 @@ void orc_gemv_q4K_q8_1(const uint8_t *w, int64_t M, int64_t K, int64_t row_strid
                     acc += tq - tm;
                     acc_l1 += fabs(tq) + fabs(tm);
                     if (sqq) sqq[(c * M + r) * ns + kb * 8 + s] = s_qq[s];
-                    if (r == 0) {
-                        dq[kb * 8 + s] = s_q[s];
-                    }
+                    if (sq && r == 0) sq[c * ns + kb * 8 + s] = s_q[s];
                 }
             }
             if (y64) y64[c * M + r] = acc;
             if (l1) l1[c * M + r] = acc_l1;
         }
-        if (sq && M > 0) memcpy(sq + c * ns, dq, sizeof(int32_t) * (size_t)ns);
     }
-    free(dq);
+}
+
+void orc_gemv_q4K_q8_1(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride,
+                       const uint8_t *q8, int64_t N, int64_t stride_col_y,
+                       double *y64, double *l1, int32_t *sqq, int32_t *sq) {
+    orc_gemv_q4K_rows(w, M, K, row_stride, q8, N, stride_col_y, 0, M, y64, l1, sqq, sq);
+}
+
+/* The same with the rows split over nthreads threads (contiguous ranges). */
+typedef struct {
+    const uint8_t *w, *q8;
+    int64_t M, K, row_stride, N, stride_col_y, r0, r1;
+    double *y64, *l1;
+    int32_t *sqq, *sq;
+} orc_gemv_task;
+
+static void *orc_gemv_q4K_task(void *arg) {
+    orc_gemv_task *t = (orc_gemv_task *)arg;
+    orc_gemv_q4K_rows(t->w, t->M, t->K, t->row_stride, t->q8, t->N, t->stride_col_y, t->r0, t->r1, t->y64,
+                      t->l1, t->sqq, t->sq);
+    return NULL;
+}
+
+void orc_gemv_q4K_q8_1_mt(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const uint8_t *q8,
+                          int64_t N, int64_t stride_col_y, double *y64, double *l1, int32_t *sqq, int32_t *sq,
+                          int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > M) nthreads = M > 0 ? (int)M : 1;
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    orc_gemv_task *task = (orc_gemv_task *)malloc(sizeof(orc_gemv_task) * (size_t)nthreads);
+    for (int i = 0; i < nthreads; ++i) {
+        orc_gemv_task t = {w, q8, M, K, row_stride, N, stride_col_y, M * i / nthreads, M * (i + 1) / nthreads,
+                           y64, l1, sqq, sq};
+        task[i] = t;
+        if (i > 0) pthread_create(&th[i], NULL, orc_gemv_q4K_task, &task[i]);
+    }
+    orc_gemv_q4K_task(&task[0]);
+    for (int i = 1; i < nthreads; ++i) pthread_join(th[i], NULL);
+    free(th);
+    free(task);
 }
 
 /* ------------------------------------------------------------------------ */

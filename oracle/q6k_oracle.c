@@ -30,7 +30,9 @@
  * Build: oracle/Makefile (gcc, -ffp-contract=off).
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define ORC_QK_K 256
@@ -215,13 +217,14 @@ static inline int32_t orc_vsubss4(int32_t a, int32_t b) {
  * 16-weight group their q8 values belong to (0: the two index formulas of
  * the reference agree).
  */
-int64_t orc_gemv_q6K_q8_1(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const uint8_t *q8,
-                          int64_t N, int64_t stride_col_y, double *y64, double *l1, int32_t *s16) {
+static int64_t orc_gemv_q6K_rows(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const uint8_t *q8,
+                                 int64_t N, int64_t stride_col_y, int64_t r0, int64_t r1, double *y64, double *l1,
+                                 int32_t *s16) {
     const int64_t nb = K / ORC_QK_K, ng = K / 16;
     int64_t mismatches = 0;
     for (int64_t c = 0; c < N; ++c) {
         const uint8_t *yc = q8 + c * stride_col_y * ORC_Q81_BYTES;
-        for (int64_t r = 0; r < M; ++r) {
+        for (int64_t r = r0; r < r1; ++r) {
             const uint8_t *wr = w + r * row_stride;
             double acc = 0.0, acc_l1 = 0.0;
             for (int64_t kb = 0; kb < nb; ++kb) {
@@ -264,4 +267,50 @@ int64_t orc_gemv_q6K_q8_1(const uint8_t *w, int64_t M, int64_t K, int64_t row_st
         }
     }
     return mismatches;
+}
+
+int64_t orc_gemv_q6K_q8_1(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const uint8_t *q8,
+                          int64_t N, int64_t stride_col_y, double *y64, double *l1, int32_t *s16) {
+    return orc_gemv_q6K_rows(w, M, K, row_stride, q8, N, stride_col_y, 0, M, y64, l1, s16);
+}
+
+/* The same with the rows split over nthreads threads (contiguous ranges);
+ * returns the summed mismatch count. */
+typedef struct {
+    const uint8_t *w, *q8;
+    int64_t M, K, row_stride, N, stride_col_y, r0, r1;
+    double *y64, *l1;
+    int32_t *s16;
+    int64_t mismatches;
+} orc_q6_task;
+
+static void *orc_gemv_q6K_task(void *arg) {
+    orc_q6_task *t = (orc_q6_task *)arg;
+    t->mismatches = orc_gemv_q6K_rows(t->w, t->M, t->K, t->row_stride, t->q8, t->N, t->stride_col_y, t->r0,
+                                      t->r1, t->y64, t->l1, t->s16);
+    return NULL;
+}
+
+int64_t orc_gemv_q6K_q8_1_mt(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const uint8_t *q8,
+                             int64_t N, int64_t stride_col_y, double *y64, double *l1, int32_t *s16,
+                             int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > M) nthreads = M > 0 ? (int)M : 1;
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    orc_q6_task *task = (orc_q6_task *)malloc(sizeof(orc_q6_task) * (size_t)nthreads);
+    for (int i = 0; i < nthreads; ++i) {
+        orc_q6_task t = {w, q8, M, K, row_stride, N, stride_col_y, M * i / nthreads, M * (i + 1) / nthreads,
+                         y64, l1, s16, 0};
+        task[i] = t;
+        if (i > 0) pthread_create(&th[i], NULL, orc_gemv_q6K_task, &task[i]);
+    }
+    orc_gemv_q6K_task(&task[0]);
+    int64_t mism = task[0].mismatches;
+    for (int i = 1; i < nthreads; ++i) {
+        pthread_join(th[i], NULL);
+        mism += task[i].mismatches;
+    }
+    free(th);
+    free(task);
+    return mism;
 }

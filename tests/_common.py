@@ -69,7 +69,12 @@ def activations(N: int, K: int, seed: int = 0) -> np.ndarray:
 
 def assert_within_tolerance(O, y, ref, where=""):
     """y (float32 [N, M]) against the oracle's f64 result within the parity
-    tolerance; returns (max abs err / tol, count failing strict 1e-5 rel)."""
+    tolerance.  Returns a dict: n outputs; max_ratio = max |err| / tol;
+    strict_fail = outputs outside the strict bar (1e-5 relative or 4 ulp of
+    the result), i.e. those inside the tolerance only through its
+    cancellation term (8 f32 epsilons of the row's sum of |term|);
+    max_cancel_ulps = the largest |err| among those in units of
+    eps32 * sum |term|."""
     y = np.asarray(y, dtype=np.float64)
     tol = O.parity_tolerance(ref["y64"], ref["l1"])
     err = np.abs(y - ref["y64"])
@@ -78,5 +83,10 @@ def assert_within_tolerance(O, y, ref, where=""):
         idx = np.argwhere(bad)[:5]
         details = [(tuple(i), float(y[tuple(i)]), float(ref["y64"][tuple(i)]), float(tol[tuple(i)])) for i in idx]
         raise AssertionError(f"{where}: {int(bad.sum())} outputs outside tolerance, e.g. {details}")
-    strict = int((err > 1e-5 * np.abs(ref["y64"])).sum())
-    return float((err / tol).max()), strict
+    strict_tol = np.maximum(1e-5 * np.abs(ref["y64"]),
+                            4.0 * np.spacing(np.abs(ref["y64"]).astype(np.float32)).astype(np.float64))
+    loose = err > strict_tol
+    eps_l1 = np.finfo(np.float32).eps * np.asarray(ref["l1"], np.float64)
+    cancel = float((err[loose] / eps_l1[loose]).max()) if loose.any() else 0.0
+    return {"n": int(err.size), "max_ratio": float((err / tol).max()), "strict_fail": int(loose.sum()),
+            "max_cancel_ulps": cancel}
