@@ -9,26 +9,42 @@ than 1 GiB so every step streams it from HBM rather than from the 256 MB
 Infinity Cache.
 
 Timing: W untimed eager warm-up steps; the K timed steps are captured into one
-HIP graph (the way ggml launches decode), which is replayed once untimed and
-then once between two HIP events recorded on the stream the kernels run on.
-value = algorithmic bytes per step / seconds per step (GB/s); the roofline
-object prices the same bytes against the 8 TB/s HBM peak.  The CPU baseline is
-the oracle's restatement of ggml's CPU path (Q8_K activations +
-vec_dot_q4_K_q8_K, AVX2, a thread per core) timed on a bounded sample on the
-host cores of the same machine.
+HIP graph (the way ggml launches decode).  A trial is: synchronise, replay the
+graph once untimed, record an event, replay it again, record an event,
+synchronise -- so the timed replay of exactly K steps is already queued
+behind the untimed one when the GPU reaches the first event, and host
+submission latency stays out of the window.  value is the median over the
+trials (min and max reported); events are recorded on the stream the kernels
+run on.  value = algorithmic bytes per step / seconds per step (GB/s); the
+roofline object prices the same bytes against the 8 TB/s HBM peak, and its
+traffic is the HBM bytes rocprofv3 counted for the same launch
+(profiles/q4k_traffic_all_configs.txt).  The CPU baseline is the oracle's
+restatement of ggml's CPU path (Q8_K activations + vec_dot_q4_K_q8_K, AVX2)
+on pinned threads of this machine, timed on a bounded sample.
 
---sweep prints one line per (workload, shape, ncols) of the five workloads
-instead of the headline JSON; with --wtype q6_K, of the Q6_K tensors of a
-Q4_K_M model (ffn_down, attn_v, output projection).
+Modes:
+  (default)         the headline JSON line
+  --sweep           one JSON line per (shape, ncols) of the five workloads
+                    (--wtype q6_K: the Q6_K tensors of a Q4_K_M model), each
+                    with the roofline fraction, the measured traffic and, for
+                    Q4_K, a CPU baseline with and without Q8_K quantisation
+  --fused, --moe    the fused gate/up launch and MUL_MAT_ID workloads
+  --profile         plain eager launches of one shape (for rocprofv3)
+  --profile-sweep   plain eager launches of every sweep config in order, each
+                    preceded by a one-block quantiser launch that marks where
+                    it starts, after a device copy of known size (the counter
+                    calibration); --summarize reads the rocprofv3 output of
+                    such a run and prints the per-config tables
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import math
 import os
 import sys
-import time
 
 import numpy as np
 
@@ -37,7 +53,9 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 METRIC = "Q4_K GEMV µs/call + achieved HBM GB/s (% of 8 TB/s), 14336x4096 b=1"
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_14336x4096_b1_traffic.txt")
+PROFILES = os.path.join(ROOT, "profiles")
+CPU_SHARE = 16  # CPUs a one-GPU box grants a job
+CAL_BYTES = 256 << 20  # the calibration copy of --profile-sweep
 
 
 def log(msg):
@@ -57,10 +75,24 @@ def make_inputs(Q, M, K, N, seed=0, wtype="q4_K"):
     import _common
     W = _common.weights(M, K, seed)
     quant = Q.quantize_rows_q4_K if wtype == "q4_K" else Q.quantize_rows_q6_K
-    wq = quant(W, nthreads=min(16, len(os.sched_getaffinity(0))))
+    wq = quant(W, nthreads=min(CPU_SHARE, len(os.sched_getaffinity(0))))
     del W
     x = _common.activations(N, K, seed)
     return wq, x
+
+
+def sweep_configs(wtype: str):
+    """(workload, M, K, N) of the sweep, each (M, K, N) once, in table order."""
+    import _common
+    table = _common.WORKLOADS if wtype == "q4_K" else _common.Q6K_WORKLOADS
+    out, seen = [], set()
+    for wl, items in table.items():
+        for M, K, ns in items:
+            for N in ns:
+                if (M, K, N) not in seen:
+                    seen.add((M, K, N))
+                    out.append((wl, M, K, N))
+    return out
 
 
 class OpRunner:
@@ -126,7 +158,6 @@ class FusedRunner(OpRunner):
 def fused_sweep(args):
     """Gate+up with SWIGLU in one launch against the two plain launches, on
     the FFN shapes (batch 1, the only fused case)."""
-    import _common
     import torch
     Q = _pkg()
     wt = args.wtype
@@ -134,11 +165,11 @@ def fused_sweep(args):
         wu, x = make_inputs(Q, M, K, 1, seed=0, wtype=wt)
         wg, _ = make_inputs(Q, M, K, 1, seed=1, wtype=wt)
         fr = FusedRunner(Q, wu, wg, x, wtype=wt)
-        tf = time_gpu(fr, args.steps, args.warmup)["graph_s"]
+        tf = time_gpu(fr, args.steps, args.warmup, args.trials)["graph_s"]
         del fr
         torch.cuda.empty_cache()
         pr = OpRunner(Q, wu, x, wtype=wt)
-        tp = time_gpu(pr, args.steps, args.warmup)["graph_s"]
+        tp = time_gpu(pr, args.steps, args.warmup, args.trials)["graph_s"]
         del pr
         torch.cuda.empty_cache()
         nbytes = 2 * M * (K // 256) * BLOCK_BYTES[wt] + 4 * K + 4 * M
@@ -213,11 +244,11 @@ def moe_sweep(args):
     Q = _pkg()
     for name, nexp, M, K, ids, ne11, wt, fused in MOE_CASES:
         quant = Q.quantize_rows_q4_K if wt == "q4_K" else Q.quantize_rows_q6_K
-        nthr = min(16, len(os.sched_getaffinity(0)))
+        nthr = min(CPU_SHARE, len(os.sched_getaffinity(0)))
         wq = np.stack([quant(_common.weights(M, K, seed=e), nthreads=nthr) for e in range(nexp)])
         gq = np.stack([quant(_common.weights(M, K, seed=1000 + e), nthreads=nthr) for e in range(nexp)]) if fused else None
         r = MoeRunner(Q, wq, nexp, M, K, ids, ne11, gq=gq, wtype=wt)
-        t = time_gpu(r, args.steps, args.warmup)["graph_s"]
+        t = time_gpu(r, args.steps, args.warmup, args.trials)["graph_s"]
         del r
         torch.cuda.empty_cache()
         nused = len(ids)
@@ -228,8 +259,10 @@ def moe_sweep(args):
               flush=True)
 
 
-def time_gpu(runner: OpRunner, steps: int, warmup: int):
-    """Returns dict with graph-launched and eager seconds per step."""
+def time_gpu(runner, steps: int, warmup: int, trials: int = 7):
+    """Seconds per step: graph_s (median over trials of one timed replay of
+    the K-step graph, queued behind an untimed replay), graph_min_s,
+    graph_max_s, and eager_s (K back-to-back eager calls, one window)."""
     import ctypes
     import torch
     stream = torch.cuda.Stream()
@@ -239,7 +272,6 @@ def time_gpu(runner: OpRunner, steps: int, warmup: int):
         for _ in range(warmup):
             runner.step(sp)
         torch.cuda.synchronize()
-        # eager: K back-to-back launches from the host
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(steps):
@@ -247,7 +279,6 @@ def time_gpu(runner: OpRunner, steps: int, warmup: int):
         e1.record(stream)
         torch.cuda.synchronize()
         res["eager_s"] = e0.elapsed_time(e1) * 1e-3 / steps
-        # graph: the same K calls captured once, replayed
         g = torch.cuda.CUDAGraph()
         runner.i = 0
         with torch.cuda.graph(g, stream=stream):
@@ -255,49 +286,81 @@ def time_gpu(runner: OpRunner, steps: int, warmup: int):
                 runner.step(sp)
         g.replay()
         torch.cuda.synchronize()
-        e0.record(stream)
-        g.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        res["graph_s"] = e0.elapsed_time(e1) * 1e-3 / steps
+        per = []
+        for _ in range(trials):
+            torch.cuda.synchronize()
+            g.replay()            # untimed: keeps the GPU busy while the timed replay is queued
+            e0.record(stream)
+            g.replay()            # timed: exactly `steps` calls
+            e1.record(stream)
+            torch.cuda.synchronize()
+            per.append(e0.elapsed_time(e1) * 1e-3 / steps)
+        res["graph_s"] = float(np.median(per))
+        res["graph_min_s"] = float(min(per))
+        res["graph_max_s"] = float(max(per))
+        res["trials"] = trials
     return res
 
 
-def read_traffic():
-    """HBM bytes per launch from the committed rocprofv3 PMC summary."""
-    if not os.path.exists(TRAFFIC_FILE):
-        return None
-    for line in open(TRAFFIC_FILE):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+def traffic_file(wtype: str) -> str:
+    return os.path.join(PROFILES, f"{wtype.replace('_', '').lower()}_traffic_all_configs.txt")
 
 
-def cpu_baseline(wq, x, target_s=12.0):
+def read_traffic(M: int, K: int, N: int, wtype: str = "q4_K"):
+    """HBM bytes per launch of the GEMV kernel (and of the whole op) for one
+    config, from the committed rocprofv3 counter summary: (kernel, op) or
+    (None, None) when the config is not in it."""
+    path = traffic_file(wtype)
+    if not os.path.exists(path):
+        return None, None
+    key = f"traffic M={M} K={K} N={N} "
+    for line in open(path):
+        if line.startswith(key):
+            kv = dict(f.split("=") for f in line.split()[1:])
+            return int(kv["gemv_bytes"]), int(kv["op_bytes"])
+    return None, None
+
+
+def cpu_baseline(wq, x, target_s=12.0, min_reps=10):
+    """ggml's CPU path (restated in the oracle) on this machine: Q8_K
+    quantisation of x + vec_dot_q4_K_q8_K per (row, column), AVX2, one thread
+    per CPU of the job's share, each pinned.  Median of >= min_reps calls
+    with quantisation and without (Q8_K activation prepared beforehand)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     if not os.path.exists(O.LIB_PATH):
         O.build()
-    cores = min(16, len(os.sched_getaffinity(0)))
+    cpus = sorted(os.sched_getaffinity(0))[:CPU_SHARE]
+    cores = len(cpus)
+    O.set_pin_cpus(cpus)
     K = wq.shape[1] // 144 * 256
-    t1 = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, 2)
-    per = float(np.median(t1))
-    reps = int(max(3, min(5000, target_s / max(per, 1e-6))))
-    t = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, reps)
-    isa = "avx2" if O.lib().orc_cpu_has_avx2() else "scalar"
-    med = float(np.median(t))
     M, N = wq.shape[0], x.shape[0]
+    out = {}
+    for mode, quant in (("with_q8K", True), ("without_q8K", False)):
+        t1 = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, 2, quantize=quant)
+        per = float(np.median(t1))
+        reps = int(max(min_reps, min(5000, target_s / 2 / max(per, 1e-6))))
+        t = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, reps, quantize=quant)
+        out[mode] = (float(np.median(t)), reps, float(np.sum(t)))
+    O.set_pin_cpus([])
+    isa = "avx2" if O.lib().orc_cpu_has_avx2() else "scalar"
     model = "unknown"
     try:
         with open("/proc/cpuinfo") as fh:
             model = next((ln.split(":", 1)[1].strip() for ln in fh if ln.startswith("model name")), model)
     except OSError:
         pass
-    return {"value": algorithmic_bytes(M, K, N) / med / 1e9, "unit": "GB/s", "cores": cores,
-            "kind": "port", "us_per_call": med * 1e6, "cpu_model": model, "isa": isa,
-            "sample": f"{reps} calls of the full {M}x{K} N={N} product (Q8_K quantisation + "
-                      f"vec_dot_q4_K_q8_K, {isa}, {cores} threads, row chunks of 16), "
-                      f"{float(np.sum(t)):.1f} s total, median reported"}
+    med, reps, tot = out["with_q8K"]
+    med_nq, reps_nq, tot_nq = out["without_q8K"]
+    nbytes = algorithmic_bytes(M, K, N)
+    return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+            "us_per_call": round(med * 1e6, 1), "us_per_call_without_q8K": round(med_nq * 1e6, 1),
+            "GBps_without_q8K": round(nbytes / med_nq / 1e9, 2), "cpu_model": model, "isa": isa,
+            "host_cpus": os.cpu_count(), "pinned_cpus": f"{cpus[0]}..{cpus[-1]}" if cpus else "",
+            "sample": f"{reps} calls of the full {M}x{K} N={N} product with Q8_K quantisation of x "
+                      f"({tot:.1f} s) and {reps_nq} without ({tot_nq:.1f} s): vec_dot_q4_K_q8_K ({isa}), "
+                      f"{cores} threads pinned one per CPU (the job's CPU share of this {os.cpu_count()}-CPU "
+                      f"host), ggml's row chunks of 16; medians"}
 
 
 def headline(args):
@@ -310,11 +373,13 @@ def headline(args):
     log(f"[bench] {runner.ncopies} weight copies ({runner.ncopies * wq.nbytes / 2**30:.2f} GiB); "
         f"geometry {Q.geometry(K, M, N)}")
     torch.cuda.synchronize()
-    t = time_gpu(runner, args.steps, args.warmup)
+    t = time_gpu(runner, args.steps, args.warmup, args.trials)
     sec = t["graph_s"]
     nbytes = algorithmic_bytes(M, K, N)
     achieved = nbytes / sec / 1e9
-    log(f"[bench] graph {sec * 1e6:.2f} us/call ({achieved:.0f} GB/s), eager {t['eager_s'] * 1e6:.2f} us/call")
+    log(f"[bench] graph {sec * 1e6:.3f} us/call median of {t['trials']} (min {t['graph_min_s'] * 1e6:.3f}, "
+        f"max {t['graph_max_s'] * 1e6:.3f}), {achieved:.0f} GB/s; eager {t['eager_s'] * 1e6:.2f} us/call")
+    traffic, _ = read_traffic(M, K, N)
     rec = {
         "metric": METRIC, "value": round(achieved, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": sec * 1e3,
@@ -322,14 +387,16 @@ def headline(args):
         "dtype": "q4_K x q8_1: int8 dot4 -> int32, f32 scale/accumulate",
         "data": "synthetic: W ~ N(0,0.02) -> Q4_K (quantize_row_q4_K_ref arithmetic), x ~ N(0,1); seed 0",
         "config": {"workload": "mistral7b_ffn_gate_14336x4096_b1", "M": M, "K": K, "ncols": N,
-                   "launch": "hipGraph of the K timed calls", "weight_copies": runner.ncopies,
-                   "geometry": Q.geometry(K, M, N)},
+                   "launch": f"hipGraph of the K timed calls, median of {t['trials']} timed replays",
+                   "weight_copies": runner.ncopies, "geometry": Q.geometry(K, M, N)},
         "us_per_call": round(sec * 1e6, 3),
+        "us_per_call_min": round(t["graph_min_s"] * 1e6, 3),
+        "us_per_call_max": round(t["graph_max_s"] * 1e6, 3),
         "us_per_call_eager": round(t["eager_s"] * 1e6, 3),
         "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(), "algorithmic_bytes_per_launch": nbytes},
+                     "traffic": traffic, "algorithmic_bytes_per_launch": nbytes},
     }
     if not args.no_cpu:
         log("[bench] CPU baseline (bounded sample)")
@@ -341,37 +408,38 @@ def sweep(args):
     import _common
     import torch
     Q = _pkg()
-    rows = []
-    seen = set()
     wt = args.wtype
     gtype = Q.GGML_TYPE_Q4_K if wt == "q4_K" else Q.GGML_TYPE_Q6_K
-    table = _common.WORKLOADS if wt == "q4_K" else _common.Q6K_WORKLOADS
-    for wl, items in table.items():
-        for M, K, ns in items:
-            wq = None
-            for N in ns:
-                if (M, K, N) in seen:
-                    continue
-                seen.add((M, K, N))
-                if wq is None:
-                    log(f"[sweep] inputs {wt} {M}x{K}")
-                    wq, _ = make_inputs(Q, M, K, 1, wtype=wt)
-                x = _common.activations(N, K, 0)
-                runner = OpRunner(Q, wq, x, wtype=wt)
-                t = time_gpu(runner, args.steps, args.warmup)
-                sec = t["graph_s"]
-                gbs = algorithmic_bytes(M, K, N, wt) / sec / 1e9
-                r = {"workload": wl, "wtype": wt, "M": M, "K": K, "N": N, "us_per_call": round(sec * 1e6, 3),
-                     "us_eager": round(t["eager_s"] * 1e6, 3), "GBps": round(gbs, 1),
-                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "geometry": Q.geometry(K, M, N, gtype)}
-                rows.append(r)
-                print(json.dumps(r), flush=True)
-                del runner
-                torch.cuda.empty_cache()
+    wq_cache = {}
+    for wl, M, K, N in sweep_configs(wt):
+        if (M, K) not in wq_cache:
+            wq_cache.clear()
+            log(f"[sweep] inputs {wt} {M}x{K}")
+            wq_cache[(M, K)], _ = make_inputs(Q, M, K, 1, wtype=wt)
+        wq = wq_cache[(M, K)]
+        x = _common.activations(N, K, 0)
+        runner = OpRunner(Q, wq, x, wtype=wt)
+        t = time_gpu(runner, args.steps, args.warmup, args.trials)
+        del runner
+        torch.cuda.empty_cache()
+        sec = t["graph_s"]
+        nbytes = algorithmic_bytes(M, K, N, wt)
+        gbs = nbytes / sec / 1e9
+        traffic, op_traffic = read_traffic(M, K, N, wt)
+        r = {"workload": wl, "wtype": wt, "M": M, "K": K, "N": N, "us_per_call": round(sec * 1e6, 3),
+             "us_min": round(t["graph_min_s"] * 1e6, 3), "us_max": round(t["graph_max_s"] * 1e6, 3),
+             "trials": t["trials"], "us_eager": round(t["eager_s"] * 1e6, 3), "GBps": round(gbs, 1),
+             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes,
+             "traffic_gemv_bytes": traffic, "traffic_op_bytes": op_traffic,
+             "traffic_ratio": round(op_traffic / nbytes, 4) if op_traffic else None,
+             "geometry": Q.geometry(K, M, N, gtype)}
+        if wt == "q4_K" and not args.no_cpu:
+            r["cpu_baseline"] = cpu_baseline(wq, x, target_s=args.cpu_seconds, min_reps=10)
+        print(json.dumps(r), flush=True)
 
 
 def profile_mode(args):
-    """Only the GEMV launches of the headline workload (for rocprofv3)."""
+    """Only the op launches of one shape (for rocprofv3)."""
     import ctypes
     import torch
     Q = _pkg()
@@ -389,17 +457,136 @@ def profile_mode(args):
     log(f"[profile] {args.warmup + args.steps} launches of {M}x{K} N={N} done")
 
 
-def copy_calibration(args):
-    """A plain device copy of known size (read N bytes, write N bytes) whose
-    FETCH_SIZE / WRITE_SIZE readings calibrate the GEMV's counter values."""
+def _separator(Q, buf_x, buf_y):
+    """A one-block quantiser launch (32 values): the segment marker of
+    --profile-sweep (the configs' own quantiser launches have >= 4 blocks)."""
+    Q._check(Q.lib().q4k_quantize_row_q8_1(Q._ptr(buf_x), Q._ptr(buf_y), 32, 32, 32, 1, Q._stream()), "separator")
+
+
+def profile_sweep(args):
+    """Plain eager launches of every sweep config, for rocprofv3: first a
+    device copy of CAL_BYTES (counter calibration), then per config a
+    separator launch followed by warmup + steps op launches."""
+    import ctypes
+    import _common
     import torch
-    n = args.copy_cal // 4
-    src = torch.randn(n, device="cuda:0")
+    Q = _pkg()
+    wt = args.wtype
+    dev = torch.device("cuda:0")
+    src = torch.randn(CAL_BYTES // 4, device=dev)
     dst = torch.empty_like(src)
-    for _ in range(args.warmup + args.steps):
+    for _ in range(4):
         torch.add(src, 0.0, out=dst)
-    torch.cuda.synchronize()
-    log(f"[copy-cal] {args.warmup + args.steps} elementwise copies of {n * 4} bytes done")
+    del src, dst
+    sx = torch.zeros(32, device=dev)
+    sy = torch.empty(36, dtype=torch.uint8, device=dev)
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    wq = None
+    for wl, M, K, N in sweep_configs(wt):
+        if wq is None or wq.shape[0] != M or wq.shape[1] != K // 256 * BLOCK_BYTES[wt]:
+            wq, _ = make_inputs(Q, M, K, 1, wtype=wt)
+        runner = OpRunner(Q, wq, _common.activations(N, K, 0), wtype=wt, min_pool_bytes=args.pool_bytes)
+        torch.cuda.synchronize()
+        _separator(Q, sx, sy)
+        for _ in range(args.warmup + args.steps):
+            runner.step(s)
+        torch.cuda.synchronize()
+        del runner
+        torch.cuda.empty_cache()
+        log(f"[profile-sweep] {wl} {wt} {M}x{K} N={N}: {args.warmup + args.steps} launches")
+
+
+def _rows(path):
+    with open(path, newline="") as fh:
+        return list(csv.DictReader(fh))
+
+
+def _grid_threads(r):
+    if "Grid_Size" in r:
+        return int(r["Grid_Size"])
+    return int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+
+
+def _segments(rows, value_of):
+    """Dispatches in order, split at the separator launches: [calibration
+    segment, config 1, config 2, ...]; each a list of (kernel name, value)."""
+    rows = sorted(rows, key=lambda r: int(r["Dispatch_Id"]))
+    segs = [[]]
+    for r in rows:
+        name = r["Kernel_Name"]
+        if "quantize_q8_1_kernel" in name and _grid_threads(r) == 256:
+            segs.append([])
+            continue
+        if "copyBuffer" in name:  # weight copies of the runner set-up
+            continue
+        segs[-1].append((name, value_of(r)))
+    return segs
+
+
+def _short(name):
+    base = name.split("(")[0]
+    return base.replace("void ", "")
+
+
+def _per_kernel(seg, warmup, steps):
+    """{kernel: (launches per op, values of its dispatches in the timed
+    launches)} for a config segment of warmup + steps op launches (a kernel
+    launched n times per op keeps its last n * steps values)."""
+    by = {}
+    for name, v in seg:
+        by.setdefault(name, []).append(v)
+    out = {}
+    for name, vals in by.items():
+        n = max(1, len(vals) // (warmup + steps))
+        out[name] = (n, vals[-n * steps:])
+    return out
+
+
+def summarize(args):
+    """Per-config tables from the rocprofv3 output of a --profile-sweep run:
+    kernel durations (--kernel-trace) or HBM bytes (--pmc FETCH_SIZE /
+    WRITE_SIZE, scaled by the calibration copy's reading)."""
+    d = args.summarize
+    cfgs = sweep_configs(args.wtype)
+    trace = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+    counters = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if trace:
+        segs = _segments(_rows(trace[0]), lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+        assert len(segs) == len(cfgs) + 1, (len(segs), len(cfgs))
+        print("| workload | shape | N | kernel | launches/op | median us | mean us | min us | max us | "
+              "op us (sum of medians) | GEMV GB/s (median) | % of 8 TB/s |")
+        print("|---|---|---|---|---|---|---|---|---|---|---|---|")
+        for (wl, M, K, N), seg in zip(cfgs, segs[1:]):
+            ks = _per_kernel(seg, args.warmup, args.steps)
+            op_us = sum(n * float(np.median(v)) for n, v in ks.values())
+            gemv = [k for k in ks if "gemv" in k]
+            gemv_us = sum(ks[k][0] * float(np.median(ks[k][1])) for k in gemv)
+            gbs = algorithmic_bytes(M, K, N, args.wtype) / (gemv_us * 1e-6) / 1e9 if gemv_us else 0.0
+            for k, (n, v) in ks.items():
+                v = np.asarray(v)
+                print(f"| {wl} | {M}x{K} | {N} | `{_short(k)}` | {n} | {np.median(v):.3f} | {v.mean():.3f} | "
+                      f"{v.min():.3f} | {v.max():.3f} | {op_us:.3f} | {gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} |")
+    if counters:
+        rows = _rows(counters[0])
+        by_counter = {}
+        for r in rows:
+            by_counter.setdefault(r["Counter_Name"], []).append(r)
+        for cname, crows in sorted(by_counter.items()):
+            segs = _segments(crows, lambda r: float(r["Counter_Value"]))
+            assert len(segs) == len(cfgs) + 1, (len(segs), len(cfgs))
+            # the calibration copy (the most frequent kernel before the first
+            # separator) reads and writes CAL_BYTES once per dispatch
+            names = [n for n, _ in segs[0]]
+            copy_kernel = max(set(names), key=names.count)
+            cal = [v for n, v in segs[0] if n == copy_kernel]
+            factor = CAL_BYTES / (float(np.median(cal)) * 1024.0)
+            print(f"# {cname}: calibration copy of {CAL_BYTES} B -> median {np.median(cal):.1f} KiB per dispatch, "
+                  f"scale factor {factor:.4f}")
+            for (wl, M, K, N), seg in zip(cfgs, segs[1:]):
+                ks = _per_kernel(seg, args.warmup, args.steps)
+                gemv = sum(n * float(np.median(v)) for k, (n, v) in ks.items() if "gemv" in k) * 1024 * factor
+                op = sum(n * float(np.median(v)) for n, v in ks.values()) * 1024 * factor
+                print(f"{cname} M={M} K={K} N={N} gemv_bytes={gemv:.0f} op_bytes={op:.0f}")
 
 
 def _pkg():
@@ -412,26 +599,31 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--trials", type=int, default=7, help="timed replays of the K-step graph (median reported)")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--profile", action="store_true", help="plain launches only, for rocprofv3")
+    ap.add_argument("--profile-sweep", action="store_true", help="plain launches of every sweep config, for rocprofv3")
+    ap.add_argument("--pool-bytes", type=int, default=1 << 30, help="--profile-sweep: weight copies per config")
+    ap.add_argument("--summarize", metavar="DIR", help="per-config tables from a --profile-sweep rocprofv3 output")
     ap.add_argument("--shape", type=int, nargs=3, default=[14336, 4096, 1], metavar=("M", "K", "N"))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=2.0, help="--sweep: CPU seconds per config and mode")
     ap.add_argument("--moe", action="store_true",
                     help="time MUL_MAT_ID (one token) on expert-FFN shapes")
     ap.add_argument("--fused", action="store_true",
                     help="time the gate+up SWIGLU launch against two plain launches")
     ap.add_argument("--wtype", choices=sorted(BLOCK_BYTES), default="q4_K",
-                    help="weight format of --sweep and --profile (the headline is Q4_K)")
-    ap.add_argument("--copy-cal", type=int, default=0, metavar="BYTES",
-                    help="run only a plain device copy of BYTES (counter calibration)")
+                    help="weight format of --sweep, --profile and --profile-sweep (the headline is Q4_K)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the Q4_K GEMV has no multi-GPU path here "
               "(rows would shard across GPUs through q4k_op_mul_mat_vec_q); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
-    if args.copy_cal:
-        copy_calibration(args)
+    if args.summarize:
+        summarize(args)
+    elif args.profile_sweep:
+        profile_sweep(args)
     elif args.profile:
         profile_mode(args)
     elif args.fused:

@@ -71,6 +71,7 @@ def lib():
             "orc_cpu_has_avx2": (I, []),
             "orc_cpu_mul_mat_q4_K": (I, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I]),
             "orc_time_cpu_mul_mat_q4_K": (None, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I, I, P]),
+            "orc_set_pin_cpus": (None, [P, I]),
             "orc_quantize_q6_K": (None, [P, P, I64]),
             "orc_dequantize_q6_K": (None, [P, P, I64]),
             "orc_gemv_q6K_q8_1": (I64, [P, I64, I64, I64, P, I64, I64, P, P, P]),
@@ -267,6 +268,13 @@ def cpu_mul_mat_q4_K(w_q: np.ndarray, K: int, x: np.ndarray, nthreads: int = 1, 
     used = lib().orc_cpu_mul_mat_q4_K(_p(w_q), M, K, row_bytes, _p(x), N, K, _p(yq), _p(dst), M,
                                       nthreads, 1 if isa == "avx2" else 0, 1)
     return dst, ("avx2" if used else "scalar")
+
+
+def set_pin_cpus(cpus):
+    """Pins the threads of the CPU path: thread t runs on cpus[t % len]
+    (an empty list: no pinning)."""
+    a = np.ascontiguousarray(np.asarray(list(cpus), dtype=np.int32))
+    lib().orc_set_pin_cpus(_p(a) if a.size else None, int(a.size))
 
 
 def time_cpu_mul_mat_q4_K(w_q: np.ndarray, K: int, x: np.ndarray, nthreads: int, reps: int,

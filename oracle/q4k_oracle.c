@@ -38,8 +38,10 @@
  * Build: oracle/Makefile (gcc, -ffp-contract=off so float expressions are
  * evaluated exactly as written).
  */
+#define _GNU_SOURCE
 #include <math.h>
 #include <pthread.h>
+#include <sched.h>
 #include <stdatomic.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -762,11 +764,32 @@ typedef struct {
     int ith;
 } orc_mm_arg;
 
+/* CPUs the threads of orc_cpu_mul_mat_q4_K are pinned to (thread t on
+ * cpus[t % n]); n = 0: not pinned. */
+static int orc_pin_cpus[1024];
+static int orc_pin_n = 0;
+
+void orc_set_pin_cpus(const int *cpus, int n) {
+    if (n < 0) n = 0;
+    if (n > 1024) n = 1024;
+    for (int i = 0; i < n; ++i) orc_pin_cpus[i] = cpus[i];
+    orc_pin_n = n;
+}
+
+static void orc_pin_self(int t) {
+    if (orc_pin_n == 0) return;
+    cpu_set_t set;
+    CPU_ZERO(&set);
+    CPU_SET(orc_pin_cpus[t % orc_pin_n], &set);
+    pthread_setaffinity_np(pthread_self(), sizeof(set), &set);
+}
+
 #define ORC_ROW_CHUNK 16
 
 static void *orc_mm_worker(void *p) {
     orc_mm_arg *a = (orc_mm_arg *)p;
     orc_mm_job *j = a->job;
+    if (a->ith > 0) orc_pin_self(a->ith);
     const int64_t nbk = j->K / ORC_QK_K;
     /* 1. activations -> Q8_K, columns spread over threads */
     if (j->quantize) {
@@ -809,6 +832,11 @@ int orc_cpu_mul_mat_q4_K(const uint8_t *w, int64_t M, int64_t K, int64_t row_str
     job.quantize = quantize;
     atomic_init(&job.next_chunk, 0);
     pthread_barrier_init(&job.bar, NULL, (unsigned)nthreads);
+    /* the calling thread works as thread 0: pinned for the call, then
+     * restored */
+    cpu_set_t saved;
+    const int restore = orc_pin_n > 0 && pthread_getaffinity_np(pthread_self(), sizeof(saved), &saved) == 0;
+    orc_pin_self(0);
     pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
     orc_mm_arg *args = (orc_mm_arg *)malloc(sizeof(orc_mm_arg) * (size_t)nthreads);
     for (int t = 0; t < nthreads; ++t) {
@@ -818,6 +846,7 @@ int orc_cpu_mul_mat_q4_K(const uint8_t *w, int64_t M, int64_t K, int64_t row_str
     }
     orc_mm_worker(&args[0]);
     for (int t = 1; t < nthreads; ++t) pthread_join(th[t], NULL);
+    if (restore) pthread_setaffinity_np(pthread_self(), sizeof(saved), &saved);
     pthread_barrier_destroy(&job.bar);
     free(th);
     free(args);
