@@ -438,6 +438,29 @@ def sweep(args):
         print(json.dumps(r), flush=True)
 
 
+def _launch_steps(runner, s, args):
+    """warmup eager op launches, then `steps` more: eager, or (--graph)
+    captured into a HIP graph and replayed once, as the timed steps of the
+    benchmark run."""
+    import torch
+    for _ in range(args.warmup):
+        runner.step(s)
+    if not args.graph:
+        for _ in range(args.steps):
+            runner.step(s)
+        return
+    import ctypes
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        for _ in range(args.steps):
+            runner.step(sp)
+    g.replay()
+    torch.cuda.synchronize()
+
+
 def profile_mode(args):
     """Only the op launches of one shape (for rocprofv3)."""
     import ctypes
@@ -451,10 +474,10 @@ def profile_mode(args):
     else:
         runner = OpRunner(Q, wq, x, wtype=args.wtype)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    for _ in range(args.warmup + args.steps):
-        runner.step(s)
+    _launch_steps(runner, s, args)
     torch.cuda.synchronize()
-    log(f"[profile] {args.warmup + args.steps} launches of {M}x{K} N={N} done")
+    log(f"[profile] {args.warmup + args.steps} launches of {M}x{K} N={N} done"
+        f"{' (timed steps as one graph replay)' if args.graph else ''}")
 
 
 def _separator(Q, buf_x, buf_y):
@@ -488,8 +511,7 @@ def profile_sweep(args):
         runner = OpRunner(Q, wq, _common.activations(N, K, 0), wtype=wt, min_pool_bytes=args.pool_bytes)
         torch.cuda.synchronize()
         _separator(Q, sx, sy)
-        for _ in range(args.warmup + args.steps):
-            runner.step(s)
+        _launch_steps(runner, s, args)
         torch.cuda.synchronize()
         del runner
         torch.cuda.empty_cache()
@@ -546,10 +568,11 @@ def summarize(args):
     """Per-config tables from the rocprofv3 output of a --profile-sweep run:
     kernel durations (--kernel-trace) or HBM bytes (--pmc FETCH_SIZE /
     WRITE_SIZE, scaled by the calibration copy's reading)."""
-    d = args.summarize
     cfgs = sweep_configs(args.wtype)
-    trace = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
-    counters = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    trace, counters = [], []
+    for d in args.summarize:
+        trace += glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+        counters += glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
     if trace:
         segs = _segments(_rows(trace[0]), lambda r: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
         assert len(segs) == len(cfgs) + 1, (len(segs), len(cfgs))
@@ -567,10 +590,11 @@ def summarize(args):
                 print(f"| {wl} | {M}x{K} | {N} | `{_short(k)}` | {n} | {np.median(v):.3f} | {v.mean():.3f} | "
                       f"{v.min():.3f} | {v.max():.3f} | {op_us:.3f} | {gbs:.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} |")
     if counters:
-        rows = _rows(counters[0])
         by_counter = {}
-        for r in rows:
-            by_counter.setdefault(r["Counter_Name"], []).append(r)
+        for path in counters:
+            for r in _rows(path):
+                by_counter.setdefault(r["Counter_Name"], []).append(r)
+        per = {}
         for cname, crows in sorted(by_counter.items()):
             segs = _segments(crows, lambda r: float(r["Counter_Value"]))
             assert len(segs) == len(cfgs) + 1, (len(segs), len(cfgs))
@@ -587,6 +611,20 @@ def summarize(args):
                 gemv = sum(n * float(np.median(v)) for k, (n, v) in ks.items() if "gemv" in k) * 1024 * factor
                 op = sum(n * float(np.median(v)) for n, v in ks.values()) * 1024 * factor
                 print(f"{cname} M={M} K={K} N={N} gemv_bytes={gemv:.0f} op_bytes={op:.0f}")
+                per.setdefault((M, K, N), {})[cname] = (gemv, op)
+        if all({"FETCH_SIZE", "WRITE_SIZE"} <= set(v) for v in per.values()):
+            print("| workload | shape | N | algorithmic B | GEMV read B | GEMV written B | op B (all kernels) | "
+                  "op / algorithmic |")
+            print("|---|---|---|---|---|---|---|---|")
+            lines = []
+            for wl, M, K, N in cfgs:
+                f, w = per[(M, K, N)]["FETCH_SIZE"], per[(M, K, N)]["WRITE_SIZE"]
+                alg = algorithmic_bytes(M, K, N, args.wtype)
+                print(f"| {wl} | {M}x{K} | {N} | {alg:,} | {f[0]:,.0f} | {w[0]:,.0f} | {f[1] + w[1]:,.0f} | "
+                      f"{(f[1] + w[1]) / alg:.4f} |")
+                lines.append(f"traffic M={M} K={K} N={N} gemv_bytes={f[0] + w[0]:.0f} op_bytes={f[1] + w[1]:.0f}")
+            print()
+            print("\n".join(lines))
 
 
 def _pkg():
@@ -604,7 +642,10 @@ def main():
     ap.add_argument("--profile", action="store_true", help="plain launches only, for rocprofv3")
     ap.add_argument("--profile-sweep", action="store_true", help="plain launches of every sweep config, for rocprofv3")
     ap.add_argument("--pool-bytes", type=int, default=1 << 30, help="--profile-sweep: weight copies per config")
-    ap.add_argument("--summarize", metavar="DIR", help="per-config tables from a --profile-sweep rocprofv3 output")
+    ap.add_argument("--summarize", metavar="DIR", nargs="+",
+                    help="per-config tables from the rocprofv3 output directories of --profile-sweep runs")
+    ap.add_argument("--graph", action="store_true",
+                    help="--profile/--profile-sweep: run the timed steps as one HIP graph replay")
     ap.add_argument("--shape", type=int, nargs=3, default=[14336, 4096, 1], metavar=("M", "K", "N"))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=2.0, help="--sweep: CPU seconds per config and mode")
