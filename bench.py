@@ -81,15 +81,17 @@ def make_inputs(Q, M, K, N, seed=0, wtype="q4_K"):
     return wq, x
 
 
-def sweep_configs(wtype: str):
-    """(workload, M, K, N) of the sweep, each (M, K, N) once, in table order."""
+def sweep_configs(wtype: str, only=None):
+    """(workload, M, K, N) of the sweep, each (M, K, N) once, in table order;
+    `only`: a list of "MxKxN" strings to keep."""
     import _common
     table = _common.WORKLOADS if wtype == "q4_K" else _common.Q6K_WORKLOADS
+    keep = {tuple(int(v) for v in o.split("x")) for o in only} if only else None
     out, seen = [], set()
     for wl, items in table.items():
         for M, K, ns in items:
             for N in ns:
-                if (M, K, N) not in seen:
+                if (M, K, N) not in seen and (keep is None or (M, K, N) in keep):
                     seen.add((M, K, N))
                     out.append((wl, M, K, N))
     return out
@@ -411,7 +413,7 @@ def sweep(args):
     wt = args.wtype
     gtype = Q.GGML_TYPE_Q4_K if wt == "q4_K" else Q.GGML_TYPE_Q6_K
     wq_cache = {}
-    for wl, M, K, N in sweep_configs(wt):
+    for wl, M, K, N in sweep_configs(wt, args.only):
         if (M, K) not in wq_cache:
             wq_cache.clear()
             log(f"[sweep] inputs {wt} {M}x{K}")
@@ -505,7 +507,7 @@ def profile_sweep(args):
     sy = torch.empty(36, dtype=torch.uint8, device=dev)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     wq = None
-    for wl, M, K, N in sweep_configs(wt):
+    for wl, M, K, N in sweep_configs(wt, args.only):
         if wq is None or wq.shape[0] != M or wq.shape[1] != K // 256 * BLOCK_BYTES[wt]:
             wq, _ = make_inputs(Q, M, K, 1, wtype=wt)
         runner = OpRunner(Q, wq, _common.activations(N, K, 0), wtype=wt, min_pool_bytes=args.pool_bytes)
@@ -568,7 +570,7 @@ def summarize(args):
     """Per-config tables from the rocprofv3 output of a --profile-sweep run:
     kernel durations (--kernel-trace) or HBM bytes (--pmc FETCH_SIZE /
     WRITE_SIZE, scaled by the calibration copy's reading)."""
-    cfgs = sweep_configs(args.wtype)
+    cfgs = sweep_configs(args.wtype, args.only)
     trace, counters = [], []
     for d in args.summarize:
         trace += glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
@@ -598,6 +600,13 @@ def summarize(args):
         for cname, crows in sorted(by_counter.items()):
             segs = _segments(crows, lambda r: float(r["Counter_Value"]))
             assert len(segs) == len(cfgs) + 1, (len(segs), len(cfgs))
+            if cname not in ("FETCH_SIZE", "WRITE_SIZE"):  # raw counts per dispatch
+                for (wl, M, K, N), seg in zip(cfgs, segs[1:]):
+                    ks = _per_kernel(seg, args.warmup, args.steps)
+                    for k, (n, v) in ks.items():
+                        print(f"{cname} M={M} K={K} N={N} kernel={_short(k).replace(' ', '')} launches/op={n} "
+                              f"median={float(np.median(v)):.0f}")
+                continue
             # the calibration copy (the most frequent kernel before the first
             # separator) reads and writes CAL_BYTES once per dispatch
             names = [n for n, _ in segs[0]]
@@ -612,7 +621,7 @@ def summarize(args):
                 op = sum(n * float(np.median(v)) for n, v in ks.values()) * 1024 * factor
                 print(f"{cname} M={M} K={K} N={N} gemv_bytes={gemv:.0f} op_bytes={op:.0f}")
                 per.setdefault((M, K, N), {})[cname] = (gemv, op)
-        if all({"FETCH_SIZE", "WRITE_SIZE"} <= set(v) for v in per.values()):
+        if per and all({"FETCH_SIZE", "WRITE_SIZE"} <= set(v) for v in per.values()):
             print("| workload | shape | N | algorithmic B | GEMV read B | GEMV written B | op B (all kernels) | "
                   "op / algorithmic |")
             print("|---|---|---|---|---|---|---|---|")
@@ -644,6 +653,8 @@ def main():
     ap.add_argument("--pool-bytes", type=int, default=1 << 30, help="--profile-sweep: weight copies per config")
     ap.add_argument("--summarize", metavar="DIR", nargs="+",
                     help="per-config tables from the rocprofv3 output directories of --profile-sweep runs")
+    ap.add_argument("--only", nargs="+", metavar="MxKxN",
+                    help="--profile-sweep/--summarize: only these configs of the sweep")
     ap.add_argument("--graph", action="store_true",
                     help="--profile/--profile-sweep: run the timed steps as one HIP graph replay")
     ap.add_argument("--shape", type=int, nargs=3, default=[14336, 4096, 1], metavar=("M", "K", "N"))

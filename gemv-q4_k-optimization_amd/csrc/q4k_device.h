@@ -170,6 +170,10 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 //             of super-block kb = 16i + g at c*qcol + 4096i + 1024m +
 //             16(4g + 2h + j') + t -- lane 4g + 2h + j' reads, for each m, the 16
 //             values that share one Q6_K scale.
+//   Q6K dense the Q6K tile layout with qcol = K: the row's last, partial
+//             16-block group packs its four chunks 64 bytes per block apart
+//             (1024m becomes cs*m, cs = 64*(nb mod 16); group_chunk_stride),
+//             for column counts whose padded columns would not fit the LDS.
 //
 // Auxiliary terms for the linear and Q4K layouts: per 32-value block b of
 // column c, dk[c*K/32 + b] = (d8, d8 * sum of the block's q8) as a float2 --
@@ -184,17 +188,28 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 constexpr int kLayoutLinear = 0;
 constexpr int kLayoutQ4K = 1;
 constexpr int kLayoutQ6K = 2;
+constexpr int kLayoutQ6KDense = 3;
 
-// LDS offset of values [4e, 4e+4) of 32-value block b of column c.
+constexpr bool is_q6_layout(int layout) { return layout == kLayoutQ6K || layout == kLayoutQ6KDense; }
+
+// Chunk stride of 16-block group i of a row of nb super-blocks in the dense
+// layout: 1024 bytes for a full group, 64 per block for a partial last one.
+__host__ __device__ constexpr int group_chunk_stride(int i, int nb) {
+    return 16 * (i + 1) <= nb ? 1024 : (nb & 15) * 64;
+}
+
+// LDS offset of values [4e, 4e+4) of 32-value block b of column c (rows of
+// nb super-blocks).
 template <int LAYOUT>
-__device__ __forceinline__ int q8_offset(int c, int qcol, int b, int e) {
+__device__ __forceinline__ int q8_offset(int c, int qcol, int nb, int b, int e) {
     if (LAYOUT == kLayoutLinear) return c * qcol + b * 32 + e * 4;
     const int kb = b >> 3, s = b & 7;
     if (LAYOUT == kLayoutQ4K)
-        return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (e >> 2)) * 1024 +
-               ((kb & 15) * 4 + (s >> 1)) * 16 + (e & 3) * 4;
+        return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (e >> 2)) * 1024 + ((kb & 15) * 4 + (s >> 1)) * 16 +
+               (e & 3) * 4;
+    const int cs = LAYOUT == kLayoutQ6KDense ? group_chunk_stride(kb >> 4, nb) : 1024;
     // Q6K: s = 4h + m, values 16j' + 4(e & 3) + [0, 4) with j' = e >> 2
-    return c * qcol + (kb >> 4) * 4096 + (s & 3) * 1024 + ((kb & 15) * 4 + (s >> 2) * 2 + (e >> 2)) * 16 +
+    return c * qcol + (kb >> 4) * 4096 + (s & 3) * cs + ((kb & 15) * 4 + (s >> 2) * 2 + (e >> 2)) * 16 +
            (e & 3) * 4;
 }
 
@@ -211,7 +226,7 @@ __device__ __forceinline__ int q6_sq_index(int total, int nblk, int c, int b, in
 template <int LAYOUT>
 __device__ __forceinline__ void store_aux(void *aux, int total, int nblk, int c, int b, int qb, int half,
                                           float d8, int qsum, int hsum) {
-    if (LAYOUT == kLayoutQ6K) {
+    if (is_q6_layout(LAYOUT)) {
         if (half == 0) reinterpret_cast<float *>(aux)[qb] = d8;
         reinterpret_cast<int *>(aux)[q6_sq_index(total, nblk, c, b, half)] = -32 * hsum;
     } else if (half == 0) {
@@ -398,7 +413,7 @@ __device__ __forceinline__ void quantize_block_part(const float (&v)[32 / LPB], 
     }
     int hsum, fsum;
     block_sums<LPB>(qsum[0], hsum, fsum);
-    int8_t *dst = q8s + q8_offset<LAYOUT>(c, qcol, b, e * (V / 4));
+    int8_t *dst = q8s + q8_offset<LAYOUT>(c, qcol, nblk >> 3, b, e * (V / 4));
     if (V == 4) *reinterpret_cast<uint32_t *>(dst) = word[0];
     else *reinterpret_cast<uint2 *>(dst) = make_uint2(word[0], word[V / 4 - 1]);
     const float d8 = (float)(_Float16)d;
@@ -528,7 +543,7 @@ __device__ __forceinline__ void store_q81_part(uint32_t w0, uint32_t w1, uint32_
     block_sums<4>(__builtin_amdgcn_sdot4((int)w0, 0x01010101, __builtin_amdgcn_sdot4((int)w1, 0x01010101, 0, false),
                                          false),
                   hsum, fsum);
-    *reinterpret_cast<uint2 *>(q8s + q8_offset<LAYOUT>(c, qcol, b, 2 * quarter)) = make_uint2(w0, w1);
+    *reinterpret_cast<uint2 *>(q8s + q8_offset<LAYOUT>(c, qcol, nblk >> 3, b, 2 * quarter)) = make_uint2(w0, w1);
     if ((quarter & 1) == 0)
         store_aux<LAYOUT>(aux, total, nblk, c, b, qb, quarter >> 1, half_bits_to_float(ds), fsum, hsum);
     if (sq_out && quarter == 0) sq_out[qb] = fsum;

@@ -77,7 +77,7 @@ struct SumsOut {
 // automatic geometry picks for plain products are).
 const void *q4k_sums_kernel(int nc, int waves, int pro, int slots);
 const void *q4k_bpl_sums_kernel(int waves);
-const void *q6k_sums_kernel(int nc, int waves, int pro, int slots);
+const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense);
 
 // Q6_K weight checks and launch (q6k_gemv.hip), for the type-dispatching
 // entry points of q4k_gemv.hip.
@@ -103,7 +103,9 @@ inline int64_t pad512(int64_t k) { return (k + 511) / 512 * 512; }
 // 16.8 us, 8 columns 27.2 vs 35.5 us; 8192 x 28672 at 2 columns 32.0 vs
 // 33.2 us; 4096-value rows up to 8 columns stay in one launch).
 inline bool prefer_prequantised(int64_t K, int64_t ncols) { return K * ncols > 40960; }
-// LDS bytes of one staged q8 column in a tile layout (whole 16-block groups)
-inline int q8_col_bytes(int K) { return (K + 4095) / 4096 * 4096; }
+// LDS bytes of one staged q8 column in a tile layout: whole 16-block groups,
+// or exactly K in the dense Q6_K layout (whose last, partial group packs its
+// chunks 64 bytes per block apart)
+inline int q8_col_bytes(int K, bool dense = false) { return dense ? K : (K + 4095) / 4096 * 4096; }
 
 }  // namespace q4k

@@ -65,8 +65,15 @@ __global__ __launch_bounds__(256) void q6_group_sums_kernel(Q6SumsParams p) {
 // LDS of the staged activation: q8 columns in the Q6K layout, d8 per
 // 32-value block (K/8 bytes per column), the -32*sum(q8) terms per 16 values
 // (K/4 bytes per column), then a result ring per wave.
-static int q6_act_bytes(int K, int nc) { return nc * (q8_col_bytes(K) + K / 8 + K / 4); }
-static int q6_tile_lds_bytes(int K, int nc, int waves) { return q6_act_bytes(K, nc) + waves * ring_floats(nc) * 4; }
+static int q6_act_bytes(int K, int nc, bool dense) { return nc * (q8_col_bytes(K, dense) + K / 8 + K / 4); }
+static int q6_tile_lds_bytes(int K, int nc, int waves, bool dense) {
+    return q6_act_bytes(K, nc, dense) + waves * ring_floats(nc) * 4;
+}
+
+// Column counts with dense-layout kernels: from 5 columns up, where halving
+// the column count (two launches, each streaming the whole weight matrix) is
+// what the dense layout's saving of up to 4095 bytes per column avoids.
+constexpr int kDenseMinCols = 5;
 
 struct Q6Geometry {
     int waves = 16;
@@ -74,6 +81,7 @@ struct Q6Geometry {
     int lds = 0;
     int lds_launch = 0;
     int nc_chunk = 1;
+    bool dense = false;  // nc_chunk columns fit the LDS only in the dense layout
     int rows_base = 0;
     int rows_extra = 0;
     int prologue = 0;
@@ -93,7 +101,15 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
     int nc = (int)N;
-    while (nc > 1 && q6_tile_lds_bytes((int)K, nc, 16) > max_lds) nc = (nc + 1) / 2;
+    // Measured on MI355X: 4096 x 14336 at 8 columns, one dense launch 26.8 us
+    // against two padded 4-column launches 34.5 us.
+    while (nc > 1 && q6_tile_lds_bytes((int)K, nc, 16, false) > max_lds) {
+        if (nc >= kDenseMinCols && q6_tile_lds_bytes((int)K, nc, 16, true) <= max_lds) {
+            g.dense = true;
+            break;
+        }
+        nc = (nc + 1) / 2;
+    }
     g.nc_chunk = nc;
     const int owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load(), oslots = g_ovr_slots.load();
     g.grid = owgs > 0 ? owgs : grid_per_matrix(cus, mats, M);
@@ -114,9 +130,10 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     // single-matrix shape it measured slower (1024 x 4096: 3.71 -> 4.71 us).
     g.slots = mats > 1 && steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
     if (oslots == 1 || oslots == 2) g.slots = oslots;
+    if (g.dense) g.slots = 1;  // the dense kernels are one-slot
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
-    g.lds = q6_tile_lds_bytes((int)K, nc, g.waves);
+    g.lds = q6_tile_lds_bytes((int)K, nc, g.waves, g.dense);
     g.lds_launch = g.lds;
     if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
     const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave, nc);
@@ -126,10 +143,22 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     return g;
 }
 
-template <int NC, int WAVES, int S, int EPI, bool BATCH>
+template <int NC, int WAVES, int S, int EPI, bool BATCH, bool DENSE = false>
 static const void *q6_sym(int pro) {
-    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 0, S, EPI, BATCH>)
-                    : reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 1, S, EPI, BATCH>);
+    return pro == 0 ? reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 0, S, EPI, BATCH, false, DENSE>)
+                    : reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 1, S, EPI, BATCH, false, DENSE>);
+}
+
+template <int WAVES, bool BATCH>
+static const void *q6_sym_dense(int nc, int pro) {
+    static_assert(kDenseMinCols == 5, "dense kernels for 5..8 columns");
+    switch (nc) {
+        case 5: return q6_sym<5, WAVES, 1, kEpiNone, BATCH, true>(pro);
+        case 6: return q6_sym<6, WAVES, 1, kEpiNone, BATCH, true>(pro);
+        case 7: return q6_sym<7, WAVES, 1, kEpiNone, BATCH, true>(pro);
+        case 8: return q6_sym<8, WAVES, 1, kEpiNone, BATCH, true>(pro);
+        default: return nullptr;
+    }
 }
 
 template <int WAVES, int S, bool BATCH>
@@ -154,8 +183,12 @@ static const void *q6_kernel_epi(int waves, int pro, int slots) {
 }
 
 template <bool BATCH>
-static const void *q6_kernel_for(int nc, int waves, int pro, int slots, int fused) {
+static const void *q6_kernel_for(int nc, int waves, int pro, int slots, int fused, bool dense) {
     if (pro != 0 && pro != 1) return nullptr;
+    if (dense) {
+        if (fused || slots != 1) return nullptr;
+        return waves <= 8 ? q6_sym_dense<8, BATCH>(nc, pro) : q6_sym_dense<16, BATCH>(nc, pro);
+    }
     if (fused) {
         if (nc != 1) return nullptr;
         return fused == kFusedGate ? q6_kernel_epi<kEpiGlu, BATCH>(waves, pro, slots)
@@ -194,8 +227,11 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
     if (ldx > INT32_MAX || stride_col_y > INT32_MAX) return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
+        // a last chunk of under kDenseMinCols columns is staged padded
+        const bool dense = geo.dense && nc >= kDenseMinCols;
         int lds_launch = geo.lds_launch;
-        const int lds = q6_tile_lds_bytes((int)ne00, nc, geo.waves);
+        const int lds = q6_tile_lds_bytes((int)ne00, nc, geo.waves, dense);
+        if (lds > di->max_lds) return Q4K_EUNSUPPORTED;
         if (lds_launch < lds) lds_launch = lds;
         GemvParams p{};
         p.w = static_cast<const uint8_t *>(src0);
@@ -210,11 +246,11 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         p.K = (int)ne00;
         p.nb = (int)(ne00 / kQK);
         p.G = (p.nb + 15) / 16;
-        p.qcol = q8_col_bytes((int)ne00);
+        p.qcol = q8_col_bytes((int)ne00, dense);
         p.vec_ok = x && aligned(p.x, 16) && (ldx % 4 == 0);
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
-        p.ring_off = q6_act_bytes(p.K, nc);
+        p.ring_off = q6_act_bytes(p.K, nc, dense);
         p.nblk32 = fastdiv_init((uint32_t)(ne00 / 32));
         if (fused) {
             p.gate = ep->gate;
@@ -222,11 +258,11 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
             p.glu_op = ep->glu_op;
         }
-        const void *fn = bl ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused)
-                            : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused);
+        const void *fn = bl ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
+                            : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
         if (so) {  // parity variant: this chunk's columns of the group sums
             if (fused || bl) return Q4K_EINVAL;
-            fn = q6k_sums_kernel(nc, geo.waves, geo.prologue, geo.slots);
+            fn = q6k_sums_kernel(nc, geo.waves, geo.prologue, geo.slots, dense);
             if (!fn) return Q4K_EUNSUPPORTED;  // a launch shape with no parity variant (overrides)
             p.sums = so->sums + c0 * ne01 * (ne00 / 16);
         }
@@ -351,7 +387,7 @@ int q6k_group_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, c
     DeviceInfo *di = nullptr;
     st = device_info(&di);
     if (st != Q4K_OK) return st;
-    const int lds = q6_act_bytes((int)ne00, 1);
+    const int lds = q6_act_bytes((int)ne00, 1, false);
     if (lds > di->max_lds) return Q4K_EUNSUPPORTED;
     st = ensure_lds(di, reinterpret_cast<const void *>(&q6_group_sums_kernel), lds);
     if (st != Q4K_OK) return st;

@@ -120,14 +120,26 @@ struct Q6Act {
     int4 s0;
 };
 
+// FULL: group i is stored with its chunks 1 KB apart (immediate offsets): a
+// whole 16-block group, or any group of the padded layout; else the row's
+// last, partial group of the dense layout (chunks 64 bytes per block apart).
+template <bool FULL = true>
 __device__ __forceinline__ Q6Act q6_act(const GemvParams &p, const Q6Lane &ln, int i, int c, int ncols,
                                         const int8_t *q8s, const uint8_t *aux) {
     const int kb = 16 * i + ln.g;
     const int kbc = kb < p.nb ? kb : 0;  // blocks past the row's end: weights read as 0
-    const int8_t *qa = q8s + c * p.qcol + i * 4096 + ln.lane * 16;
+    const int8_t *qa = q8s + c * p.qcol + i * 4096;
     Q6Act a;
+    if constexpr (FULL) {
+        qa += ln.lane * 16;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) a.a[m] = *reinterpret_cast<const u32x4 *>(qa + 1024 * m);
+        for (int m = 0; m < 4; ++m) a.a[m] = *reinterpret_cast<const u32x4 *>(qa + 1024 * m);
+    } else {
+        const int cs = (p.nb & 15) * 64;
+        qa += kb < p.nb ? ln.lane * 16 : (ln.lane & 3) * 16;  // lanes past the row's end read block 0
+#pragma unroll
+        for (int m = 0; m < 4; ++m) a.a[m] = *reinterpret_cast<const u32x4 *>(qa + cs * m);
+    }
     const int nblk = p.K / 32;
     a.d8 = *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(aux) + c * nblk + kbc * 8 + 4 * ln.h);
     a.s0 = *reinterpret_cast<const int4 *>(reinterpret_cast<const int *>(aux) + ncols * nblk + c * 2 * nblk +
@@ -184,10 +196,11 @@ __device__ __forceinline__ void q6_record_sums(const GemvParams &p, const Q6Lane
 
 // Consumes one group held in w (one row, or the row and its gate row); at
 // the tile's last group moves the R x NC sums to the result ring.
-template <int NC, int R, int EPI, bool SUMS = false>
-__device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6Lane &ln, Step st,
-                                                 const int8_t *q8s, const uint8_t *aux, const Q6Regs (&w)[R],
-                                                 float (&acc)[R][NC], ResultRing &rr) {
+// FULL: group st.i has its chunks 1 KB apart (see q6_act).
+template <int NC, int R, bool SUMS, bool FULL>
+__device__ __forceinline__ void q6_process_group_as(const GemvParams &p, const Q6Lane &ln, Step st,
+                                                    const int8_t *q8s, const uint8_t *aux, const Q6Regs (&w)[R],
+                                                    float (&acc)[R][NC], const ResultRing &rr) {
     uint32_t v[R][4][4];
     int sc[R][4];
     float d[R];
@@ -199,7 +212,7 @@ __device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6La
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const Q6Act a = q6_act(p, ln, st.i, c, NC, q8s, aux);
+        const Q6Act a = q6_act<FULL>(p, ln, st.i, c, NC, q8s, aux);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             int s[4];
@@ -214,6 +227,18 @@ __device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6La
             acc[r][c] = __builtin_fmaf(d[r], f, acc[r][c]);
         }
     }
+}
+
+// DENSE: the activation is staged in the dense layout (the branch on the
+// group kind is taken once per group, wave-uniformly).
+template <int NC, int R, int EPI, bool SUMS = false, bool DENSE = false>
+__device__ __forceinline__ void q6_process_group(const GemvParams &p, const Q6Lane &ln, Step st,
+                                                 const int8_t *q8s, const uint8_t *aux, const Q6Regs (&w)[R],
+                                                 float (&acc)[R][NC], ResultRing &rr) {
+    if (!DENSE || __builtin_amdgcn_readfirstlane(16 * (st.i + 1) <= p.nb))
+        q6_process_group_as<NC, R, SUMS, true>(p, ln, st, q8s, aux, w, acc, rr);
+    else
+        q6_process_group_as<NC, R, SUMS, false>(p, ln, st, q8s, aux, w, acc, rr);
     if (st.i == p.G - 1) tile_to_ring<NC, R, EPI>(p, ln.lane, acc, rr);
 }
 
@@ -253,10 +278,15 @@ __device__ __forceinline__ void q6_process_reg(const GemvParams &p, const Q6Lane
 // column).
 // SUMS: the parity variant of a plain launch, which also stores every lane's
 // int32 group sums (p.sums).
-template <int NC, int WAVES, int PRO, int S, int EPI = kEpiNone, bool BATCH = false, bool SUMS = false>
+// DENSE: the activation columns take K bytes each in LDS (kLayoutQ6KDense)
+// instead of whole 16-block groups.
+template <int NC, int WAVES, int PRO, int S, int EPI = kEpiNone, bool BATCH = false, bool SUMS = false,
+          bool DENSE = false>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr bool GLU = EPI == kEpiGlu;
     static_assert(!SUMS || (EPI == kEpiNone && !BATCH), "parity variants of the plain product only");
+    static_assert(!DENSE || EPI == kEpiNone, "the dense layout is for several columns");
+    constexpr int kLayout = DENSE ? kLayoutQ6KDense : kLayoutQ6K;
     static_assert(EPI == kEpiNone || NC == 1, "the fused epilogue is one-column");
     constexpr int R = GLU ? 2 : 1;
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
@@ -299,10 +329,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
 #pragma unroll
     for (int k = 0; k < kEarly; ++k) q6_load_step<R>(p, ln, ws, st[k], w[k]);
     if (p.x)
-        stage_f32_finish<kLayoutQ6K, kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs,
+        stage_f32_finish<kLayout, kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs,
                                                           p.qcol, q8s, aux);
     else
-        stage_q81_finish<kLayoutQ6K, kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s,
+        stage_q81_finish<kLayout, kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s,
                                                     aux);
     __syncthreads();
     if (remaining == 0) return;  // no barrier below this point
@@ -318,7 +348,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
 
     // (one column at 16 waves, eight at 8 waves: wider variants would spill
     // registers)
-    if constexpr ((NC == 1 || WAVES == 8) && R == 1 && S <= 2) {
+    if constexpr ((NC == 1 || WAVES == 8) && R == 1 && S <= 2 && !DENSE) {
         if (p.G == 1) {  // every step reads the same activation slice: keep it in registers
             Q6Act a0[NC];
 #pragma unroll
@@ -340,7 +370,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     for (;;) {
 #pragma unroll
         for (int k = 0; k < S; ++k) {
-            q6_process_group<NC, R, EPI, SUMS>(p, ln, st[k], q8s, aux, w[k], acc, rr);
+            q6_process_group<NC, R, EPI, SUMS, DENSE>(p, ln, st[k], q8s, aux, w[k], acc, rr);
             st[k] = next_step(st[(k + S - 1) % S], p.G);
             q6_load_step<R>(p, ln, ws, st[k], w[k]);
         }

@@ -11,11 +11,25 @@
 namespace q4k {
 namespace {
 
-template <int NC, int WAVES>
+template <int NC, int WAVES, bool DENSE = false>
 const void *q6_sums(int pro) {
-    if (pro == 0) return reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 0, 1, kEpiNone, false, true>);
-    if (pro == 1) return reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 1, 1, kEpiNone, false, true>);
+    if (pro == 0)
+        return reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 0, 1, kEpiNone, false, true, DENSE>);
+    if (pro == 1)
+        return reinterpret_cast<const void *>(&gemv_q6k_kernel<NC, WAVES, 1, 1, kEpiNone, false, true, DENSE>);
     return nullptr;
+}
+
+// the dense-layout kernels (5 to 8 columns)
+template <int WAVES>
+const void *q6_sums_dense(int nc, int pro) {
+    switch (nc) {
+        case 5: return q6_sums<5, WAVES, true>(pro);
+        case 6: return q6_sums<6, WAVES, true>(pro);
+        case 7: return q6_sums<7, WAVES, true>(pro);
+        case 8: return q6_sums<8, WAVES, true>(pro);
+        default: return nullptr;
+    }
 }
 
 template <int WAVES>
@@ -35,8 +49,9 @@ const void *q6_sums_nc(int nc, int pro) {
 
 }  // namespace
 
-const void *q6k_sums_kernel(int nc, int waves, int pro, int slots) {
+const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense) {
     if (slots != 1) return nullptr;
+    if (dense) return waves <= 8 ? q6_sums_dense<8>(nc, pro) : q6_sums_dense<16>(nc, pro);
     return waves <= 8 ? q6_sums_nc<8>(nc, pro) : q6_sums_nc<16>(nc, pro);
 }
 

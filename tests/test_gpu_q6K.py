@@ -173,6 +173,32 @@ def test_eight_wave_register_path_long_products(Q, O, gpu):
     assert np.array_equal(y, y2)
 
 
+@pytest.mark.parametrize("M,K,waves", [(300, 12544, 8), (1000, 13568, 16), (300, 14080, 8), (1000, 14336, 16)])
+def test_dense_layout_partial_groups(Q, O, gpu, M, K, waves):
+    """Eight columns whose padded staging would not fit the LDS run in one
+    launch with the dense layout (the last, partial 16-block group packed:
+    1, 5, 7 and 8 blocks here), at 8 and 16 waves: outputs of the in-kernel
+    and the pre-quantised routes against the oracle, and the launch's int32
+    group sums exact."""
+    import torch
+    N = 8
+    geo = Q.geometry(K, M, N, wtype=Q.GGML_TYPE_Q6_K)
+    assert geo["cols_per_launch"] == N and geo["waves_per_wg"] == waves
+    # K bytes of q8 per column, d8 and offset terms, a 256-byte ring per wave
+    assert geo["lds_bytes"] == N * (K + K // 8 + K // 4) + waves * 64 * 4
+    wq, x = inputs(Q, M, K, N, seed=3)
+    q8 = O.quantize_q8_1(x)
+    ref = O.gemv_q6K_q8_1(wq, K, q8)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    ws = torch.empty(Q.q8_1_bytes(K, N), dtype=torch.uint8, device=gpu)
+    for w in (None, ws):
+        y, s16, _ = Q.mul_mat_vec_q_sums(wd, K, xd, workspace=w, wtype=Q.GGML_TYPE_Q6_K)
+        assert np.array_equal(s16.cpu().numpy(), ref["s16"]), f"K={K}: group sums differ"
+        y2 = Q.mul_mat_vec_q(wd, K, xd, workspace=w, wtype=Q.GGML_TYPE_Q6_K)
+        assert torch.equal(y, y2)
+        _common.assert_within_tolerance(O, y2.cpu().numpy(), ref, f"dense {M}x{K} N={N}")
+
+
 # ------------------------------------------------------- workloads ----
 # Q6_K tensors of a Q4_K_M model: ffn_down (4096 x 14336), attn_v
 # (1024 x 4096) and the output projection (32000 x 4096, Mistral 7B).
