@@ -558,7 +558,8 @@ def _per_kernel(seg, warmup, steps):
     launched n times per op keeps its last n * steps values)."""
     by = {}
     for name, v in seg:
-        by.setdefault(name, []).append(v)
+        if "q4k::" in name:  # the library's kernels (not torch's graph-replay fill)
+            by.setdefault(name, []).append(v)
     out = {}
     for name, vals in by.items():
         n = max(1, len(vals) // (warmup + steps))
