@@ -20,6 +20,7 @@
 #include "../../include/q4k_gemv.h"
 #include "q4k_runtime.h"
 #include "q4k_gemv_kernels.h"
+#include "q4k_mfma.h"
 #include "q4k_tile.h"
 
 namespace q4k {
@@ -192,6 +193,9 @@ struct Geometry {
     int rows_extra = 0;
     int prologue = 0;   // tile kernel: when the first weight loads go out (PRO)
     int slots = 2;      // tile kernel: groups in flight per wave (S)
+    int mfma = 0;       // 1: matrix-core kernel (tiles of 16 rows; rows_base/rows_extra count tiles)
+    int ks = 1;         // matrix-core kernel: waves sharing one tile
+    int segs = 1;       // matrix-core kernel: summation segments of a row
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
@@ -220,6 +224,51 @@ static int lds_bytes(int K, int nc) { return nc * (q8_col_bytes(K) + K / 4); }
 // The tile kernel adds a result ring per wave after the activation.
 static int tile_lds_bytes(int K, int nc, int waves) { return lds_bytes(K, nc) + waves * ring_floats(nc) * 4; }
 static int lds_bytes_linear(int K) { return K + K / 4; }
+
+// Products that run on the matrix-core kernel when no override says
+// otherwise: eight columns of 4096 or more row tiles.  Measured on MI355X
+// against the tile kernel (interleaved, one process): 128256 x 4096 N=8
+// 79.7 against 83.0 us, 14336 x 4096 N=8 even (15.64 against 15.65); slower
+// on every other shape of 2-8 columns, by 10-100 % (4096 x 4096, 1024 x
+// 4096, 4096 x 14336, 28672 x 8192).  Its VALU work is a third lower, but
+// each of its loads reads 144 bytes from each of 16 rows: at 3.7 TB/s that
+// access pattern, not the arithmetic, bounds it.
+static bool use_mfma(int64_t M, int64_t N) { return N == 8 && (M + kMfmaRows - 1) / kMfmaRows >= 4096; }
+
+// The matrix-core kernel: one workgroup per CU (at most one per tile) of 8
+// or 16 waves, the tiles of 16 rows split evenly over the workgroups, and as
+// many waves sharing a tile (KS) as leave every wave group a tile in the
+// first round -- KS at most the S summation segments of a row (S = min(8,
+// the largest power of two <= the super-blocks per row), a function of K
+// alone, which fixes the summation order).
+static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, int nc, int owgs, int owaves) {
+    Geometry g;
+    const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
+    const int cus = di.cus > 0 ? di.cus : 1;
+    const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
+    g.mfma = 1;
+    g.R = kMfmaRows;
+    g.slots = 2;
+    g.nc_chunk = nc;
+    const int64_t wgs = owgs > 0 ? owgs : cus;
+    g.grid = (int)(tiles < wgs ? tiles : wgs);
+    if (g.grid < 1) g.grid = 1;
+    g.rows_base = (int)(tiles / g.grid);
+    g.rows_extra = (int)(tiles % g.grid);
+    const int64_t nt = g.rows_base + (g.rows_extra ? 1 : 0);
+    g.waves = 16;  // measured faster than 8 where the kernel is chosen
+    if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;
+    const int64_t nb = K / kQK;
+    g.segs = 1;
+    while (g.segs < kMfmaMaxSegs && 2 * g.segs <= nb) g.segs *= 2;
+    int groups = 1;
+    while (groups < g.waves && 2 * groups <= nt) groups *= 2;
+    g.ks = g.waves / groups;
+    while (g.ks > g.segs) g.ks /= 2;
+    g.lds = mfma_lds_bytes((int)K, nc, g.waves);
+    g.lds_launch = g.lds <= max_lds / 2 ? max_lds / 2 + 256 : g.lds;  // one workgroup per CU
+    return g;
+}
 
 // Launch geometry for an (M, K, N) product.
 //  tile kernel: one workgroup per CU (requesting just over half the CU's LDS
@@ -278,6 +327,11 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         g.lds = lds_bytes_linear((int)K);
         g.lds_launch = g.lds;
         return g;
+    }
+    if (!fused && mats == 1 && (okern == 4 || (okern == 0 && use_mfma(M, N)))) {
+        int mc = (int)N;
+        while (mc > 1 && mfma_lds_bytes((int)K, mc, 16) > max_lds) mc = (mc + 1) / 2;
+        if (mfma_lds_bytes((int)K, mc, 16) <= max_lds) return pick_geometry_mfma(di, K, M, mc, owgs, owaves);
     }
     g.grid = owgs > 0 ? owgs : grid_per_matrix(cus, mats, M);
     // One column with rows of at most 8192 values and ~500 KB or more of
@@ -478,6 +532,25 @@ static const void *gemv_kernel_for(int nc, int R, int waves, int pro, int slots)
     return slots == 4 ? gemv_sym_r<16, 4>(nc, R, pro) : gemv_sym_r<16, 2>(nc, R, pro);
 }
 
+template <int WAVES>
+static const void *mfma_kernel_nc(int nc) {
+    switch (nc) {
+        case 1: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<1, WAVES>);
+        case 2: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<2, WAVES>);
+        case 3: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<3, WAVES>);
+        case 4: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<4, WAVES>);
+        case 5: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<5, WAVES>);
+        case 6: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<6, WAVES>);
+        case 7: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<7, WAVES>);
+        case 8: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<8, WAVES>);
+        default: return nullptr;
+    }
+}
+
+static const void *mfma_kernel_for(int nc, int waves) {
+    return waves > 8 ? mfma_kernel_nc<16>(nc) : mfma_kernel_nc<8>(nc);
+}
+
 static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc, hipStream_t stream,
                        const BatchLaunch *bl = nullptr) {
     const void *fn = nullptr;
@@ -500,6 +573,12 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
         p.ring_off = lds_bytes(p.K, nc);
+    } else if (geo.mfma) {
+        fn = p.sums ? q4k_mfma_sums_kernel(nc, geo.waves) : mfma_kernel_for(nc, geo.waves);
+        p.rows_base = geo.rows_base;
+        p.rows_extra = geo.rows_extra;
+        p.rpw = geo.ks;
+        p.ntiles = geo.segs;
     } else if (geo.bpl == 2 && nc == 1) {
         if (p.sums) return Q4K_EUNSUPPORTED;  // no parity variant of the override-only kernel
         fn = reinterpret_cast<const void *>(&gemv_q4k_blk_kernel<8>);
@@ -570,13 +649,15 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // the tile kernel addresses a wave's rows with 31-bit offsets; column
     // strides travel as 32-bit kernel arguments
-    if (!geo.bpl && (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31)) return Q4K_EUNSUPPORTED;
+    if (geo.mfma ? (int64_t)(geo.rows_base + 1) * kMfmaRows * nb01 >= ((int64_t)1 << 31)
+                 : !geo.bpl && (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31))
+        return Q4K_EUNSUPPORTED;
     if (ldx > INT32_MAX || stride_col_y > INT32_MAX) return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
         if (!geo.bpl) {
-            g2.lds = tile_lds_bytes((int)ne00, nc, geo.waves);
+            g2.lds = geo.mfma ? mfma_lds_bytes((int)ne00, nc, geo.waves) : tile_lds_bytes((int)ne00, nc, geo.waves);
             if (g2.lds_launch < g2.lds) g2.lds_launch = g2.lds;
         }
         GemvParams p{};
@@ -1014,7 +1095,7 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
 int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32_t workgroups,
                               int32_t kernel) {
     if (rows_per_tile < 0 || waves_per_wg < 0 || workgroups < 0) return Q4K_EINVAL;
-    if (kernel < 0 || kernel > 3) return Q4K_EINVAL;
+    if (kernel < 0 || kernel > 4) return Q4K_EINVAL;
     if (rows_per_tile != 0 && rows_per_tile != 1 && rows_per_tile != 2 && rows_per_tile != 4)
         return Q4K_EINVAL;
     if (waves_per_wg < 0 || waves_per_wg > 16) return Q4K_EINVAL;
@@ -1046,7 +1127,7 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) 
     out[3] = g.lds_launch;
     out[4] = g.nc_chunk;
     out[5] = g.nc_chunk >= ne11 ? 1 : 0;
-    out[6] = g.bpl == 2 ? 3 : (g.bpl ? 2 : 1);
+    out[6] = g.mfma ? 4 : (g.bpl == 2 ? 3 : (g.bpl ? 2 : 1));
     out[7] = g.bpl ? g.rpw : g.R;
     return Q4K_OK;
 }

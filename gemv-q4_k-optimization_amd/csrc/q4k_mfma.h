@@ -1,0 +1,361 @@
+// q4k_mfma.h -- the Q4_K GEMV for several activation columns on the matrix
+// cores: v_mfma_i32_16x16x64_i8 forms the int32 sub-block sums of a tile of
+// 16 weight rows against up to 8 columns, the VALU only unpacks nibbles and
+// applies the per-(row, column, sub-block) scales.
+//
+// Operands of one MFMA (chunk jj of super-block kb: qs bytes [32jj, 32jj+32)
+// of each row, i.e. sub-blocks 2jj (low nibbles) and 2jj+1 (high nibbles)).
+// The instruction's 64 k-slots are lane group g = lane/16, byte t; A row i
+// and B column j of lane l are l % 16, and D element v of lane l is
+// D[4(l/16) + v][l % 16] (checked on the device).  Here
+//   k-slots   g = 0, 1: sub-block 2jj, values 16g + t; g = 2, 3: sub-block
+//             2jj+1, values 16(g-2) + t;
+//   A row i   activation column i % 8 for sub-block 2jj (i < 8) or 2jj+1
+//             (i >= 8): its q8 in the slots of its own sub-block, zeros in
+//             the other two lane groups (read from a zero area of LDS);
+//   B col r   weight row r of the tile: the nibbles of its 32 qs bytes;
+//   D         D[i][r] = the int32 sum S_qq of row r, column i % 8, sub-block
+//             2jj + i/8: every output is one the product needs.
+// So lane l ends up with one weight row (l % 16), one sub-block parity
+// (l / 32) and four columns (4((l/16) & 1) + v): the row's scale and min
+// are unpacked once per lane and used for four columns.
+//
+// Work split: tiles of 16 rows, split evenly over the workgroups (one per
+// CU, 8 waves).  The waves of a workgroup form 8/KS groups of KS waves; in
+// each round every group takes one tile and its KS waves take equal shares
+// of the tile's super-blocks.  At the end of a round each wave leaves its
+// partial results in LDS and, after a barrier, the workgroup combines the KS
+// partials of each tile and writes the outputs.
+//
+// Summation order: a row's super-blocks form S = min(8, 2^floor(log2 nb))
+// segments [s nb/S, (s+1) nb/S), each summed in order; the segment sums are
+// combined in a fixed balanced binary tree.  A wave owns an aligned run of
+// S/KS segments and forms that subtree itself; the reduction completes the
+// tree across the KS waves.  So the result depends on K alone -- not on the
+// number of rows, the tiles per workgroup or KS -- and row slices of a
+// product reproduce it bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "q4k_tile.h"
+
+namespace q4k {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaRows = 16;   // weight rows per tile
+constexpr int kMfmaCols = 8;    // activation columns of one MFMA (padded)
+constexpr int kMfmaMaxSegs = 8; // summation segments of a row, at most
+constexpr int kMfmaZeroBytes = 512;
+// per-wave partial results of a round: 32 lanes x 4 columns, two buffers
+__host__ __device__ constexpr int mfma_part_bytes(int waves) { return 2 * waves * 32 * 16; }
+
+// LDS layout (bytes from the start): NC q8 columns of qcol = K + 16 bytes
+// (the 16-byte skew puts the eight columns' reads of one lane octet in
+// different banks), then the (d8, d8*sum q8) pairs of every 32-value block
+// for 8 columns ([block][column], float2), the zero area, the partials.
+__host__ __device__ constexpr int mfma_qcol(int K) { return K + 16; }
+__host__ __device__ constexpr int mfma_dk_off(int K, int nc) { return nc * mfma_qcol(K); }
+__host__ __device__ constexpr int mfma_zero_off(int K, int nc) { return mfma_dk_off(K, nc) + (K / 32) * kMfmaCols * 8; }
+__host__ __device__ constexpr int mfma_part_off(int K, int nc) { return mfma_zero_off(K, nc) + kMfmaZeroBytes; }
+__host__ __device__ constexpr int mfma_lds_bytes(int K, int nc, int waves) {
+    return mfma_part_off(K, nc) + mfma_part_bytes(waves);
+}
+
+// One super-block's weights in a lane's registers: the header of row
+// l % 16 and the 16 qs bytes of each chunk jj the lane's lane group reads.
+struct MfmaRegs {
+    u32x4 h;
+    u32x4 q[4];
+};
+
+// Per-lane constants.
+struct MfmaLane {
+    int lane;
+    int wrow;         // weight row in the tile (B column, D column)
+    int half;         // which 16 bytes of a chunk the lane loads (lane group & 1)
+    uint32_t nshift;  // 0: low nibbles (lane groups 0, 1), 4: high nibbles
+    int hid;          // D: sub-block parity of the lane's outputs (lane / 32)
+    int c0;           // D: first of the lane's four columns
+    int a_off;        // LDS byte offset of the lane's A operand for super-block 0
+    int a_inc;        // per super-block: 256 (data lanes) or 0 (zero lanes)
+    int dk_off;       // LDS byte offset of its (d8, d8*sum) pairs for super-block 0
+    uint32_t selx, sely;  // byte selectors of its scales (sub-blocks hid, 2+hid, ...)
+};
+
+template <int NC>
+__device__ __forceinline__ MfmaLane mfma_lane(int K) {
+    MfmaLane m;
+    const int l = threadIdx.x & (kWave - 1);
+    const int g = l >> 4;
+    m.lane = l;
+    m.wrow = l & 15;
+    m.half = g & 1;
+    m.nshift = (uint32_t)(g >> 1) * 4u;
+    m.hid = l >> 5;
+    m.c0 = 4 * (g & 1);
+    // A: row i = l % 16 -> column i % 8, sub-block parity i / 8; it holds
+    // data in the lane groups of its own sub-block, zeros elsewhere
+    const int ca = l & 7, hia = (l >> 3) & 1;
+    const bool data = (g >> 1) == hia && ca < NC;
+    m.a_off = data ? ca * mfma_qcol(K) + 32 * hia + 16 * (g & 1) : mfma_zero_off(K, NC) + 16 * (l & 7);
+    m.a_inc = data ? kQK : 0;
+    m.dk_off = mfma_dk_off(K, NC) + (m.hid * kMfmaCols + m.c0) * 8;
+    const uint32_t h = (uint32_t)m.hid;
+    m.selx = h | ((h + 2u) << 8) | ((h + 4u) << 16) | ((h + 6u) << 24);
+    m.sely = h | ((h + 2u) << 8) | (h << 16) | ((h + 2u) << 24);
+    return m;
+}
+
+// Loads one item: a super-block of the lane's row from byte offset off of
+// the workgroup's buffer, or zeros when off is kOOB.
+__device__ __forceinline__ void mfma_load(__amdgpu_buffer_rsrc_t rs, uint32_t off, const MfmaLane &ln,
+                                          MfmaRegs &w) {
+    w.h = load16(rs, off);
+    const uint32_t oq = off + 16u + 16u * (uint32_t)ln.half;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) w.q[jj] = load16(rs, oq + 32u * jj);
+}
+
+// The lane's (sc, m) of sub-blocks hid + 2jj, jj = 0..3: low = {sc(hid),
+// sc(2+hid), m(hid), m(2+hid)}, split = the same for 4+hid, 6+hid (the
+// 4+2-bit fields of get_scale_min_k4).
+__device__ __forceinline__ void mfma_scales(u32x4 h, const MfmaLane &ln, uint32_t &low, uint32_t &split) {
+    const uint32_t x = __builtin_amdgcn_perm(h[2], h[1], ln.selx);
+    const uint32_t y = __builtin_amdgcn_perm(h[3], h[3], ln.sely);
+    low = x & 0x3f3f3f3fu;
+    split = (y & 0x00000f0fu) | ((y >> 4) & 0x0f0f0000u) | ((x >> 2) & 0x30303030u);
+}
+
+// One item: four MFMAs and the scaling of their outputs into acc (the
+// lane's row, four columns).  SUMS: also stores the int32 sums.
+template <int NC, bool SUMS>
+__device__ __forceinline__ void mfma_item(const GemvParams &p, const MfmaLane &ln, const uint8_t *lds, int kb,
+                                          const MfmaRegs &w, float (&acc)[4], int row, bool row_ok) {
+    const uint8_t *pa = lds + ln.a_off + ln.a_inc * kb;
+    const uint8_t *pk = lds + ln.dk_off + kb * (8 * kMfmaCols * 8);
+    // the four products first (independent), then their scaling
+    i32x4 s[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+        const u32x4 av = *reinterpret_cast<const u32x4 *>(pa + 64 * jj);
+        u32x4 bv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = (w.q[jj][e] >> ln.nshift) & 0x0f0f0f0fu;
+        s[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, av), __builtin_bit_cast(i32x4, bv),
+                                                      i32x4{0, 0, 0, 0}, 0, 0, 0);
+    }
+    uint32_t low, split;
+    mfma_scales(w.h, ln, low, split);
+    const float d = half_bits_to_float(w.h[0]), dmin = half_bits_to_float(w.h[0] >> 16);
+    float t[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+        // (d8, d8*sum q8) of the lane's four columns, sub-block 2jj + hid
+        const float4 k01 = *reinterpret_cast<const float4 *>(pk + 2 * kMfmaCols * 8 * jj);
+        const float4 k23 = *reinterpret_cast<const float4 *>(pk + 2 * kMfmaCols * 8 * jj + 16);
+        const uint32_t scm = jj < 2 ? low : split;
+        const int sc = (int)((scm >> (8 * (jj & 1))) & 0xffu);
+        const float mf = (float)((scm >> (16 + 8 * (jj & 1))) & 0xffu);
+        const float d8[4] = {k01.x, k01.z, k23.x, k23.z};
+        const float km[4] = {k01.y, k01.w, k23.y, k23.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            // |s| <= 32*15*127 and sc <= 63: the 24-bit product is exact in f32
+            t[v] = __builtin_fmaf(d8[v], (float)__mul24(s[jj][v], sc), t[v]);
+            u[v] = __builtin_fmaf(km[v], mf, u[v]);
+        }
+        if constexpr (SUMS) {
+            if (row_ok) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (ln.c0 + v < NC)
+                        p.sums[((int64_t)(ln.c0 + v) * p.M + row) * (p.K / 32) + kb * 8 + 2 * jj + ln.hid] = s[jj][v];
+            }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        acc[v] = __builtin_fmaf(d, t[v], acc[v]);
+        acc[v] = __builtin_fmaf(-dmin, u[v], acc[v]);
+    }
+}
+
+// Adds segment value v (the sum of one segment, local index t in the wave's
+// run) into the wave's subtree: l1, l2, l4 hold the pending left subtrees of
+// 1, 2 and 4 segments; returns the subtree that ends at t.
+__device__ __forceinline__ void mfma_tree_push(int t, float (&v)[4], float (&l1)[4], float (&l2)[4],
+                                               float (&l4)[4]) {
+    if (t & 1) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = l1[k] + v[k];
+        if (t & 2) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = l2[k] + v[k];
+            if (t & 4) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[k] = l4[k] + v[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) l4[k] = v[k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) l2[k] = v[k];
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) l1[k] = v[k];
+    }
+}
+
+// A wave's position in its items: round r (tile group + ngroups * r) and
+// super-block kb of the tile.
+struct MfmaPos {
+    int r, kb;
+};
+
+// The kernel.  rows_base / rows_extra are the tile split: each workgroup
+// owns rows_base tiles of 16 rows, the first rows_extra one more;
+// p.rpw: KS, the waves that share one tile (1, 2, 4 or 8, at most S);
+// p.ntiles: S, the segments of a row.
+template <int NC, int WAVES, bool SUMS = false>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    static_assert(NC >= 1 && NC <= kMfmaCols, "up to 8 columns");
+    static_assert(WAVES == 8 || WAVES == 16, "8 or 16 waves");
+    constexpr int NT = kWave * WAVES;
+    int32_t *const sq_out = SUMS ? p.sq : nullptr;
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    int8_t *q8s = reinterpret_cast<int8_t *>(lds);
+    float2 *dks = reinterpret_cast<float2 *>(lds + mfma_dk_off(p.K, NC));
+
+    const MfmaLane ln = mfma_lane<NC>(p.K);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int KS = p.rpw, S = p.ntiles;
+    const int group = wave / KS, ks = wave - group * KS;
+    const int ngroups = WAVES / KS;
+    const int segs = S / KS, seg0 = ks * segs;  // the wave's run of segments
+    // this workgroup's tiles and this wave's super-blocks of each
+    const int b = (int)blockIdx.x;
+    const int t0 = b * p.rows_base + min(b, p.rows_extra);
+    const int nt = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int rounds = (nt + ngroups - 1) / ngroups;
+    const int kb0 = seg0 * p.nb / S, kb1 = (seg0 + segs) * p.nb / S;  // kb1 > kb0 (S <= nb)
+    const int items = rounds * (kb1 - kb0);
+    const int row0 = t0 * kMfmaRows;
+    const int nrows = min(nt * kMfmaRows, p.M - row0);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(p.w + (int64_t)row0 * p.row_stride, nrows > 0 ? (uint32_t)(nrows * p.row_stride) : 0u);
+
+    constexpr int kLPB = stage_lpb(NC);
+    constexpr int kPreR = pre_rounds(NC, NT);
+    ActStage<kLPB, kPreR> xs;
+    Q81Stage<kPreR> ys;
+    if (p.x) stage_f32_issue<kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+    else stage_q81_issue<NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+    __syncthreads();  // all activation loads of this CU are queued first
+
+    // items in order: rounds, and super-blocks kb0..kb1-1 of each; loads of
+    // positions past the wave's last round or the workgroup's tiles read zeros
+    auto next = [&](MfmaPos q) -> MfmaPos { return q.kb + 1 < kb1 ? MfmaPos{q.r, q.kb + 1} : MfmaPos{q.r + 1, kb0}; };
+    auto item_off = [&](MfmaPos q) -> uint32_t {
+        const int tile = group + ngroups * q.r;
+        if (q.r >= rounds || tile >= nt) return kOOB;
+        return (uint32_t)((tile * kMfmaRows + ln.wrow) * p.row_stride) + (uint32_t)q.kb * kBlockBytes;
+    };
+    MfmaPos cur{0, kb0};
+    MfmaPos ahead = next(cur);
+    MfmaRegs w[2];
+    mfma_load(rs, item_off(cur), ln, w[0]);
+    mfma_load(rs, item_off(ahead), ln, w[1]);
+    ahead = next(ahead);
+
+    if (p.x)
+        stage_f32_finish<kLayoutMfma, kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, mfma_qcol(p.K),
+                                                q8s, dks, sq_out);
+    else
+        stage_q81_finish<kLayoutMfma, NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, mfma_qcol(p.K), q8s, dks,
+                                          sq_out);
+    // the zero area of the A operand, and the pairs of the padding columns
+    // (their outputs are dropped; zeros keep them finite)
+    if (threadIdx.x < kMfmaZeroBytes / 16)
+        reinterpret_cast<u32x4 *>(lds + mfma_zero_off(p.K, NC))[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (NC < kMfmaCols) {
+        for (int q = (int)threadIdx.x; q < (p.K / 32) * (kMfmaCols - NC); q += NT) {
+            const int blk = q / (kMfmaCols - NC), c = NC + q - blk * (kMfmaCols - NC);
+            dks[blk * kMfmaCols + c] = make_float2(0.0f, 0.0f);
+        }
+    }
+    __syncthreads();
+
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float l1[4] = {0.0f, 0.0f, 0.0f, 0.0f}, l2[4] = {0.0f, 0.0f, 0.0f, 0.0f}, l4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float *part = reinterpret_cast<float *>(lds + mfma_part_off(p.K, NC));
+    int t = 0;                            // local segment of the current item
+    int seg_end = (seg0 + 1) * p.nb / S;  // its end (super-block)
+    // items go two at a time (slot k holds item it); an odd count ends with
+    // one item past the wave's, whose zeros add nothing
+    for (int it = 0; it < items;) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k, ++it) {
+            const int tile = group + ngroups * cur.r;
+            const int row = row0 + tile * kMfmaRows + ln.wrow;
+            mfma_item<NC, SUMS>(p, ln, lds, cur.kb, w[k], acc, row, SUMS && it < items && tile < nt && row < p.M);
+            mfma_load(rs, item_off(ahead), ln, w[k]);
+            ahead = next(ahead);
+            const MfmaPos done = cur;
+            cur = next(cur);
+            if (it < items && done.kb + 1 == seg_end) {
+                // segment end: its value is the sum of the two sub-block
+                // parities of each (row, column), in lanes l and l + 32
+                float v[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float hi = acc[c];
+                    permlane32_swap(acc[c], hi);
+                    v[c] = acc[c] + hi;
+                    acc[c] = 0.0f;
+                }
+                mfma_tree_push(t, v, l1, l2, l4);
+                ++t;
+                if (t < segs) {
+                    seg_end = (seg0 + t + 1) * p.nb / S;
+                    continue;
+                }
+                // round end: v is the wave's subtree of the tile
+                t = 0;
+                seg_end = (seg0 + 1) * p.nb / S;
+                const int buf = done.r & 1;
+                if (ln.lane < 32)
+                    *reinterpret_cast<float4 *>(part + ((buf * WAVES + wave) * 32 + ln.lane) * 4) =
+                        make_float4(v[0], v[1], v[2], v[3]);
+                __syncthreads();
+                // outputs of this round: tile group q, column c, row rr;
+                // consecutive threads write consecutive rows of a column.
+                // The KS subtrees combine in the same balanced tree.
+                for (int o = (int)threadIdx.x; o < ngroups * kMfmaRows * kMfmaCols; o += NT) {
+                    const int rr = o & 15, c = (o >> 4) & 7, q = o >> 7;
+                    const int otile = q + ngroups * done.r;
+                    const int orow = row0 + otile * kMfmaRows + rr;
+                    if (c < NC && otile < nt && orow < p.M) {
+                        const int l32 = rr + 16 * (c >> 2);
+                        const float *src = part + ((buf * WAVES + q * KS) * 32 + l32) * 4 + (c & 3);
+                        float pv[kMfmaMaxSegs];
+#pragma unroll
+                        for (int j = 0; j < kMfmaMaxSegs; ++j) pv[j] = j < KS ? src[j * 32 * 4] : 0.0f;
+#pragma unroll
+                        for (int wdt = 1; wdt < kMfmaMaxSegs; wdt *= 2)
+#pragma unroll
+                            for (int j = 0; j + wdt < kMfmaMaxSegs; j += 2 * wdt)
+                                if (j + wdt < KS) pv[j] = pv[j] + pv[j + wdt];
+                        p.dst[(int64_t)c * p.ld_dst + orow] = pv[0];
+                    }
+                }
+            }
+        }
+    }
+}
+
+}  // namespace q4k

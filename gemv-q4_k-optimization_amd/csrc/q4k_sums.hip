@@ -3,11 +3,13 @@
 // sub-block sums and the staging's int32 activation sums.  Instantiated in a
 // translation unit of their own for the launch shapes the automatic
 // geometry picks for plain products (one row per tile, 8 or 16 waves, 1 or 2
-// slots, prologue 0, 1 or 3; the block-per-lane kernel at 4 or 8 waves);
-// q4k_gemv.hip launches them with the product's own geometry.
+// slots, prologue 0, 1 or 3; the block-per-lane kernel at 4 or 8 waves; the
+// matrix-core kernel for 1..8 columns); q4k_gemv.hip launches them with the
+// product's own geometry.
 #include <hip/hip_runtime.h>
 
 #include "q4k_gemv_kernels.h"
+#include "q4k_mfma.h"
 #include "q4k_runtime.h"
 
 namespace q4k {
@@ -45,6 +47,25 @@ const void *q4k_sums_kernel(int nc, int waves, int pro, int slots) {
     if (slots != 1 && slots != 2) return nullptr;
     if (waves <= 8) return slots == 1 ? tile_sums_nc<8, 1>(nc, pro) : tile_sums_nc<8, 2>(nc, pro);
     return slots == 1 ? tile_sums_nc<16, 1>(nc, pro) : tile_sums_nc<16, 2>(nc, pro);
+}
+
+template <int WAVES>
+static const void *mfma_sums_nc(int nc) {
+    switch (nc) {
+        case 1: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<1, WAVES, true>);
+        case 2: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<2, WAVES, true>);
+        case 3: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<3, WAVES, true>);
+        case 4: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<4, WAVES, true>);
+        case 5: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<5, WAVES, true>);
+        case 6: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<6, WAVES, true>);
+        case 7: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<7, WAVES, true>);
+        case 8: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<8, WAVES, true>);
+        default: return nullptr;
+    }
+}
+
+const void *q4k_mfma_sums_kernel(int nc, int waves) {
+    return waves > 8 ? mfma_sums_nc<16>(nc) : mfma_sums_nc<8>(nc);
 }
 
 const void *q4k_bpl_sums_kernel(int waves) {

@@ -298,7 +298,8 @@ int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * out[0] rows per wave tile (tile kernel), out[1] waves per workgroup,
  * out[2] workgroups, out[3] LDS bytes requested per workgroup, out[4] columns per
  * launch, out[5] 1 when the activation is quantised inside the GEMV launch,
- * out[6] kernel (1 tile, 2 block-per-lane, 3 coalesced block kernel),
+ * out[6] kernel (1 tile, 2 block-per-lane, 3 coalesced block kernel, 4
+ *        matrix-core kernel: tiles of 16 rows on v_mfma_i32_16x16x64_i8),
  * out[7] rows per wave step. */
 int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
 
@@ -307,7 +308,8 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * workgroup (tile kernel: 1..8 selects the 8-wave, 9..16 the 16-wave
  * variant; reduced to 8 where 16 would not fit the registers), the number
  * of workgroups and the kernel (1 tile kernel, 2 block-per-lane, 3
- * coalesced block kernel where they apply); 0 restores the automatic
+ * coalesced block kernel where they apply, 4 matrix-core kernel for
+ * products without an epilogue); 0 restores the automatic
  * choice.  Nothing is read from the environment: until this is called the
  * geometry is automatic.  Not part of the reference interface: a
  * benchmarking knob (ggml's counterpart is editing the compile-time tables

@@ -523,15 +523,16 @@ def test_production_kernel_sums(Q, O, gpu, M, K, N):
 
 def test_parity_variants_cover_every_kernel(Q, gpu):
     """The workloads' launches, whose sums test_production_kernel_sums
-    checks, include the block-per-lane kernel, the 8-wave register path
-    for several columns, 16-wave and 8-wave tile launches and both staging
-    routes."""
+    checks, include the block-per-lane kernel, the matrix-core kernel
+    (128256 x 4096, eight columns), the 8-wave register path for several
+    columns, 16-wave and 8-wave tile launches and both staging routes."""
     kinds = set()
     for p in _cases():
         M, K, N = p.values
         g = Q.geometry(K, M, N)
         kinds.add((g["kernel"], g["waves_per_wg"] if g["kernel"] == 1 else 0, N >= 3 and K <= 4096))
     assert (2, 0, False) in kinds                      # block-per-lane (128256 x 4096, one column)
+    assert (4, 0, True) in kinds                       # matrix cores (128256 x 4096, eight columns)
     assert (1, 8, True) in kinds and (1, 16, True) in kinds   # several columns, 8 and 16 waves
     assert (1, 16, False) in kinds                     # the headline shape
 
