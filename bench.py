@@ -359,6 +359,7 @@ def cpu_baseline(wq, x, target_s=12.0, min_reps=10):
             "us_per_call": round(med * 1e6, 1), "us_per_call_without_q8K": round(med_nq * 1e6, 1),
             "GBps_without_q8K": round(nbytes / med_nq / 1e9, 2), "cpu_model": model, "isa": isa,
             "host_cpus": os.cpu_count(), "pinned_cpus": f"{cpus[0]}..{cpus[-1]}" if cpus else "",
+            "label": "ggml-equivalent restatement (ggml itself is not available offline)",
             "sample": f"{reps} calls of the full {M}x{K} N={N} product with Q8_K quantisation of x "
                       f"({tot:.1f} s) and {reps_nq} without ({tot_nq:.1f} s): vec_dot_q4_K_q8_K ({isa}), "
                       f"{cores} threads pinned one per CPU (the job's CPU share of this {os.cpu_count()}-CPU "
@@ -387,7 +388,8 @@ def headline(args):
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": sec * 1e3,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "q4_K x q8_1: int8 dot4 -> int32, f32 scale/accumulate",
-        "data": "synthetic: W ~ N(0,0.02) -> Q4_K (quantize_row_q4_K_ref arithmetic), x ~ N(0,1); seed 0",
+        "data": "synthetic: W ~ N(0,0.02) -> Q4_K (quantize_row_q4_K_ref arithmetic), x ~ N(0,1); "
+                "seed 0, numpy PCG64 streams (0, 1) for W and (0, 2) for x",
         "config": {"workload": "mistral7b_ffn_gate_14336x4096_b1", "M": M, "K": K, "ncols": N,
                    "launch": f"hipGraph of the K timed calls, median of {t['trials']} timed replays",
                    "weight_copies": runner.ncopies, "geometry": Q.geometry(K, M, N)},
