@@ -226,14 +226,15 @@ static int tile_lds_bytes(int K, int nc, int waves) { return lds_bytes(K, nc) + 
 static int lds_bytes_linear(int K) { return K + K / 4; }
 
 // Products that run on the matrix-core kernel when no override says
-// otherwise: eight columns of 4096 or more row tiles.  Measured on MI355X
-// against the tile kernel (interleaved, one process): 128256 x 4096 N=8
-// 79.7 against 83.0 us, 14336 x 4096 N=8 even (15.64 against 15.65); slower
-// on every other shape of 2-8 columns, by 10-100 % (4096 x 4096, 1024 x
-// 4096, 4096 x 14336, 28672 x 8192).  Its VALU work is a third lower, but
-// each of its loads reads 144 bytes from each of 16 rows: at 3.7 TB/s that
-// access pattern, not the arithmetic, bounds it.
-static bool use_mfma(int64_t M, int64_t N) { return N == 8 && (M + kMfmaRows - 1) / kMfmaRows >= 4096; }
+// otherwise: eight columns of 896 or more row tiles (14336 rows) whose
+// columns fit one launch.  Measured on MI355X against the tile kernel
+// (interleaved, one process): 128256 x 4096 N=8 64.6 against 84.3 us,
+// 28672 x 4096 N=8 21.2 against 22.9, 14336 x 4096 N=8 14.1 against 15.7;
+// slower with fewer rows (4096 x 4096 N=8 9.4 against 8.5), fewer columns
+// (14336 x 4096 N=6 13.5 against 13.3, N=4 12.3 against 10.5: padded
+// columns cost scaling work) or longer rows (4096 x 14336 N=8: the columns
+// need two launches).
+static bool use_mfma(int64_t M, int64_t N) { return N == 8 && (M + kMfmaRows - 1) / kMfmaRows >= 896; }
 
 // The matrix-core kernel: one workgroup per CU (at most one per tile) of 8
 // or 16 waves, the tiles of 16 rows split evenly over the workgroups, and as
@@ -331,7 +332,8 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     if (!fused && mats == 1 && (okern == 4 || (okern == 0 && use_mfma(M, N)))) {
         int mc = (int)N;
         while (mc > 1 && mfma_lds_bytes((int)K, mc, 16) > max_lds) mc = (mc + 1) / 2;
-        if (mfma_lds_bytes((int)K, mc, 16) <= max_lds) return pick_geometry_mfma(di, K, M, mc, owgs, owaves);
+        if (mfma_lds_bytes((int)K, mc, 16) <= max_lds && (okern == 4 || mc == N))
+            return pick_geometry_mfma(di, K, M, mc, owgs, owaves);
     }
     g.grid = owgs > 0 ? owgs : grid_per_matrix(cus, mats, M);
     // One column with rows of at most 8192 values and ~500 KB or more of

@@ -21,7 +21,7 @@
 // are unpacked once per lane and used for four columns.
 //
 // Work split: tiles of 16 rows, split evenly over the workgroups (one per
-// CU, 8 waves).  The waves of a workgroup form 8/KS groups of KS waves; in
+// CU, 8 or 16 waves).  The waves of a workgroup form 8/KS groups of KS waves; in
 // each round every group takes one tile and its KS waves take equal shares
 // of the tile's super-blocks.  At the end of a round each wave leaves its
 // partial results in LDS and, after a barrier, the workgroup combines the KS
@@ -54,20 +54,39 @@ __host__ __device__ constexpr int mfma_part_bytes(int waves) { return 2 * waves 
 // LDS layout (bytes from the start): NC q8 columns of qcol = K + 16 bytes
 // (the 16-byte skew puts the eight columns' reads of one lane octet in
 // different banks), then the (d8, d8*sum q8) pairs of every 32-value block
-// for 8 columns ([block][column], float2), the zero area, the partials.
+// for 8 columns ([block][column], float2), the zero area, the partials and
+// one weight slot per wave.
 __host__ __device__ constexpr int mfma_qcol(int K) { return K + 16; }
 __host__ __device__ constexpr int mfma_dk_off(int K, int nc) { return nc * mfma_qcol(K); }
 __host__ __device__ constexpr int mfma_zero_off(int K, int nc) { return mfma_dk_off(K, nc) + (K / 32) * kMfmaCols * 8; }
 __host__ __device__ constexpr int mfma_part_off(int K, int nc) { return mfma_zero_off(K, nc) + kMfmaZeroBytes; }
-__host__ __device__ constexpr int mfma_lds_bytes(int K, int nc, int waves) {
+// Weight staging: an item (16 rows x one super-block, 2304 bytes) arrives
+// with three contiguous 64-lane x 16-byte loads (chunk c = lane + 64i is
+// bytes [16 (c % 9), +16) of row c / 9; loads that each touch one or two
+// rows stream as fast as the tile kernel's, where loads touching all 16 rows
+// reached half that), goes to the wave's LDS slot at a row pitch of 160
+// bytes (the skew spreads the rows' reads over the banks) and the MFMA
+// operands are read from there.
+constexpr int kMfmaSlotPitch = kBlockBytes + 16;
+constexpr int kMfmaSlotBytes = kMfmaRows * kMfmaSlotPitch;
+constexpr int kMfmaChunks = kMfmaRows * kBlockBytes / 16;  // 144
+__host__ __device__ constexpr int mfma_slot_off(int K, int nc, int waves) {
     return mfma_part_off(K, nc) + mfma_part_bytes(waves);
 }
+__host__ __device__ constexpr int mfma_lds_bytes(int K, int nc, int waves) {
+    return mfma_slot_off(K, nc, waves) + waves * kMfmaSlotBytes;
+}
 
-// One super-block's weights in a lane's registers: the header of row
+// One super-block's weights as the MFMA lane needs them: the header of row
 // l % 16 and the 16 qs bytes of each chunk jj the lane's lane group reads.
 struct MfmaRegs {
     u32x4 h;
     u32x4 q[4];
+};
+
+// One item in flight: the lane's three 16-byte chunks of the contiguous loads.
+struct MfmaLoad {
+    u32x4 v[3];
 };
 
 // Per-lane constants.
@@ -82,6 +101,8 @@ struct MfmaLane {
     int a_inc;        // per super-block: 256 (data lanes) or 0 (zero lanes)
     int dk_off;       // LDS byte offset of its (d8, d8*sum) pairs for super-block 0
     uint32_t selx, sely;  // byte selectors of its scales (sub-blocks hid, 2+hid, ...)
+    uint32_t g_off[3];    // its chunks of an item: byte offsets from the item's first row
+    int s_off[3];         // and in the wave's slot
 };
 
 template <int NC>
@@ -108,14 +129,42 @@ __device__ __forceinline__ MfmaLane mfma_lane(int K) {
     return m;
 }
 
-// Loads one item: a super-block of the lane's row from byte offset off of
-// the workgroup's buffer, or zeros when off is kOOB.
-__device__ __forceinline__ void mfma_load(__amdgpu_buffer_rsrc_t rs, uint32_t off, const MfmaLane &ln,
-                                          MfmaRegs &w) {
-    w.h = load16(rs, off);
-    const uint32_t oq = off + 16u + 16u * (uint32_t)ln.half;
+// The lane's chunk offsets of an item (rows row_stride bytes apart); chunks
+// past the item's 144 get no offset (their loads read zeros, nothing is
+// written).
+__device__ __forceinline__ void mfma_chunks(MfmaLane &m, int64_t row_stride) {
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) w.q[jj] = load16(rs, oq + 32u * jj);
+    for (int i = 0; i < 3; ++i) {
+        const int c = m.lane + 64 * i, r = c / 9, o = c - 9 * (c / 9);
+        m.g_off[i] = c < kMfmaChunks ? (uint32_t)(r * row_stride) + 16u * (uint32_t)o : kOOB;
+        m.s_off[i] = r * kMfmaSlotPitch + 16 * o;
+    }
+}
+
+// Loads one item: one super-block of 16 rows whose first row's block
+// starts at byte offset off of the workgroup's buffer, or zeros when off is
+// kOOB.
+__device__ __forceinline__ void mfma_load(__amdgpu_buffer_rsrc_t rs, uint32_t off, const MfmaLane &ln,
+                                          MfmaLoad &w) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) w.v[i] = load16(rs, off == kOOB || ln.g_off[i] == kOOB ? kOOB : off + ln.g_off[i]);
+}
+
+// Writes an item to the wave's slot and reads the lane's operands back.
+// The lanes read bytes other lanes wrote: the wait and the compiler barrier
+// keep the reads behind the writes.
+__device__ __forceinline__ MfmaRegs mfma_stage(uint8_t *slot, const MfmaLane &ln, const MfmaLoad &w) {
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        if (i < 2 || ln.lane + 128 < kMfmaChunks) *reinterpret_cast<u32x4 *>(slot + ln.s_off[i]) = w.v[i];
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    MfmaRegs r;
+    const uint8_t *row = slot + ln.wrow * kMfmaSlotPitch;
+    r.h = *reinterpret_cast<const u32x4 *>(row);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) r.q[jj] = *reinterpret_cast<const u32x4 *>(row + 16 + 16 * ln.half + 32 * jj);
+    return r;
 }
 
 // The lane's (sc, m) of sub-blocks hid + 2jj, jj = 0..3: low = {sc(hid),
@@ -231,7 +280,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float2 *dks = reinterpret_cast<float2 *>(lds + mfma_dk_off(p.K, NC));
 
-    const MfmaLane ln = mfma_lane<NC>(p.K);
+    MfmaLane ln = mfma_lane<NC>(p.K);
+    mfma_chunks(ln, p.row_stride);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int KS = p.rpw, S = p.ntiles;
     const int group = wave / KS, ks = wave - group * KS;
@@ -263,11 +313,11 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
     auto item_off = [&](MfmaPos q) -> uint32_t {
         const int tile = group + ngroups * q.r;
         if (q.r >= rounds || tile >= nt) return kOOB;
-        return (uint32_t)((tile * kMfmaRows + ln.wrow) * p.row_stride) + (uint32_t)q.kb * kBlockBytes;
+        return (uint32_t)(tile * kMfmaRows * p.row_stride) + (uint32_t)q.kb * kBlockBytes;
     };
     MfmaPos cur{0, kb0};
     MfmaPos ahead = next(cur);
-    MfmaRegs w[2];
+    MfmaLoad w[2];
     mfma_load(rs, item_off(cur), ln, w[0]);
     mfma_load(rs, item_off(ahead), ln, w[1]);
     ahead = next(ahead);
@@ -293,6 +343,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float l1[4] = {0.0f, 0.0f, 0.0f, 0.0f}, l2[4] = {0.0f, 0.0f, 0.0f, 0.0f}, l4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float *part = reinterpret_cast<float *>(lds + mfma_part_off(p.K, NC));
+    uint8_t *slot = lds + mfma_slot_off(p.K, NC, WAVES) + wave * kMfmaSlotBytes;
     int t = 0;                            // local segment of the current item
     int seg_end = (seg0 + 1) * p.nb / S;  // its end (super-block)
     // items go two at a time (slot k holds item it); an odd count ends with
@@ -302,8 +353,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
         for (int k = 0; k < 2; ++k, ++it) {
             const int tile = group + ngroups * cur.r;
             const int row = row0 + tile * kMfmaRows + ln.wrow;
-            mfma_item<NC, SUMS>(p, ln, lds, cur.kb, w[k], acc, row, SUMS && it < items && tile < nt && row < p.M);
+            const MfmaRegs wr = mfma_stage(slot, ln, w[k]);
             mfma_load(rs, item_off(ahead), ln, w[k]);
+            mfma_item<NC, SUMS>(p, ln, lds, cur.kb, wr, acc, row, SUMS && it < items && tile < nt && row < p.M);
             ahead = next(ahead);
             const MfmaPos done = cur;
             cur = next(cur);

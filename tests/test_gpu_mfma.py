@@ -50,7 +50,7 @@ def test_mfma_kernel_against_oracle(Q, O, gpu, M, K, N):
     try:
         Q.set_geometry_override(kernel=4)
         geo = Q.geometry(K, M, N)
-        assert geo["kernel"] == 4 and geo["cols_per_launch"] == N, geo
+        assert geo["kernel"] == 4, geo
         y = Q.mul_mat_vec_q(wd, K, xd)
         _common.assert_within_tolerance(O, y.cpu().numpy()[:, rows], ref, f"mfma {M}x{K} N={N}")
         y_again = Q.mul_mat_vec_q(wd, K, xd)
