@@ -226,15 +226,20 @@ static int tile_lds_bytes(int K, int nc, int waves) { return lds_bytes(K, nc) + 
 static int lds_bytes_linear(int K) { return K + K / 4; }
 
 // Products that run on the matrix-core kernel when no override says
-// otherwise: eight columns of 896 or more row tiles (14336 rows) whose
-// columns fit one launch.  Measured on MI355X against the tile kernel
-// (interleaved, one process): 128256 x 4096 N=8 64.6 against 84.3 us,
-// 28672 x 4096 N=8 21.2 against 22.9, 14336 x 4096 N=8 14.1 against 15.7;
-// slower with fewer rows (4096 x 4096 N=8 9.4 against 8.5), fewer columns
-// (14336 x 4096 N=6 13.5 against 13.3, N=4 12.3 against 10.5: padded
-// columns cost scaling work) or longer rows (4096 x 14336 N=8: the columns
-// need two launches).
-static bool use_mfma(int64_t M, int64_t N) { return N == 8 && (M + kMfmaRows - 1) / kMfmaRows >= 896; }
+// otherwise: eight columns of 896 or more row tiles (14336 rows), or six to
+// eight of 4096 or more, whose columns fit one launch.  Measured on MI355X
+// against the tile kernel (interleaved, one process): 128256 x 4096 N=8
+// 64.5 against 83.4 us, N=6 63.6 against 73.2; 28672 x 4096 N=8 21.1
+// against 22.9; 14336 x 4096 N=8 14.1 against 15.7.  Slower with fewer
+// rows (4096 x 4096 N=8 10.2 against 8.6), fewer columns (14336 x 4096 N=6
+// 13.8 against 13.3; 128256 x 4096 N=4 62.7 against 57.6: padded columns
+// cost scaling work) or longer rows (4096 x 14336 N=8: the columns need two
+// launches).  Four items in flight per wave instead of two measured slower
+// on every shape.
+static bool use_mfma(int64_t M, int64_t N) {
+    const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
+    return (N == 8 && tiles >= 896) || (N >= 6 && tiles >= 4096);
+}
 
 // The matrix-core kernel: one workgroup per CU (at most one per tile) of 8
 // or 16 waves, the tiles of 16 rows split evenly over the workgroups, and as
