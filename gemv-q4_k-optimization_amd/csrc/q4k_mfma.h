@@ -64,10 +64,11 @@ __host__ __device__ constexpr int mfma_part_off(int K, int nc) { return mfma_zer
 // with three contiguous 64-lane x 16-byte loads (chunk c = lane + 64i is
 // bytes [16 (c % 9), +16) of row c / 9; loads that each touch one or two
 // rows stream as fast as the tile kernel's, where loads touching all 16 rows
-// reached half that), goes to the wave's LDS slot at a row pitch of 160
-// bytes (the skew spreads the rows' reads over the banks) and the MFMA
-// operands are read from there.
-constexpr int kMfmaSlotPitch = kBlockBytes + 16;
+// reached half that), goes to the wave's LDS slot as it lies in memory (row
+// pitch 144 bytes = 36 dwords: the 16-byte reads of 16 rows at one offset
+// fall in distinct banks, and the writes are one contiguous run) and the
+// MFMA operands are read from there.
+constexpr int kMfmaSlotPitch = kBlockBytes;
 constexpr int kMfmaSlotBytes = kMfmaRows * kMfmaSlotPitch;
 constexpr int kMfmaChunks = kMfmaRows * kBlockBytes / 16;  // 144
 __host__ __device__ constexpr int mfma_slot_off(int K, int nc, int waves) {
@@ -143,11 +144,14 @@ __device__ __forceinline__ void mfma_chunks(MfmaLane &m, int64_t row_stride) {
 
 // Loads one item: one super-block of 16 rows whose first row's block
 // starts at byte offset off of the workgroup's buffer, or zeros when off is
-// kOOB.
+// kOOB.  The sums need no selects: the buffer is under 2^31 bytes and off
+// under 2^31 or kOOB, so off + kOOB and kOOB + g_off (g_off < 2^31) fall
+// outside it and read zeros; kOOB + kOOB wraps to 0 and reads bytes, but
+// only for chunks past the item's 144, which are never written to the slot.
 __device__ __forceinline__ void mfma_load(__amdgpu_buffer_rsrc_t rs, uint32_t off, const MfmaLane &ln,
                                           MfmaLoad &w) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) w.v[i] = load16(rs, off == kOOB || ln.g_off[i] == kOOB ? kOOB : off + ln.g_off[i]);
+    for (int i = 0; i < 3; ++i) w.v[i] = load16(rs, off + ln.g_off[i]);
 }
 
 // Writes an item to the wave's slot and reads the lane's operands back.
