@@ -179,6 +179,9 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 //             matrix-core kernel; its auxiliary pairs are stored
 //             [block][column] for 8 columns, dk[8b + c], so a lane reads the
 //             pairs of four consecutive columns in two 16-byte reads.
+//   MFMA Q6   the MFMA layout with d8 alone as the auxiliary term, d8[8b + c]
+//             (the Q6_K matrix-core kernel folds the -32 offset into its
+//             weight bytes, so it needs no activation sums).
 //
 // Auxiliary terms for the linear and Q4K layouts: per 32-value block b of
 // column c, dk[c*K/32 + b] = (d8, d8 * sum of the block's q8) as a float2 --
@@ -195,6 +198,7 @@ constexpr int kLayoutQ4K = 1;
 constexpr int kLayoutQ6K = 2;
 constexpr int kLayoutQ6KDense = 3;
 constexpr int kLayoutMfma = 4;  // linear q8 columns; (d8, d8*sum) per [block][column] of 8 columns
+constexpr int kLayoutMfmaQ6 = 5;  // linear q8 columns; d8 per [block][column] of 8 columns
 
 constexpr bool is_q6_layout(int layout) { return layout == kLayoutQ6K || layout == kLayoutQ6KDense; }
 
@@ -208,7 +212,7 @@ __host__ __device__ constexpr int group_chunk_stride(int i, int nb) {
 // nb super-blocks).
 template <int LAYOUT>
 __device__ __forceinline__ int q8_offset(int c, int qcol, int nb, int b, int e) {
-    if (LAYOUT == kLayoutLinear || LAYOUT == kLayoutMfma) return c * qcol + b * 32 + e * 4;
+    if (LAYOUT == kLayoutLinear || LAYOUT == kLayoutMfma || LAYOUT == kLayoutMfmaQ6) return c * qcol + b * 32 + e * 4;
     const int kb = b >> 3, s = b & 7;
     if (LAYOUT == kLayoutQ4K)
         return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (e >> 2)) * 1024 + ((kb & 15) * 4 + (s >> 1)) * 16 +
@@ -237,6 +241,8 @@ __device__ __forceinline__ void store_aux(void *aux, int total, int nblk, int c,
         reinterpret_cast<int *>(aux)[q6_sq_index(total, nblk, c, b, half)] = -32 * hsum;
     } else if (LAYOUT == kLayoutMfma) {
         if (half == 0) reinterpret_cast<float2 *>(aux)[b * 8 + c] = make_float2(d8, d8 * (float)qsum);
+    } else if (LAYOUT == kLayoutMfmaQ6) {
+        if (half == 0) reinterpret_cast<float *>(aux)[b * 8 + c] = d8;
     } else if (half == 0) {
         reinterpret_cast<float2 *>(aux)[qb] = make_float2(d8, d8 * (float)qsum);
     }

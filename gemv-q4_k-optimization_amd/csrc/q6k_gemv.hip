@@ -1,7 +1,8 @@
 // q6k_gemv.hip -- the Q6_K matrix-vector product's launches and its C ABI
 // (declared in include/q4k_gemv.h next to the Q4_K entry points).  The tile
-// kernel is in q6k_kernels.h: its product variants are instantiated here,
-// its parity variants in q4k_sums.hip.
+// kernel is in q6k_kernels.h, the matrix-core kernel in q6k_mfma.h: their
+// product variants are instantiated here, their parity variants in
+// q6k_sums.hip.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -10,6 +11,7 @@
 #include "q4k_runtime.h"
 #include "q4k_tile.h"
 #include "q6k_kernels.h"
+#include "q6k_mfma.h"
 
 namespace q4k {
 
@@ -86,7 +88,54 @@ struct Q6Geometry {
     int rows_extra = 0;
     int prologue = 0;
     int slots = 2;
+    int mfma = 0;  // 1: matrix-core kernel (tiles of 16 rows; rows_base/rows_extra count tiles)
+    int ks = 1;    // matrix-core kernel: waves sharing one tile
+    int segs = 1;  // matrix-core kernel: summation segments of a row
 };
+
+// Where the matrix-core kernel is chosen: eight columns from 896 row tiles,
+// six or more from 2048.  Measured on MI355X against the tile kernel (graph
+// replays, us): 128256 x 4096 N=8 117.0 -> 93.5, N=6 106.7 -> 92.4;
+// 65536 x 4096 N=6 55.6 -> 49.5; 32768 x 4096 N=8 36.4 -> 29.1, N=6
+// 30.3 -> 28.5; 14336 x 4096 N=8 19.1 -> 18.3.  Slower at four columns
+// (128256 x 4096: 86.2 against 88.5), at 14336 x 4096 N=6 and on small or
+// long-row products (4096 x 14336 N=8: 27.7 against 37.4).
+static bool use_mfma_q6(int64_t M, int64_t N) {
+    const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
+    return (N == 8 && tiles >= 896) || (N >= 6 && tiles >= 2048);
+}
+
+// The matrix-core kernel's geometry, as for Q4_K: one workgroup per CU (at
+// most one per tile) of 8 or 16 waves, the tiles split evenly over the
+// workgroups, and KS waves sharing a tile, KS at most the S summation
+// segments of a row (a function of K alone, which fixes the summation order).
+static Q6Geometry pick_geometry_q6_mfma(const DeviceInfo &di, int64_t K, int64_t M, int nc, int owgs, int owaves) {
+    Q6Geometry g;
+    const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
+    const int cus = di.cus > 0 ? di.cus : 1;
+    const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
+    g.mfma = 1;
+    g.slots = 2;
+    g.nc_chunk = nc;
+    const int64_t wgs = owgs > 0 ? owgs : cus;
+    g.grid = (int)(tiles < wgs ? tiles : wgs);
+    if (g.grid < 1) g.grid = 1;
+    g.rows_base = (int)(tiles / g.grid);
+    g.rows_extra = (int)(tiles % g.grid);
+    const int64_t nt = g.rows_base + (g.rows_extra ? 1 : 0);
+    g.waves = 16;
+    if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;
+    const int64_t nb = K / kQK;
+    g.segs = 1;
+    while (g.segs < kMfmaMaxSegs && 2 * g.segs <= nb) g.segs *= 2;
+    int groups = 1;
+    while (groups < g.waves && 2 * groups <= nt) groups *= 2;
+    g.ks = g.waves / groups;
+    while (g.ks > g.segs) g.ks /= 2;
+    g.lds = q6m_lds_bytes((int)K, nc, g.waves);
+    g.lds_launch = g.lds <= max_lds / 2 ? max_lds / 2 + 256 : g.lds;  // one workgroup per CU
+    return g;
+}
 
 // One workgroup per CU; one group (3360 bytes per wave) in flight per wave;
 // 8 waves unless the activation is long (more than 8192 values over all
@@ -100,6 +149,13 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     Q6Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
+    const int okern = g_ovr_kernel.load();
+    if (fused == kFusedNone && mats == 1 && (okern == 4 || (okern == 0 && use_mfma_q6(M, N)))) {
+        int mc = (int)N;
+        while (mc > 1 && q6m_lds_bytes((int)K, mc, 16) > max_lds) mc = (mc + 1) / 2;
+        if (q6m_lds_bytes((int)K, mc, 16) <= max_lds && (okern == 4 || mc == N))
+            return pick_geometry_q6_mfma(di, K, M, mc, g_ovr_wgs.load(), g_ovr_waves.load());
+    }
     int nc = (int)N;
     // Measured on MI355X: 4096 x 14336 at 8 columns, one dense launch 26.8 us
     // against two padded 4-column launches 34.5 us.
@@ -198,6 +254,25 @@ static const void *q6_kernel_for(int nc, int waves, int pro, int slots, int fuse
     return slots == 1 ? q6_sym_nc<16, 1, BATCH>(nc, pro) : q6_sym_nc<16, 2, BATCH>(nc, pro);
 }
 
+template <int WAVES>
+static const void *q6_mfma_kernel_nc(int nc) {
+    switch (nc) {
+        case 1: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<1, WAVES>);
+        case 2: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<2, WAVES>);
+        case 3: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<3, WAVES>);
+        case 4: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<4, WAVES>);
+        case 5: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<5, WAVES>);
+        case 6: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<6, WAVES>);
+        case 7: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<7, WAVES>);
+        case 8: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<8, WAVES>);
+        default: return nullptr;
+    }
+}
+
+static const void *q6_mfma_kernel_for(int nc, int waves) {
+    return waves > 8 ? q6_mfma_kernel_nc<16>(nc) : q6_mfma_kernel_nc<8>(nc);
+}
+
 int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01) {
     if (ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0) return Q4K_EINVAL;
     const int64_t row_bytes = ne00 / kQK * kQ6Bytes;
@@ -221,16 +296,20 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
     const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
     const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats, fused);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
-    // a wave's rows are addressed with 31-bit offsets; column strides travel
-    // as 32-bit kernel arguments
-    if ((int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31)) return Q4K_EUNSUPPORTED;
+    // a wave's rows (the matrix-core kernel: a workgroup's tiles) are
+    // addressed with 31-bit offsets; column strides travel as 32-bit kernel
+    // arguments
+    if (geo.mfma ? (int64_t)(geo.rows_base + 1) * kMfmaRows * nb01 >= ((int64_t)1 << 31)
+                 : (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31))
+        return Q4K_EUNSUPPORTED;
     if (ldx > INT32_MAX || stride_col_y > INT32_MAX) return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         // a last chunk of under kDenseMinCols columns is staged padded
         const bool dense = geo.dense && nc >= kDenseMinCols;
         int lds_launch = geo.lds_launch;
-        const int lds = q6_tile_lds_bytes((int)ne00, nc, geo.waves, dense);
+        const int lds = geo.mfma ? q6m_lds_bytes((int)ne00, nc, geo.waves)
+                                 : q6_tile_lds_bytes((int)ne00, nc, geo.waves, dense);
         if (lds > di->max_lds) return Q4K_EUNSUPPORTED;
         if (lds_launch < lds) lds_launch = lds;
         GemvParams p{};
@@ -258,11 +337,18 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
             p.glu_op = ep->glu_op;
         }
-        const void *fn = bl ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
-                            : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
+        const void *fn = geo.mfma ? q6_mfma_kernel_for(nc, geo.waves)
+                         : bl     ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
+                                  : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
+        if (geo.mfma) {
+            if (fused || bl) return Q4K_EINVAL;
+            p.rpw = geo.ks;
+            p.ntiles = geo.segs;
+        }
         if (so) {  // parity variant: this chunk's columns of the group sums
             if (fused || bl) return Q4K_EINVAL;
-            fn = q6k_sums_kernel(nc, geo.waves, geo.prologue, geo.slots, dense);
+            fn = geo.mfma ? q6k_mfma_sums_kernel(nc, geo.waves)
+                          : q6k_sums_kernel(nc, geo.waves, geo.prologue, geo.slots, dense);
             if (!fn) return Q4K_EUNSUPPORTED;  // a launch shape with no parity variant (overrides)
             p.sums = so->sums + c0 * ne01 * (ne00 / 16);
         }
@@ -428,7 +514,7 @@ int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) 
     out[3] = g.lds_launch;
     out[4] = g.nc_chunk;
     out[5] = g.nc_chunk >= ne11 ? 1 : 0;
-    out[6] = 1;
+    out[6] = g.mfma ? 4 : 1;
     out[7] = g.slots;
     return Q4K_OK;
 }

@@ -1,12 +1,14 @@
-// q6k_sums.hip -- the parity variants (SUMS) of the Q6_K GEMV kernel: the
-// product kernel of q6k_kernels.h that also stores every lane's int32 group
-// sums.  Instantiated for the launch shapes the automatic geometry picks for
-// plain products (8 or 16 waves, one slot, prologue 0 or 1); q6k_gemv.hip
-// launches them with the product's own geometry.
+// q6k_sums.hip -- the parity variants (SUMS) of the Q6_K GEMV kernels: the
+// product kernels of q6k_kernels.h and q6k_mfma.h that also store every
+// lane's int32 group sums.  Instantiated for the launch shapes the automatic
+// geometry picks for plain products (8 or 16 waves; the tile kernel with one
+// slot and prologue 0 or 1); q6k_gemv.hip launches them with the product's
+// own geometry.
 #include <hip/hip_runtime.h>
 
 #include "q4k_runtime.h"
 #include "q6k_kernels.h"
+#include "q6k_mfma.h"
 
 namespace q4k {
 namespace {
@@ -47,7 +49,26 @@ const void *q6_sums_nc(int nc, int pro) {
     }
 }
 
+template <int WAVES>
+const void *q6_mfma_sums_nc(int nc) {
+    switch (nc) {
+        case 1: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<1, WAVES, true>);
+        case 2: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<2, WAVES, true>);
+        case 3: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<3, WAVES, true>);
+        case 4: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<4, WAVES, true>);
+        case 5: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<5, WAVES, true>);
+        case 6: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<6, WAVES, true>);
+        case 7: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<7, WAVES, true>);
+        case 8: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<8, WAVES, true>);
+        default: return nullptr;
+    }
+}
+
 }  // namespace
+
+const void *q6k_mfma_sums_kernel(int nc, int waves) {
+    return waves > 8 ? q6_mfma_sums_nc<16>(nc) : q6_mfma_sums_nc<8>(nc);
+}
 
 const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense) {
     if (slots != 1) return nullptr;

@@ -159,6 +159,14 @@ def test_eight_wave_register_path_long_products(Q, O, gpu):
     whose registers hold every column's activation slices: the oracle on a
     row sample, and bit for bit the pre-quantised launch."""
     M, K, N = 65536, 4096, 6
+    Q.set_geometry_override(kernel=1)  # the tile kernel (the automatic choice here is the matrix-core one)
+    try:
+        _eight_wave_long(Q, O, gpu, M, K, N)
+    finally:
+        Q.set_geometry_override()
+
+
+def _eight_wave_long(Q, O, gpu, M, K, N):
     assert Q.geometry(K, M, N, wtype=Q.GGML_TYPE_Q6_K)["waves_per_wg"] == 8
     rng = np.random.default_rng(12)
     wq = random_q6_blocks(rng, M, K, extremes=False)
