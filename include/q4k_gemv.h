@@ -291,7 +291,8 @@ int q6k_mul_mat_vec_q_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t
                            void *workspace, size_t workspace_bytes, int32_t *s16, void *stream);
 
 /* Launch geometry q6k_mul_mat_vec_q would use (the out[] fields of
- * q4k_gemv_geometry; out[7] = weight groups in flight per wave). */
+ * q4k_gemv_geometry; out[6] 1 tile kernel or 4 matrix-core kernel; out[7] =
+ * weight groups in flight per wave). */
 int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
 
 /* Launch geometry q4k_mul_mat_vec_q would use on the current device:
@@ -309,7 +310,8 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * variant; reduced to 8 where 16 would not fit the registers), the number
  * of workgroups and the kernel (1 tile kernel, 2 block-per-lane, 3
  * coalesced block kernel where they apply, 4 matrix-core kernel for
- * products without an epilogue); 0 restores the automatic
+ * products without an epilogue; Q6_K: 4 the matrix-core kernel, any other
+ * value the tile kernel); 0 restores the automatic
  * choice.  Nothing is read from the environment: until this is called the
  * geometry is automatic.  Not part of the reference interface: a
  * benchmarking knob (ggml's counterpart is editing the compile-time tables
