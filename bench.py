@@ -19,15 +19,16 @@ run on.  value = algorithmic bytes per step / seconds per step (GB/s); the
 roofline object prices the same bytes against the 8 TB/s HBM peak, and its
 traffic is the HBM bytes rocprofv3 counted for the same launch
 (profiles/q4k_traffic_all_configs.txt).  The CPU baseline is the oracle's
-restatement of ggml's CPU path (Q8_K activations + vec_dot_q4_K_q8_K, AVX2)
-on pinned threads of this machine, timed on a bounded sample.
+restatement of ggml's CPU path (Q8_K activations + vec_dot_q4_K_q8_K or
+vec_dot_q6_K_q8_K, AVX2) on pinned threads of this machine, timed on a bounded
+sample.
 
 Modes:
   (default)         the headline JSON line
   --sweep           one JSON line per (shape, ncols) of the five workloads
                     (--wtype q6_K: the Q6_K tensors of a Q4_K_M model), each
-                    with the roofline fraction, the measured traffic and, for
-                    Q4_K, a CPU baseline with and without Q8_K quantisation
+                    with the roofline fraction, the measured traffic and a
+                    CPU baseline with and without Q8_K quantisation
   --fused, --moe    the fused gate/up launch and MUL_MAT_ID workloads
   --profile         plain eager launches of one shape (for rocprofv3)
   --profile-sweep   plain eager launches of every sweep config in order, each
@@ -323,11 +324,12 @@ def read_traffic(M: int, K: int, N: int, wtype: str = "q4_K"):
     return None, None
 
 
-def cpu_baseline(wq, x, target_s=12.0, min_reps=10):
+def cpu_baseline(wq, x, target_s=12.0, min_reps=10, wtype="q4_K"):
     """ggml's CPU path (restated in the oracle) on this machine: Q8_K
-    quantisation of x + vec_dot_q4_K_q8_K per (row, column), AVX2, one thread
-    per CPU of the job's share, each pinned.  Median of >= min_reps calls
-    with quantisation and without (Q8_K activation prepared beforehand)."""
+    quantisation of x + vec_dot_q4_K_q8_K (vec_dot_q6_K_q8_K for Q6_K) per
+    (row, column), AVX2, one thread per CPU of the job's share, each pinned.
+    Median of >= min_reps calls with quantisation and without (Q8_K
+    activation prepared beforehand)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     if not os.path.exists(O.LIB_PATH):
@@ -335,14 +337,14 @@ def cpu_baseline(wq, x, target_s=12.0, min_reps=10):
     cpus = sorted(os.sched_getaffinity(0))[:CPU_SHARE]
     cores = len(cpus)
     O.set_pin_cpus(cpus)
-    K = wq.shape[1] // 144 * 256
+    K = wq.shape[1] // BLOCK_BYTES[wtype] * 256
     M, N = wq.shape[0], x.shape[0]
     out = {}
     for mode, quant in (("with_q8K", True), ("without_q8K", False)):
-        t1 = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, 2, quantize=quant)
+        t1 = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, 2, quantize=quant, wtype=wtype)
         per = float(np.median(t1))
         reps = int(max(min_reps, min(5000, target_s / 2 / max(per, 1e-6))))
-        t = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, reps, quantize=quant)
+        t = O.time_cpu_mul_mat_q4_K(wq, K, x, cores, reps, quantize=quant, wtype=wtype)
         out[mode] = (float(np.median(t)), reps, float(np.sum(t)))
     O.set_pin_cpus([])
     isa = "avx2" if O.lib().orc_cpu_has_avx2() else "scalar"
@@ -354,14 +356,14 @@ def cpu_baseline(wq, x, target_s=12.0, min_reps=10):
         pass
     med, reps, tot = out["with_q8K"]
     med_nq, reps_nq, tot_nq = out["without_q8K"]
-    nbytes = algorithmic_bytes(M, K, N)
+    nbytes = algorithmic_bytes(M, K, N, wtype)
     return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
             "us_per_call": round(med * 1e6, 1), "us_per_call_without_q8K": round(med_nq * 1e6, 1),
             "GBps_without_q8K": round(nbytes / med_nq / 1e9, 2), "cpu_model": model, "isa": isa,
             "host_cpus": os.cpu_count(), "pinned_cpus": f"{cpus[0]}..{cpus[-1]}" if cpus else "",
             "label": "ggml-equivalent restatement (ggml itself is not available offline)",
             "sample": f"{reps} calls of the full {M}x{K} N={N} product with Q8_K quantisation of x "
-                      f"({tot:.1f} s) and {reps_nq} without ({tot_nq:.1f} s): vec_dot_q4_K_q8_K ({isa}), "
+                      f"({tot:.1f} s) and {reps_nq} without ({tot_nq:.1f} s): vec_dot_{wtype}_q8_K ({isa}), "
                       f"{cores} threads pinned one per CPU (the job's CPU share of this {os.cpu_count()}-CPU "
                       f"host), ggml's row chunks of 16; medians"}
 
@@ -437,8 +439,8 @@ def sweep(args):
              "traffic_gemv_bytes": traffic, "traffic_op_bytes": op_traffic,
              "traffic_ratio": round(op_traffic / nbytes, 4) if op_traffic else None,
              "geometry": Q.geometry(K, M, N, gtype)}
-        if wt == "q4_K" and not args.no_cpu:
-            r["cpu_baseline"] = cpu_baseline(wq, x, target_s=args.cpu_seconds, min_reps=10)
+        if not args.no_cpu:
+            r["cpu_baseline"] = cpu_baseline(wq, x, target_s=args.cpu_seconds, min_reps=10, wtype=wt)
         print(json.dumps(r), flush=True)
 
 

@@ -68,9 +68,13 @@ def lib():
             "orc_quantize_q8_K": (None, [P, P, I64]),
             "orc_vec_dot_q4_K_q8_K_scalar": (ctypes.c_float, [I64, P, P]),
             "orc_vec_dot_q4_K_q8_K_avx2": (ctypes.c_float, [I64, P, P]),
+            "orc_vec_dot_q6_K_q8_K_scalar": (ctypes.c_float, [I64, P, P]),
+            "orc_vec_dot_q6_K_q8_K_avx2": (ctypes.c_float, [I64, P, P]),
             "orc_cpu_has_avx2": (I, []),
             "orc_cpu_mul_mat_q4_K": (I, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I]),
+            "orc_cpu_mul_mat_q6_K": (I, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I]),
             "orc_time_cpu_mul_mat_q4_K": (None, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I, I, P]),
+            "orc_time_cpu_mul_mat_q6_K": (None, [P, I64, I64, I64, P, I64, I64, P, P, I64, I, I, I, I, P]),
             "orc_set_pin_cpus": (None, [P, I]),
             "orc_quantize_q6_K": (None, [P, P, I64]),
             "orc_dequantize_q6_K": (None, [P, P, I64]),
@@ -255,18 +259,30 @@ def vec_dot_q4_K_q8_K(w_row: np.ndarray, y_row: np.ndarray, K: int, isa: str = "
     return float(f(K, _p(np.ascontiguousarray(w_row)), _p(np.ascontiguousarray(y_row))))
 
 
-def cpu_mul_mat_q4_K(w_q: np.ndarray, K: int, x: np.ndarray, nthreads: int = 1, isa: str = "avx2"):
-    """ggml CPU path: x [N, K] f32 -> Q8_K, then vec_dot per (row, column);
+def vec_dot_q6_K_q8_K(w_row: np.ndarray, y_row: np.ndarray, K: int, isa: str = "avx2") -> float:
+    f = lib().orc_vec_dot_q6_K_q8_K_avx2 if isa == "avx2" else lib().orc_vec_dot_q6_K_q8_K_scalar
+    return float(f(K, _p(np.ascontiguousarray(w_row)), _p(np.ascontiguousarray(y_row))))
+
+
+_CPU_TYPES = {"q4_K": ("orc_cpu_mul_mat_q4_K", "orc_time_cpu_mul_mat_q4_K", Q4K_BYTES),
+              "q6_K": ("orc_cpu_mul_mat_q6_K", "orc_time_cpu_mul_mat_q6_K", Q6K_BYTES)}
+
+
+def cpu_mul_mat_q4_K(w_q: np.ndarray, K: int, x: np.ndarray, nthreads: int = 1, isa: str = "avx2",
+                     wtype: str = "q4_K"):
+    """ggml CPU path: x [N, K] f32 -> Q8_K, then vec_dot per (row, column)
+    (vec_dot_q4_K_q8_K, or vec_dot_q6_K_q8_K for wtype "q6_K");
     returns (dst [N, M] float32, isa_used)."""
+    fn, _, bb = _CPU_TYPES[wtype]
     w_q = np.ascontiguousarray(w_q, dtype=np.uint8)
     x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
     N = x.shape[0]
-    row_bytes = K // QK_K * Q4K_BYTES
+    row_bytes = K // QK_K * bb
     M = w_q.size // row_bytes
     yq = np.empty((N, K // QK_K * Q8K_BYTES), dtype=np.uint8)
     dst = np.empty((N, M), dtype=np.float32)
-    used = lib().orc_cpu_mul_mat_q4_K(_p(w_q), M, K, row_bytes, _p(x), N, K, _p(yq), _p(dst), M,
-                                      nthreads, 1 if isa == "avx2" else 0, 1)
+    used = getattr(lib(), fn)(_p(w_q), M, K, row_bytes, _p(x), N, K, _p(yq), _p(dst), M,
+                              nthreads, 1 if isa == "avx2" else 0, 1)
     return dst, ("avx2" if used else "scalar")
 
 
@@ -278,19 +294,20 @@ def set_pin_cpus(cpus):
 
 
 def time_cpu_mul_mat_q4_K(w_q: np.ndarray, K: int, x: np.ndarray, nthreads: int, reps: int,
-                          isa: str = "avx2", quantize: bool = True) -> np.ndarray:
-    """Wall time (s) of each of `reps` calls of the threaded CPU path."""
+                          isa: str = "avx2", quantize: bool = True, wtype: str = "q4_K") -> np.ndarray:
+    """Wall time (s) of each of `reps` calls of the threaded CPU path (Q4_K
+    weights, or Q6_K for wtype "q6_K")."""
+    _, fn, bb = _CPU_TYPES[wtype]
     w_q = np.ascontiguousarray(w_q, dtype=np.uint8)
     x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
     N = x.shape[0]
-    row_bytes = K // QK_K * Q4K_BYTES
+    row_bytes = K // QK_K * bb
     M = w_q.size // row_bytes
     yq = quantize_q8_K(x)
     dst = np.empty((N, M), dtype=np.float32)
     t = np.empty(reps, dtype=np.float64)
-    lib().orc_time_cpu_mul_mat_q4_K(_p(w_q), M, K, row_bytes, _p(x), N, K, _p(yq), _p(dst), M,
-                                    nthreads, 1 if isa == "avx2" else 0, 1 if quantize else 0,
-                                    reps, _p(t))
+    getattr(lib(), fn)(_p(w_q), M, K, row_bytes, _p(x), N, K, _p(yq), _p(dst), M,
+                       nthreads, 1 if isa == "avx2" else 0, 1 if quantize else 0, reps, _p(t))
     return t
 
 

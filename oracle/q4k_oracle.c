@@ -753,6 +753,7 @@ typedef struct {
     float *dst;
     int64_t ld_dst;
     int use_avx2;
+    int q6; /* weights are block_q6_K (vec_dot_q6_K_q8_K) */
     int nthreads;
     atomic_long next_chunk;
     pthread_barrier_t bar;
@@ -786,6 +787,10 @@ static void orc_pin_self(int t) {
 
 #define ORC_ROW_CHUNK 16
 
+/* q6k_oracle.c */
+float orc_vec_dot_q6_K_q8_K_scalar(int64_t n, const uint8_t *x, const uint8_t *y);
+float orc_vec_dot_q6_K_q8_K_avx2(int64_t n, const uint8_t *x, const uint8_t *y);
+
 static void *orc_mm_worker(void *p) {
     orc_mm_arg *a = (orc_mm_arg *)p;
     orc_mm_job *j = a->job;
@@ -808,8 +813,11 @@ static void *orc_mm_worker(void *p) {
             const uint8_t *yc = j->yq + c * nbk * ORC_Q8K_BYTES;
             for (int64_t r = r0; r < r1; ++r) {
                 const uint8_t *wr = j->w + r * j->row_stride;
-                j->dst[c * j->ld_dst + r] = j->use_avx2 ? orc_vec_dot_q4_K_q8_K_avx2(j->K, wr, yc)
-                                                        : orc_vec_dot_q4_K_q8_K_scalar(j->K, wr, yc);
+                j->dst[c * j->ld_dst + r] =
+                    j->q6 ? (j->use_avx2 ? orc_vec_dot_q6_K_q8_K_avx2(j->K, wr, yc)
+                                         : orc_vec_dot_q6_K_q8_K_scalar(j->K, wr, yc))
+                          : (j->use_avx2 ? orc_vec_dot_q4_K_q8_K_avx2(j->K, wr, yc)
+                                         : orc_vec_dot_q4_K_q8_K_scalar(j->K, wr, yc));
             }
         }
     }
@@ -820,11 +828,12 @@ static void *orc_mm_worker(void *p) {
  * N*(K/256)*292 bytes; with quantize == 0 it must already hold Q8_K(x).
  * isa: 0 scalar, 1 AVX2 (falls back to scalar when the CPU lacks it).
  * Returns the ISA used. */
-int orc_cpu_mul_mat_q4_K(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const float *x,
-                         int64_t N, int64_t ldx, uint8_t *yq, float *dst, int64_t ld_dst,
-                         int nthreads, int isa, int quantize) {
+static int orc_cpu_mul_mat(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const float *x,
+                           int64_t N, int64_t ldx, uint8_t *yq, float *dst, int64_t ld_dst,
+                           int nthreads, int isa, int quantize, int q6) {
     if (nthreads < 1) nthreads = 1;
     orc_mm_job job;
+    job.q6 = q6;
     job.w = w; job.M = M; job.K = K; job.row_stride = row_stride;
     job.x = x; job.N = N; job.ldx = ldx; job.yq = yq; job.dst = dst; job.ld_dst = ld_dst;
     job.use_avx2 = (isa == 1) && orc_cpu_has_avx2();
@@ -853,19 +862,46 @@ int orc_cpu_mul_mat_q4_K(const uint8_t *w, int64_t M, int64_t K, int64_t row_str
     return job.use_avx2;
 }
 
-/* Times `reps` calls of orc_cpu_mul_mat_q4_K and writes each call's wall time
- * in seconds into t[0..reps). */
+int orc_cpu_mul_mat_q4_K(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const float *x,
+                         int64_t N, int64_t ldx, uint8_t *yq, float *dst, int64_t ld_dst,
+                         int nthreads, int isa, int quantize) {
+    return orc_cpu_mul_mat(w, M, K, row_stride, x, N, ldx, yq, dst, ld_dst, nthreads, isa, quantize, 0);
+}
+
+/* The same for block_q6_K weights (vec_dot_q6_K_q8_K). */
+int orc_cpu_mul_mat_q6_K(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride, const float *x,
+                         int64_t N, int64_t ldx, uint8_t *yq, float *dst, int64_t ld_dst,
+                         int nthreads, int isa, int quantize) {
+    return orc_cpu_mul_mat(w, M, K, row_stride, x, N, ldx, yq, dst, ld_dst, nthreads, isa, quantize, 1);
+}
+
+/* Times `reps` calls of orc_cpu_mul_mat_q4_K (q6: orc_cpu_mul_mat_q6_K) and
+ * writes each call's wall time in seconds into t[0..reps). */
+static void orc_time_cpu_mul_mat(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride,
+                                 const float *x, int64_t N, int64_t ldx, uint8_t *yq, float *dst,
+                                 int64_t ld_dst, int nthreads, int isa, int quantize, int reps,
+                                 double *t, int q6) {
+    for (int i = 0; i < reps; ++i) {
+        struct timespec a, b;
+        clock_gettime(CLOCK_MONOTONIC, &a);
+        orc_cpu_mul_mat(w, M, K, row_stride, x, N, ldx, yq, dst, ld_dst, nthreads, isa, quantize, q6);
+        clock_gettime(CLOCK_MONOTONIC, &b);
+        t[i] = (double)(b.tv_sec - a.tv_sec) + 1e-9 * (double)(b.tv_nsec - a.tv_nsec);
+    }
+}
+
 void orc_time_cpu_mul_mat_q4_K(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride,
                                const float *x, int64_t N, int64_t ldx, uint8_t *yq, float *dst,
                                int64_t ld_dst, int nthreads, int isa, int quantize, int reps,
                                double *t) {
-    for (int i = 0; i < reps; ++i) {
-        struct timespec a, b;
-        clock_gettime(CLOCK_MONOTONIC, &a);
-        orc_cpu_mul_mat_q4_K(w, M, K, row_stride, x, N, ldx, yq, dst, ld_dst, nthreads, isa, quantize);
-        clock_gettime(CLOCK_MONOTONIC, &b);
-        t[i] = (double)(b.tv_sec - a.tv_sec) + 1e-9 * (double)(b.tv_nsec - a.tv_nsec);
-    }
+    orc_time_cpu_mul_mat(w, M, K, row_stride, x, N, ldx, yq, dst, ld_dst, nthreads, isa, quantize, reps, t, 0);
+}
+
+void orc_time_cpu_mul_mat_q6_K(const uint8_t *w, int64_t M, int64_t K, int64_t row_stride,
+                               const float *x, int64_t N, int64_t ldx, uint8_t *yq, float *dst,
+                               int64_t ld_dst, int nthreads, int isa, int quantize, int reps,
+                               double *t) {
+    orc_time_cpu_mul_mat(w, M, K, row_stride, x, N, ldx, yq, dst, ld_dst, nthreads, isa, quantize, reps, t, 1);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -27,6 +27,14 @@
  *                        value on the nearest level; all-zero blocks;
  *                        exact-grid blocks round-trip bit for bit
  *
+ *   orc_vec_dot_q6_K_q8_K_scalar / _avx2 (ggml's CPU dot, the CPU baseline
+ *                        for Q6_K): against the f64 dot of the dequantised
+ *                        weights and the dequantised Q8_K activation, and the
+ *                        threaded product against the Q8_1 path to the
+ *                        activation-quantisation error
+ *                        (tests/test_oracle_cpu_baseline.py); bit-exactness
+ *                        with ggml is unpinned (ggml is not available)
+ *
  * Build: oracle/Makefile (gcc, -ffp-contract=off).
  */
 #include <math.h>
@@ -34,10 +42,12 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#include <immintrin.h>
 
 #define ORC_QK_K 256
 #define ORC_Q6K_BYTES 210 /* ql[128], qh[64], scales[16] (int8), d (fp16) */
 #define ORC_Q81_BYTES 36
+#define ORC_Q8K_BYTES 292 /* float d + int8 qs[256] + int16 bsums[16] */
 #define ORC_GROUP_MAX_EPS 1e-15f
 
 /* from q4k_oracle.c */
@@ -313,4 +323,101 @@ int64_t orc_gemv_q6K_q8_1_mt(const uint8_t *w, int64_t M, int64_t K, int64_t row
     free(th);
     free(task);
     return mism;
+}
+
+/* ------------------------------------------------------------------------ */
+/* ggml's CPU dot for Q6_K (the CPU baseline of the Q6_K configs)           */
+/* ------------------------------------------------------------------------ */
+
+/* The 256 weights of a block as q - 32 in [-32, 31], in weight order (the
+ * layout dequantize_row_q6_K reads: half h, l in [0, 32): weights 128h + l,
+ * +32, +64, +96 from ql[64h + l] low, ql[64h + 32 + l] low, ql[64h + l] high,
+ * ql[64h + 32 + l] high and qh[32h + l] bits 0-1, 2-3, 4-5, 6-7). */
+static void orc_q6_values(const uint8_t *x, int8_t a[ORC_QK_K]) {
+    const uint8_t *ql = x, *qh = x + 128;
+    for (int h = 0; h < 2; ++h) {
+        for (int l = 0; l < 32; ++l) {
+            const int lo0 = ql[64 * h + l], lo1 = ql[64 * h + 32 + l], hb = qh[32 * h + l];
+            a[128 * h + l] = (int8_t)(((lo0 & 0x0f) | ((hb & 3) << 4)) - 32);
+            a[128 * h + 32 + l] = (int8_t)(((lo1 & 0x0f) | (((hb >> 2) & 3) << 4)) - 32);
+            a[128 * h + 64 + l] = (int8_t)(((lo0 >> 4) | (((hb >> 4) & 3) << 4)) - 32);
+            a[128 * h + 96 + l] = (int8_t)(((lo1 >> 4) | (((hb >> 6) & 3) << 4)) - 32);
+        }
+    }
+}
+
+/* ggml_vec_dot_q6_K_q8_K, portable form: per block, eight int32 lanes (lane l
+ * takes elements 8t + l of every 8-element slice) accumulate scale * q8 * w
+ * over the 16 scale groups; each block's lanes are scaled by d_w * d_y and
+ * summed per lane in float, the lanes added at the end. */
+float orc_vec_dot_q6_K_q8_K_scalar(int64_t n, const uint8_t *x, const uint8_t *y) {
+    const int64_t nb = n / ORC_QK_K;
+    float sums[8] = {0};
+    for (int64_t i = 0; i < nb; ++i, x += ORC_Q6K_BYTES, y += ORC_Q8K_BYTES) {
+        float dy;
+        memcpy(&dy, y, 4);
+        const int8_t *q8 = (const int8_t *)(y + 4);
+        const int8_t *sc = (const int8_t *)(x + 192);
+        int8_t a[ORC_QK_K];
+        orc_q6_values(x, a);
+        int32_t lanes[8] = {0};
+        for (int g = 0; g < 16; ++g)
+            for (int t = 0; t < 2; ++t)
+                for (int l = 0; l < 8; ++l) {
+                    const int e = 16 * g + 8 * t + l;
+                    lanes[l] += sc[g] * ((int32_t)q8[e] * (int32_t)a[e]);
+                }
+        const float d = orc_f16_to_f32((uint16_t)(x[208] | (x[209] << 8))) * dy;
+        for (int l = 0; l < 8; ++l) sums[l] += d * lanes[l];
+    }
+    float sumf = 0;
+    for (int l = 0; l < 8; ++l) sumf += sums[l];
+    return sumf;
+}
+
+/* The AVX2 form (ggml-cpu's x86 path): per half block the four 32-weight runs
+ * are assembled as unsigned 6-bit values, multiplied with the q8 as u8*s8 pair
+ * products (maddubs), corrected by 32 * (pair sums of q8) and scaled by the
+ * 16-bit scales of their two scale groups (madd) into eight int32 lanes; the
+ * lanes are scaled per block by d_w * d_y in a float vector, reduced at the
+ * end. */
+__attribute__((target("avx2,fma,f16c")))
+float orc_vec_dot_q6_K_q8_K_avx2(int64_t n, const uint8_t *x, const uint8_t *y) {
+    const int64_t nb = n / ORC_QK_K;
+    const __m256i m4 = _mm256_set1_epi8(0x0f), m3 = _mm256_set1_epi8(3), k32 = _mm256_set1_epi8(32);
+    __m256 acc = _mm256_setzero_ps();
+    for (int64_t i = 0; i < nb; ++i, x += ORC_Q6K_BYTES, y += ORC_Q8K_BYTES) {
+        float dy;
+        memcpy(&dy, y, 4);
+        const float d = dy * _cvtsh_ss((unsigned short)(x[208] | (x[209] << 8)));
+        const int8_t *sc = (const int8_t *)(x + 192);
+        const int8_t *q8 = (const int8_t *)(y + 4);
+        __m256i sumi = _mm256_setzero_si256();
+        for (int h = 0; h < 2; ++h) {
+            const __m256i lo0 = _mm256_loadu_si256((const __m256i *)(x + 64 * h));
+            const __m256i lo1 = _mm256_loadu_si256((const __m256i *)(x + 64 * h + 32));
+            const __m256i hb = _mm256_loadu_si256((const __m256i *)(x + 128 + 32 * h));
+            __m256i w[4];
+            w[0] = _mm256_or_si256(_mm256_and_si256(lo0, m4), _mm256_slli_epi16(_mm256_and_si256(hb, m3), 4));
+            w[1] = _mm256_or_si256(_mm256_and_si256(lo1, m4),
+                                   _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(hb, 2), m3), 4));
+            w[2] = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(lo0, 4), m4),
+                                   _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(hb, 4), m3), 4));
+            w[3] = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(lo1, 4), m4),
+                                   _mm256_slli_epi16(_mm256_and_si256(_mm256_srli_epi16(hb, 6), m3), 4));
+            for (int r = 0; r < 4; ++r) {
+                const __m256i yv = _mm256_loadu_si256((const __m256i *)(q8 + 128 * h + 32 * r));
+                const __m256i p = _mm256_sub_epi16(_mm256_maddubs_epi16(w[r], yv), _mm256_maddubs_epi16(k32, yv));
+                /* scale groups 8h + 2r (pairs 0..7) and 8h + 2r + 1 (pairs 8..15) */
+                const __m256i s16 = _mm256_setr_m128i(_mm_set1_epi16(sc[8 * h + 2 * r]),
+                                                      _mm_set1_epi16(sc[8 * h + 2 * r + 1]));
+                sumi = _mm256_add_epi32(sumi, _mm256_madd_epi16(s16, p));
+            }
+        }
+        acc = _mm256_fmadd_ps(_mm256_set1_ps(d), _mm256_cvtepi32_ps(sumi), acc);
+    }
+    __m128 h4 = _mm_add_ps(_mm256_castps256_ps128(acc), _mm256_extractf128_ps(acc, 1));
+    h4 = _mm_add_ps(h4, _mm_movehl_ps(h4, h4));
+    h4 = _mm_add_ss(h4, _mm_movehdup_ps(h4));
+    return _mm_cvtss_f32(h4);
 }

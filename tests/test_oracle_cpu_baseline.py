@@ -53,3 +53,41 @@ def test_scalar_and_avx2_agree_with_dequantised_product(O):
     # outputs agree only to the activation-quantisation error
     ref = O.gemv_q4K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
     assert np.abs(dst - ref["y64"]).max() < 0.02 * np.abs(ref["y64"]).max()
+
+
+def test_q6_K_scalar_and_avx2_agree_with_dequantised_product(O):
+    """The same for ggml's vec_dot_q6_K_q8_K (the CPU baseline of the Q6_K
+    configs): scalar and AVX2 forms and the threaded product against the f64
+    dot of the decoded weights (d * scale * (q - 32), a numpy decode of the
+    dequantize_row_q6_K layout) and the dequantised Q8_K activation; every
+    6-bit value and scale extreme included."""
+    import pytest
+    if not O.lib().orc_cpu_has_avx2():
+        pytest.skip("no AVX2")
+    import test_oracle_q6K as T6
+    M, K = 40, 4352
+    rng = np.random.default_rng(36)
+    wq = np.concatenate([O.quantize_q6_K(_common.weights(M // 2, K, seed=36)),
+                         T6.random_q6_blocks(rng, M // 2, K)])
+    x = _common.activations(3, K, seed=36)
+    yq = O.quantize_q8_K(x)
+    q, sc, d = T6.decode(wq, K)
+    w = (np.repeat(d.astype(np.float64), 16, 1) * sc)[:, :, None] * (q.reshape(M, -1, 16) - 32)
+    w = w.reshape(M, K)
+    dy, qs, _ = _q8K_fields(yq, K)
+    a = (dy.astype(np.float64)[..., None] * qs).reshape(3, K)
+    exact = a @ w.T
+    scale = np.abs(a) @ np.abs(w).T
+    for c in range(3):
+        for r in range(M):
+            s = O.vec_dot_q6_K_q8_K(wq[r], yq[c], K, "scalar")
+            v = O.vec_dot_q6_K_q8_K(wq[r], yq[c], K, "avx2")
+            assert abs(s - exact[c, r]) <= 1e-5 * scale[c, r], (c, r, s, exact[c, r])
+            assert abs(v - exact[c, r]) <= 1e-5 * scale[c, r], (c, r, v, exact[c, r])
+    dst, isa = O.cpu_mul_mat_q4_K(wq, K, x, nthreads=4, wtype="q6_K")
+    assert isa == "avx2"
+    assert np.allclose(dst, exact, rtol=0, atol=1e-5 * scale.max())
+    # the Q8_1 path of the GPU kernels agrees to the activation-quantisation error
+    ref = O.gemv_q6K_q8_1(wq[: M // 2], K, O.quantize_q8_1(x), want_sums=False)
+    assert np.abs(dst[:, : M // 2] - ref["y64"]).max() < 0.02 * np.abs(ref["y64"]).max()
+
