@@ -508,7 +508,7 @@ int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) 
     const int st = device_info(&di);
     if (st != Q4K_OK) return st;
     const Q6Geometry g = pick_geometry_q6(*di, ne00, ne01, ne11);
-    out[0] = 1;
+    out[0] = g.mfma ? kMfmaRows : 1;
     out[1] = g.waves;
     out[2] = g.grid;
     out[3] = g.lds_launch;
