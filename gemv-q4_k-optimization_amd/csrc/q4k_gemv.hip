@@ -317,9 +317,12 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     }
     // Large single-column products with 4096-value rows stream long enough
     // for the block-per-lane kernel's lower instruction count to win; the
-    // tile kernel does better on everything else (measured on MI355X).
+    // tile kernel does better on everything else.  Measured on MI355X (tile
+    // against block-per-lane, us): 32768 x 4096 15.27 / 16.28, 65536 x 4096
+    // 26.66 / 27.45, 98304 x 4096 38.93 / 39.51, 128256 x 4096 50.90 /
+    // 50.70, 151936 x 4096 59.64 / 59.56, 256000 x 4096 100.53 / 99.39.
     const int64_t weight_bytes = M * (K / kQK) * kBlockBytes;
-    const bool auto_bpl = okern == 0 && K == 4096 && weight_bytes >= (48ll << 20);
+    const bool auto_bpl = okern == 0 && K == 4096 && weight_bytes >= (256ll << 20);
     if (N == 1 && rpw > 0 && (okern == 2 || auto_bpl) && !fused && mats == 1) {
         // ~173 VGPRs: two waves per SIMD; 4-wave workgroups, two per CU
         g.bpl = 1;
