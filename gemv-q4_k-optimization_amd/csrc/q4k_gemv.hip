@@ -226,19 +226,31 @@ static int tile_lds_bytes(int K, int nc, int waves) { return lds_bytes(K, nc) + 
 static int lds_bytes_linear(int K) { return K + K / 4; }
 
 // Products that run on the matrix-core kernel when no override says
-// otherwise: eight columns of 896 or more row tiles (14336 rows), or six to
-// eight of 4096 or more, whose columns fit one launch.  Measured on MI355X
-// against the tile kernel (interleaved, one process): 128256 x 4096 N=8
-// 64.5 against 83.4 us, N=6 63.6 against 73.2; 28672 x 4096 N=8 21.1
-// against 22.9; 14336 x 4096 N=8 14.1 against 15.7.  Slower with fewer
-// rows (4096 x 4096 N=8 10.2 against 8.6), fewer columns (14336 x 4096 N=6
-// 13.8 against 13.3; 128256 x 4096 N=4 62.7 against 57.6: padded columns
-// cost scaling work) or longer rows (4096 x 14336 N=8: the columns need two
-// launches).  Four items in flight per wave instead of two measured slower
-// on every shape.
-static bool use_mfma(int64_t M, int64_t N) {
+// otherwise (all columns in one launch, which the caller checks).  Measured
+// on MI355X against the tile kernel (interleaved, one process; us):
+//  - rows of 4096 values: eight columns from 896 row tiles (14336 rows), six
+//    to eight from 4096 tiles: 128256 x 4096 N=8 64.5 against 83.4, N=6
+//    63.6 against 73.2; 28672 x 4096 N=8 21.1 against 22.9; 14336 x 4096 N=8
+//    14.1 against 15.7.  Slower with fewer rows (4096 x 4096 N=8 10.2
+//    against 8.6; 11008 x 4096 N=8 13.7 against 12.9) or fewer columns
+//    (14336 x 4096 N=6 13.8 against 13.3; 128256 x 4096 N=4 62.7 against
+//    57.6: padded columns cost scaling work).
+//  - longer rows (two or more 16-block groups, where the tile kernel reads
+//    every column's activation from LDS at each step): six to eight columns
+//    from 512 tiles, five from 864: 8192 x 8192 N=8 17.8 against 22.0, N=6
+//    17.0 against 19.4; 13824 x 5120 N=8 18.2 against 26.0, N=5 16.6 against
+//    18.0; 28672 x 10240 N=5 43.4 against 50.1.  Slower at 5120 x 5120 and
+//    below (N=7 13.0 against 12.5), at five columns of 8192 x 5120 or 6144
+//    (13.1 against 12.9) and at four columns (8192 x 8192 14.5 against 13.3).
+//  - shorter rows: the tile kernel (18944 x 3584 N=8 17.7 against 18.7).
+// Rows longer than ~10,700 values need two launches for eight columns and
+// are left to the tile kernel (4096 x 14336 N=8).  Four items in flight per
+// wave instead of two measured slower on every shape.
+static bool use_mfma(int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
-    return (N == 8 && tiles >= 896) || (N >= 6 && tiles >= 4096);
+    if (K < 4096) return false;
+    if (K == 4096) return (N == 8 && tiles >= 896) || (N >= 6 && tiles >= 4096);
+    return (N >= 6 && tiles >= 512) || (N == 5 && tiles >= 864);
 }
 
 // The matrix-core kernel: one workgroup per CU (at most one per tile) of 8
@@ -337,7 +349,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         g.lds_launch = g.lds;
         return g;
     }
-    if (!fused && mats == 1 && (okern == 4 || (okern == 0 && use_mfma(M, N)))) {
+    if (!fused && mats == 1 && (okern == 4 || (okern == 0 && use_mfma(M, N, K)))) {
         int mc = (int)N;
         while (mc > 1 && mfma_lds_bytes((int)K, mc, 16) > max_lds) mc = (mc + 1) / 2;
         if (mfma_lds_bytes((int)K, mc, 16) <= max_lds && (okern == 4 || mc == N))
