@@ -93,16 +93,26 @@ struct Q6Geometry {
     int segs = 1;  // matrix-core kernel: summation segments of a row
 };
 
-// Where the matrix-core kernel is chosen: eight columns from 896 row tiles,
-// six or more from 2048.  Measured on MI355X against the tile kernel (graph
-// replays, us): 128256 x 4096 N=8 117.0 -> 93.5, N=6 106.7 -> 92.4;
-// 65536 x 4096 N=6 55.6 -> 49.5; 32768 x 4096 N=8 36.4 -> 29.1, N=6
-// 30.3 -> 28.5; 14336 x 4096 N=8 19.1 -> 18.3.  Slower at four columns
-// (128256 x 4096: 86.2 against 88.5), at 14336 x 4096 N=6 and on small or
-// long-row products (4096 x 14336 N=8: 27.7 against 37.4).
-static bool use_mfma_q6(int64_t M, int64_t N) {
+// Where the matrix-core kernel is chosen (all columns in one launch, which
+// the caller checks).  Measured on MI355X against the tile kernel (graph
+// replays, us):
+//  - rows of up to 4096 values: eight columns from 896 row tiles, six or more
+//    from 2048: 128256 x 4096 N=8 117.0 -> 93.5, N=6 106.7 -> 92.4;
+//    65536 x 4096 N=6 55.6 -> 49.5; 32768 x 4096 N=8 36.4 -> 29.1, N=6
+//    30.3 -> 28.5; 14336 x 4096 N=8 19.1 -> 18.3; 28672 x 3584 N=8 30.0 ->
+//    26.7.  Slower at four columns (128256 x 4096: 86.2 against 88.5), at
+//    14336 x 4096 N=6, 13824 x 3584 N=8 and on small products.
+//  - longer rows: seven or eight columns from 512 tiles (8192 x 8192 N=8
+//    24.7 -> 22.2, 8192 x 5120 N=7 19.4 -> 16.5, 28672 x 8192 N=7 53.3 ->
+//    51.9); at 5120 values also six columns from 512 tiles and five from 864
+//    (13824 x 5120 N=5 21.7 -> 21.0, 28672 x 5120 N=5 39.8 -> 33.3).  At 8192
+//    values five or six columns are slower (28672 x 8192 N=6 48.9 against
+//    51.4), and 4096 rows are slower everywhere.
+static bool use_mfma_q6(int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
-    return (N == 8 && tiles >= 896) || (N >= 6 && tiles >= 2048);
+    if (K <= 4096) return (N == 8 && tiles >= 896) || (N >= 6 && tiles >= 2048);
+    if (N >= 7 && tiles >= 512) return true;
+    return K <= 5120 && ((N == 6 && tiles >= 512) || (N == 5 && tiles >= 864));
 }
 
 // The matrix-core kernel's geometry, as for Q4_K: one workgroup per CU (at
@@ -150,7 +160,7 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
     const int okern = g_ovr_kernel.load();
-    if (fused == kFusedNone && mats == 1 && (okern == 4 || (okern == 0 && use_mfma_q6(M, N)))) {
+    if (fused == kFusedNone && mats == 1 && (okern == 4 || (okern == 0 && use_mfma_q6(M, N, K)))) {
         int mc = (int)N;
         while (mc > 1 && q6m_lds_bytes((int)K, mc, 16) > max_lds) mc = (mc + 1) / 2;
         if (q6m_lds_bytes((int)K, mc, 16) <= max_lds && (okern == 4 || mc == N))

@@ -31,6 +31,7 @@ SHAPES = [
     (4099, 1280, 2),    # 5 super-blocks per row
     (64, 16384, 4),     # 64 super-blocks per row
     (33000, 4096, 8),   # several rounds of tiles per workgroup
+    (4000, 8192, 7),    # 32 super-blocks per row, seven columns in one launch
 ]
 
 
@@ -147,11 +148,15 @@ def test_q6_mfma_result_independent_of_work_split(Q, O, gpu, M, K, N):
 
 def test_q6_automatic_choice(Q, gpu):
     """The automatic geometry takes the matrix-core kernel for eight columns
-    from 896 row tiles and six or more from 2048, the tile kernel elsewhere;
+    from 896 row tiles and six or more from 2048 on rows of up to 4096
+    values, seven or eight from 512 tiles on longer rows (and at 5120 values
+    six from 512 and five from 864), the tile kernel elsewhere;
     the Q6_K workloads' eight-column launches of 32768 and 128256 rows (whose
     sums and outputs the workload tests check) are matrix-core launches."""
     t6 = Q.GGML_TYPE_Q6_K
     for M, K, N, kern in [(128256, 4096, 8, 4), (32768, 4096, 8, 4), (14336, 4096, 8, 4), (65536, 4096, 6, 4),
                           (32768, 4096, 6, 4), (128256, 4096, 4, 1), (14336, 4096, 6, 1), (4096, 14336, 8, 1),
-                          (4096, 4096, 8, 1), (128256, 4096, 1, 1)]:
+                          (4096, 4096, 8, 1), (128256, 4096, 1, 1), (28672, 3584, 8, 4), (13824, 3584, 8, 1),
+                          (8192, 8192, 8, 4), (8192, 8192, 7, 4), (28672, 8192, 6, 1), (8192, 5120, 6, 4),
+                          (13824, 5120, 5, 4), (8192, 5120, 5, 1), (4096, 8192, 8, 1)]:
         assert Q.geometry(K, M, N, t6)["kernel"] == kern, (M, K, N)
