@@ -389,9 +389,16 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // 128256 x 4096 N=8 96 -> 83 us, N=4 63.6 -> 59.3 us, 28672 x 4096 N=4
     // 20.6 -> 16.9 us, 14336 x 4096 N=8 16.5 -> 15.8 us; N=3..5 at
     // 14336 x 4096 (56 rows) even to 3 % slower.
+    // From 64 rows per workgroup at three to five columns (18944 x 4096 N=3
+    // 13.4 -> 11.6 us, N=4 14.9 -> 13.1; 18944 x 3584 N=4 14.4 -> 12.4).
     const int64_t rows_per_wg = (M + g.grid - 1) / g.grid;
-    if (N >= 3 && K <= 16 * kQK && !fused && mats == 1 && (rows_per_wg >= 96 || (N >= 6 && rows_per_wg >= 48)))
+    if (N >= 3 && K <= 16 * kQK && !fused && mats == 1 && (rows_per_wg >= 64 || (N >= 6 && rows_per_wg >= 48)))
         g.waves = 8;
+    // Two columns with rows of two groups and at most 32 rows per workgroup:
+    // 8 waves (5120 x 5120 7.67 -> 7.02 us, 5120 x 8192 9.2 -> 8.8, 8192 x
+    // 5120 8.8 -> 8.2, 8192 x 8192 10.9 -> 10.5; 56 rows and more 1-2 %
+    // slower that way).
+    if (N == 2 && G == 2 && !fused && mats == 1 && rows_per_wg <= 32) g.waves = 8;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;  // the instantiated sizes
     g.slots = steps_per_wg >= 4 * (int64_t)g.waves ? 2 : 1;
     if (two_per_cu) g.slots = 1;
