@@ -379,8 +379,12 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // 3584 x 3584 4.38 -> 4.24 us, and 4 steps 6 % slower); two groups in
     // flight per wave once a wave has four or more to stream, else one (a
     // second slot would mostly run past the wave's rows).  Measured on MI355X.
+    // Small products with an activation of 32768 or more values (all
+    // columns) take 16 waves too: they halve the quantisation rounds that
+    // dominate them (1024 x 8192 N=4 9.44 -> 8.30 us, N=8 13.24 -> 11.52;
+    // 1024 x 4096 N=8 7.60 -> 7.31; at 28672 values 1 % slower).
     const int64_t steps_per_wg = (M + g.grid - 1) / g.grid * ((K / kQK + 15) / 16);
-    g.waves = steps_per_wg >= 12 && !four_per_cu ? 16 : 8;
+    g.waves = (steps_per_wg >= 12 || N * K >= 32768) && !four_per_cu ? 16 : 8;
     // Three or more columns with rows of one group and >= 96 rows per
     // workgroup (>= 48 from six columns on): 8 waves, whose registers hold
     // the lane's activation slices of every column, so the step loop reads

@@ -188,8 +188,16 @@ def test_dense_layout_partial_groups(Q, O, gpu, M, K, waves):
     1, 5, 7 and 8 blocks here), at 8 and 16 waves: outputs of the in-kernel
     and the pre-quantised routes against the oracle, and the launch's int32
     group sums exact."""
-    import torch
     N = 8
+    Q.set_geometry_override(waves_per_wg=waves)  # both dense-kernel sizes
+    try:
+        _dense_partial(Q, O, gpu, M, K, N, waves)
+    finally:
+        Q.set_geometry_override()
+
+
+def _dense_partial(Q, O, gpu, M, K, N, waves):
+    import torch
     geo = Q.geometry(K, M, N, wtype=Q.GGML_TYPE_Q6_K)
     assert geo["cols_per_launch"] == N and geo["waves_per_wg"] == waves
     # K bytes of q8 per column, d8 and offset terms, a 256-byte ring per wave
