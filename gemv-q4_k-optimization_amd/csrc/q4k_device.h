@@ -349,6 +349,16 @@ __host__ __device__ constexpr int early_slots(int pro, int slots) {
     return pro == 0 ? (slots < 2 ? slots : 2) : (pro == 2 ? slots : (pro == 3 ? 1 : 0));
 }
 
+// Rounds past the first PRE that finish() loads together (its CHUNK).  Two
+// halve the memory round trips of the several-column launches whose
+// activation outgrows the rounds issued ahead (4096 x 14336 N=8 24.1 ->
+// 22.6 us, 1024 x 8192 N=8 11.4 -> 10.8 on MI355X); chunks of 4 and 8
+// measured no better.  One-column kernels pass 1, one round at a time: the
+// chunk's registers would take them past the 64 that let two 16-wave (or
+// four 8-wave) workgroups share a CU, and one column rarely has rounds
+// left over.
+constexpr int kFinishRounds = 2;
+
 template <int LPB, int PRE>
 struct ActStage {
     float v[PRE][32 / LPB];
@@ -471,7 +481,7 @@ __device__ __forceinline__ void stage_f32_issue(const float *__restrict__ x, int
     }
 }
 
-template <int LAYOUT, int LPB, int NT, int PRE>
+template <int LAYOUT, int LPB, int NT, int CHUNK = kFinishRounds, int PRE>
 __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, int64_t ldx, int K,
                                                  int ncols, bool vec_ok, const FastDiv &fd,
                                                  const ActStage<LPB, PRE> &st, int qcol, int8_t *q8s,
@@ -490,12 +500,31 @@ __device__ __forceinline__ void stage_f32_finish(const float *__restrict__ x, in
                                              sq_out);
         }
     }
-    for (int qb = (int)(threadIdx.x / LPB) + PRE * step; qb < total; qb += step) {
-        const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
-        const int b = qb - c * nblk;
-        float v[V];
-        load_xv<V>(x + c * ldx + b * 32 + e * V, vec_ok, v);
-        quantize_block_part<LAYOUT, LPB>(v, e, qcol, c, b, qb, total, nblk, q8s, aux, sq_out);
+    // Further rounds a chunk at a time: all their loads first, then their
+    // quantisation, so a chunk costs one memory round trip rather than one
+    // per round.  A round past every block of the wave's lanes is not
+    // loaded (q0w, the wave's first active lane, holds its smallest block);
+    // in the others, lanes past the end re-read the last block.
+    constexpr int kChunk = CHUNK;
+    for (int q0 = (int)(threadIdx.x / LPB) + PRE * step; q0 < total; q0 += kChunk * step) {
+        const int q0w = __builtin_amdgcn_readfirstlane(q0);
+        float v[kChunk][V];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            if (j > 0 && q0w + j * step >= total) break;
+            const int qb = min(q0 + j * step, total - 1);
+            const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
+            load_xv<V>(x + c * ldx + (qb - c * nblk) * 32 + e * V, vec_ok, v[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            const int qb = q0 + j * step;
+            if (qb < total) {
+                const int c = ncols == 1 ? 0 : (int)fastdiv((uint32_t)qb, fd);
+                quantize_block_part<LAYOUT, LPB>(v[j], e, qcol, c, qb - c * nblk, qb, total, nblk, q8s, aux,
+                                                 sq_out);
+            }
+        }
     }
 }
 
@@ -563,7 +592,7 @@ __device__ __forceinline__ void store_q81_part(uint32_t w0, uint32_t w1, uint32_
     if (sq_out && quarter == 0) sq_out[qb] = fsum;
 }
 
-template <int LAYOUT, int NT, int PRE>
+template <int LAYOUT, int NT, int CHUNK = kFinishRounds, int PRE>
 __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, int64_t stride_col_y,
                                                  int K, int ncols, const FastDiv &fd,
                                                  const Q81Stage<PRE> &st, int qcol, int8_t *q8s,
@@ -581,14 +610,30 @@ __device__ __forceinline__ void stage_q81_finish(const uint8_t *__restrict__ y, 
                                    total, nblk, q8s, aux, sq_out);
         }
     }
-    for (int qb = (threadIdx.x >> 2) + PRE * step; qb < total; qb += step) {
-        const int c = (int)fastdiv((uint32_t)qb, fd);
-        const int b = qb - c * nblk;
-        const uint8_t *blk = y + ((int64_t)c * stride_col_y + b) * kQ81Bytes;
-        const uint32_t w0 = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
-        const uint32_t w1 = *reinterpret_cast<const uint32_t *>(blk + 8 + quarter * 8);
-        store_q81_part<LAYOUT>(w0, w1, *reinterpret_cast<const uint32_t *>(blk), quarter, qcol, c, b, qb,
-                               total, nblk, q8s, aux, sq_out);
+    // further rounds CHUNK at a time, loads first, as in stage_f32_finish
+    constexpr int kChunk = CHUNK;
+    for (int q0 = (threadIdx.x >> 2) + PRE * step; q0 < total; q0 += kChunk * step) {
+        const int q0w = __builtin_amdgcn_readfirstlane(q0);
+        uint32_t w[kChunk][2], ds[kChunk];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            if (j > 0 && q0w + j * step >= total) break;
+            const int qb = min(q0 + j * step, total - 1);
+            const int c = (int)fastdiv((uint32_t)qb, fd);
+            const uint8_t *blk = y + ((int64_t)c * stride_col_y + (qb - c * nblk)) * kQ81Bytes;
+            w[j][0] = *reinterpret_cast<const uint32_t *>(blk + 4 + quarter * 8);
+            w[j][1] = *reinterpret_cast<const uint32_t *>(blk + 8 + quarter * 8);
+            ds[j] = *reinterpret_cast<const uint32_t *>(blk);
+        }
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            const int qb = q0 + j * step;
+            if (qb < total) {
+                const int c = (int)fastdiv((uint32_t)qb, fd);
+                store_q81_part<LAYOUT>(w[j][0], w[j][1], ds[j], quarter, qcol, c, qb - c * nblk, qb, total, nblk,
+                                       q8s, aux, sq_out);
+            }
+        }
     }
 }
 

@@ -325,11 +325,11 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
         }
     } else {
         if (p.x)
-            stage_f32_finish<kLayoutQ4K, kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs,
-                                                              p.qcol, q8s, dks, sq_out);
+            stage_f32_finish<kLayoutQ4K, kLPB, kWave * WAVES, NC == 1 ? 1 : kFinishRounds>(
+                p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks, sq_out);
         else
-            stage_q81_finish<kLayoutQ4K, kWave * WAVES>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s,
-                                                        dks, sq_out);
+            stage_q81_finish<kLayoutQ4K, kWave * WAVES, NC == 1 ? 1 : kFinishRounds>(
+                p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks, sq_out);
         __syncthreads();
         if (remaining == 0) return;  // no barrier below this point
 #pragma unroll
@@ -501,10 +501,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_bpl_kernel(Q4K_GEMV_KER
     if (active) load_pass(p, pa, rr, kb, lane_on, wa);
     if (vb) load_pass(p, pb, rr, kb, lane_on, wb);
     if (p.x)
-        stage_f32_finish<kLayoutLinear, 8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s,
+        stage_f32_finish<kLayoutLinear, 8, kWave * WAVES, 1>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s,
                                                           dks, sq_out);
     else
-        stage_q81_finish<kLayoutLinear, kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks,
+        stage_q81_finish<kLayoutLinear, kWave * WAVES, 1>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks,
                                                        sq_out);
     __syncthreads();
     if (!active) return;  // no barrier below this point
@@ -626,8 +626,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_blk_kernel(Q4K_GEMV_KER
     u32x4 wa[9], wb[9];
     if (active) load_pass_coalesced(p, pa, po, wa);
     if (vb) load_pass_coalesced(p, pb, po, wb);
-    if (p.x) stage_f32_finish<kLayoutLinear, 8, kWave * WAVES>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
-    else stage_q81_finish<kLayoutLinear, kWave * WAVES>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
+    if (p.x) stage_f32_finish<kLayoutLinear, 8, kWave * WAVES, 1>(p.x, p.ldx, p.K, 1, p.vec_ok != 0, p.nblk32, xs, p.K, q8s, dks);
+    else stage_q81_finish<kLayoutLinear, kWave * WAVES, 1>(p.y, p.stride_col_y, p.K, 1, p.nblk32, ys, p.K, q8s, dks);
     __syncthreads();
     if (!active) return;  // no barrier below this point
 
