@@ -295,7 +295,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
-    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * ring_floats(NC), wr.beg, wr.end, 0, 0};
+    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * p.ring_cap, wr.beg, wr.end, 0, 0, p.ring_cap};
 
     // Rows of two groups (4096 < K <= 8192), one column and row, both slots
     // loaded early (the gate-weight variant would spill registers): each

@@ -46,6 +46,7 @@ struct GemvParams {
     int rows_base;           // tile kernel: each workgroup owns rows_base rows,
     int rows_extra;          //   the first rows_extra workgroups one more
     int ring_off;            // tile kernel: LDS byte offset of the per-wave result rings
+    int ring_cap;            //   and their floats per wave (ring_cap())
     FastDiv nblk32;          // division by K/32 (Q8_1 blocks per column)
     // fused epilogue (one column): gate weight rows (same layout as w), the
     // biases of the two products (indexed like dst) and the GLU op
@@ -212,12 +213,22 @@ __device__ __forceinline__ float glu_apply(int op, float up, float g) {
 // workgroup's 160 KB of LDS.
 __host__ __device__ constexpr int ring_floats(int nc) { return nc <= 4 ? 256 : 64; }
 
+// The ring of a launch: ring_floats(nc) floats per wave, or 64 where those
+// rings and an activation of act bytes would not fit max_lds bytes (up to
+// four columns of ~26,000 values or more: Q6_K 8192 x 28672 at N=4 then
+// runs in one launch instead of two).  A ring holds at least one step's
+// R * NC <= 32 entries.
+inline int ring_cap(int act, int nc, int waves, int max_lds) {
+    return act + waves * ring_floats(nc) * 4 <= max_lds ? ring_floats(nc) : 64;
+}
+
 struct ResultRing {
-    float *buf;   // this wave's ring_floats(NC) floats of LDS
+    float *buf;   // this wave's cap floats of LDS
     int beg;      // first row of the wave
     int end;      // one past its last row
     int base;     // entries already written out
     int n;        // entries buffered
+    int cap;      // floats in buf
 };
 
 // Writes the buffered entries to dst (entries of rows >= end are dropped),
@@ -339,7 +350,7 @@ __device__ __forceinline__ void tile_to_ring(const GemvParams &p, int lane, floa
     rr.n += R * NC;
     // rare (a wave's rows x NC above the ring): global stores inside the
     // loop make the compiler's load waits conservative
-    if (rr.n + R * NC > ring_floats(NC)) ring_flush<NC, EPI>(p, lane, rr);
+    if (rr.n + R * NC > rr.cap) ring_flush<NC, EPI>(p, lane, rr);
 }
 
 }  // namespace q4k

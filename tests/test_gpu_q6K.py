@@ -264,3 +264,37 @@ def test_production_kernel_sums(Q, O, gpu, M, K, N):
         got = s16[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
         assert np.array_equal(got, ref["s16"]), f"{M}x{K} N={N}: group sums differ"
     print(f"[sums] Q6_K {M}x{K} N={N} {Q.geometry(K, M, N, Q.GGML_TYPE_Q6_K)}: exact", flush=True)
+
+
+@pytest.mark.parametrize("wtype,M,K,N", [(14, 200, 28672, 4), (14, 600, 28672, 4), (12, 600, 40960, 3)])
+def test_small_result_ring_for_long_rows(Q, O, gpu, wtype, M, K, N):
+    """Columns this long fit the LDS only with 64-float result rings (Q6_K:
+    4 x 28672 values staged in 157,696 bytes; Q4_K: 3 x 40960 in 153,600),
+    so the product runs in one launch instead of two.  With one workgroup
+    (an override) each wave owns 12-38 rows, i.e. 50-150 ring entries, and
+    the ring flushes mid-stream.  Outputs against the oracle, and the
+    workspace (pre-quantised) route bit for bit."""
+    import torch
+    geo = Q.geometry(K, M, N, wtype=wtype)
+    assert geo["cols_per_launch"] == N and geo["kernel"] == 1
+    if wtype == Q.GGML_TYPE_Q6_K:
+        wq, x = inputs(Q, M, K, N, seed=21)
+        ref = O.gemv_q6K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
+        act = N * (K + K // 8 + K // 4)
+    else:
+        wq = Q.quantize_rows_q4_K(_common.weights(M, K, 21), nthreads=16)
+        x = _common.activations(N, K, 21)
+        ref = O.gemv_q4K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
+        act = N * (K + K // 4)
+    assert geo["lds_bytes"] == act + geo["waves_per_wg"] * 64 * 4
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    ws = torch.empty(Q.q8_1_bytes(K, N), dtype=torch.uint8, device=gpu)
+    for wgs in (0, 1):
+        Q.set_geometry_override(workgroups=wgs)
+        try:
+            y = Q.mul_mat_vec_q(wd, K, xd, wtype=wtype).cpu().numpy()
+            y2 = Q.mul_mat_vec_q(wd, K, xd, workspace=ws, wtype=wtype).cpu().numpy()
+        finally:
+            Q.set_geometry_override()
+        _common.assert_within_tolerance(O, y, ref, f"small ring {M}x{K} N={N} wgs={wgs}")
+        assert np.array_equal(y, y2)
