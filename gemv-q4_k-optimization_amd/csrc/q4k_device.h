@@ -353,10 +353,12 @@ __host__ __device__ constexpr int early_slots(int pro, int slots) {
 // halve the memory round trips of the several-column launches whose
 // activation outgrows the rounds issued ahead (4096 x 14336 N=8 24.1 ->
 // 22.6 us, 1024 x 8192 N=8 11.4 -> 10.8 on MI355X); chunks of 4 and 8
-// measured no better.  One-column kernels pass 1, one round at a time: the
-// chunk's registers would take them past the 64 that let two 16-wave (or
-// four 8-wave) workgroups share a CU, and one column rarely has rounds
-// left over.
+// measured no better.  Kernels of up to three columns pass 1, one round at
+// a time: they rarely have rounds left over; with one column the chunk's
+// registers would take the kernel past the 64 that let two 16-wave (or four
+// 8-wave) workgroups share a CU, and three columns measured 1-2 % faster
+// without it (4096 x 4096 N=3 6.12 -> 5.99 us, 14336 x 4096 N=3 10.39 ->
+// 10.21).
 constexpr int kFinishRounds = 2;
 
 template <int LPB, int PRE>

@@ -325,10 +325,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
         }
     } else {
         if (p.x)
-            stage_f32_finish<kLayoutQ4K, kLPB, kWave * WAVES, NC == 1 ? 1 : kFinishRounds>(
+            stage_f32_finish<kLayoutQ4K, kLPB, kWave * WAVES, NC < 4 ? 1 : kFinishRounds>(
                 p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, dks, sq_out);
         else
-            stage_q81_finish<kLayoutQ4K, kWave * WAVES, NC == 1 ? 1 : kFinishRounds>(
+            stage_q81_finish<kLayoutQ4K, kWave * WAVES, NC < 4 ? 1 : kFinishRounds>(
                 p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, dks, sq_out);
         __syncthreads();
         if (remaining == 0) return;  // no barrier below this point

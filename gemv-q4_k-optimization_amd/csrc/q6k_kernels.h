@@ -329,10 +329,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
 #pragma unroll
     for (int k = 0; k < kEarly; ++k) q6_load_step<R>(p, ln, ws, st[k], w[k]);
     if (p.x)
-        stage_f32_finish<kLayout, kLPB, kWave * WAVES, NC == 1 ? 1 : kFinishRounds>(
+        stage_f32_finish<kLayout, kLPB, kWave * WAVES, NC < 4 ? 1 : kFinishRounds>(
             p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, p.qcol, q8s, aux);
     else
-        stage_q81_finish<kLayout, kWave * WAVES, NC == 1 ? 1 : kFinishRounds>(
+        stage_q81_finish<kLayout, kWave * WAVES, NC < 4 ? 1 : kFinishRounds>(
             p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, p.qcol, q8s, aux);
     __syncthreads();
     if (remaining == 0) return;  // no barrier below this point

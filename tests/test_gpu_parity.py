@@ -345,7 +345,8 @@ def test_workspace_route_for_long_columns(Q, O, gpu, wtype, M, K, N):
     small) the GEMV quantises in-launch.  Both give the same bits, within
     the oracle's tolerance.  The activations outgrow the four staging rounds
     a 16-wave workgroup issues ahead by 1.25 (N=3), 3 (N=2, N=4) and 4 (N=8)
-    rounds, which the staging loads two rounds at a time."""
+    rounds; from four columns on the staging loads them two rounds at a
+    time."""
     import torch
     if wtype == 12:
         wq, x = inputs(Q, M, K, N, seed=8)
