@@ -222,9 +222,9 @@ static int bpl_rows_per_pass(int64_t nb) {
 // kernels) followed by the per-32-value (d8, d8*sum q8) pairs.
 static int lds_bytes(int K, int nc) { return nc * (q8_col_bytes(K) + K / 4); }
 // The tile kernel adds a result ring per wave after the activation.
-static int tile_lds_bytes(int K, int nc, int waves, int max_lds) {
+static int tile_lds_bytes(int K, int nc, int waves) {
     const int act = lds_bytes(K, nc);
-    return act + waves * ring_cap(act, nc, waves, max_lds) * 4;
+    return act + waves * ring_cap(act, nc, waves) * 4;
 }
 static int lds_bytes_linear(int K) { return K + K / 4; }
 
@@ -309,9 +309,9 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
     int nc = (int)N;
-    while (nc > 1 && tile_lds_bytes((int)K, nc, 16, max_lds) > max_lds) nc = (nc + 1) / 2;
+    while (nc > 1 && tile_lds_bytes((int)K, nc, 16) > max_lds) nc = (nc + 1) / 2;
     g.nc_chunk = nc;
-    g.lds = tile_lds_bytes((int)K, nc, 16, max_lds);
+    g.lds = tile_lds_bytes((int)K, nc, 16);
     const int orows = g_ovr_rows.load(), owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load();
     const int okern = g_ovr_kernel.load();
     const int rpw = bpl_rows_per_pass(K / kQK);
@@ -453,7 +453,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // rows per workgroup (the kernel splits each share over its waves)
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
-    g.lds = tile_lds_bytes((int)K, nc, g.waves, max_lds);
+    g.lds = tile_lds_bytes((int)K, nc, g.waves);
     g.lds_launch = g.lds;
     if (owgs == 0 && !four_per_cu && !two_per_cu && !glu_two && g.lds_launch <= max_lds / 2)
         g.lds_launch = max_lds / 2 + 256;
@@ -603,14 +603,12 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
         p.ring_off = lds_bytes(p.K, nc);
-        p.ring_cap = ring_cap(p.ring_off, nc, geo.waves, di->max_lds);
     } else if (batch) {
         if (geo.R != 1) return Q4K_EINVAL;
         fn = gemv_kernel_batch(nc, geo.waves, geo.prologue, geo.slots);
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
         p.ring_off = lds_bytes(p.K, nc);
-        p.ring_cap = ring_cap(p.ring_off, nc, geo.waves, di->max_lds);
     } else if (geo.mfma) {
         fn = p.sums ? q4k_mfma_sums_kernel(nc, geo.waves) : mfma_kernel_for(nc, geo.waves);
         p.rows_base = geo.rows_base;
@@ -637,7 +635,6 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
         p.ring_off = lds_bytes(p.K, nc);
-        p.ring_cap = ring_cap(p.ring_off, nc, geo.waves, di->max_lds);
     }
     if (!fn) return Q4K_EINVAL;
     int st = ensure_lds(di, fn, geo.lds_launch);
@@ -696,7 +693,7 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
         if (!geo.bpl) {
-            g2.lds = geo.mfma ? mfma_lds_bytes((int)ne00, nc, geo.waves) : tile_lds_bytes((int)ne00, nc, geo.waves, di->max_lds);
+            g2.lds = geo.mfma ? mfma_lds_bytes((int)ne00, nc, geo.waves) : tile_lds_bytes((int)ne00, nc, geo.waves);
             if (g2.lds_launch < g2.lds) g2.lds_launch = g2.lds;
         }
         GemvParams p{};

@@ -295,7 +295,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_kernel(Q4K_GEMV_KERNEL_
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
-    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * p.ring_cap, wr.beg, wr.end, 0, 0, p.ring_cap};
+    const int cap = ring_cap(p.ring_off, NC, WAVES);
+    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * cap, wr.beg, wr.end, 0, 0, cap};
 
     // Rows of two groups (4096 < K <= 8192), one column and row, both slots
     // loaded early (the gate-weight variant would spill registers): each

@@ -46,7 +46,6 @@ struct GemvParams {
     int rows_base;           // tile kernel: each workgroup owns rows_base rows,
     int rows_extra;          //   the first rows_extra workgroups one more
     int ring_off;            // tile kernel: LDS byte offset of the per-wave result rings
-    int ring_cap;            //   and their floats per wave (ring_cap())
     FastDiv nblk32;          // division by K/32 (Q8_1 blocks per column)
     // fused epilogue (one column): gate weight rows (same layout as w), the
     // biases of the two products (indexed like dst) and the GLU op
@@ -213,13 +212,18 @@ __device__ __forceinline__ float glu_apply(int op, float up, float g) {
 // workgroup's 160 KB of LDS.
 __host__ __device__ constexpr int ring_floats(int nc) { return nc <= 4 ? 256 : 64; }
 
-// The ring of a launch: ring_floats(nc) floats per wave, or 64 where those
-// rings and an activation of act bytes would not fit max_lds bytes (up to
-// four columns of ~26,000 values or more: Q6_K 8192 x 28672 at N=4 then
-// runs in one launch instead of two).  A ring holds at least one step's
-// R * NC <= 32 entries.
-inline int ring_cap(int act, int nc, int waves, int max_lds) {
-    return act + waves * ring_floats(nc) * 4 <= max_lds ? ring_floats(nc) : 64;
+// The ring of a launch: ring_floats(nc) floats per wave, or, from three
+// columns on, 64 where those rings and an activation of act bytes would not
+// fit a gfx950 workgroup's 160 KB of LDS (three or four columns of ~26,000
+// values or more: Q6_K 8192 x 28672 at N=4 then runs in one launch instead
+// of two).  A ring holds at least one step's R * NC <= 32 entries.  The
+// kernels derive it from the ring offset (the activation's size), which they
+// read anyway.  One and two columns keep the compile-time size: with the
+// size a run-time value the fused Q6_K gate/up launch measured 4 % slower
+// (14336 x 4096: 20.7 -> 21.6 us), and their rings always fit.
+constexpr int kLdsBytes = 160 * 1024;
+__host__ __device__ constexpr int ring_cap(int act, int nc, int waves) {
+    return nc <= 2 || act + waves * ring_floats(nc) * 4 <= kLdsBytes ? ring_floats(nc) : 64;
 }
 
 struct ResultRing {

@@ -68,9 +68,9 @@ __global__ __launch_bounds__(256) void q6_group_sums_kernel(Q6SumsParams p) {
 // 32-value block (K/8 bytes per column), the -32*sum(q8) terms per 16 values
 // (K/4 bytes per column), then a result ring per wave.
 static int q6_act_bytes(int K, int nc, bool dense) { return nc * (q8_col_bytes(K, dense) + K / 8 + K / 4); }
-static int q6_tile_lds_bytes(int K, int nc, int waves, bool dense, int max_lds) {
+static int q6_tile_lds_bytes(int K, int nc, int waves, bool dense) {
     const int act = q6_act_bytes(K, nc, dense);
-    return act + waves * ring_cap(act, nc, waves, max_lds) * 4;
+    return act + waves * ring_cap(act, nc, waves) * 4;
 }
 
 // Column counts with dense-layout kernels: from 5 columns up, where halving
@@ -170,8 +170,8 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     int nc = (int)N;
     // Measured on MI355X: 4096 x 14336 at 8 columns, one dense launch 26.8 us
     // against two padded 4-column launches 34.5 us.
-    while (nc > 1 && q6_tile_lds_bytes((int)K, nc, 16, false, max_lds) > max_lds) {
-        if (nc >= kDenseMinCols && q6_tile_lds_bytes((int)K, nc, 16, true, max_lds) <= max_lds) {
+    while (nc > 1 && q6_tile_lds_bytes((int)K, nc, 16, false) > max_lds) {
+        if (nc >= kDenseMinCols && q6_tile_lds_bytes((int)K, nc, 16, true) <= max_lds) {
             g.dense = true;
             break;
         }
@@ -204,7 +204,7 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     if (g.dense) g.slots = 1;  // the dense kernels are one-slot
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
-    g.lds = q6_tile_lds_bytes((int)K, nc, g.waves, g.dense, max_lds);
+    g.lds = q6_tile_lds_bytes((int)K, nc, g.waves, g.dense);
     g.lds_launch = g.lds;
     if (owgs == 0 && g.lds_launch <= max_lds / 2) g.lds_launch = max_lds / 2 + 256;
     const bool pro0_ok = (int64_t)nc * (K / 32) <= (int64_t)stage_capacity(stage_lpb(nc), g.waves * kWave, nc);
@@ -324,7 +324,7 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         const bool dense = geo.dense && nc >= kDenseMinCols;
         int lds_launch = geo.lds_launch;
         const int lds = geo.mfma ? q6m_lds_bytes((int)ne00, nc, geo.waves)
-                                 : q6_tile_lds_bytes((int)ne00, nc, geo.waves, dense, di->max_lds);
+                                 : q6_tile_lds_bytes((int)ne00, nc, geo.waves, dense);
         if (lds > di->max_lds) return Q4K_EUNSUPPORTED;
         if (lds_launch < lds) lds_launch = lds;
         GemvParams p{};
@@ -345,7 +345,6 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
         p.ring_off = q6_act_bytes(p.K, nc, dense);
-        p.ring_cap = ring_cap(p.ring_off, nc, geo.waves, di->max_lds);
         p.nblk32 = fastdiv_init((uint32_t)(ne00 / 32));
         if (fused) {
             p.gate = ep->gate;

@@ -344,7 +344,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_kernel(Q4K_GEMV_KERNEL_
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
-    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * p.ring_cap, wr.beg, wr.end, 0, 0, p.ring_cap};
+    const int cap = ring_cap(p.ring_off, NC, WAVES);
+    ResultRing rr{reinterpret_cast<float *>(lds + p.ring_off) + wave * cap, wr.beg, wr.end, 0, 0, cap};
 
     // (one column at 16 waves, eight at 8 waves: wider variants would spill
     // registers)
