@@ -20,6 +20,7 @@
 #include "../../include/q4k_gemv.h"
 #include "q4k_runtime.h"
 #include "q4k_gemv_kernels.h"
+#include "q4k_ksplit.h"
 #include "q4k_mfma.h"
 #include "q4k_tile.h"
 
@@ -196,6 +197,7 @@ struct Geometry {
     int mfma = 0;       // 1: matrix-core kernel (tiles of 16 rows; rows_base/rows_extra count tiles)
     int ks = 1;         // matrix-core kernel: waves sharing one tile
     int segs = 1;       // matrix-core kernel: summation segments of a row
+    int ksplit = 0;     // K-split kernel: super-blocks per wave and group (0: another kernel)
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
@@ -291,6 +293,84 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
     return g;
 }
 
+// The K-split kernel: rows_per_step TR = 16 / SBW rows per wave step (1, 4,
+// 8, 16; SBW super-blocks per wave and group), waves per workgroup
+// (whole teams of TR waves), workgroups (default one per CU) and row tiles
+// in flight per wave (1 or 2).
+static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t M, int rows_per_step, int waves, int wgs,
+                                     int slots) {
+    Geometry g;
+    const int cus = di.cus > 0 ? di.cus : 1;
+    const int tr = rows_per_step == 1 || rows_per_step == 4 || rows_per_step == 8 || rows_per_step == 16
+                       ? rows_per_step
+                       : 16;
+    g.ksplit = 16 / tr;
+    g.R = tr;
+    g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
+    if (g.waves < tr) g.waves = tr;
+    g.slots = slots == 2 ? 2 : 1;
+    int64_t grid = wgs > 0 ? wgs : cus;
+    if (grid > M) grid = M;
+    g.grid = grid < 1 ? 1 : (int)grid;
+    g.rows_base = (int)(M / g.grid);
+    g.rows_extra = (int)(M % g.grid);
+    g.lds = ksplit_lds_bytes(g.rows_base + (g.rows_extra ? 1 : 0), g.ksplit);
+    g.lds_launch = g.lds;
+    g.nc_chunk = 1;
+    return g;
+}
+
+// The K-split kernel's automatic launch shape for one aligned F32 column of
+// K = 4096 or 8192 values, one workgroup per CU; false where the tile kernel
+// measured faster.  rho = rows per CU.  Measured on MI355X (us, interleaved
+// graph timings of 200 calls; K-split against the tile kernel):
+//  - K = 4096: up to 4 rows per CU, 4 rows per step and 4 waves (1024 x
+//    4096 2.87 against 3.14); up to 8, 8 rows and 8 waves (2048 x 4096 3.19
+//    against 3.36).  Beyond, 8 rows per step: with an odd number of 8-row
+//    tiles per CU up to 64 rows, two 8-wave teams with one tile in flight
+//    (4608 x 4096 4.33 against 4.59, 6144 x 4096 4.69 / 5.02, 13312 x 4096
+//    7.39 / 7.60, 14336 x 4096 7.71 / 7.80), otherwise one 8-wave team with
+//    two tiles in flight (4096 x 4096 3.98 / 4.37, 7168 x 4096 5.14 / 5.39,
+//    12288 x 4096 6.90 / 7.28, 16384 x 4096 8.44 / 8.71, 28672 x 4096
+//    13.03 / 13.62, 128256 x 4096 50.30 / 50.79 on the block-per-lane
+//    kernel); the two shapes swap at the other parity (14336 x 4096: 7.97
+//    against 7.71; 16384 x 4096: 8.45 against 8.44).  160 to 400 rows per
+//    CU stay on the tile kernel's four 8-wave workgroups per CU (65536 x
+//    4096 26.50 against 26.71-26.84).
+//  - K = 8192: the same up to 8 rows per CU (1024 x 8192 3.95 against 4.58,
+//    2048 x 8192 4.38 / 5.03), then 4 rows per step, 4 waves and two tiles
+//    in flight (4096 x 8192 5.51 / 5.87, 14336 x 8192 12.91 / 13.45, 28672 x
+//    8192 23.33 / 24.27).
+static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
+    const int64_t rho = (M + cus - 1) / cus;
+    slots = 1;
+    if (rho <= 4) {
+        tr = 4;
+        waves = 4;
+        return true;
+    }
+    if (rho <= 8) {
+        tr = 8;
+        waves = 8;
+        return true;
+    }
+    if (K == 8192) {
+        tr = 4;
+        waves = 4;
+        slots = 2;
+        return true;
+    }
+    if (rho > 160 && rho <= 400) return false;
+    tr = 8;
+    if (rho <= 64 && ((rho + 7) / 8) % 2 == 1) {
+        waves = 16;
+    } else {
+        waves = 8;
+        slots = 2;
+    }
+    return true;
+}
+
 // Launch geometry for an (M, K, N) product.
 //  tile kernel: one workgroup per CU (requesting just over half the CU's LDS
 //    keeps a second one away), 8 or 16 waves, the M rows split evenly over
@@ -304,7 +384,7 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
 //    a gate each tile pairs one row of both weights (R = 2, one or two
 //    groups in flight).
 static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int fused = 0,
-                              int64_t mats = 1) {
+                              int64_t mats = 1, bool f32_vec = true) {
     Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
@@ -315,6 +395,17 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const int orows = g_ovr_rows.load(), owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load();
     const int okern = g_ovr_kernel.load();
     const int rpw = bpl_rows_per_pass(K / kQK);
+    // K-split kernel: one 16-byte aligned F32 column of 4096- or 8192-value
+    // rows (the tile kernel, whose outputs are the same bits, takes the rest)
+    const bool ks_ok = N == 1 && !fused && mats == 1 && f32_vec && (K == 4096 || K == 8192);
+    if (ks_ok && okern == 5) return pick_geometry_ksplit(di, M, orows, owaves, owgs, g_ovr_slots.load());
+    if (ks_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
+        int tr = 0, kw = 0, ks = 0;
+        if (ksplit_auto(K, M, di.cus > 0 ? di.cus : 1, tr, kw, ks)) {
+            const int os = g_ovr_slots.load();
+            return pick_geometry_ksplit(di, M, tr, kw, 0, os == 1 || os == 2 ? os : ks);
+        }
+    }
     if (N == 1 && rpw > 0 && okern == 3 && !fused && mats == 1) {
         // block kernel: ~2 waves per SIMD; activation + one 9216-byte LDS
         // slot per wave
@@ -330,15 +421,13 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         g.lds_launch = g.lds + g.waves * kSlotBytes;
         return g;
     }
-    // Large single-column products with 4096-value rows stream long enough
-    // for the block-per-lane kernel's lower instruction count to win; the
-    // tile kernel does better on everything else.  Measured on MI355X (tile
-    // against block-per-lane, us): 32768 x 4096 15.27 / 16.28, 65536 x 4096
-    // 26.66 / 27.45, 98304 x 4096 38.93 / 39.51, 128256 x 4096 50.90 /
-    // 50.70, 151936 x 4096 59.64 / 59.56, 256000 x 4096 100.53 / 99.39.
+    // The block-per-lane kernel (override 2) measured 0.2-1 % faster than
+    // the tile kernel on one column of >= 256 MB of 4096-value rows (128256
+    // x 4096 50.70 against 50.90 us), but sums in another order; it is not
+    // chosen automatically, so the pre-quantised route (tile kernel) gives
+    // the F32 route's (K-split kernel's) bits there too.
     const int64_t weight_bytes = M * (K / kQK) * kBlockBytes;
-    const bool auto_bpl = okern == 0 && K == 4096 && weight_bytes >= (256ll << 20);
-    if (N == 1 && rpw > 0 && (okern == 2 || auto_bpl) && !fused && mats == 1) {
+    if (N == 1 && rpw > 0 && okern == 2 && !fused && mats == 1) {
         // ~173 VGPRs: two waves per SIMD; 4-wave workgroups, two per CU
         g.bpl = 1;
         g.rpw = rpw;
@@ -609,6 +698,12 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
         p.ring_off = lds_bytes(p.K, nc);
+    } else if (geo.ksplit) {
+        if (nc != 1 || !p.x || !p.vec_ok) return Q4K_EINVAL;
+        fn = p.sums ? q4k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
+                    : ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);
+        p.rows_base = geo.rows_base;
+        p.rows_extra = geo.rows_extra;
     } else if (geo.mfma) {
         fn = p.sums ? q4k_mfma_sums_kernel(nc, geo.waves) : mfma_kernel_for(nc, geo.waves);
         p.rows_base = geo.rows_base;
@@ -676,7 +771,8 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     if (fused && ncols != 1) return Q4K_EINVAL;
     if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
     const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
-    Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused, mats);
+    const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0;
+    Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused, mats, f32_vec);
     if (bl || fused) {  // the batched and fused variants: 1 or 2 slots, prologue 0 or 1
         if (fused != kFusedGate) geo.R = 1;
         if (geo.slots > 2) geo.slots = 2;
@@ -685,14 +781,16 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // the tile kernel addresses a wave's rows with 31-bit offsets; column
     // strides travel as 32-bit kernel arguments
+    // (the K-split kernel addresses a workgroup's rows with 32-bit offsets)
     if (geo.mfma ? (int64_t)(geo.rows_base + 1) * kMfmaRows * nb01 >= ((int64_t)1 << 31)
-                 : !geo.bpl && (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31))
+                 : geo.ksplit ? (int64_t)(geo.rows_base + 1) * nb01 >= ((int64_t)1 << 31)
+                              : !geo.bpl && (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31))
         return Q4K_EUNSUPPORTED;
     if (ldx > INT32_MAX || stride_col_y > INT32_MAX) return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
-        if (!geo.bpl) {
+        if (!geo.bpl && !geo.ksplit) {
             g2.lds = geo.mfma ? mfma_lds_bytes((int)ne00, nc, geo.waves) : tile_lds_bytes((int)ne00, nc, geo.waves);
             if (g2.lds_launch < g2.lds) g2.lds_launch = g2.lds;
         }
@@ -1131,8 +1229,9 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
 int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32_t workgroups,
                               int32_t kernel) {
     if (rows_per_tile < 0 || waves_per_wg < 0 || workgroups < 0) return Q4K_EINVAL;
-    if (kernel < 0 || kernel > 4) return Q4K_EINVAL;
-    if (rows_per_tile != 0 && rows_per_tile != 1 && rows_per_tile != 2 && rows_per_tile != 4)
+    if (kernel < 0 || kernel > 5) return Q4K_EINVAL;
+    if (rows_per_tile != 0 && rows_per_tile != 1 && rows_per_tile != 2 && rows_per_tile != 4 &&
+        !(kernel == 5 && (rows_per_tile == 8 || rows_per_tile == 16)))
         return Q4K_EINVAL;
     if (waves_per_wg < 0 || waves_per_wg > 16) return Q4K_EINVAL;
     g_ovr_rows.store(rows_per_tile);
@@ -1163,7 +1262,7 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) 
     out[3] = g.lds_launch;
     out[4] = g.nc_chunk;
     out[5] = g.nc_chunk >= ne11 ? 1 : 0;
-    out[6] = g.mfma ? 4 : (g.bpl == 2 ? 3 : (g.bpl ? 2 : 1));
+    out[6] = g.ksplit ? 5 : (g.mfma ? 4 : (g.bpl == 2 ? 3 : (g.bpl ? 2 : 1)));
     out[7] = g.bpl ? g.rpw : g.R;
     return Q4K_OK;
 }

@@ -1,0 +1,340 @@
+// q4k_ksplit.h -- the K-split Q4_K GEMV kernel for gfx950: one F32
+// activation column, rows of one or two 16-block groups (K = 4096 or 8192).
+//
+// The waves of a workgroup split each row's super-blocks between them rather
+// than its rows.  A team of KW = 16/SBW waves shares every row the team
+// walks: wave w of the team owns the SBW super-blocks [16i + SBW*w, +SBW) of
+// each group i.  A wave step covers TR = 16/SBW rows of that slice, four
+// lanes per super-block as in the tile kernel:
+//
+//   lane = 4*SBW*r + 4*s + j    r: row of the step (0..TR-1)
+//                               s: super-block of the slice (0..SBW-1)
+//                               j: 32-byte qs chunk (sub-blocks 2j, 2j+1)
+//
+// so a lane again owns two whole sub-blocks of one super-block and forms
+// complete int32 sub-block sums.
+//
+// Activation.  A wave needs only its own slice, SBW*256 values per group.
+// Each lane loads 4*SBW consecutive values with 16-byte loads, the wave
+// quantises them in registers with the Q8_1 arithmetic of the other kernels
+// (32/(4*SBW) lanes per 32-value block; ggml's quantize_q8_1, called at
+// kernels/mmvq.cu:734), and ds_bpermute hands each lane the 64 q8 of its
+// two sub-blocks and their (d8, d8 * sum q8).  Those are cross-lane reads
+// through the LDS crossbar: no LDS memory and no barrier.  So every wave
+// issues its activation load and then its first weight loads as soon as it
+// starts, and the quantisation runs while the weights are in flight.  LDS
+// holds only the (row, slice) partials, which meet once, after the last
+// step, behind the kernel's only barrier.
+//
+// Summation order.  A lane's value is the fma chain over the row's groups
+// that a tile-kernel lane owning the same super-block and chunk forms
+// (accumulate).  The four chunks of a super-block, the super-blocks of a
+// slice and the slices of a row then combine in the balanced tree over the
+// 16 super-block positions of a group that the tile kernel's wave_sum forms
+// (at every level pairs (2t, 2t+1)): the DPP steps inside a wave are
+// wave_sum's first steps, and the tree over the slices finishes it.  The
+// outputs are therefore bit for bit the tile kernel's, for every SBW, team
+// count and workgroup count (tested).
+//
+// Reference: the product is kernels/mmvq.cu:150-344 with the vec-dot of
+// kernels/vecdotq.cuh:775-819 and :457-483, for one column.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "q4k_gemv_kernels.h"
+
+namespace q4k {
+
+// One lane's V <= 32 values, part of one 32-value block spread over the
+// 32/V lanes of an aligned lane group: V/4 packed q8 dwords, the block's
+// half(d) widened, and the int32 sum of its 32 q8 (in every lane of the
+// group).  The arithmetic and reduction trees are quantize_block_part's.
+template <int V>
+__device__ __forceinline__ void ks_quantize_part(const float (&v)[V], uint32_t (&word)[V / 4], float &d8,
+                                                 int &qsum) {
+    constexpr int LPB = 32 / V;
+    float amax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < V; ++k) amax = fmaxf(amax, fabsf(v[k]));
+    if constexpr (LPB >= 2) amax = dpp_max_xor1(amax);
+    if constexpr (LPB >= 4) amax = dpp_max_xor2(amax);
+    if constexpr (LPB >= 8) amax = dpp_max_half_mirror(amax);
+    const float d = div127(amax);
+    int s[1];
+    if (amax != 0.0f) {
+        quantize_values<V, 1>(v, d, __builtin_amdgcn_rcpf(d), word, s);
+    } else {
+#pragma unroll
+        for (int w = 0; w < V / 4; ++w) word[w] = 0;
+        s[0] = 0;
+    }
+    int t = s[0];
+    if constexpr (LPB >= 2) t += dpp<kDppXor1>(t);
+    if constexpr (LPB >= 4) t += dpp<kDppXor2>(t);
+    if constexpr (LPB >= 8) t += dpp<kDppHalfMirror>(t);
+    qsum = t;
+    d8 = (float)(_Float16)d;
+}
+
+__device__ __forceinline__ uint32_t bperm(int src_lane, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane * 4, (int)v);
+}
+__device__ __forceinline__ float bpermf(int src_lane, float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane * 4, __builtin_bit_cast(int, v)));
+}
+
+// The wave's activation slice of one group: lane L holds the 4*SBW values
+// [L*4*SBW, +4*SBW) of the slice; returns what lane (r, s, j) reads (the q8
+// of sub-blocks 2j and 2j+1 of super-block s and their (d8, d8 * sum q8)).
+// sq (parity variants; null in the product kernels) gets the int32 sums of
+// the slice's blocks, from each block's first lane, at sq[blk0 + b].
+template <int SBW>
+__device__ __forceinline__ LaneAct ks_stage(const float (&v)[4 * SBW], int lane, int s, int j, int32_t *sq,
+                                            int blk0) {
+    constexpr int V = 4 * SBW;
+    LaneAct a;
+    if constexpr (V <= 32) {
+        constexpr int LPB = 32 / V;
+        uint32_t word[V / 4];
+        float d8;
+        int qs;
+        ks_quantize_part<V>(v, word, d8, qs);
+        if (sq && (lane & (LPB - 1)) == 0) sq[blk0 + lane / LPB] = qs;
+        // dword t of lane (s, j) = values 256s + 64j + 4t: word t % SBW of
+        // lane (64s + 16j + t) / SBW
+        const int base = 64 * s + 16 * j;
+        uint32_t q[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) q[t] = bperm((base + t) / SBW, word[t % SBW]);
+        a.a0 = u32x4{q[0], q[1], q[2], q[3]};
+        a.a1 = u32x4{q[4], q[5], q[6], q[7]};
+        a.b0 = u32x4{q[8], q[9], q[10], q[11]};
+        a.b1 = u32x4{q[12], q[13], q[14], q[15]};
+        // block 8s + 2j + h starts in lane (8s + 2j + h) * LPB
+        const int l0 = (8 * s + 2 * j) * LPB, l1 = l0 + LPB;
+        const float d8a = bpermf(l0, d8), d8b = bpermf(l1, d8);
+        const int sa = (int)bperm(l0, (uint32_t)qs), sb = (int)bperm(l1, (uint32_t)qs);
+        a.dk = make_float4(d8a, d8a * (float)sa, d8b, d8b * (float)sb);
+    } else {  // SBW = 16: a lane's 64 values are its own two sub-blocks
+        float v0[32], v1[32];
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            v0[k] = v[k];
+            v1[k] = v[32 + k];
+        }
+        uint32_t w0[8], w1[8];
+        float d0, d1;
+        int s0, s1;
+        ks_quantize_part<32>(v0, w0, d0, s0);
+        ks_quantize_part<32>(v1, w1, d1, s1);
+        if (sq) {
+            sq[blk0 + 2 * lane] = s0;
+            sq[blk0 + 2 * lane + 1] = s1;
+        }
+        a.a0 = u32x4{w0[0], w0[1], w0[2], w0[3]};
+        a.a1 = u32x4{w0[4], w0[5], w0[6], w0[7]};
+        a.b0 = u32x4{w1[0], w1[1], w1[2], w1[3]};
+        a.b1 = u32x4{w1[4], w1[5], w1[6], w1[7]};
+        a.dk = make_float4(d0, d0 * (float)s0, d1, d1 * (float)s1);
+    }
+    return a;
+}
+
+// Sum of a step row's slice: the four chunks of each super-block (quad),
+// then the SBW super-blocks of the slice -- wave_sum's first steps; valid in
+// the last lane of each 4*SBW-lane row group (ks_writer).
+template <int SBW>
+__device__ __forceinline__ float ks_reduce(float v) {
+    v += dppf<kDppXor1>(v);
+    v += dppf<kDppXor2>(v);
+    if constexpr (SBW >= 2) v += dppf<kDppRor4>(v);
+    if constexpr (SBW >= 4) v += dppf<kDppRor8>(v);
+    if constexpr (SBW >= 8) v += dppf_rows<kDppBcast15, 0xa>(v);
+    if constexpr (SBW >= 16) v += dppf_rows<kDppBcast31, 0xc>(v);
+    return v;
+}
+
+template <int SBW>
+__device__ __forceinline__ bool ks_writer(int lane) {
+    return (lane & (4 * SBW - 1)) == 4 * SBW - 1;
+}
+
+// SBW: super-blocks per wave and group (1, 2, 4, 16), WAVES: waves per
+// workgroup (whole teams of 16/SBW), S: row tiles in flight per wave, G:
+// groups per row (K = 4096 G).  SUMS: the parity variant, which also stores
+// every lane's int32 sub-block sums and the activation's block sums.
+// Rows: the workgroup's share (rows_base / rows_extra, as the tile kernel),
+// tiles of TR rows split contiguously over the teams.
+template <int SBW, int WAVES, int S, int G, bool SUMS = false>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    constexpr int KW = 16 / SBW;  // waves sharing a row
+    constexpr int TR = 16 / SBW;  // rows per wave step
+    constexpr int TEAMS = WAVES / KW;
+    constexpr int V = 4 * SBW;    // activation values per lane and group
+    static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    float *part = reinterpret_cast<float *>(lds);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slice = wave % KW, team = wave / KW;
+    const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1), j = lane & 3;
+
+    // the workgroup's rows, and the team's tiles of TR rows among them
+    const int b = (int)blockIdx.x;
+    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
+    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int nt = (n + TR - 1) / TR;
+    const int tq = nt / TEAMS, trem = nt - tq * TEAMS;
+    const int tb = team * tq + min(team, trem);
+    const int ntiles = tq + (team < trem ? 1 : 0);
+
+    // 1. the slice's activation values, issued first (a CU returns vector
+    //    loads in order, and these come from L2); 16-byte loads only (the
+    //    host launches this kernel for 16-byte aligned activations: with an
+    //    element-load path beside them the compiler waited for every
+    //    activation load before issuing the first weight load)
+    float xv[G][V];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const float4 *src = reinterpret_cast<const float4 *>(p.x + (16 * i + SBW * slice) * kQK + lane * V);
+#pragma unroll
+        for (int k = 0; k < V / 4; ++k) {
+            const float4 a = src[k];
+            xv[i][4 * k] = a.x;
+            xv[i][4 * k + 1] = a.y;
+            xv[i][4 * k + 2] = a.z;
+            xv[i][4 * k + 3] = a.w;
+        }
+    }
+
+    // 2. the first S tiles' weights: the workgroup's rows as one buffer, so
+    //    rows past its share read zeros without memory traffic
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    const uint32_t lrow = (uint32_t)r * (uint32_t)p.row_stride;
+    const uint32_t lh = lrow + (uint32_t)((SBW * slice + s) * kBlockBytes);
+    const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
+    const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
+    auto load_tile = [&](int t, RowRegs(&w)[G]) {
+        const bool ok = t < ntiles;
+        const uint32_t base = (uint32_t)(tb + t) * tile_bytes;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const uint32_t gi = (uint32_t)i * (16u * kBlockBytes);
+            const uint32_t oh = ok ? base + gi + lh : kOOB;
+            const uint32_t oq = ok ? base + gi + lq : kOOB;
+            w[i].h = load16(rs, oh);
+            w[i].q0 = load16(rs, oq);
+            w[i].q1 = load16(rs, oq + 16u);
+        }
+    };
+    int tk[S];
+    RowRegs w[S][G];
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+        tk[k] = k;
+        load_tile(k, w[k]);
+    }
+
+    // 3. quantise the slice and hand each lane its sub-blocks
+    LaneAct act[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+        act[i] = ks_stage<SBW>(xv[i], lane, s, j, SUMS ? p.sq : nullptr, (16 * i + SBW * slice) * 8);
+
+    Lane ln;
+    ln.lane = lane;
+    ln.g = SBW * slice + s;
+    ln.j = j;
+    ln.sel = make_scale_sel(j);
+    // 4. the tiles, S in flight; slot k is consumed and then reloaded with
+    //    the tile S further on (past the team's tiles: zeros, no traffic)
+    int remaining = ntiles;
+    if (remaining > 0) {
+        for (;;) {
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < G; ++i) {
+                    const RowScales sc = row_scales(w[k][i], ln);
+                    int sa, sb;
+                    accumulate(w[k][i], sc, act[i], acc, sa, sb);
+                    if constexpr (SUMS) {
+                        const int rl = (tb + tk[k]) * TR + r;
+                        if (tk[k] < ntiles && rl < n) {
+                            int32_t *o = p.sums + (int64_t)(wg_beg + rl) * (p.K / 32) + (16 * i + ln.g) * 8 + 2 * j;
+                            o[0] = sa;
+                            o[1] = sb;
+                        }
+                    }
+                }
+                const float q = ks_reduce<SBW>(acc);
+                const int rl = (tb + tk[k]) * TR + r;
+                if (ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n) part[rl * KW + slice] = q;
+                tk[k] += S;
+                load_tile(tk[k], w[k]);
+            }
+            remaining -= S;
+            if (remaining <= 0) break;
+        }
+    }
+    __syncthreads();
+    // 5. each row: the balanced tree over its KW slice sums
+    for (int row = (int)threadIdx.x; row < n; row += kWave * WAVES) {
+        float q[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) q[k] = part[row * KW + k];
+#pragma unroll
+        for (int h = KW / 2; h >= 1; h /= 2)
+#pragma unroll
+            for (int t = 0; t < h; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+        p.dst[wg_beg + row] = q[0];
+    }
+}
+
+// LDS bytes of a K-split launch: the (row, slice) partials of the largest
+// workgroup share.
+__host__ __device__ constexpr int ksplit_lds_bytes(int rows_per_wg, int sbw) { return rows_per_wg * (16 / sbw) * 4; }
+
+// The instantiated K-split variants: whole teams per workgroup; two groups
+// per row only up to SBW = 4 (at 16 the raw activation of two groups alone
+// would take 128 registers), and no SBW = 8 (its 32 values per lane led the
+// compiler to quantise them before issuing the first weight load).
+constexpr bool ksplit_exists(int sbw, int waves, int slots, int G) {
+    return (sbw == 1 || sbw == 2 || sbw == 4 || sbw == 16) && (waves == 4 || waves == 8 || waves == 16) &&
+           waves % (16 / sbw) == 0 && !(sbw == 16 && waves == 16) && (slots == 1 || slots == 2) && (G == 1 || (G == 2 && sbw <= 4));
+}
+
+template <bool SUMS, int SBW, int WAVES, int S>
+const void *ksplit_sym_g(int G) {
+    if constexpr (ksplit_exists(SBW, WAVES, S, 1))
+        if (G == 1) return reinterpret_cast<const void *>(&gemv_q4k_ksplit_kernel<SBW, WAVES, S, 1, SUMS>);
+    if constexpr (ksplit_exists(SBW, WAVES, S, 2))
+        if (G == 2) return reinterpret_cast<const void *>(&gemv_q4k_ksplit_kernel<SBW, WAVES, S, 2, SUMS>);
+    return nullptr;
+}
+
+template <bool SUMS, int SBW>
+const void *ksplit_sym_w(int waves, int slots, int G) {
+    if (waves == 4) return slots == 2 ? ksplit_sym_g<SUMS, SBW, 4, 2>(G) : ksplit_sym_g<SUMS, SBW, 4, 1>(G);
+    if (waves == 8) return slots == 2 ? ksplit_sym_g<SUMS, SBW, 8, 2>(G) : ksplit_sym_g<SUMS, SBW, 8, 1>(G);
+    if (waves == 16) return slots == 2 ? ksplit_sym_g<SUMS, SBW, 16, 2>(G) : ksplit_sym_g<SUMS, SBW, 16, 1>(G);
+    return nullptr;
+}
+
+// The K-split kernel of a launch shape, or null when it is not instantiated.
+template <bool SUMS>
+const void *ksplit_kernel(int sbw, int waves, int slots, int G) {
+    switch (sbw) {
+        case 1: return ksplit_sym_w<SUMS, 1>(waves, slots, G);
+        case 2: return ksplit_sym_w<SUMS, 2>(waves, slots, G);
+        case 4: return ksplit_sym_w<SUMS, 4>(waves, slots, G);
+        case 16: return ksplit_sym_w<SUMS, 16>(waves, slots, G);
+        default: return nullptr;
+    }
+}
+
+}  // namespace q4k

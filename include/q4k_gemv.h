@@ -300,7 +300,9 @@ int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * out[2] workgroups, out[3] LDS bytes requested per workgroup, out[4] columns per
  * launch, out[5] 1 when the activation is quantised inside the GEMV launch,
  * out[6] kernel (1 tile, 2 block-per-lane, 3 coalesced block kernel, 4
- *        matrix-core kernel: tiles of 16 rows on v_mfma_i32_16x16x64_i8),
+ *        matrix-core kernel: tiles of 16 rows on v_mfma_i32_16x16x64_i8,
+ *        5 K-split kernel: the waves of a workgroup split each row's
+ *        super-blocks and quantise their own slice of the activation),
  * out[7] rows per wave step. */
 int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
 
@@ -310,7 +312,11 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * variant; reduced to 8 where 16 would not fit the registers), the number
  * of workgroups and the kernel (1 tile kernel, 2 block-per-lane, 3
  * coalesced block kernel where they apply, 4 matrix-core kernel for
- * products without an epilogue; Q6_K: 4 the matrix-core kernel, any other
+ * products without an epilogue, 5 K-split kernel for one 16-byte aligned
+ * F32 column of 4096 or 8192 values: rows_per_tile is then its rows per
+ * wave step (1, 4, 8, 16), waves_per_wg 4, 8 or 16 (at least the rows per
+ * step), and the pipeline override's slots its tiles in flight (1, 2);
+ * Q6_K: 4 the matrix-core kernel, any other
  * value the tile kernel); 0 restores the automatic
  * choice.  Nothing is read from the environment: until this is called the
  * geometry is automatic.  Not part of the reference interface: a

@@ -1,0 +1,130 @@
+"""GPU parity of the K-split kernel (one F32 column, rows of 4096 or 8192
+values; the waves of a workgroup split each row's super-blocks and quantise
+their own slice of the activation in registers).
+
+Bar: outputs bit for bit equal to the tile kernel's (both sum every row in
+the same balanced tree over super-block positions) in every instantiated
+launch shape, including uneven row splits and workgroups with fewer rows
+than a wave step covers, and within the parity tolerance of the oracle;
+the int32 sub-block and activation sums of its parity variant bit for bit
+against the oracle.
+"""
+import numpy as np
+import pytest
+
+import _common
+
+pytestmark = pytest.mark.gpu
+
+# (rows per wave step, waves per workgroup, tiles in flight) of the
+# instantiated variants for rows of one group; rows of two groups exist
+# for 4..16 rows per step
+SHAPES_G1 = [(tr, w, s) for tr in (16, 8, 4, 1) for w in (4, 8, 16) for s in (1, 2)
+             if w >= tr and not (tr == 1 and w == 16)]
+SHAPES_G2 = [(tr, w, s) for (tr, w, s) in SHAPES_G1 if tr >= 4]
+
+_wcache = {}
+
+
+def inputs(Q, M, K, seed):
+    key = (M, K, seed)
+    if key not in _wcache:
+        _wcache.clear()
+        _wcache[key] = Q.quantize_rows_q4_K(_common.weights(M, K, seed), nthreads=16)
+    return _wcache[key], _common.activations(1, K, seed)
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def run_forced(Q, wd, K, xd, tr, waves, slots, wgs=0):
+    try:
+        Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, workgroups=wgs, kernel=5)
+        Q.set_pipeline_override(slots=slots)
+        g = Q.geometry(K, wd.shape[0], 1)
+        assert g["kernel"] == 5 and g["rows_per_step"] == tr and g["waves_per_wg"] == waves, g
+        return Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+        Q.set_pipeline_override()
+
+
+@pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 4096), (1024, 4096), (3001, 4096), (37, 4096),
+                                 (1, 4096), (5000, 8192), (258, 8192), (20, 8192)])
+def test_ksplit_bits_equal_tile_kernel(Q, O, gpu, M, K):
+    """Every instantiated launch shape, with the default one workgroup per
+    CU, 7 workgroups (hundreds of rows each, uneven tiles per team) and 300
+    (several workgroups with fewer rows than a step), against the tile
+    kernel bit for bit; the tile kernel against the oracle."""
+    wq, x = inputs(Q, M, K, seed=21)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    try:
+        Q.set_geometry_override(kernel=1)
+        y_tile = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+    rows = np.arange(M) if M <= 4096 else np.unique(
+        np.concatenate([[0, 1, M - 2, M - 1], np.random.default_rng(M).choice(M, 400, replace=False)]))
+    ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"tile {M}x{K}")
+    shapes = SHAPES_G1 if K == 4096 else SHAPES_G2
+    for tr, waves, slots in shapes:
+        for wgs in (0, 7, 300):
+            y = run_forced(Q, wd, K, xd, tr, waves, slots, wgs)
+            if not np.array_equal(y, y_tile):
+                bad = np.flatnonzero(y[0] != y_tile[0])
+                raise AssertionError(f"{M}x{K} rows/step {tr} waves {waves} slots {slots} wgs {wgs}: "
+                                     f"{bad.size} outputs differ from the tile kernel, e.g. rows {bad[:5]}")
+
+
+@pytest.mark.parametrize("M,K", [(4096, 4096), (333, 4096), (1030, 8192)])
+def test_ksplit_sums_exact(Q, O, gpu, M, K):
+    """The parity variant of each launch shape: S_qq of every lane and S_q of
+    the in-register quantisation bit for bit against the oracle, outputs
+    equal to the product launch's."""
+    import torch
+    wq, x = inputs(Q, M, K, seed=22)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    rows = np.unique(np.concatenate([[0, M // 2, M - 1], np.random.default_rng(M).choice(M, 120, replace=False)]))
+    ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x))
+    shapes = SHAPES_G1 if K == 4096 else SHAPES_G2
+    for tr, waves, slots in shapes:
+        try:
+            Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
+            Q.set_pipeline_override(slots=slots)
+            y, sums, sq = Q.mul_mat_vec_q_sums(wd, K, xd)
+            y_prod = Q.mul_mat_vec_q(wd, K, xd)
+        finally:
+            Q.set_geometry_override()
+            Q.set_pipeline_override()
+        where = f"{M}x{K} rows/step {tr} waves {waves} slots {slots}"
+        assert torch.equal(y, y_prod), where
+        got = sums[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        assert np.array_equal(got, ref["sqq"]), f"{where}: S_qq differ"
+        assert np.array_equal(sq.cpu().numpy(), ref["sq"]), f"{where}: S_q differ"
+
+
+def test_ksplit_unaligned_activation_and_q8_1_route(Q, O, gpu):
+    """An activation that is not 16-byte aligned, and a pre-quantised Q8_1
+    activation, never reach the K-split kernel (it takes 16-byte loads of F32
+    values): the override falls back to the tile kernel there, whose outputs
+    are the same bits."""
+    import torch
+    M, K = 777, 4096
+    wq, x = inputs(Q, M, K, seed=23)
+    wd = to_dev(wq, gpu)
+    buf = torch.zeros(K + 1, dtype=torch.float32, device=gpu)
+    buf[1:] = to_dev(x[0], gpu)
+    xa = buf[:K].clone()
+    xa.copy_(buf[1:])
+    y_al = run_forced(Q, wd, K, xa.view(1, K), 8, 16, 1)
+    y_un = run_forced(Q, wd, K, buf[1:].view(1, K), 8, 16, 1)
+    assert np.array_equal(y_al, y_un)
+    try:
+        Q.set_geometry_override(rows_per_tile=8, waves_per_wg=16, kernel=5)
+        y_q8 = Q.op_mul_mat_vec_q(wd, K, Q.quantize_row_q8_1(xa.view(1, K)), 1).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+    assert np.array_equal(y_q8, y_al)

@@ -526,39 +526,52 @@ def test_production_kernel_sums(Q, O, gpu, M, K, N):
 
 def test_parity_variants_cover_every_kernel(Q, gpu):
     """The workloads' launches, whose sums test_production_kernel_sums
-    checks, include the block-per-lane kernel, the matrix-core kernel
-    (128256 x 4096, eight columns), the 8-wave register path for several
-    columns, 16-wave and 8-wave tile launches and both staging routes."""
+    checks, include the K-split kernel (one column of 4096-value rows), the
+    matrix-core kernel (128256 x 4096, eight columns), the 8-wave register
+    path for several columns, 16-wave and 8-wave tile launches and both
+    staging routes.  (The block-per-lane kernel, no longer the automatic
+    choice anywhere, is checked through the override in
+    test_kernel_variants_against_oracle.)"""
     kinds = set()
     for p in _cases():
         M, K, N = p.values
         g = Q.geometry(K, M, N)
         kinds.add((g["kernel"], g["waves_per_wg"] if g["kernel"] == 1 else 0, N >= 3 and K <= 4096))
-    assert (2, 0, False) in kinds                      # block-per-lane (128256 x 4096, one column)
+    assert Q.geometry(4096, 14336, 1)["kernel"] == 5 and Q.geometry(4096, 128256, 1)["kernel"] == 5
+    assert (5, 0, False) in kinds                      # K-split (the headline shape)
     assert (4, 0, True) in kinds                       # matrix cores (128256 x 4096, eight columns)
     assert (1, 8, True) in kinds and (1, 16, True) in kinds   # several columns, 8 and 16 waves
-    assert (1, 16, False) in kinds                     # the headline shape
+    assert (1, 16, False) in kinds                     # one column of long rows (4096 x 14336)
 
 
 @pytest.mark.parametrize("M", [8192, 14336, 20480])
 def test_two_group_rows_streamed_prologue(Q, O, gpu, M):
-    """Rows of two 4096-value groups with 16 waves and two slots per wave:
-    with 64 or more rows per workgroup (20480 rows) the one-column launch
-    consumes its first steps between the quantisation rounds; with fewer it
-    issues one early group.  Checked against the oracle on a row sample,
-    bit for bit against the pre-quantised launch (which stages the whole
-    activation first), and with the bias epilogue (same rows, bias added)."""
+    """Rows of two 4096-value groups with 16 waves and two slots per wave,
+    on the tile kernel (forced: the automatic choice for one aligned F32
+    column is the K-split kernel; the tile kernel runs this shape for
+    unaligned activations and the bias epilogue): with 64 or more rows per
+    workgroup (20480 rows) the one-column launch consumes its first steps
+    between the quantisation rounds; with fewer it issues one early group.
+    Checked against the oracle on a row sample, bit for bit against the
+    pre-quantised launch (which stages the whole activation first), against
+    the automatic (K-split) launch, and with the bias epilogue (same rows,
+    bias added)."""
     import torch
     K = 8192
-    geo = Q.geometry(K, M, 1)
-    assert geo["kernel"] == 1 and geo["waves_per_wg"] == 16 and geo["workgroups"] <= 256, geo
-    wq, x = inputs(Q, M, K, 1, seed=9)
+    Q.set_geometry_override(kernel=1)
+    try:
+        geo = Q.geometry(K, M, 1)
+        assert geo["kernel"] == 1 and geo["waves_per_wg"] == 16 and geo["workgroups"] <= 256, geo
+        wq, x = inputs(Q, M, K, 1, seed=9)
+        wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+        y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+    assert np.array_equal(Q.mul_mat_vec_q(wd, K, xd).cpu().numpy(), y)
     q8 = O.quantize_q8_1(x)
     rng = np.random.default_rng(M)
     rows = np.unique(np.concatenate([[0, 1, 31, 32, M - 2, M - 1], rng.choice(M, 250, replace=False)]))
     ref = oracle_rows(O, wq, K, q8, rows)
-    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
-    y = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
     _common.assert_within_tolerance(O, y[:, rows], ref, f"{M}x{K} streamed")
     y2 = Q.op_mul_mat_vec_q(wd, K, to_dev(q8, gpu), 1).cpu().numpy()
     assert np.array_equal(y, y2)
