@@ -34,6 +34,8 @@ Modes:
                     with the roofline fraction, the measured traffic and a
                     CPU baseline with and without Q8_K quantisation
   --fused, --moe    the fused gate/up launch and MUL_MAT_ID workloads
+  --read-ceiling    a plain read of the headline weight's bytes (the GEMV's
+                    ceiling) in several launch shapes, and the headline GEMV
   --profile         plain eager launches of one shape (for rocprofv3)
   --profile-sweep   plain eager launches of every sweep config in order, each
                     preceded by a one-block quantiser launch that marks where
@@ -414,6 +416,65 @@ def cpu_baseline(wq, x, target_s=12.0, min_reps=10, wtype="q4_K"):
                       f"host), ggml's row chunks of 16; medians"}
 
 
+class ReadRunner:
+    """One q4k_read_probe call (a plain streaming read, the GEMV's ceiling)
+    over rotating copies of an nbytes buffer totalling >= 1 GiB."""
+
+    def __init__(self, Q, nbytes, wgs, waves, per_wave, infl, min_pool_bytes=1 << 30):
+        import ctypes
+        import torch
+        dev = torch.device("cuda:0")
+        self.Q = Q
+        self.ncopies = max(2, math.ceil(min_pool_bytes / nbytes))
+        b0 = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev)
+        self.copies = [b0] + [b0.clone() for _ in range(self.ncopies - 1)]
+        self.sink = torch.empty(wgs * waves, dtype=torch.int32, device=dev)
+        self.ptrs = [ctypes.c_void_p(c.data_ptr()) for c in self.copies]
+        self.args = (nbytes, wgs, waves, per_wave, infl, ctypes.c_void_p(self.sink.data_ptr()))
+        self.fn = Q.lib().q4k_read_probe
+        self.i = 0
+
+    def step(self, stream):
+        st = self.fn(self.ptrs[self.i % self.ncopies], *self.args, stream)
+        self.i += 1
+        if st != 0:
+            raise self.Q.Q4KError(st, "q4k_read_probe")
+
+
+# (workgroups, waves per workgroup, 1-KB loads in flight per wave)
+READ_SHAPES = [(2016, 4, 4), (2016, 4, 2), (1008, 4, 4), (4032, 4, 2), (1024, 8, 4), (512, 8, 4),
+               (512, 16, 2), (256, 16, 8), (256, 16, 4), (256, 16, 2), (256, 16, 1)]
+
+
+def read_ceiling(args):
+    """A plain read of the headline weight's bytes (14336 x 4096 Q4_K:
+    33,030,144 B) in several launch shapes, timed like the headline, against
+    the headline GEMV in the same process."""
+    import torch
+    Q = _pkg()
+    M, K = 14336, 4096
+    nbytes = M * (K // 256) * BLOCK_BYTES["q4_K"]
+    for wgs, waves, infl in READ_SHAPES:
+        per_wave = math.ceil(nbytes / (wgs * waves) / 1024) * 1024
+        r = ReadRunner(Q, nbytes, wgs, waves, per_wave, infl)
+        t = time_gpu(r, args.steps, args.warmup, args.trials)
+        del r
+        torch.cuda.empty_cache()
+        print(json.dumps({"kernel": "read_probe", "bytes": nbytes, "workgroups": wgs, "waves_per_wg": waves,
+                          "bytes_per_wave": per_wave, "loads_in_flight": infl, "us_per_call": round(t["s"] * 1e6, 3),
+                          "us_min": round(t["min_s"] * 1e6, 3), "method": t["method"],
+                          "GBps": round(nbytes / t["s"] / 1e9, 1),
+                          "hbm_frac": round(nbytes / t["s"] / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
+    wq, x = make_inputs(Q, M, K, 1)
+    r = OpRunner(Q, wq, x)
+    t = time_gpu(r, args.steps, args.warmup, args.trials)
+    nb = algorithmic_bytes(M, K, 1)
+    print(json.dumps({"kernel": "q4k_mul_mat_vec_q", "bytes": nb, "geometry": Q.geometry(K, M, 1),
+                      "us_per_call": round(t["s"] * 1e6, 3), "us_min": round(t["min_s"] * 1e6, 3),
+                      "method": t["method"], "GBps": round(nb / t["s"] / 1e9, 1),
+                      "hbm_frac": round(nb / t["s"] / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
+
+
 def launch_text(t) -> str:
     if t["method"] == "queued":
         return (f"the K timed calls launched back to back behind {t['head_replays']} untimed replays of a K-call "
@@ -726,6 +787,8 @@ def main():
                     help="time MUL_MAT_ID (one token) on expert-FFN shapes")
     ap.add_argument("--fused", action="store_true",
                     help="time the gate+up SWIGLU launch against two plain launches")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="time a plain read of the headline weight's bytes in several launch shapes")
     ap.add_argument("--wtype", choices=sorted(BLOCK_BYTES), default="q4_K",
                     help="weight format of --sweep, --profile and --profile-sweep (the headline is Q4_K)")
     args = ap.parse_args()
@@ -746,6 +809,8 @@ def main():
         moe_sweep(args)
     elif args.sweep:
         sweep(args)
+    elif args.read_ceiling:
+        read_ceiling(args)
     else:
         headline(args)
 

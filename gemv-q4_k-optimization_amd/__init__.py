@@ -56,6 +56,8 @@ SIGNATURES = {
     "q4k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
     "q4k_set_geometry_override": (_I, [ctypes.c_int32] * 4),
     "q4k_set_pipeline_override": (_I, [ctypes.c_int32] * 2),
+    "q4k_read_probe": (_I, [_P, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                            _P, _P]),
     "q4k_mul_mat_vec_q_fused": (_I, [ctypes.c_int32, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
     "q4k_quantize_rows_q4_K": (_I, [_P, _P, _I64, _I64, _I]),
     "q6k_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, ctypes.c_size_t, _P]),

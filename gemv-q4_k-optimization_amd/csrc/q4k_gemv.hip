@@ -297,8 +297,8 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
 // 8, 16; SBW super-blocks per wave and group), waves per workgroup
 // (whole teams of TR waves), workgroups (default one per CU) and row tiles
 // in flight per wave (1 or 2).
-static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t M, int rows_per_step, int waves, int wgs,
-                                     int slots) {
+static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
+                                     int wgs, int slots) {
     Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
     const int tr = rows_per_step == 1 || rows_per_step == 4 || rows_per_step == 8 || rows_per_step == 16
@@ -308,7 +308,8 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t M, int rows_p
     g.R = tr;
     g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
     if (g.waves < tr) g.waves = tr;
-    g.slots = slots == 2 ? 2 : 1;
+    g.slots = slots >= 1 && slots <= 4 ? slots : 1;
+    if (!ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096))) g.slots = 2;
     int64_t grid = wgs > 0 ? wgs : cus;
     if (grid > M) grid = M;
     g.grid = grid < 1 ? 1 : (int)grid;
@@ -398,12 +399,12 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // K-split kernel: one 16-byte aligned F32 column of 4096- or 8192-value
     // rows (the tile kernel, whose outputs are the same bits, takes the rest)
     const bool ks_ok = N == 1 && !fused && mats == 1 && f32_vec && (K == 4096 || K == 8192);
-    if (ks_ok && okern == 5) return pick_geometry_ksplit(di, M, orows, owaves, owgs, g_ovr_slots.load());
+    if (ks_ok && okern == 5) return pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load());
     if (ks_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
         int tr = 0, kw = 0, ks = 0;
         if (ksplit_auto(K, M, di.cus > 0 ? di.cus : 1, tr, kw, ks)) {
             const int os = g_ovr_slots.load();
-            return pick_geometry_ksplit(di, M, tr, kw, 0, os == 1 || os == 2 ? os : ks);
+            return pick_geometry_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks);
         }
     }
     if (N == 1 && rpw > 0 && okern == 3 && !fused && mats == 1) {
@@ -1242,7 +1243,7 @@ int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32
 }
 
 int q4k_set_pipeline_override(int32_t slots, int32_t prologue) {
-    if (slots != 0 && slots != 1 && slots != 2 && slots != 4 && slots != 8) return Q4K_EINVAL;
+    if (slots < 0 || slots > 8 || (slots > 4 && slots != 8)) return Q4K_EINVAL;
     if (prologue < -1 || prologue > 3) return Q4K_EINVAL;
     g_ovr_slots.store(slots);
     g_ovr_prologue.store(prologue);

@@ -305,7 +305,9 @@ __host__ __device__ constexpr int ksplit_lds_bytes(int rows_per_wg, int sbw) { r
 // compiler to quantise them before issuing the first weight load).
 constexpr bool ksplit_exists(int sbw, int waves, int slots, int G) {
     return (sbw == 1 || sbw == 2 || sbw == 4 || sbw == 16) && (waves == 4 || waves == 8 || waves == 16) &&
-           waves % (16 / sbw) == 0 && !(sbw == 16 && waves == 16) && (slots == 1 || slots == 2) && (G == 1 || (G == 2 && sbw <= 4));
+           waves % (16 / sbw) == 0 && !(sbw == 16 && waves == 16) &&
+           (slots == 1 || slots == 2 || ((slots == 3 || slots == 4) && G == 1 && sbw <= 4)) &&
+           (G == 1 || (G == 2 && sbw <= 4));
 }
 
 template <bool SUMS, int SBW, int WAVES, int S>
@@ -317,11 +319,22 @@ const void *ksplit_sym_g(int G) {
     return nullptr;
 }
 
+template <bool SUMS, int SBW, int WAVES>
+const void *ksplit_sym_s(int slots, int G) {
+    switch (slots) {
+        case 1: return ksplit_sym_g<SUMS, SBW, WAVES, 1>(G);
+        case 2: return ksplit_sym_g<SUMS, SBW, WAVES, 2>(G);
+        case 3: return ksplit_sym_g<SUMS, SBW, WAVES, 3>(G);
+        case 4: return ksplit_sym_g<SUMS, SBW, WAVES, 4>(G);
+        default: return nullptr;
+    }
+}
+
 template <bool SUMS, int SBW>
 const void *ksplit_sym_w(int waves, int slots, int G) {
-    if (waves == 4) return slots == 2 ? ksplit_sym_g<SUMS, SBW, 4, 2>(G) : ksplit_sym_g<SUMS, SBW, 4, 1>(G);
-    if (waves == 8) return slots == 2 ? ksplit_sym_g<SUMS, SBW, 8, 2>(G) : ksplit_sym_g<SUMS, SBW, 8, 1>(G);
-    if (waves == 16) return slots == 2 ? ksplit_sym_g<SUMS, SBW, 16, 2>(G) : ksplit_sym_g<SUMS, SBW, 16, 1>(G);
+    if (waves == 4) return ksplit_sym_s<SUMS, SBW, 4>(slots, G);
+    if (waves == 8) return ksplit_sym_s<SUMS, SBW, 8>(slots, G);
+    if (waves == 16) return ksplit_sym_s<SUMS, SBW, 16>(slots, G);
     return nullptr;
 }
 

@@ -315,7 +315,8 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * products without an epilogue, 5 K-split kernel for one 16-byte aligned
  * F32 column of 4096 or 8192 values: rows_per_tile is then its rows per
  * wave step (1, 4, 8, 16), waves_per_wg 4, 8 or 16 (at least the rows per
- * step), and the pipeline override's slots its tiles in flight (1, 2);
+ * step), and the pipeline override's slots its tiles in flight (1..4;
+ * 3 and 4 for rows of 4096 values and 1, 4 or 8 rows per step);
  * Q6_K: 4 the matrix-core kernel, any other
  * value the tile kernel); 0 restores the automatic
  * choice.  Nothing is read from the environment: until this is called the
@@ -327,12 +328,24 @@ int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32
 
 /* Tuning override of the tile kernels' pipeline for every later call in the
  * process: weight groups in flight per wave (1, 2, 4 or 8; Q6_K uses 1 or 2;
- * 0 = automatic) and when the first weight loads are issued relative to the
- * activation quantisation (0 = the first two groups before it, 1 = all
+ * the K-split kernel 1 to 4; 0 = automatic) and when the first weight
+ * loads are issued relative to the activation quantisation (0 = the first
+ * two groups before it, 1 = all
  * after, 2 = all before, 3 = one before; -1 = automatic).  Values a kernel
  * has no variant for fall back to the automatic choice.  Not part of the
  * reference interface: a benchmarking knob. */
 int q4k_set_pipeline_override(int32_t slots, int32_t prologue);
+
+/* A plain streaming read of `bytes` (< 2^31) of device memory: the ceiling
+ * the GEMV is measured against, not part of its path.  workgroups x
+ * waves_per_wg (4, 8, 16) waves, wave w reading bytes [w*bytes_per_wave,
+ * +bytes_per_wave) (a multiple of 1024; past the buffer: zeros) with 16-byte
+ * loads, loads_in_flight (1, 2, 4, 8) 1-KB load instructions issued
+ * together; each wave stores an xor of its data in sink[w] (sink holds
+ * workgroups * waves_per_wg words).  No counterpart in the reference: a
+ * measurement tool for bench.py. */
+int q4k_read_probe(const void *src, size_t bytes, int32_t workgroups, int32_t waves_per_wg,
+                   int32_t bytes_per_wave, int32_t loads_in_flight, uint32_t *sink, void *stream);
 
 /* ------------------------------------------------------------ host side */
 
