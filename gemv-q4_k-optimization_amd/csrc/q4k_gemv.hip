@@ -782,9 +782,9 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // the tile kernel addresses a wave's rows with 31-bit offsets; column
     // strides travel as 32-bit kernel arguments
-    // (the K-split kernel addresses a workgroup's rows with 32-bit offsets)
+    // (the K-split kernel: a workgroup's rows and one step past them)
     if (geo.mfma ? (int64_t)(geo.rows_base + 1) * kMfmaRows * nb01 >= ((int64_t)1 << 31)
-                 : geo.ksplit ? (int64_t)(geo.rows_base + 1) * nb01 >= ((int64_t)1 << 31)
+                 : geo.ksplit ? (int64_t)(geo.rows_base + 17) * nb01 >= ((int64_t)1 << 31)
                               : !geo.bpl && (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31))
         return Q4K_EUNSUPPORTED;
     if (ldx > INT32_MAX || stride_col_y > INT32_MAX) return Q4K_EUNSUPPORTED;

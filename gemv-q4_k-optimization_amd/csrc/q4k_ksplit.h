@@ -49,10 +49,11 @@ namespace q4k {
 // One lane's V <= 32 values, part of one 32-value block spread over the
 // 32/V lanes of an aligned lane group: V/4 packed q8 dwords, the block's
 // half(d) widened, and the int32 sum of its 32 q8 (in every lane of the
-// group).  The arithmetic and reduction trees are quantize_block_part's.
+// group) and of the 16-value half the lane's values lie in (V <= 16).  The
+// arithmetic and reduction trees are quantize_block_part's.
 template <int V>
 __device__ __forceinline__ void ks_quantize_part(const float (&v)[V], uint32_t (&word)[V / 4], float &d8,
-                                                 int &qsum) {
+                                                 int &qsum, int &hsum) {
     constexpr int LPB = 32 / V;
     float amax = 0.0f;
 #pragma unroll
@@ -70,9 +71,12 @@ __device__ __forceinline__ void ks_quantize_part(const float (&v)[V], uint32_t (
         s[0] = 0;
     }
     int t = s[0];
-    if constexpr (LPB >= 2) t += dpp<kDppXor1>(t);
-    if constexpr (LPB >= 4) t += dpp<kDppXor2>(t);
-    if constexpr (LPB >= 8) t += dpp<kDppHalfMirror>(t);
+    if constexpr (LPB >= 4) t += dpp<kDppXor1>(t);
+    if constexpr (LPB >= 8) t += dpp<kDppXor2>(t);
+    hsum = t;
+    if constexpr (LPB == 2) t += dpp<kDppXor1>(t);
+    if constexpr (LPB == 4) t += dpp<kDppXor2>(t);
+    if constexpr (LPB == 8) t += dpp<kDppHalfMirror>(t);
     qsum = t;
     d8 = (float)(_Float16)d;
 }
@@ -98,8 +102,8 @@ __device__ __forceinline__ LaneAct ks_stage(const float (&v)[4 * SBW], int lane,
         constexpr int LPB = 32 / V;
         uint32_t word[V / 4];
         float d8;
-        int qs;
-        ks_quantize_part<V>(v, word, d8, qs);
+        int qs, hs;
+        ks_quantize_part<V>(v, word, d8, qs, hs);
         if (sq && (lane & (LPB - 1)) == 0) sq[blk0 + lane / LPB] = qs;
         // dword t of lane (s, j) = values 256s + 64j + 4t: word t % SBW of
         // lane (64s + 16j + t) / SBW
@@ -125,9 +129,9 @@ __device__ __forceinline__ LaneAct ks_stage(const float (&v)[4 * SBW], int lane,
         }
         uint32_t w0[8], w1[8];
         float d0, d1;
-        int s0, s1;
-        ks_quantize_part<32>(v0, w0, d0, s0);
-        ks_quantize_part<32>(v1, w1, d1, s1);
+        int s0, s1, h0, h1;
+        ks_quantize_part<32>(v0, w0, d0, s0, h0);
+        ks_quantize_part<32>(v1, w1, d1, s1, h1);
         if (sq) {
             sq[blk0 + 2 * lane] = s0;
             sq[blk0 + 2 * lane + 1] = s1;

@@ -11,6 +11,7 @@
 #include "q4k_runtime.h"
 #include "q4k_tile.h"
 #include "q6k_kernels.h"
+#include "q6k_ksplit.h"
 #include "q6k_mfma.h"
 
 namespace q4k {
@@ -92,7 +93,61 @@ struct Q6Geometry {
     int mfma = 0;  // 1: matrix-core kernel (tiles of 16 rows; rows_base/rows_extra count tiles)
     int ks = 1;    // matrix-core kernel: waves sharing one tile
     int segs = 1;  // matrix-core kernel: summation segments of a row
+    int ksplit = 0;  // K-split kernel: super-blocks per wave and group (0: another kernel)
+    int ks_tr = 0;   // K-split kernel: rows per wave step (16 / ksplit)
 };
+
+// The K-split kernel's launch shape: rows_per_step TR = 16 / SBW (4, 8, 16),
+// waves per workgroup (whole teams of TR waves), workgroups (default one per
+// CU), tiles in flight (1, 2).
+static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
+                                          int wgs, int slots) {
+    Q6Geometry g;
+    const int cus = di.cus > 0 ? di.cus : 1;
+    g.ks_tr = rows_per_step == 4 || rows_per_step == 8 || rows_per_step == 16 ? rows_per_step : 8;
+    g.ksplit = 16 / g.ks_tr;
+    g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
+    if (g.waves < g.ks_tr) g.waves = g.ks_tr;
+    g.slots = slots == 2 ? 2 : 1;
+    if (!q6_ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096))) g.slots = 1;
+    int64_t grid = wgs > 0 ? wgs : cus;
+    if (grid > M) grid = M;
+    g.grid = grid < 1 ? 1 : (int)grid;
+    g.rows_base = (int)(M / g.grid);
+    g.rows_extra = (int)(M % g.grid);
+    g.lds = ksplit_lds_bytes(g.rows_base + (g.rows_extra ? 1 : 0), g.ksplit);
+    g.lds_launch = g.lds;
+    g.nc_chunk = 1;
+    return g;
+}
+
+// The K-split kernel's automatic shape for one aligned F32 column of 4096
+// or 8192 values, one workgroup per CU; false where the tile kernel
+// measured faster.  rho = rows per CU.  Measured on MI355X (us, interleaved
+// graph timings of 200 calls; K-split against the tile kernel): up to 4
+// rows per CU, 4 rows per step and 4 waves (1024 x 4096 3.10 against 3.69,
+// 1024 x 8192 4.71 / 5.42); up to 8, 8 rows and 8 waves (2048 x 4096 3.61 /
+// 4.25); beyond, 4 rows per step, 4 waves and two tiles in flight (4096 x
+// 4096 4.79 / 5.75, 14336 x 4096 10.57 / 11.49, 32768 x 4096 21.87 / 22.19,
+// 65536 x 4096 39.54 / 41.35, 4096 x 8192 7.96 / 8.60, 28672 x 8192 35.92 /
+// 36.60), except over 256 rows per CU at 4096 values (128256 x 4096: 76.10
+// against 75.10 on the tile kernel).
+static bool q6_ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
+    const int64_t rho = (M + cus - 1) / cus;
+    slots = 1;
+    if (rho <= 4) {
+        tr = waves = 4;
+        return true;
+    }
+    if (rho <= 8) {
+        tr = waves = 8;
+        return true;
+    }
+    if (K == 4096 && rho > 256) return false;
+    tr = waves = 4;
+    slots = 2;
+    return true;
+}
 
 // Where the matrix-core kernel is chosen (all columns in one launch, which
 // the caller checks).  Measured on MI355X against the tile kernel (graph
@@ -156,11 +211,24 @@ static Q6Geometry pick_geometry_q6_mfma(const DeviceInfo &di, int64_t K, int64_t
 // weight requests in flight (16 waves x 2 groups, 27.5 MB over the chip)
 // delay the activation loads more than they hide latency.
 static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int64_t mats = 1,
-                                   int fused = kFusedNone) {
+                                   int fused = kFusedNone, bool f32_vec = true) {
     Q6Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
     const int okern = g_ovr_kernel.load();
+    // K-split kernel: one 16-byte aligned F32 column of 4096- or 8192-value
+    // rows (the tile kernel, whose outputs are the same bits, takes the rest)
+    const bool ks_ok = N == 1 && mats == 1 && fused == kFusedNone && f32_vec && (K == 4096 || K == 8192);
+    if (ks_ok && okern == 5)
+        return pick_geometry_q6_ksplit(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(), g_ovr_wgs.load(),
+                                       g_ovr_slots.load());
+    if (ks_ok && okern == 0 && g_ovr_rows.load() == 0 && g_ovr_waves.load() == 0 && g_ovr_wgs.load() == 0) {
+        int tr = 0, kw = 0, ks = 0;
+        if (q6_ksplit_auto(K, M, cus, tr, kw, ks)) {
+            const int os = g_ovr_slots.load();
+            return pick_geometry_q6_ksplit(di, K, M, tr, kw, 0, os == 1 || os == 2 ? os : ks);
+        }
+    }
     if (fused == kFusedNone && mats == 1 && (okern == 4 || (okern == 0 && use_mfma_q6(M, N, K)))) {
         int mc = (int)N;
         while (mc > 1 && q6m_lds_bytes((int)K, mc, 16) > max_lds) mc = (mc + 1) / 2;
@@ -309,13 +377,15 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
     if (fused && ncols != 1) return Q4K_EINVAL;
     if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
     const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
-    const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats, fused);
+    const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0;
+    const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats, fused, f32_vec);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
-    // a wave's rows (the matrix-core kernel: a workgroup's tiles) are
-    // addressed with 31-bit offsets; column strides travel as 32-bit kernel
-    // arguments
-    if (geo.mfma ? (int64_t)(geo.rows_base + 1) * kMfmaRows * nb01 >= ((int64_t)1 << 31)
-                 : (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31))
+    // a wave's rows (the matrix-core kernel: a workgroup's tiles; the K-split
+    // kernel: a workgroup's rows and one step past them) are addressed with
+    // 31-bit offsets; column strides travel as 32-bit kernel arguments
+    if (geo.mfma      ? (int64_t)(geo.rows_base + 1) * kMfmaRows * nb01 >= ((int64_t)1 << 31)
+        : geo.ksplit ? (int64_t)(geo.rows_base + 17) * nb01 >= ((int64_t)1 << 31)
+                     : (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31))
         return Q4K_EUNSUPPORTED;
     if (ldx > INT32_MAX || stride_col_y > INT32_MAX) return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
@@ -323,8 +393,9 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         // a last chunk of under kDenseMinCols columns is staged padded
         const bool dense = geo.dense && nc >= kDenseMinCols;
         int lds_launch = geo.lds_launch;
-        const int lds = geo.mfma ? q6m_lds_bytes((int)ne00, nc, geo.waves)
-                                 : q6_tile_lds_bytes((int)ne00, nc, geo.waves, dense);
+        const int lds = geo.mfma     ? q6m_lds_bytes((int)ne00, nc, geo.waves)
+                        : geo.ksplit ? geo.lds
+                                     : q6_tile_lds_bytes((int)ne00, nc, geo.waves, dense);
         if (lds > di->max_lds) return Q4K_EUNSUPPORTED;
         if (lds_launch < lds) lds_launch = lds;
         GemvParams p{};
@@ -352,9 +423,11 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
             p.glu_op = ep->glu_op;
         }
-        const void *fn = geo.mfma ? q6_mfma_kernel_for(nc, geo.waves)
-                         : bl     ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
-                                  : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
+        const void *fn = geo.ksplit ? q6_ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
+                         : geo.mfma ? q6_mfma_kernel_for(nc, geo.waves)
+                         : bl       ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
+                                    : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
+        if (geo.ksplit && (nc != 1 || fused || bl || !p.x || !p.vec_ok)) return Q4K_EINVAL;
         if (geo.mfma) {
             if (fused || bl) return Q4K_EINVAL;
             p.rpw = geo.ks;
@@ -362,8 +435,9 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         }
         if (so) {  // parity variant: this chunk's columns of the group sums
             if (fused || bl) return Q4K_EINVAL;
-            fn = geo.mfma ? q6k_mfma_sums_kernel(nc, geo.waves)
-                          : q6k_sums_kernel(nc, geo.waves, geo.prologue, geo.slots, dense);
+            fn = geo.ksplit ? q6k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
+                 : geo.mfma ? q6k_mfma_sums_kernel(nc, geo.waves)
+                            : q6k_sums_kernel(nc, geo.waves, geo.prologue, geo.slots, dense);
             if (!fn) return Q4K_EUNSUPPORTED;  // a launch shape with no parity variant (overrides)
             p.sums = so->sums + c0 * ne01 * (ne00 / 16);
         }
@@ -523,13 +597,13 @@ int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) 
     const int st = device_info(&di);
     if (st != Q4K_OK) return st;
     const Q6Geometry g = pick_geometry_q6(*di, ne00, ne01, ne11);
-    out[0] = g.mfma ? kMfmaRows : 1;
+    out[0] = g.ksplit ? g.ks_tr : (g.mfma ? kMfmaRows : 1);
     out[1] = g.waves;
     out[2] = g.grid;
     out[3] = g.lds_launch;
     out[4] = g.nc_chunk;
     out[5] = g.nc_chunk >= ne11 ? 1 : 0;
-    out[6] = g.mfma ? 4 : 1;
+    out[6] = g.ksplit ? 5 : (g.mfma ? 4 : 1);
     out[7] = g.slots;
     return Q4K_OK;
 }

@@ -159,6 +159,20 @@ __device__ __forceinline__ void q6_lane_sums(const uint32_t (&v)[4][4], const Q6
         for (int k = 0; k < 4; ++k) s[m] = __builtin_amdgcn_sdot4((int)v[m][k], (int)a.a[m][k], s[m], false);
 }
 
+// acc += d * sum over the lane's four scale groups of d8 * (S * sc), S the
+// group sums (returned in s): the float combine of every kernel with this
+// lane map.  |S| <= 16*32*127 and |sc| <= 128: the 24-bit products are exact
+// in f32; explicit fmas fix the rounding for every launch geometry.
+__device__ __forceinline__ void q6_accumulate(const uint32_t (&v)[4][4], const int (&sc)[4], float d, const Q6Act &a,
+                                              float &acc, int (&s)[4]) {
+    q6_lane_sums(v, a, s);
+    float f = a.d8.x * (float)__mul24(s[0], sc[0]);
+    f = __builtin_fmaf(a.d8.y, (float)__mul24(s[1], sc[1]), f);
+    f = __builtin_fmaf(a.d8.z, (float)__mul24(s[2], sc[2]), f);
+    f = __builtin_fmaf(a.d8.w, (float)__mul24(s[3], sc[3]), f);
+    acc = __builtin_fmaf(d, f, acc);
+}
+
 // A wave's rows as one buffer, as for Q4_K (and the same rows of the gate
 // weight when the launch fuses one).
 struct Q6Stream {
@@ -216,15 +230,8 @@ __device__ __forceinline__ void q6_process_group_as(const GemvParams &p, const Q
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             int s[4];
-            q6_lane_sums(v[r], a, s);
+            q6_accumulate(v[r], sc[r], d[r], a, acc[r][c], s);
             if (R == 1) q6_record_sums<SUMS>(p, ln, rr, st.tile, 16 * st.i + ln.g, c, s);
-            // |s| <= 16*32*127 and |sc| <= 128: the 24-bit products are exact
-            // in f32.  Explicit fmas fix the rounding for every launch geometry.
-            float f = a.d8.x * (float)__mul24(s[0], sc[r][0]);
-            f = __builtin_fmaf(a.d8.y, (float)__mul24(s[1], sc[r][1]), f);
-            f = __builtin_fmaf(a.d8.z, (float)__mul24(s[2], sc[r][2]), f);
-            f = __builtin_fmaf(a.d8.w, (float)__mul24(s[3], sc[r][3]), f);
-            acc[r][c] = __builtin_fmaf(d[r], f, acc[r][c]);
         }
     }
 }
@@ -255,13 +262,8 @@ __device__ __forceinline__ void q6_process_reg(const GemvParams &p, const Q6Lane
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         int s[4];
-        q6_lane_sums(v, a[c], s);
+        q6_accumulate(v, sc, d, a[c], acc[0][c], s);
         q6_record_sums<SUMS>(p, ln, rr, st.tile, ln.g, c, s);
-        float f = a[c].d8.x * (float)__mul24(s[0], sc[0]);
-        f = __builtin_fmaf(a[c].d8.y, (float)__mul24(s[1], sc[1]), f);
-        f = __builtin_fmaf(a[c].d8.z, (float)__mul24(s[2], sc[2]), f);
-        f = __builtin_fmaf(a[c].d8.w, (float)__mul24(s[3], sc[3]), f);
-        acc[0][c] = __builtin_fmaf(d, f, acc[0][c]);
     }
     tile_to_ring<NC, 1, EPI>(p, ln.lane, acc, rr);
 }

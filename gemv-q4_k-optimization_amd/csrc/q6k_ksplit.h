@@ -1,0 +1,238 @@
+// q6k_ksplit.h -- the K-split Q6_K GEMV kernel for gfx950: one F32
+// activation column, rows of one or two 16-block groups (K = 4096 or 8192),
+// on the plan of the Q4_K K-split kernel (q4k_ksplit.h).
+//
+// A team of KW = 16/SBW waves shares every row the team walks: wave w of the
+// team owns the SBW super-blocks [16i + SBW*w, +SBW) of each group i; a wave
+// step covers TR = 16/SBW rows of that slice, four lanes per super-block with
+// the Q6_K tile kernel's lane map (q6k_kernels.h):
+//
+//   lane = 4*SBW*r + 4*s + 2h + j'   r: row of the step, s: super-block of
+//                                    the slice, h: half of the block, j': l
+//                                    in [16j', 16j' + 16)
+//
+// so a lane loads ql, qh, its half's scales and d of one super-block and
+// forms four whole scale-group sums (weights 128h + 32m + 16j' + [0, 16),
+// m = 0..3; kernels/vecdotq.cuh:867-891 and :580-600 compute the same sums
+// over another partition).
+//
+// Activation: each lane loads 4*SBW consecutive values of the wave's slice
+// and the wave quantises them in registers (Q8_1 arithmetic); ds_bpermute
+// hands each lane its 64 q8, the d8 of blocks 4h..4h+3 and the -32 * (sum of
+// q8) starting values of its four 16-value groups.  No LDS staging, no
+// barrier before the weight loads; the (row, slice) partials meet in LDS
+// after the last step.
+//
+// Summation order: the tile kernel's lane value (q6_accumulate, the same fma
+// chain over the row's groups), then wave_sum's tree over the 16 super-block
+// positions of a group, split between the DPP steps inside a wave and the
+// balanced tree over the slices: the outputs are the tile kernel's bits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "q4k_ksplit.h"
+#include "q6k_kernels.h"
+
+namespace q4k {
+
+// The wave's activation slice of one group (lane L holds the 4*SBW values
+// [L*4*SBW, +4*SBW) of the slice) -> what lane (r, s, h, j') reads.  sq
+// (unused: the Q6_K parity variants store group sums only) is not taken.
+template <int SBW>
+__device__ __forceinline__ Q6Act q6_ks_stage(const float (&v)[4 * SBW], int s, int h, int jp) {
+    constexpr int V = 4 * SBW;
+    constexpr int LPB = 32 / V;  // lanes per 32-value block (8, 4, 2)
+    static_assert(V <= 16, "16-value halves span whole lanes");
+    uint32_t word[V / 4];
+    float d8;
+    int qs, hs;
+    ks_quantize_part<V>(v, word, d8, qs, hs);
+    Q6Act a;
+    // dword t of group m = values 256s + 128h + 32m + 16j' + 4t: word t % SBW
+    // of lane (64s + 32h + 8m + 4j' + t) / SBW
+    const int base = 64 * s + 32 * h + 4 * jp;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        uint32_t q[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) q[t] = bperm((base + 8 * m + t) / SBW, word[t % SBW]);
+        a.a[m] = u32x4{q[0], q[1], q[2], q[3]};
+    }
+    // block 8s + 4h + m starts in lane (8s + 4h + m) * LPB; its half j' in
+    // lane + j' * LPB / 2
+    float d[4];
+    int hsum[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int l0 = (8 * s + 4 * h + m) * LPB;
+        d[m] = bpermf(l0, d8);
+        hsum[m] = (int)bperm(l0 + jp * (LPB / 2), (uint32_t)hs);
+    }
+    a.d8 = make_float4(d[0], d[1], d[2], d[3]);
+    a.s0 = make_int4(-32 * hsum[0], -32 * hsum[1], -32 * hsum[2], -32 * hsum[3]);
+    return a;
+}
+
+// SBW: super-blocks per wave and group (1, 2, 4), WAVES: waves per
+// workgroup (whole teams of 16/SBW), S: row tiles in flight per wave, G:
+// groups per row.  SUMS: the parity variant, which also stores every lane's
+// four int32 group sums.  Rows: the workgroup's share, tiles of TR rows
+// split contiguously over the teams.
+template <int SBW, int WAVES, int S, int G, bool SUMS = false>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    constexpr int KW = 16 / SBW;
+    constexpr int TR = 16 / SBW;
+    constexpr int TEAMS = WAVES / KW;
+    constexpr int V = 4 * SBW;
+    static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    float *part = reinterpret_cast<float *>(lds);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slice = wave % KW, team = wave / KW;
+    const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1);
+    const int h = (lane >> 1) & 1, jp = lane & 1;
+
+    const int b = (int)blockIdx.x;
+    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
+    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int nt = (n + TR - 1) / TR;
+    const int tq = nt / TEAMS, trem = nt - tq * TEAMS;
+    const int tb = team * tq + min(team, trem);
+    const int ntiles = tq + (team < trem ? 1 : 0);
+
+    // 1. the slice's activation (16-byte loads: the host launches this
+    //    kernel for 16-byte aligned activations), issued first
+    float xv[G][V];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const float4 *src = reinterpret_cast<const float4 *>(p.x + (16 * i + SBW * slice) * kQK + lane * V);
+#pragma unroll
+        for (int k = 0; k < V / 4; ++k) {
+            const float4 a = src[k];
+            xv[i][4 * k] = a.x;
+            xv[i][4 * k + 1] = a.y;
+            xv[i][4 * k + 2] = a.z;
+            xv[i][4 * k + 3] = a.w;
+        }
+    }
+
+    // 2. the first S tiles' weights
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    Q6Lane ln;
+    ln.lane = lane;
+    ln.g = SBW * slice + s;
+    ln.h = h;
+    ln.jp = jp;
+    const uint32_t blk = (uint32_t)r * (uint32_t)p.row_stride + (uint32_t)ln.g * kQ6Bytes;
+    ln.o_lo = blk + 64u * (uint32_t)h + 16u * (uint32_t)jp;
+    ln.o_hi = blk + 128u + 32u * (uint32_t)h + 16u * (uint32_t)jp;
+    ln.o_sc = blk + 192u + 8u * (uint32_t)h;
+    ln.o_d = blk + 206u;
+    const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
+    auto load_tile = [&](int t, Q6Regs(&w)[G]) {
+        const bool ok = t < ntiles;
+        const uint32_t base = (uint32_t)(tb + t) * tile_bytes;
+#pragma unroll
+        for (int i = 0; i < G; ++i) q6_load(rs, ln, base + (uint32_t)i * (16u * kQ6Bytes), ok, w[i]);
+    };
+    int tk[S];
+    Q6Regs w[S][G];
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+        tk[k] = k;
+        load_tile(k, w[k]);
+    }
+
+    // 3. quantise the slice and hand each lane its groups
+    Q6Act act[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) act[i] = q6_ks_stage<SBW>(xv[i], s, h, jp);
+
+    // 4. the tiles, S in flight
+    int remaining = ntiles;
+    if (remaining > 0) {
+        for (;;) {
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < G; ++i) {
+                    uint32_t v[4][4];
+                    int sc[4], gs[4];
+                    q6_values(w[k][i], v);
+                    q6_scales(w[k][i], jp, sc);
+                    q6_accumulate(v, sc, half_bits_to_float(w[k][i].dw >> 16), act[i], acc, gs);
+                    if constexpr (SUMS) {
+                        const int rl = (tb + tk[k]) * TR + r;
+                        if (tk[k] < ntiles && rl < n) {
+                            int32_t *o = p.sums + (int64_t)(wg_beg + rl) * (p.K / 16) + (16 * i + ln.g) * 16 + 8 * h + jp;
+#pragma unroll
+                            for (int m = 0; m < 4; ++m) o[2 * m] = gs[m];
+                        }
+                    }
+                }
+                const float q = ks_reduce<SBW>(acc);
+                const int rl = (tb + tk[k]) * TR + r;
+                if (ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n) part[rl * KW + slice] = q;
+                tk[k] += S;
+                load_tile(tk[k], w[k]);
+            }
+            remaining -= S;
+            if (remaining <= 0) break;
+        }
+    }
+    __syncthreads();
+    // 5. each row: the balanced tree over its KW slice sums
+    for (int row = (int)threadIdx.x; row < n; row += kWave * WAVES) {
+        float q[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) q[k] = part[row * KW + k];
+#pragma unroll
+        for (int hh = KW / 2; hh >= 1; hh /= 2)
+#pragma unroll
+            for (int t = 0; t < hh; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+        p.dst[wg_beg + row] = q[0];
+    }
+}
+
+// The instantiated variants: SBW 1, 2, 4 in whole teams, one or two tiles in
+// flight, rows of one or two groups (two tiles of two-group rows not at 16
+// waves, where they would spill registers).
+constexpr bool q6_ksplit_exists(int sbw, int waves, int slots, int G) {
+    return (sbw == 1 || sbw == 2 || sbw == 4) && (waves == 4 || waves == 8 || waves == 16) && waves % (16 / sbw) == 0 &&
+           (slots == 1 || slots == 2) && (G == 1 || G == 2) && !(G == 2 && slots == 2 && waves == 16);
+}
+
+template <bool SUMS, int SBW, int WAVES, int S>
+const void *q6_ksplit_sym_g(int G) {
+    if constexpr (q6_ksplit_exists(SBW, WAVES, S, 1))
+        if (G == 1) return reinterpret_cast<const void *>(&gemv_q6k_ksplit_kernel<SBW, WAVES, S, 1, SUMS>);
+    if constexpr (q6_ksplit_exists(SBW, WAVES, S, 2))
+        if (G == 2) return reinterpret_cast<const void *>(&gemv_q6k_ksplit_kernel<SBW, WAVES, S, 2, SUMS>);
+    return nullptr;
+}
+
+template <bool SUMS, int SBW>
+const void *q6_ksplit_sym_w(int waves, int slots, int G) {
+    if (waves == 4) return slots == 2 ? q6_ksplit_sym_g<SUMS, SBW, 4, 2>(G) : q6_ksplit_sym_g<SUMS, SBW, 4, 1>(G);
+    if (waves == 8) return slots == 2 ? q6_ksplit_sym_g<SUMS, SBW, 8, 2>(G) : q6_ksplit_sym_g<SUMS, SBW, 8, 1>(G);
+    if (waves == 16) return slots == 2 ? q6_ksplit_sym_g<SUMS, SBW, 16, 2>(G) : q6_ksplit_sym_g<SUMS, SBW, 16, 1>(G);
+    return nullptr;
+}
+
+// The Q6_K K-split kernel of a launch shape, or null when not instantiated.
+template <bool SUMS>
+const void *q6_ksplit_kernel(int sbw, int waves, int slots, int G) {
+    switch (sbw) {
+        case 1: return q6_ksplit_sym_w<SUMS, 1>(waves, slots, G);
+        case 2: return q6_ksplit_sym_w<SUMS, 2>(waves, slots, G);
+        case 4: return q6_ksplit_sym_w<SUMS, 4>(waves, slots, G);
+        default: return nullptr;
+    }
+}
+
+}  // namespace q4k

@@ -2,12 +2,14 @@
 // product kernels of q6k_kernels.h and q6k_mfma.h that also store every
 // lane's int32 group sums.  Instantiated for the launch shapes the automatic
 // geometry picks for plain products (8 or 16 waves; the tile kernel with one
-// slot and prologue 0 or 1); q6k_gemv.hip launches them with the product's
-// own geometry.
+// slot and prologue 0 or 1; the K-split kernel in every shape it is
+// instantiated in); q6k_gemv.hip launches them with the product's own
+// geometry.
 #include <hip/hip_runtime.h>
 
 #include "q4k_runtime.h"
 #include "q6k_kernels.h"
+#include "q6k_ksplit.h"
 #include "q6k_mfma.h"
 
 namespace q4k {
@@ -68,6 +70,10 @@ const void *q6_mfma_sums_nc(int nc) {
 
 const void *q6k_mfma_sums_kernel(int nc, int waves) {
     return waves > 8 ? q6_mfma_sums_nc<16>(nc) : q6_mfma_sums_nc<8>(nc);
+}
+
+const void *q6k_ksplit_sums_kernel(int sbw, int waves, int slots, int G) {
+    return q6_ksplit_kernel<true>(sbw, waves, slots, G);
 }
 
 const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense) {

@@ -39,6 +39,12 @@ def to_dev(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
+def few_workgroups(M):
+    """A small grid (hundreds of rows per workgroup, uneven tiles per team)
+    whose (row, slice) partials still fit the LDS: at most 2048 rows each."""
+    return max(7, -(-M // 2048))
+
+
 def run_forced(Q, wd, K, xd, tr, waves, slots, wgs=0):
     try:
         Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, workgroups=wgs, kernel=5)
@@ -55,8 +61,8 @@ def run_forced(Q, wd, K, xd, tr, waves, slots, wgs=0):
                                  (1, 4096), (5000, 8192), (258, 8192), (20, 8192)])
 def test_ksplit_bits_equal_tile_kernel(Q, O, gpu, M, K):
     """Every instantiated launch shape, with the default one workgroup per
-    CU, 7 workgroups (hundreds of rows each, uneven tiles per team) and 300
-    (several workgroups with fewer rows than a step), against the tile
+    CU, a few workgroups (hundreds of rows each, uneven tiles per team) and
+    300 (several workgroups with fewer rows than a step), against the tile
     kernel bit for bit; the tile kernel against the oracle."""
     wq, x = inputs(Q, M, K, seed=21)
     wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
@@ -71,7 +77,7 @@ def test_ksplit_bits_equal_tile_kernel(Q, O, gpu, M, K):
     _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"tile {M}x{K}")
     shapes = SHAPES_G1 if K == 4096 else SHAPES_G2
     for tr, waves, slots in shapes:
-        for wgs in (0, 7, 300):
+        for wgs in (0, few_workgroups(M), 300):
             y = run_forced(Q, wd, K, xd, tr, waves, slots, wgs)
             if not np.array_equal(y, y_tile):
                 bad = np.flatnonzero(y[0] != y_tile[0])
@@ -128,3 +134,86 @@ def test_ksplit_unaligned_activation_and_q8_1_route(Q, O, gpu):
     finally:
         Q.set_geometry_override()
     assert np.array_equal(y_q8, y_al)
+
+
+# ------------------------------------------------------------------ Q6_K ----
+# (rows per wave step, waves, tiles in flight) of the Q6_K K-split variants
+Q6_SHAPES_G1 = [(tr, w, s) for tr in (16, 8, 4) for w in (4, 8, 16) for s in (1, 2) if w >= tr]
+Q6_SHAPES_G2 = [(tr, w, s) for (tr, w, s) in Q6_SHAPES_G1 if not (s == 2 and w == 16)]
+
+_w6cache = {}
+
+
+def inputs6(Q, M, K, seed):
+    key = (M, K, seed)
+    if key not in _w6cache:
+        _w6cache.clear()
+        _w6cache[key] = Q.quantize_rows_q6_K(_common.weights(M, K, seed), nthreads=16)
+    return _w6cache[key], _common.activations(1, K, seed)
+
+
+def run_forced6(Q, wd, K, xd, tr, waves, slots, wgs=0):
+    t6 = Q.GGML_TYPE_Q6_K
+    try:
+        Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, workgroups=wgs, kernel=5)
+        Q.set_pipeline_override(slots=slots)
+        g = Q.geometry(K, wd.shape[0], 1, t6)
+        assert g["kernel"] == 5 and g["rows_per_tile"] == tr and g["waves_per_wg"] == waves, g
+        return Q.mul_mat_vec_q(wd, K, xd, wtype=t6).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+        Q.set_pipeline_override()
+
+
+@pytest.mark.parametrize("M,K", [(1024, 4096), (32768, 4096), (3001, 4096), (37, 4096), (1, 4096), (2049, 8192),
+                                 (20, 8192)])
+def test_q6k_ksplit_bits_equal_tile_kernel(Q, O, gpu, M, K):
+    """Q6_K: every instantiated launch shape, with one workgroup per CU, a
+    few and 300 workgroups, against the Q6_K tile kernel bit for bit (210-byte
+    blocks: every other block's loads 2-byte aligned); the tile kernel
+    against the oracle."""
+    t6 = Q.GGML_TYPE_Q6_K
+    wq, x = inputs6(Q, M, K, seed=31)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    try:
+        Q.set_geometry_override(kernel=1)
+        y_tile = Q.mul_mat_vec_q(wd, K, xd, wtype=t6).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+    rows = np.arange(M) if M <= 4096 else np.unique(
+        np.concatenate([[0, 1, M - 2, M - 1], np.random.default_rng(M).choice(M, 400, replace=False)]))
+    ref = O.gemv_q6K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"Q6_K tile {M}x{K}")
+    for tr, waves, slots in (Q6_SHAPES_G1 if K == 4096 else Q6_SHAPES_G2):
+        for wgs in (0, few_workgroups(M), 300):
+            y = run_forced6(Q, wd, K, xd, tr, waves, slots, wgs)
+            if not np.array_equal(y, y_tile):
+                bad = np.flatnonzero(y[0] != y_tile[0])
+                raise AssertionError(f"Q6_K {M}x{K} rows/step {tr} waves {waves} slots {slots} wgs {wgs}: "
+                                     f"{bad.size} outputs differ from the tile kernel, e.g. rows {bad[:5]}")
+
+
+@pytest.mark.parametrize("M,K", [(1024, 4096), (333, 4096), (517, 8192)])
+def test_q6k_ksplit_group_sums_exact(Q, O, gpu, M, K):
+    """The Q6_K parity variant of each launch shape: every lane's int32 group
+    sums (q - 32) * q8, starting from the -32 * sum q8 the in-register
+    quantisation hands over, bit for bit against the oracle."""
+    import torch
+    t6 = Q.GGML_TYPE_Q6_K
+    wq, x = inputs6(Q, M, K, seed=32)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    rows = np.unique(np.concatenate([[0, M // 2, M - 1], np.random.default_rng(M).choice(M, 100, replace=False)]))
+    ref = O.gemv_q6K_q8_1(wq[rows], K, O.quantize_q8_1(x))
+    for tr, waves, slots in (Q6_SHAPES_G1 if K == 4096 else Q6_SHAPES_G2):
+        try:
+            Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
+            Q.set_pipeline_override(slots=slots)
+            y, s16, _ = Q.mul_mat_vec_q_sums(wd, K, xd, wtype=t6)
+            y_prod = Q.mul_mat_vec_q(wd, K, xd, wtype=t6)
+        finally:
+            Q.set_geometry_override()
+            Q.set_pipeline_override()
+        where = f"Q6_K {M}x{K} rows/step {tr} waves {waves} slots {slots}"
+        assert torch.equal(y, y_prod), where
+        got = s16[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        assert np.array_equal(got, ref["s16"]), f"{where}: group sums differ"
