@@ -689,6 +689,37 @@ def _per_kernel(seg, warmup, steps):
     return out
 
 
+SQ_NEEDED = ("SQ_WAVES", "SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VMEM_RD", "SQ_INSTS_MFMA",
+             "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS", "SQ_WAIT_INST_ANY",
+             "SQ_WAIT_ANY", "SQ_LDS_BANK_CONFLICT")
+
+
+def _sq_table(sq):
+    """Derived SQ columns per (config, kernel) with both counter sets:
+    row group = one row's 16-block group (M x ceil(K/4096) per product);
+    VALU busy = SQ_ACTIVE_INST_VALU x 4 cycles / 1024 SIMDs over
+    SQ_BUSY_CYCLES / 32 shader engines; dependency wait = SQ_WAIT_ANY /
+    SQ_WAVE_CYCLES (waves waiting at s_waitcnt or a barrier); issue wait =
+    SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES (waves with an instruction ready but
+    not issued); wave life = SQ_WAVE_CYCLES / SQ_WAVES."""
+    rows = [(key, c) for key, c in sq.items() if all(n in c for n in SQ_NEEDED)]
+    if not rows:
+        return
+    print("| shape | N | kernel | waves | VALU instr | VALU / row group | VALU / row group / column | "
+          "LDS instr / row group | VALU busy % | dependency wait % | issue wait % | wave life (SQ_WAVE_CYCLES "
+          "/ wave) | LDS bank-conflict cycles / LDS active cycles | SALU instr | VMEM rd instr | MFMA instr |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|")
+    for (M, K, N, k), c in rows:
+        groups = M * ((K // 256 + 15) // 16)
+        busy = 100 * c["SQ_ACTIVE_INST_VALU"] * 4 / 1024 / (c["SQ_BUSY_CYCLES"] / 32)
+        print(f"| {M}x{K} | {N} | `{k}` | {c['SQ_WAVES']:,.0f} | {c['SQ_INSTS_VALU']:,.0f} | "
+              f"{c['SQ_INSTS_VALU'] / groups:.0f} | {c['SQ_INSTS_VALU'] / groups / N:.0f} | "
+              f"{c['SQ_INSTS_LDS'] / groups:.1f} | {busy:.0f} | {100 * c['SQ_WAIT_ANY'] / c['SQ_WAVE_CYCLES']:.1f} | "
+              f"{100 * c['SQ_WAIT_INST_ANY'] / c['SQ_WAVE_CYCLES']:.1f} | {c['SQ_WAVE_CYCLES'] / c['SQ_WAVES']:,.0f} | "
+              f"{c['SQ_LDS_BANK_CONFLICT'] / max(c['SQ_ACTIVE_INST_LDS'], 1):.2f} | {c['SQ_INSTS_SALU']:,.0f} | "
+              f"{c['SQ_INSTS_VMEM_RD']:,.0f} | {c['SQ_INSTS_MFMA']:,.0f} |")
+
+
 def summarize(args):
     """Per-config tables from the rocprofv3 output of a --profile-sweep run:
     kernel durations (--kernel-trace) or HBM bytes (--pmc FETCH_SIZE /
@@ -720,6 +751,7 @@ def summarize(args):
             for r in _rows(path):
                 by_counter.setdefault(r["Counter_Name"], []).append(r)
         per = {}
+        sq = {}
         for cname, crows in sorted(by_counter.items()):
             segs = _segments(crows, lambda r: float(r["Counter_Value"]))
             assert len(segs) == len(cfgs) + 1, (len(segs), len(cfgs))
@@ -729,6 +761,7 @@ def summarize(args):
                     for k, (n, v) in ks.items():
                         print(f"{cname} M={M} K={K} N={N} kernel={_short(k).replace(' ', '')} launches/op={n} "
                               f"median={float(np.median(v)):.0f}")
+                        sq.setdefault((M, K, N, _short(k)), {})[cname] = float(np.median(v))
                 continue
             # the calibration copy (the most frequent kernel before the first
             # separator) reads and writes CAL_BYTES once per dispatch
@@ -744,6 +777,7 @@ def summarize(args):
                 op = sum(n * float(np.median(v)) for n, v in ks.values()) * 1024 * factor
                 print(f"{cname} M={M} K={K} N={N} gemv_bytes={gemv:.0f} op_bytes={op:.0f}")
                 per.setdefault((M, K, N), {})[cname] = (gemv, op)
+        _sq_table(sq)
         if per and all({"FETCH_SIZE", "WRITE_SIZE"} <= set(v) for v in per.values()):
             print("| workload | shape | N | algorithmic B | GEMV read B | GEMV written B | op B (all kernels) | "
                   "op / algorithmic |")
@@ -787,6 +821,9 @@ def main():
                     help="time MUL_MAT_ID (one token) on expert-FFN shapes")
     ap.add_argument("--fused", action="store_true",
                     help="time the gate+up SWIGLU launch against two plain launches")
+    ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2, 3, 4, 5),
+                    help="--profile/--profile-sweep/--sweep: force a GEMV kernel through the geometry override "
+                         "(1 tile, 2 block-per-lane, 3 coalesced block, 4 matrix-core, 5 K-split; 0 automatic)")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="time a plain read of the headline weight's bytes in several launch shapes")
     ap.add_argument("--wtype", choices=sorted(BLOCK_BYTES), default="q4_K",
@@ -797,6 +834,8 @@ def main():
               "(rows would shard across GPUs through q4k_op_mul_mat_vec_q); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+    if args.kernel:
+        _pkg().set_geometry_override(kernel=args.kernel)
     if args.summarize:
         summarize(args)
     elif args.profile_sweep:
