@@ -5,7 +5,8 @@ the previous call's Q8_1 bytes.  The shapes take the routes that use the
 scratch (a quantisation launch of its own for several long columns; column
 chunks when the activation does not fit the LDS) and one that does not
 (quantisation inside the GEMV launch).  A request beyond the scratch is
-refused with Q4K_ESCRATCH before anything is launched."""
+refused with Q4K_ESCRATCH before anything is launched.  Captured into a HIP
+graph, a scratch-using call records kernel nodes only (no allocation)."""
 import numpy as np
 import pytest
 
@@ -65,3 +66,53 @@ def test_noalloc_refuses_requests_beyond_the_scratch(Q, gpu):
     assert _noalloc(Q, wd2, M, K2, xd2, N2, dst2) == Q.Q4K_OK
     torch.cuda.synchronize()
     assert np.array_equal(dst2.cpu().numpy(), Q.mul_mat_vec_q(wd2, K2, xd2).cpu().numpy())
+
+
+def test_noalloc_graph_capture_has_kernel_nodes_only(Q, gpu):
+    """A scratch-using call (eight columns of 28672 values: column chunks on
+    a Q8_1 copy in the scratch) captured into a HIP graph on a stream of its
+    own holds kernel nodes only -- no memory-allocation, free or memset node
+    -- and its replays, with eager work between them, equal the eager call
+    bit for bit."""
+    import ctypes
+    import torch
+    hip = ctypes.CDLL("libamdhip64.so")
+    M, K, N = 300, 28672, 8
+    wq = Q.quantize_rows_q4_K(_common.weights(M, K, seed=M + 1), nthreads=16)
+    wd = torch.from_numpy(wq).to(gpu)
+    xd = torch.from_numpy(_common.activations(N, K, seed=K + 1)).to(gpu)
+    ref = torch.full((N, M), -7.0, dtype=torch.float32, device=gpu)
+    assert _noalloc(Q, wd, M, K, xd, N, ref) == Q.Q4K_OK  # eager first: resolves the device's scratch
+    torch.cuda.synchronize()
+    dst = torch.full((N, M), -7.0, dtype=torch.float32, device=gpu)
+    stream = torch.cuda.Stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipStreamBeginCapture(sp, 1) == 0  # thread-local capture mode
+    st = Q.lib().q4k_mul_mat_vec_q_noalloc(Q._ptr(wd), K, M, K // 256 * 144, Q._ptr(xd), N, K * 4, Q._ptr(dst),
+                                           M * 4, sp)
+    assert hip.hipStreamEndCapture(sp, ctypes.byref(graph)) == 0
+    assert st == Q.Q4K_OK
+    try:
+        n = ctypes.c_size_t(0)
+        assert hip.hipGraphGetNodes(graph, None, ctypes.byref(n)) == 0 and n.value >= 2
+        nodes = (ctypes.c_void_p * n.value)()
+        assert hip.hipGraphGetNodes(graph, nodes, ctypes.byref(n)) == 0
+        types = []
+        for nd in nodes:
+            t = ctypes.c_int(-1)
+            assert hip.hipGraphNodeGetType(ctypes.c_void_p(nd), ctypes.byref(t)) == 0
+            types.append(t.value)
+        assert all(t == 0 for t in types), f"node types {types} (0 = kernel; 10/11 = alloc/free, 2 = memset)"
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        want = ref.cpu().numpy()
+        for i in range(3):
+            dst.fill_(-7.0)
+            torch.cuda.synchronize()
+            assert hip.hipGraphLaunch(exe, sp) == 0
+            stream.synchronize()
+            assert np.array_equal(dst.cpu().numpy(), want), f"replay {i}"
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        hip.hipGraphDestroy(graph)
