@@ -30,6 +30,7 @@ constexpr int kWave = 64;
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that is always out of range
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // gfx9 buffer descriptor word 3: 32-bit data format, no swizzle.
 constexpr int kBufferWord3 = 0x00020000;

@@ -198,6 +198,7 @@ struct Geometry {
     int ks = 1;         // matrix-core kernel: waves sharing one tile
     int segs = 1;       // matrix-core kernel: summation segments of a row
     int ksplit = 0;     // K-split kernel: super-blocks per wave and group (0: another kernel)
+    int ks_long = 0;    // K-split kernel for rows of any length (activation slices in LDS)
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
@@ -304,25 +305,33 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
     const int tr = rows_per_step == 1 || rows_per_step == 4 || rows_per_step == 8 || rows_per_step == 16
                        ? rows_per_step
                        : 16;
+    const bool lng = K != 4096 && K != 8192;  // rows of other lengths: the long-row variant
+    g.ks_long = lng ? 1 : 0;
     g.ksplit = 16 / tr;
-    g.R = tr;
+    if (lng && g.ksplit > 2) g.ksplit = 2;
+    g.R = 16 / g.ksplit;
     g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
-    if (g.waves < tr) g.waves = tr;
+    if (g.waves < g.R) g.waves = g.R;
+    if (lng && g.waves < 8) g.waves = 8;
     g.slots = slots >= 1 && slots <= 4 ? slots : 1;
-    if (!ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096))) g.slots = 2;
+    if (lng ? !ksplit_long_exists(g.ksplit, g.waves, g.slots, 8)
+            : !ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096)))
+        g.slots = 2;
     int64_t grid = wgs > 0 ? wgs : cus;
     if (grid > M) grid = M;
     g.grid = grid < 1 ? 1 : (int)grid;
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
-    g.lds = ksplit_lds_bytes(g.rows_base + (g.rows_extra ? 1 : 0), g.ksplit);
+    const int rows = g.rows_base + (g.rows_extra ? 1 : 0);
+    g.lds = lng ? ksplit_long_lds_bytes(rows, g.ksplit, g.waves, (int)((K / kQK + 15) / 16))
+                : ksplit_lds_bytes(rows, g.ksplit);
     g.lds_launch = g.lds;
     g.nc_chunk = 1;
     return g;
 }
 
 // The K-split kernel's automatic launch shape for one aligned F32 column of
-// K = 4096 or 8192 values, one workgroup per CU; false where the tile kernel
+// rows of up to 8 groups, one workgroup per CU; false where the tile kernel
 // measured faster.  rho = rows per CU.  Measured on MI355X (us, interleaved
 // graph timings of 200 calls; K-split against the tile kernel):
 //  - K = 4096: up to 4 rows per CU, 4 rows per step and 4 waves (1024 x
@@ -342,9 +351,29 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //    2048 x 8192 4.38 / 5.03), then 4 rows per step, 4 waves and two tiles
 //    in flight (4096 x 8192 5.51 / 5.87, 14336 x 8192 12.91 / 13.45, 28672 x
 //    8192 23.33 / 24.27).
+//  - other lengths up to 8 groups (the long-row variant, 8 or 16 rows per
+//    step): up to 8 rows per CU, 8 rows, 8 waves, two steps in flight
+//    (1024 x 14336 5.56 against 6.65, 2048 x 14336 5.79 / 7.21, 1024 x 28672
+//    9.33 / 11.11, 2048 x 11008 5.88 / 6.09); at 16 rows per CU, 16 rows
+//    and 16 waves, one step (4096 x 14336 8.32 / 8.54, 4096 x 11008 6.97 /
+//    7.42, 4096 x 5120 4.81 / 5.53); beyond, 8 rows, 8 waves, two steps
+//    where 8-row tiles leave at most one row in eight idle (8192 x 28672
+//    25.50 / 28.62, 14336 x 14336 21.55 / 22.46, 13824 x 5120 9.97 / 10.17,
+//    32000 x 5120 19.32 / 19.77, 18944 x 3584 9.17 / 9.42, 11008 x 2048
+//    5.44 / 5.46), the tile kernel otherwise (5120 x 13824, 20 rows per CU:
+//    10.23 against 9.50) and over 160 rows per CU (not measured).
 static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
+    if (K != 4096 && K != 8192) {
+        if (rho == 16) {
+            tr = waves = 16;
+            return true;
+        }
+        tr = waves = 8;
+        slots = 2;
+        return rho <= 8 || (rho <= 160 && ((rho + 7) / 8 * 8 - rho) * 8 <= rho);
+    }
     if (rho <= 4) {
         tr = 4;
         waves = 4;
@@ -396,9 +425,11 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const int orows = g_ovr_rows.load(), owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load();
     const int okern = g_ovr_kernel.load();
     const int rpw = bpl_rows_per_pass(K / kQK);
-    // K-split kernel: one 16-byte aligned F32 column of 4096- or 8192-value
-    // rows (the tile kernel, whose outputs are the same bits, takes the rest)
-    const bool ks_ok = N == 1 && !fused && mats == 1 && f32_vec && (K == 4096 || K == 8192);
+    // K-split kernel: one 16-byte aligned F32 column of rows of up to 8
+    // groups (4096 or 8192 values: activation in registers; other lengths:
+    // the long-row variant); the tile kernel, whose outputs are the same
+    // bits, takes the rest
+    const bool ks_ok = N == 1 && !fused && mats == 1 && f32_vec && K <= 8 * 4096;
     if (ks_ok && okern == 5) return pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load());
     if (ks_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
         int tr = 0, kw = 0, ks = 0;
@@ -701,8 +732,14 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         p.ring_off = lds_bytes(p.K, nc);
     } else if (geo.ksplit) {
         if (nc != 1 || !p.x || !p.vec_ok) return Q4K_EINVAL;
-        fn = p.sums ? q4k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
-                    : ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);
+        if (geo.ks_long) {
+            fn = p.sums ? q4k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
+                        : ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);
+            p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit);
+        } else {
+            fn = p.sums ? q4k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
+                        : ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);
+        }
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
     } else if (geo.mfma) {

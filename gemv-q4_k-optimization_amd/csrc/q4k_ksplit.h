@@ -42,6 +42,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "q4k_gemv_kernels.h"
 
 namespace q4k {
@@ -303,6 +305,209 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_
 // workgroup share.
 __host__ __device__ constexpr int ksplit_lds_bytes(int rows_per_wg, int sbw) { return rows_per_wg * (16 / sbw) * 4; }
 
+// ------------------------------------------------------------------------
+// Rows of any length: G groups of 16 super-blocks (G <= GMAX), the last one
+// possibly partial.  The activation of G groups would not fit the
+// registers, so each wave keeps its quantised slice of every group in a
+// wave-private LDS area -- the slice's q8, linear, then one (d8, d8 * sum
+// q8) pair per 32-value block -- written once by the wave and read back by
+// each lane at each step.  No other wave reads it, so there is still no
+// barrier before the weight loads.  The activation is read through a buffer
+// descriptor of exactly K floats: groups past the row read zeros, so every
+// load is issued unconditionally (the compiler then waits for exactly the
+// loads a step needs).  Steps walk (tile, group) pairs, S in flight.
+// Super-blocks past the row's end hold zero weights; a tile-kernel lane
+// adds exactly zero for them (its accumulator is never -0), so the wave
+// skips groups its slice does not reach and the sums stay the tile
+// kernel's bits.
+// ------------------------------------------------------------------------
+
+// LDS bytes of one wave's quantised slice of one group (q8, then a float2
+// per 32-value block).
+__host__ __device__ constexpr int ks_slice_bytes(int sbw) { return 320 * sbw; }
+
+// The wave's slice of one group, quantised (lane L: values [L*V, +V)), into
+// its LDS area; sq (parity variants) gets the int32 sums of the blocks that
+// lie inside the row (blk0: the slice's first block in the row).
+template <int SBW>
+__device__ __forceinline__ void ks_stage_lds(const float (&v)[4 * SBW], int lane, uint8_t *area, int32_t *sq,
+                                             int blk0, int nblk) {
+    constexpr int V = 4 * SBW;
+    constexpr int LPB = 32 / V;
+    uint32_t word[V / 4];
+    float d8;
+    int qs, hs;
+    ks_quantize_part<V>(v, word, d8, qs, hs);
+    uint32_t *q = reinterpret_cast<uint32_t *>(area + lane * V);
+#pragma unroll
+    for (int w = 0; w < V / 4; ++w) q[w] = word[w];
+    if ((lane & (LPB - 1)) == 0) {
+        const int b = lane / LPB;
+        reinterpret_cast<float2 *>(area + 256 * SBW)[b] = make_float2(d8, d8 * (float)qs);
+        if (sq && blk0 + b < nblk) sq[blk0 + b] = qs;
+    }
+}
+
+// What lane (s, j) reads of a staged slice: the q8 of sub-blocks 2j, 2j+1
+// of super-block s and their two (d8, d8 * sum q8) pairs.
+__device__ __forceinline__ LaneAct ks_read_lds(const uint8_t *area, int sbw, int s, int j) {
+    const uint8_t *q = area + 256 * s + 64 * j;
+    LaneAct a;
+    a.a0 = *reinterpret_cast<const u32x4 *>(q);
+    a.a1 = *reinterpret_cast<const u32x4 *>(q + 16);
+    a.b0 = *reinterpret_cast<const u32x4 *>(q + 32);
+    a.b1 = *reinterpret_cast<const u32x4 *>(q + 48);
+    a.dk = *reinterpret_cast<const float4 *>(area + 256 * sbw + (8 * s + 2 * j) * 8);
+    return a;
+}
+
+// SBW: 1 or 2 super-blocks per wave and group; GMAX: the most groups per
+// row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
+// partials).
+template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    constexpr int KW = 16 / SBW;
+    constexpr int TR = 16 / SBW;
+    constexpr int TEAMS = WAVES / KW;
+    constexpr int V = 4 * SBW;
+    static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    float *part = reinterpret_cast<float *>(lds);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slice = wave % KW, team = wave / KW;
+    const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1), j = lane & 3;
+    const int G = p.G;
+
+    const int b = (int)blockIdx.x;
+    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
+    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int nt = (n + TR - 1) / TR;
+    const int tq = nt / TEAMS, trem = nt - tq * TEAMS;
+    const int tb = team * tq + min(team, trem);
+    const int ntiles = tq + (team < trem ? 1 : 0);
+
+    // 1. the slice's activation in every group, issued first; past the row: zeros
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)p.K * 4u);
+    float xv[GMAX][V];
+#pragma unroll
+    for (int i = 0; i < GMAX; ++i) {
+        const uint32_t off = (uint32_t)(((16 * i + SBW * slice) * kQK + lane * V) * 4);
+#pragma unroll
+        for (int k = 0; k < V / 4; ++k) {
+            // the whole vector is cast: this clang's bit_cast of one element
+            // of an ext_vector lvalue reads element 0
+            const f32x4 a = __builtin_bit_cast(f32x4, load16(rx, off + 16u * k));
+            xv[i][4 * k] = a[0];
+            xv[i][4 * k + 1] = a[1];
+            xv[i][4 * k + 2] = a[2];
+            xv[i][4 * k + 3] = a[3];
+        }
+    }
+
+    // 2. the first S steps' weights
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    const uint32_t lrow = (uint32_t)r * (uint32_t)p.row_stride;
+    const uint32_t lh = lrow + (uint32_t)((SBW * slice + s) * kBlockBytes);
+    const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
+    const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
+    const int kb0 = SBW * slice + s;  // the lane's super-block within each group
+    auto load_step = [&](Step st, RowRegs &w) {
+        const bool ok = st.tile < ntiles && 16 * st.i + kb0 < p.nb;
+        const uint32_t base = (uint32_t)(tb + st.tile) * tile_bytes + (uint32_t)st.i * (16u * kBlockBytes);
+        const uint32_t oh = ok ? base + lh : kOOB;
+        const uint32_t oq = ok ? base + lq : kOOB;
+        w.h = load16(rs, oh);
+        w.q0 = load16(rs, oq);
+        w.q1 = load16(rs, oq + 16u);
+    };
+    Step st[S];
+    RowRegs w[S];
+    st[0] = Step{0, 0};
+#pragma unroll
+    for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], G);
+#pragma unroll
+    for (int k = 0; k < S; ++k) load_step(st[k], w[k]);
+
+    // 3. quantise the groups the slice reaches into the wave's LDS area;
+    // group 0 unconditionally (a slice past the row quantises zeros and
+    // writes no sums), so its load is not sunk below the weight loads
+    uint8_t *area = lds + p.ring_off + wave * G * ks_slice_bytes(SBW);
+#pragma unroll
+    for (int i = 0; i < GMAX; ++i)
+        if (i == 0 || (i < G && 16 * i + SBW * slice < p.nb))
+            ks_stage_lds<SBW>(xv[i], lane, area + i * ks_slice_bytes(SBW), SUMS ? p.sq : nullptr,
+                              (16 * i + SBW * slice) * 8, p.K / 32);
+    // lanes read what other lanes of the wave wrote: keep the reads below
+    // (a wave's LDS operations complete in order)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    Lane ln;
+    ln.lane = lane;
+    ln.g = kb0;
+    ln.j = j;
+    ln.sel = make_scale_sel(j);
+    // 4. the (tile, group) steps, S in flight
+    float acc = 0.0f;
+    int remaining = ntiles * G;
+    if (remaining > 0) {
+        for (;;) {
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                if (16 * st[k].i + SBW * slice < p.nb) {  // the wave's slice reaches this group
+                    const LaneAct a = ks_read_lds(area + st[k].i * ks_slice_bytes(SBW), SBW, s, j);
+                    const RowScales sc = row_scales(w[k], ln);
+                    int sa, sb;
+                    accumulate(w[k], sc, a, acc, sa, sb);
+                    if constexpr (SUMS) {
+                        const int rl = (tb + st[k].tile) * TR + r;
+                        const int kb = 16 * st[k].i + kb0;
+                        if (st[k].tile < ntiles && rl < n && kb < p.nb) {
+                            int32_t *o = p.sums + (int64_t)(wg_beg + rl) * (p.K / 32) + kb * 8 + 2 * j;
+                            o[0] = sa;
+                            o[1] = sb;
+                        }
+                    }
+                }
+                if (st[k].i == G - 1) {
+                    const float q = ks_reduce<SBW>(acc);
+                    const int rl = (tb + st[k].tile) * TR + r;
+                    if (ks_writer<SBW>(lane) && st[k].tile < ntiles && rl < n) part[rl * KW + slice] = q;
+                    acc = 0.0f;
+                }
+                st[k] = next_step(st[(k + S - 1) % S], G);
+                load_step(st[k], w[k]);
+            }
+            remaining -= S;
+            if (remaining <= 0) break;
+        }
+    }
+    __syncthreads();
+    for (int row = (int)threadIdx.x; row < n; row += kWave * WAVES) {
+        float q[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) q[k] = part[row * KW + k];
+#pragma unroll
+        for (int h = KW / 2; h >= 1; h /= 2)
+#pragma unroll
+            for (int t = 0; t < h; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+        p.dst[wg_beg + row] = q[0];
+    }
+}
+
+// LDS bytes of a long-row K-split launch: the partials, padded to 16 bytes,
+// then every wave's slice of every group.
+__host__ __device__ constexpr int ksplit_long_part_bytes(int rows_per_wg, int sbw) {
+    return (ksplit_lds_bytes(rows_per_wg, sbw) + 15) / 16 * 16;
+}
+__host__ __device__ constexpr int ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G) {
+    return ksplit_long_part_bytes(rows_per_wg, sbw) + waves * G * ks_slice_bytes(sbw);
+}
+
 // The instantiated K-split variants: whole teams per workgroup; two groups
 // per row only up to SBW = 4 (at 16 the raw activation of two groups alone
 // would take 128 registers), and no SBW = 8 (its 32 values per lane led the
@@ -339,6 +544,39 @@ const void *ksplit_sym_w(int waves, int slots, int G) {
     if (waves == 4) return ksplit_sym_s<SUMS, SBW, 4>(slots, G);
     if (waves == 8) return ksplit_sym_s<SUMS, SBW, 8>(slots, G);
     if (waves == 16) return ksplit_sym_s<SUMS, SBW, 16>(slots, G);
+    return nullptr;
+}
+
+// The long-row variants: SBW 1 or 2, whole teams of 8 or 16 waves, one or
+// two steps in flight, rows of up to 4 or 8 groups.
+constexpr bool ksplit_long_exists(int sbw, int waves, int slots, int gmax) {
+    return (sbw == 1 || sbw == 2) && (waves == 8 || waves == 16) && waves % (16 / sbw) == 0 &&
+           (slots == 1 || slots == 2) && (gmax == 4 || gmax == 8);
+}
+
+template <bool SUMS, int SBW, int WAVES, int S>
+const void *ksplit_long_sym_g(int gmax) {
+    if constexpr (ksplit_long_exists(SBW, WAVES, S, 4))
+        if (gmax == 4) return reinterpret_cast<const void *>(&gemv_q4k_ksplit_long_kernel<SBW, WAVES, S, 4, SUMS>);
+    if constexpr (ksplit_long_exists(SBW, WAVES, S, 8))
+        if (gmax == 8) return reinterpret_cast<const void *>(&gemv_q4k_ksplit_long_kernel<SBW, WAVES, S, 8, SUMS>);
+    return nullptr;
+}
+
+// The long-row K-split kernel for rows of G groups (G <= 8), or null.
+template <bool SUMS>
+const void *ksplit_long_kernel(int sbw, int waves, int slots, int G) {
+    const int gmax = G <= 4 ? 4 : 8;
+    if (G > 8) return nullptr;
+    auto pick = [&](auto sbw_c) -> const void * {
+        constexpr int B = decltype(sbw_c)::value;
+        if (waves == 8) return slots == 2 ? ksplit_long_sym_g<SUMS, B, 8, 2>(gmax) : ksplit_long_sym_g<SUMS, B, 8, 1>(gmax);
+        if (waves == 16)
+            return slots == 2 ? ksplit_long_sym_g<SUMS, B, 16, 2>(gmax) : ksplit_long_sym_g<SUMS, B, 16, 1>(gmax);
+        return nullptr;
+    };
+    if (sbw == 1) return pick(std::integral_constant<int, 1>{});
+    if (sbw == 2) return pick(std::integral_constant<int, 2>{});
     return nullptr;
 }
 

@@ -74,6 +74,10 @@ const void *q4k_ksplit_sums_kernel(int sbw, int waves, int slots, int G) {
     return ksplit_kernel<true>(sbw, waves, slots, G);
 }
 
+const void *q4k_ksplit_long_sums_kernel(int sbw, int waves, int slots, int G) {
+    return ksplit_long_kernel<true>(sbw, waves, slots, G);
+}
+
 const void *q4k_bpl_sums_kernel(int waves) {
     return waves == 8 ? reinterpret_cast<const void *>(&gemv_q4k_bpl_kernel<8, true>)
                       : reinterpret_cast<const void *>(&gemv_q4k_bpl_kernel<4, true>);

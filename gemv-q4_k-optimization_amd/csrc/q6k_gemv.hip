@@ -95,34 +95,41 @@ struct Q6Geometry {
     int segs = 1;  // matrix-core kernel: summation segments of a row
     int ksplit = 0;  // K-split kernel: super-blocks per wave and group (0: another kernel)
     int ks_tr = 0;   // K-split kernel: rows per wave step (16 / ksplit)
+    int ks_long = 0; // K-split kernel for rows of any length (activation slices in LDS)
 };
 
-// The K-split kernel's launch shape: rows_per_step TR = 16 / SBW (4, 8, 16),
-// waves per workgroup (whole teams of TR waves), workgroups (default one per
-// CU), tiles in flight (1, 2).
+// The K-split kernel's launch shape: rows_per_step TR = 16 / SBW (4, 8, 16;
+// rows of other lengths than 4096 and 8192 values: the long-row variant, 8
+// or 16), waves per workgroup (whole teams of TR waves; long rows: 8 or 16),
+// workgroups (default one per CU), tiles in flight (1, 2).
 static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
                                           int wgs, int slots) {
     Q6Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
+    const bool lng = K != 4096 && K != 8192;
+    g.ks_long = lng ? 1 : 0;
     g.ks_tr = rows_per_step == 4 || rows_per_step == 8 || rows_per_step == 16 ? rows_per_step : 8;
+    if (lng && g.ks_tr < 8) g.ks_tr = 8;
     g.ksplit = 16 / g.ks_tr;
     g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
     if (g.waves < g.ks_tr) g.waves = g.ks_tr;
     g.slots = slots == 2 ? 2 : 1;
-    if (!q6_ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096))) g.slots = 1;
+    if (!lng && !q6_ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096))) g.slots = 1;
     int64_t grid = wgs > 0 ? wgs : cus;
     if (grid > M) grid = M;
     g.grid = grid < 1 ? 1 : (int)grid;
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
-    g.lds = ksplit_lds_bytes(g.rows_base + (g.rows_extra ? 1 : 0), g.ksplit);
+    const int rows = g.rows_base + (g.rows_extra ? 1 : 0);
+    g.lds = lng ? q6_ksplit_long_lds_bytes(rows, g.ksplit, g.waves, (int)((K / kQK + 15) / 16))
+                : ksplit_lds_bytes(rows, g.ksplit);
     g.lds_launch = g.lds;
     g.nc_chunk = 1;
     return g;
 }
 
-// The K-split kernel's automatic shape for one aligned F32 column of 4096
-// or 8192 values, one workgroup per CU; false where the tile kernel
+// The K-split kernel's automatic shape for one aligned F32 column of rows
+// of up to 8 groups, one workgroup per CU; false where the tile kernel
 // measured faster.  rho = rows per CU.  Measured on MI355X (us, interleaved
 // graph timings of 200 calls; K-split against the tile kernel): up to 4
 // rows per CU, 4 rows per step and 4 waves (1024 x 4096 3.10 against 3.69,
@@ -131,10 +138,20 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
 // 4096 4.79 / 5.75, 14336 x 4096 10.57 / 11.49, 32768 x 4096 21.87 / 22.19,
 // 65536 x 4096 39.54 / 41.35, 4096 x 8192 7.96 / 8.60, 28672 x 8192 35.92 /
 // 36.60), except over 256 rows per CU at 4096 values (128256 x 4096: 76.10
-// against 75.10 on the tile kernel).
+// against 75.10 on the tile kernel).  Rows of other lengths up to 8 groups
+// (the long-row variant): 8 rows per step, 8 waves, two steps in flight up
+// to 160 rows per CU (4096 x 14336 12.26 against 13.58, 1024 x 14336 6.41 /
+// 7.91, 2048 x 14336 7.84 / 9.17, 8192 x 28672 38.47 / 42.46, 14336 x 14336
+// 33.44 / 35.93, 4096 x 11008 10.54 / 10.84, 13824 x 5120 15.26 / 17.32,
+// 5120 x 13824 14.92 / 14.95).
 static bool q6_ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
+    if (K != 4096 && K != 8192) {
+        tr = waves = 8;
+        slots = 2;
+        return rho <= 160;
+    }
     if (rho <= 4) {
         tr = waves = 4;
         return true;
@@ -216,9 +233,11 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
     const int okern = g_ovr_kernel.load();
-    // K-split kernel: one 16-byte aligned F32 column of 4096- or 8192-value
-    // rows (the tile kernel, whose outputs are the same bits, takes the rest)
-    const bool ks_ok = N == 1 && mats == 1 && fused == kFusedNone && f32_vec && (K == 4096 || K == 8192);
+    // K-split kernel: one 16-byte aligned F32 column of rows of up to 8
+    // groups (4096 or 8192 values: activation in registers; other lengths:
+    // the long-row variant); the tile kernel, whose outputs are the same
+    // bits, takes the rest
+    const bool ks_ok = N == 1 && mats == 1 && fused == kFusedNone && f32_vec && K <= 8 * 4096;
     if (ks_ok && okern == 5)
         return pick_geometry_q6_ksplit(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(), g_ovr_wgs.load(),
                                        g_ovr_slots.load());
@@ -423,7 +442,8 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
             p.glu_op = ep->glu_op;
         }
-        const void *fn = geo.ksplit ? q6_ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
+        const void *fn = geo.ks_long  ? q6_ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
+                         : geo.ksplit ? q6_ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.mfma ? q6_mfma_kernel_for(nc, geo.waves)
                          : bl       ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
                                     : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
@@ -435,13 +455,15 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         }
         if (so) {  // parity variant: this chunk's columns of the group sums
             if (fused || bl) return Q4K_EINVAL;
-            fn = geo.ksplit ? q6k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
+            fn = geo.ks_long  ? q6k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
+                 : geo.ksplit ? q6k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                  : geo.mfma ? q6k_mfma_sums_kernel(nc, geo.waves)
                             : q6k_sums_kernel(nc, geo.waves, geo.prologue, geo.slots, dense);
             if (!fn) return Q4K_EUNSUPPORTED;  // a launch shape with no parity variant (overrides)
             p.sums = so->sums + c0 * ne01 * (ne00 / 16);
         }
         if (bl) p.bt = bl->bt;
+        if (geo.ks_long) p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit);
         if (!fn) return Q4K_EINVAL;
         st = ensure_lds(di, fn, lds_launch);
         if (st != Q4K_OK) return st;

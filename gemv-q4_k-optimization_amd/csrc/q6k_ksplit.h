@@ -199,6 +199,222 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_
     }
 }
 
+// ------------------------------------------------------------------------
+// Rows of other lengths (up to 8 groups, the last one partial): the Q4_K
+// long-row plan (q4k_ksplit.h).  Each wave quantises its slice of every
+// group the row has into its own LDS area once, then walks (tile, group)
+// steps reading the slice back; the lane map, the per-lane fma chain over
+// the groups and the trees are the K-split kernel's, so the outputs are the
+// tile kernel's bits (super-blocks past the row, which the tile kernel adds
+// as exact zeros, are skipped).
+// ------------------------------------------------------------------------
+
+// LDS bytes of one wave's slice of one group: the q8, d8 per 32-value
+// block, then the -32 * sum(q8) starting values per 16 values (first halves
+// of the slice's blocks, then second halves).
+__host__ __device__ constexpr int q6_ks_slice_bytes(int sbw) { return 352 * sbw; }
+
+template <int SBW>
+__device__ __forceinline__ void q6_ks_stage_lds(const float (&v)[4 * SBW], int lane, uint8_t *area) {
+    constexpr int V = 4 * SBW;
+    constexpr int LPB = 32 / V;
+    uint32_t word[V / 4];
+    float d8;
+    int qs, hs;
+    ks_quantize_part<V>(v, word, d8, qs, hs);
+    uint32_t *q = reinterpret_cast<uint32_t *>(area + lane * V);
+#pragma unroll
+    for (int w = 0; w < V / 4; ++w) q[w] = word[w];
+    const int b = lane / LPB;
+    if ((lane & (LPB - 1)) == 0) reinterpret_cast<float *>(area + 256 * SBW)[b] = d8;
+    if ((lane & (LPB / 2 - 1)) == 0) {
+        const int half = (lane / (LPB / 2)) & 1;
+        reinterpret_cast<int *>(area + 288 * SBW)[8 * SBW * half + b] = -32 * hs;
+    }
+}
+
+// What lane (s, h, j') reads of a staged slice: its four 16-value groups of
+// q8 (blocks 8s + 4h + m, half j'), their d8 and starting values.
+__device__ __forceinline__ Q6Act q6_ks_read_lds(const uint8_t *area, int sbw, int s, int h, int jp) {
+    Q6Act a;
+    const uint8_t *q = area + 256 * s + 128 * h + 16 * jp;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) a.a[m] = *reinterpret_cast<const u32x4 *>(q + 32 * m);
+    a.d8 = *reinterpret_cast<const float4 *>(area + 256 * sbw + 4 * (8 * s + 4 * h));
+    a.s0 = *reinterpret_cast<const int4 *>(area + 288 * sbw + 4 * (8 * sbw * jp + 8 * s + 4 * h));
+    return a;
+}
+
+// SBW: 1 or 2 super-blocks per wave and group; GMAX: the most groups per
+// row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
+// partials).
+template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    constexpr int KW = 16 / SBW;
+    constexpr int TR = 16 / SBW;
+    constexpr int TEAMS = WAVES / KW;
+    constexpr int V = 4 * SBW;
+    static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    float *part = reinterpret_cast<float *>(lds);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slice = wave % KW, team = wave / KW;
+    const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1);
+    const int h = (lane >> 1) & 1, jp = lane & 1;
+    const int G = p.G;
+
+    const int b = (int)blockIdx.x;
+    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
+    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int nt = (n + TR - 1) / TR;
+    const int tq = nt / TEAMS, trem = nt - tq * TEAMS;
+    const int tb = team * tq + min(team, trem);
+    const int ntiles = tq + (team < trem ? 1 : 0);
+
+    // 1. the slice's activation in every group, issued first; past the row:
+    //    zeros (buffer loads; the whole vector is cast, see the Q4_K kernel)
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)p.K * 4u);
+    float xv[GMAX][V];
+#pragma unroll
+    for (int i = 0; i < GMAX; ++i) {
+        const uint32_t off = (uint32_t)(((16 * i + SBW * slice) * kQK + lane * V) * 4);
+#pragma unroll
+        for (int k = 0; k < V / 4; ++k) {
+            const f32x4 a = __builtin_bit_cast(f32x4, load16(rx, off + 16u * k));
+            xv[i][4 * k] = a[0];
+            xv[i][4 * k + 1] = a[1];
+            xv[i][4 * k + 2] = a[2];
+            xv[i][4 * k + 3] = a[3];
+        }
+    }
+
+    // 2. the first S steps' weights
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    Q6Lane ln;
+    ln.lane = lane;
+    ln.g = SBW * slice + s;  // the lane's super-block within each group
+    ln.h = h;
+    ln.jp = jp;
+    const uint32_t blk = (uint32_t)r * (uint32_t)p.row_stride + (uint32_t)ln.g * kQ6Bytes;
+    ln.o_lo = blk + 64u * (uint32_t)h + 16u * (uint32_t)jp;
+    ln.o_hi = blk + 128u + 32u * (uint32_t)h + 16u * (uint32_t)jp;
+    ln.o_sc = blk + 192u + 8u * (uint32_t)h;
+    ln.o_d = blk + 206u;
+    const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
+    auto load_step = [&](Step st, Q6Regs &w) {
+        const bool ok = st.tile < ntiles && 16 * st.i + ln.g < p.nb;
+        q6_load(rs, ln, (uint32_t)(tb + st.tile) * tile_bytes + (uint32_t)st.i * (16u * kQ6Bytes), ok, w);
+    };
+    Step st[S];
+    Q6Regs w[S];
+    st[0] = Step{0, 0};
+#pragma unroll
+    for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], G);
+#pragma unroll
+    for (int k = 0; k < S; ++k) load_step(st[k], w[k]);
+
+    // 3. quantise the groups the slice reaches into the wave's LDS area
+    //    (group 0 unconditionally, so its load stays ahead of the weights)
+    uint8_t *area = lds + p.ring_off + wave * G * q6_ks_slice_bytes(SBW);
+#pragma unroll
+    for (int i = 0; i < GMAX; ++i)
+        if (i == 0 || (i < G && 16 * i + SBW * slice < p.nb))
+            q6_ks_stage_lds<SBW>(xv[i], lane, area + i * q6_ks_slice_bytes(SBW));
+    // lanes read what other lanes of the wave wrote
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // 4. the (tile, group) steps, S in flight
+    float acc = 0.0f;
+    int remaining = ntiles * G;
+    if (remaining > 0) {
+        for (;;) {
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                if (16 * st[k].i + SBW * slice < p.nb) {  // the wave's slice reaches this group
+                    const Q6Act a = q6_ks_read_lds(area + st[k].i * q6_ks_slice_bytes(SBW), SBW, s, h, jp);
+                    uint32_t v[4][4];
+                    int sc[4], gs[4];
+                    q6_values(w[k], v);
+                    q6_scales(w[k], jp, sc);
+                    q6_accumulate(v, sc, half_bits_to_float(w[k].dw >> 16), a, acc, gs);
+                    if constexpr (SUMS) {
+                        const int rl = (tb + st[k].tile) * TR + r;
+                        const int kb = 16 * st[k].i + ln.g;
+                        if (st[k].tile < ntiles && rl < n && kb < p.nb) {
+                            int32_t *o = p.sums + (int64_t)(wg_beg + rl) * (p.K / 16) + kb * 16 + 8 * h + jp;
+#pragma unroll
+                            for (int m = 0; m < 4; ++m) o[2 * m] = gs[m];
+                        }
+                    }
+                }
+                if (st[k].i == G - 1) {
+                    const float q = ks_reduce<SBW>(acc);
+                    const int rl = (tb + st[k].tile) * TR + r;
+                    if (ks_writer<SBW>(lane) && st[k].tile < ntiles && rl < n) part[rl * KW + slice] = q;
+                    acc = 0.0f;
+                }
+                st[k] = next_step(st[(k + S - 1) % S], G);
+                load_step(st[k], w[k]);
+            }
+            remaining -= S;
+            if (remaining <= 0) break;
+        }
+    }
+    __syncthreads();
+    for (int row = (int)threadIdx.x; row < n; row += kWave * WAVES) {
+        float q[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) q[k] = part[row * KW + k];
+#pragma unroll
+        for (int hh = KW / 2; hh >= 1; hh /= 2)
+#pragma unroll
+            for (int t = 0; t < hh; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+        p.dst[wg_beg + row] = q[0];
+    }
+}
+
+__host__ __device__ constexpr int q6_ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G) {
+    return ksplit_long_part_bytes(rows_per_wg, sbw) + waves * G * q6_ks_slice_bytes(sbw);
+}
+
+// The long-row variants: SBW 1 or 2, whole teams of 8 or 16 waves, one or
+// two steps in flight, rows of up to 4 or 8 groups.
+constexpr bool q6_ksplit_long_exists(int sbw, int waves, int slots, int gmax) {
+    return ksplit_long_exists(sbw, waves, slots, gmax);
+}
+
+template <bool SUMS, int SBW, int WAVES, int S>
+const void *q6_ksplit_long_sym_g(int gmax) {
+    if constexpr (q6_ksplit_long_exists(SBW, WAVES, S, 4))
+        if (gmax == 4) return reinterpret_cast<const void *>(&gemv_q6k_ksplit_long_kernel<SBW, WAVES, S, 4, SUMS>);
+    if constexpr (q6_ksplit_long_exists(SBW, WAVES, S, 8))
+        if (gmax == 8) return reinterpret_cast<const void *>(&gemv_q6k_ksplit_long_kernel<SBW, WAVES, S, 8, SUMS>);
+    return nullptr;
+}
+
+// The Q6_K long-row K-split kernel for rows of G groups (G <= 8), or null.
+template <bool SUMS>
+const void *q6_ksplit_long_kernel(int sbw, int waves, int slots, int G) {
+    const int gmax = G <= 4 ? 4 : 8;
+    if (G > 8) return nullptr;
+    auto pick = [&](auto sbw_c) -> const void * {
+        constexpr int B = decltype(sbw_c)::value;
+        if (waves == 8)
+            return slots == 2 ? q6_ksplit_long_sym_g<SUMS, B, 8, 2>(gmax) : q6_ksplit_long_sym_g<SUMS, B, 8, 1>(gmax);
+        if (waves == 16)
+            return slots == 2 ? q6_ksplit_long_sym_g<SUMS, B, 16, 2>(gmax) : q6_ksplit_long_sym_g<SUMS, B, 16, 1>(gmax);
+        return nullptr;
+    };
+    if (sbw == 1) return pick(std::integral_constant<int, 1>{});
+    if (sbw == 2) return pick(std::integral_constant<int, 2>{});
+    return nullptr;
+}
+
 // The instantiated variants: SBW 1, 2, 4 in whole teams, one or two tiles in
 // flight, rows of one or two groups (two tiles of two-group rows not at 16
 // waves, where they would spill registers).

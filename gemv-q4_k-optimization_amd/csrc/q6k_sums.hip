@@ -76,6 +76,10 @@ const void *q6k_ksplit_sums_kernel(int sbw, int waves, int slots, int G) {
     return q6_ksplit_kernel<true>(sbw, waves, slots, G);
 }
 
+const void *q6k_ksplit_long_sums_kernel(int sbw, int waves, int slots, int G) {
+    return q6_ksplit_long_kernel<true>(sbw, waves, slots, G);
+}
+
 const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense) {
     if (slots != 1) return nullptr;
     if (dense) return waves <= 8 ? q6_sums_dense<8>(nc, pro) : q6_sums_dense<16>(nc, pro);

@@ -1,6 +1,7 @@
-"""GPU parity of the K-split kernel (one F32 column, rows of 4096 or 8192
-values; the waves of a workgroup split each row's super-blocks and quantise
-their own slice of the activation in registers).
+"""GPU parity of the K-split kernels (one F32 column; the waves of a
+workgroup split each row's super-blocks and quantise their own slice of the
+activation: in registers for rows of 4096 or 8192 values, into per-wave LDS
+slices for rows of other lengths up to 8 groups).
 
 Bar: outputs bit for bit equal to the tile kernel's (both sum every row in
 the same balanced tree over super-block positions) in every instantiated
@@ -214,6 +215,118 @@ def test_q6k_ksplit_group_sums_exact(Q, O, gpu, M, K):
             Q.set_geometry_override()
             Q.set_pipeline_override()
         where = f"Q6_K {M}x{K} rows/step {tr} waves {waves} slots {slots}"
+        assert torch.equal(y, y_prod), where
+        got = s16[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        assert np.array_equal(got, ref["s16"]), f"{where}: group sums differ"
+
+
+# -------------------------------------------------------- long rows ----
+# (rows per wave step, waves, steps in flight) of the long-row variants
+LONG_SHAPES = [(tr, w, s) for tr in (16, 8) for w in (8, 16) for s in (1, 2) if w >= tr]
+
+
+@pytest.mark.parametrize("M,K", [(4096, 14336), (1000, 14336), (37, 12544), (300, 3584), (513, 2048),
+                                 (96, 28672), (2000, 28672), (5, 256), (33, 20480)])
+def test_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
+    """Rows of any length up to 8 groups (the last group partial: 14336 =
+    3.5 groups, 12544 = 3 groups + 1 block, 3584 and 2048 under one group,
+    256 = one block): every long-row launch shape, with the default grid, a
+    few and 300 workgroups, against the tile kernel bit for bit; the tile
+    kernel against the oracle."""
+    wq, x = inputs(Q, M, K, seed=41)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    try:
+        Q.set_geometry_override(kernel=1)
+        y_tile = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+    rows = np.arange(M) if M <= 1024 else np.unique(
+        np.concatenate([[0, 1, M - 2, M - 1], np.random.default_rng(M).choice(M, 300, replace=False)]))
+    ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"tile {M}x{K}")
+    for tr, waves, slots in LONG_SHAPES:
+        for wgs in (0, few_workgroups(M), 300):
+            y = run_forced(Q, wd, K, xd, tr, waves, slots, wgs)
+            if not np.array_equal(y, y_tile):
+                bad = np.flatnonzero(y[0] != y_tile[0])
+                raise AssertionError(f"long {M}x{K} rows/step {tr} waves {waves} slots {slots} wgs {wgs}: "
+                                     f"{bad.size} outputs differ from the tile kernel, e.g. rows {bad[:5]}")
+
+
+@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048)])
+def test_ksplit_long_rows_sums_exact(Q, O, gpu, M, K):
+    """The long-row parity variants: S_qq of every lane in the row's blocks
+    and S_q of the in-register quantisation (blocks of the partial group
+    included) bit for bit against the oracle."""
+    import torch
+    wq, x = inputs(Q, M, K, seed=42)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    rows = np.unique(np.concatenate([[0, M // 2, M - 1], np.random.default_rng(M).choice(M, min(M, 100), replace=False)]))
+    ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x))
+    for tr, waves, slots in LONG_SHAPES:
+        try:
+            Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
+            Q.set_pipeline_override(slots=slots)
+            y, sums, sq = Q.mul_mat_vec_q_sums(wd, K, xd)
+            y_prod = Q.mul_mat_vec_q(wd, K, xd)
+        finally:
+            Q.set_geometry_override()
+            Q.set_pipeline_override()
+        where = f"long {M}x{K} rows/step {tr} waves {waves} slots {slots}"
+        assert torch.equal(y, y_prod), where
+        got = sums[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        assert np.array_equal(got, ref["sqq"]), f"{where}: S_qq differ"
+        assert np.array_equal(sq.cpu().numpy(), ref["sq"]), f"{where}: S_q differ"
+
+
+@pytest.mark.parametrize("M,K", [(4096, 14336), (1000, 14336), (37, 12544), (300, 3584), (96, 28672),
+                                 (5, 256), (33, 20480)])
+def test_q6k_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
+    """Q6_K rows of any length up to 8 groups: every long-row launch shape,
+    with the default grid, a few and 300 workgroups, against the Q6_K tile
+    kernel bit for bit; the tile kernel against the oracle."""
+    t6 = Q.GGML_TYPE_Q6_K
+    wq, x = inputs6(Q, M, K, seed=43)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    try:
+        Q.set_geometry_override(kernel=1)
+        y_tile = Q.mul_mat_vec_q(wd, K, xd, wtype=t6).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+    rows = np.arange(M) if M <= 1024 else np.unique(
+        np.concatenate([[0, 1, M - 2, M - 1], np.random.default_rng(M).choice(M, 300, replace=False)]))
+    ref = O.gemv_q6K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"Q6_K tile {M}x{K}")
+    for tr, waves, slots in LONG_SHAPES:
+        for wgs in (0, few_workgroups(M), 300):
+            y = run_forced6(Q, wd, K, xd, tr, waves, slots, wgs)
+            if not np.array_equal(y, y_tile):
+                bad = np.flatnonzero(y[0] != y_tile[0])
+                raise AssertionError(f"Q6_K long {M}x{K} rows/step {tr} waves {waves} slots {slots} wgs {wgs}: "
+                                     f"{bad.size} outputs differ from the tile kernel, e.g. rows {bad[:5]}")
+
+
+@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048)])
+def test_q6k_ksplit_long_rows_group_sums_exact(Q, O, gpu, M, K):
+    """The Q6_K long-row parity variants: every lane's int32 group sums,
+    from the -32 * sum q8 starting values staged per 16 values, bit for bit
+    against the oracle (the partial group's blocks included)."""
+    import torch
+    t6 = Q.GGML_TYPE_Q6_K
+    wq, x = inputs6(Q, M, K, seed=44)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    rows = np.unique(np.concatenate([[0, M // 2, M - 1], np.random.default_rng(M).choice(M, min(M, 100), replace=False)]))
+    ref = O.gemv_q6K_q8_1(wq[rows], K, O.quantize_q8_1(x))
+    for tr, waves, slots in LONG_SHAPES:
+        try:
+            Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
+            Q.set_pipeline_override(slots=slots)
+            y, s16, _ = Q.mul_mat_vec_q_sums(wd, K, xd, wtype=t6)
+            y_prod = Q.mul_mat_vec_q(wd, K, xd, wtype=t6)
+        finally:
+            Q.set_geometry_override()
+            Q.set_pipeline_override()
+        where = f"Q6_K long {M}x{K} rows/step {tr} waves {waves} slots {slots}"
         assert torch.equal(y, y_prod), where
         got = s16[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
         assert np.array_equal(got, ref["s16"]), f"{where}: group sums differ"

@@ -526,22 +526,25 @@ def test_production_kernel_sums(Q, O, gpu, M, K, N):
 
 def test_parity_variants_cover_every_kernel(Q, gpu):
     """The workloads' launches, whose sums test_production_kernel_sums
-    checks, include the K-split kernel (one column of 4096-value rows), the
-    matrix-core kernel (128256 x 4096, eight columns), the 8-wave register
-    path for several columns, 16-wave and 8-wave tile launches and both
-    staging routes.  (The block-per-lane kernel, no longer the automatic
-    choice anywhere, is checked through the override in
-    test_kernel_variants_against_oracle.)"""
+    checks, include the K-split kernel (one column: 4096-value rows with the
+    activation in registers, 14336- and 28672-value rows in the long-row
+    variant), the matrix-core kernel (128256 x 4096, eight columns), the
+    8-wave register path for several columns, 16-wave and 8-wave tile
+    launches and both staging routes.  (The block-per-lane kernel, no longer
+    the automatic choice anywhere, is checked through the override in
+    test_kernel_variants_against_oracle; the one-column tile kernel, which
+    runs unaligned activations, the pre-quantised route and the epilogues,
+    in the tests of those.)"""
     kinds = set()
     for p in _cases():
         M, K, N = p.values
         g = Q.geometry(K, M, N)
         kinds.add((g["kernel"], g["waves_per_wg"] if g["kernel"] == 1 else 0, N >= 3 and K <= 4096))
     assert Q.geometry(4096, 14336, 1)["kernel"] == 5 and Q.geometry(4096, 128256, 1)["kernel"] == 5
-    assert (5, 0, False) in kinds                      # K-split (the headline shape)
+    assert Q.geometry(14336, 4096, 1)["kernel"] == 5 and Q.geometry(28672, 8192, 1)["kernel"] == 5
+    assert (5, 0, False) in kinds                      # K-split (the headline shape, long rows)
     assert (4, 0, True) in kinds                       # matrix cores (128256 x 4096, eight columns)
     assert (1, 8, True) in kinds and (1, 16, True) in kinds   # several columns, 8 and 16 waves
-    assert (1, 16, False) in kinds                     # one column of long rows (4096 x 14336)
 
 
 @pytest.mark.parametrize("M", [8192, 14336, 20480])
