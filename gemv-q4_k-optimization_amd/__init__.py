@@ -54,6 +54,7 @@ SIGNATURES = {
     "q4k_ggml_mul_mat_vec_q": (_I, [_P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]),
     "q4k_subblock_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P, _P]),
     "q4k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
+    "q4k_gemv_geometry_q8_1": (_I, [_I64, _I64, _I64, _P]),
     "q4k_set_geometry_override": (_I, [ctypes.c_int32] * 4),
     "q4k_set_pipeline_override": (_I, [ctypes.c_int32] * 2),
     "q4k_read_probe": (_I, [_P, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
@@ -64,6 +65,7 @@ SIGNATURES = {
     "q6k_op_mul_mat_vec_q": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
     "q6k_group_sums": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P]),
     "q6k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
+    "q6k_gemv_geometry_q8_1": (_I, [_I64, _I64, _I64, _P]),
     "q4k_quantize_rows_q6_K": (_I, [_P, _P, _I64, _I64, _I]),
     # include/q4k_gguf.h
     "q4k_gguf_open": (_I, [ctypes.c_char_p, ctypes.POINTER(_P)]),
@@ -340,9 +342,16 @@ def set_pipeline_override(slots: int = 0, prologue: int = -1):
     _check(lib().q4k_set_pipeline_override(slots, prologue), "q4k_set_pipeline_override")
 
 
-def geometry(K: int, M: int, N: int, wtype: int = GGML_TYPE_Q4_K) -> dict:
+def geometry(K: int, M: int, N: int, wtype: int = GGML_TYPE_Q4_K, route: str = "f32") -> dict:
+    """The launch of an (M x K) x (K x N) product: route "f32" quantises
+    the F32 activation inside the GEMV launch, "q8_1" runs on a Q8_1
+    activation (op_mul_mat_vec_q, or mul_mat_vec_q with a workspace where
+    it quantises separately)."""
     out = (ctypes.c_int32 * 8)()
-    name, fn = _entry(wtype, "q4k_gemv_geometry", "q6k_gemv_geometry")
+    if route == "q8_1":
+        name, fn = _entry(wtype, "q4k_gemv_geometry_q8_1", "q6k_gemv_geometry_q8_1")
+    else:
+        name, fn = _entry(wtype, "q4k_gemv_geometry", "q6k_gemv_geometry")
     _check(fn(K, M, N, ctypes.cast(out, _P)), name)
     keys = ("rows_per_tile", "waves_per_wg", "workgroups", "lds_bytes", "cols_per_launch", "fused",
             "kernel", "rows_per_step")

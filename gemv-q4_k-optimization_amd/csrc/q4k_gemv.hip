@@ -195,6 +195,7 @@ struct Geometry {
     int prologue = 0;   // tile kernel: when the first weight loads go out (PRO)
     int slots = 2;      // tile kernel: groups in flight per wave (S)
     int mfma = 0;       // 1: matrix-core kernel (tiles of 16 rows; rows_base/rows_extra count tiles)
+    int mfma_ga = 0;    // matrix-core kernel: A operand from the Q8_1 buffer (pre-quantised route)
     int ks = 1;         // matrix-core kernel: waves sharing one tile
     int segs = 1;       // matrix-core kernel: summation segments of a row
     int ksplit = 0;     // K-split kernel: super-blocks per wave and group (0: another kernel)
@@ -259,13 +260,31 @@ static bool use_mfma(int64_t M, int64_t N, int64_t K) {
     return (N >= 6 && tiles >= 512) || (N == 5 && tiles >= 864);
 }
 
+// Where the pre-quantised route runs the matrix-core kernel with its A
+// operand read from the Q8_1 buffer (GA): rows longer than 8192 values,
+// five to eight columns, a tile per CU or more, and (the caller checks)
+// columns the staged kernel cannot hold in LDS.  Measured on MI355X (us per
+// op with a Q8_1 workspace, the quantiser launch included; GA against the
+// tile kernel): 4096 x 14336 N=8 18.66 against 22.63, N=6 17.64 / 19.04,
+// N=5 17.27 / 17.50; 8192 x 28672 N=8 45.75 / 66.01, N=6 42.65 / 62.90.
+// Slower at four columns (4096 x 14336 17.55 / 16.87, 8192 x 28672 39.93 /
+// 36.31) and than the staged matrix-core kernel where that holds the
+// columns (13824 x 5120 N=8 24.74 against 17.87, 8192 x 8192 N=8 18.03 /
+// 16.93, 28672 x 4096 N=8 22.99 / 21.70).  Two items in flight per wave,
+// not four (4096 x 14336 N=8 18.66 against 20.02).
+static bool use_mfma_ga(int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
+    return K > 8192 && N >= 5 && tiles >= 256;
+}
+
 // The matrix-core kernel: one workgroup per CU (at most one per tile) of 8
 // or 16 waves, the tiles of 16 rows split evenly over the workgroups, and as
 // many waves sharing a tile (KS) as leave every wave group a tile in the
 // first round -- KS at most the S summation segments of a row (S = min(8,
 // the largest power of two <= the super-blocks per row), a function of K
 // alone, which fixes the summation order).
-static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, int nc, int owgs, int owaves) {
+static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, int nc, int owgs, int owaves,
+                                   bool ga = false) {
     Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
@@ -282,6 +301,11 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
     const int64_t nt = g.rows_base + (g.rows_extra ? 1 : 0);
     g.waves = 16;  // measured faster than 8 where the kernel is chosen
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;
+    if (ga) {  // GA: its A operands in flight take 146 registers at 2 items
+        g.waves = 8;
+        const int os = g_ovr_slots.load();
+        g.slots = os == 2 || os == 4 ? os : 2;
+    }
     const int64_t nb = K / kQK;
     g.segs = 1;
     while (g.segs < kMfmaMaxSegs && 2 * g.segs <= nb) g.segs *= 2;
@@ -289,7 +313,8 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
     while (groups < g.waves && 2 * groups <= nt) groups *= 2;
     g.ks = g.waves / groups;
     while (g.ks > g.segs) g.ks /= 2;
-    g.lds = mfma_lds_bytes((int)K, nc, g.waves);
+    g.mfma_ga = ga ? 1 : 0;
+    g.lds = ga ? mfma_ga_lds_bytes((int)K, g.waves) : mfma_lds_bytes((int)K, nc, g.waves);
     g.lds_launch = g.lds <= max_lds / 2 ? max_lds / 2 + 256 : g.lds;  // one workgroup per CU
     return g;
 }
@@ -414,7 +439,7 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
 //    a gate each tile pairs one row of both weights (R = 2, one or two
 //    groups in flight).
 static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int fused = 0,
-                              int64_t mats = 1, bool f32_vec = true) {
+                              int64_t mats = 1, bool f32_vec = true, bool q81 = false) {
     Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
@@ -473,6 +498,11 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         g.lds_launch = g.lds;
         return g;
     }
+    // the matrix-core kernel with its A operand from the Q8_1 buffer: the
+    // pre-quantised route, up to 8 columns in one launch
+    if (q81 && !fused && mats == 1 && N <= kMfmaCols &&
+        (okern == 6 || (okern == 0 && use_mfma_ga(M, N, K) && mfma_lds_bytes((int)K, (int)N, 16) > max_lds)))
+        return pick_geometry_mfma(di, K, M, (int)N, owgs, owaves, true);
     if (!fused && mats == 1 && (okern == 4 || (okern == 0 && use_mfma(M, N, K)))) {
         int mc = (int)N;
         while (mc > 1 && mfma_lds_bytes((int)K, mc, 16) > max_lds) mc = (mc + 1) / 2;
@@ -708,6 +738,27 @@ static const void *mfma_kernel_for(int nc, int waves) {
     return waves > 8 ? mfma_kernel_nc<16>(nc) : mfma_kernel_nc<8>(nc);
 }
 
+template <int NIF>
+static const void *mfma_ga_kernel_nc(int nc) {
+    switch (nc) {
+        case 1: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<1, 8, false, true, NIF>);
+        case 2: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<2, 8, false, true, NIF>);
+        case 3: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<3, 8, false, true, NIF>);
+        case 4: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<4, 8, false, true, NIF>);
+        case 5: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<5, 8, false, true, NIF>);
+        case 6: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<6, 8, false, true, NIF>);
+        case 7: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<7, 8, false, true, NIF>);
+        case 8: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<8, 8, false, true, NIF>);
+        default: return nullptr;
+    }
+}
+
+// GA: 8-wave workgroups, 2 or 4 items in flight per wave
+static const void *mfma_ga_kernel_for(int nc, int waves, int nif) {
+    if (waves != 8) return nullptr;
+    return nif == 4 ? mfma_ga_kernel_nc<4>(nc) : mfma_ga_kernel_nc<2>(nc);
+}
+
 static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc, hipStream_t stream,
                        const BatchLaunch *bl = nullptr) {
     const void *fn = nullptr;
@@ -743,7 +794,10 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
     } else if (geo.mfma) {
-        fn = p.sums ? q4k_mfma_sums_kernel(nc, geo.waves) : mfma_kernel_for(nc, geo.waves);
+        if (geo.mfma_ga && (p.x || !p.y)) return Q4K_EINVAL;  // GA reads the Q8_1 buffer
+        fn = geo.mfma_ga ? (p.sums ? q4k_mfma_ga_sums_kernel(nc, geo.waves, geo.slots)
+                                   : mfma_ga_kernel_for(nc, geo.waves, geo.slots))
+                         : (p.sums ? q4k_mfma_sums_kernel(nc, geo.waves) : mfma_kernel_for(nc, geo.waves));
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
         p.rpw = geo.ks;
@@ -810,7 +864,7 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
     const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
     const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0;
-    Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused, mats, f32_vec);
+    Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused, mats, f32_vec, !x && y);
     if (bl || fused) {  // the batched and fused variants: 1 or 2 slots, prologue 0 or 1
         if (fused != kFusedGate) geo.R = 1;
         if (geo.slots > 2) geo.slots = 2;
@@ -825,10 +879,13 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
                               : !geo.bpl && (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31))
         return Q4K_EUNSUPPORTED;
     if (ldx > INT32_MAX || stride_col_y > INT32_MAX) return Q4K_EUNSUPPORTED;
+    // GA: the Q8_1 columns of a launch as one buffer of 32-bit offsets
+    if (geo.mfma_ga && (int64_t)geo.nc_chunk * stride_col_y * kQ81Bytes >= ((int64_t)1 << 31))
+        return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
-        if (!geo.bpl && !geo.ksplit) {
+        if (!geo.bpl && !geo.ksplit && !geo.mfma_ga) {
             g2.lds = geo.mfma ? mfma_lds_bytes((int)ne00, nc, geo.waves) : tile_lds_bytes((int)ne00, nc, geo.waves);
             if (g2.lds_launch < g2.lds) g2.lds_launch = g2.lds;
         }
@@ -942,12 +999,17 @@ static int mul_mat_vec_q_q4k(const void *src0, int64_t ne00, int64_t ne01, int64
     const int64_t ldx = nb11 / 4, ldd = nb1 / 4;
     const size_t need = q4k_q8_1_bytes(ne00, ne11);
     const bool ws_fits = workspace && workspace_bytes >= need && aligned(workspace, 4);
-    if (geo.nc_chunk >= ne11 && !(ws_fits && prefer_prequantised(ne00, ne11))) {
+    // the matrix-core kernel that reads its A operand from a Q8_1 copy is
+    // reached through that copy, with or without a workspace (so both give
+    // the pre-quantised entry point's bits)
+    const bool ga_route = pick_geometry(*di, ne00, ne01, ne11, 0, 1, false, true).mfma_ga != 0;
+    if (geo.nc_chunk >= ne11 && !ga_route && !(ws_fits && prefer_prequantised(ne00, ne11))) {
         // quantisation inside the GEMV launch
         return run_gemv(src0, ne00, ne01, nb01, src1, ldx, nullptr, 0, ne11, dst, ldd, s, nullptr, nullptr, so);
     }
-    // activation too large for one workgroup's LDS at this column count, or
-    // (with a workspace) too many values for every workgroup to quantise:
+    // activation too large for one workgroup's LDS at this column count,
+    // (with a workspace) too many values for every workgroup to quantise, or
+    // the matrix-core kernel with its A operand in the Q8_1 copy:
     // quantise once to a Q8_1 buffer and run the GEMV on it (in column
     // chunks when the columns do not fit the LDS together).
     void *buf = workspace;
@@ -1267,7 +1329,7 @@ int q4k_subblock_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01
 int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32_t workgroups,
                               int32_t kernel) {
     if (rows_per_tile < 0 || waves_per_wg < 0 || workgroups < 0) return Q4K_EINVAL;
-    if (kernel < 0 || kernel > 5) return Q4K_EINVAL;
+    if (kernel < 0 || kernel > 6) return Q4K_EINVAL;
     if (rows_per_tile != 0 && rows_per_tile != 1 && rows_per_tile != 2 && rows_per_tile != 4 &&
         !(kernel == 5 && (rows_per_tile == 8 || rows_per_tile == 16)))
         return Q4K_EINVAL;
@@ -1287,22 +1349,38 @@ int q4k_set_pipeline_override(int32_t slots, int32_t prologue) {
     return Q4K_OK;
 }
 
-int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) {
+static int gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, bool q81, int32_t out[8]) {
     if (!out || ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0 || ne11 < 1 || ne11 > Q4K_MAX_BATCH)
         return Q4K_EINVAL;
     DeviceInfo *di = nullptr;
     int st = device_info(&di);
     if (st != Q4K_OK) return st;
-    const Geometry g = pick_geometry(*di, ne00, ne01, ne11);
+    Geometry g = pick_geometry(*di, ne00, ne01, ne11, 0, 1, !q81, q81);
+    if (!q81) {  // the F32 entry reaches the GA kernel through a Q8_1 copy
+        const Geometry gq = pick_geometry(*di, ne00, ne01, ne11, 0, 1, false, true);
+        if (gq.mfma_ga) {
+            g = gq;
+            q81 = true;
+        }
+    }
     out[0] = g.R;
     out[1] = g.waves;
     out[2] = g.grid;
     out[3] = g.lds_launch;
     out[4] = g.nc_chunk;
     out[5] = g.nc_chunk >= ne11 ? 1 : 0;
-    out[6] = g.ksplit ? 5 : (g.mfma ? 4 : (g.bpl == 2 ? 3 : (g.bpl ? 2 : 1)));
+    out[6] = g.ksplit ? 5 : (g.mfma_ga ? 6 : (g.mfma ? 4 : (g.bpl == 2 ? 3 : (g.bpl ? 2 : 1))));
     out[7] = g.bpl ? g.rpw : g.R;
+    if (q81) out[5] = 0;
     return Q4K_OK;
+}
+
+int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) {
+    return gemv_geometry(ne00, ne01, ne11, false, out);
+}
+
+int q4k_gemv_geometry_q8_1(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) {
+    return gemv_geometry(ne00, ne01, ne11, true, out);
 }
 
 }  // extern "C"

@@ -27,6 +27,17 @@
 // partial results in LDS and, after a barrier, the workgroup combines the KS
 // partials of each tile and writes the outputs.
 //
+// A operand from the Q8_1 buffer (GA variants, pre-quantised activation):
+// each lane loads its 16 q8 bytes of every chunk straight from the AoS
+// block_q8_1 columns (the zero lanes' loads fall outside the buffer and read
+// zeros) instead of from an LDS copy of the whole activation, so the LDS
+// holds only the d8 of every (block, column) and the length of the rows is
+// not bounded by the LDS (eight 14336-value columns staged would take 170 KB
+// of its 160).  The sum of each block's q8, which the staged layout keeps
+// beside d8, comes from a second MFMA of the same A operand against a B of
+// ones (D[i][r] = the sum of A row i); d8 * that sum is the staged product,
+// so both variants compute the same bits.
+//
 // Summation order: a row's super-blocks form S = min(8, 2^floor(log2 nb))
 // segments [s nb/S, (s+1) nb/S), each summed in order; the segment sums are
 // combined in a fixed balanced binary tree.  A wave owns an aligned run of
@@ -77,6 +88,17 @@ __host__ __device__ constexpr int mfma_slot_off(int K, int nc, int waves) {
 __host__ __device__ constexpr int mfma_lds_bytes(int K, int nc, int waves) {
     return mfma_slot_off(K, nc, waves) + waves * kMfmaSlotBytes;
 }
+// GA variants: d8 of every (block, column) ([block][8 columns], float: K
+// bytes), the partials, one weight slot per wave.
+__host__ __device__ constexpr int mfma_ga_part_off(int K) { return K; }
+__host__ __device__ constexpr int mfma_ga_slot_off(int K, int waves) { return K + mfma_part_bytes(waves); }
+__host__ __device__ constexpr int mfma_ga_lds_bytes(int K, int waves) {
+    return mfma_ga_slot_off(K, waves) + waves * kMfmaSlotBytes;
+}
+// Bytes between the A operands of consecutive super-blocks and chunks in
+// the Q8_1 buffer (8 and 2 blocks of 36 bytes).
+constexpr uint32_t kGaSuperBytes = 8u * kQ81Bytes;
+constexpr uint32_t kGaChunkBytes = 2u * kQ81Bytes;
 
 // One super-block's weights as the MFMA lane needs them: the header of row
 // l % 16 and the 16 qs bytes of each chunk jj the lane's lane group reads.
@@ -104,10 +126,11 @@ struct MfmaLane {
     uint32_t selx, sely;  // byte selectors of its scales (sub-blocks hid, 2+hid, ...)
     uint32_t g_off[3];    // its chunks of an item: byte offsets from the item's first row
     int s_off[3];         // and in the wave's slot
+    uint32_t ga_off;      // GA: byte offset of its A operand (super-block 0, chunk 0) in the Q8_1 buffer
 };
 
 template <int NC>
-__device__ __forceinline__ MfmaLane mfma_lane(int K) {
+__device__ __forceinline__ MfmaLane mfma_lane(int K, int64_t stride_col_y = 0) {
     MfmaLane m;
     const int l = threadIdx.x & (kWave - 1);
     const int g = l >> 4;
@@ -127,6 +150,9 @@ __device__ __forceinline__ MfmaLane mfma_lane(int K) {
     const uint32_t h = (uint32_t)m.hid;
     m.selx = h | ((h + 2u) << 8) | ((h + 4u) << 16) | ((h + 6u) << 24);
     m.sely = h | ((h + 2u) << 8) | (h << 16) | ((h + 2u) << 24);
+    // GA: q8 bytes 16 (g & 1) .. of block 2jj + hia of column ca, at
+    // ga_off + kb * kGaSuperBytes + jj * kGaChunkBytes; zero lanes out of range
+    m.ga_off = data ? (uint32_t)(ca * stride_col_y + hia) * (uint32_t)kQ81Bytes + 4u + 16u * (uint32_t)(g & 1) : kOOB;
     return m;
 }
 
@@ -235,6 +261,71 @@ __device__ __forceinline__ void mfma_item(const GemvParams &p, const MfmaLane &l
     }
 }
 
+// GA: the lane's A operands of super-block kb (zeros for the zero lanes).
+__device__ __forceinline__ void mfma_load_a(__amdgpu_buffer_rsrc_t ry, const MfmaLane &ln, int kb, u32x4 (&a)[4]) {
+    const uint32_t o = ln.ga_off + (uint32_t)kb * kGaSuperBytes;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) a[jj] = load16(ry, o + (uint32_t)jj * kGaChunkBytes);
+}
+
+// mfma_item with the A operand in registers (GA): d8 from the LDS table,
+// d8 * sum q8 from the ones product.  SQ: also stores the block sums of q8
+// (lanes of weight row 0 hold them for their four columns).
+template <int NC, bool SUMS>
+__device__ __forceinline__ void mfma_item_ga(const GemvParams &p, const MfmaLane &ln, const uint8_t *lds, int kb,
+                                             const MfmaRegs &w, const u32x4 (&a)[4], float (&acc)[4], int row,
+                                             bool row_ok, bool sq_ok) {
+    const float *pd = reinterpret_cast<const float *>(lds) + (kb * 8 + ln.hid) * kMfmaCols + ln.c0;
+    i32x4 s[4], z[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+        u32x4 bv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bv[e] = (w.q[jj][e] >> ln.nshift) & 0x0f0f0f0fu;
+        const i32x4 av = __builtin_bit_cast(i32x4, a[jj]);
+        s[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bv), i32x4{0, 0, 0, 0}, 0, 0, 0);
+        z[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, i32x4{0x01010101, 0x01010101, 0x01010101, 0x01010101},
+                                                      i32x4{0, 0, 0, 0}, 0, 0, 0);
+    }
+    uint32_t low, split;
+    mfma_scales(w.h, ln, low, split);
+    const float d = half_bits_to_float(w.h[0]), dmin = half_bits_to_float(w.h[0] >> 16);
+    float t[4] = {0.0f, 0.0f, 0.0f, 0.0f}, u[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+        // d8 of the lane's four columns, sub-block 2jj + hid
+        const float4 d4 = *reinterpret_cast<const float4 *>(pd + 2 * kMfmaCols * jj);
+        const uint32_t scm = jj < 2 ? low : split;
+        const int sc = (int)((scm >> (8 * (jj & 1))) & 0xffu);
+        const float mf = (float)((scm >> (16 + 8 * (jj & 1))) & 0xffu);
+        const float d8[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float km = d8[v] * (float)z[jj][v];
+            t[v] = __builtin_fmaf(d8[v], (float)__mul24(s[jj][v], sc), t[v]);
+            u[v] = __builtin_fmaf(km, mf, u[v]);
+        }
+        if constexpr (SUMS) {
+            if (row_ok) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (ln.c0 + v < NC)
+                        p.sums[((int64_t)(ln.c0 + v) * p.M + row) * (p.K / 32) + kb * 8 + 2 * jj + ln.hid] = s[jj][v];
+            }
+            if (sq_ok && ln.wrow == 0) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (ln.c0 + v < NC) p.sq[(ln.c0 + v) * (p.K / 32) + kb * 8 + 2 * jj + ln.hid] = z[jj][v];
+            }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        acc[v] = __builtin_fmaf(d, t[v], acc[v]);
+        acc[v] = __builtin_fmaf(-dmin, u[v], acc[v]);
+    }
+}
+
 // Adds segment value v (the sum of one segment, local index t in the wave's
 // run) into the wave's subtree: l1, l2, l4 hold the pending left subtrees of
 // 1, 2 and 4 segments; returns the subtree that ends at t.
@@ -272,8 +363,10 @@ struct MfmaPos {
 // The kernel.  rows_base / rows_extra are the tile split: each workgroup
 // owns rows_base tiles of 16 rows, the first rows_extra one more;
 // p.rpw: KS, the waves that share one tile (1, 2, 4 or 8, at most S);
-// p.ntiles: S, the segments of a row.
-template <int NC, int WAVES, bool SUMS = false>
+// p.ntiles: S, the segments of a row.  GA: the A operand from the Q8_1
+// buffer p.y (which the GA variants require).  NIF: items in flight per
+// wave (2, or 4 in the GA variants).
+template <int NC, int WAVES, bool SUMS = false, bool GA = false, int NIF = 2>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KERNEL_ARGS) {
     static_assert(NC >= 1 && NC <= kMfmaCols, "up to 8 columns");
     static_assert(WAVES == 8 || WAVES == 16, "8 or 16 waves");
@@ -284,7 +377,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float2 *dks = reinterpret_cast<float2 *>(lds + mfma_dk_off(p.K, NC));
 
-    MfmaLane ln = mfma_lane<NC>(p.K);
+    MfmaLane ln = mfma_lane<NC>(p.K, p.stride_col_y);
     mfma_chunks(ln, p.row_stride);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int KS = p.rpw, S = p.ntiles;
@@ -304,12 +397,17 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
         make_rsrc(p.w + (int64_t)row0 * p.row_stride, nrows > 0 ? (uint32_t)(nrows * p.row_stride) : 0u);
 
     constexpr int kLPB = stage_lpb(NC);
-    constexpr int kPreR = pre_rounds(NC, NT);
+    constexpr int kPreR = GA ? 1 : pre_rounds(NC, NT);
     ActStage<kLPB, kPreR> xs;
     Q81Stage<kPreR> ys;
-    if (p.x) stage_f32_issue<kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
-    else stage_q81_issue<NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
-    __syncthreads();  // all activation loads of this CU are queued first
+    if constexpr (!GA) {
+        if (p.x) stage_f32_issue<kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+        else stage_q81_issue<NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+        __syncthreads();  // all activation loads of this CU are queued first
+    }
+    // GA: the Q8_1 columns as one buffer (columns stride_col_y blocks apart)
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(p.y, GA ? (uint32_t)((int64_t)(NC - 1) * p.stride_col_y * kQ81Bytes + (p.K / 32) * kQ81Bytes) : 0u);
 
     // items in order: rounds, and super-blocks kb0..kb1-1 of each; loads of
     // positions past the wave's last round or the workgroup's tiles read zeros
@@ -319,47 +417,78 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
         if (q.r >= rounds || tile >= nt) return kOOB;
         return (uint32_t)(tile * kMfmaRows * p.row_stride) + (uint32_t)q.kb * kBlockBytes;
     };
+    static_assert(NIF == 2 || (GA && NIF == 4), "items in flight");
     MfmaPos cur{0, kb0};
-    MfmaPos ahead = next(cur);
-    MfmaLoad w[2];
-    mfma_load(rs, item_off(cur), ln, w[0]);
-    mfma_load(rs, item_off(ahead), ln, w[1]);
-    ahead = next(ahead);
+    MfmaPos ahead = cur;
+    MfmaLoad w[NIF];
+    u32x4 av[GA ? NIF : 1][4];
+#pragma unroll
+    for (int k = 0; k < NIF; ++k) {
+        mfma_load(rs, item_off(ahead), ln, w[k]);
+        if constexpr (GA) mfma_load_a(ry, ln, ahead.kb, av[GA ? k : 0]);
+        ahead = next(ahead);
+    }
 
-    if (p.x)
-        stage_f32_finish<kLayoutMfma, kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, mfma_qcol(p.K),
-                                                q8s, dks, sq_out);
-    else
-        stage_q81_finish<kLayoutMfma, NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, mfma_qcol(p.K), q8s, dks,
-                                          sq_out);
-    // the zero area of the A operand, and the pairs of the padding columns
-    // (their outputs are dropped; zeros keep them finite)
-    if (threadIdx.x < kMfmaZeroBytes / 16)
-        reinterpret_cast<u32x4 *>(lds + mfma_zero_off(p.K, NC))[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (NC < kMfmaCols) {
-        for (int q = (int)threadIdx.x; q < (p.K / 32) * (kMfmaCols - NC); q += NT) {
-            const int blk = q / (kMfmaCols - NC), c = NC + q - blk * (kMfmaCols - NC);
-            dks[blk * kMfmaCols + c] = make_float2(0.0f, 0.0f);
+    if constexpr (GA) {
+        // d8 of every (block, column); zeros for the padding columns (their
+        // outputs are dropped; zeros keep them finite)
+        float *d8s = reinterpret_cast<float *>(lds);
+        for (int q = (int)threadIdx.x; q < (p.K / 32) * kMfmaCols; q += NT) {
+            const int blk = q >> 3, c = q & 7;
+            float dv = 0.0f;
+            if (c < NC)
+                dv = half_bits_to_float(
+                    *reinterpret_cast<const uint32_t *>(p.y + ((int64_t)c * p.stride_col_y + blk) * kQ81Bytes));
+            d8s[q] = dv;
+        }
+    } else {
+        if (p.x)
+            stage_f32_finish<kLayoutMfma, kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs,
+                                                    mfma_qcol(p.K), q8s, dks, sq_out);
+        else
+            stage_q81_finish<kLayoutMfma, NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, mfma_qcol(p.K), q8s,
+                                              dks, sq_out);
+        // the zero area of the A operand, and the pairs of the padding columns
+        // (their outputs are dropped; zeros keep them finite)
+        if (threadIdx.x < kMfmaZeroBytes / 16)
+            reinterpret_cast<u32x4 *>(lds + mfma_zero_off(p.K, NC))[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (NC < kMfmaCols) {
+            for (int q = (int)threadIdx.x; q < (p.K / 32) * (kMfmaCols - NC); q += NT) {
+                const int blk = q / (kMfmaCols - NC), c = NC + q - blk * (kMfmaCols - NC);
+                dks[blk * kMfmaCols + c] = make_float2(0.0f, 0.0f);
+            }
         }
     }
     __syncthreads();
 
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float l1[4] = {0.0f, 0.0f, 0.0f, 0.0f}, l2[4] = {0.0f, 0.0f, 0.0f, 0.0f}, l4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float *part = reinterpret_cast<float *>(lds + mfma_part_off(p.K, NC));
-    uint8_t *slot = lds + mfma_slot_off(p.K, NC, WAVES) + wave * kMfmaSlotBytes;
+    float *part = reinterpret_cast<float *>(lds + (GA ? mfma_ga_part_off(p.K) : mfma_part_off(p.K, NC)));
+    uint8_t *slot =
+        lds + (GA ? mfma_ga_slot_off(p.K, WAVES) : mfma_slot_off(p.K, NC, WAVES)) + wave * kMfmaSlotBytes;
     int t = 0;                            // local segment of the current item
     int seg_end = (seg0 + 1) * p.nb / S;  // its end (super-block)
-    // items go two at a time (slot k holds item it); an odd count ends with
-    // one item past the wave's, whose zeros add nothing
+    // items go NIF at a time (registers k hold item it); a count that is
+    // not a multiple ends with items past the wave's, whose zeros add nothing
     for (int it = 0; it < items;) {
 #pragma unroll
-        for (int k = 0; k < 2; ++k, ++it) {
+        for (int k = 0; k < NIF; ++k, ++it) {
             const int tile = group + ngroups * cur.r;
             const int row = row0 + tile * kMfmaRows + ln.wrow;
             const MfmaRegs wr = mfma_stage(slot, ln, w[k]);
             mfma_load(rs, item_off(ahead), ln, w[k]);
-            mfma_item<NC, SUMS>(p, ln, lds, cur.kb, wr, acc, row, SUMS && it < items && tile < nt && row < p.M);
+            if constexpr (GA) {
+                u32x4 a[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) a[jj] = av[k][jj];
+                mfma_load_a(ry, ln, ahead.kb, av[k]);
+                // sq: the group of waves holding tile 0 of workgroup 0 covers
+                // every super-block once
+                mfma_item_ga<NC, SUMS>(p, ln, lds, cur.kb, wr, a, acc, row, SUMS && it < items && tile < nt && row < p.M,
+                                       SUMS && blockIdx.x == 0 && group == 0 && cur.r == 0 && it < items);
+            } else {
+                mfma_item<NC, SUMS>(p, ln, lds, cur.kb, wr, acc, row, SUMS && it < items && tile < nt && row < p.M);
+            }
             ahead = next(ahead);
             const MfmaPos done = cur;
             cur = next(cur);

@@ -80,9 +80,11 @@ const void *q4k_bpl_sums_kernel(int waves);
 const void *q4k_mfma_sums_kernel(int nc, int waves);
 const void *q4k_ksplit_sums_kernel(int sbw, int waves, int slots, int G);
 const void *q4k_ksplit_long_sums_kernel(int sbw, int waves, int slots, int G);
+const void *q4k_mfma_ga_sums_kernel(int nc, int waves, int nif);
 const void *q6k_mfma_sums_kernel(int nc, int waves);
 const void *q6k_ksplit_sums_kernel(int sbw, int waves, int slots, int G);
 const void *q6k_ksplit_long_sums_kernel(int sbw, int waves, int slots, int G);
+const void *q6k_mfma_ga_sums_kernel(int nc, int waves);
 const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense);
 
 // Q6_K weight checks and launch (q6k_gemv.hip), for the type-dispatching

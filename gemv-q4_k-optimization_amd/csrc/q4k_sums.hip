@@ -70,6 +70,26 @@ const void *q4k_mfma_sums_kernel(int nc, int waves) {
     return waves > 8 ? mfma_sums_nc<16>(nc) : mfma_sums_nc<8>(nc);
 }
 
+template <int NIF>
+static const void *mfma_ga_sums_nc(int nc) {
+    switch (nc) {
+        case 1: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<1, 8, true, true, NIF>);
+        case 2: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<2, 8, true, true, NIF>);
+        case 3: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<3, 8, true, true, NIF>);
+        case 4: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<4, 8, true, true, NIF>);
+        case 5: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<5, 8, true, true, NIF>);
+        case 6: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<6, 8, true, true, NIF>);
+        case 7: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<7, 8, true, true, NIF>);
+        case 8: return reinterpret_cast<const void *>(&gemv_q4k_mfma_kernel<8, 8, true, true, NIF>);
+        default: return nullptr;
+    }
+}
+
+const void *q4k_mfma_ga_sums_kernel(int nc, int waves, int nif) {
+    if (waves != 8) return nullptr;
+    return nif == 4 ? mfma_ga_sums_nc<4>(nc) : mfma_ga_sums_nc<2>(nc);
+}
+
 const void *q4k_ksplit_sums_kernel(int sbw, int waves, int slots, int G) {
     return ksplit_kernel<true>(sbw, waves, slots, G);
 }

@@ -96,6 +96,7 @@ struct Q6Geometry {
     int ksplit = 0;  // K-split kernel: super-blocks per wave and group (0: another kernel)
     int ks_tr = 0;   // K-split kernel: rows per wave step (16 / ksplit)
     int ks_long = 0; // K-split kernel for rows of any length (activation slices in LDS)
+    int mfma_ga = 0; // matrix-core kernel: A operand from the Q8_1 buffer (pre-quantised route)
 };
 
 // The K-split kernel's launch shape: rows_per_step TR = 16 / SBW (4, 8, 16;
@@ -181,6 +182,20 @@ static bool q6_ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, i
 //    (13824 x 5120 N=5 21.7 -> 21.0, 28672 x 5120 N=5 39.8 -> 33.3).  At 8192
 //    values five or six columns are slower (28672 x 8192 N=6 48.9 against
 //    51.4), and 4096 rows are slower everywhere.
+// Where the pre-quantised route runs the matrix-core kernel with its A
+// operand read from the Q8_1 buffer (GA): rows longer than 8192 values, a
+// tile per CU or more, eight columns, or five to eight of rows longer than
+// 16384 values, and (the caller checks) columns the staged kernel cannot
+// hold in LDS.  Measured on MI355X (us per op with a Q8_1 workspace, the
+// quantiser launch included; GA against the tile kernel): 4096 x 14336 N=8
+// 24.84 against 27.35; 8192 x 28672 N=8 65.54 / 91.20, N=5 64.46 / 85.28.
+// Slower at 4096 x 14336 with six or five columns (24.61 / 23.28, 24.47 /
+// 21.26) and four (20.79 / 20.13).
+static bool use_mfma_q6_ga(int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
+    return K > 8192 && tiles >= 256 && (N == 8 || (N >= 5 && K > 16384));
+}
+
 static bool use_mfma_q6(int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
     if (K <= 4096) return (N == 8 && tiles >= 896) || (N >= 6 && tiles >= 2048);
@@ -192,7 +207,8 @@ static bool use_mfma_q6(int64_t M, int64_t N, int64_t K) {
 // most one per tile) of 8 or 16 waves, the tiles split evenly over the
 // workgroups, and KS waves sharing a tile, KS at most the S summation
 // segments of a row (a function of K alone, which fixes the summation order).
-static Q6Geometry pick_geometry_q6_mfma(const DeviceInfo &di, int64_t K, int64_t M, int nc, int owgs, int owaves) {
+static Q6Geometry pick_geometry_q6_mfma(const DeviceInfo &di, int64_t K, int64_t M, int nc, int owgs, int owaves,
+                                        bool ga = false) {
     Q6Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
@@ -208,6 +224,7 @@ static Q6Geometry pick_geometry_q6_mfma(const DeviceInfo &di, int64_t K, int64_t
     const int64_t nt = g.rows_base + (g.rows_extra ? 1 : 0);
     g.waves = 16;
     if (owaves >= 1 && owaves <= 16) g.waves = owaves > 8 ? 16 : 8;
+    if (ga) g.waves = 8;  // GA: its A operands in flight need more than 16 waves' registers
     const int64_t nb = K / kQK;
     g.segs = 1;
     while (g.segs < kMfmaMaxSegs && 2 * g.segs <= nb) g.segs *= 2;
@@ -215,7 +232,8 @@ static Q6Geometry pick_geometry_q6_mfma(const DeviceInfo &di, int64_t K, int64_t
     while (groups < g.waves && 2 * groups <= nt) groups *= 2;
     g.ks = g.waves / groups;
     while (g.ks > g.segs) g.ks /= 2;
-    g.lds = q6m_lds_bytes((int)K, nc, g.waves);
+    g.mfma_ga = ga ? 1 : 0;
+    g.lds = ga ? q6m_ga_lds_bytes((int)K, g.waves) : q6m_lds_bytes((int)K, nc, g.waves);
     g.lds_launch = g.lds <= max_lds / 2 ? max_lds / 2 + 256 : g.lds;  // one workgroup per CU
     return g;
 }
@@ -228,7 +246,7 @@ static Q6Geometry pick_geometry_q6_mfma(const DeviceInfo &di, int64_t K, int64_t
 // weight requests in flight (16 waves x 2 groups, 27.5 MB over the chip)
 // delay the activation loads more than they hide latency.
 static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int64_t mats = 1,
-                                   int fused = kFusedNone, bool f32_vec = true) {
+                                   int fused = kFusedNone, bool f32_vec = true, bool q81 = false) {
     Q6Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
@@ -248,6 +266,12 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
             return pick_geometry_q6_ksplit(di, K, M, tr, kw, 0, os == 1 || os == 2 ? os : ks);
         }
     }
+    // the matrix-core kernel with its A operand from the Q8_1 buffer: the
+    // pre-quantised route, up to 8 columns in one launch
+    if (q81 && fused == kFusedNone && mats == 1 && N <= kMfmaCols &&
+        (okern == 6 ||
+         (okern == 0 && use_mfma_q6_ga(M, N, K) && q6m_lds_bytes((int)K, (int)N, 16) > max_lds)))
+        return pick_geometry_q6_mfma(di, K, M, (int)N, g_ovr_wgs.load(), g_ovr_waves.load(), true);
     if (fused == kFusedNone && mats == 1 && (okern == 4 || (okern == 0 && use_mfma_q6(M, N, K)))) {
         int mc = (int)N;
         while (mc > 1 && q6m_lds_bytes((int)K, mc, 16) > max_lds) mc = (mc + 1) / 2;
@@ -375,6 +399,22 @@ static const void *q6_mfma_kernel_for(int nc, int waves) {
     return waves > 8 ? q6_mfma_kernel_nc<16>(nc) : q6_mfma_kernel_nc<8>(nc);
 }
 
+// GA: 8-wave workgroups
+static const void *q6_mfma_ga_kernel_for(int nc, int waves) {
+    if (waves != 8) return nullptr;
+    switch (nc) {
+        case 1: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<1, 8, false, true>);
+        case 2: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<2, 8, false, true>);
+        case 3: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<3, 8, false, true>);
+        case 4: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<4, 8, false, true>);
+        case 5: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<5, 8, false, true>);
+        case 6: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<6, 8, false, true>);
+        case 7: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<7, 8, false, true>);
+        case 8: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<8, 8, false, true>);
+        default: return nullptr;
+    }
+}
+
 int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01) {
     if (ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0) return Q4K_EINVAL;
     const int64_t row_bytes = ne00 / kQK * kQ6Bytes;
@@ -397,7 +437,7 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
     if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
     const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
     const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0;
-    const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats, fused, f32_vec);
+    const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats, fused, f32_vec, !x && y);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // a wave's rows (the matrix-core kernel: a workgroup's tiles; the K-split
     // kernel: a workgroup's rows and one step past them) are addressed with
@@ -407,12 +447,16 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
                      : (int64_t)(geo.rows_base / geo.waves + 2) * nb01 >= ((int64_t)1 << 31))
         return Q4K_EUNSUPPORTED;
     if (ldx > INT32_MAX || stride_col_y > INT32_MAX) return Q4K_EUNSUPPORTED;
+    // GA: the Q8_1 columns of a launch as one buffer of 32-bit offsets
+    if (geo.mfma_ga && (int64_t)geo.nc_chunk * stride_col_y * kQ81Bytes >= ((int64_t)1 << 31))
+        return Q4K_EUNSUPPORTED;
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         // a last chunk of under kDenseMinCols columns is staged padded
         const bool dense = geo.dense && nc >= kDenseMinCols;
         int lds_launch = geo.lds_launch;
-        const int lds = geo.mfma     ? q6m_lds_bytes((int)ne00, nc, geo.waves)
+        const int lds = geo.mfma_ga  ? geo.lds
+                        : geo.mfma   ? q6m_lds_bytes((int)ne00, nc, geo.waves)
                         : geo.ksplit ? geo.lds
                                      : q6_tile_lds_bytes((int)ne00, nc, geo.waves, dense);
         if (lds > di->max_lds) return Q4K_EUNSUPPORTED;
@@ -444,12 +488,14 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         }
         const void *fn = geo.ks_long  ? q6_ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.ksplit ? q6_ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
+                         : geo.mfma_ga ? q6_mfma_ga_kernel_for(nc, geo.waves)
                          : geo.mfma ? q6_mfma_kernel_for(nc, geo.waves)
                          : bl       ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
                                     : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
         if (geo.ksplit && (nc != 1 || fused || bl || !p.x || !p.vec_ok)) return Q4K_EINVAL;
         if (geo.mfma) {
             if (fused || bl) return Q4K_EINVAL;
+            if (geo.mfma_ga && (p.x || !p.y)) return Q4K_EINVAL;  // GA reads the Q8_1 buffer
             p.rpw = geo.ks;
             p.ntiles = geo.segs;
         }
@@ -457,6 +503,7 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             if (fused || bl) return Q4K_EINVAL;
             fn = geo.ks_long  ? q6k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                  : geo.ksplit ? q6k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
+                 : geo.mfma_ga ? q6k_mfma_ga_sums_kernel(nc, geo.waves)
                  : geo.mfma ? q6k_mfma_sums_kernel(nc, geo.waves)
                             : q6k_sums_kernel(nc, geo.waves, geo.prologue, geo.slots, dense);
             if (!fn) return Q4K_EUNSUPPORTED;  // a launch shape with no parity variant (overrides)
@@ -507,10 +554,15 @@ static int mul_mat_vec_q_q6k(const void *src0, int64_t ne00, int64_t ne01, int64
     const int64_t ldx = nb11 / 4, ldd = nb1 / 4;
     const size_t need = q4k_q8_1_bytes(ne00, ne11);
     const bool ws_fits = workspace && workspace_bytes >= need && aligned(workspace, 4);
-    if (geo.nc_chunk >= ne11 && !(ws_fits && prefer_prequantised(ne00, ne11)))
+    // the matrix-core kernel that reads its A operand from a Q8_1 copy is
+    // reached through that copy, with or without a workspace (so both give
+    // the pre-quantised entry point's bits)
+    const bool ga_route = pick_geometry_q6(*di, ne00, ne01, ne11, 1, kFusedNone, false, true).mfma_ga != 0;
+    if (geo.nc_chunk >= ne11 && !ga_route && !(ws_fits && prefer_prequantised(ne00, ne11)))
         return run_gemv_q6(src0, ne00, ne01, nb01, src1, ldx, nullptr, 0, ne11, dst, ldd, s, nullptr, nullptr, so);
-    // activation too large for one workgroup's LDS at this column count, or
-    // (with a workspace) too many values for every workgroup to quantise:
+    // activation too large for one workgroup's LDS at this column count,
+    // (with a workspace) too many values for every workgroup to quantise, or
+    // the matrix-core kernel with its A operand in the Q8_1 copy:
     // quantise once to a Q8_1 buffer and run the GEMV on it
     void *buf = workspace;
     bool owned = false;
@@ -612,22 +664,38 @@ int q6k_group_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, c
     return Q4K_OK;
 }
 
-int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) {
+static int gemv_geometry_q6(int64_t ne00, int64_t ne01, int64_t ne11, bool q81, int32_t out[8]) {
     if (!out || ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0 || ne11 < 1 || ne11 > Q4K_MAX_BATCH)
         return Q4K_EINVAL;
     DeviceInfo *di = nullptr;
     const int st = device_info(&di);
     if (st != Q4K_OK) return st;
-    const Q6Geometry g = pick_geometry_q6(*di, ne00, ne01, ne11);
+    Q6Geometry g = pick_geometry_q6(*di, ne00, ne01, ne11, 1, kFusedNone, !q81, q81);
+    if (!q81) {  // the F32 entry reaches the GA kernel through a Q8_1 copy
+        const Q6Geometry gq = pick_geometry_q6(*di, ne00, ne01, ne11, 1, kFusedNone, false, true);
+        if (gq.mfma_ga) {
+            g = gq;
+            q81 = true;
+        }
+    }
     out[0] = g.ksplit ? g.ks_tr : (g.mfma ? kMfmaRows : 1);
     out[1] = g.waves;
     out[2] = g.grid;
     out[3] = g.lds_launch;
     out[4] = g.nc_chunk;
     out[5] = g.nc_chunk >= ne11 ? 1 : 0;
-    out[6] = g.ksplit ? 5 : (g.mfma ? 4 : 1);
+    out[6] = g.ksplit ? 5 : (g.mfma_ga ? 6 : (g.mfma ? 4 : 1));
     out[7] = g.slots;
+    if (q81) out[5] = 0;
     return Q4K_OK;
+}
+
+int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) {
+    return gemv_geometry_q6(ne00, ne01, ne11, false, out);
+}
+
+int q6k_gemv_geometry_q8_1(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) {
+    return gemv_geometry_q6(ne00, ne01, ne11, true, out);
 }
 
 }  // extern "C"

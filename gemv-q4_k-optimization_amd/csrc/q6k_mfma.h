@@ -31,7 +31,10 @@
 // exact in float) and t += d8 * I; the row's d / 4 scales the item.
 //
 // Work split, summation segments, rounds and the reduction are those of the
-// Q4_K matrix-core kernel (q4k_mfma.h): the result depends on K alone.  A
+// Q4_K matrix-core kernel (q4k_mfma.h): the result depends on K alone.  As
+// there, the GA variants (pre-quantised route) read the A operand straight
+// from the Q8_1 columns: chunk j of super-block kb of column c is q8 bytes
+// 16 (j & 1) .. of block 8 kb + 2g + j / 2; the LDS holds only the d8 table.  A
 // lane's eight column accumulators are summed over the four lane groups of
 // its row at each segment end (two lane swaps), leaving lane l the columns
 // 2(l / 16) and 2(l / 16) + 1 of row l % 16.
@@ -87,10 +90,11 @@ struct Q6MLane {
     int a_step[2];     // its advance per chunk (16 (kb * 16 + j) from there): 16 (data lanes) or 0
     int dk_off;        // LDS byte offset of d8 of its block 2g, super-block 0, column 0
     uint32_t g_off[4]; // its chunks of an item: byte offsets from the item's first row
+    uint32_t ga_off[2];  // GA: byte offset of its A operand of super-block 0, chunk 0 in the Q8_1 buffer
 };
 
-template <int NC>
-__device__ __forceinline__ Q6MLane q6m_lane(int K) {
+template <int NC, bool GA = false>
+__device__ __forceinline__ Q6MLane q6m_lane(int K, int64_t stride_col_y = 0) {
     Q6MLane m;
     const int l = threadIdx.x & (kWave - 1);
     const int g = l >> 4;
@@ -110,9 +114,30 @@ __device__ __forceinline__ Q6MLane q6m_lane(int K) {
         const bool dq = data && c < NC;
         m.a_off[q] = dq ? c * mfma_qcol(K) + 64 * g : q6m_zero_off(K, NC) + 16 * (l & 7);
         m.a_step[q] = dq ? 16 : 0;
+        m.ga_off[q] = dq ? (uint32_t)(c * stride_col_y + 2 * g) * (uint32_t)kQ81Bytes + 4u : kOOB;
     }
-    m.dk_off = q6m_dk_off(K, NC) + (2 * g) * kMfmaCols * 4;
+    m.dk_off = (GA ? 0 : q6m_dk_off(K, NC)) + (2 * g) * kMfmaCols * 4;
     return m;
+}
+
+// GA LDS layout: the d8 table ([block][8 columns], float: K bytes), the
+// partials, one weight slot per wave.
+__host__ __device__ constexpr int q6m_ga_part_off(int K) { return K; }
+__host__ __device__ constexpr int q6m_ga_slot_off(int K, int waves) { return K + q6m_part_bytes(waves); }
+__host__ __device__ constexpr int q6m_ga_lds_bytes(int K, int waves) {
+    return q6m_ga_slot_off(K, waves) + waves * kQ6SlotBytes;
+}
+
+// GA: the lane's A operands of super-block kb, chunk j at a[j][q] (zeros for
+// the zero lanes and the halves past NC).
+template <int NQ>
+__device__ __forceinline__ void q6m_load_a(__amdgpu_buffer_rsrc_t ry, const Q6MLane &ln, int kb, u32x4 (&a)[4][2]) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        const uint32_t o = ln.ga_off[q] + (uint32_t)kb * kGaSuperBytes;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j][q] = load16(ry, o + (uint32_t)(36 * (j >> 1) + 16 * (j & 1)));
+    }
 }
 
 // The lane's chunk offsets of an item (rows row_stride bytes apart); chunks
@@ -160,10 +185,10 @@ __device__ __forceinline__ uint32_t q6m_bytes(uint32_t ql, uint32_t qhx, uint32_
 // One item: eight MFMAs (four for up to four columns) and the scaling of
 // their outputs into acc (the lane's row and scale groups, eight columns).
 // SUMS: also stores the int32 group sums.
-template <int NC, bool SUMS>
+template <int NC, bool SUMS, bool GA = false>
 __device__ __forceinline__ void q6m_item(const GemvParams &p, const Q6MLane &ln, const uint8_t *lds,
                                          const uint8_t *slot, int kb, float (&acc)[kMfmaCols], int row,
-                                         bool row_ok) {
+                                         bool row_ok, const u32x4 (&ga)[4][2]) {
     constexpr int NQ = NC > 4 ? 2 : 1;
     const uint8_t *wr = slot + ln.wrow * kQ6SlotPitch;
     const int h = ln.g >> 1;
@@ -196,7 +221,7 @@ __device__ __forceinline__ void q6m_item(const GemvParams &p, const Q6MLane &ln,
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
                 const u32x4 av =
-                    *reinterpret_cast<const u32x4 *>(lds + ln.a_off[q] + ln.a_step[q] * (16 * kb + j));
+                    GA ? ga[j][q] : *reinterpret_cast<const u32x4 *>(lds + ln.a_off[q] + ln.a_step[q] * (16 * kb + j));
                 s[jj][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, av),
                                                                  __builtin_bit_cast(i32x4, bv),
                                                                  i32x4{0, 0, 0, 0}, 0, 0, 0);
@@ -285,8 +310,9 @@ __device__ __forceinline__ void q6m_tree_push(int t, float (&v)[2], float (&l1)[
 // The kernel.  rows_base / rows_extra are the tile split: each workgroup
 // owns rows_base tiles of 16 rows, the first rows_extra one more;
 // p.rpw: KS, the waves that share one tile (1, 2, 4 or 8, at most S);
-// p.ntiles: S, the segments of a row.
-template <int NC, int WAVES, bool SUMS = false>
+// p.ntiles: S, the segments of a row.  GA: the A operand from the Q8_1
+// buffer p.y (which the GA variants require).
+template <int NC, int WAVES, bool SUMS = false, bool GA = false>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KERNEL_ARGS) {
     static_assert(NC >= 1 && NC <= kMfmaCols, "up to 8 columns");
     static_assert(WAVES == 8 || WAVES == 16, "8 or 16 waves");
@@ -296,7 +322,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KE
     int8_t *q8s = reinterpret_cast<int8_t *>(lds);
     float *dks = reinterpret_cast<float *>(lds + q6m_dk_off(p.K, NC));
 
-    Q6MLane ln = q6m_lane<NC>(p.K);
+    Q6MLane ln = q6m_lane<NC, GA>(p.K, p.stride_col_y);
     q6m_chunks(ln, p.row_stride);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int KS = p.rpw, S = p.ntiles;
@@ -314,13 +340,18 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KE
     const __amdgpu_buffer_rsrc_t rs =
         make_rsrc(p.w + (int64_t)row0 * p.row_stride, nrows > 0 ? (uint32_t)(nrows * p.row_stride) : 0u);
 
+    constexpr int NQ = NC > 4 ? 2 : 1;
     constexpr int kLPB = stage_lpb(NC);
-    constexpr int kPreR = pre_rounds(NC, NT);
+    constexpr int kPreR = GA ? 1 : pre_rounds(NC, NT);
     ActStage<kLPB, kPreR> xs;
     Q81Stage<kPreR> ys;
-    if (p.x) stage_f32_issue<kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
-    else stage_q81_issue<NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
-    __syncthreads();  // all activation loads of this CU are queued first
+    if constexpr (!GA) {
+        if (p.x) stage_f32_issue<kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs);
+        else stage_q81_issue<NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
+        __syncthreads();  // all activation loads of this CU are queued first
+    }
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(p.y, GA ? (uint32_t)((int64_t)(NC - 1) * p.stride_col_y * kQ81Bytes + (p.K / 32) * kQ81Bytes) : 0u);
 
     auto next = [&](MfmaPos q) -> MfmaPos { return q.kb + 1 < kb1 ? MfmaPos{q.r, q.kb + 1} : MfmaPos{q.r + 1, kb0}; };
     auto item_off = [&](MfmaPos q) -> uint32_t {
@@ -329,25 +360,43 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KE
         return (uint32_t)(tile * kMfmaRows * p.row_stride) + (uint32_t)q.kb * kQ6Bytes;
     };
     MfmaPos cur{0, kb0};
-    MfmaPos ahead = next(cur);
+    MfmaPos ahead = cur;
     Q6MLoad w[2];
-    q6m_load(rs, item_off(cur), ln, w[0]);
-    q6m_load(rs, item_off(ahead), ln, w[1]);
-    ahead = next(ahead);
+    u32x4 av[GA ? 2 : 1][4][2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        q6m_load(rs, item_off(ahead), ln, w[k]);
+        if constexpr (GA) q6m_load_a<NQ>(ry, ln, ahead.kb, av[GA ? k : 0]);
+        ahead = next(ahead);
+    }
 
-    if (p.x)
-        stage_f32_finish<kLayoutMfmaQ6, kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs, mfma_qcol(p.K),
-                                                  q8s, dks);
-    else
-        stage_q81_finish<kLayoutMfmaQ6, NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, mfma_qcol(p.K), q8s, dks);
-    // the zero area of the A operand, and d8 of the padding columns (their
-    // outputs are dropped; zeros keep them finite)
-    if (threadIdx.x < kMfmaZeroBytes / 16)
-        reinterpret_cast<u32x4 *>(lds + q6m_zero_off(p.K, NC))[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
-    if constexpr (NC < kMfmaCols) {
-        for (int q = (int)threadIdx.x; q < (p.K / 32) * (kMfmaCols - NC); q += NT) {
-            const int blk = q / (kMfmaCols - NC), c = NC + q - blk * (kMfmaCols - NC);
-            dks[blk * kMfmaCols + c] = 0.0f;
+    if constexpr (GA) {
+        // d8 of every (block, column); zeros for the padding columns
+        float *d8s = reinterpret_cast<float *>(lds);
+        for (int q = (int)threadIdx.x; q < (p.K / 32) * kMfmaCols; q += NT) {
+            const int blk = q >> 3, c = q & 7;
+            float dv = 0.0f;
+            if (c < NC)
+                dv = half_bits_to_float(
+                    *reinterpret_cast<const uint32_t *>(p.y + ((int64_t)c * p.stride_col_y + blk) * kQ81Bytes));
+            d8s[q] = dv;
+        }
+    } else {
+        if (p.x)
+            stage_f32_finish<kLayoutMfmaQ6, kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs,
+                                                      mfma_qcol(p.K), q8s, dks);
+        else
+            stage_q81_finish<kLayoutMfmaQ6, NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys, mfma_qcol(p.K), q8s,
+                                                dks);
+        // the zero area of the A operand, and d8 of the padding columns (their
+        // outputs are dropped; zeros keep them finite)
+        if (threadIdx.x < kMfmaZeroBytes / 16)
+            reinterpret_cast<u32x4 *>(lds + q6m_zero_off(p.K, NC))[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+        if constexpr (NC < kMfmaCols) {
+            for (int q = (int)threadIdx.x; q < (p.K / 32) * (kMfmaCols - NC); q += NT) {
+                const int blk = q / (kMfmaCols - NC), c = NC + q - blk * (kMfmaCols - NC);
+                dks[blk * kMfmaCols + c] = 0.0f;
+            }
         }
     }
     __syncthreads();
@@ -356,8 +405,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KE
 #pragma unroll
     for (int c = 0; c < kMfmaCols; ++c) acc[c] = 0.0f;
     float l1[2] = {0.0f, 0.0f}, l2[2] = {0.0f, 0.0f}, l4[2] = {0.0f, 0.0f};
-    float *part = reinterpret_cast<float *>(lds + q6m_part_off(p.K, NC));
-    uint8_t *slot = lds + q6m_slot_off(p.K, NC, WAVES) + wave * kQ6SlotBytes;
+    float *part = reinterpret_cast<float *>(lds + (GA ? q6m_ga_part_off(p.K) : q6m_part_off(p.K, NC)));
+    uint8_t *slot = lds + (GA ? q6m_ga_slot_off(p.K, WAVES) : q6m_slot_off(p.K, NC, WAVES)) + wave * kQ6SlotBytes;
     int t = 0;                            // local segment of the current item
     int seg_end = (seg0 + 1) * p.nb / S;  // its end (super-block)
     // items go two at a time (load slot k holds item it); an odd count ends
@@ -369,7 +418,19 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KE
             const int row = row0 + tile * kMfmaRows + ln.wrow;
             q6m_stage(slot, ln, w[k]);
             q6m_load(rs, item_off(ahead), ln, w[k]);
-            q6m_item<NC, SUMS>(p, ln, lds, slot, cur.kb, acc, row, SUMS && it < items && tile < nt && row < p.M);
+            if constexpr (GA) {
+                u32x4 a[4][2];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int q = 0; q < NQ; ++q) a[j][q] = av[k][j][q];
+                q6m_load_a<NQ>(ry, ln, ahead.kb, av[k]);
+                q6m_item<NC, SUMS, true>(p, ln, lds, slot, cur.kb, acc, row,
+                                         SUMS && it < items && tile < nt && row < p.M, a);
+            } else {
+                q6m_item<NC, SUMS>(p, ln, lds, slot, cur.kb, acc, row, SUMS && it < items && tile < nt && row < p.M,
+                                   av[0]);
+            }
             ahead = next(ahead);
             const MfmaPos done = cur;
             cur = next(cur);

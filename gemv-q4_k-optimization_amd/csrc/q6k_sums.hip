@@ -72,6 +72,21 @@ const void *q6k_mfma_sums_kernel(int nc, int waves) {
     return waves > 8 ? q6_mfma_sums_nc<16>(nc) : q6_mfma_sums_nc<8>(nc);
 }
 
+const void *q6k_mfma_ga_sums_kernel(int nc, int waves) {
+    if (waves != 8) return nullptr;
+    switch (nc) {
+        case 1: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<1, 8, true, true>);
+        case 2: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<2, 8, true, true>);
+        case 3: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<3, 8, true, true>);
+        case 4: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<4, 8, true, true>);
+        case 5: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<5, 8, true, true>);
+        case 6: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<6, 8, true, true>);
+        case 7: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<7, 8, true, true>);
+        case 8: return reinterpret_cast<const void *>(&gemv_q6k_mfma_kernel<8, 8, true, true>);
+        default: return nullptr;
+    }
+}
+
 const void *q6k_ksplit_sums_kernel(int sbw, int waves, int slots, int G) {
     return q6_ksplit_kernel<true>(sbw, waves, slots, G);
 }

@@ -291,9 +291,14 @@ int q6k_mul_mat_vec_q_sums(const void *src0, int64_t ne00, int64_t ne01, int64_t
                            void *workspace, size_t workspace_bytes, int32_t *s16, void *stream);
 
 /* Launch geometry q6k_mul_mat_vec_q would use (the out[] fields of
- * q4k_gemv_geometry; out[6] 1 tile kernel or 4 matrix-core kernel; out[7] =
- * weight groups in flight per wave). */
+ * q4k_gemv_geometry; out[6] 1 tile kernel, 4 matrix-core kernel, 5 K-split
+ * kernel, 6 matrix-core kernel reading its A operand from the Q8_1 buffer;
+ * out[7] = weight groups in flight per wave). */
 int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
+
+/* The same for the pre-quantised route (as q4k_gemv_geometry_q8_1).  No
+ * counterpart in the reference; for tests and benchmarks. */
+int q6k_gemv_geometry_q8_1(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
 
 /* Launch geometry q4k_mul_mat_vec_q would use on the current device:
  * out[0] rows per wave tile (tile kernel), out[1] waves per workgroup,
@@ -302,9 +307,20 @@ int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * out[6] kernel (1 tile, 2 block-per-lane, 3 coalesced block kernel, 4
  *        matrix-core kernel: tiles of 16 rows on v_mfma_i32_16x16x64_i8,
  *        5 K-split kernel: the waves of a workgroup split each row's
- *        super-blocks and quantise their own slice of the activation),
- * out[7] rows per wave step. */
+ *        super-blocks and quantise their own slice of the activation,
+ *        6 matrix-core kernel reading its A operand from the Q8_1 buffer
+ *        (pre-quantised route only)),
+ * out[7] rows per wave step.  Where q4k_mul_mat_vec_q quantises into a
+ * Q8_1 copy first for kernel 6, out[5] is 0 and the rest describes that
+ * launch; the choice made with a workspace for long activations
+ * (q4k_mul_mat_vec_q, workspace) is not modelled. */
 int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
+
+/* The same for the pre-quantised route: the launch q4k_op_mul_mat_vec_q
+ * makes on a Q8_1 activation, and q4k_mul_mat_vec_q after quantising into
+ * its workspace (out[5] is 0).  No counterpart in the reference; for tests
+ * and benchmarks. */
+int q4k_gemv_geometry_q8_1(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
 
 /* Tuning override of the launch geometry for every later call in the
  * process: rows per wave tile of the tile kernel (1, 2, 4), waves per
@@ -313,12 +329,16 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * of workgroups and the kernel (1 tile kernel, 2 block-per-lane, 3
  * coalesced block kernel where they apply, 4 matrix-core kernel for
  * products without an epilogue, 5 K-split kernel for one 16-byte aligned
- * F32 column of 4096 or 8192 values: rows_per_tile is then its rows per
- * wave step (1, 4, 8, 16), waves_per_wg 4, 8 or 16 (at least the rows per
- * step), and the pipeline override's slots its tiles in flight (1..4;
- * 3 and 4 for rows of 4096 values and 1, 4 or 8 rows per step);
- * Q6_K: 4 the matrix-core kernel, any other
- * value the tile kernel); 0 restores the automatic
+ * F32 column of rows of up to 8 groups of 4096 values: rows_per_tile is
+ * then its rows per wave step (1, 4, 8, 16; rows of other lengths than 4096
+ * and 8192: 8 or 16), waves_per_wg 4, 8 or 16 (at least the rows per step;
+ * other lengths: 8 or 16), and the pipeline override's slots its tiles in
+ * flight (1..4; 3 and 4 for rows of 4096 values and 1, 4 or 8 rows per
+ * step; other lengths 1 or 2), 6 matrix-core kernel with its A operand read
+ * from the Q8_1 buffer, for products of up to 8 columns on the
+ * pre-quantised route; Q6_K: 4 the matrix-core kernel, 5 the K-split
+ * kernel as for Q4_K (4, 8 or 16 rows per step), any other value the tile
+ * kernel); 0 restores the automatic
  * choice.  Nothing is read from the environment: until this is called the
  * geometry is automatic.  Not part of the reference interface: a
  * benchmarking knob (ggml's counterpart is editing the compile-time tables

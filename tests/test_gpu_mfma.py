@@ -119,9 +119,11 @@ def test_automatic_choice(Q, gpu):
     """The automatic geometry takes the matrix-core kernel where it measured
     faster: eight columns from 896 row tiles and six to eight from 4096 at
     4096-value rows; six to eight from 512 tiles and five from 864 at longer
-    rows whose eight columns fit one launch; never below 4096 values."""
+    rows whose eight columns fit one launch; never below 4096 values; and
+    where the columns do not fit the staged kernel's LDS (4096 x 14336, eight
+    columns), the variant that reads its A operand from a Q8_1 copy."""
     for M, K, N, kern in [(14336, 4096, 8, 4), (14336, 4096, 6, 1), (128256, 4096, 6, 4), (4096, 4096, 8, 1),
                           (11008, 4096, 8, 1), (8192, 8192, 8, 4), (8192, 8192, 6, 4), (8192, 8192, 4, 1),
-                          (13824, 5120, 5, 4), (8192, 5120, 5, 1), (5120, 5120, 8, 1), (4096, 14336, 8, 1),
+                          (13824, 5120, 5, 4), (8192, 5120, 5, 1), (5120, 5120, 8, 1), (4096, 14336, 8, 6),
                           (18944, 3584, 8, 1), (28672, 10240, 5, 4)]:
         assert Q.geometry(K, M, N)["kernel"] == kern, (M, K, N)

@@ -528,7 +528,8 @@ def test_parity_variants_cover_every_kernel(Q, gpu):
     """The workloads' launches, whose sums test_production_kernel_sums
     checks, include the K-split kernel (one column: 4096-value rows with the
     activation in registers, 14336- and 28672-value rows in the long-row
-    variant), the matrix-core kernel (128256 x 4096, eight columns), the
+    variant), the matrix-core kernels (128256 x 4096, eight columns; 4096 x
+    14336, eight columns, its A operand read from the Q8_1 copy), the
     8-wave register path for several columns, 16-wave and 8-wave tile
     launches and both staging routes.  (The block-per-lane kernel, no longer
     the automatic choice anywhere, is checked through the override in
@@ -544,6 +545,7 @@ def test_parity_variants_cover_every_kernel(Q, gpu):
     assert Q.geometry(14336, 4096, 1)["kernel"] == 5 and Q.geometry(28672, 8192, 1)["kernel"] == 5
     assert (5, 0, False) in kinds                      # K-split (the headline shape, long rows)
     assert (4, 0, True) in kinds                       # matrix cores (128256 x 4096, eight columns)
+    assert (6, 0, False) in kinds                      # matrix cores, A from the Q8_1 copy (4096 x 14336 N=8)
     assert (1, 8, True) in kinds and (1, 16, True) in kinds   # several columns, 8 and 16 waves
 
 

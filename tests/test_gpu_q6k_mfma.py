@@ -150,12 +150,14 @@ def test_q6_automatic_choice(Q, gpu):
     """The automatic geometry takes the matrix-core kernel for eight columns
     from 896 row tiles and six or more from 2048 on rows of up to 4096
     values, seven or eight from 512 tiles on longer rows (and at 5120 values
-    six from 512 and five from 864), the tile kernel elsewhere;
+    six from 512 and five from 864), the variant that reads its A operand
+    from a Q8_1 copy for eight columns the staged kernel cannot hold (4096 x
+    14336), the tile kernel elsewhere;
     the Q6_K workloads' eight-column launches of 32768 and 128256 rows (whose
     sums and outputs the workload tests check) are matrix-core launches."""
     t6 = Q.GGML_TYPE_Q6_K
     for M, K, N, kern in [(128256, 4096, 8, 4), (32768, 4096, 8, 4), (14336, 4096, 8, 4), (65536, 4096, 6, 4),
-                          (32768, 4096, 6, 4), (128256, 4096, 4, 1), (14336, 4096, 6, 1), (4096, 14336, 8, 1),
+                          (32768, 4096, 6, 4), (128256, 4096, 4, 1), (14336, 4096, 6, 1), (4096, 14336, 8, 6),
                           (4096, 4096, 8, 1), (128256, 4096, 1, 1), (28672, 3584, 8, 4), (13824, 3584, 8, 1),
                           (8192, 8192, 8, 4), (8192, 8192, 7, 4), (28672, 8192, 6, 1), (8192, 5120, 6, 4),
                           (13824, 5120, 5, 4), (8192, 5120, 5, 1), (4096, 8192, 8, 1)]:
