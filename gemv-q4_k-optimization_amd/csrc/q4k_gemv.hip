@@ -262,16 +262,18 @@ static bool use_mfma(int64_t M, int64_t N, int64_t K) {
 
 // Where the pre-quantised route runs the matrix-core kernel with its A
 // operand read from the Q8_1 buffer (GA): rows longer than 8192 values,
-// five to eight columns, a tile per CU or more, and (the caller checks)
-// columns the staged kernel cannot hold in LDS.  Measured on MI355X (us per
-// op with a Q8_1 workspace, the quantiser launch included; GA against the
-// tile kernel): 4096 x 14336 N=8 18.66 against 22.63, N=6 17.64 / 19.04,
-// N=5 17.27 / 17.50; 8192 x 28672 N=8 45.75 / 66.01, N=6 42.65 / 62.90.
-// Slower at four columns (4096 x 14336 17.55 / 16.87, 8192 x 28672 39.93 /
-// 36.31) and than the staged matrix-core kernel where that holds the
-// columns (13824 x 5120 N=8 24.74 against 17.87, 8192 x 8192 N=8 18.03 /
-// 16.93, 28672 x 4096 N=8 22.99 / 21.70).  Two items in flight per wave,
-// not four (4096 x 14336 N=8 18.66 against 20.02).
+// five to eight columns, a tile per CU or more, where (the caller checks)
+// the staged matrix-core kernel is not chosen or cannot hold the columns.
+// Measured on MI355X (us per op with a Q8_1 workspace, the quantiser launch
+// included; GA against the tile kernel): 4096 x 14336 N=8 18.35 against
+// 22.84, N=6 17.66 / 19.86, N=5 17.38 / 18.16; 8192 x 28672 N=8 44.07 /
+// 66.95, N=6 42.65 / 62.90.  Slower at four columns (8192 x 28672 39.40 /
+// 37.62) and than the staged matrix-core kernel where that is chosen and
+// holds the columns (13824 x 5120 N=8 24.74 against 17.87, 8192 x 8192
+// N=8 17.54 / 17.34, 28672 x 4096 N=8 22.99 / 21.70).  Two items in flight
+// per wave, not four (4096 x 14336 N=8 18.35 against 20.07); weights
+// through the slot, not loaded straight into the lanes' registers in MFMA
+// order (4096 x 14336 N=6 17.57 against 21.43).
 static bool use_mfma_ga(int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
     return K > 8192 && N >= 5 && tiles >= 256;
@@ -501,7 +503,8 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // the matrix-core kernel with its A operand from the Q8_1 buffer: the
     // pre-quantised route, up to 8 columns in one launch
     if (q81 && !fused && mats == 1 && N <= kMfmaCols &&
-        (okern == 6 || (okern == 0 && use_mfma_ga(M, N, K) && mfma_lds_bytes((int)K, (int)N, 16) > max_lds)))
+        (okern == 6 || (okern == 0 && use_mfma_ga(M, N, K) &&
+                         !(use_mfma(M, N, K) && mfma_lds_bytes((int)K, (int)N, 16) <= max_lds))))
         return pick_geometry_mfma(di, K, M, (int)N, owgs, owaves, true);
     if (!fused && mats == 1 && (okern == 4 || (okern == 0 && use_mfma(M, N, K)))) {
         int mc = (int)N;

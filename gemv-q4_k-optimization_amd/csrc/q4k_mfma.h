@@ -28,12 +28,15 @@
 // partials of each tile and writes the outputs.
 //
 // A operand from the Q8_1 buffer (GA variants, pre-quantised activation):
-// each lane loads its 16 q8 bytes of every chunk straight from the AoS
-// block_q8_1 columns (the zero lanes' loads fall outside the buffer and read
-// zeros) instead of from an LDS copy of the whole activation, so the LDS
-// holds only the d8 of every (block, column) and the length of the rows is
-// not bounded by the LDS (eight 14336-value columns staged would take 170 KB
-// of its 160).  The sum of each block's q8, which the staged layout keeps
+// instead of an LDS copy of the whole activation, each item's activation --
+// super-block kb of the NC columns, 8 AoS block_q8_1 of 36 bytes (288
+// contiguous bytes) per column -- arrives with the item's weights, in three
+// 64-lane x 16-byte loads (chunk c = lane + 64i is bytes [16 (c % 18), +16)
+// of column c / 18), goes to a second LDS slot of the wave as it lies in
+// memory, and the MFMA lanes read their A operands from there.  The LDS
+// holds only the d8 of every (block, column) besides, so the length of the
+// rows is not bounded by the LDS (eight 14336-value columns staged would
+// take 170 KB of its 160).  The sum of each block's q8, which the staged layout keeps
 // beside d8, comes from a second MFMA of the same A operand against a B of
 // ones (D[i][r] = the sum of A row i); d8 * that sum is the staged product,
 // so both variants compute the same bits.
@@ -89,16 +92,20 @@ __host__ __device__ constexpr int mfma_lds_bytes(int K, int nc, int waves) {
     return mfma_slot_off(K, nc, waves) + waves * kMfmaSlotBytes;
 }
 // GA variants: d8 of every (block, column) ([block][8 columns], float: K
-// bytes), the partials, one weight slot per wave.
-__host__ __device__ constexpr int mfma_ga_part_off(int K) { return K; }
-__host__ __device__ constexpr int mfma_ga_slot_off(int K, int waves) { return K + mfma_part_bytes(waves); }
-__host__ __device__ constexpr int mfma_ga_lds_bytes(int K, int waves) {
+// bytes), a zero area, the partials, one weight slot and one activation
+// slot (8 columns x 288 bytes) per wave.
+constexpr int kGaZeroBytes = 256;
+constexpr int kGaSuperBytes = 8 * kQ81Bytes;  // one super-block of one Q8_1 column
+constexpr int kGaSlotBytes = kMfmaCols * kGaSuperBytes;
+__host__ __device__ constexpr int mfma_ga_zero_off(int K) { return K; }
+__host__ __device__ constexpr int mfma_ga_part_off(int K) { return K + kGaZeroBytes; }
+__host__ __device__ constexpr int mfma_ga_slot_off(int K, int waves) { return mfma_ga_part_off(K) + mfma_part_bytes(waves); }
+__host__ __device__ constexpr int mfma_ga_aslot_off(int K, int waves) {
     return mfma_ga_slot_off(K, waves) + waves * kMfmaSlotBytes;
 }
-// Bytes between the A operands of consecutive super-blocks and chunks in
-// the Q8_1 buffer (8 and 2 blocks of 36 bytes).
-constexpr uint32_t kGaSuperBytes = 8u * kQ81Bytes;
-constexpr uint32_t kGaChunkBytes = 2u * kQ81Bytes;
+__host__ __device__ constexpr int mfma_ga_lds_bytes(int K, int waves) {
+    return mfma_ga_aslot_off(K, waves) + waves * kGaSlotBytes;
+}
 
 // One super-block's weights as the MFMA lane needs them: the header of row
 // l % 16 and the 16 qs bytes of each chunk jj the lane's lane group reads.
@@ -126,7 +133,10 @@ struct MfmaLane {
     uint32_t selx, sely;  // byte selectors of its scales (sub-blocks hid, 2+hid, ...)
     uint32_t g_off[3];    // its chunks of an item: byte offsets from the item's first row
     int s_off[3];         // and in the wave's slot
-    uint32_t ga_off;      // GA: byte offset of its A operand (super-block 0, chunk 0) in the Q8_1 buffer
+    uint32_t ya_off[3];   // GA: its chunks of an item's activation, byte offsets from the item's first block
+    int ar_off;           // GA: its A operand of chunk 0 in the activation slot (data lanes)
+    int ar_step;          // GA: per chunk (2 blocks) in the slot: 72 (data lanes) or 0 (zero lanes)
+    bool a_data;          // GA: the lane carries activation (else it reads the zero area)
 };
 
 template <int NC>
@@ -150,9 +160,17 @@ __device__ __forceinline__ MfmaLane mfma_lane(int K, int64_t stride_col_y = 0) {
     const uint32_t h = (uint32_t)m.hid;
     m.selx = h | ((h + 2u) << 8) | ((h + 4u) << 16) | ((h + 6u) << 24);
     m.sely = h | ((h + 2u) << 8) | (h << 16) | ((h + 2u) << 24);
-    // GA: q8 bytes 16 (g & 1) .. of block 2jj + hia of column ca, at
-    // ga_off + kb * kGaSuperBytes + jj * kGaChunkBytes; zero lanes out of range
-    m.ga_off = data ? (uint32_t)(ca * stride_col_y + hia) * (uint32_t)kQ81Bytes + 4u + 16u * (uint32_t)(g & 1) : kOOB;
+    // GA: chunk c = l + 64i of an item's activation is bytes [16 (c % 18),
+    // +16) of column c / 18 (kOOB past the NC columns); the A operand of
+    // chunk jj is q8 bytes 16 (g & 1) .. of block 2jj + hia of column ca
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int c = l + 64 * i, col = c / 18, o = c - 18 * col;
+        m.ya_off[i] = col < NC ? (uint32_t)(col * stride_col_y) * (uint32_t)kQ81Bytes + 16u * (uint32_t)o : kOOB;
+    }
+    m.a_data = data;
+    m.ar_off = ca * kGaSuperBytes + hia * kQ81Bytes + 4 + 16 * (g & 1);
+    m.ar_step = data ? 2 * kQ81Bytes : 0;
     return m;
 }
 
@@ -261,19 +279,42 @@ __device__ __forceinline__ void mfma_item(const GemvParams &p, const MfmaLane &l
     }
 }
 
-// GA: the lane's A operands of super-block kb (zeros for the zero lanes).
-__device__ __forceinline__ void mfma_load_a(__amdgpu_buffer_rsrc_t ry, const MfmaLane &ln, int kb, u32x4 (&a)[4]) {
-    const uint32_t o = ln.ga_off + (uint32_t)kb * kGaSuperBytes;
+// GA: the lane's chunks of the activation of super-block kb (zeros past the
+// NC columns: kOOB + 288 kb stays outside the buffer).
+__device__ __forceinline__ void mfma_load_act(__amdgpu_buffer_rsrc_t ry, const MfmaLane &ln, int kb, MfmaLoad &a) {
+    const uint32_t o = (uint32_t)kb * (uint32_t)kGaSuperBytes;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) a[jj] = load16(ry, o + (uint32_t)jj * kGaChunkBytes);
+    for (int i = 0; i < 3; ++i) a.v[i] = load16(ry, o + ln.ya_off[i]);
+}
+
+// GA: writes an item's weights and activation to the wave's two slots and
+// reads the lane's weight operands back (the A operands are read in
+// mfma_item_ga); as mfma_stage.
+__device__ __forceinline__ MfmaRegs mfma_stage_ga(uint8_t *slot, uint8_t *aslot, const MfmaLane &ln,
+                                                  const MfmaLoad &w, const MfmaLoad &a, int nc) {
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        if (i < 2 || ln.lane + 128 < kMfmaChunks) *reinterpret_cast<u32x4 *>(slot + ln.s_off[i]) = w.v[i];
+        if (ln.lane + 64 * i < 18 * nc) *reinterpret_cast<u32x4 *>(aslot + 16 * (ln.lane + 64 * i)) = a.v[i];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    MfmaRegs r;
+    const uint8_t *row = slot + ln.wrow * kMfmaSlotPitch;
+    r.h = *reinterpret_cast<const u32x4 *>(row);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) r.q[jj] = *reinterpret_cast<const u32x4 *>(row + 16 + 16 * ln.half + 32 * jj);
+    return r;
 }
 
 // mfma_item with the A operand in registers (GA): d8 from the LDS table,
 // d8 * sum q8 from the ones product.  SQ: also stores the block sums of q8
 // (lanes of weight row 0 hold them for their four columns).
+// pa: the lane's A operand of chunk 0 (in the activation slot, 4-byte
+// aligned, or the zero area), pa + ar_step * jj that of chunk jj.
 template <int NC, bool SUMS>
 __device__ __forceinline__ void mfma_item_ga(const GemvParams &p, const MfmaLane &ln, const uint8_t *lds, int kb,
-                                             const MfmaRegs &w, const u32x4 (&a)[4], float (&acc)[4], int row,
+                                             const MfmaRegs &w, const uint8_t *pa, float (&acc)[4], int row,
                                              bool row_ok, bool sq_ok) {
     const float *pd = reinterpret_cast<const float *>(lds) + (kb * 8 + ln.hid) * kMfmaCols + ln.c0;
     i32x4 s[4], z[4];
@@ -282,7 +323,8 @@ __device__ __forceinline__ void mfma_item_ga(const GemvParams &p, const MfmaLane
         u32x4 bv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) bv[e] = (w.q[jj][e] >> ln.nshift) & 0x0f0f0f0fu;
-        const i32x4 av = __builtin_bit_cast(i32x4, a[jj]);
+        const uint32_t *q = reinterpret_cast<const uint32_t *>(pa + ln.ar_step * jj);
+        const i32x4 av = i32x4{(int)q[0], (int)q[1], (int)q[2], (int)q[3]};
         s[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, __builtin_bit_cast(i32x4, bv), i32x4{0, 0, 0, 0}, 0, 0, 0);
         z[jj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, i32x4{0x01010101, 0x01010101, 0x01010101, 0x01010101},
                                                       i32x4{0, 0, 0, 0}, 0, 0, 0);
@@ -405,7 +447,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
         else stage_q81_issue<NT>(p.y, p.stride_col_y, p.K, NC, p.nblk32, ys);
         __syncthreads();  // all activation loads of this CU are queued first
     }
-    // GA: the Q8_1 columns as one buffer (columns stride_col_y blocks apart)
+    // GA: the Q8_1 columns as one buffer (columns stride_col_y blocks apart;
+    // the host keeps it under 2^31 bytes)
     const __amdgpu_buffer_rsrc_t ry =
         make_rsrc(p.y, GA ? (uint32_t)((int64_t)(NC - 1) * p.stride_col_y * kQ81Bytes + (p.K / 32) * kQ81Bytes) : 0u);
 
@@ -421,11 +464,11 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
     MfmaPos cur{0, kb0};
     MfmaPos ahead = cur;
     MfmaLoad w[NIF];
-    u32x4 av[GA ? NIF : 1][4];
+    MfmaLoad av[GA ? NIF : 1];
 #pragma unroll
     for (int k = 0; k < NIF; ++k) {
         mfma_load(rs, item_off(ahead), ln, w[k]);
-        if constexpr (GA) mfma_load_a(ry, ln, ahead.kb, av[GA ? k : 0]);
+        if constexpr (GA) mfma_load_act(ry, ln, ahead.kb, av[GA ? k : 0]);
         ahead = next(ahead);
     }
 
@@ -441,6 +484,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
                     *reinterpret_cast<const uint32_t *>(p.y + ((int64_t)c * p.stride_col_y + blk) * kQ81Bytes));
             d8s[q] = dv;
         }
+        // the zero area the A operand's zero lanes read
+        if (threadIdx.x < kGaZeroBytes / 16)
+            reinterpret_cast<u32x4 *>(lds + mfma_ga_zero_off(p.K))[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
     } else {
         if (p.x)
             stage_f32_finish<kLayoutMfma, kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs,
@@ -466,6 +512,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
     float *part = reinterpret_cast<float *>(lds + (GA ? mfma_ga_part_off(p.K) : mfma_part_off(p.K, NC)));
     uint8_t *slot =
         lds + (GA ? mfma_ga_slot_off(p.K, WAVES) : mfma_slot_off(p.K, NC, WAVES)) + wave * kMfmaSlotBytes;
+    uint8_t *aslot = lds + mfma_ga_aslot_off(p.K, WAVES) + wave * kGaSlotBytes;  // GA only
+    const uint8_t *pa = GA && ln.a_data ? aslot + ln.ar_off : lds + mfma_ga_zero_off(p.K);
     int t = 0;                            // local segment of the current item
     int seg_end = (seg0 + 1) * p.nb / S;  // its end (super-block)
     // items go NIF at a time (registers k hold item it); a count that is
@@ -475,18 +523,17 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_mfma_kernel(Q4K_GEMV_KE
         for (int k = 0; k < NIF; ++k, ++it) {
             const int tile = group + ngroups * cur.r;
             const int row = row0 + tile * kMfmaRows + ln.wrow;
-            const MfmaRegs wr = mfma_stage(slot, ln, w[k]);
-            mfma_load(rs, item_off(ahead), ln, w[k]);
             if constexpr (GA) {
-                u32x4 a[4];
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) a[jj] = av[k][jj];
-                mfma_load_a(ry, ln, ahead.kb, av[k]);
+                const MfmaRegs wr = mfma_stage_ga(slot, aslot, ln, w[k], av[GA ? k : 0], NC);
+                mfma_load(rs, item_off(ahead), ln, w[k]);
+                mfma_load_act(ry, ln, ahead.kb, av[GA ? k : 0]);
                 // sq: the group of waves holding tile 0 of workgroup 0 covers
                 // every super-block once
-                mfma_item_ga<NC, SUMS>(p, ln, lds, cur.kb, wr, a, acc, row, SUMS && it < items && tile < nt && row < p.M,
+                mfma_item_ga<NC, SUMS>(p, ln, lds, cur.kb, wr, pa, acc, row, SUMS && it < items && tile < nt && row < p.M,
                                        SUMS && blockIdx.x == 0 && group == 0 && cur.r == 0 && it < items);
             } else {
+                const MfmaRegs wr = mfma_stage(slot, ln, w[k]);
+                mfma_load(rs, item_off(ahead), ln, w[k]);
                 mfma_item<NC, SUMS>(p, ln, lds, cur.kb, wr, acc, row, SUMS && it < items && tile < nt && row < p.M);
             }
             ahead = next(ahead);

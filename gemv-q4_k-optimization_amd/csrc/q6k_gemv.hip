@@ -184,16 +184,16 @@ static bool q6_ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, i
 //    51.4), and 4096 rows are slower everywhere.
 // Where the pre-quantised route runs the matrix-core kernel with its A
 // operand read from the Q8_1 buffer (GA): rows longer than 8192 values, a
-// tile per CU or more, eight columns, or five to eight of rows longer than
-// 16384 values, and (the caller checks) columns the staged kernel cannot
-// hold in LDS.  Measured on MI355X (us per op with a Q8_1 workspace, the
-// quantiser launch included; GA against the tile kernel): 4096 x 14336 N=8
-// 24.84 against 27.35; 8192 x 28672 N=8 65.54 / 91.20, N=5 64.46 / 85.28.
-// Slower at 4096 x 14336 with six or five columns (24.61 / 23.28, 24.47 /
-// 21.26) and four (20.79 / 20.13).
+// tile per CU or more, six to eight columns, or five of rows longer than
+// 16384 values, where (the caller checks) the staged matrix-core kernel is
+// not chosen or cannot hold the columns.  Measured on MI355X (us per op
+// with a Q8_1 workspace, the quantiser launch included; GA against the tile
+// kernel): 4096 x 14336 N=8 21.88 against 24.52, N=6 20.94 / 21.59;
+// 8192 x 28672 N=8 55.79 / 89.89, N=5 52.27 / 85.27.  Even at 4096 x 14336
+// with five columns (20.75 / 20.65); slower with four (20.79 / 20.13).
 static bool use_mfma_q6_ga(int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = (M + kMfmaRows - 1) / kMfmaRows;
-    return K > 8192 && tiles >= 256 && (N == 8 || (N >= 5 && K > 16384));
+    return K > 8192 && tiles >= 256 && (N >= 6 || (N == 5 && K > 16384));
 }
 
 static bool use_mfma_q6(int64_t M, int64_t N, int64_t K) {
@@ -270,7 +270,8 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     // pre-quantised route, up to 8 columns in one launch
     if (q81 && fused == kFusedNone && mats == 1 && N <= kMfmaCols &&
         (okern == 6 ||
-         (okern == 0 && use_mfma_q6_ga(M, N, K) && q6m_lds_bytes((int)K, (int)N, 16) > max_lds)))
+         (okern == 0 && use_mfma_q6_ga(M, N, K) &&
+          !(use_mfma_q6(M, N, K) && q6m_lds_bytes((int)K, (int)N, 16) <= max_lds))))
         return pick_geometry_q6_mfma(di, K, M, (int)N, g_ovr_wgs.load(), g_ovr_waves.load(), true);
     if (fused == kFusedNone && mats == 1 && (okern == 4 || (okern == 0 && use_mfma_q6(M, N, K)))) {
         int mc = (int)N;

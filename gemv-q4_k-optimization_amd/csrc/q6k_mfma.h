@@ -32,9 +32,11 @@
 //
 // Work split, summation segments, rounds and the reduction are those of the
 // Q4_K matrix-core kernel (q4k_mfma.h): the result depends on K alone.  As
-// there, the GA variants (pre-quantised route) read the A operand straight
-// from the Q8_1 columns: chunk j of super-block kb of column c is q8 bytes
-// 16 (j & 1) .. of block 8 kb + 2g + j / 2; the LDS holds only the d8 table.  A
+// there, the GA variants (pre-quantised route) bring each item's activation
+// (super-block kb of the columns, 288 contiguous bytes of each) into an
+// activation slot of the wave with the item's weights, and the LDS holds
+// only the d8 table besides; chunk j of column c is q8 bytes 16 (j & 1) ..
+// of block 2g + j / 2 of the column's 288.  A
 // lane's eight column accumulators are summed over the four lane groups of
 // its row at each segment end (two lane swaps), leaving lane l the columns
 // 2(l / 16) and 2(l / 16) + 1 of row l % 16.
@@ -90,7 +92,9 @@ struct Q6MLane {
     int a_step[2];     // its advance per chunk (16 (kb * 16 + j) from there): 16 (data lanes) or 0
     int dk_off;        // LDS byte offset of d8 of its block 2g, super-block 0, column 0
     uint32_t g_off[4]; // its chunks of an item: byte offsets from the item's first row
-    uint32_t ga_off[2];  // GA: byte offset of its A operand of super-block 0, chunk 0 in the Q8_1 buffer
+    int ar_off[2];       // GA: its A operand of chunk 0, column half q: offset in the activation slot
+    bool a_data[2];      // GA: the lane carries activation in half q (else it reads the zero area)
+    uint32_t ya_off[3];  // GA: its chunks of an item's activation, byte offsets from the item's first block
 };
 
 template <int NC, bool GA = false>
@@ -114,30 +118,36 @@ __device__ __forceinline__ Q6MLane q6m_lane(int K, int64_t stride_col_y = 0) {
         const bool dq = data && c < NC;
         m.a_off[q] = dq ? c * mfma_qcol(K) + 64 * g : q6m_zero_off(K, NC) + 16 * (l & 7);
         m.a_step[q] = dq ? 16 : 0;
-        m.ga_off[q] = dq ? (uint32_t)(c * stride_col_y + 2 * g) * (uint32_t)kQ81Bytes + 4u : kOOB;
+        m.ar_off[q] = c * kGaSuperBytes + 2 * g * kQ81Bytes + 4;
+        m.a_data[q] = dq;
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int c = l + 64 * i, col = c / 18, o = c - 18 * col;
+        m.ya_off[i] = col < NC ? (uint32_t)(col * stride_col_y) * (uint32_t)kQ81Bytes + 16u * (uint32_t)o : kOOB;
     }
     m.dk_off = (GA ? 0 : q6m_dk_off(K, NC)) + (2 * g) * kMfmaCols * 4;
     return m;
 }
 
-// GA LDS layout: the d8 table ([block][8 columns], float: K bytes), the
-// partials, one weight slot per wave.
-__host__ __device__ constexpr int q6m_ga_part_off(int K) { return K; }
-__host__ __device__ constexpr int q6m_ga_slot_off(int K, int waves) { return K + q6m_part_bytes(waves); }
-__host__ __device__ constexpr int q6m_ga_lds_bytes(int K, int waves) {
+// GA LDS layout: the d8 table ([block][8 columns], float: K bytes), a zero
+// area, the partials, one weight slot and one activation slot per wave.
+__host__ __device__ constexpr int q6m_ga_zero_off(int K) { return K; }
+__host__ __device__ constexpr int q6m_ga_part_off(int K) { return K + kGaZeroBytes; }
+__host__ __device__ constexpr int q6m_ga_slot_off(int K, int waves) { return q6m_ga_part_off(K) + q6m_part_bytes(waves); }
+__host__ __device__ constexpr int q6m_ga_aslot_off(int K, int waves) {
     return q6m_ga_slot_off(K, waves) + waves * kQ6SlotBytes;
 }
+__host__ __device__ constexpr int q6m_ga_lds_bytes(int K, int waves) {
+    return q6m_ga_aslot_off(K, waves) + waves * kGaSlotBytes;
+}
 
-// GA: the lane's A operands of super-block kb, chunk j at a[j][q] (zeros for
-// the zero lanes and the halves past NC).
-template <int NQ>
-__device__ __forceinline__ void q6m_load_a(__amdgpu_buffer_rsrc_t ry, const Q6MLane &ln, int kb, u32x4 (&a)[4][2]) {
+// GA: the lane's chunks of the activation of super-block kb (zeros past the
+// NC columns).
+__device__ __forceinline__ void q6m_load_act(__amdgpu_buffer_rsrc_t ry, const Q6MLane &ln, int kb, MfmaLoad &a) {
+    const uint32_t o = (uint32_t)kb * (uint32_t)kGaSuperBytes;
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-        const uint32_t o = ln.ga_off[q] + (uint32_t)kb * kGaSuperBytes;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a[j][q] = load16(ry, o + (uint32_t)(36 * (j >> 1) + 16 * (j & 1)));
-    }
+    for (int i = 0; i < 3; ++i) a.v[i] = load16(ry, o + ln.ya_off[i]);
 }
 
 // The lane's chunk offsets of an item (rows row_stride bytes apart); chunks
@@ -163,13 +173,21 @@ __device__ __forceinline__ void q6m_load(__amdgpu_buffer_rsrc_t rs, uint32_t off
     for (int i = 0; i < 4; ++i) w.v[i] = load16(rs, off + ln.g_off[i]);
 }
 
-// Writes an item to the wave's slot; the wait and the compiler barrier keep
-// the lanes' reads of other lanes' bytes behind the writes.
-__device__ __forceinline__ void q6m_stage(uint8_t *slot, const Q6MLane &ln, const Q6MLoad &w) {
+// Writes an item to the wave's slot (GA: and its activation to the
+// activation slot); the wait and the compiler barrier keep the lanes' reads
+// of other lanes' bytes behind the writes.
+template <bool GA = false>
+__device__ __forceinline__ void q6m_stage(uint8_t *slot, const Q6MLane &ln, const Q6MLoad &w, uint8_t *aslot = nullptr,
+                                          const MfmaLoad *a = nullptr, int nc = 0) {
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         if (i < 3 || ln.lane + 192 < kQ6Chunks) *reinterpret_cast<u32x4 *>(slot + 16 * ln.lane + 1024 * i) = w.v[i];
+    if constexpr (GA) {
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            if (ln.lane + 64 * i < 18 * nc) *reinterpret_cast<u32x4 *>(aslot + 16 * (ln.lane + 64 * i)) = a->v[i];
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
@@ -188,7 +206,7 @@ __device__ __forceinline__ uint32_t q6m_bytes(uint32_t ql, uint32_t qhx, uint32_
 template <int NC, bool SUMS, bool GA = false>
 __device__ __forceinline__ void q6m_item(const GemvParams &p, const Q6MLane &ln, const uint8_t *lds,
                                          const uint8_t *slot, int kb, float (&acc)[kMfmaCols], int row,
-                                         bool row_ok, const u32x4 (&ga)[4][2]) {
+                                         bool row_ok, const uint8_t *const (&pa)[2]) {
     constexpr int NQ = NC > 4 ? 2 : 1;
     const uint8_t *wr = slot + ln.wrow * kQ6SlotPitch;
     const int h = ln.g >> 1;
@@ -220,8 +238,14 @@ __device__ __forceinline__ void q6m_item(const GemvParams &p, const Q6MLane &ln,
             for (int e = 0; e < 4; ++e) bv[e] = q6m_bytes(ql[e], qh[jj][e], ln.rot_ql, rq);
 #pragma unroll
             for (int q = 0; q < NQ; ++q) {
-                const u32x4 av =
-                    GA ? ga[j][q] : *reinterpret_cast<const u32x4 *>(lds + ln.a_off[q] + ln.a_step[q] * (16 * kb + j));
+                u32x4 av;
+                if constexpr (GA) {  // 4-byte aligned in the activation slot (data lanes)
+                    const uint32_t *qa =
+                        reinterpret_cast<const uint32_t *>(pa[q] + (ln.a_data[q] ? 36 * (j >> 1) + 16 * (j & 1) : 0));
+                    av = u32x4{qa[0], qa[1], qa[2], qa[3]};
+                } else {
+                    av = *reinterpret_cast<const u32x4 *>(lds + ln.a_off[q] + ln.a_step[q] * (16 * kb + j));
+                }
                 s[jj][q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, av),
                                                                  __builtin_bit_cast(i32x4, bv),
                                                                  i32x4{0, 0, 0, 0}, 0, 0, 0);
@@ -362,11 +386,11 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KE
     MfmaPos cur{0, kb0};
     MfmaPos ahead = cur;
     Q6MLoad w[2];
-    u32x4 av[GA ? 2 : 1][4][2];
+    MfmaLoad av[GA ? 2 : 1];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         q6m_load(rs, item_off(ahead), ln, w[k]);
-        if constexpr (GA) q6m_load_a<NQ>(ry, ln, ahead.kb, av[GA ? k : 0]);
+        if constexpr (GA) q6m_load_act(ry, ln, ahead.kb, av[GA ? k : 0]);
         ahead = next(ahead);
     }
 
@@ -381,6 +405,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KE
                     *reinterpret_cast<const uint32_t *>(p.y + ((int64_t)c * p.stride_col_y + blk) * kQ81Bytes));
             d8s[q] = dv;
         }
+        // the zero area the A operand's zero lanes read
+        if (threadIdx.x < kGaZeroBytes / 16)
+            reinterpret_cast<u32x4 *>(lds + q6m_ga_zero_off(p.K))[threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
     } else {
         if (p.x)
             stage_f32_finish<kLayoutMfmaQ6, kLPB, NT>(p.x, p.ldx, p.K, NC, p.vec_ok != 0, p.nblk32, xs,
@@ -407,6 +434,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KE
     float l1[2] = {0.0f, 0.0f}, l2[2] = {0.0f, 0.0f}, l4[2] = {0.0f, 0.0f};
     float *part = reinterpret_cast<float *>(lds + (GA ? q6m_ga_part_off(p.K) : q6m_part_off(p.K, NC)));
     uint8_t *slot = lds + (GA ? q6m_ga_slot_off(p.K, WAVES) : q6m_slot_off(p.K, NC, WAVES)) + wave * kQ6SlotBytes;
+    uint8_t *aslot = lds + q6m_ga_aslot_off(p.K, WAVES) + wave * kGaSlotBytes;  // GA only
+    const uint8_t *const pa[2] = {GA && ln.a_data[0] ? aslot + ln.ar_off[0] : lds + q6m_ga_zero_off(p.K),
+                                  GA && ln.a_data[1] ? aslot + ln.ar_off[1] : lds + q6m_ga_zero_off(p.K)};
     int t = 0;                            // local segment of the current item
     int seg_end = (seg0 + 1) * p.nb / S;  // its end (super-block)
     // items go two at a time (load slot k holds item it); an odd count ends
@@ -416,20 +446,17 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_mfma_kernel(Q4K_GEMV_KE
         for (int k = 0; k < 2; ++k, ++it) {
             const int tile = group + ngroups * cur.r;
             const int row = row0 + tile * kMfmaRows + ln.wrow;
-            q6m_stage(slot, ln, w[k]);
-            q6m_load(rs, item_off(ahead), ln, w[k]);
             if constexpr (GA) {
-                u32x4 a[4][2];
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int q = 0; q < NQ; ++q) a[j][q] = av[k][j][q];
-                q6m_load_a<NQ>(ry, ln, ahead.kb, av[k]);
+                q6m_stage<true>(slot, ln, w[k], aslot, &av[GA ? k : 0], NC);
+                q6m_load(rs, item_off(ahead), ln, w[k]);
+                q6m_load_act(ry, ln, ahead.kb, av[GA ? k : 0]);
                 q6m_item<NC, SUMS, true>(p, ln, lds, slot, cur.kb, acc, row,
-                                         SUMS && it < items && tile < nt && row < p.M, a);
+                                         SUMS && it < items && tile < nt && row < p.M, pa);
             } else {
+                q6m_stage(slot, ln, w[k]);
+                q6m_load(rs, item_off(ahead), ln, w[k]);
                 q6m_item<NC, SUMS>(p, ln, lds, slot, cur.kb, acc, row, SUMS && it < items && tile < nt && row < p.M,
-                                   av[0]);
+                                   pa);
             }
             ahead = next(ahead);
             const MfmaPos done = cur;
