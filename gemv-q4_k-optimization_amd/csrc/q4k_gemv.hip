@@ -322,7 +322,8 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
 }
 
 // The K-split kernel: rows_per_step TR = 16 / SBW rows per wave step (1, 4,
-// 8, 16; SBW super-blocks per wave and group), waves per workgroup
+// 8, 16; SBW super-blocks per wave and group; rows of other lengths than
+// 4096 and 8192 values: 4 for up to 4 groups, 8, 16), waves per workgroup
 // (whole teams of TR waves), workgroups (default one per CU) and row tiles
 // in flight per wave (1 or 2).
 static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
@@ -333,15 +334,16 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
                        ? rows_per_step
                        : 16;
     const bool lng = K != 4096 && K != 8192;  // rows of other lengths: the long-row variant
+    const int G = (int)((K / kQK + 15) / 16), gmax = G <= 4 ? 4 : 8;
     g.ks_long = lng ? 1 : 0;
     g.ksplit = 16 / tr;
-    if (lng && g.ksplit > 2) g.ksplit = 2;
+    // long rows: 4 super-blocks per wave for up to 4 groups, else at most 2
+    if (lng && g.ksplit > (G <= 4 ? 4 : 2)) g.ksplit = G <= 4 ? 4 : 2;
     g.R = 16 / g.ksplit;
     g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
     if (g.waves < g.R) g.waves = g.R;
-    if (lng && g.waves < 8) g.waves = 8;
     g.slots = slots >= 1 && slots <= 4 ? slots : 1;
-    if (lng ? !ksplit_long_exists(g.ksplit, g.waves, g.slots, 8)
+    if (lng ? !ksplit_long_exists(g.ksplit, g.waves, g.slots, gmax)
             : !ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096)))
         g.slots = 2;
     int64_t grid = wgs > 0 ? wgs : cus;
@@ -350,8 +352,7 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
     const int rows = g.rows_base + (g.rows_extra ? 1 : 0);
-    g.lds = lng ? ksplit_long_lds_bytes(rows, g.ksplit, g.waves, (int)((K / kQK + 15) / 16))
-                : ksplit_lds_bytes(rows, g.ksplit);
+    g.lds = lng ? ksplit_long_lds_bytes(rows, g.ksplit, g.waves, G) : ksplit_lds_bytes(rows, g.ksplit);
     g.lds_launch = g.lds;
     g.nc_chunk = 1;
     return g;
@@ -378,10 +379,15 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //    2048 x 8192 4.38 / 5.03), then 4 rows per step, 4 waves and two tiles
 //    in flight (4096 x 8192 5.51 / 5.87, 14336 x 8192 12.91 / 13.45, 28672 x
 //    8192 23.33 / 24.27).
-//  - other lengths up to 8 groups (the long-row variant, 8 or 16 rows per
-//    step): up to 8 rows per CU, 8 rows, 8 waves, two steps in flight
-//    (1024 x 14336 5.56 against 6.65, 2048 x 14336 5.79 / 7.21, 1024 x 28672
-//    9.33 / 11.11, 2048 x 11008 5.88 / 6.09); at 16 rows per CU, 16 rows
+//  - other lengths up to 8 groups (the long-row variant): up to 4 rows per
+//    CU and 4 groups, 4 rows, 4 waves, two steps in flight (1024 x 14336
+//    5.48 against 5.54 on the next shape); up to 8 rows per CU, 8 rows, 8
+//    waves, two steps (1024 x 14336 5.56 against 6.65 on the tile kernel,
+//    2048 x 14336 5.79 / 7.21, 1024 x 28672 9.33 / 11.11, 2048 x 11008 5.88
+//    / 6.09); three or four steps in flight measured slower everywhere but
+//    at 1024 x 14336 (4096 x 14336 8.69 and 9.09 against 8.35, 14336 x 14336
+//    22.64 and 22.12 against 21.61, 1024 x 14336 at 4 rows 5.40 against
+//    5.48); at 16 rows per CU, 16 rows
 //    and 16 waves, one step (4096 x 14336 8.32 / 8.54, 4096 x 11008 6.97 /
 //    7.42, 4096 x 5120 4.81 / 5.53); beyond, 8 rows, 8 waves, two steps
 //    where 8-row tiles leave at most one row in eight idle (8192 x 28672
@@ -393,6 +399,11 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
     if (K != 4096 && K != 8192) {
+        if (rho <= 4 && K <= 4 * 4096) {
+            tr = waves = 4;
+            slots = 2;
+            return true;
+        }
         if (rho == 16) {
             tr = waves = 16;
             return true;

@@ -361,7 +361,7 @@ __device__ __forceinline__ LaneAct ks_read_lds(const uint8_t *area, int sbw, int
     return a;
 }
 
-// SBW: 1 or 2 super-blocks per wave and group; GMAX: the most groups per
+// SBW: 1, 2 or 4 super-blocks per wave and group; GMAX: the most groups per
 // row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
 // partials).
 template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false>
@@ -547,11 +547,15 @@ const void *ksplit_sym_w(int waves, int slots, int G) {
     return nullptr;
 }
 
-// The long-row variants: SBW 1 or 2, whole teams of 8 or 16 waves, one or
-// two steps in flight, rows of up to 4 or 8 groups.
+// The long-row variants: SBW 1 or 2 in whole teams of 8 or 16 waves for rows
+// of up to 4 or 8 groups, SBW 4 in teams of 4 waves (4, 8 or 16 per
+// workgroup) for rows of up to 4 groups (its 16 values per lane and group
+// held for 8 groups would take 128 registers); one or two steps in flight,
+// or three or four in workgroups of up to 8 waves.
 constexpr bool ksplit_long_exists(int sbw, int waves, int slots, int gmax) {
-    return (sbw == 1 || sbw == 2) && (waves == 8 || waves == 16) && waves % (16 / sbw) == 0 &&
-           (slots == 1 || slots == 2) && (gmax == 4 || gmax == 8);
+    return (((sbw == 1 || sbw == 2) && (waves == 8 || waves == 16) && (gmax == 4 || gmax == 8)) ||
+           (sbw == 4 && (waves == 4 || waves == 8 || waves == 16) && gmax == 4)) &&
+           waves % (16 / sbw) == 0 && (slots == 1 || slots == 2 || ((slots == 3 || slots == 4) && waves <= 8));
 }
 
 template <bool SUMS, int SBW, int WAVES, int S>
@@ -570,13 +574,24 @@ const void *ksplit_long_kernel(int sbw, int waves, int slots, int G) {
     if (G > 8) return nullptr;
     auto pick = [&](auto sbw_c) -> const void * {
         constexpr int B = decltype(sbw_c)::value;
-        if (waves == 8) return slots == 2 ? ksplit_long_sym_g<SUMS, B, 8, 2>(gmax) : ksplit_long_sym_g<SUMS, B, 8, 1>(gmax);
-        if (waves == 16)
-            return slots == 2 ? ksplit_long_sym_g<SUMS, B, 16, 2>(gmax) : ksplit_long_sym_g<SUMS, B, 16, 1>(gmax);
+        auto by_slots = [&](auto waves_c) -> const void * {
+            constexpr int W = decltype(waves_c)::value;
+            switch (slots) {
+                case 1: return ksplit_long_sym_g<SUMS, B, W, 1>(gmax);
+                case 2: return ksplit_long_sym_g<SUMS, B, W, 2>(gmax);
+                case 3: return ksplit_long_sym_g<SUMS, B, W, 3>(gmax);
+                case 4: return ksplit_long_sym_g<SUMS, B, W, 4>(gmax);
+                default: return nullptr;
+            }
+        };
+        if (waves == 4) return by_slots(std::integral_constant<int, 4>{});
+        if (waves == 8) return by_slots(std::integral_constant<int, 8>{});
+        if (waves == 16) return by_slots(std::integral_constant<int, 16>{});
         return nullptr;
     };
     if (sbw == 1) return pick(std::integral_constant<int, 1>{});
     if (sbw == 2) return pick(std::integral_constant<int, 2>{});
+    if (sbw == 4) return pick(std::integral_constant<int, 4>{});
     return nullptr;
 }
 

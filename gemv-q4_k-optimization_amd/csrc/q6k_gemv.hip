@@ -108,21 +108,24 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
     Q6Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
     const bool lng = K != 4096 && K != 8192;
+    const int G = (int)((K / kQK + 15) / 16);
     g.ks_long = lng ? 1 : 0;
     g.ks_tr = rows_per_step == 4 || rows_per_step == 8 || rows_per_step == 16 ? rows_per_step : 8;
-    if (lng && g.ks_tr < 8) g.ks_tr = 8;
+    if (lng && g.ks_tr == 4 && G > 4) g.ks_tr = 8;  // 4 rows per step: rows of up to 4 groups
     g.ksplit = 16 / g.ks_tr;
     g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
     if (g.waves < g.ks_tr) g.waves = g.ks_tr;
-    g.slots = slots == 2 ? 2 : 1;
-    if (!lng && !q6_ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096))) g.slots = 1;
+    g.slots = slots >= 1 && slots <= (lng ? 4 : 2) ? slots : 1;
+    if (lng ? !q6_ksplit_long_exists(g.ksplit, g.waves, g.slots, G <= 4 ? 4 : 8)
+            : !q6_ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096)))
+        g.slots = lng ? 2 : 1;
     int64_t grid = wgs > 0 ? wgs : cus;
     if (grid > M) grid = M;
     g.grid = grid < 1 ? 1 : (int)grid;
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
     const int rows = g.rows_base + (g.rows_extra ? 1 : 0);
-    g.lds = lng ? q6_ksplit_long_lds_bytes(rows, g.ksplit, g.waves, (int)((K / kQK + 15) / 16))
+    g.lds = lng ? q6_ksplit_long_lds_bytes(rows, g.ksplit, g.waves, G)
                 : ksplit_lds_bytes(rows, g.ksplit);
     g.lds_launch = g.lds;
     g.nc_chunk = 1;
@@ -144,12 +147,14 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
 // to 160 rows per CU (4096 x 14336 12.26 against 13.58, 1024 x 14336 6.41 /
 // 7.91, 2048 x 14336 7.84 / 9.17, 8192 x 28672 38.47 / 42.46, 14336 x 14336
 // 33.44 / 35.93, 4096 x 11008 10.54 / 10.84, 13824 x 5120 15.26 / 17.32,
-// 5120 x 13824 14.92 / 14.95).
+// 5120 x 13824 14.92 / 14.95), 4 rows and 4 waves up to 4 rows per CU and 4
+// groups (1024 x 14336 6.20 against 6.43); three or four steps in flight
+// measured slower (4096 x 14336 13.32 against 12.30).
 static bool q6_ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
     if (K != 4096 && K != 8192) {
-        tr = waves = 8;
+        tr = waves = rho <= 4 && K <= 4 * 4096 ? 4 : 8;
         slots = 2;
         return rho <= 160;
     }
@@ -263,7 +268,7 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
         int tr = 0, kw = 0, ks = 0;
         if (q6_ksplit_auto(K, M, cus, tr, kw, ks)) {
             const int os = g_ovr_slots.load();
-            return pick_geometry_q6_ksplit(di, K, M, tr, kw, 0, os == 1 || os == 2 ? os : ks);
+            return pick_geometry_q6_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks);
         }
     }
     // the matrix-core kernel with its A operand from the Q8_1 buffer: the

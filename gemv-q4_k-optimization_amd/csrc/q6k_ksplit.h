@@ -245,7 +245,7 @@ __device__ __forceinline__ Q6Act q6_ks_read_lds(const uint8_t *area, int sbw, in
     return a;
 }
 
-// SBW: 1 or 2 super-blocks per wave and group; GMAX: the most groups per
+// SBW: 1, 2 or 4 super-blocks per wave and group; GMAX: the most groups per
 // row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
 // partials).
 template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false>
@@ -382,8 +382,9 @@ __host__ __device__ constexpr int q6_ksplit_long_lds_bytes(int rows_per_wg, int 
     return ksplit_long_part_bytes(rows_per_wg, sbw) + waves * G * q6_ks_slice_bytes(sbw);
 }
 
-// The long-row variants: SBW 1 or 2, whole teams of 8 or 16 waves, one or
-// two steps in flight, rows of up to 4 or 8 groups.
+// The long-row variants: those of the Q4_K kernel (SBW 1 or 2 for rows of
+// up to 8 groups, 4 for rows of up to 4; three or four steps in flight in
+// workgroups of up to 8 waves).
 constexpr bool q6_ksplit_long_exists(int sbw, int waves, int slots, int gmax) {
     return ksplit_long_exists(sbw, waves, slots, gmax);
 }
@@ -404,14 +405,24 @@ const void *q6_ksplit_long_kernel(int sbw, int waves, int slots, int G) {
     if (G > 8) return nullptr;
     auto pick = [&](auto sbw_c) -> const void * {
         constexpr int B = decltype(sbw_c)::value;
-        if (waves == 8)
-            return slots == 2 ? q6_ksplit_long_sym_g<SUMS, B, 8, 2>(gmax) : q6_ksplit_long_sym_g<SUMS, B, 8, 1>(gmax);
-        if (waves == 16)
-            return slots == 2 ? q6_ksplit_long_sym_g<SUMS, B, 16, 2>(gmax) : q6_ksplit_long_sym_g<SUMS, B, 16, 1>(gmax);
+        auto by_slots = [&](auto waves_c) -> const void * {
+            constexpr int W = decltype(waves_c)::value;
+            switch (slots) {
+                case 1: return q6_ksplit_long_sym_g<SUMS, B, W, 1>(gmax);
+                case 2: return q6_ksplit_long_sym_g<SUMS, B, W, 2>(gmax);
+                case 3: return q6_ksplit_long_sym_g<SUMS, B, W, 3>(gmax);
+                case 4: return q6_ksplit_long_sym_g<SUMS, B, W, 4>(gmax);
+                default: return nullptr;
+            }
+        };
+        if (waves == 4) return by_slots(std::integral_constant<int, 4>{});
+        if (waves == 8) return by_slots(std::integral_constant<int, 8>{});
+        if (waves == 16) return by_slots(std::integral_constant<int, 16>{});
         return nullptr;
     };
     if (sbw == 1) return pick(std::integral_constant<int, 1>{});
     if (sbw == 2) return pick(std::integral_constant<int, 2>{});
+    if (sbw == 4) return pick(std::integral_constant<int, 4>{});
     return nullptr;
 }
 

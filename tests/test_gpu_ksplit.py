@@ -221,8 +221,15 @@ def test_q6k_ksplit_group_sums_exact(Q, O, gpu, M, K):
 
 
 # -------------------------------------------------------- long rows ----
-# (rows per wave step, waves, steps in flight) of the long-row variants
-LONG_SHAPES = [(tr, w, s) for tr in (16, 8) for w in (8, 16) for s in (1, 2) if w >= tr]
+# (rows per wave step, waves, steps in flight) of the long-row variants: 8
+# or 16 rows per step for rows of up to 8 groups, 4 for rows of up to 4;
+# three or four steps in flight in workgroups of up to 8 waves
+LONG_SHAPES = [(tr, w, s) for tr in (16, 8) for w in (8, 16) for s in (1, 2) if w >= tr] + [(8, 8, 3), (8, 8, 4)]
+LONG_SHAPES_4 = [(4, w, s) for w in (4, 8, 16) for s in (1, 2)] + [(4, w, s) for w in (4, 8) for s in (3, 4)]
+
+
+def long_shapes(K):
+    return LONG_SHAPES + (LONG_SHAPES_4 if -(-K // 4096) <= 4 else [])
 
 
 @pytest.mark.parametrize("M,K", [(4096, 14336), (1000, 14336), (37, 12544), (300, 3584), (513, 2048),
@@ -244,7 +251,7 @@ def test_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
         np.concatenate([[0, 1, M - 2, M - 1], np.random.default_rng(M).choice(M, 300, replace=False)]))
     ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
     _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"tile {M}x{K}")
-    for tr, waves, slots in LONG_SHAPES:
+    for tr, waves, slots in long_shapes(K):
         for wgs in (0, few_workgroups(M), 300):
             y = run_forced(Q, wd, K, xd, tr, waves, slots, wgs)
             if not np.array_equal(y, y_tile):
@@ -263,7 +270,7 @@ def test_ksplit_long_rows_sums_exact(Q, O, gpu, M, K):
     wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
     rows = np.unique(np.concatenate([[0, M // 2, M - 1], np.random.default_rng(M).choice(M, min(M, 100), replace=False)]))
     ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x))
-    for tr, waves, slots in LONG_SHAPES:
+    for tr, waves, slots in long_shapes(K):
         try:
             Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
             Q.set_pipeline_override(slots=slots)
@@ -297,7 +304,7 @@ def test_q6k_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
         np.concatenate([[0, 1, M - 2, M - 1], np.random.default_rng(M).choice(M, 300, replace=False)]))
     ref = O.gemv_q6K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
     _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"Q6_K tile {M}x{K}")
-    for tr, waves, slots in LONG_SHAPES:
+    for tr, waves, slots in long_shapes(K):
         for wgs in (0, few_workgroups(M), 300):
             y = run_forced6(Q, wd, K, xd, tr, waves, slots, wgs)
             if not np.array_equal(y, y_tile):
@@ -317,7 +324,7 @@ def test_q6k_ksplit_long_rows_group_sums_exact(Q, O, gpu, M, K):
     wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
     rows = np.unique(np.concatenate([[0, M // 2, M - 1], np.random.default_rng(M).choice(M, min(M, 100), replace=False)]))
     ref = O.gemv_q6K_q8_1(wq[rows], K, O.quantize_q8_1(x))
-    for tr, waves, slots in LONG_SHAPES:
+    for tr, waves, slots in long_shapes(K):
         try:
             Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
             Q.set_pipeline_override(slots=slots)
