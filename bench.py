@@ -821,9 +821,10 @@ def main():
                     help="time MUL_MAT_ID (one token) on expert-FFN shapes")
     ap.add_argument("--fused", action="store_true",
                     help="time the gate+up SWIGLU launch against two plain launches")
-    ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2, 3, 4, 5),
+    ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2, 3, 4, 5, 6),
                     help="--profile/--profile-sweep/--sweep: force a GEMV kernel through the geometry override "
-                         "(1 tile, 2 block-per-lane, 3 coalesced block, 4 matrix-core, 5 K-split; 0 automatic)")
+                         "(1 tile, 2 block-per-lane, 3 coalesced block, 4 matrix-core, 5 K-split, 6 matrix-core "
+                         "reading its A operand from the Q8_1 copy; 0 automatic)")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="time a plain read of the headline weight's bytes in several launch shapes")
     ap.add_argument("--wtype", choices=sorted(BLOCK_BYTES), default="q4_K",
