@@ -443,19 +443,24 @@ class ReadRunner:
 
 # (workgroups, waves per workgroup, 1-KB loads in flight per wave)
 READ_SHAPES = [(2016, 4, 4), (2016, 4, 2), (1008, 4, 4), (4032, 4, 2), (1024, 8, 4), (512, 8, 4),
-               (512, 16, 2), (256, 16, 8), (256, 16, 4), (256, 16, 2), (256, 16, 1)]
+               (512, 16, 2), (256, 16, 8), (256, 16, 4), (256, 16, 2), (256, 16, 1),
+               (256, 8, 2), (256, 8, 1), (256, 4, 2), (256, 4, 1)]
 
 
 def read_ceiling(args):
-    """A plain read of the headline weight's bytes (14336 x 4096 Q4_K:
-    33,030,144 B) in several launch shapes, timed like the headline, against
-    the headline GEMV in the same process."""
+    """A plain read of a weight's bytes (--shape M K; default the headline
+    14336 x 4096 Q4_K: 33,030,144 B) in several launch shapes, timed like the
+    headline, against that product's GEMV (one column) in the same process.
+    Shapes whose waves would read more than 1.5 times the bytes (the probe
+    reads zeros past the end) are skipped."""
     import torch
     Q = _pkg()
-    M, K = 14336, 4096
+    M, K = args.shape[0], args.shape[1]
     nbytes = M * (K // 256) * BLOCK_BYTES["q4_K"]
     for wgs, waves, infl in READ_SHAPES:
         per_wave = math.ceil(nbytes / (wgs * waves) / 1024) * 1024
+        if per_wave * wgs * waves > 1.5 * nbytes:
+            continue
         r = ReadRunner(Q, nbytes, wgs, waves, per_wave, infl)
         t = time_gpu(r, args.steps, args.warmup, args.trials)
         del r
@@ -826,7 +831,8 @@ def main():
                          "(1 tile, 2 block-per-lane, 3 coalesced block, 4 matrix-core, 5 K-split, 6 matrix-core "
                          "reading its A operand from the Q8_1 copy; 0 automatic)")
     ap.add_argument("--read-ceiling", action="store_true",
-                    help="time a plain read of the headline weight's bytes in several launch shapes")
+                    help="time a plain read of a weight's bytes (--shape M K, default the headline's) in "
+                         "several launch shapes")
     ap.add_argument("--wtype", choices=sorted(BLOCK_BYTES), default="q4_K",
                     help="weight format of --sweep, --profile and --profile-sweep (the headline is Q4_K)")
     args = ap.parse_args()
