@@ -380,8 +380,8 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //    in flight (4096 x 8192 5.51 / 5.87, 14336 x 8192 12.91 / 13.45, 28672 x
 //    8192 23.33 / 24.27).
 //  - other lengths up to 8 groups (the long-row variant): up to 4 rows per
-//    CU and 4 groups, 4 rows, 4 waves, two steps in flight (1024 x 14336
-//    5.48 against 5.54 on the next shape); up to 8 rows per CU, 8 rows, 8
+//    CU and 4 groups, 4 rows, 4 waves, one step in flight (1024 x 14336
+//    5.48 against 5.60 with two and 5.65 on the next shape); up to 8 rows per CU, 8 rows, 8
 //    waves, two steps (1024 x 14336 5.56 against 6.65 on the tile kernel,
 //    2048 x 14336 5.79 / 7.21, 1024 x 28672 9.33 / 11.11, 2048 x 11008 5.88
 //    / 6.09); three or four steps in flight measured slower everywhere but
@@ -401,7 +401,7 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
     if (K != 4096 && K != 8192) {
         if (rho <= 4 && K <= 4 * 4096) {
             tr = waves = 4;
-            slots = 2;
+            slots = 1;
             return true;
         }
         if (rho == 16) {
@@ -801,6 +801,14 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
             fn = p.sums ? q4k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                         : ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);
             p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit);
+            // groups quantised before the first step: all of them for one
+            // super-block per wave and group (4096 x 14336 8.27 against 8.39
+            // us, 4096 x 11008 6.97 / 7.02), else one, the others just before
+            // the first step that reads them (8192 x 28672 25.10 against
+            // 25.60); the pipeline override's prologue 2 forces all, 0, 1 or 3
+            // one
+            const int opro = g_ovr_prologue.load();
+            p.rpw = (opro == 2 || (opro < 0 && geo.ksplit == 1)) ? p.G : 1;
         } else {
             fn = p.sums ? q4k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                         : ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);

@@ -431,20 +431,26 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
 #pragma unroll
     for (int k = 0; k < S; ++k) load_step(st[k], w[k]);
 
-    // 3. quantise the groups the slice reaches into the wave's LDS area;
-    // group 0 unconditionally (a slice past the row quantises zeros and
-    // writes no sums), so its load is not sunk below the weight loads
+    // 3. quantise group 0 of the slice into the wave's LDS area, the other
+    // groups just before the step that first reads them (the first tile
+    // walks the groups in order); group 0 unconditionally (a slice past the
+    // row quantises zeros and writes no sums), so its load is not sunk below
+    // the weight loads
     uint8_t *area = lds + p.ring_off + wave * G * ks_slice_bytes(SBW);
+    auto stage = [&](int i) {
+        ks_stage_lds<SBW>(xv[i], lane, area + i * ks_slice_bytes(SBW), SUMS ? p.sq : nullptr,
+                          (16 * i + SBW * slice) * 8, p.K / 32);
+        // lanes read what other lanes of the wave wrote: keep the reads
+        // below (a wave's LDS operations complete in order)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // p.rpw: groups quantised before the first step (1, or all of them)
 #pragma unroll
     for (int i = 0; i < GMAX; ++i)
-        if (i == 0 || (i < G && 16 * i + SBW * slice < p.nb))
-            ks_stage_lds<SBW>(xv[i], lane, area + i * ks_slice_bytes(SBW), SUMS ? p.sq : nullptr,
-                              (16 * i + SBW * slice) * 8, p.K / 32);
-    // lanes read what other lanes of the wave wrote: keep the reads below
-    // (a wave's LDS operations complete in order)
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (i == 0 || (i < p.rpw && i < G && 16 * i + SBW * slice < p.nb)) stage(i);
+    int staged = max(1, min(p.rpw, G));  // groups staged so far
 
     Lane ln;
     ln.lane = lane;
@@ -458,6 +464,12 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
         for (;;) {
 #pragma unroll
             for (int k = 0; k < S; ++k) {
+                if (st[k].i >= staged) {  // the first tile reaches a new group
+#pragma unroll
+                    for (int i = 1; i < GMAX; ++i)
+                        if (i >= staged && i <= st[k].i && i < G && 16 * i + SBW * slice < p.nb) stage(i);
+                    staged = st[k].i + 1;
+                }
                 if (16 * st[k].i + SBW * slice < p.nb) {  // the wave's slice reaches this group
                     const LaneAct a = ks_read_lds(area + st[k].i * ks_slice_bytes(SBW), SBW, s, j);
                     const RowScales sc = row_scales(w[k], ln);

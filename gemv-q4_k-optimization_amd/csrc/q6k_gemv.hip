@@ -143,19 +143,22 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
 // 65536 x 4096 39.54 / 41.35, 4096 x 8192 7.96 / 8.60, 28672 x 8192 35.92 /
 // 36.60), except over 256 rows per CU at 4096 values (128256 x 4096: 76.10
 // against 75.10 on the tile kernel).  Rows of other lengths up to 8 groups
-// (the long-row variant): 8 rows per step, 8 waves, two steps in flight up
-// to 160 rows per CU (4096 x 14336 12.26 against 13.58, 1024 x 14336 6.41 /
-// 7.91, 2048 x 14336 7.84 / 9.17, 8192 x 28672 38.47 / 42.46, 14336 x 14336
-// 33.44 / 35.93, 4096 x 11008 10.54 / 10.84, 13824 x 5120 15.26 / 17.32,
-// 5120 x 13824 14.92 / 14.95), 4 rows and 4 waves up to 4 rows per CU and 4
-// groups (1024 x 14336 6.20 against 6.43); three or four steps in flight
-// measured slower (4096 x 14336 13.32 against 12.30).
+// (the long-row variant): 8 rows per step, 8 waves, one step in flight up
+// to 160 rows per CU (4096 x 14336 12.10 against 12.36 with two in flight
+// and 13.58 on the tile kernel, 8192 x 28672 37.15 / 39.13 / 42.46,
+// 4096 x 11008 9.93 / 10.44 / 10.84, 14336 x 14336 33.75 / 33.84 / 35.93;
+// with two: 2048 x 14336 7.84 / 9.17, 13824 x 5120 15.26 / 17.32, 5120 x
+// 13824 14.92 / 14.95), 4 rows, 4 waves and two steps up to 4 rows per CU
+// and 4 groups (1024 x 14336 6.26 against 6.32); three or four steps in
+// flight, 16 waves or two workgroups per CU measured slower (4096 x 14336
+// 13.29, 13.32, 13.34, 13.12 against 12.10).
 static bool q6_ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
     if (K != 4096 && K != 8192) {
-        tr = waves = rho <= 4 && K <= 4 * 4096 ? 4 : 8;
-        slots = 2;
+        const bool small = rho <= 4 && K <= 4 * 4096;
+        tr = waves = small ? 4 : 8;
+        slots = small ? 2 : 1;
         return rho <= 160;
     }
     if (rho <= 4) {
@@ -516,7 +519,14 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.sums = so->sums + c0 * ne01 * (ne00 / 16);
         }
         if (bl) p.bt = bl->bt;
-        if (geo.ks_long) p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit);
+        if (geo.ks_long) {
+            p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit);
+            // groups quantised before the first step: one, the others just
+            // before the first step that reads them (4096 x 14336 12.08
+            // against 12.14 us with all before, 8192 x 28672 37.04 / 38.42);
+            // the pipeline override's prologue 2 forces all
+            p.rpw = g_ovr_prologue.load() == 2 ? p.G : 1;
+        }
         if (!fn) return Q4K_EINVAL;
         st = ensure_lds(di, fn, lds_launch);
         if (st != Q4K_OK) return st;

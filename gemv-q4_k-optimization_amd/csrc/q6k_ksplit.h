@@ -316,17 +316,22 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
 #pragma unroll
     for (int k = 0; k < S; ++k) load_step(st[k], w[k]);
 
-    // 3. quantise the groups the slice reaches into the wave's LDS area
-    //    (group 0 unconditionally, so its load stays ahead of the weights)
+    // 3. quantise group 0 of the slice into the wave's LDS area, the other
+    //    groups just before the step that first reads them (group 0
+    //    unconditionally, so its load stays ahead of the weights)
     uint8_t *area = lds + p.ring_off + wave * G * q6_ks_slice_bytes(SBW);
+    auto stage = [&](int i) {
+        q6_ks_stage_lds<SBW>(xv[i], lane, area + i * q6_ks_slice_bytes(SBW));
+        // lanes read what other lanes of the wave wrote
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // p.rpw: groups quantised before the first step (1, or all of them)
 #pragma unroll
     for (int i = 0; i < GMAX; ++i)
-        if (i == 0 || (i < G && 16 * i + SBW * slice < p.nb))
-            q6_ks_stage_lds<SBW>(xv[i], lane, area + i * q6_ks_slice_bytes(SBW));
-    // lanes read what other lanes of the wave wrote
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (i == 0 || (i < p.rpw && i < G && 16 * i + SBW * slice < p.nb)) stage(i);
+    int staged = max(1, min(p.rpw, G));  // groups staged so far
 
     // 4. the (tile, group) steps, S in flight
     float acc = 0.0f;
@@ -335,6 +340,12 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
         for (;;) {
 #pragma unroll
             for (int k = 0; k < S; ++k) {
+                if (st[k].i >= staged) {  // the first tile reaches a new group
+#pragma unroll
+                    for (int i = 1; i < GMAX; ++i)
+                        if (i >= staged && i <= st[k].i && i < G && 16 * i + SBW * slice < p.nb) stage(i);
+                    staged = st[k].i + 1;
+                }
                 if (16 * st[k].i + SBW * slice < p.nb) {  // the wave's slice reaches this group
                     const Q6Act a = q6_ks_read_lds(area + st[k].i * q6_ks_slice_bytes(SBW), SBW, s, h, jp);
                     uint32_t v[4][4];

@@ -351,7 +351,9 @@ int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32
  * the K-split kernel 1 to 4; 0 = automatic) and when the first weight
  * loads are issued relative to the activation quantisation (0 = the first
  * two groups before it, 1 = all
- * after, 2 = all before, 3 = one before; -1 = automatic).  Values a kernel
+ * after, 2 = all before, 3 = one before; -1 = automatic; the long-row
+ * K-split kernels: 2 = every group's slice quantised before the first
+ * step, 0, 1, 3 = each group's just before the first step that reads it).  Values a kernel
  * has no variant for fall back to the automatic choice.  Not part of the
  * reference interface: a benchmarking knob. */
 int q4k_set_pipeline_override(int32_t slots, int32_t prologue);

@@ -46,10 +46,10 @@ def few_workgroups(M):
     return max(7, -(-M // 2048))
 
 
-def run_forced(Q, wd, K, xd, tr, waves, slots, wgs=0):
+def run_forced(Q, wd, K, xd, tr, waves, slots, wgs=0, prologue=-1):
     try:
         Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, workgroups=wgs, kernel=5)
-        Q.set_pipeline_override(slots=slots)
+        Q.set_pipeline_override(slots=slots, prologue=prologue)
         g = Q.geometry(K, wd.shape[0], 1)
         assert g["kernel"] == 5 and g["rows_per_step"] == tr and g["waves_per_wg"] == waves, g
         return Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
@@ -153,11 +153,11 @@ def inputs6(Q, M, K, seed):
     return _w6cache[key], _common.activations(1, K, seed)
 
 
-def run_forced6(Q, wd, K, xd, tr, waves, slots, wgs=0):
+def run_forced6(Q, wd, K, xd, tr, waves, slots, wgs=0, prologue=-1):
     t6 = Q.GGML_TYPE_Q6_K
     try:
         Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, workgroups=wgs, kernel=5)
-        Q.set_pipeline_override(slots=slots)
+        Q.set_pipeline_override(slots=slots, prologue=prologue)
         g = Q.geometry(K, wd.shape[0], 1, t6)
         assert g["kernel"] == 5 and g["rows_per_tile"] == tr and g["waves_per_wg"] == waves, g
         return Q.mul_mat_vec_q(wd, K, xd, wtype=t6).cpu().numpy()
@@ -252,12 +252,15 @@ def test_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
     ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
     _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"tile {M}x{K}")
     for tr, waves, slots in long_shapes(K):
-        for wgs in (0, few_workgroups(M), 300):
-            y = run_forced(Q, wd, K, xd, tr, waves, slots, wgs)
+        # every group staged before the first step (prologue 2) and each just
+        # before the step that first reads it (0), with the default grid
+        for wgs, pro in ((0, 0), (0, 2), (few_workgroups(M), -1), (300, -1)):
+            y = run_forced(Q, wd, K, xd, tr, waves, slots, wgs, pro)
             if not np.array_equal(y, y_tile):
                 bad = np.flatnonzero(y[0] != y_tile[0])
-                raise AssertionError(f"long {M}x{K} rows/step {tr} waves {waves} slots {slots} wgs {wgs}: "
-                                     f"{bad.size} outputs differ from the tile kernel, e.g. rows {bad[:5]}")
+                raise AssertionError(f"long {M}x{K} rows/step {tr} waves {waves} slots {slots} wgs {wgs} "
+                                     f"prologue {pro}: {bad.size} outputs differ from the tile kernel, "
+                                     f"e.g. rows {bad[:5]}")
 
 
 @pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048)])
@@ -305,12 +308,13 @@ def test_q6k_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
     ref = O.gemv_q6K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
     _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"Q6_K tile {M}x{K}")
     for tr, waves, slots in long_shapes(K):
-        for wgs in (0, few_workgroups(M), 300):
-            y = run_forced6(Q, wd, K, xd, tr, waves, slots, wgs)
+        for wgs, pro in ((0, 0), (0, 2), (few_workgroups(M), -1), (300, -1)):
+            y = run_forced6(Q, wd, K, xd, tr, waves, slots, wgs, pro)
             if not np.array_equal(y, y_tile):
                 bad = np.flatnonzero(y[0] != y_tile[0])
-                raise AssertionError(f"Q6_K long {M}x{K} rows/step {tr} waves {waves} slots {slots} wgs {wgs}: "
-                                     f"{bad.size} outputs differ from the tile kernel, e.g. rows {bad[:5]}")
+                raise AssertionError(f"Q6_K long {M}x{K} rows/step {tr} waves {waves} slots {slots} wgs {wgs} "
+                                     f"prologue {pro}: {bad.size} outputs differ from the tile kernel, "
+                                     f"e.g. rows {bad[:5]}")
 
 
 @pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048)])
