@@ -21,6 +21,7 @@
 #include "q4k_runtime.h"
 #include "q4k_gemv_kernels.h"
 #include "q4k_ksplit.h"
+#include "q4k_ksplit_nc.h"
 #include "q4k_mfma.h"
 #include "q4k_tile.h"
 
@@ -200,6 +201,7 @@ struct Geometry {
     int segs = 1;       // matrix-core kernel: summation segments of a row
     int ksplit = 0;     // K-split kernel: super-blocks per wave and group (0: another kernel)
     int ks_long = 0;    // K-split kernel for rows of any length (activation slices in LDS)
+    int ks_staged = 0;  // several-column K-split kernel: activation quantised once per workgroup into LDS
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
@@ -327,9 +329,37 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
 // (whole teams of TR waves), workgroups (default one per CU) and row tiles
 // in flight per wave (1 or 2).
 static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
-                                     int wgs, int slots) {
+                                     int wgs, int slots, int N = 1, int staged = 0) {
     Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
+    if (N >= 2) {  // two to four columns of rows of 1 or 2 groups
+        const int G = (int)(K / 4096);
+        g.ksplit = N == 2 && rows_per_step == 8 ? 2 : 4;
+        g.R = 16 / g.ksplit;
+        g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 8;
+        if (g.waves < g.R) g.waves = g.R;
+        g.slots = slots == 1 || slots == 2 ? slots : 2;
+        if (!ksplit_nc_exists(N, g.ksplit, g.waves, g.slots, G)) g.slots = 1;
+        if (!ksplit_nc_exists(N, g.ksplit, g.waves, g.slots, G)) {
+            g.waves = 8;
+            g.slots = 2;
+        }
+        // three or four columns: the activation quantised once per
+        // workgroup (prologue override 0) or by every wave for its own
+        // slices (2); otherwise as `staged` says
+        const int opro = g_ovr_prologue.load();
+        g.ks_staged = N >= 3 && (opro == 0 || (opro != 2 && staged)) ? 1 : 0;
+        int64_t grid = wgs > 0 ? wgs : cus;
+        if (grid > M) grid = M;
+        g.grid = grid < 1 ? 1 : (int)grid;
+        g.rows_base = (int)(M / g.grid);
+        g.rows_extra = (int)(M % g.grid);
+        g.lds = ksplit_nc_part_bytes(g.rows_base + (g.rows_extra ? 1 : 0), N, g.ksplit) +
+                (g.ks_staged ? lds_bytes((int)K, N) : 0);
+        g.lds_launch = g.lds;
+        g.nc_chunk = N;
+        return g;
+    }
     const int tr = rows_per_step == 1 || rows_per_step == 4 || rows_per_step == 8 || rows_per_step == 16
                        ? rows_per_step
                        : 16;
@@ -439,6 +469,67 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
     return true;
 }
 
+// The several-column K-split kernel's automatic launch shape (N = 2..4
+// aligned F32 columns, rows of 4096 or 8192 values, one workgroup per CU;
+// staged: the activation quantised once per workgroup into LDS); false
+// where the tile kernel measured faster.  rho = rows per CU.  Measured on
+// MI355X (us, interleaved timings of 200 ops; K-split against the tile
+// kernel, whose outputs are the same bits):
+//  - two columns, K = 4096: up to 16 rows per CU 8 rows per step, 8 waves,
+//    one tile in flight (1024 x 4096 3.97 against 4.09, 2048 x 4096 4.12 /
+//    4.30, 4096 x 4096 4.86 / 5.26); beyond, an odd number of 8-row tiles
+//    per CU up to 64 rows two 8-wave teams with one tile in flight (6144 x
+//    4096 5.85 / 6.09, 14336 x 4096 8.53 / 8.94), otherwise one team with
+//    two (8192 x 4096 6.00 / 6.82, 16384 x 4096 9.03 / 10.07, 28672 x 4096
+//    13.56 / 15.13, 128256 x 4096 52.08 / 54.82); the activation
+//    quantised by every wave in registers (staged in LDS: 4096 x 4096 5.29,
+//    14336 x 4096 8.86).
+//  - two columns, K = 8192: up to 4 rows per CU 4 rows per step and 4
+//    waves (1024 x 8192 5.40 / 5.91), else 8 rows and 8 waves, one tile in
+//    flight (4096 x 8192 6.78 / 7.25, 14336 x 8192 14.55 / 15.61, 28672 x
+//    8192 26.00 / 27.49).
+//  - three columns, up to 16 rows per CU: 4 rows per step, 8 waves,
+//    staged, one tile in flight up to 4 rows per CU (1024 x 4096 4.43 /
+//    4.48, 1024 x 8192 7.11 / 8.09), else two (4096 x 4096 5.50 / 5.68;
+//    4096 x 8192 stays on the tile kernel: 9.57 against 8.37).
+//  - three or four columns, K = 8192, 96 rows per CU or more: 4 rows, 4
+//    waves, two tiles in flight, in registers (28672 x 8192 N=3 28.63 /
+//    29.19, N=4 30.28 / 32.03).
+//  The tile kernel elsewhere: four columns of 4096 values (14336 x 4096
+//  10.97 staged against 10.68, 4096 x 4096 6.47 / 6.29), 56 rows per CU of
+//  8192 values (14336 x 8192 N=3 17.54 / 16.77, N=4 19.06 / 18.88).
+static bool ksplit_nc_auto(int64_t K, int64_t M, int64_t N, int cus, int &tr, int &waves, int &slots,
+                           int &staged) {
+    const int64_t rho = (M + cus - 1) / cus;
+    staged = 0;
+    slots = 1;
+    if (N == 2) {
+        if (K == 8192) {
+            tr = waves = rho <= 4 ? 4 : 8;
+            return true;
+        }
+        tr = 8;
+        waves = 8;
+        if (rho <= 16) return true;
+        if (rho <= 64 && ((rho + 7) / 8) % 2 == 1) waves = 16;
+        else slots = 2;
+        return true;
+    }
+    tr = 4;
+    if (N == 3 && (rho <= 4 || (rho <= 16 && K == 4096))) {
+        waves = 8;
+        staged = 1;
+        slots = rho <= 4 ? 1 : 2;
+        return true;
+    }
+    if (K == 8192 && rho >= 96) {
+        waves = 4;
+        slots = 2;
+        return true;
+    }
+    return false;
+}
+
 // Launch geometry for an (M, K, N) product.
 //  tile kernel: one workgroup per CU (requesting just over half the CU's LDS
 //    keeps a second one away), 8 or 16 waves, the M rows split evenly over
@@ -468,12 +559,25 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // the long-row variant); the tile kernel, whose outputs are the same
     // bits, takes the rest
     const bool ks_ok = N == 1 && !fused && mats == 1 && f32_vec && K <= 8 * 4096;
-    if (ks_ok && okern == 5) return pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load());
+    // two to four columns: the K-split kernel for rows of 1 or 2 groups
+    const bool ksn_ok = N >= 2 && N <= 4 && !fused && mats == 1 && f32_vec && (K == 4096 || K == 8192);
+    if ((ks_ok || ksn_ok) && okern == 5)
+        return pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load(), (int)N, 1);
+    // (automatic: where the partials fit the LDS)
     if (ks_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
         int tr = 0, kw = 0, ks = 0;
         if (ksplit_auto(K, M, di.cus > 0 ? di.cus : 1, tr, kw, ks)) {
             const int os = g_ovr_slots.load();
-            return pick_geometry_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks);
+            const Geometry gk = pick_geometry_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks);
+            if (gk.lds <= max_lds) return gk;
+        }
+    }
+    if (ksn_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
+        int tr = 0, kw = 0, ks = 0, st = 0;
+        if (ksplit_nc_auto(K, M, N, cus, tr, kw, ks, st)) {
+            const int os = g_ovr_slots.load();
+            const Geometry gk = pick_geometry_ksplit(di, K, M, tr, kw, 0, os == 1 || os == 2 ? os : ks, (int)N, st);
+            if (gk.lds <= max_lds) return gk;
         }
     }
     if (N == 1 && rpw > 0 && okern == 3 && !fused && mats == 1) {
@@ -796,8 +900,13 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         p.rows_extra = geo.rows_extra;
         p.ring_off = lds_bytes(p.K, nc);
     } else if (geo.ksplit) {
-        if (nc != 1 || !p.x || !p.vec_ok) return Q4K_EINVAL;
-        if (geo.ks_long) {
+        if (!p.x || !p.vec_ok) return Q4K_EINVAL;
+        if (nc > 1) {
+            if (geo.ks_long || nc != geo.nc_chunk) return Q4K_EINVAL;
+            fn = p.sums ? q4k_ksplit_nc_sums_kernel(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0)
+                        : ksplit_nc_kernel<false>(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0);
+            p.ring_off = geo.ks_staged ? lds_bytes(p.K, nc) : 0;
+        } else if (geo.ks_long) {
             fn = p.sums ? q4k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                         : ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);
             p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit);

@@ -90,14 +90,21 @@ __device__ __forceinline__ float bpermf(int src_lane, float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane * 4, __builtin_bit_cast(int, v)));
 }
 
+// Block b of a slice of consecutive super-blocks starting at block blk0.
+struct KsBlocks {
+    int blk0;
+    __device__ int operator()(int b) const { return blk0 + b; }
+};
+
 // The wave's activation slice of one group: lane L holds the 4*SBW values
 // [L*4*SBW, +4*SBW) of the slice; returns what lane (r, s, j) reads (the q8
 // of sub-blocks 2j and 2j+1 of super-block s and their (d8, d8 * sum q8)).
 // sq (parity variants; null in the product kernels) gets the int32 sums of
-// the slice's blocks, from each block's first lane, at sq[blk0 + b].
-template <int SBW>
+// the slice's blocks, from each block's first lane, at sq[blk(b)] (blk:
+// the row's block index of the slice's block b).
+template <int SBW, class BlockOf = KsBlocks>
 __device__ __forceinline__ LaneAct ks_stage(const float (&v)[4 * SBW], int lane, int s, int j, int32_t *sq,
-                                            int blk0) {
+                                            BlockOf blk) {
     constexpr int V = 4 * SBW;
     LaneAct a;
     if constexpr (V <= 32) {
@@ -106,7 +113,7 @@ __device__ __forceinline__ LaneAct ks_stage(const float (&v)[4 * SBW], int lane,
         float d8;
         int qs, hs;
         ks_quantize_part<V>(v, word, d8, qs, hs);
-        if (sq && (lane & (LPB - 1)) == 0) sq[blk0 + lane / LPB] = qs;
+        if (sq && (lane & (LPB - 1)) == 0) sq[blk(lane / LPB)] = qs;
         // dword t of lane (s, j) = values 256s + 64j + 4t: word t % SBW of
         // lane (64s + 16j + t) / SBW
         const int base = 64 * s + 16 * j;
@@ -135,8 +142,8 @@ __device__ __forceinline__ LaneAct ks_stage(const float (&v)[4 * SBW], int lane,
         ks_quantize_part<32>(v0, w0, d0, s0, h0);
         ks_quantize_part<32>(v1, w1, d1, s1, h1);
         if (sq) {
-            sq[blk0 + 2 * lane] = s0;
-            sq[blk0 + 2 * lane + 1] = s1;
+            sq[blk(2 * lane)] = s0;
+            sq[blk(2 * lane + 1)] = s1;
         }
         a.a0 = u32x4{w0[0], w0[1], w0[2], w0[3]};
         a.a1 = u32x4{w0[4], w0[5], w0[6], w0[7]};
@@ -248,7 +255,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_
     LaneAct act[G];
 #pragma unroll
     for (int i = 0; i < G; ++i)
-        act[i] = ks_stage<SBW>(xv[i], lane, s, j, SUMS ? p.sq : nullptr, (16 * i + SBW * slice) * 8);
+        act[i] = ks_stage<SBW>(xv[i], lane, s, j, SUMS ? p.sq : nullptr, KsBlocks{(16 * i + SBW * slice) * 8});
 
     Lane ln;
     ln.lane = lane;

@@ -1,0 +1,299 @@
+// q4k_ksplit_nc.h -- the K-split Q4_K GEMV kernel for two to four F32
+// activation columns, rows of one or two 16-block groups (K = 4096 or 8192).
+//
+// The one-column K-split kernel (q4k_ksplit.h) with NC accumulators per
+// lane.  What changes is which super-blocks a wave owns, so that the
+// outputs stay the tile kernel's bits.  With several columns the tile
+// kernel reduces a wave's lanes in another order than with one
+// (column_sums): first super-blocks g and g^8 (lane bit 5), with three or
+// four columns then g and g^4 (lane bit 4), then the four chunks of a
+// super-block, then the remaining bits of g from the lowest up.  So a wave
+// here owns whole residue classes of super-blocks: with P = 2 (two columns)
+// the C = SBW/2 super-blocks [C*w, +C) of slice w and the same ones 8
+// further on, with P = 4 (three or four columns, SBW = 4) super-block w and
+// those 4, 8 and 12 further on.  Its DPP steps (ksn_reduce) are column_sums'
+// levels that stay inside the wave, in column_sums' order; the balanced tree
+// over the KW slices of a row forms the rest (the low bits of g).  Each
+// column's output is therefore the tile kernel's, for every launch shape
+// (tested).
+//
+// Lanes: lane = 4*SBW*r + 4*s + j as in the one-column kernel; position s of
+// slice w is super-block ksn_block(w, s) of each group.
+//
+// Activation.  Either each wave quantises its own slices in registers and
+// hands the lanes their sub-blocks through ds_bpermute, as the one-column
+// kernel (every team quantises the whole activation), or (STAGED) the
+// workgroup quantises the activation once into LDS with the tile kernel's
+// staging (layout, arithmetic and barriers) and each lane reads its
+// sub-blocks there, as a tile-kernel lane owning the same super-block and
+// chunk would: with three or four columns the per-team quantisation costs
+// more than the barrier.
+//
+// Reference: kernels/mmvq.cu:150-344 (ncols_dst 2-4) with the vec-dot of
+// kernels/vecdotq.cuh:775-819 and :457-483.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "q4k_ksplit.h"
+
+namespace q4k {
+
+// Super-block of slice position s of slice w, within a group.
+template <int P, int SBW>
+__device__ __forceinline__ int ksn_block(int w, int s) {
+    constexpr int C = SBW / P, L = 16 / P;
+    return C * w + (s % C) + L * (s / C);
+}
+
+// Block b (0 .. 8*SBW-1) of the slice of group i, as a block index of the row.
+template <int P, int SBW>
+struct KsnBlocks {
+    int i, w;
+    __device__ int operator()(int b) const { return (16 * i + ksn_block<P, SBW>(w, b >> 3)) * 8 + (b & 7); }
+};
+
+// The in-wave levels of column_sums' tree for one column's lane values,
+// valid in the ks_writer lanes (a row rotation by 4 pairs a lane with lane
+// bit 2 set with the one 4 below it).
+//  P = 2, SBW = 2: g ^ 8 (lane bit 2), the chunks;
+//  P = 2, SBW = 4: g ^ 8 (lane bit 3), the chunks, g ^ 1 (lane bit 2);
+//  P = 4, SBW = 4: g ^ 8 (lane bit 3), g ^ 4 (lane bit 2), the chunks.
+template <int P, int SBW>
+__device__ __forceinline__ float ksn_reduce(float v) {
+    if constexpr (SBW == 4) v += dppf<kDppRor8>(v);
+    if constexpr (P == 4 || SBW == 2) v += dppf<kDppRor4>(v);
+    v += dppf<kDppXor1>(v);
+    v += dppf<kDppXor2>(v);
+    if constexpr (P == 2 && SBW == 4) v += dppf<kDppRor4>(v);
+    return v;
+}
+
+// NC: columns (2..4); SBW: super-blocks per wave and group (2 or 4 for two
+// columns, 4 for three or four); WAVES: whole teams of 16/SBW waves; S: row
+// tiles in flight per wave; G: groups per row; STAGED: the activation
+// quantised once per workgroup into LDS (the partials then start at
+// p.ring_off).  SUMS: the parity variant.
+template <int NC, int SBW, int WAVES, int S, int G, bool STAGED, bool SUMS = false>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_nc_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    constexpr int P = NC <= 2 ? 2 : 4;
+    constexpr int KW = 16 / SBW;  // waves sharing a row
+    constexpr int TR = 16 / SBW;  // rows per wave step
+    constexpr int TEAMS = WAVES / KW;
+    constexpr int V = 4 * SBW;    // activation values per lane, group and column
+    static_assert(NC >= 2 && NC <= 4 && SBW >= P && SBW <= 4, "two to four columns, 2 or 4 super-blocks");
+    static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    float *part = reinterpret_cast<float *>(lds + (STAGED ? p.ring_off : 0));
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slice = wave % KW, team = wave / KW;
+    const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1), j = lane & 3;
+
+    const int b = (int)blockIdx.x;
+    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
+    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int nt = (n + TR - 1) / TR;
+    const int tq = nt / TEAMS, trem = nt - tq * TEAMS;
+    const int tb = team * tq + min(team, trem);
+    const int ntiles = tq + (team < trem ? 1 : 0);
+    const int kb0 = ksn_block<P, SBW>(slice, s);  // the lane's super-block within each group
+
+    // 1. the slice's activation values of every column, issued first: lane
+    //    L holds values [L*V, +V) of the slice's super-blocks taken in
+    //    position order (16-byte loads; the host launches this kernel for
+    //    16-byte aligned columns)
+    //    (STAGED: the tile kernel's staging loads, every wave's queued ahead
+    //    of the weight loads by a barrier)
+    const int xsb = lane / (64 / SBW);  // the slice position the lane's values lie in
+    const int xoff = ksn_block<P, SBW>(slice, xsb) * kQK + (lane * V) % kQK;
+    constexpr int kLPB = stage_lpb(NC);
+    constexpr int kPreR = pre_rounds(NC, kWave * WAVES);
+    float xv[STAGED ? 1 : G][NC][V];
+    ActStage<kLPB, kPreR> xs;
+    if constexpr (STAGED) {
+        stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, true, p.nblk32, xs);
+        __syncthreads();
+    } else {
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float4 *src = reinterpret_cast<const float4 *>(p.x + c * p.ldx + 16 * i * kQK + xoff);
+#pragma unroll
+                for (int k = 0; k < V / 4; ++k) {
+                    const float4 a = src[k];
+                    xv[i][c][4 * k] = a.x;
+                    xv[i][c][4 * k + 1] = a.y;
+                    xv[i][c][4 * k + 2] = a.z;
+                    xv[i][c][4 * k + 3] = a.w;
+                }
+            }
+    }
+
+    // 2. the first S tiles' weights
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    const uint32_t lh = (uint32_t)r * (uint32_t)p.row_stride + (uint32_t)(kb0 * kBlockBytes);
+    const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
+    const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
+    auto load_tile = [&](int t, RowRegs(&w)[G]) {
+        const bool ok = t < ntiles;
+        const uint32_t base = (uint32_t)(tb + t) * tile_bytes;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const uint32_t gi = (uint32_t)i * (16u * kBlockBytes);
+            const uint32_t oh = ok ? base + gi + lh : kOOB;
+            const uint32_t oq = ok ? base + gi + lq : kOOB;
+            w[i].h = load16(rs, oh);
+            w[i].q0 = load16(rs, oq);
+            w[i].q1 = load16(rs, oq + 16u);
+        }
+    };
+    int tk[S];
+    RowRegs w[S][G];
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+        tk[k] = k;
+        load_tile(k, w[k]);
+    }
+
+    // 3. quantise the slices and hand each lane its sub-blocks (STAGED: the
+    //    workgroup's staging, then each lane reads what the tile kernel's
+    //    lane 4*kb0 + j reads)
+    Lane ln;
+    ln.lane = 4 * kb0 + j;
+    ln.g = kb0;
+    ln.j = j;
+    ln.sel = make_scale_sel(j);
+    LaneAct act[G][NC];
+    if constexpr (STAGED) {
+        int8_t *q8s = reinterpret_cast<int8_t *>(lds);
+        float2 *dks = reinterpret_cast<float2 *>(lds + NC * p.qcol);
+        stage_f32_finish<kLayoutQ4K, kLPB, kWave * WAVES, NC < 4 ? 1 : kFinishRounds>(
+            p.x, p.ldx, p.K, NC, true, p.nblk32, xs, p.qcol, q8s, dks, SUMS ? p.sq : nullptr);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) act[i][c] = lane_act(p, ln, i, c, q8s, dks);
+    } else {
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+                act[i][c] = ks_stage<SBW>(xv[i][c], lane, s, j, SUMS ? p.sq + c * (p.K / 32) : nullptr,
+                                          KsnBlocks<P, SBW>{i, slice});
+    }
+    // 4. the tiles, S in flight
+    int remaining = ntiles;
+    if (remaining > 0) {
+        for (;;) {
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                const int rl = (tb + tk[k]) * TR + r;
+                float acc[NC];
+#pragma unroll
+                for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
+#pragma unroll
+                for (int i = 0; i < G; ++i) {
+                    const RowScales sc = row_scales(w[k][i], ln);
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) {
+                        int sa, sb;
+                        accumulate(w[k][i], sc, act[i][c], acc[c], sa, sb);
+                        if constexpr (SUMS) {
+                            if (tk[k] < ntiles && rl < n) {
+                                int32_t *o = p.sums + ((int64_t)c * p.M + wg_beg + rl) * (p.K / 32) +
+                                             (16 * i + kb0) * 8 + 2 * j;
+                                o[0] = sa;
+                                o[1] = sb;
+                            }
+                        }
+                    }
+                }
+                const bool wr = ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const float q = ksn_reduce<P, SBW>(acc[c]);
+                    if (wr) part[(rl * NC + c) * KW + slice] = q;
+                }
+                tk[k] += S;
+                load_tile(tk[k], w[k]);
+            }
+            remaining -= S;
+            if (remaining <= 0) break;
+        }
+    }
+    __syncthreads();
+    // 5. each (row, column): the balanced tree over its KW slice sums
+    for (int e = (int)threadIdx.x; e < n * NC; e += kWave * WAVES) {
+        const int row = e / NC, c = e - row * NC;
+        float q[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) q[k] = part[e * KW + k];
+#pragma unroll
+        for (int h = KW / 2; h >= 1; h /= 2)
+#pragma unroll
+            for (int t = 0; t < h; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+        p.dst[c * p.ld_dst + wg_beg + row] = q[0];
+    }
+}
+
+// LDS bytes of the (row, column, slice) partials of the largest workgroup
+// share (STAGED launches: after the staged activation).
+__host__ __device__ constexpr int ksplit_nc_part_bytes(int rows_per_wg, int nc, int sbw) {
+    return rows_per_wg * nc * (16 / sbw) * 4;
+}
+
+// The instantiated variants: those whose registers fit the launch bounds
+// without spilling (16-wave workgroups: rows of one group, and one tile in
+// flight with four columns); the STAGED ones for three or four columns.
+constexpr bool ksplit_nc_exists(int nc, int sbw, int waves, int slots, int G) {
+    return nc >= 2 && nc <= 4 && (sbw == 4 || (sbw == 2 && nc == 2)) && (waves == 4 || waves == 8 || waves == 16) &&
+           waves % (16 / sbw) == 0 && (slots == 1 || slots == 2) && (G == 1 || G == 2) &&
+           (waves < 16 || (G == 1 && (nc < 4 || slots == 1)));
+}
+
+template <bool SUMS, int NC, int SBW, int WAVES>
+const void *ksplit_nc_sym(int slots, int G, bool staged) {
+    auto one = [&](auto s_c, auto g_c) -> const void * {
+        constexpr int S = decltype(s_c)::value, GG = decltype(g_c)::value;
+        if constexpr (ksplit_nc_exists(NC, SBW, WAVES, S, GG)) {
+            if (!staged)
+                return reinterpret_cast<const void *>(&gemv_q4k_ksplit_nc_kernel<NC, SBW, WAVES, S, GG, false, SUMS>);
+            if constexpr (NC >= 3)
+                return reinterpret_cast<const void *>(&gemv_q4k_ksplit_nc_kernel<NC, SBW, WAVES, S, GG, true, SUMS>);
+        }
+        return nullptr;
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    if (slots == 1) return G == 1 ? one(I1{}, I1{}) : (G == 2 ? one(I1{}, I2{}) : nullptr);
+    if (slots == 2) return G == 1 ? one(I2{}, I1{}) : (G == 2 ? one(I2{}, I2{}) : nullptr);
+    return nullptr;
+}
+
+// The K-split kernel for nc = 2..4 columns, or null.
+template <bool SUMS>
+const void *ksplit_nc_kernel(int nc, int sbw, int waves, int slots, int G, bool staged) {
+    auto by_waves = [&](auto nc_c, auto sbw_c) -> const void * {
+        constexpr int NC = decltype(nc_c)::value, B = decltype(sbw_c)::value;
+        if (waves == 4) return ksplit_nc_sym<SUMS, NC, B, 4>(slots, G, staged);
+        if (waves == 8) return ksplit_nc_sym<SUMS, NC, B, 8>(slots, G, staged);
+        if (waves == 16) return ksplit_nc_sym<SUMS, NC, B, 16>(slots, G, staged);
+        return nullptr;
+    };
+    using B2 = std::integral_constant<int, 2>;
+    using B4 = std::integral_constant<int, 4>;
+    switch (nc) {
+        case 2: return sbw == 2 ? by_waves(std::integral_constant<int, 2>{}, B2{})
+                                : (sbw == 4 ? by_waves(std::integral_constant<int, 2>{}, B4{}) : nullptr);
+        case 3: return sbw == 4 ? by_waves(std::integral_constant<int, 3>{}, B4{}) : nullptr;
+        case 4: return sbw == 4 ? by_waves(std::integral_constant<int, 4>{}, B4{}) : nullptr;
+        default: return nullptr;
+    }
+}
+
+}  // namespace q4k

@@ -4,13 +4,14 @@
 // translation unit of their own for the launch shapes the automatic
 // geometry picks for plain products (one row per tile, 8 or 16 waves, 1 or 2
 // slots, prologue 0, 1 or 3; the block-per-lane kernel at 4 or 8 waves; the
-// matrix-core kernel for 1..8 columns; the K-split kernel in every shape it
-// is instantiated in); q4k_gemv.hip launches them with the
+// matrix-core kernel for 1..8 columns; the K-split kernels in every shape they
+// are instantiated in); q4k_gemv.hip launches them with the
 // product's own geometry.
 #include <hip/hip_runtime.h>
 
 #include "q4k_gemv_kernels.h"
 #include "q4k_ksplit.h"
+#include "q4k_ksplit_nc.h"
 #include "q4k_mfma.h"
 #include "q4k_runtime.h"
 
@@ -96,6 +97,10 @@ const void *q4k_ksplit_sums_kernel(int sbw, int waves, int slots, int G) {
 
 const void *q4k_ksplit_long_sums_kernel(int sbw, int waves, int slots, int G) {
     return ksplit_long_kernel<true>(sbw, waves, slots, G);
+}
+
+const void *q4k_ksplit_nc_sums_kernel(int nc, int sbw, int waves, int slots, int G, bool staged) {
+    return ksplit_nc_kernel<true>(nc, sbw, waves, slots, G, staged);
 }
 
 const void *q4k_bpl_sums_kernel(int waves) {

@@ -1,0 +1,175 @@
+"""GPU parity of the K-split kernel for two to four F32 columns (rows of
+4096 or 8192 values; each wave owns a residue class of super-blocks so that
+its DPP steps and the tree over the waves form the tile kernel's
+several-column reduction tree), with the activation quantised by every wave
+for its own slices (in registers) or once per workgroup into LDS (staged;
+pipeline override prologue 2 and 0).
+
+Bar: outputs bit for bit equal to the tile kernel's in every instantiated
+launch shape, including uneven row splits and workgroups with fewer rows
+than a wave step covers, and within the parity tolerance of the oracle;
+the int32 sub-block and activation sums of its parity variant bit for bit
+against the oracle.
+"""
+import numpy as np
+import pytest
+
+import _common
+
+pytestmark = pytest.mark.gpu
+
+
+def exists(nc, tr, waves, slots, G):
+    """The instantiated variants (rows per step 8 = two super-blocks per
+    wave, two columns only; 4 = four super-blocks; 16 waves where the
+    registers fit)."""
+    sbw = 16 // tr
+    if not (sbw == 4 or (sbw == 2 and nc == 2)):
+        return False
+    if waves % (16 // sbw) or slots not in (1, 2):
+        return False
+    return waves < 16 or (G == 1 and (nc < 4 or slots == 1))
+
+
+def shapes(nc, G):
+    return [(tr, w, s) for tr in (8, 4) for w in (4, 8, 16) for s in (1, 2) if exists(nc, tr, w, s, G)]
+
+
+_wcache = {}
+
+
+def inputs(Q, M, K, N, seed):
+    key = (M, K, seed)
+    if key not in _wcache:
+        _wcache.clear()
+        _wcache[key] = Q.quantize_rows_q4_K(_common.weights(M, K, seed), nthreads=16)
+    return _wcache[key], _common.activations(N, K, seed)
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+STAGING = {"registers": 2, "staged": 0}
+
+
+def stagings(nc):
+    """Staged variants exist for three or four columns."""
+    return list(STAGING) if nc >= 3 else ["registers"]
+
+
+def run_forced(Q, wd, K, xd, tr, waves, slots, wgs=0, staging="registers"):
+    N = xd.shape[0]
+    try:
+        Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, workgroups=wgs, kernel=5)
+        Q.set_pipeline_override(slots=slots, prologue=STAGING[staging])
+        g = Q.geometry(K, wd.shape[0], N)
+        assert g["kernel"] == 5 and g["rows_per_step"] == tr and g["waves_per_wg"] == waves, g
+        assert g["cols_per_launch"] == N, g
+        return Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+        Q.set_pipeline_override()
+
+
+@pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 4096), (1024, 4096), (3001, 4096), (37, 4096),
+                                 (1, 4096), (5000, 8192), (258, 8192), (20, 8192)])
+@pytest.mark.parametrize("N", [2, 3, 4])
+def test_ksplit_nc_bits_equal_tile_kernel(Q, O, gpu, M, K, N):
+    """Every instantiated launch shape, with one workgroup per CU, 7 (up to
+    2048 rows each: uneven tiles per team) and 300 (workgroups with fewer
+    rows than a step), against the tile kernel bit for bit; the tile kernel
+    against the oracle."""
+    wq, x = inputs(Q, M, K, N, seed=31 + N)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    try:
+        Q.set_geometry_override(kernel=1)
+        assert Q.geometry(K, M, N)["kernel"] == 1
+        y_tile = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+    rows = np.arange(M) if M <= 1024 else np.unique(
+        np.concatenate([[0, 1, M - 2, M - 1], np.random.default_rng(M).choice(M, 300, replace=False)]))
+    ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"tile {M}x{K} N={N}")
+    for tr, waves, slots in shapes(N, K // 4096):
+        for wgs in (0, max(7, -(-M // 2048)), 300):
+            for staging in stagings(N):
+                y = run_forced(Q, wd, K, xd, tr, waves, slots, wgs, staging)
+                if not np.array_equal(y, y_tile):
+                    bad = np.argwhere(y != y_tile)
+                    raise AssertionError(f"{M}x{K} N={N} rows/step {tr} waves {waves} slots {slots} wgs {wgs} "
+                                         f"{staging}: {len(bad)} outputs differ from the tile kernel, e.g. "
+                                         f"(col, row) {bad[:5].tolist()}")
+
+
+@pytest.mark.parametrize("M,K", [(4096, 4096), (333, 4096), (1030, 8192)])
+@pytest.mark.parametrize("N", [2, 3, 4])
+def test_ksplit_nc_sums_exact(Q, O, gpu, M, K, N):
+    """The parity variant of each launch shape: S_qq of every lane and
+    column and S_q of the in-register quantisation bit for bit against the
+    oracle, outputs equal to the product launch's."""
+    import torch
+    wq, x = inputs(Q, M, K, N, seed=41 + N)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    rows = np.unique(np.concatenate([[0, M // 2, M - 1], np.random.default_rng(M).choice(M, 100, replace=False)]))
+    ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x))
+    for (tr, waves, slots), staging in [(sh, st) for sh in shapes(N, K // 4096) for st in stagings(N)]:
+        try:
+            Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
+            Q.set_pipeline_override(slots=slots, prologue=STAGING[staging])
+            assert Q.geometry(K, M, N)["kernel"] == 5
+            y, sums, sq = Q.mul_mat_vec_q_sums(wd, K, xd)
+            y_prod = Q.mul_mat_vec_q(wd, K, xd)
+        finally:
+            Q.set_geometry_override()
+            Q.set_pipeline_override()
+        where = f"{M}x{K} N={N} rows/step {tr} waves {waves} slots {slots} {staging}"
+        assert torch.equal(y, y_prod), where
+        got = sums[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        assert np.array_equal(got, ref["sqq"]), f"{where}: S_qq differ"
+        assert np.array_equal(sq.cpu().numpy(), ref["sq"]), f"{where}: S_q differ"
+
+
+def test_ksplit_nc_column_strides(Q, O, gpu):
+    """Columns further apart than K (a 16-byte multiple) and an output with
+    its own stride: the same bits as the tile kernel on the same views."""
+    import torch
+    M, K, N = 2000, 4096, 3
+    wq, x = inputs(Q, M, K, N, seed=51)
+    wd = to_dev(wq, gpu)
+    xb = torch.zeros((N, K + 64), dtype=torch.float32, device=gpu)
+    xb[:, :K] = to_dev(x, gpu)
+    xv = xb[:, :K]
+    outs = []
+    for kern, pro in ((1, -1), (5, 2), (5, 0)):
+        ob = torch.full((N, M + 8), -1.0, dtype=torch.float32, device=gpu)
+        try:
+            Q.set_geometry_override(rows_per_tile=4 if kern == 5 else 0, waves_per_wg=8 if kern == 5 else 0,
+                                    kernel=kern)
+            Q.set_pipeline_override(prologue=pro)
+            assert Q.geometry(K, M, N)["kernel"] == kern
+            Q.mul_mat_vec_q(wd, K, xv, out=ob[:, :M])
+        finally:
+            Q.set_geometry_override()
+            Q.set_pipeline_override()
+        assert torch.all(ob[:, M:] == -1.0), "wrote past the output rows"
+        outs.append(ob[:, :M].cpu().numpy())
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("M,K,N,kernel", [(14336, 4096, 2, 5), (4096, 4096, 2, 5), (1024, 4096, 2, 5),
+                                          (128256, 4096, 2, 5), (4096, 8192, 2, 5), (4096, 4096, 3, 5),
+                                          (1024, 4096, 3, 5), (14336, 4096, 3, 1), (14336, 4096, 4, 1),
+                                          (28672, 8192, 3, 5), (28672, 8192, 4, 5), (14336, 8192, 4, 1),
+                                          (4096, 14336, 2, 1)])
+def test_ksplit_nc_automatic_choice(Q, gpu, M, K, N, kernel):
+    """The automatic geometry: the K-split kernel where it measured faster
+    than the tile kernel (two columns of 4096 or 8192 values, three columns
+    up to 16 rows per CU, three or four columns of 8192 values at 96 rows
+    per CU or more), the tile kernel elsewhere; the pre-quantised route
+    stays on the tile kernel (same bits)."""
+    g = Q.geometry(K, M, N)
+    assert g["kernel"] == kernel and g["cols_per_launch"] == N, g
+    assert Q.geometry(K, M, N, route="q8_1")["kernel"] == 1
