@@ -167,6 +167,13 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 //             c*qcol + 4096i + 1024k + 16(4g + j) + t (qcol = 4096*ceil(K/4096)),
 //             so that the 64 lanes of a wave reading chunk k of their blocks
 //             read one contiguous, bank-conflict-free 1 KB.
+//   Q4K K-split  the Q4K tile layout with the 16 super-block positions g of
+//             a group permuted, at slot (g mod 8)*2 + g/8 (two-column tree)
+//             or (g mod 4)*4 + g/4 (four-column tree): the several-column
+//             K-split kernels' waves own positions {w, w+8} or {w, w+4, w+8,
+//             w+12}, which the tile order puts 512 or 256 bytes apart, in
+//             the same banks; permuted, a wave's lanes again read one
+//             contiguous span.
 //   Q6K tile  the Q6_K tile kernel's read order: position 128h + 32m + 16j' + t
 //             of super-block kb = 16i + g at c*qcol + 4096i + 1024m +
 //             16(4g + 2h + j') + t -- lane 4g + 2h + j' reads, for each m, the 16
@@ -200,6 +207,14 @@ constexpr int kLayoutQ6K = 2;
 constexpr int kLayoutQ6KDense = 3;
 constexpr int kLayoutMfma = 4;  // linear q8 columns; (d8, d8*sum) per [block][column] of 8 columns
 constexpr int kLayoutMfmaQ6 = 5;  // linear q8 columns; d8 per [block][column] of 8 columns
+constexpr int kLayoutQ4KS2 = 6;   // Q4K, positions permuted for the two-column K-split tree
+constexpr int kLayoutQ4KS4 = 7;   // Q4K, positions permuted for the four-column K-split tree
+
+// Slot of super-block position g (0..15) of a group in the Q4K layouts.
+template <int LAYOUT>
+__host__ __device__ constexpr int q4k_slot(int g) {
+    return LAYOUT == kLayoutQ4KS2 ? (g & 7) * 2 + (g >> 3) : (LAYOUT == kLayoutQ4KS4 ? (g & 3) * 4 + (g >> 2) : g);
+}
 
 constexpr bool is_q6_layout(int layout) { return layout == kLayoutQ6K || layout == kLayoutQ6KDense; }
 
@@ -215,9 +230,9 @@ template <int LAYOUT>
 __device__ __forceinline__ int q8_offset(int c, int qcol, int nb, int b, int e) {
     if (LAYOUT == kLayoutLinear || LAYOUT == kLayoutMfma || LAYOUT == kLayoutMfmaQ6) return c * qcol + b * 32 + e * 4;
     const int kb = b >> 3, s = b & 7;
-    if (LAYOUT == kLayoutQ4K)
-        return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (e >> 2)) * 1024 + ((kb & 15) * 4 + (s >> 1)) * 16 +
-               (e & 3) * 4;
+    if (LAYOUT == kLayoutQ4K || LAYOUT == kLayoutQ4KS2 || LAYOUT == kLayoutQ4KS4)
+        return c * qcol + (kb >> 4) * 4096 + ((s & 1) * 2 + (e >> 2)) * 1024 +
+               (q4k_slot<LAYOUT>(kb & 15) * 4 + (s >> 1)) * 16 + (e & 3) * 4;
     const int cs = LAYOUT == kLayoutQ6KDense ? group_chunk_stride(kb >> 4, nb) : 1024;
     // Q6K: s = 4h + m, values 16j' + 4(e & 3) + [0, 4) with j' = e >> 2
     return c * qcol + (kb >> 4) * 4096 + (s & 3) * cs + ((kb & 15) * 4 + (s >> 2) * 2 + (e >> 2)) * 16 +

@@ -202,6 +202,7 @@ struct Geometry {
     int ksplit = 0;     // K-split kernel: super-blocks per wave and group (0: another kernel)
     int ks_long = 0;    // K-split kernel for rows of any length (activation slices in LDS)
     int ks_staged = 0;  // several-column K-split kernel: activation quantised once per workgroup into LDS
+    int ks_p = 0;       // several-column K-split kernel: columns of its reduction tree (2 or 4)
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
@@ -329,26 +330,33 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
 // (whole teams of TR waves), workgroups (default one per CU) and row tiles
 // in flight per wave (1 or 2).
 static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
-                                     int wgs, int slots, int N = 1, int staged = 0) {
+                                     int wgs, int slots, int N = 1, int staged = 0, int P = 0) {
     Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
-    if (N >= 2) {  // two to four columns of rows of 1 or 2 groups
-        const int G = (int)(K / 4096);
-        g.ksplit = N == 2 && rows_per_step == 8 ? 2 : 4;
+    if (N >= 2) {  // two to four columns
+        const bool lng = K != 4096 && K != 8192;  // rows of other lengths: the long-row form (staged)
+        const int G = lng ? (int)((K / kQK + 15) / 16) : (int)(K / 4096);
+        g.ks_long = lng ? 1 : 0;
+        g.ks_p = lng && P == 2 ? 2 : (N <= 2 ? 2 : 4);  // rows of 1 or 2 groups: the columns rounded up
+        g.ksplit = g.ks_p == 2 && rows_per_step == 8 ? 2 : 4;
         g.R = 16 / g.ksplit;
         g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 8;
         if (g.waves < g.R) g.waves = g.R;
         g.slots = slots == 1 || slots == 2 ? slots : 2;
-        if (!ksplit_nc_exists(N, g.ksplit, g.waves, g.slots, G)) g.slots = 1;
-        if (!ksplit_nc_exists(N, g.ksplit, g.waves, g.slots, G)) {
+        auto exists = [&]() {
+            return lng ? ksplit_nc_long_exists(N, g.ks_p, g.ksplit, g.waves, g.slots)
+                       : ksplit_nc_exists(N, g.ksplit, g.waves, g.slots, G);
+        };
+        if (!exists()) g.slots = 1;
+        if (!exists()) {
             g.waves = 8;
             g.slots = 2;
         }
-        // three or four columns: the activation quantised once per
-        // workgroup (prologue override 0) or by every wave for its own
-        // slices (2); otherwise as `staged` says
+        // rows of 1 or 2 groups, three or four columns: the activation
+        // quantised once per workgroup (prologue override 0) or by every
+        // wave for its own slices (2); otherwise as `staged` says
         const int opro = g_ovr_prologue.load();
-        g.ks_staged = N >= 3 && (opro == 0 || (opro != 2 && staged)) ? 1 : 0;
+        g.ks_staged = lng || (N >= 3 && (opro == 0 || (opro != 2 && staged))) ? 1 : 0;
         int64_t grid = wgs > 0 ? wgs : cus;
         if (grid > M) grid = M;
         g.grid = grid < 1 ? 1 : (int)grid;
@@ -495,12 +503,38 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
 //  - three or four columns, K = 8192, 96 rows per CU or more: 4 rows, 4
 //    waves, two tiles in flight, in registers (28672 x 8192 N=3 28.63 /
 //    29.19, N=4 30.28 / 32.03).
+//  - rows of other lengths over 8192 values (the long-row form, staged): 4 rows per step
+//    and 16 waves (four teams; two columns: 4 super-blocks per wave).  Two
+//    columns: two tiles in flight where a wave's steps are even in number,
+//    else one (4096 x 14336 10.52 against 10.94, 1024 x 14336 7.90 / 8.94,
+//    14336 x 14336 24.82 / 25.20, 8192 x 28672 30.44 / 31.54, 4096 x 11008
+//    9.06 / 9.30); three or four columns up to 16384 values, one tile in
+//    flight, two up to 4 rows per CU (4096 x 14336 N=3 13.15 against 14.5-15.9
+//    with the quantiser launch, N=4 16.11 / 17.29, 1024 x 14336 N=4 11.51 /
+//    11.97, 4096 x 11008 N=4 12.29 / 13.75; 8192 x 28672 N=4 40.02 / 38.17
+//    stays on the tile kernel).  Staged in the tile kernel's layout, with
+//    the super-block positions unpermuted, the reads of the four-column tree
+//    conflicted four ways (4096 x 14336 N=4 18.39, 8192 x 28672 N=4 47.37).
 //  The tile kernel elsewhere: four columns of 4096 values (14336 x 4096
 //  10.97 staged against 10.68, 4096 x 4096 6.47 / 6.29), 56 rows per CU of
 //  8192 values (14336 x 8192 N=3 17.54 / 16.77, N=4 19.06 / 18.88).
 static bool ksplit_nc_auto(int64_t K, int64_t M, int64_t N, int cus, int &tr, int &waves, int &slots,
                            int &staged) {
     const int64_t rho = (M + cus - 1) / cus;
+    if (K != 4096 && K != 8192) {
+        if (K < 8192) return false;  // rows shorter than two groups: not measured
+        tr = 4;
+        waves = 16;
+        staged = 1;
+        if (N == 2) {
+            const int64_t G = (K / kQK + 15) / 16;
+            const int64_t steps = ((rho + 3) / 4 + 3) / 4 * G;  // per wave: tiles per team x groups
+            slots = steps % 2 == 0 ? 2 : 1;
+            return true;
+        }
+        slots = rho <= 4 ? 2 : 1;
+        return K <= 16384;
+    }
     staged = 0;
     slots = 1;
     if (N == 2) {
@@ -560,9 +594,13 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // bits, takes the rest
     const bool ks_ok = N == 1 && !fused && mats == 1 && f32_vec && K <= 8 * 4096;
     // two to four columns: the K-split kernel for rows of 1 or 2 groups
-    const bool ksn_ok = N >= 2 && N <= 4 && !fused && mats == 1 && f32_vec && (K == 4096 || K == 8192);
+    // (the tile kernel's launches, whose bits these are: all columns in one,
+    // or four columns two by two)
+    const bool ksn_ok = N >= 2 && N <= 4 && !fused && mats == 1 && f32_vec && K <= 8 * 4096 &&
+                        (nc == N || (nc == 2 && N == 4));
+    const int ksn_p = nc <= 2 ? 2 : 4;
     if ((ks_ok || ksn_ok) && okern == 5)
-        return pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load(), (int)N, 1);
+        return pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load(), (int)N, 1, ksn_p);
     // (automatic: where the partials fit the LDS)
     if (ks_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
         int tr = 0, kw = 0, ks = 0;
@@ -576,7 +614,8 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
         int tr = 0, kw = 0, ks = 0, st = 0;
         if (ksplit_nc_auto(K, M, N, cus, tr, kw, ks, st)) {
             const int os = g_ovr_slots.load();
-            const Geometry gk = pick_geometry_ksplit(di, K, M, tr, kw, 0, os == 1 || os == 2 ? os : ks, (int)N, st);
+            const Geometry gk =
+                pick_geometry_ksplit(di, K, M, tr, kw, 0, os == 1 || os == 2 ? os : ks, (int)N, st, ksn_p);
             if (gk.lds <= max_lds) return gk;
         }
     }
@@ -902,9 +941,13 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
     } else if (geo.ksplit) {
         if (!p.x || !p.vec_ok) return Q4K_EINVAL;
         if (nc > 1) {
-            if (geo.ks_long || nc != geo.nc_chunk) return Q4K_EINVAL;
-            fn = p.sums ? q4k_ksplit_nc_sums_kernel(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0)
-                        : ksplit_nc_kernel<false>(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0);
+            if (nc != geo.nc_chunk) return Q4K_EINVAL;
+            if (geo.ks_long)
+                fn = p.sums ? q4k_ksplit_nc_long_sums_kernel(nc, geo.ks_p, geo.ksplit, geo.waves, geo.slots)
+                            : ksplit_nc_long_kernel<false>(nc, geo.ks_p, geo.ksplit, geo.waves, geo.slots);
+            else
+                fn = p.sums ? q4k_ksplit_nc_sums_kernel(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0)
+                            : ksplit_nc_kernel<false>(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0);
             p.ring_off = geo.ks_staged ? lds_bytes(p.K, nc) : 0;
         } else if (geo.ks_long) {
             fn = p.sums ? q4k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
@@ -1134,8 +1177,9 @@ static int mul_mat_vec_q_q4k(const void *src0, int64_t ne00, int64_t ne01, int64
     // reached through that copy, with or without a workspace (so both give
     // the pre-quantised entry point's bits)
     const bool ga_route = pick_geometry(*di, ne00, ne01, ne11, 0, 1, false, true).mfma_ga != 0;
-    if (geo.nc_chunk >= ne11 && !ga_route && !(ws_fits && prefer_prequantised(ne00, ne11))) {
-        // quantisation inside the GEMV launch
+    if (geo.nc_chunk >= ne11 && !ga_route && (geo.ksplit || !(ws_fits && prefer_prequantised(ne00, ne11)))) {
+        // quantisation inside the GEMV launch (always for the K-split
+        // kernels, the one route they have)
         return run_gemv(src0, ne00, ne01, nb01, src1, ldx, nullptr, 0, ne11, dst, ldd, s, nullptr, nullptr, so);
     }
     // activation too large for one workgroup's LDS at this column count,

@@ -1,5 +1,6 @@
-// q4k_ksplit_nc.h -- the K-split Q4_K GEMV kernel for two to four F32
-// activation columns, rows of one or two 16-block groups (K = 4096 or 8192).
+// q4k_ksplit_nc.h -- the K-split Q4_K GEMV kernels for two to four F32
+// activation columns: rows of one or two 16-block groups (K = 4096 or 8192),
+// and rows of other lengths up to 8 groups (the long-row form).
 //
 // The one-column K-split kernel (q4k_ksplit.h) with NC accumulators per
 // lane.  What changes is which super-blocks a wave owns, so that the
@@ -24,10 +25,10 @@
 // hands the lanes their sub-blocks through ds_bpermute, as the one-column
 // kernel (every team quantises the whole activation), or (STAGED) the
 // workgroup quantises the activation once into LDS with the tile kernel's
-// staging (layout, arithmetic and barriers) and each lane reads its
-// sub-blocks there, as a tile-kernel lane owning the same super-block and
-// chunk would: with three or four columns the per-team quantisation costs
-// more than the barrier.
+// staging (arithmetic and barriers; the layout with the super-block
+// positions permuted so that a wave's lanes read one contiguous span) and
+// each lane reads its sub-blocks there: with three or four columns the
+// per-team quantisation costs more than the barrier.
 //
 // Reference: kernels/mmvq.cu:150-344 (ncols_dst 2-4) with the vec-dot of
 // kernels/vecdotq.cuh:775-819 and :457-483.
@@ -80,6 +81,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_nc_kernel(Q4K_GE
     constexpr int KW = 16 / SBW;  // waves sharing a row
     constexpr int TR = 16 / SBW;  // rows per wave step
     constexpr int TEAMS = WAVES / KW;
+    constexpr int kLayout = P == 2 ? kLayoutQ4KS2 : kLayoutQ4KS4;  // the staged activation's layout
     constexpr int V = 4 * SBW;    // activation values per lane, group and column
     static_assert(NC >= 2 && NC <= 4 && SBW >= P && SBW <= 4, "two to four columns, 2 or 4 super-blocks");
     static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_nc_kernel(Q4K_GE
     //    workgroup's staging, then each lane reads what the tile kernel's
     //    lane 4*kb0 + j reads)
     Lane ln;
-    ln.lane = 4 * kb0 + j;
+    ln.lane = 4 * q4k_slot<kLayout>(kb0) + j;
     ln.g = kb0;
     ln.j = j;
     ln.sel = make_scale_sel(j);
@@ -171,7 +173,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_nc_kernel(Q4K_GE
     if constexpr (STAGED) {
         int8_t *q8s = reinterpret_cast<int8_t *>(lds);
         float2 *dks = reinterpret_cast<float2 *>(lds + NC * p.qcol);
-        stage_f32_finish<kLayoutQ4K, kLPB, kWave * WAVES, NC < 4 ? 1 : kFinishRounds>(
+        stage_f32_finish<kLayout, kLPB, kWave * WAVES, NC < 4 ? 1 : kFinishRounds>(
             p.x, p.ldx, p.K, NC, true, p.nblk32, xs, p.qcol, q8s, dks, SUMS ? p.sq : nullptr);
         __syncthreads();
 #pragma unroll
@@ -272,6 +274,191 @@ const void *ksplit_nc_sym(int slots, int G, bool staged) {
     using I2 = std::integral_constant<int, 2>;
     if (slots == 1) return G == 1 ? one(I1{}, I1{}) : (G == 2 ? one(I1{}, I2{}) : nullptr);
     if (slots == 2) return G == 1 ? one(I2{}, I1{}) : (G == 2 ? one(I2{}, I2{}) : nullptr);
+    return nullptr;
+}
+
+// ------------------------------------------------------------------------
+// Rows of any other length up to 8 groups (the last one possibly partial):
+// the activation is staged once per workgroup as in the STAGED variant, and
+// each step's lanes read their sub-blocks of the step's group from LDS (as
+// the tile kernel's lanes do at each group); steps walk (tile, group)
+// pairs, S in flight, as in the one-column long-row kernel.  A lane whose
+// super-block lies past the row's end reads zero weights (outside the
+// workgroup's buffer) and adds exactly zero, as the tile kernel's lane of
+// that super-block does; a wave whose first super-block of a group lies
+// past the end skips the group.
+// P: the reduction tree's column count (2 or 4), that of the tile kernel's
+// launches for the same product: NC rounded up, or 2 for four columns when
+// the tile kernel's LDS holds only two of them per launch (then each column
+// gets that launch's two-column tree).
+// ------------------------------------------------------------------------
+template <int NC, int P, int SBW, int WAVES, int S, bool SUMS = false>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_nc_long_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    static_assert(P == 2 || P == 4, "two- or four-column trees");
+    constexpr int KW = 16 / SBW;
+    constexpr int TR = 16 / SBW;
+    constexpr int TEAMS = WAVES / KW;
+    constexpr int kLayout = P == 2 ? kLayoutQ4KS2 : kLayoutQ4KS4;  // the staged activation's layout
+    static_assert(NC >= 2 && NC <= 4 && SBW >= P && SBW <= 4, "two to four columns, 2 or 4 super-blocks");
+    static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    int8_t *q8s = reinterpret_cast<int8_t *>(lds);
+    float2 *dks = reinterpret_cast<float2 *>(lds + NC * p.qcol);
+    float *part = reinterpret_cast<float *>(lds + p.ring_off);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slice = wave % KW, team = wave / KW;
+    const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1), j = lane & 3;
+    const int G = p.G;
+
+    const int b = (int)blockIdx.x;
+    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
+    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int nt = (n + TR - 1) / TR;
+    const int tq = nt / TEAMS, trem = nt - tq * TEAMS;
+    const int tb = team * tq + min(team, trem);
+    const int ntiles = tq + (team < trem ? 1 : 0);
+    const int kb0 = ksn_block<P, SBW>(slice, s);       // the lane's super-block within each group
+    const int wkb = ksn_block<P, SBW>(slice, 0);       // the wave's first one
+
+    // 1. the staging loads of every wave, queued ahead of the weight loads
+    constexpr int kLPB = stage_lpb(NC);
+    constexpr int kPreR = pre_rounds(NC, kWave * WAVES);
+    ActStage<kLPB, kPreR> xs;
+    stage_f32_issue<kLPB, kWave * WAVES>(p.x, p.ldx, p.K, NC, true, p.nblk32, xs);
+    __syncthreads();
+
+    // 2. the first S steps' weights
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    const uint32_t lh = (uint32_t)r * (uint32_t)p.row_stride + (uint32_t)(kb0 * kBlockBytes);
+    const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
+    const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
+    auto load_step = [&](Step st, RowRegs &w) {
+        const bool ok = st.tile < ntiles && 16 * st.i + kb0 < p.nb;
+        const uint32_t base = (uint32_t)(tb + st.tile) * tile_bytes + (uint32_t)st.i * (16u * kBlockBytes);
+        const uint32_t oh = ok ? base + lh : kOOB;
+        const uint32_t oq = ok ? base + lq : kOOB;
+        w.h = load16(rs, oh);
+        w.q0 = load16(rs, oq);
+        w.q1 = load16(rs, oq + 16u);
+    };
+    Step st[S];
+    RowRegs w[S];
+    st[0] = Step{0, 0};
+#pragma unroll
+    for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], G);
+#pragma unroll
+    for (int k = 0; k < S; ++k) load_step(st[k], w[k]);
+
+    // 3. quantise into LDS (the tile kernel's layout and arithmetic)
+    stage_f32_finish<kLayout, kLPB, kWave * WAVES, NC < 4 ? 1 : kFinishRounds>(
+        p.x, p.ldx, p.K, NC, true, p.nblk32, xs, p.qcol, q8s, dks, SUMS ? p.sq : nullptr);
+    __syncthreads();
+
+    Lane ln;
+    ln.lane = 4 * q4k_slot<kLayout>(kb0) + j;
+    ln.g = kb0;
+    ln.j = j;
+    ln.sel = make_scale_sel(j);
+    // 4. the (tile, group) steps, S in flight
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
+    int remaining = ntiles * G;
+    if (remaining > 0) {
+        for (;;) {
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                const int rl = (tb + st[k].tile) * TR + r;
+                if (16 * st[k].i + wkb < p.nb) {  // the wave's slice reaches this group
+                    const RowScales sc = row_scales(w[k], ln);
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) {
+                        const LaneAct a = lane_act(p, ln, st[k].i, c, q8s, dks);
+                        int sa, sb;
+                        accumulate(w[k], sc, a, acc[c], sa, sb);
+                        if constexpr (SUMS) {
+                            const int kb = 16 * st[k].i + kb0;
+                            if (st[k].tile < ntiles && rl < n && kb < p.nb) {
+                                int32_t *o = p.sums + ((int64_t)c * p.M + wg_beg + rl) * (p.K / 32) + kb * 8 + 2 * j;
+                                o[0] = sa;
+                                o[1] = sb;
+                            }
+                        }
+                    }
+                }
+                if (st[k].i == G - 1) {
+                    const bool wr = ks_writer<SBW>(lane) && st[k].tile < ntiles && rl < n;
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) {
+                        const float q = ksn_reduce<P, SBW>(acc[c]);
+                        if (wr) part[(rl * NC + c) * KW + slice] = q;
+                        acc[c] = 0.0f;
+                    }
+                }
+                st[k] = next_step(st[(k + S - 1) % S], G);
+                load_step(st[k], w[k]);
+            }
+            remaining -= S;
+            if (remaining <= 0) break;
+        }
+    }
+    __syncthreads();
+    for (int e = (int)threadIdx.x; e < n * NC; e += kWave * WAVES) {
+        const int row = e / NC, c = e - row * NC;
+        float q[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) q[k] = part[e * KW + k];
+#pragma unroll
+        for (int h = KW / 2; h >= 1; h /= 2)
+#pragma unroll
+            for (int t = 0; t < h; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+        p.dst[c * p.ld_dst + wg_beg + row] = q[0];
+    }
+}
+
+// The instantiated long-row variants (P: 2 for two columns, 4 for three,
+// 2 or 4 for four).
+constexpr bool ksplit_nc_long_exists(int nc, int p, int sbw, int waves, int slots) {
+    return ((nc == 2 && p == 2) || (nc == 3 && p == 4) || (nc == 4 && (p == 2 || p == 4))) && sbw >= p &&
+           (sbw == 2 || sbw == 4) && (waves == 4 || waves == 8 || waves == 16) && waves % (16 / sbw) == 0 &&
+           (slots == 1 || slots == 2);
+}
+
+// The long-row K-split kernel for nc = 2..4 columns and a p-column tree, or null.
+template <bool SUMS>
+const void *ksplit_nc_long_kernel(int nc, int p, int sbw, int waves, int slots) {
+    auto pick = [&](auto nc_c, auto p_c, auto sbw_c) -> const void * {
+        constexpr int NC = decltype(nc_c)::value, PP = decltype(p_c)::value, B = decltype(sbw_c)::value;
+        auto by_slots = [&](auto waves_c) -> const void * {
+            constexpr int W = decltype(waves_c)::value;
+            if constexpr (ksplit_nc_long_exists(NC, PP, B, W, 1))
+                if (slots == 1)
+                    return reinterpret_cast<const void *>(&gemv_q4k_ksplit_nc_long_kernel<NC, PP, B, W, 1, SUMS>);
+            if constexpr (ksplit_nc_long_exists(NC, PP, B, W, 2))
+                if (slots == 2)
+                    return reinterpret_cast<const void *>(&gemv_q4k_ksplit_nc_long_kernel<NC, PP, B, W, 2, SUMS>);
+            return nullptr;
+        };
+        if (waves == 4) return by_slots(std::integral_constant<int, 4>{});
+        if (waves == 8) return by_slots(std::integral_constant<int, 8>{});
+        if (waves == 16) return by_slots(std::integral_constant<int, 16>{});
+        return nullptr;
+    };
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    auto by_sbw = [&](auto nc_c, auto p_c) -> const void * {
+        if (sbw == 2) return pick(nc_c, p_c, I2{});
+        if (sbw == 4) return pick(nc_c, p_c, I4{});
+        return nullptr;
+    };
+    if (nc == 2 && p == 2) return by_sbw(I2{}, I2{});
+    if (nc == 3 && p == 4) return by_sbw(I3{}, I4{});
+    if (nc == 4 && p == 2) return by_sbw(I4{}, I2{});
+    if (nc == 4 && p == 4) return by_sbw(I4{}, I4{});
     return nullptr;
 }
 

@@ -81,6 +81,7 @@ const void *q4k_mfma_sums_kernel(int nc, int waves);
 const void *q4k_ksplit_sums_kernel(int sbw, int waves, int slots, int G);
 const void *q4k_ksplit_long_sums_kernel(int sbw, int waves, int slots, int G);
 const void *q4k_ksplit_nc_sums_kernel(int nc, int sbw, int waves, int slots, int G, bool staged);
+const void *q4k_ksplit_nc_long_sums_kernel(int nc, int p, int sbw, int waves, int slots);
 const void *q4k_mfma_ga_sums_kernel(int nc, int waves, int nif);
 const void *q6k_mfma_sums_kernel(int nc, int waves);
 const void *q6k_ksplit_sums_kernel(int sbw, int waves, int slots, int G);

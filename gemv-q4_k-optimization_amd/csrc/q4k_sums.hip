@@ -103,6 +103,10 @@ const void *q4k_ksplit_nc_sums_kernel(int nc, int sbw, int waves, int slots, int
     return ksplit_nc_kernel<true>(nc, sbw, waves, slots, G, staged);
 }
 
+const void *q4k_ksplit_nc_long_sums_kernel(int nc, int p, int sbw, int waves, int slots) {
+    return ksplit_nc_long_kernel<true>(nc, p, sbw, waves, slots);
+}
+
 const void *q4k_bpl_sums_kernel(int waves) {
     return waves == 8 ? reinterpret_cast<const void *>(&gemv_q4k_bpl_kernel<8, true>)
                       : reinterpret_cast<const void *>(&gemv_q4k_bpl_kernel<4, true>);

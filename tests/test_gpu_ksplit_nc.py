@@ -35,6 +35,24 @@ def shapes(nc, G):
     return [(tr, w, s) for tr in (8, 4) for w in (4, 8, 16) for s in (1, 2) if exists(nc, tr, w, s, G)]
 
 
+def long_shapes(p):
+    """The long-row form's variants for a p-column tree (rows per step 8:
+    two super-blocks per wave, p = 2 only)."""
+    return [(tr, w, s) for tr in (8, 4) for w in (4, 8, 16) for s in (1, 2)
+            if 16 // tr >= p and w % tr == 0]
+
+
+def tile_tree(Q, K, M, N):
+    """Columns per launch of the tile kernel (whose bits the K-split forms
+    reproduce), rounded up to its reduction tree's 2 or 4."""
+    try:
+        Q.set_geometry_override(kernel=1)
+        chunk = Q.geometry(K, M, N)["cols_per_launch"]
+    finally:
+        Q.set_geometry_override()
+    return chunk, (2 if chunk <= 2 else 4)
+
+
 _wcache = {}
 
 
@@ -163,13 +181,78 @@ def test_ksplit_nc_column_strides(Q, O, gpu):
                                           (128256, 4096, 2, 5), (4096, 8192, 2, 5), (4096, 4096, 3, 5),
                                           (1024, 4096, 3, 5), (14336, 4096, 3, 1), (14336, 4096, 4, 1),
                                           (28672, 8192, 3, 5), (28672, 8192, 4, 5), (14336, 8192, 4, 1),
-                                          (4096, 14336, 2, 1)])
+                                          (4096, 14336, 2, 5), (4096, 14336, 3, 5), (4096, 14336, 4, 5),
+                                          (8192, 28672, 2, 5), (8192, 28672, 4, 1), (4096, 11008, 4, 5)])
 def test_ksplit_nc_automatic_choice(Q, gpu, M, K, N, kernel):
     """The automatic geometry: the K-split kernel where it measured faster
-    than the tile kernel (two columns of 4096 or 8192 values, three columns
+    than the tile kernel (two columns, three columns of 4096 or 8192 values
     up to 16 rows per CU, three or four columns of 8192 values at 96 rows
-    per CU or more), the tile kernel elsewhere; the pre-quantised route
-    stays on the tile kernel (same bits)."""
+    per CU or more, three or four columns of other lengths up to 16384
+    values), the tile kernel elsewhere; the pre-quantised route stays on
+    the tile kernel (same bits)."""
     g = Q.geometry(K, M, N)
     assert g["kernel"] == kernel and g["cols_per_launch"] == N, g
     assert Q.geometry(K, M, N, route="q8_1")["kernel"] == 1
+
+
+@pytest.mark.parametrize("M,K", [(4096, 14336), (1000, 14336), (333, 28672), (777, 11008), (500, 5120),
+                                 (64, 2304), (37, 256)])
+@pytest.mark.parametrize("N", [2, 3, 4])
+def test_ksplit_nc_long_bits_equal_tile_kernel(Q, O, gpu, M, K, N):
+    """The long-row form (rows of any length up to 8 groups, the last one
+    partial here except at 14336 and 28672; 256 and 2304 values: one
+    partial group), every instantiated launch shape at one workgroup per CU,
+    7 and 300 workgroups, against the tile kernel bit for bit (28672 values
+    in four columns: the tile kernel's LDS takes two per launch, and the
+    K-split form forms their two-column tree); the tile kernel against the
+    oracle."""
+    chunk, p = tile_tree(Q, K, M, N)
+    if N % chunk:
+        pytest.skip(f"the tile kernel launches {chunk} of {N} columns at a time: no K-split form")
+    wq, x = inputs(Q, M, K, N, seed=61 + N)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    try:
+        Q.set_geometry_override(kernel=1)
+        y_tile = Q.mul_mat_vec_q(wd, K, xd).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+    rows = np.arange(M) if M <= 1024 else np.unique(
+        np.concatenate([[0, 1, M - 2, M - 1], np.random.default_rng(M).choice(M, 300, replace=False)]))
+    ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"tile {M}x{K} N={N}")
+    for tr, waves, slots in long_shapes(p):
+        for wgs in (0, 7, 300):
+            y = run_forced(Q, wd, K, xd, tr, waves, slots, wgs, "staged")
+            if not np.array_equal(y, y_tile):
+                bad = np.argwhere(y != y_tile)
+                raise AssertionError(f"{M}x{K} N={N} rows/step {tr} waves {waves} slots {slots} wgs {wgs}: "
+                                     f"{len(bad)} outputs differ from the tile kernel, e.g. (col, row) "
+                                     f"{bad[:5].tolist()}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1000, 14336, 2), (333, 14336, 3), (300, 28672, 4), (129, 5120, 4)])
+def test_ksplit_nc_long_sums_exact(Q, O, gpu, M, K, N):
+    """The long-row form's parity variant: S_qq of every lane and column and
+    S_q of the staging bit for bit against the oracle, outputs equal to the
+    product launch's."""
+    import torch
+    chunk, p = tile_tree(Q, K, M, N)
+    wq, x = inputs(Q, M, K, N, seed=71 + N)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    rows = np.unique(np.concatenate([[0, M // 2, M - 1], np.random.default_rng(M).choice(M, 60, replace=False)]))
+    ref = O.gemv_q4K_q8_1(wq[rows], K, O.quantize_q8_1(x))
+    for tr, waves, slots in long_shapes(p):
+        try:
+            Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
+            Q.set_pipeline_override(slots=slots)
+            assert Q.geometry(K, M, N)["kernel"] == 5
+            y, sums, sq = Q.mul_mat_vec_q_sums(wd, K, xd)
+            y_prod = Q.mul_mat_vec_q(wd, K, xd)
+        finally:
+            Q.set_geometry_override()
+            Q.set_pipeline_override()
+        where = f"{M}x{K} N={N} rows/step {tr} waves {waves} slots {slots}"
+        assert torch.equal(y, y_prod), where
+        got = sums[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        assert np.array_equal(got, ref["sqq"]), f"{where}: S_qq differ"
+        assert np.array_equal(sq.cpu().numpy(), ref["sq"]), f"{where}: S_q differ"
