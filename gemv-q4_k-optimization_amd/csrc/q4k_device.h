@@ -173,7 +173,10 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 //             K-split kernels' waves own positions {w, w+8} or {w, w+4, w+8,
 //             w+12}, which the tile order puts 512 or 256 bytes apart, in
 //             the same banks; permuted, a wave's lanes again read one
-//             contiguous span.
+//             contiguous span.  Their auxiliary pairs are permuted alike
+//             and padded to whole groups: dk[c*pb + 128i + 8*slot + s] for
+//             block s of position g of group i (pb = K/32 rounded up to a
+//             multiple of 128).
 //   Q6K tile  the Q6_K tile kernel's read order: position 128h + 32m + 16j' + t
 //             of super-block kb = 16i + g at c*qcol + 4096i + 1024m +
 //             16(4g + 2h + j') + t -- lane 4g + 2h + j' reads, for each m, the 16
@@ -259,6 +262,12 @@ __device__ __forceinline__ void store_aux(void *aux, int total, int nblk, int c,
         if (half == 0) reinterpret_cast<float2 *>(aux)[b * 8 + c] = make_float2(d8, d8 * (float)qsum);
     } else if (LAYOUT == kLayoutMfmaQ6) {
         if (half == 0) reinterpret_cast<float *>(aux)[b * 8 + c] = d8;
+    } else if (LAYOUT == kLayoutQ4KS2 || LAYOUT == kLayoutQ4KS4) {
+        if (half == 0) {
+            const int kb = b >> 3, pb = (nblk + 127) & ~127;
+            reinterpret_cast<float2 *>(aux)[c * pb + (kb >> 4) * 128 + q4k_slot<LAYOUT>(kb & 15) * 8 + (b & 7)] =
+                make_float2(d8, d8 * (float)qsum);
+        }
     } else if (half == 0) {
         reinterpret_cast<float2 *>(aux)[qb] = make_float2(d8, d8 * (float)qsum);
     }

@@ -363,7 +363,7 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
         g.rows_base = (int)(M / g.grid);
         g.rows_extra = (int)(M % g.grid);
         g.lds = ksplit_nc_part_bytes(g.rows_base + (g.rows_extra ? 1 : 0), N, g.ksplit) +
-                (g.ks_staged ? lds_bytes((int)K, N) : 0);
+                (g.ks_staged ? ksn_stage_bytes((int)K, N) : 0);
         g.lds_launch = g.lds;
         g.nc_chunk = N;
         return g;
@@ -948,7 +948,7 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
             else
                 fn = p.sums ? q4k_ksplit_nc_sums_kernel(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0)
                             : ksplit_nc_kernel<false>(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0);
-            p.ring_off = geo.ks_staged ? lds_bytes(p.K, nc) : 0;
+            p.ring_off = geo.ks_staged ? ksn_stage_bytes(p.K, nc) : 0;
         } else if (geo.ks_long) {
             fn = p.sums ? q4k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                         : ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);

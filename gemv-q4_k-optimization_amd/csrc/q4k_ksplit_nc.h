@@ -70,6 +70,31 @@ __device__ __forceinline__ float ksn_reduce(float v) {
     return v;
 }
 
+// What a lane reads of a staged column in the K-split layouts: the q8 of
+// sub-blocks 2j, 2j+1 of the super-block at slot sl of group i and their
+// (d8, d8 * sum q8) pairs (pb: the column's padded block count).  A lane
+// whose super-block lies past the row's end (in_row false; its weights read
+// as zero) takes the pairs of the group's first super-block: the slots past
+// the row are never written, and stale LDS contents could hold an infinity
+// or NaN that a zero weight would not cancel.
+__device__ __forceinline__ LaneAct ksn_lane_act(int i, int c, int sl, int j, bool in_row, int qcol, int pb,
+                                                const int8_t *q8s, const float2 *dks) {
+    const int8_t *qa = q8s + c * qcol + i * 4096 + (4 * sl + j) * 16;
+    LaneAct a;
+    a.a0 = *reinterpret_cast<const u32x4 *>(qa);
+    a.a1 = *reinterpret_cast<const u32x4 *>(qa + 1024);
+    a.b0 = *reinterpret_cast<const u32x4 *>(qa + 2048);
+    a.b1 = *reinterpret_cast<const u32x4 *>(qa + 3072);
+    a.dk = *reinterpret_cast<const float4 *>(dks + c * pb + (16 * i + (in_row ? sl : 0)) * 8 + 2 * j);
+    return a;
+}
+
+// LDS bytes of the staged activation of nc columns of K values in the
+// K-split layouts (q8 and auxiliary pairs of whole groups).
+__host__ __device__ constexpr int ksn_stage_bytes(int K, int nc) {
+    return nc * ((K + 4095) / 4096 * 4096) * 5 / 4;
+}
+
 // NC: columns (2..4); SBW: super-blocks per wave and group (2 or 4 for two
 // columns, 4 for three or four); WAVES: whole teams of 16/SBW waves; S: row
 // tiles in flight per wave; G: groups per row; STAGED: the activation
@@ -164,8 +189,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_nc_kernel(Q4K_GE
     // 3. quantise the slices and hand each lane its sub-blocks (STAGED: the
     //    workgroup's staging, then each lane reads what the tile kernel's
     //    lane 4*kb0 + j reads)
+    const int sl = q4k_slot<kLayout>(kb0);  // its slot in the staged layout
+    const int pb = (p.K / 32 + 127) & ~127;
     Lane ln;
-    ln.lane = 4 * q4k_slot<kLayout>(kb0) + j;
+    ln.lane = 4 * sl + j;
     ln.g = kb0;
     ln.j = j;
     ln.sel = make_scale_sel(j);
@@ -179,7 +206,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_nc_kernel(Q4K_GE
 #pragma unroll
         for (int i = 0; i < G; ++i)
 #pragma unroll
-            for (int c = 0; c < NC; ++c) act[i][c] = lane_act(p, ln, i, c, q8s, dks);
+            for (int c = 0; c < NC; ++c) act[i][c] = ksn_lane_act(i, c, sl, j, true, p.qcol, pb, q8s, dks);
     } else {
 #pragma unroll
         for (int i = 0; i < G; ++i)
@@ -357,8 +384,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_nc_long_kernel(Q
         p.x, p.ldx, p.K, NC, true, p.nblk32, xs, p.qcol, q8s, dks, SUMS ? p.sq : nullptr);
     __syncthreads();
 
+    const int sl = q4k_slot<kLayout>(kb0);  // its slot in the staged layout
+    const int pb = (p.K / 32 + 127) & ~127;
     Lane ln;
-    ln.lane = 4 * q4k_slot<kLayout>(kb0) + j;
+    ln.lane = 4 * sl + j;
     ln.g = kb0;
     ln.j = j;
     ln.sel = make_scale_sel(j);
@@ -376,7 +405,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_nc_long_kernel(Q
                     const RowScales sc = row_scales(w[k], ln);
 #pragma unroll
                     for (int c = 0; c < NC; ++c) {
-                        const LaneAct a = lane_act(p, ln, st[k].i, c, q8s, dks);
+                        const LaneAct a =
+                            ksn_lane_act(st[k].i, c, sl, j, 16 * st[k].i + kb0 < p.nb, p.qcol, pb, q8s, dks);
                         int sa, sb;
                         accumulate(w[k], sc, a, acc[c], sa, sb);
                         if constexpr (SUMS) {
