@@ -181,6 +181,11 @@ __device__ __forceinline__ int byte_sum16(u32x4 a) {
 //             of super-block kb = 16i + g at c*qcol + 4096i + 1024m +
 //             16(4g + 2h + j') + t -- lane 4g + 2h + j' reads, for each m, the 16
 //             values that share one Q6_K scale.
+//   Q6K K-split  the Q6K tile layout with the super-block positions
+//             permuted as in the Q4K K-split layouts; per column its d8 of
+//             whole groups, dq[c*3pb + 128i + 8*slot + s], then its -32 *
+//             sum(q8) values, at c*3pb + pb + 16*(16i + slot) + 4(2h + j') + m
+//             (int units from the start of the auxiliary area).
 //   Q6K dense the Q6K tile layout with qcol = K: the row's last, partial
 //             16-block group packs its four chunks 64 bytes per block apart
 //             (1024m becomes cs*m, cs = 64*(nb mod 16); group_chunk_stride),
@@ -212,11 +217,17 @@ constexpr int kLayoutMfma = 4;  // linear q8 columns; (d8, d8*sum) per [block][c
 constexpr int kLayoutMfmaQ6 = 5;  // linear q8 columns; d8 per [block][column] of 8 columns
 constexpr int kLayoutQ4KS2 = 6;   // Q4K, positions permuted for the two-column K-split tree
 constexpr int kLayoutQ4KS4 = 7;   // Q4K, positions permuted for the four-column K-split tree
+constexpr int kLayoutQ6KS2 = 8;   // Q6K, positions permuted for the two-column K-split tree
+constexpr int kLayoutQ6KS4 = 9;   // Q6K, positions permuted for the four-column K-split tree
 
-// Slot of super-block position g (0..15) of a group in the Q4K layouts.
+constexpr bool is_q6_split_layout(int layout) { return layout == kLayoutQ6KS2 || layout == kLayoutQ6KS4; }
+
+// Slot of super-block position g (0..15) of a group in the Q4K and Q6K layouts.
 template <int LAYOUT>
 __host__ __device__ constexpr int q4k_slot(int g) {
-    return LAYOUT == kLayoutQ4KS2 ? (g & 7) * 2 + (g >> 3) : (LAYOUT == kLayoutQ4KS4 ? (g & 3) * 4 + (g >> 2) : g);
+    return LAYOUT == kLayoutQ4KS2 || LAYOUT == kLayoutQ6KS2
+               ? (g & 7) * 2 + (g >> 3)
+               : (LAYOUT == kLayoutQ4KS4 || LAYOUT == kLayoutQ6KS4 ? (g & 3) * 4 + (g >> 2) : g);
 }
 
 constexpr bool is_q6_layout(int layout) { return layout == kLayoutQ6K || layout == kLayoutQ6KDense; }
@@ -238,8 +249,8 @@ __device__ __forceinline__ int q8_offset(int c, int qcol, int nb, int b, int e) 
                (q4k_slot<LAYOUT>(kb & 15) * 4 + (s >> 1)) * 16 + (e & 3) * 4;
     const int cs = LAYOUT == kLayoutQ6KDense ? group_chunk_stride(kb >> 4, nb) : 1024;
     // Q6K: s = 4h + m, values 16j' + 4(e & 3) + [0, 4) with j' = e >> 2
-    return c * qcol + (kb >> 4) * 4096 + (s & 3) * cs + ((kb & 15) * 4 + (s >> 2) * 2 + (e >> 2)) * 16 +
-           (e & 3) * 4;
+    return c * qcol + (kb >> 4) * 4096 + (s & 3) * cs +
+           (q4k_slot<LAYOUT>(kb & 15) * 4 + (s >> 2) * 2 + (e >> 2)) * 16 + (e & 3) * 4;
 }
 
 // Int index (from the start of the auxiliary area) of the Q6K offset
@@ -255,7 +266,12 @@ __device__ __forceinline__ int q6_sq_index(int total, int nblk, int c, int b, in
 template <int LAYOUT>
 __device__ __forceinline__ void store_aux(void *aux, int total, int nblk, int c, int b, int qb, int half,
                                           float d8, int qsum, int hsum) {
-    if (is_q6_layout(LAYOUT)) {
+    if (is_q6_split_layout(LAYOUT)) {
+        const int kb = b >> 3, s = b & 7, pb = (nblk + 127) & ~127;
+        const int at = (kb >> 4) * 16 + q4k_slot<LAYOUT>(kb & 15);  // 16i + slot
+        if (half == 0) reinterpret_cast<float *>(aux)[c * 3 * pb + at * 8 + s] = d8;
+        reinterpret_cast<int *>(aux)[c * 3 * pb + pb + at * 16 + ((s >> 2) * 2 + half) * 4 + (s & 3)] = -32 * hsum;
+    } else if (is_q6_layout(LAYOUT)) {
         if (half == 0) reinterpret_cast<float *>(aux)[qb] = d8;
         reinterpret_cast<int *>(aux)[q6_sq_index(total, nblk, c, b, half)] = -32 * hsum;
     } else if (LAYOUT == kLayoutMfma) {

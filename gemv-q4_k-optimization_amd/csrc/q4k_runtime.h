@@ -86,6 +86,7 @@ const void *q4k_mfma_ga_sums_kernel(int nc, int waves, int nif);
 const void *q6k_mfma_sums_kernel(int nc, int waves);
 const void *q6k_ksplit_sums_kernel(int sbw, int waves, int slots, int G);
 const void *q6k_ksplit_long_sums_kernel(int sbw, int waves, int slots, int G);
+const void *q6k_ksplit_nc_sums_kernel(int nc, int p, int sbw, int waves, int slots);
 const void *q6k_mfma_ga_sums_kernel(int nc, int waves);
 const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense);
 

@@ -12,6 +12,7 @@
 #include "q4k_tile.h"
 #include "q6k_kernels.h"
 #include "q6k_ksplit.h"
+#include "q6k_ksplit_nc.h"
 #include "q6k_mfma.h"
 
 namespace q4k {
@@ -97,7 +98,53 @@ struct Q6Geometry {
     int ks_tr = 0;   // K-split kernel: rows per wave step (16 / ksplit)
     int ks_long = 0; // K-split kernel for rows of any length (activation slices in LDS)
     int mfma_ga = 0; // matrix-core kernel: A operand from the Q8_1 buffer (pre-quantised route)
+    int ks_nc_p = 0; // several-column K-split kernel: columns of its reduction tree (2 or 4; 0: not it)
 };
+
+// Columns per launch of the tile kernel for N columns of K values (halved
+// until they fit the LDS, or all of five or more in the dense layout).
+static int q6_tile_chunk(int64_t K, int64_t N, int max_lds, bool &dense) {
+    int nc = (int)N;
+    dense = false;
+    while (nc > 1 && q6_tile_lds_bytes((int)K, nc, 16, false) > max_lds) {
+        if (nc >= kDenseMinCols && q6_tile_lds_bytes((int)K, nc, 16, true) <= max_lds) {
+            dense = true;
+            break;
+        }
+        nc = (nc + 1) / 2;
+    }
+    return nc;
+}
+
+// The several-column K-split kernel's launch shape (N = 2..4 aligned F32
+// columns; P: the tile kernel's tree column count): rows_per_step 8 (two
+// super-blocks per wave; P = 2) or 4, waves per workgroup (whole teams),
+// workgroups (default one per CU), steps in flight (1, 2).
+static Q6Geometry pick_geometry_q6_ksplit_nc(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step,
+                                             int waves, int wgs, int slots, int N, int P) {
+    Q6Geometry g;
+    const int cus = di.cus > 0 ? di.cus : 1;
+    g.ks_nc_p = P;
+    g.ksplit = P == 2 && rows_per_step == 8 ? 2 : 4;
+    g.ks_tr = 16 / g.ksplit;
+    g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
+    if (g.waves < g.ks_tr) g.waves = g.ks_tr;
+    g.slots = slots == 1 || slots == 2 ? slots : 1;
+    if (!q6_ksplit_nc_exists(N, P, g.ksplit, g.waves, g.slots)) {
+        g.waves = 16;
+        g.slots = 1;
+    }
+    int64_t grid = wgs > 0 ? wgs : cus;
+    if (grid > M) grid = M;
+    g.grid = grid < 1 ? 1 : (int)grid;
+    g.rows_base = (int)(M / g.grid);
+    g.rows_extra = (int)(M % g.grid);
+    g.lds = q6_ksn_stage_bytes((int)K, N) +
+            ksplit_nc_part_bytes(g.rows_base + (g.rows_extra ? 1 : 0), N, g.ksplit);
+    g.lds_launch = g.lds;
+    g.nc_chunk = N;
+    return g;
+}
 
 // The K-split kernel's launch shape: rows_per_step TR = 16 / SBW (4, 8, 16;
 // rows of other lengths than 4096 and 8192 values: the long-row variant, 8
@@ -264,6 +311,22 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     // the long-row variant); the tile kernel, whose outputs are the same
     // bits, takes the rest
     const bool ks_ok = N == 1 && mats == 1 && fused == kFusedNone && f32_vec && K <= 8 * 4096;
+    // two to four columns: the several-column K-split kernel, whose outputs
+    // are the bits of the tile kernel's launches (all columns in one, or
+    // four two by two; not the dense layout).  Through the override only:
+    // measured on MI355X no faster than the tile kernel (4096 x 14336 N=2
+    // 15.58 against 15.26 us, N=4 20.25 / 19.93, 1024 x 4096 N=4 5.77 /
+    // 5.61, 4096 x 4096 N=2 6.58 / 6.56) -- a Q6_K step reads six 16-byte
+    // LDS chunks per column and unpacks more per weight byte, so spreading
+    // rows over more waves buys nothing.
+    bool tdense = false;
+    const int tchunk = q6_tile_chunk(K, N, max_lds, tdense);
+    const bool ksn_ok = N >= 2 && N <= 4 && mats == 1 && fused == kFusedNone && f32_vec && K <= 8 * 4096 &&
+                        !tdense && (tchunk == N || (tchunk == 2 && N == 4));
+    const int ksn_p = tchunk <= 2 ? 2 : 4;
+    if (ksn_ok && okern == 5)
+        return pick_geometry_q6_ksplit_nc(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(), g_ovr_wgs.load(),
+                                          g_ovr_slots.load(), (int)N, ksn_p);
     if (ks_ok && okern == 5)
         return pick_geometry_q6_ksplit(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(), g_ovr_wgs.load(),
                                        g_ovr_slots.load());
@@ -495,13 +558,16 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
             p.glu_op = ep->glu_op;
         }
-        const void *fn = geo.ks_long  ? q6_ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
+        const void *fn = geo.ks_nc_p  ? q6_ksplit_nc_kernel<false>(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
+                         : geo.ks_long  ? q6_ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.ksplit ? q6_ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.mfma_ga ? q6_mfma_ga_kernel_for(nc, geo.waves)
                          : geo.mfma ? q6_mfma_kernel_for(nc, geo.waves)
                          : bl       ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
                                     : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
-        if (geo.ksplit && (nc != 1 || fused || bl || !p.x || !p.vec_ok)) return Q4K_EINVAL;
+        if (geo.ksplit && (nc != (geo.ks_nc_p ? geo.nc_chunk : 1) || fused || bl || !p.x || !p.vec_ok))
+            return Q4K_EINVAL;
+        if (geo.ks_nc_p) p.ring_off = q6_ksn_stage_bytes(p.K, nc);
         if (geo.mfma) {
             if (fused || bl) return Q4K_EINVAL;
             if (geo.mfma_ga && (p.x || !p.y)) return Q4K_EINVAL;  // GA reads the Q8_1 buffer
@@ -510,7 +576,8 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         }
         if (so) {  // parity variant: this chunk's columns of the group sums
             if (fused || bl) return Q4K_EINVAL;
-            fn = geo.ks_long  ? q6k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
+            fn = geo.ks_nc_p  ? q6k_ksplit_nc_sums_kernel(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
+                 : geo.ks_long  ? q6k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                  : geo.ksplit ? q6k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                  : geo.mfma_ga ? q6k_mfma_ga_sums_kernel(nc, geo.waves)
                  : geo.mfma ? q6k_mfma_sums_kernel(nc, geo.waves)
@@ -574,7 +641,8 @@ static int mul_mat_vec_q_q6k(const void *src0, int64_t ne00, int64_t ne01, int64
     // reached through that copy, with or without a workspace (so both give
     // the pre-quantised entry point's bits)
     const bool ga_route = pick_geometry_q6(*di, ne00, ne01, ne11, 1, kFusedNone, false, true).mfma_ga != 0;
-    if (geo.nc_chunk >= ne11 && !ga_route && !(ws_fits && prefer_prequantised(ne00, ne11)))
+    // (the K-split kernels quantise inside the launch: their one route)
+    if (geo.nc_chunk >= ne11 && !ga_route && (geo.ksplit || !(ws_fits && prefer_prequantised(ne00, ne11))))
         return run_gemv_q6(src0, ne00, ne01, nb01, src1, ldx, nullptr, 0, ne11, dst, ldd, s, nullptr, nullptr, so);
     // activation too large for one workgroup's LDS at this column count,
     // (with a workspace) too many values for every workgroup to quantise, or

@@ -10,6 +10,7 @@
 #include "q4k_runtime.h"
 #include "q6k_kernels.h"
 #include "q6k_ksplit.h"
+#include "q6k_ksplit_nc.h"
 #include "q6k_mfma.h"
 
 namespace q4k {
@@ -89,6 +90,10 @@ const void *q6k_mfma_ga_sums_kernel(int nc, int waves) {
 
 const void *q6k_ksplit_sums_kernel(int sbw, int waves, int slots, int G) {
     return q6_ksplit_kernel<true>(sbw, waves, slots, G);
+}
+
+const void *q6k_ksplit_nc_sums_kernel(int nc, int p, int sbw, int waves, int slots) {
+    return q6_ksplit_nc_kernel<true>(nc, p, sbw, waves, slots);
 }
 
 const void *q6k_ksplit_long_sums_kernel(int sbw, int waves, int slots, int G) {

@@ -256,3 +256,102 @@ def test_ksplit_nc_long_sums_exact(Q, O, gpu, M, K, N):
         got = sums[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
         assert np.array_equal(got, ref["sqq"]), f"{where}: S_qq differ"
         assert np.array_equal(sq.cpu().numpy(), ref["sq"]), f"{where}: S_q differ"
+
+
+# ---------------------------------------------------------------- Q6_K ----
+
+_w6cache = {}
+
+
+def inputs_q6(Q, M, K, N, seed):
+    key = (M, K, seed)
+    if key not in _w6cache:
+        _w6cache.clear()
+        _w6cache[key] = Q.quantize_rows_q6_K(_common.weights(M, K, seed), nthreads=16)
+    return _w6cache[key], _common.activations(N, K, seed)
+
+
+def tile_tree_q6(Q, K, M, N):
+    t6 = Q.GGML_TYPE_Q6_K
+    try:
+        Q.set_geometry_override(kernel=1)
+        chunk = Q.geometry(K, M, N, t6)["cols_per_launch"]
+    finally:
+        Q.set_geometry_override()
+    return chunk, (2 if chunk <= 2 else 4)
+
+
+def run_forced_q6(Q, wd, K, xd, tr, waves, slots, wgs=0):
+    t6 = Q.GGML_TYPE_Q6_K
+    N = xd.shape[0]
+    try:
+        Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, workgroups=wgs, kernel=5)
+        Q.set_pipeline_override(slots=slots)
+        g = Q.geometry(K, wd.shape[0], N, t6)
+        assert g["kernel"] == 5 and g["rows_per_tile"] == tr and g["waves_per_wg"] == waves, g
+        assert g["cols_per_launch"] == N, g
+        return Q.mul_mat_vec_q(wd, K, xd, wtype=t6).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+        Q.set_pipeline_override()
+
+
+@pytest.mark.parametrize("M,K", [(4096, 14336), (1000, 14336), (333, 28672), (777, 11008), (500, 5120),
+                                 (64, 2304), (37, 256), (1024, 4096), (300, 8192)])
+@pytest.mark.parametrize("N", [2, 3, 4])
+def test_q6k_ksplit_nc_bits_equal_tile_kernel(Q, O, gpu, M, K, N):
+    """Q6_K, two to four columns (the staged form for rows of any length up
+    to 8 groups, partial last groups included), every instantiated launch
+    shape at one workgroup per CU, 7 and 300 workgroups, against the Q6_K
+    tile kernel bit for bit; the tile kernel against the oracle."""
+    t6 = Q.GGML_TYPE_Q6_K
+    chunk, p = tile_tree_q6(Q, K, M, N)
+    if N % chunk:
+        pytest.skip(f"the tile kernel launches {chunk} of {N} columns at a time: no K-split form")
+    wq, x = inputs_q6(Q, M, K, N, seed=81 + N)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    try:
+        Q.set_geometry_override(kernel=1)
+        y_tile = Q.mul_mat_vec_q(wd, K, xd, wtype=t6).cpu().numpy()
+    finally:
+        Q.set_geometry_override()
+    rows = np.arange(M) if M <= 1024 else np.unique(
+        np.concatenate([[0, 1, M - 2, M - 1], np.random.default_rng(M).choice(M, 300, replace=False)]))
+    ref = O.gemv_q6K_q8_1(wq[rows], K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, y_tile[:, rows], ref, f"Q6_K tile {M}x{K} N={N}")
+    for tr, waves, slots in long_shapes(p):
+        for wgs in (0, 7, 300):
+            y = run_forced_q6(Q, wd, K, xd, tr, waves, slots, wgs)
+            if not np.array_equal(y, y_tile):
+                bad = np.argwhere(y != y_tile)
+                raise AssertionError(f"Q6_K {M}x{K} N={N} rows/step {tr} waves {waves} slots {slots} wgs {wgs}: "
+                                     f"{len(bad)} outputs differ from the tile kernel, e.g. (col, row) "
+                                     f"{bad[:5].tolist()}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1000, 14336, 2), (333, 14336, 3), (300, 28672, 4), (129, 5120, 4),
+                                   (500, 4096, 4)])
+def test_q6k_ksplit_nc_sums_exact(Q, O, gpu, M, K, N):
+    """Q6_K: the parity variant's int32 group sums of every lane and column
+    bit for bit against the oracle, outputs equal to the product launch's."""
+    import torch
+    t6 = Q.GGML_TYPE_Q6_K
+    chunk, p = tile_tree_q6(Q, K, M, N)
+    wq, x = inputs_q6(Q, M, K, N, seed=91 + N)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    rows = np.unique(np.concatenate([[0, M // 2, M - 1], np.random.default_rng(M).choice(M, 60, replace=False)]))
+    ref = O.gemv_q6K_q8_1(wq[rows], K, O.quantize_q8_1(x))
+    for tr, waves, slots in long_shapes(p):
+        try:
+            Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
+            Q.set_pipeline_override(slots=slots)
+            assert Q.geometry(K, M, N, t6)["kernel"] == 5
+            y, s16, _ = Q.mul_mat_vec_q_sums(wd, K, xd, wtype=t6)
+            y_prod = Q.mul_mat_vec_q(wd, K, xd, wtype=t6)
+        finally:
+            Q.set_geometry_override()
+            Q.set_pipeline_override()
+        where = f"Q6_K {M}x{K} N={N} rows/step {tr} waves {waves} slots {slots}"
+        assert torch.equal(y, y_prod), where
+        got = s16[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        assert np.array_equal(got, ref["s16"]), f"{where}: group sums differ"
