@@ -334,7 +334,14 @@ int q4k_gemv_geometry_q8_1(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out
  * and 8192: 8 or 16), waves_per_wg 4, 8 or 16 (at least the rows per step;
  * other lengths: 8 or 16), and the pipeline override's slots its tiles in
  * flight (1..4; 3 and 4 for rows of 4096 values and 1, 4 or 8 rows per
- * step; other lengths 1 or 2), 6 matrix-core kernel with its A operand read
+ * step; other lengths 1 or 2); for two to four aligned F32 columns the
+ * several-column K-split kernel (Q4_K and Q6_K): rows_per_tile 8 (two
+ * columns, or four where the tile kernel would launch them two by two) or
+ * 4, waves_per_wg 4, 8 or 16 (at least the rows per step), slots 1 or 2,
+ * and with three or four columns of 4096 or 8192 values the pipeline
+ * override's prologue 2 quantises the activation per wave in registers, any
+ * other value once per workgroup into LDS (other lengths: always the
+ * latter), 6 matrix-core kernel with its A operand read
  * from the Q8_1 buffer, for products of up to 8 columns on the
  * pre-quantised route; Q6_K: 4 the matrix-core kernel, 5 the K-split
  * kernel as for Q4_K (4, 8 or 16 rows per step), any other value the tile
@@ -353,7 +360,10 @@ int q4k_set_geometry_override(int32_t rows_per_tile, int32_t waves_per_wg, int32
  * two groups before it, 1 = all
  * after, 2 = all before, 3 = one before; -1 = automatic; the long-row
  * K-split kernels: 2 = every group's slice quantised before the first
- * step, 0, 1, 3 = each group's just before the first step that reads it).  Values a kernel
+ * step, 0, 1, 3 = each group's just before the first step that reads it;
+ * the several-column K-split kernel at three or four columns of 4096 or
+ * 8192 values: 2 = quantised per wave in registers, else once per
+ * workgroup).  Values a kernel
  * has no variant for fall back to the automatic choice.  Not part of the
  * reference interface: a benchmarking knob. */
 int q4k_set_pipeline_override(int32_t slots, int32_t prologue);
