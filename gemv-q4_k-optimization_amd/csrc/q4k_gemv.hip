@@ -496,10 +496,12 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
 //    waves (1024 x 8192 5.40 / 5.91), else 8 rows and 8 waves, one tile in
 //    flight (4096 x 8192 6.78 / 7.25, 14336 x 8192 14.55 / 15.61, 28672 x
 //    8192 26.00 / 27.49).
-//  - three columns, up to 16 rows per CU: 4 rows per step, 8 waves,
-//    staged, one tile in flight up to 4 rows per CU (1024 x 4096 4.43 /
-//    4.48, 1024 x 8192 7.11 / 8.09), else two (4096 x 4096 5.50 / 5.68;
-//    4096 x 8192 stays on the tile kernel: 9.57 against 8.37).
+//  - three columns: 4 rows per step, 8 waves, staged; 8192 values up to 4
+//    rows per CU, one tile in flight (1024 x 8192 7.11 / 8.09; 4096 x 8192
+//    stays on the tile kernel: 9.57 against 8.37); 4096 values over 4 and
+//    up to 16 rows per CU, two (4096 x 4096 5.52 / 5.69 over three
+//    alternations; 1024 x 4096 stays on the tile kernel: 4.62 against
+//    4.51).
 //  - three or four columns, K = 8192, 96 rows per CU or more: 4 rows, 4
 //    waves, two tiles in flight, in registers (28672 x 8192 N=3 28.63 /
 //    29.19, N=4 30.28 / 32.03).
@@ -550,7 +552,7 @@ static bool ksplit_nc_auto(int64_t K, int64_t M, int64_t N, int cus, int &tr, in
         return true;
     }
     tr = 4;
-    if (N == 3 && (rho <= 4 || (rho <= 16 && K == 4096))) {
+    if (N == 3 && (K == 8192 ? rho <= 4 : rho > 4 && rho <= 16)) {
         waves = 8;
         staged = 1;
         slots = rho <= 4 ? 1 : 2;

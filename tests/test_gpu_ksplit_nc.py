@@ -179,14 +179,14 @@ def test_ksplit_nc_column_strides(Q, O, gpu):
 
 @pytest.mark.parametrize("M,K,N,kernel", [(14336, 4096, 2, 5), (4096, 4096, 2, 5), (1024, 4096, 2, 5),
                                           (128256, 4096, 2, 5), (4096, 8192, 2, 5), (4096, 4096, 3, 5),
-                                          (1024, 4096, 3, 5), (14336, 4096, 3, 1), (14336, 4096, 4, 1),
+                                          (1024, 4096, 3, 1), (1024, 8192, 3, 5), (14336, 4096, 3, 1), (14336, 4096, 4, 1),
                                           (28672, 8192, 3, 5), (28672, 8192, 4, 5), (14336, 8192, 4, 1),
                                           (4096, 14336, 2, 5), (4096, 14336, 3, 5), (4096, 14336, 4, 5),
                                           (8192, 28672, 2, 5), (8192, 28672, 4, 1), (4096, 11008, 4, 5)])
 def test_ksplit_nc_automatic_choice(Q, gpu, M, K, N, kernel):
     """The automatic geometry: the K-split kernel where it measured faster
-    than the tile kernel (two columns, three columns of 4096 or 8192 values
-    up to 16 rows per CU, three or four columns of 8192 values at 96 rows
+    than the tile kernel (two columns, three columns of 8192 values up to 4
+    rows per CU or of 4096 values at 5 to 16, three or four columns of 8192 values at 96 rows
     per CU or more, three or four columns of other lengths up to 16384
     values), the tile kernel elsewhere; the pre-quantised route stays on
     the tile kernel (same bits)."""
