@@ -145,8 +145,10 @@ int q4k_quantize_row_q8_1(const float *x, void *vy, int64_t ne00, int64_t s01, i
  * bytes, 4-B aligned) or, when NULL, a stream-ordered temporary.  With a
  * workspace of that size the buffer is also used, in a quantisation launch
  * of its own as the reference does, when ne00 * ne11 > 40960 (several long
- * columns, which every workgroup would otherwise quantise in full).  Both
- * routes give the same bits. */
+ * columns, which every workgroup would otherwise quantise in full) and the
+ * launch is not a K-split kernel (those quantise inside the launch; three or
+ * four columns of 8193..16384 values run one).  Both routes give the same
+ * bits. */
 int q4k_mul_mat_vec_q(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01,
                       const float *src1, int64_t ne11, int64_t nb11, float *dst, int64_t nb1,
                       void *workspace, size_t workspace_bytes, void *stream);
