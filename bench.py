@@ -448,15 +448,16 @@ READ_SHAPES = [(2016, 4, 4), (2016, 4, 2), (1008, 4, 4), (4032, 4, 2), (1024, 8,
 
 
 def read_ceiling(args):
-    """A plain read of a weight's bytes (--shape M K; default the headline
-    14336 x 4096 Q4_K: 33,030,144 B) in several launch shapes, timed like the
-    headline, against that product's GEMV (one column) in the same process.
-    Shapes whose waves would read more than 1.5 times the bytes (the probe
-    reads zeros past the end) are skipped."""
+    """A plain read of a weight's bytes (--shape M K, --wtype; default the
+    headline 14336 x 4096 Q4_K: 33,030,144 B) in several launch shapes, timed
+    like the headline, against that product's GEMV (one column) in the same
+    process.  Shapes whose waves would read more than 1.5 times the bytes
+    (the probe reads zeros past the end) are skipped."""
     import torch
     Q = _pkg()
     M, K = args.shape[0], args.shape[1]
-    nbytes = M * (K // 256) * BLOCK_BYTES["q4_K"]
+    wt = args.wtype
+    nbytes = M * (K // 256) * BLOCK_BYTES[wt]
     for wgs, waves, infl in READ_SHAPES:
         per_wave = math.ceil(nbytes / (wgs * waves) / 1024) * 1024
         if per_wave * wgs * waves > 1.5 * nbytes:
@@ -470,11 +471,13 @@ def read_ceiling(args):
                           "us_min": round(t["min_s"] * 1e6, 3), "method": t["method"],
                           "GBps": round(nbytes / t["s"] / 1e9, 1),
                           "hbm_frac": round(nbytes / t["s"] / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
-    wq, x = make_inputs(Q, M, K, 1)
-    r = OpRunner(Q, wq, x)
+    wq, x = make_inputs(Q, M, K, 1, wtype=wt)
+    r = OpRunner(Q, wq, x, wtype=wt)
     t = time_gpu(r, args.steps, args.warmup, args.trials)
-    nb = algorithmic_bytes(M, K, 1)
-    print(json.dumps({"kernel": "q4k_mul_mat_vec_q", "bytes": nb, "geometry": Q.geometry(K, M, 1),
+    nb = algorithmic_bytes(M, K, 1, wt)
+    gt = Q.GGML_TYPE_Q4_K if wt == "q4_K" else Q.GGML_TYPE_Q6_K
+    print(json.dumps({"kernel": f"{wt.replace('_', '').lower()}_mul_mat_vec_q", "bytes": nb,
+                      "geometry": Q.geometry(K, M, 1, gt),
                       "us_per_call": round(t["s"] * 1e6, 3), "us_min": round(t["min_s"] * 1e6, 3),
                       "method": t["method"], "GBps": round(nb / t["s"] / 1e9, 1),
                       "hbm_frac": round(nb / t["s"] / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
