@@ -330,7 +330,7 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
 // (whole teams of TR waves), workgroups (default one per CU) and row tiles
 // in flight per wave (1 or 2).
 static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
-                                     int wgs, int slots, int N = 1, int staged = 0, int P = 0) {
+                                     int wgs, int slots, int N = 1, int staged = 0, int P = 0, int fused = 0) {
     Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
     if (N >= 2) {  // two to four columns
@@ -390,7 +390,20 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
     const int rows = g.rows_base + (g.rows_extra ? 1 : 0);
-    g.lds = lng ? ksplit_long_lds_bytes(rows, g.ksplit, g.waves, G) : ksplit_lds_bytes(rows, g.ksplit);
+    // fused epilogue: the variants that exist (else ksplit = 0: the caller
+    // takes the tile kernel); with a gate two partials per (row, slice)
+    if (fused) {
+        if (g.slots > 2) g.slots = 2;
+        const bool ok = lng ? ksplit_long_epi_exists(g.ksplit, g.waves, g.slots, gmax)
+                            : ksplit_epi_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096));
+        if (!ok) g.slots = 1;
+        if (!(lng ? ksplit_long_epi_exists(g.ksplit, g.waves, g.slots, gmax)
+                  : ksplit_epi_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096))))
+            g.ksplit = 0;
+    }
+    const int nw = fused == kFusedGate ? 2 : 1;
+    g.lds = lng ? ksplit_long_lds_bytes(rows, g.ksplit ? g.ksplit : 1, g.waves, G, nw)
+                : ksplit_lds_bytes(rows, g.ksplit ? g.ksplit : 1, nw);
     g.lds_launch = g.lds;
     g.nc_chunk = 1;
     return g;
@@ -474,6 +487,34 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
         waves = 8;
         slots = 2;
     }
+    return true;
+}
+
+// The K-split kernel's automatic launch shape for one aligned F32 column
+// with a gate weight and the GLU (two weights' rows per step); false where
+// the tile kernel is kept.  rho = rows per CU.  Measured on MI355X (us per
+// fused op, one process, K-split against the fused tile kernel): rows of
+// 4096 values up to 16 rows per CU 8 rows per step and 8 waves, one tile in
+// flight (4096 x 4096 5.68 against 6.10), beyond 4 rows, 4 waves, two tiles
+// (14336 x 4096 13.45 / 13.71, 11008 x 4096 11.27 / 11.90 -- 4 rows and 8
+// waves 10.94 there, 13.98 at 14336 rows); 8192 values 4 rows, 4 waves, one
+// tile (28672 x 8192 45.05 / 48.40); other lengths 8 rows, 8 waves, one step
+// (4096 x 14336 13.96 / 17.40).  Rows of 4096 values or more, up to 160
+// rows per CU: the range measured.
+static bool ksplit_glu_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
+    const int64_t rho = (M + cus - 1) / cus;
+    if (rho > 160 || K < 4096) return false;  // (shorter rows: not measured)
+    slots = 1;
+    if (K == 4096) {
+        if (rho <= 16) {
+            tr = waves = 8;
+        } else {
+            tr = waves = 4;
+            slots = 2;
+        }
+        return true;
+    }
+    tr = waves = K == 8192 ? 4 : 8;
     return true;
 }
 
@@ -594,22 +635,27 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // groups (4096 or 8192 values: activation in registers; other lengths:
     // the long-row variant); the tile kernel, whose outputs are the same
     // bits, takes the rest
-    const bool ks_ok = N == 1 && !fused && mats == 1 && f32_vec && K <= 8 * 4096;
+    const bool ks_ok = N == 1 && mats == 1 && f32_vec && K <= 8 * 4096;  // (fused epilogues included)
     // two to four columns: the K-split kernel for rows of 1 or 2 groups
     // (the tile kernel's launches, whose bits these are: all columns in one,
     // or four columns two by two)
     const bool ksn_ok = N >= 2 && N <= 4 && !fused && mats == 1 && f32_vec && K <= 8 * 4096 &&
                         (nc == N || (nc == 2 && N == 4));
     const int ksn_p = nc <= 2 ? 2 : 4;
-    if ((ks_ok || ksn_ok) && okern == 5)
+    if (ksn_ok && okern == 5)
         return pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load(), (int)N, 1, ksn_p);
+    if (ks_ok && okern == 5) {
+        const Geometry gk = pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load(), 1, 0, 0, fused);
+        if (gk.ksplit) return gk;
+    }
     // (automatic: where the partials fit the LDS)
     if (ks_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
         int tr = 0, kw = 0, ks = 0;
-        if (ksplit_auto(K, M, di.cus > 0 ? di.cus : 1, tr, kw, ks)) {
+        if (fused == kFusedGate ? ksplit_glu_auto(K, M, cus, tr, kw, ks) : ksplit_auto(K, M, cus, tr, kw, ks)) {
             const int os = g_ovr_slots.load();
-            const Geometry gk = pick_geometry_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks);
-            if (gk.lds <= max_lds) return gk;
+            const Geometry gk =
+                pick_geometry_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks, 1, 0, 0, fused);
+            if (gk.ksplit && gk.lds <= max_lds) return gk;
         }
     }
     if (ksn_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
@@ -923,7 +969,7 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
     const void *fn = nullptr;
     const bool batch = bl != nullptr;
     if (batch && geo.bpl) return Q4K_EINVAL;
-    if (p.gate || p.bias) {
+    if ((p.gate || p.bias) && !geo.ksplit) {
         if (nc != 1 || geo.bpl || geo.R != (p.gate ? 2 : 1)) return Q4K_EINVAL;
         if (p.gate)
             fn = batch ? gemv_kernel_epi<kEpiGlu, true>(geo.waves, geo.prologue, geo.slots)
@@ -952,9 +998,14 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
                             : ksplit_nc_kernel<false>(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0);
             p.ring_off = geo.ks_staged ? ksn_stage_bytes(p.K, nc) : 0;
         } else if (geo.ks_long) {
-            fn = p.sums ? q4k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
-                        : ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);
-            p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit);
+            if (p.gate)
+                fn = ksplit_long_kernel_epi<kEpiGlu>(geo.ksplit, geo.waves, geo.slots, p.G);
+            else if (p.bias)
+                fn = ksplit_long_kernel_epi<kEpiBias>(geo.ksplit, geo.waves, geo.slots, p.G);
+            else
+                fn = p.sums ? q4k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
+                            : ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);
+            p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit, p.gate ? 2 : 1);
             // groups quantised before the first step: all of them for one
             // super-block per wave and group (4096 x 14336 8.27 against 8.39
             // us, 4096 x 11008 6.97 / 7.02), else one, the others just before
@@ -963,6 +1014,10 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
             // one
             const int opro = g_ovr_prologue.load();
             p.rpw = (opro == 2 || (opro < 0 && geo.ksplit == 1)) ? p.G : 1;
+        } else if (p.gate) {
+            fn = ksplit_kernel_epi<kEpiGlu>(geo.ksplit, geo.waves, geo.slots, p.G);
+        } else if (p.bias) {
+            fn = ksplit_kernel_epi<kEpiBias>(geo.ksplit, geo.waves, geo.slots, p.G);
         } else {
             fn = p.sums ? q4k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                         : ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G);
@@ -1041,7 +1096,7 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
     const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0;
     Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused, mats, f32_vec, !x && y);
-    if (bl || fused) {  // the batched and fused variants: 1 or 2 slots, prologue 0 or 1
+    if ((bl || fused) && !geo.ksplit) {  // the batched and fused tile variants: 1 or 2 slots, prologue 0 or 1
         if (fused != kFusedGate) geo.R = 1;
         if (geo.slots > 2) geo.slots = 2;
         if (geo.prologue > 1) geo.prologue = 0;
@@ -1526,6 +1581,18 @@ int q4k_set_pipeline_override(int32_t slots, int32_t prologue) {
     return Q4K_OK;
 }
 
+static void fill_geometry_out(const Geometry &g, int64_t ne11, bool q81, int32_t out[8]) {
+    out[0] = g.R;
+    out[1] = g.waves;
+    out[2] = g.grid;
+    out[3] = g.lds_launch;
+    out[4] = g.nc_chunk;
+    out[5] = g.nc_chunk >= ne11 ? 1 : 0;
+    out[6] = g.ksplit ? 5 : (g.mfma_ga ? 6 : (g.mfma ? 4 : (g.bpl == 2 ? 3 : (g.bpl ? 2 : 1))));
+    out[7] = g.bpl ? g.rpw : g.R;
+    if (q81) out[5] = 0;
+}
+
 static int gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, bool q81, int32_t out[8]) {
     if (!out || ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0 || ne11 < 1 || ne11 > Q4K_MAX_BATCH)
         return Q4K_EINVAL;
@@ -1540,15 +1607,7 @@ static int gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, bool q81, int
             q81 = true;
         }
     }
-    out[0] = g.R;
-    out[1] = g.waves;
-    out[2] = g.grid;
-    out[3] = g.lds_launch;
-    out[4] = g.nc_chunk;
-    out[5] = g.nc_chunk >= ne11 ? 1 : 0;
-    out[6] = g.ksplit ? 5 : (g.mfma_ga ? 6 : (g.mfma ? 4 : (g.bpl == 2 ? 3 : (g.bpl ? 2 : 1))));
-    out[7] = g.bpl ? g.rpw : g.R;
-    if (q81) out[5] = 0;
+    fill_geometry_out(g, ne11, q81, out);
     return Q4K_OK;
 }
 
@@ -1558,6 +1617,20 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) 
 
 int q4k_gemv_geometry_q8_1(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) {
     return gemv_geometry(ne00, ne01, ne11, true, out);
+}
+
+int q4k_gemv_geometry_fused(int64_t ne00, int64_t ne01, int32_t with_gate, int32_t out[8]) {
+    if (!out || ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0) return Q4K_EINVAL;
+    DeviceInfo *di = nullptr;
+    int st = device_info(&di);
+    if (st != Q4K_OK) return st;
+    Geometry g = pick_geometry(*di, ne00, ne01, 1, with_gate ? kFusedGate : kFusedBias, 1, true, false);
+    if (!g.ksplit) {  // the tile variants' adjustments (run_gemv)
+        if (!with_gate) g.R = 1;
+        if (g.slots > 2) g.slots = 2;
+    }
+    fill_geometry_out(g, 1, false, out);
+    return Q4K_OK;
 }
 
 }  // extern "C"

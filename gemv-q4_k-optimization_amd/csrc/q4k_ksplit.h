@@ -173,19 +173,41 @@ __device__ __forceinline__ bool ks_writer(int lane) {
     return (lane & (4 * SBW - 1)) == 4 * SBW - 1;
 }
 
+// The fused epilogues of the one-column K-split kernels (EPI: kEpiBias,
+// kEpiGlu), applied where a row's slice sums meet: the tile kernel's
+// ring_flush arithmetic on the same products.  q[0]: the product with the
+// weight, q[1] (GLU): the product with the gate weight.
+template <int EPI>
+__device__ __forceinline__ float ks_epilogue(const GemvParams &p, int row, const float (&q)[EPI == kEpiGlu ? 2 : 1]) {
+    if constexpr (EPI == kEpiGlu) {
+        const float up = p.bias ? q[0] + p.bias[row] : q[0];
+        const float g = p.gate_bias ? q[1] + p.gate_bias[row] : q[1];
+        return glu_apply(p.glu_op, up, g);
+    } else if constexpr (EPI == kEpiBias) {
+        return q[0] + p.bias[row];
+    } else {
+        return q[0];
+    }
+}
+
 // SBW: super-blocks per wave and group (1, 2, 4, 16), WAVES: waves per
 // workgroup (whole teams of 16/SBW), S: row tiles in flight per wave, G:
 // groups per row (K = 4096 G).  SUMS: the parity variant, which also stores
-// every lane's int32 sub-block sums and the activation's block sums.
+// every lane's int32 sub-block sums and the activation's block sums.  EPI:
+// the fused epilogue (kEpiBias: dst = product + bias; kEpiGlu: each step
+// also loads the same rows of the gate weight p.gate, and dst = glu(product
+// + bias, gate product + gate bias); kernels/mmvq.cu:254-262, :309-336).
 // Rows: the workgroup's share (rows_base / rows_extra, as the tile kernel),
 // tiles of TR rows split contiguously over the teams.
-template <int SBW, int WAVES, int S, int G, bool SUMS = false>
+template <int SBW, int WAVES, int S, int G, bool SUMS = false, int EPI = kEpiNone>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;  // waves sharing a row
     constexpr int TR = 16 / SBW;  // rows per wave step
     constexpr int TEAMS = WAVES / KW;
     constexpr int V = 4 * SBW;    // activation values per lane and group
+    constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
     static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    static_assert(!SUMS || EPI == kEpiNone, "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
@@ -224,13 +246,16 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_
     }
 
     // 2. the first S tiles' weights: the workgroup's rows as one buffer, so
-    //    rows past its share read zeros without memory traffic
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    //    rows past its share read zeros without memory traffic (GLU: the
+    //    same rows of the gate weight, at the same offsets)
+    __amdgpu_buffer_rsrc_t rsw[NW];
+    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
     const uint32_t lrow = (uint32_t)r * (uint32_t)p.row_stride;
     const uint32_t lh = lrow + (uint32_t)((SBW * slice + s) * kBlockBytes);
     const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
     const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
-    auto load_tile = [&](int t, RowRegs(&w)[G]) {
+    auto load_tile = [&](int t, RowRegs(&w)[G][NW]) {
         const bool ok = t < ntiles;
         const uint32_t base = (uint32_t)(tb + t) * tile_bytes;
 #pragma unroll
@@ -238,13 +263,16 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_
             const uint32_t gi = (uint32_t)i * (16u * kBlockBytes);
             const uint32_t oh = ok ? base + gi + lh : kOOB;
             const uint32_t oq = ok ? base + gi + lq : kOOB;
-            w[i].h = load16(rs, oh);
-            w[i].q0 = load16(rs, oq);
-            w[i].q1 = load16(rs, oq + 16u);
+#pragma unroll
+            for (int u = 0; u < NW; ++u) {
+                w[i][u].h = load16(rsw[u], oh);
+                w[i][u].q0 = load16(rsw[u], oq);
+                w[i][u].q1 = load16(rsw[u], oq + 16u);
+            }
         }
     };
     int tk[S];
-    RowRegs w[S][G];
+    RowRegs w[S][G][NW];
 #pragma unroll
     for (int k = 0; k < S; ++k) {
         tk[k] = k;
@@ -269,12 +297,17 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_
         for (;;) {
 #pragma unroll
             for (int k = 0; k < S; ++k) {
-                float acc = 0.0f;
+                float acc[NW];
+#pragma unroll
+                for (int u = 0; u < NW; ++u) acc[u] = 0.0f;
 #pragma unroll
                 for (int i = 0; i < G; ++i) {
-                    const RowScales sc = row_scales(w[k][i], ln);
                     int sa, sb;
-                    accumulate(w[k][i], sc, act[i], acc, sa, sb);
+#pragma unroll
+                    for (int u = 0; u < NW; ++u) {
+                        const RowScales sc = row_scales(w[k][i][u], ln);
+                        accumulate(w[k][i][u], sc, act[i], acc[u], sa, sb);
+                    }
                     if constexpr (SUMS) {
                         const int rl = (tb + tk[k]) * TR + r;
                         if (tk[k] < ntiles && rl < n) {
@@ -284,9 +317,13 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_
                         }
                     }
                 }
-                const float q = ks_reduce<SBW>(acc);
                 const int rl = (tb + tk[k]) * TR + r;
-                if (ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n) part[rl * KW + slice] = q;
+                const bool wr = ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n;
+#pragma unroll
+                for (int u = 0; u < NW; ++u) {
+                    const float q = ks_reduce<SBW>(acc[u]);
+                    if (wr) part[(rl * NW + u) * KW + slice] = q;
+                }
                 tk[k] += S;
                 load_tile(tk[k], w[k]);
             }
@@ -295,22 +332,29 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_
         }
     }
     __syncthreads();
-    // 5. each row: the balanced tree over its KW slice sums
+    // 5. each row: the balanced tree over its KW slice sums, then the epilogue
     for (int row = (int)threadIdx.x; row < n; row += kWave * WAVES) {
-        float q[KW];
+        float out[NW];
 #pragma unroll
-        for (int k = 0; k < KW; ++k) q[k] = part[row * KW + k];
+        for (int u = 0; u < NW; ++u) {
+            float q[KW];
 #pragma unroll
-        for (int h = KW / 2; h >= 1; h /= 2)
+            for (int k = 0; k < KW; ++k) q[k] = part[(row * NW + u) * KW + k];
 #pragma unroll
-            for (int t = 0; t < h; ++t) q[t] = q[2 * t] + q[2 * t + 1];
-        p.dst[wg_beg + row] = q[0];
+            for (int h = KW / 2; h >= 1; h /= 2)
+#pragma unroll
+                for (int t = 0; t < h; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+            out[u] = q[0];
+        }
+        p.dst[wg_beg + row] = ks_epilogue<EPI>(p, wg_beg + row, out);
     }
 }
 
 // LDS bytes of a K-split launch: the (row, slice) partials of the largest
-// workgroup share.
-__host__ __device__ constexpr int ksplit_lds_bytes(int rows_per_wg, int sbw) { return rows_per_wg * (16 / sbw) * 4; }
+// workgroup share (nw: 2 with a gate weight, else 1).
+__host__ __device__ constexpr int ksplit_lds_bytes(int rows_per_wg, int sbw, int nw = 1) {
+    return rows_per_wg * (16 / sbw) * 4 * nw;
+}
 
 // ------------------------------------------------------------------------
 // Rows of any length: G groups of 16 super-blocks (G <= GMAX), the last one
@@ -370,14 +414,16 @@ __device__ __forceinline__ LaneAct ks_read_lds(const uint8_t *area, int sbw, int
 
 // SBW: 1, 2 or 4 super-blocks per wave and group; GMAX: the most groups per
 // row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
-// partials).
-template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false>
+// partials); EPI: the fused epilogue, as in gemv_q4k_ksplit_kernel.
+template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
     constexpr int TR = 16 / SBW;
     constexpr int TEAMS = WAVES / KW;
     constexpr int V = 4 * SBW;
+    constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
     static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    static_assert(!SUMS || EPI == kEpiNone, "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
@@ -414,24 +460,29 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
         }
     }
 
-    // 2. the first S steps' weights
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    // 2. the first S steps' weights (GLU: and the gate weight's)
+    __amdgpu_buffer_rsrc_t rsw[NW];
+    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
     const uint32_t lrow = (uint32_t)r * (uint32_t)p.row_stride;
     const uint32_t lh = lrow + (uint32_t)((SBW * slice + s) * kBlockBytes);
     const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
     const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
     const int kb0 = SBW * slice + s;  // the lane's super-block within each group
-    auto load_step = [&](Step st, RowRegs &w) {
+    auto load_step = [&](Step st, RowRegs(&w)[NW]) {
         const bool ok = st.tile < ntiles && 16 * st.i + kb0 < p.nb;
         const uint32_t base = (uint32_t)(tb + st.tile) * tile_bytes + (uint32_t)st.i * (16u * kBlockBytes);
         const uint32_t oh = ok ? base + lh : kOOB;
         const uint32_t oq = ok ? base + lq : kOOB;
-        w.h = load16(rs, oh);
-        w.q0 = load16(rs, oq);
-        w.q1 = load16(rs, oq + 16u);
+#pragma unroll
+        for (int u = 0; u < NW; ++u) {
+            w[u].h = load16(rsw[u], oh);
+            w[u].q0 = load16(rsw[u], oq);
+            w[u].q1 = load16(rsw[u], oq + 16u);
+        }
     };
     Step st[S];
-    RowRegs w[S];
+    RowRegs w[S][NW];
     st[0] = Step{0, 0};
 #pragma unroll
     for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], G);
@@ -465,7 +516,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
     ln.j = j;
     ln.sel = make_scale_sel(j);
     // 4. the (tile, group) steps, S in flight
-    float acc = 0.0f;
+    float acc[NW];
+#pragma unroll
+    for (int u = 0; u < NW; ++u) acc[u] = 0.0f;
     int remaining = ntiles * G;
     if (remaining > 0) {
         for (;;) {
@@ -479,9 +532,12 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
                 }
                 if (16 * st[k].i + SBW * slice < p.nb) {  // the wave's slice reaches this group
                     const LaneAct a = ks_read_lds(area + st[k].i * ks_slice_bytes(SBW), SBW, s, j);
-                    const RowScales sc = row_scales(w[k], ln);
                     int sa, sb;
-                    accumulate(w[k], sc, a, acc, sa, sb);
+#pragma unroll
+                    for (int u = 0; u < NW; ++u) {
+                        const RowScales sc = row_scales(w[k][u], ln);
+                        accumulate(w[k][u], sc, a, acc[u], sa, sb);
+                    }
                     if constexpr (SUMS) {
                         const int rl = (tb + st[k].tile) * TR + r;
                         const int kb = 16 * st[k].i + kb0;
@@ -493,10 +549,14 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
                     }
                 }
                 if (st[k].i == G - 1) {
-                    const float q = ks_reduce<SBW>(acc);
                     const int rl = (tb + st[k].tile) * TR + r;
-                    if (ks_writer<SBW>(lane) && st[k].tile < ntiles && rl < n) part[rl * KW + slice] = q;
-                    acc = 0.0f;
+                    const bool wr = ks_writer<SBW>(lane) && st[k].tile < ntiles && rl < n;
+#pragma unroll
+                    for (int u = 0; u < NW; ++u) {
+                        const float q = ks_reduce<SBW>(acc[u]);
+                        if (wr) part[(rl * NW + u) * KW + slice] = q;
+                        acc[u] = 0.0f;
+                    }
                 }
                 st[k] = next_step(st[(k + S - 1) % S], G);
                 load_step(st[k], w[k]);
@@ -507,24 +567,29 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
     }
     __syncthreads();
     for (int row = (int)threadIdx.x; row < n; row += kWave * WAVES) {
-        float q[KW];
+        float out[NW];
 #pragma unroll
-        for (int k = 0; k < KW; ++k) q[k] = part[row * KW + k];
+        for (int u = 0; u < NW; ++u) {
+            float q[KW];
 #pragma unroll
-        for (int h = KW / 2; h >= 1; h /= 2)
+            for (int k = 0; k < KW; ++k) q[k] = part[(row * NW + u) * KW + k];
 #pragma unroll
-            for (int t = 0; t < h; ++t) q[t] = q[2 * t] + q[2 * t + 1];
-        p.dst[wg_beg + row] = q[0];
+            for (int h = KW / 2; h >= 1; h /= 2)
+#pragma unroll
+                for (int t = 0; t < h; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+            out[u] = q[0];
+        }
+        p.dst[wg_beg + row] = ks_epilogue<EPI>(p, wg_beg + row, out);
     }
 }
 
 // LDS bytes of a long-row K-split launch: the partials, padded to 16 bytes,
-// then every wave's slice of every group.
-__host__ __device__ constexpr int ksplit_long_part_bytes(int rows_per_wg, int sbw) {
-    return (ksplit_lds_bytes(rows_per_wg, sbw) + 15) / 16 * 16;
+// then every wave's slice of every group (nw: 2 with a gate weight).
+__host__ __device__ constexpr int ksplit_long_part_bytes(int rows_per_wg, int sbw, int nw = 1) {
+    return (ksplit_lds_bytes(rows_per_wg, sbw, nw) + 15) / 16 * 16;
 }
-__host__ __device__ constexpr int ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G) {
-    return ksplit_long_part_bytes(rows_per_wg, sbw) + waves * G * ks_slice_bytes(sbw);
+__host__ __device__ constexpr int ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G, int nw = 1) {
+    return ksplit_long_part_bytes(rows_per_wg, sbw, nw) + waves * G * ks_slice_bytes(sbw);
 }
 
 // The instantiated K-split variants: whole teams per workgroup; two groups
@@ -606,6 +671,78 @@ const void *ksplit_long_kernel(int sbw, int waves, int slots, int G) {
         if (waves == 4) return by_slots(std::integral_constant<int, 4>{});
         if (waves == 8) return by_slots(std::integral_constant<int, 8>{});
         if (waves == 16) return by_slots(std::integral_constant<int, 16>{});
+        return nullptr;
+    };
+    if (sbw == 1) return pick(std::integral_constant<int, 1>{});
+    if (sbw == 2) return pick(std::integral_constant<int, 2>{});
+    if (sbw == 4) return pick(std::integral_constant<int, 4>{});
+    return nullptr;
+}
+
+// The fused-epilogue variants (EPI = kEpiBias or kEpiGlu), in the shapes of
+// the plain kernels with 2 or 4 super-blocks per wave (short rows) or 1, 2
+// or 4 (long rows) and one or two steps in flight, where their registers fit
+// the launch bounds: not two steps in flight at 16 waves (the gate weight's
+// registers spilled there).
+constexpr bool ksplit_epi_exists(int sbw, int waves, int slots, int G) {
+    return (sbw == 2 || sbw == 4) && (slots == 1 || (slots == 2 && waves <= 8)) &&
+           ksplit_exists(sbw, waves, slots, G);
+}
+constexpr bool ksplit_long_epi_exists(int sbw, int waves, int slots, int gmax) {
+    return (slots == 1 || (slots == 2 && waves <= 8)) && ksplit_long_exists(sbw, waves, slots, gmax);
+}
+
+template <int EPI>
+const void *ksplit_kernel_epi(int sbw, int waves, int slots, int G) {
+    auto pick = [&](auto sbw_c) -> const void * {
+        constexpr int B = decltype(sbw_c)::value;
+        auto by = [&](auto waves_c, auto s_c, auto g_c) -> const void * {
+            constexpr int W = decltype(waves_c)::value, SS = decltype(s_c)::value, GG = decltype(g_c)::value;
+            if constexpr (ksplit_epi_exists(B, W, SS, GG))
+                return reinterpret_cast<const void *>(&gemv_q4k_ksplit_kernel<B, W, SS, GG, false, EPI>);
+            return nullptr;
+        };
+        auto by_w = [&](auto waves_c) -> const void * {
+            using I1 = std::integral_constant<int, 1>;
+            using I2 = std::integral_constant<int, 2>;
+            if (slots == 1) return G == 1 ? by(waves_c, I1{}, I1{}) : (G == 2 ? by(waves_c, I1{}, I2{}) : nullptr);
+            if (slots == 2) return G == 1 ? by(waves_c, I2{}, I1{}) : (G == 2 ? by(waves_c, I2{}, I2{}) : nullptr);
+            return nullptr;
+        };
+        if (waves == 4) return by_w(std::integral_constant<int, 4>{});
+        if (waves == 8) return by_w(std::integral_constant<int, 8>{});
+        if (waves == 16) return by_w(std::integral_constant<int, 16>{});
+        return nullptr;
+    };
+    if (sbw == 2) return pick(std::integral_constant<int, 2>{});
+    if (sbw == 4) return pick(std::integral_constant<int, 4>{});
+    return nullptr;
+}
+
+template <int EPI>
+const void *ksplit_long_kernel_epi(int sbw, int waves, int slots, int G) {
+    const int gmax = G <= 4 ? 4 : 8;
+    if (G > 8) return nullptr;
+    auto pick = [&](auto sbw_c) -> const void * {
+        constexpr int B = decltype(sbw_c)::value;
+        auto by = [&](auto waves_c, auto s_c, auto g_c) -> const void * {
+            constexpr int W = decltype(waves_c)::value, SS = decltype(s_c)::value, GM = decltype(g_c)::value;
+            if constexpr (ksplit_long_epi_exists(B, W, SS, GM))
+                return reinterpret_cast<const void *>(&gemv_q4k_ksplit_long_kernel<B, W, SS, GM, false, EPI>);
+            return nullptr;
+        };
+        auto by_w = [&](auto waves_c) -> const void * {
+            using I1 = std::integral_constant<int, 1>;
+            using I2 = std::integral_constant<int, 2>;
+            using I4 = std::integral_constant<int, 4>;
+            using I8 = std::integral_constant<int, 8>;
+            if (slots == 1) return gmax == 4 ? by(waves_c, I1{}, I4{}) : by(waves_c, I1{}, I8{});
+            if (slots == 2) return gmax == 4 ? by(waves_c, I2{}, I4{}) : by(waves_c, I2{}, I8{});
+            return nullptr;
+        };
+        if (waves == 4) return by_w(std::integral_constant<int, 4>{});
+        if (waves == 8) return by_w(std::integral_constant<int, 8>{});
+        if (waves == 16) return by_w(std::integral_constant<int, 16>{});
         return nullptr;
     };
     if (sbw == 1) return pick(std::integral_constant<int, 1>{});

@@ -324,6 +324,12 @@ int q4k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * and benchmarks. */
 int q4k_gemv_geometry_q8_1(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
 
+/* The same for a one-column Q4_K launch with the fused epilogue, as
+ * q4k_mul_mat_vec_q_fused makes it on a 16-byte aligned F32 activation:
+ * with_gate != 0 a gate weight and the GLU, else a bias only.  No
+ * counterpart in the reference; for tests and benchmarks. */
+int q4k_gemv_geometry_fused(int64_t ne00, int64_t ne01, int32_t with_gate, int32_t out[8]);
+
 /* Tuning override of the launch geometry for every later call in the
  * process: rows per wave tile of the tile kernel (1, 2, 4), waves per
  * workgroup (tile kernel: 1..8 selects the 8-wave, 9..16 the 16-wave
