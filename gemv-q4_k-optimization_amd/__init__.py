@@ -56,6 +56,7 @@ SIGNATURES = {
     "q4k_gemv_geometry": (_I, [_I64, _I64, _I64, _P]),
     "q4k_gemv_geometry_q8_1": (_I, [_I64, _I64, _I64, _P]),
     "q4k_gemv_geometry_fused": (_I, [_I64, _I64, ctypes.c_int32, _P]),
+    "q6k_gemv_geometry_fused": (_I, [_I64, _I64, ctypes.c_int32, _P]),
     "q4k_set_geometry_override": (_I, [ctypes.c_int32] * 4),
     "q4k_set_pipeline_override": (_I, [ctypes.c_int32] * 2),
     "q4k_read_probe": (_I, [_P, ctypes.c_size_t, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
@@ -347,14 +348,14 @@ def geometry(K: int, M: int, N: int, wtype: int = GGML_TYPE_Q4_K, route: str = "
     """The launch of an (M x K) x (K x N) product: route "f32" quantises
     the F32 activation inside the GEMV launch, "q8_1" runs on a Q8_1
     activation (op_mul_mat_vec_q, or mul_mat_vec_q with a workspace where
-    it quantises separately), "gate" / "bias" the one-column Q4_K launch
-    with that fused epilogue (mul_mat_vec_q_fused)."""
+    it quantises separately), "gate" / "bias" the one-column launch with
+    that fused epilogue (mul_mat_vec_q_fused)."""
     out = (ctypes.c_int32 * 8)()
     if route in ("gate", "bias"):
-        if N != 1 or wtype != GGML_TYPE_Q4_K:
-            raise ValueError("fused geometry: one Q4_K column")
-        _check(lib().q4k_gemv_geometry_fused(K, M, 1 if route == "gate" else 0, ctypes.cast(out, _P)),
-               "q4k_gemv_geometry_fused")
+        if N != 1:
+            raise ValueError("fused geometry: one column")
+        name, fn = _entry(wtype, "q4k_gemv_geometry_fused", "q6k_gemv_geometry_fused")
+        _check(fn(K, M, 1 if route == "gate" else 0, ctypes.cast(out, _P)), name)
     elif route == "q8_1":
         name, fn = _entry(wtype, "q4k_gemv_geometry_q8_1", "q6k_gemv_geometry_q8_1")
     else:

@@ -151,7 +151,7 @@ static Q6Geometry pick_geometry_q6_ksplit_nc(const DeviceInfo &di, int64_t K, in
 // or 16), waves per workgroup (whole teams of TR waves; long rows: 8 or 16),
 // workgroups (default one per CU), tiles in flight (1, 2).
 static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
-                                          int wgs, int slots) {
+                                          int wgs, int slots, int fused = kFusedNone) {
     Q6Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
     const bool lng = K != 4096 && K != 8192;
@@ -172,8 +172,20 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
     const int rows = g.rows_base + (g.rows_extra ? 1 : 0);
-    g.lds = lng ? q6_ksplit_long_lds_bytes(rows, g.ksplit, g.waves, G)
-                : ksplit_lds_bytes(rows, g.ksplit);
+    // fused epilogue: the variants that exist (else ksplit = 0: the caller
+    // takes the tile kernel); with a gate two partials per (row, slice)
+    if (fused != kFusedNone) {
+        const bool glu = fused == kFusedGate;
+        auto ok = [&]() {
+            return lng ? q6_ksplit_long_epi_exists(g.ksplit, g.waves, g.slots, G <= 4 ? 4 : 8, glu)
+                       : q6_ksplit_epi_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096), glu);
+        };
+        if (g.slots > 2 || !ok()) g.slots = 1;
+        if (!ok()) g.ksplit = 0;
+    }
+    const int nw = fused == kFusedGate ? 2 : 1;
+    const int sbw = g.ksplit ? g.ksplit : 1;
+    g.lds = lng ? q6_ksplit_long_lds_bytes(rows, sbw, g.waves, G, nw) : ksplit_lds_bytes(rows, sbw, nw);
     g.lds_launch = g.lds;
     g.nc_chunk = 1;
     return g;
@@ -300,6 +312,22 @@ static Q6Geometry pick_geometry_q6_mfma(const DeviceInfo &di, int64_t K, int64_t
 // the staging rounds issued ahead of them.  Measured on MI355X: with 210-byte blocks, more
 // weight requests in flight (16 waves x 2 groups, 27.5 MB over the chip)
 // delay the activation loads more than they hide latency.
+// The K-split kernel's automatic shape for one aligned F32 column with a
+// gate weight and the GLU; false where the tile kernel is kept.  Measured on
+// MI355X (us per fused op, one process, K-split against the fused tile
+// kernel): rows of 4096 or 8192 values 4 rows per step, 4 waves, one tile in
+// flight (4096 x 4096 7.57 against 8.88, 14336 x 4096 19.71 / 21.55, 28672 x
+// 8192 69.51 / 72.01, where the one-column rule's shape, two tiles in
+// flight, took 74.51); other lengths 8 rows, 8 waves, one step (4096 x
+// 14336 21.94 / 23.63).  Rows of 4096 values or more, up to 160 rows per CU.
+static bool q6_ksplit_glu_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
+    const int64_t rho = (M + cus - 1) / cus;
+    if (rho > 160 || K < 4096) return false;
+    tr = waves = K == 4096 || K == 8192 ? 4 : 8;
+    slots = 1;
+    return true;
+}
+
 static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int64_t mats = 1,
                                    int fused = kFusedNone, bool f32_vec = true, bool q81 = false) {
     Q6Geometry g;
@@ -310,7 +338,7 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     // groups (4096 or 8192 values: activation in registers; other lengths:
     // the long-row variant); the tile kernel, whose outputs are the same
     // bits, takes the rest
-    const bool ks_ok = N == 1 && mats == 1 && fused == kFusedNone && f32_vec && K <= 8 * 4096;
+    const bool ks_ok = N == 1 && mats == 1 && f32_vec && K <= 8 * 4096;  // (fused epilogues included)
     // two to four columns: the several-column K-split kernel, whose outputs
     // are the bits of the tile kernel's launches (all columns in one, or
     // four two by two; not the dense layout).  Through the override only:
@@ -327,14 +355,17 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     if (ksn_ok && okern == 5)
         return pick_geometry_q6_ksplit_nc(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(), g_ovr_wgs.load(),
                                           g_ovr_slots.load(), (int)N, ksn_p);
-    if (ks_ok && okern == 5)
-        return pick_geometry_q6_ksplit(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(), g_ovr_wgs.load(),
-                                       g_ovr_slots.load());
+    if (ks_ok && okern == 5) {
+        const Q6Geometry gk = pick_geometry_q6_ksplit(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(),
+                                                      g_ovr_wgs.load(), g_ovr_slots.load(), fused);
+        if (gk.ksplit) return gk;
+    }
     if (ks_ok && okern == 0 && g_ovr_rows.load() == 0 && g_ovr_waves.load() == 0 && g_ovr_wgs.load() == 0) {
         int tr = 0, kw = 0, ks = 0;
-        if (q6_ksplit_auto(K, M, cus, tr, kw, ks)) {
+        if (fused == kFusedGate ? q6_ksplit_glu_auto(K, M, cus, tr, kw, ks) : q6_ksplit_auto(K, M, cus, tr, kw, ks)) {
             const int os = g_ovr_slots.load();
-            return pick_geometry_q6_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks);
+            const Q6Geometry gk = pick_geometry_q6_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks, fused);
+            if (gk.ksplit && gk.lds <= max_lds) return gk;
         }
     }
     // the matrix-core kernel with its A operand from the Q8_1 buffer: the
@@ -559,13 +590,17 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.glu_op = ep->glu_op;
         }
         const void *fn = geo.ks_nc_p  ? q6_ksplit_nc_kernel<false>(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
+                         : geo.ksplit && fused == kFusedGate
+                             ? q6_ksplit_kernel_epi<kEpiGlu>(geo.ks_long != 0, geo.ksplit, geo.waves, geo.slots, p.G)
+                         : geo.ksplit && fused == kFusedBias
+                             ? q6_ksplit_kernel_epi<kEpiBias>(geo.ks_long != 0, geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.ks_long  ? q6_ksplit_long_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.ksplit ? q6_ksplit_kernel<false>(geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.mfma_ga ? q6_mfma_ga_kernel_for(nc, geo.waves)
                          : geo.mfma ? q6_mfma_kernel_for(nc, geo.waves)
                          : bl       ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
                                     : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
-        if (geo.ksplit && (nc != (geo.ks_nc_p ? geo.nc_chunk : 1) || fused || bl || !p.x || !p.vec_ok))
+        if (geo.ksplit && (nc != (geo.ks_nc_p ? geo.nc_chunk : 1) || (fused && geo.ks_nc_p) || bl || !p.x || !p.vec_ok))
             return Q4K_EINVAL;
         if (geo.ks_nc_p) p.ring_off = q6_ksn_stage_bytes(p.K, nc);
         if (geo.mfma) {
@@ -587,7 +622,8 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         }
         if (bl) p.bt = bl->bt;
         if (geo.ks_long) {
-            p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit);
+            p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit,
+                                                fused == kFusedGate ? 2 : 1);
             // groups quantised before the first step: one, the others just
             // before the first step that reads them (4096 x 14336 12.08
             // against 12.14 us with all before, 8192 x 28672 37.04 / 38.42);
@@ -780,6 +816,23 @@ int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) 
 
 int q6k_gemv_geometry_q8_1(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]) {
     return gemv_geometry_q6(ne00, ne01, ne11, true, out);
+}
+
+int q6k_gemv_geometry_fused(int64_t ne00, int64_t ne01, int32_t with_gate, int32_t out[8]) {
+    if (!out || ne00 <= 0 || ne00 % kQK != 0 || ne01 < 0) return Q4K_EINVAL;
+    DeviceInfo *di = nullptr;
+    const int st = device_info(&di);
+    if (st != Q4K_OK) return st;
+    const Q6Geometry g = pick_geometry_q6(*di, ne00, ne01, 1, 1, with_gate ? kFusedGate : kFusedBias, true, false);
+    out[0] = g.ksplit ? g.ks_tr : (g.mfma ? kMfmaRows : 1);
+    out[1] = g.waves;
+    out[2] = g.grid;
+    out[3] = g.lds_launch;
+    out[4] = g.nc_chunk;
+    out[5] = 1;
+    out[6] = g.ksplit ? 5 : (g.mfma ? 4 : 1);
+    out[7] = g.slots;
+    return Q4K_OK;
 }
 
 }  // extern "C"

@@ -79,13 +79,16 @@ __device__ __forceinline__ Q6Act q6_ks_stage(const float (&v)[4 * SBW], int s, i
 // groups per row.  SUMS: the parity variant, which also stores every lane's
 // four int32 group sums.  Rows: the workgroup's share, tiles of TR rows
 // split contiguously over the teams.
-template <int SBW, int WAVES, int S, int G, bool SUMS = false>
+// EPI: the fused epilogue, as in the Q4_K K-split kernels (ks_epilogue).
+template <int SBW, int WAVES, int S, int G, bool SUMS = false, int EPI = kEpiNone>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
     constexpr int TR = 16 / SBW;
     constexpr int TEAMS = WAVES / KW;
     constexpr int V = 4 * SBW;
+    constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
     static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    static_assert(!SUMS || EPI == kEpiNone, "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
@@ -120,8 +123,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_
         }
     }
 
-    // 2. the first S tiles' weights
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    // 2. the first S tiles' weights (GLU: and the gate weight's, at the same offsets)
+    __amdgpu_buffer_rsrc_t rsw[NW];
+    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
     Q6Lane ln;
     ln.lane = lane;
     ln.g = SBW * slice + s;
@@ -133,14 +138,16 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_
     ln.o_sc = blk + 192u + 8u * (uint32_t)h;
     ln.o_d = blk + 206u;
     const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
-    auto load_tile = [&](int t, Q6Regs(&w)[G]) {
+    auto load_tile = [&](int t, Q6Regs(&w)[G][NW]) {
         const bool ok = t < ntiles;
         const uint32_t base = (uint32_t)(tb + t) * tile_bytes;
 #pragma unroll
-        for (int i = 0; i < G; ++i) q6_load(rs, ln, base + (uint32_t)i * (16u * kQ6Bytes), ok, w[i]);
+        for (int i = 0; i < G; ++i)
+#pragma unroll
+            for (int u = 0; u < NW; ++u) q6_load(rsw[u], ln, base + (uint32_t)i * (16u * kQ6Bytes), ok, w[i][u]);
     };
     int tk[S];
-    Q6Regs w[S][G];
+    Q6Regs w[S][G][NW];
 #pragma unroll
     for (int k = 0; k < S; ++k) {
         tk[k] = k;
@@ -158,14 +165,20 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_
         for (;;) {
 #pragma unroll
             for (int k = 0; k < S; ++k) {
-                float acc = 0.0f;
+                float acc[NW];
+#pragma unroll
+                for (int u = 0; u < NW; ++u) acc[u] = 0.0f;
 #pragma unroll
                 for (int i = 0; i < G; ++i) {
-                    uint32_t v[4][4];
-                    int sc[4], gs[4];
-                    q6_values(w[k][i], v);
-                    q6_scales(w[k][i], jp, sc);
-                    q6_accumulate(v, sc, half_bits_to_float(w[k][i].dw >> 16), act[i], acc, gs);
+                    int gs[4];
+#pragma unroll
+                    for (int u = 0; u < NW; ++u) {
+                        uint32_t v[4][4];
+                        int sc[4];
+                        q6_values(w[k][i][u], v);
+                        q6_scales(w[k][i][u], jp, sc);
+                        q6_accumulate(v, sc, half_bits_to_float(w[k][i][u].dw >> 16), act[i], acc[u], gs);
+                    }
                     if constexpr (SUMS) {
                         const int rl = (tb + tk[k]) * TR + r;
                         if (tk[k] < ntiles && rl < n) {
@@ -175,9 +188,13 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_
                         }
                     }
                 }
-                const float q = ks_reduce<SBW>(acc);
                 const int rl = (tb + tk[k]) * TR + r;
-                if (ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n) part[rl * KW + slice] = q;
+                const bool wr = ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n;
+#pragma unroll
+                for (int u = 0; u < NW; ++u) {
+                    const float q = ks_reduce<SBW>(acc[u]);
+                    if (wr) part[(rl * NW + u) * KW + slice] = q;
+                }
                 tk[k] += S;
                 load_tile(tk[k], w[k]);
             }
@@ -188,14 +205,19 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_
     __syncthreads();
     // 5. each row: the balanced tree over its KW slice sums
     for (int row = (int)threadIdx.x; row < n; row += kWave * WAVES) {
-        float q[KW];
+        float out[NW];
 #pragma unroll
-        for (int k = 0; k < KW; ++k) q[k] = part[row * KW + k];
+        for (int u = 0; u < NW; ++u) {
+            float q[KW];
 #pragma unroll
-        for (int hh = KW / 2; hh >= 1; hh /= 2)
+            for (int k = 0; k < KW; ++k) q[k] = part[(row * NW + u) * KW + k];
 #pragma unroll
-            for (int t = 0; t < hh; ++t) q[t] = q[2 * t] + q[2 * t + 1];
-        p.dst[wg_beg + row] = q[0];
+            for (int hh = KW / 2; hh >= 1; hh /= 2)
+#pragma unroll
+                for (int t = 0; t < hh; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+            out[u] = q[0];
+        }
+        p.dst[wg_beg + row] = ks_epilogue<EPI>(p, wg_beg + row, out);
     }
 }
 
@@ -248,13 +270,15 @@ __device__ __forceinline__ Q6Act q6_ks_read_lds(const uint8_t *area, int sbw, in
 // SBW: 1, 2 or 4 super-blocks per wave and group; GMAX: the most groups per
 // row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
 // partials).
-template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false>
+template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
     constexpr int TR = 16 / SBW;
     constexpr int TEAMS = WAVES / KW;
     constexpr int V = 4 * SBW;
+    constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
     static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    static_assert(!SUMS || EPI == kEpiNone, "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
@@ -291,8 +315,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
         }
     }
 
-    // 2. the first S steps' weights
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    // 2. the first S steps' weights (GLU: and the gate weight's)
+    __amdgpu_buffer_rsrc_t rsw[NW];
+    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
     Q6Lane ln;
     ln.lane = lane;
     ln.g = SBW * slice + s;  // the lane's super-block within each group
@@ -304,12 +330,14 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
     ln.o_sc = blk + 192u + 8u * (uint32_t)h;
     ln.o_d = blk + 206u;
     const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
-    auto load_step = [&](Step st, Q6Regs &w) {
+    auto load_step = [&](Step st, Q6Regs(&w)[NW]) {
         const bool ok = st.tile < ntiles && 16 * st.i + ln.g < p.nb;
-        q6_load(rs, ln, (uint32_t)(tb + st.tile) * tile_bytes + (uint32_t)st.i * (16u * kQ6Bytes), ok, w);
+#pragma unroll
+        for (int u = 0; u < NW; ++u)
+            q6_load(rsw[u], ln, (uint32_t)(tb + st.tile) * tile_bytes + (uint32_t)st.i * (16u * kQ6Bytes), ok, w[u]);
     };
     Step st[S];
-    Q6Regs w[S];
+    Q6Regs w[S][NW];
     st[0] = Step{0, 0};
 #pragma unroll
     for (int k = 1; k < S; ++k) st[k] = next_step(st[k - 1], G);
@@ -334,7 +362,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
     int staged = max(1, min(p.rpw, G));  // groups staged so far
 
     // 4. the (tile, group) steps, S in flight
-    float acc = 0.0f;
+    float acc[NW];
+#pragma unroll
+    for (int u = 0; u < NW; ++u) acc[u] = 0.0f;
     int remaining = ntiles * G;
     if (remaining > 0) {
         for (;;) {
@@ -348,11 +378,15 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
                 }
                 if (16 * st[k].i + SBW * slice < p.nb) {  // the wave's slice reaches this group
                     const Q6Act a = q6_ks_read_lds(area + st[k].i * q6_ks_slice_bytes(SBW), SBW, s, h, jp);
-                    uint32_t v[4][4];
-                    int sc[4], gs[4];
-                    q6_values(w[k], v);
-                    q6_scales(w[k], jp, sc);
-                    q6_accumulate(v, sc, half_bits_to_float(w[k].dw >> 16), a, acc, gs);
+                    int gs[4];
+#pragma unroll
+                    for (int u = 0; u < NW; ++u) {
+                        uint32_t v[4][4];
+                        int sc[4];
+                        q6_values(w[k][u], v);
+                        q6_scales(w[k][u], jp, sc);
+                        q6_accumulate(v, sc, half_bits_to_float(w[k][u].dw >> 16), a, acc[u], gs);
+                    }
                     if constexpr (SUMS) {
                         const int rl = (tb + st[k].tile) * TR + r;
                         const int kb = 16 * st[k].i + ln.g;
@@ -364,10 +398,14 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
                     }
                 }
                 if (st[k].i == G - 1) {
-                    const float q = ks_reduce<SBW>(acc);
                     const int rl = (tb + st[k].tile) * TR + r;
-                    if (ks_writer<SBW>(lane) && st[k].tile < ntiles && rl < n) part[rl * KW + slice] = q;
-                    acc = 0.0f;
+                    const bool wr = ks_writer<SBW>(lane) && st[k].tile < ntiles && rl < n;
+#pragma unroll
+                    for (int u = 0; u < NW; ++u) {
+                        const float q = ks_reduce<SBW>(acc[u]);
+                        if (wr) part[(rl * NW + u) * KW + slice] = q;
+                        acc[u] = 0.0f;
+                    }
                 }
                 st[k] = next_step(st[(k + S - 1) % S], G);
                 load_step(st[k], w[k]);
@@ -378,19 +416,24 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
     }
     __syncthreads();
     for (int row = (int)threadIdx.x; row < n; row += kWave * WAVES) {
-        float q[KW];
+        float out[NW];
 #pragma unroll
-        for (int k = 0; k < KW; ++k) q[k] = part[row * KW + k];
+        for (int u = 0; u < NW; ++u) {
+            float q[KW];
 #pragma unroll
-        for (int hh = KW / 2; hh >= 1; hh /= 2)
+            for (int k = 0; k < KW; ++k) q[k] = part[(row * NW + u) * KW + k];
 #pragma unroll
-            for (int t = 0; t < hh; ++t) q[t] = q[2 * t] + q[2 * t + 1];
-        p.dst[wg_beg + row] = q[0];
+            for (int hh = KW / 2; hh >= 1; hh /= 2)
+#pragma unroll
+                for (int t = 0; t < hh; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+            out[u] = q[0];
+        }
+        p.dst[wg_beg + row] = ks_epilogue<EPI>(p, wg_beg + row, out);
     }
 }
 
-__host__ __device__ constexpr int q6_ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G) {
-    return ksplit_long_part_bytes(rows_per_wg, sbw) + waves * G * q6_ks_slice_bytes(sbw);
+__host__ __device__ constexpr int q6_ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G, int nw = 1) {
+    return ksplit_long_part_bytes(rows_per_wg, sbw, nw) + waves * G * q6_ks_slice_bytes(sbw);
 }
 
 // The long-row variants: those of the Q4_K kernel (SBW 1 or 2 for rows of
@@ -459,6 +502,63 @@ const void *q6_ksplit_sym_w(int waves, int slots, int G) {
     if (waves == 4) return slots == 2 ? q6_ksplit_sym_g<SUMS, SBW, 4, 2>(G) : q6_ksplit_sym_g<SUMS, SBW, 4, 1>(G);
     if (waves == 8) return slots == 2 ? q6_ksplit_sym_g<SUMS, SBW, 8, 2>(G) : q6_ksplit_sym_g<SUMS, SBW, 8, 1>(G);
     if (waves == 16) return slots == 2 ? q6_ksplit_sym_g<SUMS, SBW, 16, 2>(G) : q6_ksplit_sym_g<SUMS, SBW, 16, 1>(G);
+    return nullptr;
+}
+
+// The fused-epilogue variants (EPI = kEpiBias or kEpiGlu): the plain
+// kernels' shapes with one step in flight, or two in workgroups of up to 8
+// waves; with a gate weight 16-wave workgroups only at one super-block per
+// wave (elsewhere the gate weight's registers spilled).
+constexpr bool q6_ksplit_epi_exists(int sbw, int waves, int slots, int G, bool glu) {
+    return (slots == 1 || (slots == 2 && waves <= 8)) && !(glu && waves == 16 && sbw != 1) &&
+           q6_ksplit_exists(sbw, waves, slots, G);
+}
+constexpr bool q6_ksplit_long_epi_exists(int sbw, int waves, int slots, int gmax, bool glu) {
+    return (slots == 1 || (slots == 2 && waves <= 8)) && !(glu && waves == 16 && sbw != 1) &&
+           q6_ksplit_long_exists(sbw, waves, slots, gmax);
+}
+
+// The fused Q6_K K-split kernel (rows of 1 or 2 groups, long = false; any
+// other length up to 8 groups, long = true) of a launch shape, or null.
+template <int EPI>
+const void *q6_ksplit_kernel_epi(bool lng, int sbw, int waves, int slots, int G) {
+    const int gsel = lng ? (G <= 4 ? 4 : 8) : G;
+    if (lng ? G > 8 : (G != 1 && G != 2)) return nullptr;
+    auto pick = [&](auto sbw_c) -> const void * {
+        constexpr int B = decltype(sbw_c)::value;
+        auto by = [&](auto waves_c, auto s_c, auto g_c) -> const void * {
+            constexpr int W = decltype(waves_c)::value, SS = decltype(s_c)::value, GG = decltype(g_c)::value;
+            if constexpr (GG <= 2) {
+                if constexpr (q6_ksplit_epi_exists(B, W, SS, GG, EPI == kEpiGlu))
+                    if (!lng) return reinterpret_cast<const void *>(&gemv_q6k_ksplit_kernel<B, W, SS, GG, false, EPI>);
+            } else {
+                if constexpr (q6_ksplit_long_epi_exists(B, W, SS, GG, EPI == kEpiGlu))
+                    if (lng) return reinterpret_cast<const void *>(&gemv_q6k_ksplit_long_kernel<B, W, SS, GG, false, EPI>);
+            }
+            return nullptr;
+        };
+        auto by_g = [&](auto waves_c, auto s_c) -> const void * {
+            switch (gsel) {
+                case 1: return by(waves_c, s_c, std::integral_constant<int, 1>{});
+                case 2: return by(waves_c, s_c, std::integral_constant<int, 2>{});
+                case 4: return by(waves_c, s_c, std::integral_constant<int, 4>{});
+                case 8: return by(waves_c, s_c, std::integral_constant<int, 8>{});
+                default: return nullptr;
+            }
+        };
+        auto by_w = [&](auto waves_c) -> const void * {
+            if (slots == 1) return by_g(waves_c, std::integral_constant<int, 1>{});
+            if (slots == 2) return by_g(waves_c, std::integral_constant<int, 2>{});
+            return nullptr;
+        };
+        if (waves == 4) return by_w(std::integral_constant<int, 4>{});
+        if (waves == 8) return by_w(std::integral_constant<int, 8>{});
+        if (waves == 16) return by_w(std::integral_constant<int, 16>{});
+        return nullptr;
+    };
+    if (sbw == 1) return pick(std::integral_constant<int, 1>{});
+    if (sbw == 2) return pick(std::integral_constant<int, 2>{});
+    if (sbw == 4) return pick(std::integral_constant<int, 4>{});
     return nullptr;
 }
 

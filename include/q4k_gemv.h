@@ -302,6 +302,11 @@ int q6k_gemv_geometry(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
  * counterpart in the reference; for tests and benchmarks. */
 int q6k_gemv_geometry_q8_1(int64_t ne00, int64_t ne01, int64_t ne11, int32_t out[8]);
 
+/* The same for a one-column Q6_K launch with the fused epilogue (as
+ * q4k_gemv_geometry_fused).  No counterpart in the reference; for tests and
+ * benchmarks. */
+int q6k_gemv_geometry_fused(int64_t ne00, int64_t ne01, int32_t with_gate, int32_t out[8]);
+
 /* Launch geometry q4k_mul_mat_vec_q would use on the current device:
  * out[0] rows per wave tile (tile kernel), out[1] waves per workgroup,
  * out[2] workgroups, out[3] LDS bytes requested per workgroup, out[4] columns per

@@ -1,4 +1,4 @@
-"""GPU parity of the one-column Q4_K K-split kernels with the fused
+"""GPU parity of the one-column Q4_K and Q6_K K-split kernels with the fused
 epilogue (kernels/mmvq.cu:254-262, :309-336): the bias on the product, or
 the gate weight streamed in the same launch, its bias and the GLU of the
 pair.
@@ -20,16 +20,18 @@ pytestmark = pytest.mark.gpu
 
 SHORT = [(8, 8, 1), (8, 8, 2), (8, 16, 1), (4, 4, 1), (4, 4, 2), (4, 8, 1), (4, 8, 2), (4, 16, 1)]
 LONG = [(16, 16, 1), (8, 8, 1), (8, 8, 2), (8, 16, 1), (4, 4, 1), (4, 4, 2), (4, 8, 1), (4, 8, 2), (4, 16, 1)]
+Q4, Q6 = 12, 14  # ggml type ids
 
 _cache = {}
 
 
-def weights(Q, M, K, seed):
-    key = (M, K, seed)
+def weights(Q, M, K, seed, wtype=Q4):
+    key = (M, K, seed, wtype)
     if key not in _cache:
         if len(_cache) > 4:
             _cache.clear()
-        _cache[key] = Q.quantize_rows_q4_K(_common.weights(M, K, seed), nthreads=16)
+        quant = Q.quantize_rows_q4_K if wtype == Q4 else Q.quantize_rows_q6_K
+        _cache[key] = quant(_common.weights(M, K, seed), nthreads=16)
     return _cache[key]
 
 
@@ -38,21 +40,25 @@ def to_dev(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-def launch_shapes(K):
+def launch_shapes(K, wtype):
+    if wtype == Q6:
+        return LONG  # (16 rows per step exists for rows of 4096 and 8192 values too)
     return SHORT if K in (4096, 8192) else LONG
 
 
-def fused(Q, wd, K, xd, gd, bu, bg, op):
-    return Q.mul_mat_vec_q_fused(wd, K, xd, gate=gd, x_bias=bu, gate_bias=bg, glu_op=op).cpu().numpy()
+def fused(Q, wd, K, xd, gd, bu, bg, op, wtype=Q4):
+    return Q.mul_mat_vec_q_fused(wd, K, xd, gate=gd, x_bias=bu, gate_bias=bg, glu_op=op,
+                                 wtype=wtype).cpu().numpy()
 
 
+@pytest.mark.parametrize("wtype", [Q4, Q6])
 @pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 4096), (1024, 4096), (37, 4096), (5000, 8192), (258, 8192),
                                  (4096, 14336), (1000, 11008), (300, 5120)])
-def test_ksplit_fused_bits_equal_tile_kernel(Q, gpu, M, K):
+def test_ksplit_fused_bits_equal_tile_kernel(Q, gpu, wtype, M, K):
     """Gate + GLU (SWIGLU, GEGLU, SWIGLU_OAI; with and without biases) and
     the bias-only epilogue, every K-split launch shape against the fused
     tile kernel."""
-    wu, wg = weights(Q, M, K, 1), weights(Q, M, K, 2)
+    wu, wg = weights(Q, M, K, 1, wtype), weights(Q, M, K, 2, wtype)
     x = _common.activations(1, K, seed=3)
     rng = np.random.default_rng([M, K])
     bu = to_dev(rng.standard_normal(M).astype(np.float32) * np.float32(0.1), gpu)
@@ -63,43 +69,48 @@ def test_ksplit_fused_bits_equal_tile_kernel(Q, gpu, M, K):
         gd = wgd if route == "gate" else None
         try:
             Q.set_geometry_override(kernel=1)
-            assert Q.geometry(K, M, 1, route=route)["kernel"] == 1
-            y_tile = fused(Q, wud, K, xd, gd, b1, b2, op or 2)
+            assert Q.geometry(K, M, 1, wtype, route=route)["kernel"] == 1
+            y_tile = fused(Q, wud, K, xd, gd, b1, b2, op or 2, wtype)
         finally:
             Q.set_geometry_override()
         ran = 0
-        for tr, waves, slots in launch_shapes(K):
+        for tr, waves, slots in launch_shapes(K, wtype):
             for wgs in (0, 7, 300):
                 try:
                     Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, workgroups=wgs, kernel=5)
                     Q.set_pipeline_override(slots=slots)
-                    g = Q.geometry(K, M, 1, route=route)
+                    g = Q.geometry(K, M, 1, wtype, route=route)
                     if g["kernel"] != 5:
                         continue  # no fused variant of this shape (its registers would spill)
-                    assert g["rows_per_step"] == tr and g["waves_per_wg"] == waves, g
-                    y = fused(Q, wud, K, xd, gd, b1, b2, op or 2)
+                    if g["lds_bytes"] > 160 * 1024:
+                        continue  # two weights' partials of this many rows per workgroup exceed the LDS
+                    rows = g["rows_per_step"] if wtype == Q4 else g["rows_per_tile"]
+                    assert rows == tr and g["waves_per_wg"] == waves, g
+                    y = fused(Q, wud, K, xd, gd, b1, b2, op or 2, wtype)
                 finally:
                     Q.set_geometry_override()
                     Q.set_pipeline_override()
                 ran += 1
                 if not np.array_equal(y, y_tile):
                     bad = np.flatnonzero(y[0] != y_tile[0])
-                    raise AssertionError(f"{M}x{K} {route} op {op} rows/step {tr} waves {waves} slots {slots} "
+                    raise AssertionError(f"type {wtype} {M}x{K} {route} op {op} rows/step {tr} waves {waves} "
+                                         f"slots {slots} "
                                          f"wgs {wgs}: {bad.size} outputs differ from the tile kernel, e.g. rows "
                                          f"{bad[:5]}")
-        assert ran >= 9, f"{M}x{K} {route}: only {ran} K-split launches ran"
+        assert ran >= 9, f"type {wtype} {M}x{K} {route}: only {ran} K-split launches ran"
         # the automatic choice: the same bits
-        assert np.array_equal(fused(Q, wud, K, xd, gd, b1, b2, op or 2), y_tile)
+        assert np.array_equal(fused(Q, wud, K, xd, gd, b1, b2, op or 2, wtype), y_tile)
 
 
 @pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 4096), (28672, 8192), (4096, 14336)])
 def test_ksplit_fused_automatic_choice(Q, gpu, M, K):
     """The fused one-column launches of the workload shapes take the K-split
-    kernel automatically, and an unaligned activation the tile kernel (same
-    bits)."""
+    kernel automatically (Q4_K and Q6_K), and an unaligned activation the
+    tile kernel (same bits)."""
     import torch
-    for route in ("gate", "bias"):
-        assert Q.geometry(K, M, 1, route=route)["kernel"] == 5
+    for wtype in (Q4, Q6):
+        for route in ("gate", "bias"):
+            assert Q.geometry(K, M, 1, wtype, route=route)["kernel"] == 5, (wtype, route)
     if M * K > 4096 * 4096:
         return
     wu, wg = weights(Q, M, K, 1), weights(Q, M, K, 2)
