@@ -330,7 +330,8 @@ static Geometry pick_geometry_mfma(const DeviceInfo &di, int64_t K, int64_t M, i
 // (whole teams of TR waves), workgroups (default one per CU) and row tiles
 // in flight per wave (1 or 2).
 static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
-                                     int wgs, int slots, int N = 1, int staged = 0, int P = 0, int fused = 0) {
+                                     int wgs, int slots, int N = 1, int staged = 0, int P = 0, int fused = 0,
+                                     bool batch = false) {
     Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
     if (N >= 2) {  // two to four columns
@@ -390,16 +391,19 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
     const int rows = g.rows_base + (g.rows_extra ? 1 : 0);
-    // fused epilogue: the variants that exist (else ksplit = 0: the caller
-    // takes the tile kernel); with a gate two partials per (row, slice)
-    if (fused) {
-        if (g.slots > 2) g.slots = 2;
-        const bool ok = lng ? ksplit_long_epi_exists(g.ksplit, g.waves, g.slots, gmax)
-                            : ksplit_epi_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096));
-        if (!ok) g.slots = 1;
-        if (!(lng ? ksplit_long_epi_exists(g.ksplit, g.waves, g.slots, gmax)
-                  : ksplit_epi_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096))))
-            g.ksplit = 0;
+    // fused epilogue or batched launch: the variants that exist (else
+    // ksplit = 0: the caller takes the tile kernel); with a gate two
+    // partials per (row, slice)
+    if (fused || batch) {
+        const int gk = lng ? gmax : (int)(K / 4096);
+        auto ok = [&]() {
+            return batch ? (lng ? ksplit_long_batch_exists(g.ksplit, g.waves, g.slots, gk)
+                                : ksplit_batch_exists(g.ksplit, g.waves, g.slots, gk))
+                         : (lng ? ksplit_long_epi_exists(g.ksplit, g.waves, g.slots, gk)
+                                : ksplit_epi_exists(g.ksplit, g.waves, g.slots, gk));
+        };
+        if (g.slots > 2 || !ok()) g.slots = 1;
+        if (!ok()) g.ksplit = 0;
     }
     const int nw = fused == kFusedGate ? 2 : 1;
     g.lds = lng ? ksplit_long_lds_bytes(rows, g.ksplit ? g.ksplit : 1, g.waves, G, nw)
@@ -635,7 +639,13 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // groups (4096 or 8192 values: activation in registers; other lengths:
     // the long-row variant); the tile kernel, whose outputs are the same
     // bits, takes the rest
-    const bool ks_ok = N == 1 && mats == 1 && f32_vec && K <= 8 * 4096;  // (fused epilogues included)
+    // (fused epilogues and batched launches included; a batched launch's
+    // workgroups per weight matrix: grid_per_matrix.  Batched, rows of 4096
+    // values or more: MUL_MAT_ID measured on MI355X, Mixtral 8x7B gate/up
+    // with SWIGLU, Q4_K, 26.61 -> 25.27 us, down, Q6_K, 22.27 -> 19.64; the
+    // 2048 x 768 Q6_K experts of a Qwen3-30B-A3B-like down 7.72 -> 7.98)
+    const bool ks_ok = N == 1 && f32_vec && K <= 8 * 4096 && (mats == 1 || K >= 4096);
+    const int cus_m = mats > 1 ? grid_per_matrix(cus, mats, M) : cus;
     // two to four columns: the K-split kernel for rows of 1 or 2 groups
     // (the tile kernel's launches, whose bits these are: all columns in one,
     // or four columns two by two)
@@ -645,16 +655,17 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     if (ksn_ok && okern == 5)
         return pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load(), (int)N, 1, ksn_p);
     if (ks_ok && okern == 5) {
-        const Geometry gk = pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load(), 1, 0, 0, fused);
+        const Geometry gk = pick_geometry_ksplit(di, K, M, orows, owaves, owgs > 0 ? owgs : (mats > 1 ? cus_m : 0),
+                                                 g_ovr_slots.load(), 1, 0, 0, fused, mats > 1);
         if (gk.ksplit) return gk;
     }
     // (automatic: where the partials fit the LDS)
     if (ks_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
         int tr = 0, kw = 0, ks = 0;
-        if (fused == kFusedGate ? ksplit_glu_auto(K, M, cus, tr, kw, ks) : ksplit_auto(K, M, cus, tr, kw, ks)) {
+        if (fused == kFusedGate ? ksplit_glu_auto(K, M, cus_m, tr, kw, ks) : ksplit_auto(K, M, cus_m, tr, kw, ks)) {
             const int os = g_ovr_slots.load();
-            const Geometry gk =
-                pick_geometry_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks, 1, 0, 0, fused);
+            const Geometry gk = pick_geometry_ksplit(di, K, M, tr, kw, mats > 1 ? cus_m : 0,
+                                                     os >= 1 && os <= 4 ? os : ks, 1, 0, 0, fused, mats > 1);
             if (gk.ksplit && gk.lds <= max_lds) return gk;
         }
     }
@@ -980,7 +991,7 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         p.rows_base = geo.rows_base;
         p.rows_extra = geo.rows_extra;
         p.ring_off = lds_bytes(p.K, nc);
-    } else if (batch) {
+    } else if (batch && !geo.ksplit) {
         if (geo.R != 1) return Q4K_EINVAL;
         fn = gemv_kernel_batch(nc, geo.waves, geo.prologue, geo.slots);
         p.rows_base = geo.rows_base;
@@ -998,7 +1009,11 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
                             : ksplit_nc_kernel<false>(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0);
             p.ring_off = geo.ks_staged ? ksn_stage_bytes(p.K, nc) : 0;
         } else if (geo.ks_long) {
-            if (p.gate)
+            if (batch)
+                fn = p.gate   ? ksplit_long_kernel_epi<kEpiGlu, true>(geo.ksplit, geo.waves, geo.slots, p.G)
+                     : p.bias ? ksplit_long_kernel_epi<kEpiBias, true>(geo.ksplit, geo.waves, geo.slots, p.G)
+                              : ksplit_long_kernel_epi<kEpiNone, true>(geo.ksplit, geo.waves, geo.slots, p.G);
+            else if (p.gate)
                 fn = ksplit_long_kernel_epi<kEpiGlu>(geo.ksplit, geo.waves, geo.slots, p.G);
             else if (p.bias)
                 fn = ksplit_long_kernel_epi<kEpiBias>(geo.ksplit, geo.waves, geo.slots, p.G);
@@ -1014,6 +1029,10 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
             // one
             const int opro = g_ovr_prologue.load();
             p.rpw = (opro == 2 || (opro < 0 && geo.ksplit == 1)) ? p.G : 1;
+        } else if (batch) {
+            fn = p.gate   ? ksplit_kernel_epi<kEpiGlu, true>(geo.ksplit, geo.waves, geo.slots, p.G)
+                 : p.bias ? ksplit_kernel_epi<kEpiBias, true>(geo.ksplit, geo.waves, geo.slots, p.G)
+                          : ksplit_kernel_epi<kEpiNone, true>(geo.ksplit, geo.waves, geo.slots, p.G);
         } else if (p.gate) {
             fn = ksplit_kernel_epi<kEpiGlu>(geo.ksplit, geo.waves, geo.slots, p.G);
         } else if (p.bias) {
@@ -1094,7 +1113,9 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     if (fused && ncols != 1) return Q4K_EINVAL;
     if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
     const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
-    const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0;
+    // (batched: every channel's and sample's activation 16-byte aligned too)
+    const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0 &&
+                         (!bl || (bl->bt.x_channel % 4 == 0 && bl->bt.x_sample % 4 == 0));
     Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused, mats, f32_vec, !x && y);
     if ((bl || fused) && !geo.ksplit) {  // the batched and fused tile variants: 1 or 2 slots, prologue 0 or 1
         if (fused != kFusedGate) geo.R = 1;

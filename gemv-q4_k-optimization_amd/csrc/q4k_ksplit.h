@@ -197,9 +197,12 @@ __device__ __forceinline__ float ks_epilogue(const GemvParams &p, int row, const
 // the fused epilogue (kEpiBias: dst = product + bias; kEpiGlu: each step
 // also loads the same rows of the gate weight p.gate, and dst = glu(product
 // + bias, gate product + gate bias); kernels/mmvq.cu:254-262, :309-336).
-// Rows: the workgroup's share (rows_base / rows_extra, as the tile kernel),
-// tiles of TR rows split contiguously over the teams.
-template <int SBW, int WAVES, int S, int G, bool SUMS = false, int EPI = kEpiNone>
+// BATCH: one launch over dst channels (grid y) and samples (grid z), each
+// workgroup first selecting its activation and dst slice and, after its
+// activation loads, its weight matrix (batch_activation, batch_weights, as
+// the tile kernel).  Rows: the workgroup's share (rows_base / rows_extra, as
+// the tile kernel), tiles of TR rows split contiguously over the teams.
+template <int SBW, int WAVES, int S, int G, bool SUMS = false, int EPI = kEpiNone, bool BATCH = false>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;  // waves sharing a row
     constexpr int TR = 16 / SBW;  // rows per wave step
@@ -207,8 +210,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_
     constexpr int V = 4 * SBW;    // activation values per lane and group
     constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
     static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
-    static_assert(!SUMS || EPI == kEpiNone, "parity variants of the plain product only");
+    static_assert(!SUMS || (EPI == kEpiNone && !BATCH), "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    if constexpr (BATCH) batch_activation(p);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
 
@@ -247,10 +251,13 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_kernel(Q4K_GEMV_
 
     // 2. the first S tiles' weights: the workgroup's rows as one buffer, so
     //    rows past its share read zeros without memory traffic (GLU: the
-    //    same rows of the gate weight, at the same offsets)
+    //    same rows of the gate weight, at the same offsets; BATCH: of the
+    //    workgroup's weight matrix, none for an absent expert)
+    if constexpr (BATCH) batch_weights(p);
+    const uint32_t wbytes = BATCH && p.w_absent ? 0u : (uint32_t)(n * p.row_stride);
     __amdgpu_buffer_rsrc_t rsw[NW];
-    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
-    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, wbytes);
+    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, wbytes);
     const uint32_t lrow = (uint32_t)r * (uint32_t)p.row_stride;
     const uint32_t lh = lrow + (uint32_t)((SBW * slice + s) * kBlockBytes);
     const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
@@ -414,8 +421,9 @@ __device__ __forceinline__ LaneAct ks_read_lds(const uint8_t *area, int sbw, int
 
 // SBW: 1, 2 or 4 super-blocks per wave and group; GMAX: the most groups per
 // row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
-// partials); EPI: the fused epilogue, as in gemv_q4k_ksplit_kernel.
-template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone>
+// partials); EPI, BATCH: the fused epilogue and batched launches, as in
+// gemv_q4k_ksplit_kernel.
+template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone, bool BATCH = false>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
     constexpr int TR = 16 / SBW;
@@ -423,8 +431,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
     constexpr int V = 4 * SBW;
     constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
     static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
-    static_assert(!SUMS || EPI == kEpiNone, "parity variants of the plain product only");
+    static_assert(!SUMS || (EPI == kEpiNone && !BATCH), "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    if constexpr (BATCH) batch_activation(p);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
 
@@ -460,10 +469,13 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
         }
     }
 
-    // 2. the first S steps' weights (GLU: and the gate weight's)
+    // 2. the first S steps' weights (GLU: and the gate weight's; BATCH: of
+    //    the workgroup's weight matrix, none for an absent expert)
+    if constexpr (BATCH) batch_weights(p);
+    const uint32_t wbytes = BATCH && p.w_absent ? 0u : (uint32_t)(n * p.row_stride);
     __amdgpu_buffer_rsrc_t rsw[NW];
-    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
-    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, wbytes);
+    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, wbytes);
     const uint32_t lrow = (uint32_t)r * (uint32_t)p.row_stride;
     const uint32_t lh = lrow + (uint32_t)((SBW * slice + s) * kBlockBytes);
     const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
@@ -692,14 +704,29 @@ constexpr bool ksplit_long_epi_exists(int sbw, int waves, int slots, int gmax) {
     return (slots == 1 || (slots == 2 && waves <= 8)) && ksplit_long_exists(sbw, waves, slots, gmax);
 }
 
-template <int EPI>
+// The batched variants (broadcasting and MUL_MAT_ID, with or without a
+// fused epilogue): in the shapes the automatic rules pick -- 4 super-blocks
+// per wave in 4-wave workgroups, 2 in 8-wave ones (or 16 with one step in
+// flight), and for long rows also 1 in 16-wave workgroups.
+constexpr bool ksplit_batch_exists(int sbw, int waves, int slots, int G) {
+    return ksplit_epi_exists(sbw, waves, slots, G) &&
+           ((sbw == 4 && waves == 4) || (sbw == 2 && (waves == 8 || (waves == 16 && slots == 1))));
+}
+constexpr bool ksplit_long_batch_exists(int sbw, int waves, int slots, int gmax) {
+    return ksplit_long_epi_exists(sbw, waves, slots, gmax) &&
+           ((sbw == 4 && waves == 4) || (sbw == 2 && waves == 8) || (sbw == 1 && waves == 16 && slots == 1));
+}
+
+// The fused (EPI kEpiBias, kEpiGlu) or batched (BATCH; any EPI) K-split
+// kernel of a launch shape, or null.
+template <int EPI, bool BATCH = false>
 const void *ksplit_kernel_epi(int sbw, int waves, int slots, int G) {
     auto pick = [&](auto sbw_c) -> const void * {
         constexpr int B = decltype(sbw_c)::value;
         auto by = [&](auto waves_c, auto s_c, auto g_c) -> const void * {
             constexpr int W = decltype(waves_c)::value, SS = decltype(s_c)::value, GG = decltype(g_c)::value;
-            if constexpr (ksplit_epi_exists(B, W, SS, GG))
-                return reinterpret_cast<const void *>(&gemv_q4k_ksplit_kernel<B, W, SS, GG, false, EPI>);
+            if constexpr (BATCH ? ksplit_batch_exists(B, W, SS, GG) : ksplit_epi_exists(B, W, SS, GG))
+                return reinterpret_cast<const void *>(&gemv_q4k_ksplit_kernel<B, W, SS, GG, false, EPI, BATCH>);
             return nullptr;
         };
         auto by_w = [&](auto waves_c) -> const void * {
@@ -719,7 +746,7 @@ const void *ksplit_kernel_epi(int sbw, int waves, int slots, int G) {
     return nullptr;
 }
 
-template <int EPI>
+template <int EPI, bool BATCH = false>
 const void *ksplit_long_kernel_epi(int sbw, int waves, int slots, int G) {
     const int gmax = G <= 4 ? 4 : 8;
     if (G > 8) return nullptr;
@@ -727,8 +754,8 @@ const void *ksplit_long_kernel_epi(int sbw, int waves, int slots, int G) {
         constexpr int B = decltype(sbw_c)::value;
         auto by = [&](auto waves_c, auto s_c, auto g_c) -> const void * {
             constexpr int W = decltype(waves_c)::value, SS = decltype(s_c)::value, GM = decltype(g_c)::value;
-            if constexpr (ksplit_long_epi_exists(B, W, SS, GM))
-                return reinterpret_cast<const void *>(&gemv_q4k_ksplit_long_kernel<B, W, SS, GM, false, EPI>);
+            if constexpr (BATCH ? ksplit_long_batch_exists(B, W, SS, GM) : ksplit_long_epi_exists(B, W, SS, GM))
+                return reinterpret_cast<const void *>(&gemv_q4k_ksplit_long_kernel<B, W, SS, GM, false, EPI, BATCH>);
             return nullptr;
         };
         auto by_w = [&](auto waves_c) -> const void * {

@@ -151,7 +151,7 @@ static Q6Geometry pick_geometry_q6_ksplit_nc(const DeviceInfo &di, int64_t K, in
 // or 16), waves per workgroup (whole teams of TR waves; long rows: 8 or 16),
 // workgroups (default one per CU), tiles in flight (1, 2).
 static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64_t M, int rows_per_step, int waves,
-                                          int wgs, int slots, int fused = kFusedNone) {
+                                          int wgs, int slots, int fused = kFusedNone, bool batch = false) {
     Q6Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
     const bool lng = K != 4096 && K != 8192;
@@ -172,13 +172,15 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
     g.rows_base = (int)(M / g.grid);
     g.rows_extra = (int)(M % g.grid);
     const int rows = g.rows_base + (g.rows_extra ? 1 : 0);
-    // fused epilogue: the variants that exist (else ksplit = 0: the caller
-    // takes the tile kernel); with a gate two partials per (row, slice)
-    if (fused != kFusedNone) {
+    // fused epilogue or batched launch: the variants that exist (else
+    // ksplit = 0: the caller takes the tile kernel); with a gate two
+    // partials per (row, slice)
+    if (fused != kFusedNone || batch) {
         const bool glu = fused == kFusedGate;
         auto ok = [&]() {
-            return lng ? q6_ksplit_long_epi_exists(g.ksplit, g.waves, g.slots, G <= 4 ? 4 : 8, glu)
-                       : q6_ksplit_epi_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096), glu);
+            return (!batch || q6_ksplit_batch_ok(g.ksplit, g.waves)) &&
+                   (lng ? q6_ksplit_long_epi_exists(g.ksplit, g.waves, g.slots, G <= 4 ? 4 : 8, glu)
+                        : q6_ksplit_epi_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096), glu));
         };
         if (g.slots > 2 || !ok()) g.slots = 1;
         if (!ok()) g.ksplit = 0;
@@ -338,7 +340,13 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     // groups (4096 or 8192 values: activation in registers; other lengths:
     // the long-row variant); the tile kernel, whose outputs are the same
     // bits, takes the rest
-    const bool ks_ok = N == 1 && mats == 1 && f32_vec && K <= 8 * 4096;  // (fused epilogues included)
+    // (fused epilogues and batched launches included; a batched launch's
+    // workgroups per weight matrix: grid_per_matrix.  Batched, rows of 4096
+    // values or more: MUL_MAT_ID measured on MI355X, Mixtral 8x7B gate/up
+    // with SWIGLU, Q4_K, 26.61 -> 25.27 us, down, Q6_K, 22.27 -> 19.64; the
+    // 2048 x 768 Q6_K experts of a Qwen3-30B-A3B-like down 7.72 -> 7.98)
+    const bool ks_ok = N == 1 && f32_vec && K <= 8 * 4096 && (mats == 1 || K >= 4096);
+    const int cus_m = mats > 1 ? grid_per_matrix(cus, mats, M) : cus;
     // two to four columns: the several-column K-split kernel, whose outputs
     // are the bits of the tile kernel's launches (all columns in one, or
     // four two by two; not the dense layout).  Through the override only:
@@ -356,15 +364,18 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
         return pick_geometry_q6_ksplit_nc(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(), g_ovr_wgs.load(),
                                           g_ovr_slots.load(), (int)N, ksn_p);
     if (ks_ok && okern == 5) {
+        const int ow = g_ovr_wgs.load();
         const Q6Geometry gk = pick_geometry_q6_ksplit(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(),
-                                                      g_ovr_wgs.load(), g_ovr_slots.load(), fused);
+                                                      ow > 0 ? ow : (mats > 1 ? cus_m : 0), g_ovr_slots.load(), fused,
+                                                      mats > 1);
         if (gk.ksplit) return gk;
     }
     if (ks_ok && okern == 0 && g_ovr_rows.load() == 0 && g_ovr_waves.load() == 0 && g_ovr_wgs.load() == 0) {
         int tr = 0, kw = 0, ks = 0;
-        if (fused == kFusedGate ? q6_ksplit_glu_auto(K, M, cus, tr, kw, ks) : q6_ksplit_auto(K, M, cus, tr, kw, ks)) {
+        if (fused == kFusedGate ? q6_ksplit_glu_auto(K, M, cus_m, tr, kw, ks) : q6_ksplit_auto(K, M, cus_m, tr, kw, ks)) {
             const int os = g_ovr_slots.load();
-            const Q6Geometry gk = pick_geometry_q6_ksplit(di, K, M, tr, kw, 0, os >= 1 && os <= 4 ? os : ks, fused);
+            const Q6Geometry gk = pick_geometry_q6_ksplit(di, K, M, tr, kw, mats > 1 ? cus_m : 0,
+                                                          os >= 1 && os <= 4 ? os : ks, fused, mats > 1);
             if (gk.ksplit && gk.lds <= max_lds) return gk;
         }
     }
@@ -539,7 +550,9 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
     if (fused && ncols != 1) return Q4K_EINVAL;
     if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
     const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
-    const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0;
+    // (batched: every channel's and sample's activation 16-byte aligned too)
+    const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0 &&
+                         (!bl || (bl->bt.x_channel % 4 == 0 && bl->bt.x_sample % 4 == 0));
     const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats, fused, f32_vec, !x && y);
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // a wave's rows (the matrix-core kernel: a workgroup's tiles; the K-split
@@ -590,6 +603,12 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.glu_op = ep->glu_op;
         }
         const void *fn = geo.ks_nc_p  ? q6_ksplit_nc_kernel<false>(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
+                         : geo.ksplit && bl && fused == kFusedGate
+                             ? q6_ksplit_kernel_epi<kEpiGlu, true>(geo.ks_long != 0, geo.ksplit, geo.waves, geo.slots, p.G)
+                         : geo.ksplit && bl && fused == kFusedBias
+                             ? q6_ksplit_kernel_epi<kEpiBias, true>(geo.ks_long != 0, geo.ksplit, geo.waves, geo.slots, p.G)
+                         : geo.ksplit && bl
+                             ? q6_ksplit_kernel_epi<kEpiNone, true>(geo.ks_long != 0, geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.ksplit && fused == kFusedGate
                              ? q6_ksplit_kernel_epi<kEpiGlu>(geo.ks_long != 0, geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.ksplit && fused == kFusedBias
@@ -600,7 +619,7 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
                          : geo.mfma ? q6_mfma_kernel_for(nc, geo.waves)
                          : bl       ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
                                     : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
-        if (geo.ksplit && (nc != (geo.ks_nc_p ? geo.nc_chunk : 1) || (fused && geo.ks_nc_p) || bl || !p.x || !p.vec_ok))
+        if (geo.ksplit && (nc != (geo.ks_nc_p ? geo.nc_chunk : 1) || ((fused || bl) && geo.ks_nc_p) || !p.x || !p.vec_ok))
             return Q4K_EINVAL;
         if (geo.ks_nc_p) p.ring_off = q6_ksn_stage_bytes(p.K, nc);
         if (geo.mfma) {

@@ -79,8 +79,9 @@ __device__ __forceinline__ Q6Act q6_ks_stage(const float (&v)[4 * SBW], int s, i
 // groups per row.  SUMS: the parity variant, which also stores every lane's
 // four int32 group sums.  Rows: the workgroup's share, tiles of TR rows
 // split contiguously over the teams.
-// EPI: the fused epilogue, as in the Q4_K K-split kernels (ks_epilogue).
-template <int SBW, int WAVES, int S, int G, bool SUMS = false, int EPI = kEpiNone>
+// EPI, BATCH: the fused epilogue and batched launches, as in the Q4_K
+// K-split kernels (ks_epilogue, batch_activation / batch_weights).
+template <int SBW, int WAVES, int S, int G, bool SUMS = false, int EPI = kEpiNone, bool BATCH = false>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
     constexpr int TR = 16 / SBW;
@@ -88,8 +89,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_
     constexpr int V = 4 * SBW;
     constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
     static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
-    static_assert(!SUMS || EPI == kEpiNone, "parity variants of the plain product only");
+    static_assert(!SUMS || (EPI == kEpiNone && !BATCH), "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    if constexpr (BATCH) batch_activation(p);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
 
@@ -123,10 +125,13 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_kernel(Q4K_GEMV_
         }
     }
 
-    // 2. the first S tiles' weights (GLU: and the gate weight's, at the same offsets)
+    // 2. the first S tiles' weights (GLU: and the gate weight's, at the same
+    //    offsets; BATCH: of the workgroup's weight matrix, none if absent)
+    if constexpr (BATCH) batch_weights(p);
+    const uint32_t wbytes = BATCH && p.w_absent ? 0u : (uint32_t)(n * p.row_stride);
     __amdgpu_buffer_rsrc_t rsw[NW];
-    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
-    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, wbytes);
+    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, wbytes);
     Q6Lane ln;
     ln.lane = lane;
     ln.g = SBW * slice + s;
@@ -270,7 +275,7 @@ __device__ __forceinline__ Q6Act q6_ks_read_lds(const uint8_t *area, int sbw, in
 // SBW: 1, 2 or 4 super-blocks per wave and group; GMAX: the most groups per
 // row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
 // partials).
-template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone>
+template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone, bool BATCH = false>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
     constexpr int TR = 16 / SBW;
@@ -278,8 +283,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
     constexpr int V = 4 * SBW;
     constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
     static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
-    static_assert(!SUMS || EPI == kEpiNone, "parity variants of the plain product only");
+    static_assert(!SUMS || (EPI == kEpiNone && !BATCH), "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    if constexpr (BATCH) batch_activation(p);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
 
@@ -315,10 +321,13 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
         }
     }
 
-    // 2. the first S steps' weights (GLU: and the gate weight's)
+    // 2. the first S steps' weights (GLU: and the gate weight's; BATCH: of
+    //    the workgroup's weight matrix, none if absent)
+    if constexpr (BATCH) batch_weights(p);
+    const uint32_t wbytes = BATCH && p.w_absent ? 0u : (uint32_t)(n * p.row_stride);
     __amdgpu_buffer_rsrc_t rsw[NW];
-    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
-    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    rsw[0] = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, wbytes);
+    if constexpr (NW == 2) rsw[NW - 1] = make_rsrc(p.gate + (int64_t)wg_beg * p.row_stride, wbytes);
     Q6Lane ln;
     ln.lane = lane;
     ln.g = SBW * slice + s;  // the lane's super-block within each group
@@ -518,9 +527,14 @@ constexpr bool q6_ksplit_long_epi_exists(int sbw, int waves, int slots, int gmax
            q6_ksplit_long_exists(sbw, waves, slots, gmax);
 }
 
-// The fused Q6_K K-split kernel (rows of 1 or 2 groups, long = false; any
-// other length up to 8 groups, long = true) of a launch shape, or null.
-template <int EPI>
+// The batched variants: in the shapes the automatic rules pick (4
+// super-blocks per wave in 4-wave workgroups, 2 in 8-wave ones).
+constexpr bool q6_ksplit_batch_ok(int sbw, int waves) { return (sbw == 4 && waves == 4) || (sbw == 2 && waves == 8); }
+
+// The fused (EPI kEpiBias, kEpiGlu) or batched (BATCH; any EPI) Q6_K K-split
+// kernel (rows of 1 or 2 groups, long = false; any other length up to 8
+// groups, long = true) of a launch shape, or null.
+template <int EPI, bool BATCH = false>
 const void *q6_ksplit_kernel_epi(bool lng, int sbw, int waves, int slots, int G) {
     const int gsel = lng ? (G <= 4 ? 4 : 8) : G;
     if (lng ? G > 8 : (G != 1 && G != 2)) return nullptr;
@@ -529,11 +543,15 @@ const void *q6_ksplit_kernel_epi(bool lng, int sbw, int waves, int slots, int G)
         auto by = [&](auto waves_c, auto s_c, auto g_c) -> const void * {
             constexpr int W = decltype(waves_c)::value, SS = decltype(s_c)::value, GG = decltype(g_c)::value;
             if constexpr (GG <= 2) {
-                if constexpr (q6_ksplit_epi_exists(B, W, SS, GG, EPI == kEpiGlu))
-                    if (!lng) return reinterpret_cast<const void *>(&gemv_q6k_ksplit_kernel<B, W, SS, GG, false, EPI>);
+                if constexpr (q6_ksplit_epi_exists(B, W, SS, GG, EPI == kEpiGlu) && (!BATCH || q6_ksplit_batch_ok(B, W)))
+                    if (!lng)
+                        return reinterpret_cast<const void *>(&gemv_q6k_ksplit_kernel<B, W, SS, GG, false, EPI, BATCH>);
             } else {
-                if constexpr (q6_ksplit_long_epi_exists(B, W, SS, GG, EPI == kEpiGlu))
-                    if (lng) return reinterpret_cast<const void *>(&gemv_q6k_ksplit_long_kernel<B, W, SS, GG, false, EPI>);
+                if constexpr (q6_ksplit_long_epi_exists(B, W, SS, GG, EPI == kEpiGlu) &&
+                              (!BATCH || q6_ksplit_batch_ok(B, W)))
+                    if (lng)
+                        return reinterpret_cast<const void *>(
+                            &gemv_q6k_ksplit_long_kernel<B, W, SS, GG, false, EPI, BATCH>);
             }
             return nullptr;
         };

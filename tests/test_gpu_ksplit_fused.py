@@ -122,3 +122,58 @@ def test_ksplit_fused_automatic_choice(Q, gpu, M, K):
     y_a = Q.mul_mat_vec_q_fused(wud, K, xa, gate=wgd, glu_op=2).cpu().numpy()
     y_u = Q.mul_mat_vec_q_fused(wud, K, xb[:, 1:K + 1], gate=wgd, glu_op=2).cpu().numpy()
     assert np.array_equal(y_a, y_u)
+
+
+def _tensor(Q, t, ne, nb, ptr):
+    return Q.make_tensor(t, list(ne), list(nb), ptr)
+
+
+@pytest.mark.parametrize("wtype", [Q4, Q6])
+@pytest.mark.parametrize("M,K,fuse", [(14336, 4096, False), (14336, 4096, True), (4096, 14336, False),
+                                      (1024, 8192, True), (3000, 11008, True)])
+def test_ksplit_batched_mul_mat_id_bits_equal_tile_kernel(Q, gpu, wtype, M, K, fuse):
+    """MUL_MAT_ID for one token (three experts, slots using two of them, one
+    twice, and an absent id), with and without the gate weight and SWIGLU:
+    the automatic launch (the batched K-split kernels) and a forced
+    8-row, 8-wave K-split launch against the batched tile kernel, bit for
+    bit; the absent expert's slot reads no weight."""
+    import ctypes
+    import torch
+    BB = {Q4: 144, Q6: 210}
+    nexp = 3
+    ids = np.array([2, 0, 2, 7], np.int32)
+    nused = len(ids)
+    wu = np.stack([weights(Q, M, K, 60 + e, wtype) for e in range(nexp)])
+    wg = np.stack([weights(Q, M, K, 70 + e, wtype) for e in range(nexp)]) if fuse else None
+    x = _common.activations(1, K, seed=61)
+    wud, xd, idd = to_dev(wu, gpu), to_dev(x, gpu), to_dev(ids, gpu)
+    wgd = to_dev(wg, gpu) if fuse else None
+    rb = wu.shape[-1]
+    s0 = _tensor(Q, wtype, (K, M, nexp), (BB[wtype], rb, rb * M), wud.data_ptr())
+    s1 = _tensor(Q, 0, (K, 1, 1), (4, 4 * K, 4 * K), xd.data_ptr())
+    ti = _tensor(Q, 26, (nused, 1), (4, 4 * nused), idd.data_ptr())
+    fa = None
+    if fuse:
+        sg = _tensor(Q, wtype, (K, M, nexp), (BB[wtype], rb, rb * M), wgd.data_ptr())
+        fa = Q.q4k_fusion_args(None, ctypes.pointer(sg), None, Q.GLU_OP_SWIGLU)
+
+    def run(**ovr):
+        dst = torch.full((nused, M), 7.0, dtype=torch.float32, device=gpu)
+        d = _tensor(Q, 0, (M, nused, 1), (4, 4 * M, 4 * M * nused), dst.data_ptr())
+        try:
+            Q.set_geometry_override(**ovr)
+            assert Q.ggml_mul_mat_vec_q(s0, s1, d, ids=ti, fusion=fa) == Q.Q4K_OK
+        finally:
+            Q.set_geometry_override()
+        return dst.cpu().numpy()
+
+    y_tile = run(kernel=1)
+    assert np.array_equal(y_tile[0], y_tile[2])
+    expect_absent = 0.0  # no weight bytes: zero products (SWIGLU of 0 and 0 is 0)
+    assert (y_tile[3] == expect_absent).all()
+    for ovr in ({}, {"rows_per_tile": 8, "waves_per_wg": 8, "kernel": 5}):
+        y = run(**ovr)
+        if not np.array_equal(y, y_tile):
+            bad = np.argwhere(y != y_tile)
+            raise AssertionError(f"type {wtype} {M}x{K} fuse {fuse} {ovr}: {len(bad)} outputs differ from the "
+                                 f"tile kernel, e.g. (slot, row) {bad[:5].tolist()}")
