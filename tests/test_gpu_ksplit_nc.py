@@ -355,3 +355,23 @@ def test_q6k_ksplit_nc_sums_exact(Q, O, gpu, M, K, N):
         assert torch.equal(y, y_prod), where
         got = s16[:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
         assert np.array_equal(got, ref["s16"]), f"{where}: group sums differ"
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 2), (1000, 14336, 3), (28672, 8192, 4)])
+def test_ksplit_nc_unaligned_activation_same_bits(Q, gpu, M, K, N):
+    """An activation that is not 16-byte aligned cannot take the K-split
+    kernels (16-byte loads): the op runs the tile kernel there, whose
+    outputs are the same bits as the automatic (K-split) launch on an
+    aligned copy of the same values."""
+    import torch
+    assert Q.geometry(K, M, N)["kernel"] == 5
+    wq, x = inputs(Q, M, K, N, seed=101 + N)
+    wd = to_dev(wq, gpu)
+    xa = to_dev(x, gpu)
+    xb = torch.zeros((N, K + 4), dtype=torch.float32, device=gpu)
+    xb[:, 1:K + 1] = xa
+    xu = xb[:, 1:K + 1]  # 4-byte aligned, not 16
+    assert xu.data_ptr() % 16 != 0
+    y_aligned = Q.mul_mat_vec_q(wd, K, xa).cpu().numpy()
+    y_unaligned = Q.mul_mat_vec_q(wd, K, xu).cpu().numpy()
+    assert np.array_equal(y_aligned, y_unaligned)
