@@ -38,7 +38,8 @@ def build(verbose: bool = False, save_temps: bool = False) -> str:
     host_obj = os.path.join(BUILD, "q4k_quantize_host.o")
     # the device sources compile in parallel (each instantiates many kernels)
     dev_objs, procs = [], []
-    for src in ("q4k_gemv.hip", "q6k_gemv.hip", "q4k_sums.hip", "q6k_sums.hip", "q4k_probe.hip"):
+    for src in ("q4k_gemv.hip", "q6k_gemv.hip", "q4k_sums.hip", "q6k_sums.hip", "q4k_short.hip", "q6k_short.hip",
+                "q4k_probe.hip"):
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
         cmd = [hipcc, f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
                # no packed-FP32 instructions in device code

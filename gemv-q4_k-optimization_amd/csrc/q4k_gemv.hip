@@ -203,6 +203,7 @@ struct Geometry {
     int ks_long = 0;    // K-split kernel for rows of any length (activation slices in LDS)
     int ks_staged = 0;  // several-column K-split kernel: activation quantised once per workgroup into LDS
     int ks_p = 0;       // several-column K-split kernel: columns of its reduction tree (2 or 4)
+    int ks_kt = 0;      // long-row K-split kernel, rows shorter than one group: waves per team (0: 16/SBW)
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
@@ -380,11 +381,23 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
     if (lng && g.ksplit > (G <= 4 ? 4 : 2)) g.ksplit = G <= 4 ? 4 : 2;
     g.R = 16 / g.ksplit;
     g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
-    if (g.waves < g.R) g.waves = g.R;
     g.slots = slots >= 1 && slots <= 4 ? slots : 1;
-    if (lng ? !ksplit_long_exists(g.ksplit, g.waves, g.slots, gmax)
-            : !ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096)))
-        g.slots = 2;
+    // rows shorter than one group: teams of only the waves the row needs,
+    // where that variant is instantiated (else the whole team)
+    const int epi = fused == kFusedGate ? kEpiGlu : (fused == kFusedBias ? kEpiBias : kEpiNone);
+    int kt = lng ? ksplit_short_team((int)(K / kQK), g.ksplit) : 0;
+    if (kt) {
+        if (g.waves < kt) g.waves = kt;
+        if (!ksplit_short_exists(false, g.ksplit, kt, g.waves, g.slots, false, epi, batch)) g.slots = 1;
+        if (!ksplit_short_exists(false, g.ksplit, kt, g.waves, g.slots, false, epi, batch)) kt = 0;
+    }
+    g.ks_kt = kt;
+    if (!kt) {
+        if (g.waves < g.R) g.waves = g.R;
+        if (lng ? !ksplit_long_exists(g.ksplit, g.waves, g.slots, gmax)
+                : !ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096)))
+            g.slots = 2;
+    }
     int64_t grid = wgs > 0 ? wgs : cus;
     if (grid > M) grid = M;
     g.grid = grid < 1 ? 1 : (int)grid;
@@ -394,7 +407,7 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
     // fused epilogue or batched launch: the variants that exist (else
     // ksplit = 0: the caller takes the tile kernel); with a gate two
     // partials per (row, slice)
-    if (fused || batch) {
+    if ((fused || batch) && !kt) {
         const int gk = lng ? gmax : (int)(K / 4096);
         auto ok = [&]() {
             return batch ? (lng ? ksplit_long_batch_exists(g.ksplit, g.waves, g.slots, gk)
@@ -406,7 +419,7 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
         if (!ok()) g.ksplit = 0;
     }
     const int nw = fused == kFusedGate ? 2 : 1;
-    g.lds = lng ? ksplit_long_lds_bytes(rows, g.ksplit ? g.ksplit : 1, g.waves, G, nw)
+    g.lds = lng ? ksplit_long_lds_bytes(rows, g.ksplit ? g.ksplit : 1, g.waves, G, nw, kt)
                 : ksplit_lds_bytes(rows, g.ksplit ? g.ksplit : 1, nw);
     g.lds_launch = g.lds;
     g.nc_chunk = 1;
@@ -450,9 +463,21 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //    32000 x 5120 19.32 / 19.77, 18944 x 3584 9.17 / 9.42, 11008 x 2048
 //    5.44 / 5.46), the tile kernel otherwise (5120 x 13824, 20 rows per CU:
 //    10.23 against 9.50) and over 160 rows per CU (not measured).
+//  - rows of 3 to 8 blocks (768 .. 2048 values; the long-row kernel with
+//    teams of only the waves a row needs): 8 rows per step, one step in
+//    flight, 4 waves up to 16 rows per CU (512 x 2048 2.60 against 2.88 on
+//    the tile kernel, 2048 x 2048 2.81 / 3.15, 4096 x 1024 2.85 / 3.64,
+//    1024 x 768 2.51 / 2.81), 8 up to 24 (6144 x 2048 3.84 / 4.40), 16
+//    beyond (8960 x 1536 4.13 / 4.90, 16384 x 2048 5.37 / 6.69, 8192 x 2048
+//    4.22 / 4.72, 32768 x 2048 8.57 / 9.74, 128256 x 2048 26.44 / 30.31).
 static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
+    if (ksplit_short_rows(K)) {
+        tr = 8;
+        waves = rho <= 16 ? 4 : (rho <= 24 ? 8 : 16);
+        return true;
+    }
     if (K != 4096 && K != 8192) {
         if (rho <= 4 && K <= 4 * 4096) {
             tr = waves = 4;
@@ -504,11 +529,19 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
 // waves 10.94 there, 13.98 at 14336 rows); 8192 values 4 rows, 4 waves, one
 // tile (28672 x 8192 45.05 / 48.40); other lengths 8 rows, 8 waves, one step
 // (4096 x 14336 13.96 / 17.40).  Rows of 4096 values or more, up to 160
-// rows per CU: the range measured.
+// rows per CU: the range measured; rows of 3 to 8 blocks (short teams) 8
+// rows per step, 4 waves up to 16 rows per CU, else 8 (2048 x 2048 3.53 /
+// 3.97, 5632 x 2048 4.85 / 6.27, 6144 x 2048 5.13 / 6.32, 8192 x 2048 5.93
+// / 7.46; MUL_MAT_ID of eight 768 x 2048 experts 5.09 / 6.62).
 static bool ksplit_glu_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
-    if (rho > 160 || K < 4096) return false;  // (shorter rows: not measured)
     slots = 1;
+    if (ksplit_short_rows(K)) {
+        tr = 8;
+        waves = rho <= 16 ? 4 : 8;
+        return true;
+    }
+    if (rho > 160 || K < 4096) return false;  // (other rows under 4096 values: not measured)
     if (K == 4096) {
         if (rho <= 16) {
             tr = waves = 8;
@@ -641,10 +674,13 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     // bits, takes the rest
     // (fused epilogues and batched launches included; a batched launch's
     // workgroups per weight matrix: grid_per_matrix.  Batched, rows of 4096
-    // values or more: MUL_MAT_ID measured on MI355X, Mixtral 8x7B gate/up
-    // with SWIGLU, Q4_K, 26.61 -> 25.27 us, down, Q6_K, 22.27 -> 19.64; the
-    // 2048 x 768 Q6_K experts of a Qwen3-30B-A3B-like down 7.72 -> 7.98)
-    const bool ks_ok = N == 1 && f32_vec && K <= 8 * 4096 && (mats == 1 || K >= 4096);
+    // values or more and rows of 3 to 8 blocks (short teams): MUL_MAT_ID
+    // measured on MI355X, Mixtral 8x7B gate/up with SWIGLU, Q4_K, 26.61 ->
+    // 25.27 us, down, Q6_K, 22.27 -> 19.64; Qwen3-30B-A3B-like gate/up 6.62
+    // -> 5.09, down 7.73 -> 4.43; other lengths under 4096 values not
+    // measured)
+    const bool ks_ok = N == 1 && f32_vec && K <= 8 * 4096 &&
+                       (mats == 1 || K >= 4096 || okern == 5 || ksplit_short_rows(K));
     const int cus_m = mats > 1 ? grid_per_matrix(cus, mats, M) : cus;
     // two to four columns: the K-split kernel for rows of 1 or 2 groups
     // (the tile kernel's launches, whose bits these are: all columns in one,
@@ -666,7 +702,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
             const int os = g_ovr_slots.load();
             const Geometry gk = pick_geometry_ksplit(di, K, M, tr, kw, mats > 1 ? cus_m : 0,
                                                      os >= 1 && os <= 4 ? os : ks, 1, 0, 0, fused, mats > 1);
-            if (gk.ksplit && gk.lds <= max_lds) return gk;
+            if (gk.ksplit && gk.lds <= max_lds && (mats == 1 || K >= 4096 || gk.ks_kt)) return gk;
         }
     }
     if (ksn_ok && okern == 0 && orows == 0 && owaves == 0 && owgs == 0) {
@@ -1008,6 +1044,12 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
                 fn = p.sums ? q4k_ksplit_nc_sums_kernel(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0)
                             : ksplit_nc_kernel<false>(nc, geo.ksplit, geo.waves, geo.slots, p.G, geo.ks_staged != 0);
             p.ring_off = geo.ks_staged ? ksn_stage_bytes(p.K, nc) : 0;
+        } else if (geo.ks_long && geo.ks_kt) {
+            const int epi = p.gate ? kEpiGlu : (p.bias ? kEpiBias : kEpiNone);
+            fn = q4k_ksplit_short_kernel(geo.ksplit, geo.ks_kt, geo.waves, geo.slots, p.sums != nullptr, epi, batch);
+            p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit,
+                                                p.gate ? 2 : 1, geo.ks_kt);
+            p.rpw = 1;
         } else if (geo.ks_long) {
             if (batch)
                 fn = p.gate   ? ksplit_long_kernel_epi<kEpiGlu, true>(geo.ksplit, geo.waves, geo.slots, p.G)

@@ -423,14 +423,23 @@ __device__ __forceinline__ LaneAct ks_read_lds(const uint8_t *area, int sbw, int
 // row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
 // partials); EPI, BATCH: the fused epilogue and batched launches, as in
 // gemv_q4k_ksplit_kernel.
-template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone, bool BATCH = false>
+// KT (rows shorter than one group, GMAX = 1): waves per team, 0 for the
+// whole KW = 16/SBW.  A team of KT < KW waves covers the super-blocks [0,
+// SBW*KT), which hold the row's nb; the slices it leaves out would hold
+// only super-blocks past the row, whose tile-kernel sums are exact zeros,
+// so the tree over the KW slice sums takes +0 there and the bits stay the
+// tile kernel's.
+template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone, bool BATCH = false,
+          int KT = 0>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
+    constexpr int KS = KT > 0 ? KT : KW;  // slices a team computes
     constexpr int TR = 16 / SBW;
-    constexpr int TEAMS = WAVES / KW;
+    constexpr int TEAMS = WAVES / KS;
     constexpr int V = 4 * SBW;
     constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
-    static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    static_assert(TEAMS >= 1 && WAVES % KS == 0, "whole teams");
+    static_assert(KS <= KW && (KS == KW || GMAX == 1), "short teams for rows of one partial group only");
     static_assert(!SUMS || (EPI == kEpiNone && !BATCH), "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     if constexpr (BATCH) batch_activation(p);
@@ -439,7 +448,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int slice = wave % KW, team = wave / KW;
+    const int slice = wave % KS, team = wave / KS;
     const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1), j = lane & 3;
     const int G = p.G;
 
@@ -566,7 +575,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
 #pragma unroll
                     for (int u = 0; u < NW; ++u) {
                         const float q = ks_reduce<SBW>(acc[u]);
-                        if (wr) part[(rl * NW + u) * KW + slice] = q;
+                        if (wr) part[(rl * NW + u) * KS + slice] = q;
                         acc[u] = 0.0f;
                     }
                 }
@@ -584,7 +593,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
         for (int u = 0; u < NW; ++u) {
             float q[KW];
 #pragma unroll
-            for (int k = 0; k < KW; ++k) q[k] = part[(row * NW + u) * KW + k];
+            for (int k = 0; k < KW; ++k) q[k] = k < KS ? part[(row * NW + u) * KS + k] : 0.0f;
 #pragma unroll
             for (int h = KW / 2; h >= 1; h /= 2)
 #pragma unroll
@@ -597,11 +606,30 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
 
 // LDS bytes of a long-row K-split launch: the partials, padded to 16 bytes,
 // then every wave's slice of every group (nw: 2 with a gate weight).
-__host__ __device__ constexpr int ksplit_long_part_bytes(int rows_per_wg, int sbw, int nw = 1) {
-    return (ksplit_lds_bytes(rows_per_wg, sbw, nw) + 15) / 16 * 16;
+// (kt: waves per team, 0 for 16/sbw).
+__host__ __device__ constexpr int ksplit_long_part_bytes(int rows_per_wg, int sbw, int nw = 1, int kt = 0) {
+    return (rows_per_wg * (kt > 0 ? kt : 16 / sbw) * 4 * nw + 15) / 16 * 16;
 }
-__host__ __device__ constexpr int ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G, int nw = 1) {
-    return ksplit_long_part_bytes(rows_per_wg, sbw, nw) + waves * G * ks_slice_bytes(sbw);
+__host__ __device__ constexpr int ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G, int nw = 1,
+                                                        int kt = 0) {
+    return ksplit_long_part_bytes(rows_per_wg, sbw, nw, kt) + waves * G * ks_slice_bytes(sbw);
+}
+
+// Rows of 3 to 8 super-blocks (K = 768 .. 2048 values): the rows the
+// short-team variants serve.
+__host__ __device__ constexpr bool ksplit_short_rows(int64_t K) {
+    return K % 256 == 0 && K >= 3 * 256 && K <= 8 * 256;
+}
+
+// Waves per team of the long-row kernel for rows of nb super-blocks at sbw
+// per wave: for rows shorter than one group the fewest that cover the row,
+// rounded up to a power of two; 0 (the whole 16/sbw) otherwise or where that
+// is no fewer.
+__host__ __device__ constexpr int ksplit_short_team(int nb, int sbw) {
+    if (nb >= 16 || sbw <= 0) return 0;
+    int kt = 1;
+    while (kt * sbw < nb) kt *= 2;
+    return kt < 16 / sbw ? kt : 0;
 }
 
 // The instantiated K-split variants: whole teams per workgroup; two groups
@@ -689,6 +717,21 @@ const void *ksplit_long_kernel(int sbw, int waves, int slots, int G) {
     if (sbw == 2) return pick(std::integral_constant<int, 2>{});
     if (sbw == 4) return pick(std::integral_constant<int, 4>{});
     return nullptr;
+}
+
+// The short-team variants of the long-row kernel (rows of one partial group;
+// q4k_short.hip): (SBW, KT) = (1, 4), (1, 8), (2, 2), (2, 4), (4, 1),
+// (4, 2), the teams of rows of 3 to 8 super-blocks; q6: the Q6_K kernel.
+constexpr bool ksplit_short_exists(bool q6, int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
+    const bool shape = ((sbw == 1 && (kt == 4 || kt == 8)) || (sbw == 2 && (kt == 2 || kt == 4)) ||
+                        (sbw == 4 && (kt == 1 || kt == 2))) &&
+                       (waves == 4 || waves == 8 || waves == 16) && waves % kt == 0 && (slots == 1 || slots == 2);
+    if (!shape) return false;
+    if (sums) return !batch && epi == kEpiNone;
+    if (epi == kEpiNone && !batch) return true;
+    // fused and batched: one step in flight (a gate weight at 16 waves
+    // spills the Q6_K kernel's registers)
+    return slots == 1 && !(q6 && epi == kEpiGlu && waves == 16);
 }
 
 // The fused-epilogue variants (EPI = kEpiBias or kEpiGlu), in the shapes of

@@ -90,6 +90,13 @@ const void *q6k_ksplit_nc_sums_kernel(int nc, int p, int sbw, int waves, int slo
 const void *q6k_mfma_ga_sums_kernel(int nc, int waves);
 const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense);
 
+// The long-row K-split kernels with short teams (q4k_short.hip): the variant
+// of the launch shape and kind given (sums: the parity variant; epi:
+// kEpiNone, kEpiBias, kEpiGlu; batch: broadcasting / MUL_MAT_ID), or null
+// where ksplit_short_exists says it is not instantiated.
+const void *q4k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch);
+const void *q6k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch);
+
 // Q6_K weight checks and launch (q6k_gemv.hip), for the type-dispatching
 // entry points of q4k_gemv.hip.
 int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01);

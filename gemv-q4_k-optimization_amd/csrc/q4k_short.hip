@@ -1,0 +1,85 @@
+// q4k_short.hip -- the long-row K-split kernels (one F32 column) with short
+// teams, for rows of 3 to 8 super-blocks (K = 768 .. 2048 values): a team
+// of KW = 16/SBW waves would leave the waves past the row's super-blocks
+// without work, so a team is only as many waves as the row needs
+// (ksplit_short_team).  Instantiated in translation units of
+// their own (this one with Q6 = false for Q4_K, q6k_short.hip for Q6_K), in
+// the shapes ksplit_short_exists lists: plain, parity (SUMS), fused (bias;
+// gate weight + GLU) and batched launches.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "q4k_ksplit.h"
+#include "q4k_runtime.h"
+#include "q6k_ksplit.h"
+
+namespace q4k {
+namespace {
+
+template <bool Q6, int SBW, int KT, int W, int S, bool SUMS, int EPI, bool BATCH>
+const void *short_sym() {
+    if constexpr (ksplit_short_exists(Q6, SBW, KT, W, S, SUMS, EPI, BATCH)) {
+        if constexpr (Q6)
+            return reinterpret_cast<const void *>(&gemv_q6k_ksplit_long_kernel<SBW, W, S, 1, SUMS, EPI, BATCH, KT>);
+        else
+            return reinterpret_cast<const void *>(&gemv_q4k_ksplit_long_kernel<SBW, W, S, 1, SUMS, EPI, BATCH, KT>);
+    }
+    return nullptr;
+}
+
+template <bool Q6, int SBW, int KT, int W, int S>
+const void *short_by_kind(bool sums, int epi, bool batch) {
+    if (sums) return (epi == kEpiNone && !batch) ? short_sym<Q6, SBW, KT, W, S, true, kEpiNone, false>() : nullptr;
+    switch (epi) {
+        case kEpiNone:
+            return batch ? short_sym<Q6, SBW, KT, W, S, false, kEpiNone, true>()
+                         : short_sym<Q6, SBW, KT, W, S, false, kEpiNone, false>();
+        case kEpiBias:
+            return batch ? short_sym<Q6, SBW, KT, W, S, false, kEpiBias, true>()
+                         : short_sym<Q6, SBW, KT, W, S, false, kEpiBias, false>();
+        case kEpiGlu:
+            return batch ? short_sym<Q6, SBW, KT, W, S, false, kEpiGlu, true>()
+                         : short_sym<Q6, SBW, KT, W, S, false, kEpiGlu, false>();
+        default: return nullptr;
+    }
+}
+
+template <bool Q6, int SBW, int KT>
+const void *short_by_shape(int waves, int slots, bool sums, int epi, bool batch) {
+    auto by_s = [&](auto w_c) -> const void * {
+        constexpr int W = decltype(w_c)::value;
+        if (slots == 1) return short_by_kind<Q6, SBW, KT, W, 1>(sums, epi, batch);
+        if (slots == 2) return short_by_kind<Q6, SBW, KT, W, 2>(sums, epi, batch);
+        return nullptr;
+    };
+    if (waves == 4) return by_s(std::integral_constant<int, 4>{});
+    if (waves == 8) return by_s(std::integral_constant<int, 8>{});
+    if (waves == 16) return by_s(std::integral_constant<int, 16>{});
+    return nullptr;
+}
+
+template <bool Q6>
+const void *short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
+    if (sbw == 1 && kt == 4) return short_by_shape<Q6, 1, 4>(waves, slots, sums, epi, batch);
+    if (sbw == 1 && kt == 8) return short_by_shape<Q6, 1, 8>(waves, slots, sums, epi, batch);
+    if (sbw == 2 && kt == 2) return short_by_shape<Q6, 2, 2>(waves, slots, sums, epi, batch);
+    if (sbw == 2 && kt == 4) return short_by_shape<Q6, 2, 4>(waves, slots, sums, epi, batch);
+    if (sbw == 4 && kt == 1) return short_by_shape<Q6, 4, 1>(waves, slots, sums, epi, batch);
+    if (sbw == 4 && kt == 2) return short_by_shape<Q6, 4, 2>(waves, slots, sums, epi, batch);
+    return nullptr;
+}
+
+}  // namespace
+
+#ifndef Q4K_SHORT_Q6
+const void *q4k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
+    return short_kernel<false>(sbw, kt, waves, slots, sums, epi, batch);
+}
+#else
+const void *q6k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
+    return short_kernel<true>(sbw, kt, waves, slots, sums, epi, batch);
+}
+#endif
+
+}  // namespace q4k

@@ -99,6 +99,7 @@ struct Q6Geometry {
     int ks_long = 0; // K-split kernel for rows of any length (activation slices in LDS)
     int mfma_ga = 0; // matrix-core kernel: A operand from the Q8_1 buffer (pre-quantised route)
     int ks_nc_p = 0; // several-column K-split kernel: columns of its reduction tree (2 or 4; 0: not it)
+    int ks_kt = 0;   // long-row K-split kernel, rows shorter than one group: waves per team (0: 16/SBW)
 };
 
 // Columns per launch of the tile kernel for N columns of K values (halved
@@ -161,11 +162,23 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
     if (lng && g.ks_tr == 4 && G > 4) g.ks_tr = 8;  // 4 rows per step: rows of up to 4 groups
     g.ksplit = 16 / g.ks_tr;
     g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
-    if (g.waves < g.ks_tr) g.waves = g.ks_tr;
     g.slots = slots >= 1 && slots <= (lng ? 4 : 2) ? slots : 1;
-    if (lng ? !q6_ksplit_long_exists(g.ksplit, g.waves, g.slots, G <= 4 ? 4 : 8)
-            : !q6_ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096)))
-        g.slots = lng ? 2 : 1;
+    // rows shorter than one group: teams of only the waves the row needs,
+    // where that variant is instantiated (else the whole team)
+    const int epi = fused == kFusedGate ? kEpiGlu : (fused == kFusedBias ? kEpiBias : kEpiNone);
+    int kt = lng ? ksplit_short_team((int)(K / kQK), g.ksplit) : 0;
+    if (kt) {
+        if (g.waves < kt) g.waves = kt;
+        if (!ksplit_short_exists(true, g.ksplit, kt, g.waves, g.slots, false, epi, batch)) g.slots = 1;
+        if (!ksplit_short_exists(true, g.ksplit, kt, g.waves, g.slots, false, epi, batch)) kt = 0;
+    }
+    g.ks_kt = kt;
+    if (!kt) {
+        if (g.waves < g.ks_tr) g.waves = g.ks_tr;
+        if (lng ? !q6_ksplit_long_exists(g.ksplit, g.waves, g.slots, G <= 4 ? 4 : 8)
+                : !q6_ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096)))
+            g.slots = lng ? 2 : 1;
+    }
     int64_t grid = wgs > 0 ? wgs : cus;
     if (grid > M) grid = M;
     g.grid = grid < 1 ? 1 : (int)grid;
@@ -175,7 +188,7 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
     // fused epilogue or batched launch: the variants that exist (else
     // ksplit = 0: the caller takes the tile kernel); with a gate two
     // partials per (row, slice)
-    if (fused != kFusedNone || batch) {
+    if ((fused != kFusedNone || batch) && !kt) {
         const bool glu = fused == kFusedGate;
         auto ok = [&]() {
             return (!batch || q6_ksplit_batch_ok(g.ksplit, g.waves)) &&
@@ -187,7 +200,7 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
     }
     const int nw = fused == kFusedGate ? 2 : 1;
     const int sbw = g.ksplit ? g.ksplit : 1;
-    g.lds = lng ? q6_ksplit_long_lds_bytes(rows, sbw, g.waves, G, nw) : ksplit_lds_bytes(rows, sbw, nw);
+    g.lds = lng ? q6_ksplit_long_lds_bytes(rows, sbw, g.waves, G, nw, kt) : ksplit_lds_bytes(rows, sbw, nw);
     g.lds_launch = g.lds;
     g.nc_chunk = 1;
     return g;
@@ -213,9 +226,19 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
 // and 4 groups (1024 x 14336 6.26 against 6.32); three or four steps in
 // flight, 16 waves or two workgroups per CU measured slower (4096 x 14336
 // 13.29, 13.32, 13.34, 13.12 against 12.10).
+// Rows of 3 to 8 blocks (768 .. 2048 values; short teams): 8 rows per
+// step, one step in flight, 4 waves up to 16 rows per CU (2048 x 768 2.88
+// against 3.49 on the tile kernel, 2048 x 2048 3.16 / 3.65), 8 beyond
+// (16384 x 768 4.68 / 9.40, 128256 x 2048 38.75 / 57.98; MUL_MAT_ID of
+// eight 2048 x 768 experts 4.43 / 7.73).
 static bool q6_ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
+    if (ksplit_short_rows(K)) {
+        tr = 8;
+        waves = rho <= 16 ? 4 : 8;
+        return true;
+    }
     if (K != 4096 && K != 8192) {
         const bool small = rho <= 4 && K <= 4 * 4096;
         tr = waves = small ? 4 : 8;
@@ -324,6 +347,7 @@ static Q6Geometry pick_geometry_q6_mfma(const DeviceInfo &di, int64_t K, int64_t
 // 14336 21.94 / 23.63).  Rows of 4096 values or more, up to 160 rows per CU.
 static bool q6_ksplit_glu_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
+    if (ksplit_short_rows(K)) return q6_ksplit_auto(K, M, cus, tr, waves, slots);  // (the plain rule's shapes)
     if (rho > 160 || K < 4096) return false;
     tr = waves = K == 4096 || K == 8192 ? 4 : 8;
     slots = 1;
@@ -342,10 +366,12 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     // bits, takes the rest
     // (fused epilogues and batched launches included; a batched launch's
     // workgroups per weight matrix: grid_per_matrix.  Batched, rows of 4096
-    // values or more: MUL_MAT_ID measured on MI355X, Mixtral 8x7B gate/up
-    // with SWIGLU, Q4_K, 26.61 -> 25.27 us, down, Q6_K, 22.27 -> 19.64; the
-    // 2048 x 768 Q6_K experts of a Qwen3-30B-A3B-like down 7.72 -> 7.98)
-    const bool ks_ok = N == 1 && f32_vec && K <= 8 * 4096 && (mats == 1 || K >= 4096);
+    // values or more and rows of 3 to 8 blocks (short teams): MUL_MAT_ID
+    // measured on MI355X, Mixtral 8x7B gate/up with SWIGLU, Q4_K, 26.61 ->
+    // 25.27 us, down, Q6_K, 22.27 -> 19.64; Qwen3-30B-A3B-like down 7.73 ->
+    // 4.43)
+    const bool ks_ok = N == 1 && f32_vec && K <= 8 * 4096 &&
+                       (mats == 1 || K >= 4096 || okern == 5 || ksplit_short_rows(K));
     const int cus_m = mats > 1 ? grid_per_matrix(cus, mats, M) : cus;
     // two to four columns: the several-column K-split kernel, whose outputs
     // are the bits of the tile kernel's launches (all columns in one, or
@@ -376,7 +402,7 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
             const int os = g_ovr_slots.load();
             const Q6Geometry gk = pick_geometry_q6_ksplit(di, K, M, tr, kw, mats > 1 ? cus_m : 0,
                                                           os >= 1 && os <= 4 ? os : ks, fused, mats > 1);
-            if (gk.ksplit && gk.lds <= max_lds) return gk;
+            if (gk.ksplit && gk.lds <= max_lds && (mats == 1 || K >= 4096 || gk.ks_kt)) return gk;
         }
     }
     // the matrix-core kernel with its A operand from the Q8_1 buffer: the
@@ -602,7 +628,10 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.gate_bias = ep->gate ? ep->gate_bias : nullptr;
             p.glu_op = ep->glu_op;
         }
+        const int epi = fused == kFusedGate ? kEpiGlu : (fused == kFusedBias ? kEpiBias : kEpiNone);
         const void *fn = geo.ks_nc_p  ? q6_ksplit_nc_kernel<false>(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
+                         : geo.ks_kt
+                             ? q6k_ksplit_short_kernel(geo.ksplit, geo.ks_kt, geo.waves, geo.slots, false, epi, bl != nullptr)
                          : geo.ksplit && bl && fused == kFusedGate
                              ? q6_ksplit_kernel_epi<kEpiGlu, true>(geo.ks_long != 0, geo.ksplit, geo.waves, geo.slots, p.G)
                          : geo.ksplit && bl && fused == kFusedBias
@@ -631,6 +660,7 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         if (so) {  // parity variant: this chunk's columns of the group sums
             if (fused || bl) return Q4K_EINVAL;
             fn = geo.ks_nc_p  ? q6k_ksplit_nc_sums_kernel(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
+                 : geo.ks_kt    ? q6k_ksplit_short_kernel(geo.ksplit, geo.ks_kt, geo.waves, geo.slots, true, kEpiNone, false)
                  : geo.ks_long  ? q6k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                  : geo.ksplit ? q6k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                  : geo.mfma_ga ? q6k_mfma_ga_sums_kernel(nc, geo.waves)
@@ -642,7 +672,7 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         if (bl) p.bt = bl->bt;
         if (geo.ks_long) {
             p.ring_off = ksplit_long_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), geo.ksplit,
-                                                fused == kFusedGate ? 2 : 1);
+                                                fused == kFusedGate ? 2 : 1, geo.ks_kt);
             // groups quantised before the first step: one, the others just
             // before the first step that reads them (4096 x 14336 12.08
             // against 12.14 us with all before, 8192 x 28672 37.04 / 38.42);

@@ -274,15 +274,19 @@ __device__ __forceinline__ Q6Act q6_ks_read_lds(const uint8_t *area, int sbw, in
 
 // SBW: 1, 2 or 4 super-blocks per wave and group; GMAX: the most groups per
 // row (K <= 4096 GMAX); p.ring_off: LDS offset of the wave areas (after the
-// partials).
-template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone, bool BATCH = false>
+// partials).  KT: waves per team for rows shorter than one group (GMAX =
+// 1), 0 for the whole 16/SBW, as in the Q4_K kernel.
+template <int SBW, int WAVES, int S, int GMAX, bool SUMS = false, int EPI = kEpiNone, bool BATCH = false,
+          int KT = 0>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
+    constexpr int KS = KT > 0 ? KT : KW;  // slices a team computes
     constexpr int TR = 16 / SBW;
-    constexpr int TEAMS = WAVES / KW;
+    constexpr int TEAMS = WAVES / KS;
     constexpr int V = 4 * SBW;
     constexpr int NW = EPI == kEpiGlu ? 2 : 1;  // weights per step (the weight, the gate weight)
-    static_assert(TEAMS >= 1 && WAVES % KW == 0, "whole teams");
+    static_assert(TEAMS >= 1 && WAVES % KS == 0, "whole teams");
+    static_assert(KS <= KW && (KS == KW || GMAX == 1), "short teams for rows of one partial group only");
     static_assert(!SUMS || (EPI == kEpiNone && !BATCH), "parity variants of the plain product only");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     if constexpr (BATCH) batch_activation(p);
@@ -291,7 +295,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int slice = wave % KW, team = wave / KW;
+    const int slice = wave % KS, team = wave / KS;
     const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1);
     const int h = (lane >> 1) & 1, jp = lane & 1;
     const int G = p.G;
@@ -412,7 +416,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
 #pragma unroll
                     for (int u = 0; u < NW; ++u) {
                         const float q = ks_reduce<SBW>(acc[u]);
-                        if (wr) part[(rl * NW + u) * KW + slice] = q;
+                        if (wr) part[(rl * NW + u) * KS + slice] = q;
                         acc[u] = 0.0f;
                     }
                 }
@@ -430,7 +434,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
         for (int u = 0; u < NW; ++u) {
             float q[KW];
 #pragma unroll
-            for (int k = 0; k < KW; ++k) q[k] = part[(row * NW + u) * KW + k];
+            for (int k = 0; k < KW; ++k) q[k] = k < KS ? part[(row * NW + u) * KS + k] : 0.0f;
 #pragma unroll
             for (int hh = KW / 2; hh >= 1; hh /= 2)
 #pragma unroll
@@ -441,8 +445,9 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_long_kernel(Q4K_
     }
 }
 
-__host__ __device__ constexpr int q6_ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G, int nw = 1) {
-    return ksplit_long_part_bytes(rows_per_wg, sbw, nw) + waves * G * q6_ks_slice_bytes(sbw);
+__host__ __device__ constexpr int q6_ksplit_long_lds_bytes(int rows_per_wg, int sbw, int waves, int G, int nw = 1,
+                                                           int kt = 0) {
+    return ksplit_long_part_bytes(rows_per_wg, sbw, nw, kt) + waves * G * q6_ks_slice_bytes(sbw);
 }
 
 // The long-row variants: those of the Q4_K kernel (SBW 1 or 2 for rows of

@@ -233,13 +233,15 @@ def long_shapes(K):
 
 
 @pytest.mark.parametrize("M,K", [(4096, 14336), (1000, 14336), (37, 12544), (300, 3584), (513, 2048),
-                                 (96, 28672), (2000, 28672), (5, 256), (33, 20480)])
+                                 (96, 28672), (2000, 28672), (5, 256), (33, 20480), (700, 1024), (300, 1536),
+                                 (1030, 768)])
 def test_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
     """Rows of any length up to 8 groups (the last group partial: 14336 =
     3.5 groups, 12544 = 3 groups + 1 block, 3584 and 2048 under one group,
     256 = one block): every long-row launch shape, with the default grid, a
     few and 300 workgroups, against the tile kernel bit for bit; the tile
-    kernel against the oracle."""
+    kernel against the oracle.  Rows of 3 to 8 blocks (768 .. 2048) run
+    with teams of only the waves the row needs."""
     wq, x = inputs(Q, M, K, seed=41)
     wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
     try:
@@ -263,7 +265,7 @@ def test_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
                                      f"e.g. rows {bad[:5]}")
 
 
-@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048)])
+@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048), (77, 768)])
 def test_ksplit_long_rows_sums_exact(Q, O, gpu, M, K):
     """The long-row parity variants: S_qq of every lane in the row's blocks
     and S_q of the in-register quantisation (blocks of the partial group
@@ -290,7 +292,7 @@ def test_ksplit_long_rows_sums_exact(Q, O, gpu, M, K):
 
 
 @pytest.mark.parametrize("M,K", [(4096, 14336), (1000, 14336), (37, 12544), (300, 3584), (96, 28672),
-                                 (5, 256), (33, 20480)])
+                                 (5, 256), (33, 20480), (513, 2048), (300, 1536), (1030, 768)])
 def test_q6k_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
     """Q6_K rows of any length up to 8 groups: every long-row launch shape,
     with the default grid, a few and 300 workgroups, against the Q6_K tile
@@ -317,7 +319,7 @@ def test_q6k_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
                                      f"e.g. rows {bad[:5]}")
 
 
-@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048)])
+@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048), (77, 768)])
 def test_q6k_ksplit_long_rows_group_sums_exact(Q, O, gpu, M, K):
     """The Q6_K long-row parity variants: every lane's int32 group sums,
     from the -32 * sum q8 starting values staged per 16 values, bit for bit

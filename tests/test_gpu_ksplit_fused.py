@@ -53,11 +53,12 @@ def fused(Q, wd, K, xd, gd, bu, bg, op, wtype=Q4):
 
 @pytest.mark.parametrize("wtype", [Q4, Q6])
 @pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 4096), (1024, 4096), (37, 4096), (5000, 8192), (258, 8192),
-                                 (4096, 14336), (1000, 11008), (300, 5120)])
+                                 (4096, 14336), (1000, 11008), (300, 5120), (2048, 2048), (1030, 768)])
 def test_ksplit_fused_bits_equal_tile_kernel(Q, gpu, wtype, M, K):
     """Gate + GLU (SWIGLU, GEGLU, SWIGLU_OAI; with and without biases) and
     the bias-only epilogue, every K-split launch shape against the fused
-    tile kernel."""
+    tile kernel (rows of 768 and 2048 values: teams of only the waves a row
+    needs)."""
     wu, wg = weights(Q, M, K, 1, wtype), weights(Q, M, K, 2, wtype)
     x = _common.activations(1, K, seed=3)
     rng = np.random.default_rng([M, K])
@@ -102,7 +103,8 @@ def test_ksplit_fused_bits_equal_tile_kernel(Q, gpu, wtype, M, K):
         assert np.array_equal(fused(Q, wud, K, xd, gd, b1, b2, op or 2, wtype), y_tile)
 
 
-@pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 4096), (28672, 8192), (4096, 14336)])
+@pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 4096), (28672, 8192), (4096, 14336), (8192, 2048),
+                                 (2048, 768)])
 def test_ksplit_fused_automatic_choice(Q, gpu, M, K):
     """The fused one-column launches of the workload shapes take the K-split
     kernel automatically (Q4_K and Q6_K), and an unaligned activation the
@@ -130,13 +132,15 @@ def _tensor(Q, t, ne, nb, ptr):
 
 @pytest.mark.parametrize("wtype", [Q4, Q6])
 @pytest.mark.parametrize("M,K,fuse", [(14336, 4096, False), (14336, 4096, True), (4096, 14336, False),
-                                      (1024, 8192, True), (3000, 11008, True)])
+                                      (1024, 8192, True), (3000, 11008, True), (768, 2048, True),
+                                      (2048, 768, False), (1000, 1536, True)])
 def test_ksplit_batched_mul_mat_id_bits_equal_tile_kernel(Q, gpu, wtype, M, K, fuse):
     """MUL_MAT_ID for one token (three experts, slots using two of them, one
     twice, and an absent id), with and without the gate weight and SWIGLU:
-    the automatic launch (the batched K-split kernels) and a forced
-    8-row, 8-wave K-split launch against the batched tile kernel, bit for
-    bit; the absent expert's slot reads no weight."""
+    the automatic launch (the batched K-split kernels; rows of 768 .. 2048
+    values in short teams) and a forced 8-row, 8-wave K-split launch
+    against the batched tile kernel, bit for bit; the absent expert's slot
+    reads no weight."""
     import ctypes
     import torch
     BB = {Q4: 144, Q6: 210}
