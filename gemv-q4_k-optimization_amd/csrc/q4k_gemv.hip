@@ -380,10 +380,11 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
     // long rows: 4 super-blocks per wave for up to 4 groups, else at most 2
     if (lng && g.ksplit > (G <= 4 ? 4 : 2)) g.ksplit = G <= 4 ? 4 : 2;
     g.R = 16 / g.ksplit;
-    g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
+    g.waves = waves >= 1 && waves <= 16 ? waves : 16;
     g.slots = slots >= 1 && slots <= 4 ? slots : 1;
     // rows shorter than one group: teams of only the waves the row needs,
-    // where that variant is instantiated (else the whole team)
+    // where that variant is instantiated (else the whole team; team sizes
+    // other than powers of two take workgroups of whole teams)
     const int epi = fused == kFusedGate ? kEpiGlu : (fused == kFusedBias ? kEpiBias : kEpiNone);
     int kt = lng ? ksplit_short_team((int)(K / kQK), g.ksplit) : 0;
     if (kt) {
@@ -393,6 +394,7 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
     }
     g.ks_kt = kt;
     if (!kt) {
+        if (g.waves != 4 && g.waves != 8 && g.waves != 16) g.waves = 16;
         if (g.waves < g.R) g.waves = g.R;
         if (lng ? !ksplit_long_exists(g.ksplit, g.waves, g.slots, gmax)
                 : !ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096)))
@@ -460,9 +462,9 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //    7.42, 4096 x 5120 4.81 / 5.53); beyond, 8 rows, 8 waves, two steps
 //    where 8-row tiles leave at most one row in eight idle (8192 x 28672
 //    25.50 / 28.62, 14336 x 14336 21.55 / 22.46, 13824 x 5120 9.97 / 10.17,
-//    32000 x 5120 19.32 / 19.77, 18944 x 3584 9.17 / 9.42, 11008 x 2048
-//    5.44 / 5.46), the tile kernel otherwise (5120 x 13824, 20 rows per CU:
-//    10.23 against 9.50) and over 160 rows per CU (not measured).
+//    32000 x 5120 19.32 / 19.77), the tile kernel otherwise (5120 x 13824,
+//    20 rows per CU: 10.23 against 9.50) and over 160 rows per CU (not
+//    measured); rows under 4096 values as below.
 //  - rows of 3 to 8 blocks (768 .. 2048 values; the long-row kernel with
 //    teams of only the waves a row needs): 8 rows per step, one step in
 //    flight, 4 waves up to 16 rows per CU (512 x 2048 2.60 against 2.88 on
@@ -470,14 +472,32 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //    1024 x 768 2.51 / 2.81), 8 up to 24 (6144 x 2048 3.84 / 4.40), 16
 //    beyond (8960 x 1536 4.13 / 4.90, 16384 x 2048 5.37 / 6.69, 8192 x 2048
 //    4.22 / 4.72, 32768 x 2048 8.57 / 9.74, 128256 x 2048 26.44 / 30.31).
+//  - rows of 9 to 14 blocks (2304 .. 3584 values): 8 rows per step, two
+//    teams of ceil(blocks / 2) waves and one step in flight (2304 x 2304
+//    3.60 / 3.82, 9216 x 2304 5.10 / 5.15, 2560 x 2560 3.62 / 3.85, 9728 x
+//    2560 5.25 / 5.41, 3072 x 3072 3.73 / 3.83, 8192 x 3072 4.89 / 5.13);
+//    teams of 7 one per workgroup with two steps (3584 x 3584 3.94 / 4.13,
+//    18944 x 3584 8.78 / 9.40); the tile kernel up to 4 rows per CU (512 x
+//    3584 3.07 against 3.17) and over 160 (151936 x 2560 40.01 against
+//    40.81).
+static bool ksplit_short_auto(int64_t K, int64_t rho, bool glu, int &tr, int &waves, int &slots) {
+    const int nb = (int)(K / kQK);
+    tr = 8;
+    slots = 1;
+    if (nb <= 8) {
+        waves = rho <= 16 ? 4 : (rho <= 24 || glu ? 8 : 16);
+        return true;
+    }
+    const int kt = (nb + 1) / 2;
+    waves = kt == 7 ? 7 : 2 * kt;
+    if (kt == 7 && !glu) slots = 2;
+    return rho > 4 && rho <= 160;
+}
+
 static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
-    if (ksplit_short_rows(K)) {
-        tr = 8;
-        waves = rho <= 16 ? 4 : (rho <= 24 ? 8 : 16);
-        return true;
-    }
+    if (ksplit_short_rows(K)) return ksplit_short_auto(K, rho, false, tr, waves, slots);
     if (K != 4096 && K != 8192) {
         if (rho <= 4 && K <= 4 * 4096) {
             tr = waves = 4;
@@ -532,15 +552,14 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
 // rows per CU: the range measured; rows of 3 to 8 blocks (short teams) 8
 // rows per step, 4 waves up to 16 rows per CU, else 8 (2048 x 2048 3.53 /
 // 3.97, 5632 x 2048 4.85 / 6.27, 6144 x 2048 5.13 / 6.32, 8192 x 2048 5.93
-// / 7.46; MUL_MAT_ID of eight 768 x 2048 experts 5.09 / 6.62).
+// / 7.46; MUL_MAT_ID of eight 768 x 2048 experts 5.09 / 6.62); rows of 9 to
+// 14 blocks two teams of ceil(blocks / 2) waves (teams of 7: one), one step
+// (2560 x 2560 4.66 / 4.81, 9728 x 2560 7.44 / 8.89, 8192 x 3072 7.74 /
+// 8.07, 18944 x 3584 15.86 / 16.55).
 static bool ksplit_glu_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
-    if (ksplit_short_rows(K)) {
-        tr = 8;
-        waves = rho <= 16 ? 4 : 8;
-        return true;
-    }
+    if (ksplit_short_rows(K)) return ksplit_short_auto(K, rho, true, tr, waves, slots);
     if (rho > 160 || K < 4096) return false;  // (other rows under 4096 values: not measured)
     if (K == 4096) {
         if (rho <= 16) {

@@ -615,21 +615,33 @@ __host__ __device__ constexpr int ksplit_long_lds_bytes(int rows_per_wg, int sbw
     return ksplit_long_part_bytes(rows_per_wg, sbw, nw, kt) + waves * G * ks_slice_bytes(sbw);
 }
 
-// Rows of 3 to 8 super-blocks (K = 768 .. 2048 values): the rows the
-// short-team variants serve.
+// Rows of 3 to 14 super-blocks (K = 768 .. 3584 values): the rows the
+// short-team variants serve at 2 super-blocks per wave.
 __host__ __device__ constexpr bool ksplit_short_rows(int64_t K) {
-    return K % 256 == 0 && K >= 3 * 256 && K <= 8 * 256;
+    return K % 256 == 0 && K >= 3 * 256 && K <= 14 * 256;
+}
+
+// The instantiated team sizes (waves per team) of the short-team variants
+// at sbw super-blocks per wave: powers of two below 16/sbw for rows of 3 to
+// 8 blocks, and 5, 6, 7 (sbw 2) or 3 (sbw 4) for rows of 9 to 14.
+__host__ __device__ constexpr bool ksplit_short_kt_ok(int sbw, int kt) {
+    return (sbw == 1 && (kt == 4 || kt == 8)) || (sbw == 2 && (kt == 2 || (kt >= 4 && kt <= 7))) ||
+           (sbw == 4 && kt >= 1 && kt <= 3);
 }
 
 // Waves per team of the long-row kernel for rows of nb super-blocks at sbw
-// per wave: for rows shorter than one group the fewest that cover the row,
-// rounded up to a power of two; 0 (the whole 16/sbw) otherwise or where that
-// is no fewer.
+// per wave: for rows shorter than one group the fewest that cover the row
+// where that team size is instantiated, else the next power of two; 0 (the
+// whole 16/sbw) otherwise or where that is no fewer.
 __host__ __device__ constexpr int ksplit_short_team(int nb, int sbw) {
     if (nb >= 16 || sbw <= 0) return 0;
-    int kt = 1;
-    while (kt * sbw < nb) kt *= 2;
-    return kt < 16 / sbw ? kt : 0;
+    int kt = (nb + sbw - 1) / sbw;
+    if (!ksplit_short_kt_ok(sbw, kt)) {
+        int p = 1;
+        while (p < kt) p *= 2;
+        kt = p;
+    }
+    return kt < 16 / sbw && ksplit_short_kt_ok(sbw, kt) ? kt : 0;
 }
 
 // The instantiated K-split variants: whole teams per workgroup; two groups
@@ -720,12 +732,15 @@ const void *ksplit_long_kernel(int sbw, int waves, int slots, int G) {
 }
 
 // The short-team variants of the long-row kernel (rows of one partial group;
-// q4k_short.hip): (SBW, KT) = (1, 4), (1, 8), (2, 2), (2, 4), (4, 1),
-// (4, 2), the teams of rows of 3 to 8 super-blocks; q6: the Q6_K kernel.
+// q4k_short.hip, q6k_short.hip): the team sizes of ksplit_short_kt_ok in
+// workgroups of 4, 8 or 16 waves (power-of-two teams) or of one, two or
+// four teams (the others, up to 16 waves); q6: the Q6_K kernel.
 constexpr bool ksplit_short_exists(bool q6, int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
-    const bool shape = ((sbw == 1 && (kt == 4 || kt == 8)) || (sbw == 2 && (kt == 2 || kt == 4)) ||
-                        (sbw == 4 && (kt == 1 || kt == 2))) &&
-                       (waves == 4 || waves == 8 || waves == 16) && waves % kt == 0 && (slots == 1 || slots == 2);
+    const bool pow2 = (kt & (kt - 1)) == 0;
+    const bool shape = ksplit_short_kt_ok(sbw, kt) &&
+                       (pow2 ? (waves == 4 || waves == 8 || waves == 16)
+                             : (waves == kt || waves == 2 * kt || waves == 4 * kt)) &&
+                       waves <= 16 && waves % kt == 0 && (slots == 1 || slots == 2);
     if (!shape) return false;
     if (sums) return !batch && epi == kEpiNone;
     if (epi == kEpiNone && !batch) return true;

@@ -1,5 +1,5 @@
 // q4k_short.hip -- the long-row K-split kernels (one F32 column) with short
-// teams, for rows of 3 to 8 super-blocks (K = 768 .. 2048 values): a team
+// teams, for rows of 3 to 14 super-blocks (K = 768 .. 3584 values): a team
 // of KW = 16/SBW waves would leave the waves past the row's super-blocks
 // without work, so a team is only as many waves as the row needs
 // (ksplit_short_team).  Instantiated in translation units of
@@ -53,9 +53,16 @@ const void *short_by_shape(int waves, int slots, bool sums, int epi, bool batch)
         if (slots == 2) return short_by_kind<Q6, SBW, KT, W, 2>(sums, epi, batch);
         return nullptr;
     };
-    if (waves == 4) return by_s(std::integral_constant<int, 4>{});
-    if (waves == 8) return by_s(std::integral_constant<int, 8>{});
-    if (waves == 16) return by_s(std::integral_constant<int, 16>{});
+    if constexpr ((KT & (KT - 1)) == 0) {
+        if (waves == 4) return by_s(std::integral_constant<int, 4>{});
+        if (waves == 8) return by_s(std::integral_constant<int, 8>{});
+        if (waves == 16) return by_s(std::integral_constant<int, 16>{});
+    } else {
+        if (waves == KT) return by_s(std::integral_constant<int, KT>{});
+        if (waves == 2 * KT) return by_s(std::integral_constant<int, 2 * KT>{});
+        if constexpr (4 * KT <= 16)
+            if (waves == 4 * KT) return by_s(std::integral_constant<int, 4 * KT>{});
+    }
     return nullptr;
 }
 
@@ -65,8 +72,12 @@ const void *short_kernel(int sbw, int kt, int waves, int slots, bool sums, int e
     if (sbw == 1 && kt == 8) return short_by_shape<Q6, 1, 8>(waves, slots, sums, epi, batch);
     if (sbw == 2 && kt == 2) return short_by_shape<Q6, 2, 2>(waves, slots, sums, epi, batch);
     if (sbw == 2 && kt == 4) return short_by_shape<Q6, 2, 4>(waves, slots, sums, epi, batch);
+    if (sbw == 2 && kt == 5) return short_by_shape<Q6, 2, 5>(waves, slots, sums, epi, batch);
+    if (sbw == 2 && kt == 6) return short_by_shape<Q6, 2, 6>(waves, slots, sums, epi, batch);
+    if (sbw == 2 && kt == 7) return short_by_shape<Q6, 2, 7>(waves, slots, sums, epi, batch);
     if (sbw == 4 && kt == 1) return short_by_shape<Q6, 4, 1>(waves, slots, sums, epi, batch);
     if (sbw == 4 && kt == 2) return short_by_shape<Q6, 4, 2>(waves, slots, sums, epi, batch);
+    if (sbw == 4 && kt == 3) return short_by_shape<Q6, 4, 3>(waves, slots, sums, epi, batch);
     return nullptr;
 }
 

@@ -161,10 +161,11 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
     g.ks_tr = rows_per_step == 4 || rows_per_step == 8 || rows_per_step == 16 ? rows_per_step : 8;
     if (lng && g.ks_tr == 4 && G > 4) g.ks_tr = 8;  // 4 rows per step: rows of up to 4 groups
     g.ksplit = 16 / g.ks_tr;
-    g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 16;
+    g.waves = waves >= 1 && waves <= 16 ? waves : 16;
     g.slots = slots >= 1 && slots <= (lng ? 4 : 2) ? slots : 1;
     // rows shorter than one group: teams of only the waves the row needs,
-    // where that variant is instantiated (else the whole team)
+    // where that variant is instantiated (else the whole team; team sizes
+    // other than powers of two take workgroups of whole teams)
     const int epi = fused == kFusedGate ? kEpiGlu : (fused == kFusedBias ? kEpiBias : kEpiNone);
     int kt = lng ? ksplit_short_team((int)(K / kQK), g.ksplit) : 0;
     if (kt) {
@@ -174,6 +175,7 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
     }
     g.ks_kt = kt;
     if (!kt) {
+        if (g.waves != 4 && g.waves != 8 && g.waves != 16) g.waves = 16;
         if (g.waves < g.ks_tr) g.waves = g.ks_tr;
         if (lng ? !q6_ksplit_long_exists(g.ksplit, g.waves, g.slots, G <= 4 ? 4 : 8)
                 : !q6_ksplit_exists(g.ksplit, g.waves, g.slots, (int)(K / 4096)))
@@ -230,13 +232,17 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
 // step, one step in flight, 4 waves up to 16 rows per CU (2048 x 768 2.88
 // against 3.49 on the tile kernel, 2048 x 2048 3.16 / 3.65), 8 beyond
 // (16384 x 768 4.68 / 9.40, 128256 x 2048 38.75 / 57.98; MUL_MAT_ID of
-// eight 2048 x 768 experts 4.43 / 7.73).
+// eight 2048 x 768 experts 4.43 / 7.73).  Rows of 9 to 14 blocks: teams of
+// ceil(blocks / 2) waves, one per workgroup up to 16 rows per CU (1024 x
+// 2560 3.12 / 3.37, 3584 x 3584 4.71 / 5.33), else two (teams of 7: one;
+// 151936 x 2560 57.15 / 72.32, 128256 x 3072 60.09 / 64.66).
 static bool q6_ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
     if (ksplit_short_rows(K)) {
+        const int nb = (int)(K / kQK), kt = (nb + 1) / 2;
         tr = 8;
-        waves = rho <= 16 ? 4 : 8;
+        waves = nb <= 8 ? (rho <= 16 ? 4 : 8) : (rho <= 16 || kt == 7 ? kt : 2 * kt);
         return true;
     }
     if (K != 4096 && K != 8192) {

@@ -228,19 +228,33 @@ LONG_SHAPES = [(tr, w, s) for tr in (16, 8) for w in (8, 16) for s in (1, 2) if 
 LONG_SHAPES_4 = [(4, w, s) for w in (4, 8, 16) for s in (1, 2)] + [(4, w, s) for w in (4, 8) for s in (3, 4)]
 
 
+def short_team_shapes(K):
+    """Rows of 9 to 14 blocks: the team sizes other than powers of two (teams
+    of ceil(blocks / 2) waves at 8 rows per step, of 3 at 4 rows for up to
+    12 blocks), one, two or four teams per workgroup."""
+    nb = K // 256
+    if not 9 <= nb <= 14:
+        return []
+    kt = (nb + 1) // 2
+    out = [(8, kt, 1), (8, 2 * kt, 1), (8, kt, 2), (8, 2 * kt, 2)]
+    if nb <= 12:
+        out += [(4, 3, 1), (4, 6, 1), (4, 12, 1), (4, 6, 2)]
+    return out
+
+
 def long_shapes(K):
-    return LONG_SHAPES + (LONG_SHAPES_4 if -(-K // 4096) <= 4 else [])
+    return LONG_SHAPES + (LONG_SHAPES_4 if -(-K // 4096) <= 4 else []) + short_team_shapes(K)
 
 
 @pytest.mark.parametrize("M,K", [(4096, 14336), (1000, 14336), (37, 12544), (300, 3584), (513, 2048),
                                  (96, 28672), (2000, 28672), (5, 256), (33, 20480), (700, 1024), (300, 1536),
-                                 (1030, 768)])
+                                 (1030, 768), (700, 2560), (300, 3072), (129, 2304)])
 def test_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
     """Rows of any length up to 8 groups (the last group partial: 14336 =
     3.5 groups, 12544 = 3 groups + 1 block, 3584 and 2048 under one group,
     256 = one block): every long-row launch shape, with the default grid, a
     few and 300 workgroups, against the tile kernel bit for bit; the tile
-    kernel against the oracle.  Rows of 3 to 8 blocks (768 .. 2048) run
+    kernel against the oracle.  Rows of 3 to 14 blocks (768 .. 3584) run
     with teams of only the waves the row needs."""
     wq, x = inputs(Q, M, K, seed=41)
     wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
@@ -265,7 +279,7 @@ def test_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
                                      f"e.g. rows {bad[:5]}")
 
 
-@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048), (77, 768)])
+@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048), (77, 768), (77, 2560)])
 def test_ksplit_long_rows_sums_exact(Q, O, gpu, M, K):
     """The long-row parity variants: S_qq of every lane in the row's blocks
     and S_q of the in-register quantisation (blocks of the partial group
@@ -292,7 +306,8 @@ def test_ksplit_long_rows_sums_exact(Q, O, gpu, M, K):
 
 
 @pytest.mark.parametrize("M,K", [(4096, 14336), (1000, 14336), (37, 12544), (300, 3584), (96, 28672),
-                                 (5, 256), (33, 20480), (513, 2048), (300, 1536), (1030, 768)])
+                                 (5, 256), (33, 20480), (513, 2048), (300, 1536), (1030, 768), (700, 2560),
+                                 (129, 3072)])
 def test_q6k_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
     """Q6_K rows of any length up to 8 groups: every long-row launch shape,
     with the default grid, a few and 300 workgroups, against the Q6_K tile
@@ -319,7 +334,7 @@ def test_q6k_ksplit_long_rows_bits_equal_tile_kernel(Q, O, gpu, M, K):
                                      f"e.g. rows {bad[:5]}")
 
 
-@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048), (77, 768)])
+@pytest.mark.parametrize("M,K", [(700, 14336), (50, 12544), (129, 2048), (77, 768), (77, 3072)])
 def test_q6k_ksplit_long_rows_group_sums_exact(Q, O, gpu, M, K):
     """The Q6_K long-row parity variants: every lane's int32 group sums,
     from the -32 * sum q8 starting values staged per 16 values, bit for bit

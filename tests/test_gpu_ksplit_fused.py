@@ -40,10 +40,19 @@ def to_dev(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
+def team_shapes(K):
+    """Rows of 9 to 14 blocks: teams of other sizes than powers of two."""
+    nb = K // 256
+    if not 9 <= nb <= 14:
+        return []
+    kt = (nb + 1) // 2
+    return [(8, kt, 1), (8, 2 * kt, 1)] + ([(4, 3, 1), (4, 6, 1), (4, 12, 1)] if nb <= 12 else [])
+
+
 def launch_shapes(K, wtype):
     if wtype == Q6:
-        return LONG  # (16 rows per step exists for rows of 4096 and 8192 values too)
-    return SHORT if K in (4096, 8192) else LONG
+        return LONG + team_shapes(K)  # (16 rows per step exists for rows of 4096 and 8192 values too)
+    return SHORT if K in (4096, 8192) else LONG + team_shapes(K)
 
 
 def fused(Q, wd, K, xd, gd, bu, bg, op, wtype=Q4):
@@ -53,7 +62,8 @@ def fused(Q, wd, K, xd, gd, bu, bg, op, wtype=Q4):
 
 @pytest.mark.parametrize("wtype", [Q4, Q6])
 @pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 4096), (1024, 4096), (37, 4096), (5000, 8192), (258, 8192),
-                                 (4096, 14336), (1000, 11008), (300, 5120), (2048, 2048), (1030, 768)])
+                                 (4096, 14336), (1000, 11008), (300, 5120), (2048, 2048), (1030, 768),
+                                 (2560, 2560), (700, 3584)])
 def test_ksplit_fused_bits_equal_tile_kernel(Q, gpu, wtype, M, K):
     """Gate + GLU (SWIGLU, GEGLU, SWIGLU_OAI; with and without biases) and
     the bias-only epilogue, every K-split launch shape against the fused
@@ -104,7 +114,7 @@ def test_ksplit_fused_bits_equal_tile_kernel(Q, gpu, wtype, M, K):
 
 
 @pytest.mark.parametrize("M,K", [(14336, 4096), (4096, 4096), (28672, 8192), (4096, 14336), (8192, 2048),
-                                 (2048, 768)])
+                                 (2048, 768), (9728, 2560)])
 def test_ksplit_fused_automatic_choice(Q, gpu, M, K):
     """The fused one-column launches of the workload shapes take the K-split
     kernel automatically (Q4_K and Q6_K), and an unaligned activation the
@@ -133,7 +143,8 @@ def _tensor(Q, t, ne, nb, ptr):
 @pytest.mark.parametrize("wtype", [Q4, Q6])
 @pytest.mark.parametrize("M,K,fuse", [(14336, 4096, False), (14336, 4096, True), (4096, 14336, False),
                                       (1024, 8192, True), (3000, 11008, True), (768, 2048, True),
-                                      (2048, 768, False), (1000, 1536, True)])
+                                      (2048, 768, False), (1000, 1536, True), (1000, 2560, True),
+                                      (2000, 3584, False)])
 def test_ksplit_batched_mul_mat_id_bits_equal_tile_kernel(Q, gpu, wtype, M, K, fuse):
     """MUL_MAT_ID for one token (three experts, slots using two of them, one
     twice, and an absent id), with and without the gate weight and SWIGLU:
