@@ -204,6 +204,7 @@ struct Geometry {
     int ks_staged = 0;  // several-column K-split kernel: activation quantised once per workgroup into LDS
     int ks_p = 0;       // several-column K-split kernel: columns of its reduction tree (2 or 4)
     int ks_kt = 0;      // long-row K-split kernel, rows shorter than one group: waves per team (0: 16/SBW)
+    int colsplit = 0;   // several columns as one launch over one-column channels (the columns; 0: not)
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
@@ -663,6 +664,29 @@ static bool ksplit_nc_auto(int64_t K, int64_t M, int64_t N, int cus, int &tr, in
     return false;
 }
 
+// Several columns over few rows per CU: every workgroup of a several-column
+// launch quantises (or stages) all N columns for its few rows, so the
+// columns go to one launch of one-column products instead, column c as
+// dst channel c of a broadcast batched launch (the weight shared, grid y =
+// columns), whose workgroups quantise one column each.  Each column then
+// carries the one-column product's bits, on both routes (F32: the
+// one-column K-split kernel; pre-quantised: the one-column tile kernel).
+// Measured on MI355X (us, N columns in one launch against N one-column
+// channels, same buffers): 512 x 4096 N=4 4.97 -> 3.56, N=8 7.27 -> 3.93;
+// 1024 x 4096 N=2 3.98 -> 3.59, N=3 4.48 -> 4.18, N=4 5.16 -> 3.98, N=8
+// 7.29 -> 4.69; 2048 x 4096 N=3 5.48 -> 5.20, N=4 5.41 -> 4.75, N=8 7.65 ->
+// 6.23; 3072 x 4096 N=4 6.01 -> 5.58, N=8 8.12 -> 7.76; 1024 x 8192 N=4
+// 8.02 -> 5.44; 1024 x 14336 N=4 11.95 -> 7.23, N=8 16.00 -> 10.21; 1024 x
+// 2048 N=8 5.57 -> 5.11; Q6_K 1024 x 4096 N=4 5.59 -> 5.01, N=8 7.92 ->
+// 6.64.  Not at 4096 rows (4096 x 4096 N=2 4.86 -> 5.08, N=4 6.29 -> 6.42)
+// nor beyond; two columns only up to 8 rows per CU (2048 x 4096: 4.12 ->
+// 4.11).
+bool split_columns(int64_t K, int64_t M, int64_t N, int cus) {
+    if (N < 2 || N > Q4K_MAX_BATCH || cus < 1) return false;
+    const int64_t rho = (M + cus - 1) / cus;
+    return rho <= (N == 2 ? 8 : 12) && K <= 8 * 4096 && (K >= 4096 || ksplit_short_rows(K));
+}
+
 // Launch geometry for an (M, K, N) product.
 //  tile kernel: one workgroup per CU (requesting just over half the CU's LDS
 //    keeps a second one away), 8 or 16 waves, the M rows split evenly over
@@ -687,6 +711,16 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const int orows = g_ovr_rows.load(), owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load();
     const int okern = g_ovr_kernel.load();
     const int rpw = bpl_rows_per_pass(K / kQK);
+    // several columns over few rows: one-column channels (automatic only;
+    // where the aligned F32 column takes the K-split kernel, so both routes
+    // decide alike)
+    if (!fused && mats == 1 && okern == 0 && orows == 0 && owaves == 0 && owgs == 0 && split_columns(K, M, N, cus) &&
+        pick_geometry(di, K, M, 1, 0, N, true, false).ksplit) {
+        Geometry g1 = pick_geometry(di, K, M, 1, 0, N, f32_vec, q81);
+        g1.colsplit = (int)N;
+        g1.nc_chunk = (int)N;
+        return g1;
+    }
     // K-split kernel: one 16-byte aligned F32 column of rows of up to 8
     // groups (4096 or 8192 values: activation in registers; other lengths:
     // the long-row variant); the tile kernel, whose outputs are the same
@@ -1178,7 +1212,7 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0 &&
                          (!bl || (bl->bt.x_channel % 4 == 0 && bl->bt.x_sample % 4 == 0));
     Geometry geo = pick_geometry(*di, ne00, ne01, ncols, fused, mats, f32_vec, !x && y);
-    if ((bl || fused) && !geo.ksplit) {  // the batched and fused tile variants: 1 or 2 slots, prologue 0 or 1
+    if ((bl || fused || geo.colsplit) && !geo.ksplit) {  // the batched and fused tile variants: 1 or 2 slots, prologue 0 or 1
         if (fused != kFusedGate) geo.R = 1;
         if (geo.slots > 2) geo.slots = 2;
         if (geo.prologue > 1) geo.prologue = 0;
@@ -1195,6 +1229,55 @@ static int run_gemv(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, 
     // GA: the Q8_1 columns of a launch as one buffer of 32-bit offsets
     if (geo.mfma_ga && (int64_t)geo.nc_chunk * stride_col_y * kQ81Bytes >= ((int64_t)1 << 31))
         return Q4K_EUNSUPPORTED;
+    if (geo.colsplit) {  // the columns as one-column channels of one launch
+        if (bl || fused || geo.colsplit != ncols) return Q4K_EINVAL;
+        GemvParams p{};
+        p.w = static_cast<const uint8_t *>(src0);
+        p.row_stride = nb01;
+        p.ldx = ldx;
+        p.stride_col_y = stride_col_y;
+        p.ld_dst = ld_dst;
+        p.M = (int)ne01;
+        p.K = (int)ne00;
+        p.nb = (int)(ne00 / kQK);
+        p.G = (p.nb + 15) / 16;
+        p.qcol = q8_col_bytes((int)ne00);
+        p.ntiles = geo.ntiles;
+        p.nblk32 = fastdiv_init((uint32_t)(ne00 / 32));
+        if (so) {  // parity variant: each column's launch on its own, same geometry and kernel
+            for (int64_t c = 0; c < ncols; ++c) {
+                GemvParams pc = p;
+                pc.x = x ? x + c * ldx : nullptr;
+                pc.y = y ? y + c * stride_col_y * kQ81Bytes : nullptr;
+                pc.dst = dst + c * ld_dst;
+                pc.vec_ok = x && aligned(pc.x, 16) && (ldx % 4 == 0);
+                pc.sums = so->sums + c * ne01 * (ne00 / 32);
+                pc.sq = so->sq + c * (ne00 / 32);
+                st = launch_gemv(di, geo, pc, 1, stream, nullptr);
+                if (st != Q4K_OK) return st;
+            }
+            return Q4K_OK;
+        }
+        p.x = x;
+        p.y = y;
+        p.dst = dst;
+        p.vec_ok = x && aligned(x, 16) && (ldx % 4 == 0);
+        BatchLaunch cb;
+        cb.nch = (int)ncols;
+        cb.nsmp = 1;
+        cb.bt.ids = nullptr;
+        cb.bt.w_channel = 0;
+        cb.bt.w_sample = 0;
+        cb.bt.x_channel = x ? ldx : stride_col_y;
+        cb.bt.x_sample = 0;
+        cb.bt.dst_channel = ld_dst;
+        cb.bt.dst_sample = 0;
+        cb.bt.channel_ratio = (int)ncols;
+        cb.bt.sample_ratio = 1;
+        cb.bt.nchannels_y = (int)ncols;
+        cb.bt.nexperts = 1;
+        return launch_gemv(di, geo, p, 1, stream, &cb);
+    }
     for (int64_t c0 = 0; c0 < ncols; c0 += geo.nc_chunk) {
         const int nc = (int)(ncols - c0 < geo.nc_chunk ? ncols - c0 : geo.nc_chunk);
         Geometry g2 = geo;
@@ -1668,8 +1751,8 @@ static void fill_geometry_out(const Geometry &g, int64_t ne11, bool q81, int32_t
     out[1] = g.waves;
     out[2] = g.grid;
     out[3] = g.lds_launch;
-    out[4] = g.nc_chunk;
-    out[5] = g.nc_chunk >= ne11 ? 1 : 0;
+    out[4] = g.colsplit ? 1 : g.nc_chunk;  // (column split: one column per channel, all in one launch)
+    out[5] = g.colsplit || g.nc_chunk >= ne11 ? 1 : 0;
     out[6] = g.ksplit ? 5 : (g.mfma_ga ? 6 : (g.mfma ? 4 : (g.bpl == 2 ? 3 : (g.bpl ? 2 : 1))));
     out[7] = g.bpl ? g.rpw : g.R;
     if (q81) out[5] = 0;

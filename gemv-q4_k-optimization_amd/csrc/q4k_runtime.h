@@ -100,10 +100,16 @@ const void *q6k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool 
 // Q6_K weight checks and launch (q6k_gemv.hip), for the type-dispatching
 // entry points of q4k_gemv.hip.
 int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01);
+// (geo_mats: the geometry of a launch over that many one-column channels,
+// for the parity variant's per-column launches of a column-split product)
 int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x, int64_t ldx,
                 const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst, int64_t ld_dst,
                 hipStream_t stream, const Epilogue *ep = nullptr, const BatchLaunch *bl = nullptr,
-                const SumsOut *so = nullptr);
+                const SumsOut *so = nullptr, int64_t geo_mats = 1);
+
+// Whether N columns of an (M, K) product run as one launch of N one-column
+// channels (q4k_gemv.hip: the measured rule), on cus CUs.
+bool split_columns(int64_t K, int64_t M, int64_t N, int cus);
 
 // Workgroups per weight matrix of a launch over `mats` matrices of M rows:
 // the CUs shared among the matrices, at least one, at most one per row.

@@ -100,6 +100,7 @@ struct Q6Geometry {
     int mfma_ga = 0; // matrix-core kernel: A operand from the Q8_1 buffer (pre-quantised route)
     int ks_nc_p = 0; // several-column K-split kernel: columns of its reduction tree (2 or 4; 0: not it)
     int ks_kt = 0;   // long-row K-split kernel, rows shorter than one group: waves per team (0: 16/SBW)
+    int colsplit = 0; // several columns as one launch over one-column channels (the columns; 0: not)
 };
 
 // Columns per launch of the tile kernel for N columns of K values (halved
@@ -366,6 +367,16 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
     const int okern = g_ovr_kernel.load();
+    // several columns over few rows per CU: one launch of one-column channels
+    // (split_columns; automatic only)
+    if (fused == kFusedNone && mats == 1 && okern == 0 && g_ovr_rows.load() == 0 && g_ovr_waves.load() == 0 &&
+        g_ovr_wgs.load() == 0 && split_columns(K, M, N, cus) &&
+        pick_geometry_q6(di, K, M, 1, N, kFusedNone, true, false).ksplit) {
+        Q6Geometry g1 = pick_geometry_q6(di, K, M, 1, N, kFusedNone, f32_vec, q81);
+        g1.colsplit = (int)N;
+        g1.nc_chunk = (int)N;
+        return g1;
+    }
     // K-split kernel: one 16-byte aligned F32 column of rows of up to 8
     // groups (4096 or 8192 values: activation in registers; other lengths:
     // the long-row variant); the tile kernel, whose outputs are the same
@@ -574,18 +585,48 @@ int check_weight_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01) 
 
 int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, const float *x, int64_t ldx,
                 const uint8_t *y, int64_t stride_col_y, int64_t ncols, float *dst, int64_t ld_dst,
-                hipStream_t stream, const Epilogue *ep, const BatchLaunch *bl, const SumsOut *so) {
+                hipStream_t stream, const Epilogue *ep, const BatchLaunch *bl, const SumsOut *so,
+                int64_t geo_mats) {
     DeviceInfo *di = nullptr;
     int st = device_info(&di);
     if (st != Q4K_OK) return st;
     const int fused = fused_kind(ep);
     if (fused && ncols != 1) return Q4K_EINVAL;
     if (bl && ((int64_t)bl->nch > 65535 || (int64_t)bl->nsmp > 65535)) return Q4K_EUNSUPPORTED;
-    const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : 1;
+    if (geo_mats < 1 || (geo_mats > 1 && (bl || ncols != 1))) return Q4K_EINVAL;
+    const int64_t mats = bl ? (int64_t)bl->nch * bl->nsmp : geo_mats;
     // (batched: every channel's and sample's activation 16-byte aligned too)
     const bool f32_vec = x && aligned(x, 16) && ldx % 4 == 0 &&
                          (!bl || (bl->bt.x_channel % 4 == 0 && bl->bt.x_sample % 4 == 0));
     const Q6Geometry geo = pick_geometry_q6(*di, ne00, ne01, ncols, mats, fused, f32_vec, !x && y);
+    if (geo.colsplit) {  // the columns as one-column channels of one launch
+        if (bl || fused || geo.colsplit != ncols) return Q4K_EINVAL;
+        if (so) {  // parity variant: each column's launch on its own, same geometry and kernel
+            for (int64_t c = 0; c < ncols; ++c) {
+                const SumsOut sc{so->sums + c * ne01 * (ne00 / 16), nullptr};
+                st = run_gemv_q6(src0, ne00, ne01, nb01, x ? x + c * ldx : nullptr, ldx,
+                                 y ? y + c * stride_col_y * kQ81Bytes : nullptr, stride_col_y, 1, dst + c * ld_dst,
+                                 ld_dst, stream, nullptr, nullptr, &sc, ncols);
+                if (st != Q4K_OK) return st;
+            }
+            return Q4K_OK;
+        }
+        BatchLaunch cb;
+        cb.nch = (int)ncols;
+        cb.nsmp = 1;
+        cb.bt.ids = nullptr;
+        cb.bt.w_channel = 0;
+        cb.bt.w_sample = 0;
+        cb.bt.x_channel = x ? ldx : stride_col_y;
+        cb.bt.x_sample = 0;
+        cb.bt.dst_channel = ld_dst;
+        cb.bt.dst_sample = 0;
+        cb.bt.channel_ratio = (int)ncols;
+        cb.bt.sample_ratio = 1;
+        cb.bt.nchannels_y = (int)ncols;
+        cb.bt.nexperts = 1;
+        return run_gemv_q6(src0, ne00, ne01, nb01, x, ldx, y, stride_col_y, 1, dst, ld_dst, stream, nullptr, &cb);
+    }
     if (geo.lds > di->max_lds) return Q4K_EUNSUPPORTED;  // one column exceeds the LDS
     // a wave's rows (the matrix-core kernel: a workgroup's tiles; the K-split
     // kernel: a workgroup's rows and one step past them) are addressed with
@@ -857,8 +898,8 @@ static int gemv_geometry_q6(int64_t ne00, int64_t ne01, int64_t ne11, bool q81, 
     out[1] = g.waves;
     out[2] = g.grid;
     out[3] = g.lds_launch;
-    out[4] = g.nc_chunk;
-    out[5] = g.nc_chunk >= ne11 ? 1 : 0;
+    out[4] = g.colsplit ? 1 : g.nc_chunk;  // (column split: one column per channel, all in one launch)
+    out[5] = g.colsplit || g.nc_chunk >= ne11 ? 1 : 0;
     out[6] = g.ksplit ? 5 : (g.mfma_ga ? 6 : (g.mfma ? 4 : 1));
     out[7] = g.slots;
     if (q81) out[5] = 0;

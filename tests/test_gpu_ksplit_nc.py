@@ -179,19 +179,25 @@ def test_ksplit_nc_column_strides(Q, O, gpu):
 
 @pytest.mark.parametrize("M,K,N,kernel", [(14336, 4096, 2, 5), (4096, 4096, 2, 5), (1024, 4096, 2, 5),
                                           (128256, 4096, 2, 5), (4096, 8192, 2, 5), (4096, 4096, 3, 5),
-                                          (1024, 4096, 3, 1), (1024, 8192, 3, 5), (14336, 4096, 3, 1), (14336, 4096, 4, 1),
+                                          (1024, 4096, 3, 5), (1024, 8192, 3, 5), (14336, 4096, 3, 1), (14336, 4096, 4, 1),
                                           (28672, 8192, 3, 5), (28672, 8192, 4, 5), (14336, 8192, 4, 1),
                                           (4096, 14336, 2, 5), (4096, 14336, 3, 5), (4096, 14336, 4, 5),
-                                          (8192, 28672, 2, 5), (8192, 28672, 4, 1), (4096, 11008, 4, 5)])
+                                          (8192, 28672, 2, 5), (8192, 28672, 4, 1), (4096, 11008, 4, 5),
+                                          (1000, 14336, 3, 5)])
 def test_ksplit_nc_automatic_choice(Q, gpu, M, K, N, kernel):
     """The automatic geometry: the K-split kernel where it measured faster
     than the tile kernel (two columns, three columns of 8192 values up to 4
     rows per CU or of 4096 values at 5 to 16, three or four columns of 8192 values at 96 rows
     per CU or more, three or four columns of other lengths up to 16384
-    values), the tile kernel elsewhere; the pre-quantised route stays on
-    the tile kernel (same bits)."""
+    values; up to 12 rows per CU, 8 for two columns, the one-column K-split
+    kernel over the columns as channels), the tile kernel elsewhere; the
+    pre-quantised route stays on the tile kernel (same bits)."""
     g = Q.geometry(K, M, N)
-    assert g["kernel"] == kernel and g["cols_per_launch"] == N, g
+    # few rows per CU: the columns as one-column channels of one launch (one
+    # column each, on the one-column K-split kernel; not at 1000 x 14336,
+    # whose one-column channels would take the tile kernel)
+    cols = 1 if (M, K, N) in {(1024, 4096, 2), (1024, 4096, 3), (1024, 8192, 3)} else N
+    assert g["kernel"] == kernel and g["cols_per_launch"] == cols, g
     assert Q.geometry(K, M, N, route="q8_1")["kernel"] == 1
 
 

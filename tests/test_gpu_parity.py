@@ -191,7 +191,17 @@ def test_eight_wave_register_path(Q, O, gpu, M, K, N):
     activation slices of every column held in registers, and staging rounds
     issued ahead of the weights up to the column count, of which only those
     holding values are loaded (2048- and 3072-value rows need fewer).  Checked
-    against the oracle, and bit for bit against the pre-quantised launch."""
+    against the oracle, and bit for bit against the pre-quantised launch.
+    (The tile kernel forced: up to 12 rows per CU the automatic launch runs
+    the columns as one-column channels.)"""
+    Q.set_geometry_override(kernel=1)
+    try:
+        _eight_wave_register_path(Q, O, gpu, M, K, N)
+    finally:
+        Q.set_geometry_override()
+
+
+def _eight_wave_register_path(Q, O, gpu, M, K, N):
     assert Q.geometry(K, M, N)["waves_per_wg"] == 8
     wq, x = inputs(Q, M, K, N, seed=11)
     q8 = O.quantize_q8_1(x)
@@ -481,7 +491,7 @@ def test_workload_parity(Q, O, gpu, M, K, N):
     cut = (M // 3) // 16 * 16 + 5
     top = Q.op_mul_mat_vec_q(wd[:cut], K, q8d, N, row_low=0, row_high=cut).cpu().numpy()
     bot = Q.op_mul_mat_vec_q(wd[cut:], K, q8d, N, row_low=cut, row_high=M).cpu().numpy()
-    kern = {Q.geometry(K, m, N)["kernel"] for m in (M, cut, M - cut)}
+    kern = {tuple(Q.geometry(K, m, N)[f] for f in ("kernel", "cols_per_launch")) for m in (M, cut, M - cut)}
     if len(kern) == 1:
         assert np.array_equal(np.concatenate([top, bot], axis=1), y)
     else:
@@ -528,10 +538,11 @@ def test_parity_variants_cover_every_kernel(Q, gpu):
     """The workloads' launches, whose sums test_production_kernel_sums
     checks, include the K-split kernel (one column: 4096-value rows with the
     activation in registers, 14336- and 28672-value rows in the long-row
-    variant), the matrix-core kernels (128256 x 4096, eight columns; 4096 x
-    14336, eight columns, its A operand read from the Q8_1 copy), the
-    8-wave register path for several columns, 16-wave and 8-wave tile
-    launches and both staging routes.  (The block-per-lane kernel, no longer
+    variant; several columns, and the one-column kernel over the columns of
+    1024 x 4096 as channels), the matrix-core kernels (128256 x 4096, eight
+    columns; 4096 x 14336, eight columns, its A operand read from the Q8_1
+    copy), 16-wave tile launches for several columns and both staging
+    routes (the 8-wave register path: test_eight_wave_register_path).  (The block-per-lane kernel, no longer
     the automatic choice anywhere, is checked through the override in
     test_kernel_variants_against_oracle; the one-column tile kernel, which
     runs unaligned activations, the pre-quantised route and the epilogues,
@@ -544,9 +555,10 @@ def test_parity_variants_cover_every_kernel(Q, gpu):
     assert Q.geometry(4096, 14336, 1)["kernel"] == 5 and Q.geometry(4096, 128256, 1)["kernel"] == 5
     assert Q.geometry(14336, 4096, 1)["kernel"] == 5 and Q.geometry(28672, 8192, 1)["kernel"] == 5
     assert (5, 0, False) in kinds                      # K-split (the headline shape, long rows)
+    assert (5, 0, True) in kinds                       # several columns: K-split kernels, or one-column channels
     assert (4, 0, True) in kinds                       # matrix cores (128256 x 4096, eight columns)
     assert (6, 0, False) in kinds                      # matrix cores, A from the Q8_1 copy (4096 x 14336 N=8)
-    assert (1, 8, True) in kinds and (1, 16, True) in kinds   # several columns, 8 and 16 waves
+    assert (1, 16, True) in kinds                      # several columns on the tile kernel, 16 waves
 
 
 @pytest.mark.parametrize("M", [8192, 14336, 20480])

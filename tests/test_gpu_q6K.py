@@ -273,9 +273,15 @@ def test_small_result_ring_for_long_rows(Q, O, gpu, wtype, M, K, N):
     so the product runs in one launch instead of two.  With one workgroup
     (an override) each wave owns 12-38 rows, i.e. 50-150 ring entries, and
     the ring flushes mid-stream.  Outputs against the oracle, and the
-    workspace (pre-quantised) route bit for bit."""
+    workspace (pre-quantised) route bit for bit.  (The tile kernel forced:
+    at this few rows per CU the automatic launch runs the columns as
+    one-column channels.)"""
     import torch
-    geo = Q.geometry(K, M, N, wtype=wtype)
+    Q.set_geometry_override(kernel=1)
+    try:
+        geo = Q.geometry(K, M, N, wtype=wtype)
+    finally:
+        Q.set_geometry_override()
     assert geo["cols_per_launch"] == N and geo["kernel"] == 1
     if wtype == Q.GGML_TYPE_Q6_K:
         wq, x = inputs(Q, M, K, N, seed=21)
@@ -290,7 +296,7 @@ def test_small_result_ring_for_long_rows(Q, O, gpu, wtype, M, K, N):
     wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
     ws = torch.empty(Q.q8_1_bytes(K, N), dtype=torch.uint8, device=gpu)
     for wgs in (0, 1):
-        Q.set_geometry_override(workgroups=wgs)
+        Q.set_geometry_override(workgroups=wgs, kernel=1)
         try:
             y = Q.mul_mat_vec_q(wd, K, xd, wtype=wtype).cpu().numpy()
             y2 = Q.mul_mat_vec_q(wd, K, xd, workspace=ws, wtype=wtype).cpu().numpy()
