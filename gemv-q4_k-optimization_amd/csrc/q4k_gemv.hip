@@ -618,6 +618,8 @@ static bool ksplit_glu_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, 
 //  The tile kernel elsewhere: four columns of 4096 values (14336 x 4096
 //  10.97 staged against 10.68, 4096 x 4096 6.47 / 6.29), 56 rows per CU of
 //  8192 values (14336 x 8192 N=3 17.54 / 16.77, N=4 19.06 / 18.88).
+//  Up to 12 rows per CU (8 with two columns) split_columns comes first: the
+//  columns as one-column channels of one launch.
 static bool ksplit_nc_auto(int64_t K, int64_t M, int64_t N, int cus, int &tr, int &waves, int &slots,
                            int &staged) {
     const int64_t rho = (M + cus - 1) / cus;
