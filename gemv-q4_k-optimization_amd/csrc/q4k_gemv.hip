@@ -458,14 +458,18 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //    / 6.09); three or four steps in flight measured slower everywhere but
 //    at 1024 x 14336 (4096 x 14336 8.69 and 9.09 against 8.35, 14336 x 14336
 //    22.64 and 22.12 against 21.61, 1024 x 14336 at 4 rows 5.40 against
-//    5.48); at 16 rows per CU, 16 rows
+//    5.48); from 9 to 16 rows per CU, 16 rows
 //    and 16 waves, one step (4096 x 14336 8.32 / 8.54, 4096 x 11008 6.97 /
-//    7.42, 4096 x 5120 4.81 / 5.53); beyond, 8 rows, 8 waves, two steps
+//    7.42, 4096 x 5120 4.81 / 5.53, 3584 x 18944 9.91 / 11.89, 3072 x 14336
+//    7.47 / 8.02, 2816 x 11008 6.20 / 6.50, 2304 x 9216 5.77 / 6.14; 8 rows,
+//    8 waves, two steps 10.28 and 8.19 at the first two, which that rule
+//    took only with at most one row in eight idle); beyond, 8 rows, 8 waves, two steps
 //    where 8-row tiles leave at most one row in eight idle (8192 x 28672
 //    25.50 / 28.62, 14336 x 14336 21.55 / 22.46, 13824 x 5120 9.97 / 10.17,
 //    32000 x 5120 19.32 / 19.77), the tile kernel otherwise (5120 x 13824,
-//    20 rows per CU: 10.23 against 9.50) and over 160 rows per CU (not
-//    measured); rows under 4096 values as below.
+//    20 rows per CU: 10.23 against 9.50; 16 rows and 16 waves 11.31; 4608 x
+//    14336, 18 rows, 10.06 / 9.24) and over 160 rows per CU (not measured);
+//    rows under 4096 values as below.
 //  - rows of 3 to 8 blocks (768 .. 2048 values; the long-row kernel with
 //    teams of only the waves a row needs): 8 rows per step, one step in
 //    flight, 4 waves up to 16 rows per CU (512 x 2048 2.60 against 2.88 on
@@ -476,7 +480,9 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //  - rows of 9 to 14 blocks (2304 .. 3584 values): 8 rows per step, two
 //    teams of ceil(blocks / 2) waves and one step in flight (2304 x 2304
 //    3.60 / 3.82, 9216 x 2304 5.10 / 5.15, 2560 x 2560 3.62 / 3.85, 9728 x
-//    2560 5.25 / 5.41, 3072 x 3072 3.73 / 3.83, 8192 x 3072 4.89 / 5.13);
+//    2560 5.25 / 5.41, 3072 x 3072 3.73 / 3.83, 8192 x 3072 4.89 / 5.13),
+//    one team up to 8 rows per CU (2048 x 2304 3.23 against 3.30 with two,
+//    3.24 on the tile kernel);
 //    teams of 7 one per workgroup with two steps (3584 x 3584 3.94 / 4.13,
 //    18944 x 3584 8.78 / 9.40); the tile kernel up to 4 rows per CU (512 x
 //    3584 3.07 against 3.17) and over 160 (151936 x 2560 40.01 against
@@ -490,7 +496,7 @@ static bool ksplit_short_auto(int64_t K, int64_t rho, bool glu, int &tr, int &wa
         return true;
     }
     const int kt = (nb + 1) / 2;
-    waves = kt == 7 ? 7 : 2 * kt;
+    waves = kt == 7 || rho <= 8 ? kt : 2 * kt;
     if (kt == 7 && !glu) slots = 2;
     return rho > 4 && rho <= 160;
 }
@@ -505,7 +511,7 @@ static bool ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, int 
             slots = 1;
             return true;
         }
-        if (rho == 16) {
+        if (rho > 8 && rho <= 16) {
             tr = waves = 16;
             return true;
         }

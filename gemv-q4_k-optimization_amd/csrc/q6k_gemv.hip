@@ -226,9 +226,13 @@ static Q6Geometry pick_geometry_q6_ksplit(const DeviceInfo &di, int64_t K, int64
 // 4096 x 11008 9.93 / 10.44 / 10.84, 14336 x 14336 33.75 / 33.84 / 35.93;
 // with two: 2048 x 14336 7.84 / 9.17, 13824 x 5120 15.26 / 17.32, 5120 x
 // 13824 14.92 / 14.95), 4 rows, 4 waves and two steps up to 4 rows per CU
-// and 4 groups (1024 x 14336 6.26 against 6.32); three or four steps in
-// flight, 16 waves or two workgroups per CU measured slower (4096 x 14336
-// 13.29, 13.32, 13.34, 13.12 against 12.10).
+// and 4 groups (1024 x 14336 6.26 against 6.32), 16 rows and 16 waves from
+// 9 to 11 rows per CU (2304 x 9216 7.46 against 7.93 on 8 rows and 8.03 on
+// the tile kernel, 2560 x 9728 7.87 / 8.30 / 8.25; at 12 and 14 rows 8 rows
+// stay faster: 3072 x 14336 10.73 / 10.88, 3584 x 18944 14.15 / 15.19);
+// three or four steps in flight, 16 waves or two workgroups per CU measured
+// slower at 16 rows (4096 x 14336 13.29, 13.32, 13.34, 13.12 against
+// 12.10).
 // Rows of 3 to 8 blocks (768 .. 2048 values; short teams): 8 rows per
 // step, one step in flight, 4 waves up to 16 rows per CU (2048 x 768 2.88
 // against 3.49 on the tile kernel, 2048 x 2048 3.16 / 3.65), 8 beyond
@@ -248,7 +252,7 @@ static bool q6_ksplit_auto(int64_t K, int64_t M, int cus, int &tr, int &waves, i
     }
     if (K != 4096 && K != 8192) {
         const bool small = rho <= 4 && K <= 4 * 4096;
-        tr = waves = small ? 4 : 8;
+        tr = waves = small ? 4 : (rho >= 9 && rho <= 11 ? 16 : 8);
         slots = small ? 2 : 1;
         return rho <= 160;
     }
@@ -417,8 +421,11 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
         int tr = 0, kw = 0, ks = 0;
         if (fused == kFusedGate ? q6_ksplit_glu_auto(K, M, cus_m, tr, kw, ks) : q6_ksplit_auto(K, M, cus_m, tr, kw, ks)) {
             const int os = g_ovr_slots.load();
-            const Q6Geometry gk = pick_geometry_q6_ksplit(di, K, M, tr, kw, mats > 1 ? cus_m : 0,
-                                                          os >= 1 && os <= 4 ? os : ks, fused, mats > 1);
+            Q6Geometry gk = pick_geometry_q6_ksplit(di, K, M, tr, kw, mats > 1 ? cus_m : 0,
+                                                    os >= 1 && os <= 4 ? os : ks, fused, mats > 1);
+            if (!gk.ksplit && tr == 16)  // (no batched 16-row variant: the 8-row shape)
+                gk = pick_geometry_q6_ksplit(di, K, M, 8, 8, mats > 1 ? cus_m : 0, os >= 1 && os <= 4 ? os : ks,
+                                             fused, mats > 1);
             if (gk.ksplit && gk.lds <= max_lds && (mats == 1 || K >= 4096 || gk.ks_kt)) return gk;
         }
     }

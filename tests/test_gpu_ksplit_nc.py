@@ -194,9 +194,8 @@ def test_ksplit_nc_automatic_choice(Q, gpu, M, K, N, kernel):
     pre-quantised route stays on the tile kernel (same bits)."""
     g = Q.geometry(K, M, N)
     # few rows per CU: the columns as one-column channels of one launch (one
-    # column each, on the one-column K-split kernel; not at 1000 x 14336,
-    # whose one-column channels would take the tile kernel)
-    cols = 1 if (M, K, N) in {(1024, 4096, 2), (1024, 4096, 3), (1024, 8192, 3)} else N
+    # column each, on the one-column K-split kernel)
+    cols = 1 if (M, K, N) in {(1024, 4096, 2), (1024, 4096, 3), (1024, 8192, 3), (1000, 14336, 3)} else N
     assert g["kernel"] == kernel and g["cols_per_launch"] == cols, g
     assert Q.geometry(K, M, N, route="q8_1")["kernel"] == 1
 

@@ -15,8 +15,10 @@ import _common
 pytestmark = pytest.mark.gpu
 
 # (M, K, N), largest first: column chunks (28672 x 8 values do not fit the
-# LDS), the quantisation launch (14336 x 4 > 40960 values), then in-launch
-CALLS = [(300, 28672, 8), (150, 14336, 4), (64, 4096, 2)]
+# LDS), the quantisation launch (28672 x 4 > 40960 values), then in-launch;
+# 3400 rows, more per CU than the columns-as-channels launch takes (it
+# quantises each column inside its own launch)
+CALLS = [(3400, 28672, 8), (3400, 28672, 4), (64, 4096, 2)]
 
 
 def _noalloc(Q, wd, M, K, xd, N, dst):
@@ -69,15 +71,16 @@ def test_noalloc_refuses_requests_beyond_the_scratch(Q, gpu):
 
 
 def test_noalloc_graph_capture_has_kernel_nodes_only(Q, gpu):
-    """A scratch-using call (eight columns of 28672 values: column chunks on
-    a Q8_1 copy in the scratch) captured into a HIP graph on a stream of its
-    own holds kernel nodes only -- no memory-allocation, free or memset node
-    -- and its replays, with eager work between them, equal the eager call
-    bit for bit."""
+    """A scratch-using call (eight columns of 28672 values over 3400 rows,
+    more rows per CU than the columns-as-channels launch takes: column
+    chunks on a Q8_1 copy in the scratch) captured into a HIP graph on a
+    stream of its own holds kernel nodes only -- no memory-allocation, free
+    or memset node -- and its replays, with eager work between them, equal
+    the eager call bit for bit."""
     import ctypes
     import torch
     hip = ctypes.CDLL("libamdhip64.so")
-    M, K, N = 300, 28672, 8
+    M, K, N = 3400, 28672, 8
     wq = Q.quantize_rows_q4_K(_common.weights(M, K, seed=M + 1), nthreads=16)
     wd = torch.from_numpy(wq).to(gpu)
     xd = torch.from_numpy(_common.activations(N, K, seed=K + 1)).to(gpu)
