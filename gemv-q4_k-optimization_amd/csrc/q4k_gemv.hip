@@ -463,8 +463,9 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //    7.42, 4096 x 5120 4.81 / 5.53, 3584 x 18944 9.91 / 11.89, 3072 x 14336
 //    7.47 / 8.02, 2816 x 11008 6.20 / 6.50, 2304 x 9216 5.77 / 6.14; 8 rows,
 //    8 waves, two steps 10.28 and 8.19 at the first two, which that rule
-//    took only with at most one row in eight idle); beyond, 8 rows, 8 waves, two steps
-//    where 8-row tiles leave at most one row in eight idle (8192 x 28672
+//    took only with at most one row in eight idle); beyond, 8 rows, 8
+//    waves, two steps where 8-row tiles leave at most one row in eight idle
+//    (8192 x 28672
 //    25.50 / 28.62, 14336 x 14336 21.55 / 22.46, 13824 x 5120 9.97 / 10.17,
 //    32000 x 5120 19.32 / 19.77), the tile kernel otherwise (5120 x 13824,
 //    20 rows per CU: 10.23 against 9.50; 16 rows and 16 waves 11.31; 4608 x
@@ -482,11 +483,10 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
 //    3.60 / 3.82, 9216 x 2304 5.10 / 5.15, 2560 x 2560 3.62 / 3.85, 9728 x
 //    2560 5.25 / 5.41, 3072 x 3072 3.73 / 3.83, 8192 x 3072 4.89 / 5.13),
 //    one team up to 8 rows per CU (2048 x 2304 3.23 against 3.30 with two,
-//    3.24 on the tile kernel);
-//    teams of 7 one per workgroup with two steps (3584 x 3584 3.94 / 4.13,
-//    18944 x 3584 8.78 / 9.40); the tile kernel up to 4 rows per CU (512 x
-//    3584 3.07 against 3.17) and over 160 (151936 x 2560 40.01 against
-//    40.81).
+//    3.24 on the tile kernel); teams of 7 one per workgroup with two steps
+//    (3584 x 3584 3.94 / 4.13, 18944 x 3584 8.78 / 9.40); the tile kernel
+//    up to 4 rows per CU (512 x 3584 3.07 against 3.17) and over 160
+//    (151936 x 2560 40.01 against 40.81).
 static bool ksplit_short_auto(int64_t K, int64_t rho, bool glu, int &tr, int &waves, int &slots) {
     const int nb = (int)(K / kQK);
     tr = 8;
