@@ -205,6 +205,7 @@ struct Geometry {
     int ks_p = 0;       // several-column K-split kernel: columns of its reduction tree (2 or 4)
     int ks_kt = 0;      // long-row K-split kernel, rows shorter than one group: waves per team (0: 16/SBW)
     int colsplit = 0;   // several columns as one launch over one-column channels (the columns; 0: not)
+    int ks_snc = 0;     // several columns of rows shorter than one group in short teams
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
@@ -427,6 +428,78 @@ static Geometry pick_geometry_ksplit(const DeviceInfo &di, int64_t K, int64_t M,
     g.lds_launch = g.lds;
     g.nc_chunk = 1;
     return g;
+}
+
+// The several-column short-team kernel (gemv_q4k_ksplit_short_nc_kernel) for
+// N columns of rows of nb blocks: rows_per_step 8 or 4 (2 or 4 super-blocks
+// per wave), waves, workgroups (default one per CU), tiles in flight; the
+// team is the fewest waves that cover the row.  ksplit = 0 where that
+// variant is not instantiated.
+static Geometry pick_geometry_short_nc(const DeviceInfo &di, int64_t K, int64_t M, int N, int rows_per_step,
+                                       int waves, int wgs, int slots) {
+    Geometry g;
+    const int cus = di.cus > 0 ? di.cus : 1;
+    g.ksplit = rows_per_step == 4 || N > 2 ? 4 : 2;
+    g.R = 16 / g.ksplit;
+    g.ks_kt = ksplit_short_team((int)(K / kQK), g.ksplit);
+    g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 8;
+    g.slots = slots == 1 || slots == 2 ? slots : 1;
+    if (!g.ks_kt || !ksplit_short_nc_exists(N, g.ksplit, g.ks_kt, g.waves, g.slots)) {
+        g.ksplit = 0;
+        return g;
+    }
+    g.ks_long = 1;
+    g.ks_snc = 1;
+    int64_t grid = wgs > 0 ? wgs : cus;
+    if (grid > M) grid = M;
+    g.grid = grid < 1 ? 1 : (int)grid;
+    g.rows_base = (int)(M / g.grid);
+    g.rows_extra = (int)(M % g.grid);
+    g.lds = ksplit_short_nc_lds_bytes(g.rows_base + (g.rows_extra ? 1 : 0), N, g.ksplit, g.ks_kt, g.waves);
+    g.lds_launch = g.lds;
+    if (g.lds > (di.max_lds > 0 ? di.max_lds : 65536)) g.ksplit = 0;
+    g.nc_chunk = N;
+    return g;
+}
+
+// Whether N columns of rows of K values can take the several-column
+// short-team kernel: their tile-kernel tree reduces to the one-column tree
+// (rows of 3 to 8 blocks with two columns, 3 or 4 with three or four) and
+// the tile kernel launches all N at once.
+static bool short_nc_ok(int64_t K, int N, int tile_nc) {
+    const int64_t nb = K / kQK;
+    return tile_nc == N && K % kQK == 0 && nb >= 3 && nb <= (N == 2 ? 8 : 4) && N >= 2 && N <= 4;
+}
+
+// The several-column short-team kernel's automatic launch shape (aligned F32
+// columns whose rows short_nc_ok admits), one workgroup per CU; false where
+// the column split or the tile kernel measured faster.  Rows per CU rho:
+// two columns at 2 super-blocks per wave, 4 waves to rho 16, 8 to 24, then
+// two tiles in flight (16 waves at rho 41 to 48); three or four columns at
+// 4 per wave, 4 waves, from rho 13 (below: the column split), two tiles in
+// flight from rho 17.  Measured on MI355X, us, before -> after: two columns
+// 512 x 2048 3.09 -> 2.86, 2048 x 2048 4.14 -> 3.05, 1536 x 1536 4.04 ->
+// 3.03, 2048 x 1024 3.59 -> 2.98, 3072 x 1024 4.22 -> 3.05, 4096 x 768
+// 4.38 -> 3.04, 6144 x 2048 5.22 -> 4.09, 8192 x 2048 5.63 -> 4.53, 8960 x
+// 1536 5.75 -> 4.62, 11008 x 2048 6.42 -> 5.22, 12288 x 768 6.52 -> 4.11,
+// 14336 x 1024 6.80 -> 4.50, 16384 x 2048 7.88 -> 5.98; three columns 4096
+// x 768 4.87 -> 4.11, 5120 x 1024 5.25 -> 4.65, 6144 x 1024 5.51 -> 4.67,
+// 8192 x 768 6.39 -> 4.66; four columns 4096 x 768 5.18 -> 4.79, 5120 x
+// 1024 5.54 -> 5.47, 6144 x 1024 5.81 -> 5.48, 8192 x 768 6.95 -> 5.48.
+// Not measured past rho 64 (two columns) or 32 (three or four).
+static bool short_nc_auto(int64_t M, int N, int cus, int &rows_per_step, int &waves, int &slots) {
+    const int64_t rho = (M + cus - 1) / cus;
+    slots = 1;
+    if (N == 2) {
+        rows_per_step = 8;
+        waves = rho <= 16 ? 4 : (rho > 40 && rho <= 48 ? 16 : 8);
+        if (rho > 24 && waves == 8) slots = 2;
+        return rho <= 64;
+    }
+    rows_per_step = 4;
+    waves = 4;
+    if (rho > 16) slots = 2;
+    return rho > 12 && rho <= 32;
 }
 
 // The K-split kernel's automatic launch shape for one aligned F32 column of
@@ -719,6 +792,17 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const int orows = g_ovr_rows.load(), owaves = g_ovr_waves.load(), owgs = g_ovr_wgs.load();
     const int okern = g_ovr_kernel.load();
     const int rpw = bpl_rows_per_pass(K / kQK);
+    // several columns of rows shorter than one group: short teams (aligned
+    // F32 columns, automatic only; before the column split, which these
+    // shapes measured slower)
+    if (!fused && mats == 1 && okern == 0 && orows == 0 && owaves == 0 && owgs == 0 && f32_vec && N >= 2 &&
+        N <= 4 && short_nc_ok(K, (int)N, nc)) {
+        int tr = 0, w = 0, s = 0;
+        if (short_nc_auto(M, (int)N, cus, tr, w, s)) {
+            const Geometry gs = pick_geometry_short_nc(di, K, M, (int)N, tr, w, 0, s);
+            if (gs.ksplit) return gs;
+        }
+    }
     // several columns over few rows: one-column channels (automatic only;
     // where the aligned F32 column takes the K-split kernel, so both routes
     // decide alike)
@@ -749,6 +833,12 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     const bool ksn_ok = N >= 2 && N <= 4 && !fused && mats == 1 && f32_vec && K <= 8 * 4096 &&
                         (nc == N || (nc == 2 && N == 4));
     const int ksn_p = nc <= 2 ? 2 : 4;
+    // several columns of rows shorter than one group: short teams
+    const bool snc_ok = ksn_ok && short_nc_ok(K, (int)N, nc);
+    if (snc_ok && okern == 5) {
+        const Geometry gs = pick_geometry_short_nc(di, K, M, (int)N, orows, owaves, owgs, g_ovr_slots.load());
+        if (gs.ksplit) return gs;
+    }
     if (ksn_ok && okern == 5)
         return pick_geometry_ksplit(di, K, M, orows, owaves, owgs, g_ovr_slots.load(), (int)N, 1, ksn_p);
     if (ks_ok && okern == 5) {
@@ -1096,7 +1186,11 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         p.ring_off = lds_bytes(p.K, nc);
     } else if (geo.ksplit) {
         if (!p.x || !p.vec_ok) return Q4K_EINVAL;
-        if (nc > 1) {
+        if (nc > 1 && geo.ks_snc) {
+            if (nc != geo.nc_chunk) return Q4K_EINVAL;
+            fn = q4k_ksplit_short_nc_kernel(nc, geo.ksplit, geo.ks_kt, geo.waves, geo.slots, p.sums != nullptr);
+            p.ring_off = ksplit_short_nc_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), nc, geo.ks_kt);
+        } else if (nc > 1) {
             if (nc != geo.nc_chunk) return Q4K_EINVAL;
             if (geo.ks_long)
                 fn = p.sums ? q4k_ksplit_nc_long_sums_kernel(nc, geo.ks_p, geo.ksplit, geo.waves, geo.slots)

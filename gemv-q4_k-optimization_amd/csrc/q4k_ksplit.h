@@ -604,6 +604,176 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_long_kernel(Q4K_
     }
 }
 
+// ------------------------------------------------------------------------
+// Several columns of rows shorter than one group, in short teams (one
+// partial group: nb <= 8 blocks for two columns, nb <= 4 for three or four).
+// The several-column tile kernel sums a wave's lanes first over super-blocks
+// g and g^8 (and, with three or four columns, g^4), then over the chunks,
+// then over the low bits of g (column_sums).  Positions past the row hold
+// exact zeros there (a lane's accumulator is never -0), so for such rows the
+// g^8 and g^4 levels add +0 and the tree left is the one-column tree: the
+// chunks, then pairs (2t, 2t+1) of positions.  So this kernel is the
+// one-column short-team kernel with NC accumulators per lane: each wave
+// stages its slice of every column once (ks_stage_lds), each step loads the
+// weights once and accumulates every column, and the (row, column, slice)
+// partials meet in the balanced tree over the slices.
+// ------------------------------------------------------------------------
+
+// LDS bytes of the partials (rows x NC x KT floats, padded to 16 bytes).
+__host__ __device__ constexpr int ksplit_short_nc_part_bytes(int rows_per_wg, int nc, int kt) {
+    return (rows_per_wg * nc * kt * 4 + 15) / 16 * 16;
+}
+__host__ __device__ constexpr int ksplit_short_nc_lds_bytes(int rows_per_wg, int nc, int sbw, int kt, int waves) {
+    return ksplit_short_nc_part_bytes(rows_per_wg, nc, kt) + waves * nc * ks_slice_bytes(sbw);
+}
+
+// NC: columns (2..4), SBW: super-blocks per wave, WAVES: waves per
+// workgroup (whole teams of KT), S: row tiles in flight per wave.  SUMS: the
+// parity variant (every lane's int32 sub-block sums and the activation's
+// block sums, per column).  p.ring_off: LDS offset of the wave areas.
+template <int NC, int SBW, int WAVES, int S, int KT, bool SUMS = false>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_short_nc_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    constexpr int KW = 16 / SBW;
+    constexpr int TR = 16 / SBW;
+    constexpr int TEAMS = WAVES / KT;
+    constexpr int V = 4 * SBW;
+    static_assert(NC >= 2 && NC <= 4 && TEAMS >= 1 && WAVES % KT == 0 && KT < KW, "short teams, 2-4 columns");
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    float *part = reinterpret_cast<float *>(lds);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slice = wave % KT, team = wave / KT;
+    const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1), j = lane & 3;
+
+    const int b = (int)blockIdx.x;
+    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
+    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int nt = (n + TR - 1) / TR;
+    const int tq = nt / TEAMS, trem = nt - tq * TEAMS;
+    const int tb = team * tq + min(team, trem);
+    const int ntiles = tq + (team < trem ? 1 : 0);
+
+    // 1. the slice of every column, issued first; past the row: zeros
+    float xv[NC][V];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x + (int64_t)c * p.ldx, (uint32_t)p.K * 4u);
+        const uint32_t off = (uint32_t)(((SBW * slice) * kQK + lane * V) * 4);
+#pragma unroll
+        for (int k = 0; k < V / 4; ++k) {
+            // the whole vector is cast (see the one-column long-row kernel)
+            const f32x4 a = __builtin_bit_cast(f32x4, load16(rx, off + 16u * k));
+            xv[c][4 * k] = a[0];
+            xv[c][4 * k + 1] = a[1];
+            xv[c][4 * k + 2] = a[2];
+            xv[c][4 * k + 3] = a[3];
+        }
+    }
+
+    // 2. the first S tiles' weights (rows past the workgroup's share: zeros)
+    const __amdgpu_buffer_rsrc_t rsw = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    const int kb0 = SBW * slice + s;  // the lane's super-block
+    const uint32_t lh = (uint32_t)r * (uint32_t)p.row_stride + (uint32_t)(kb0 * kBlockBytes);
+    const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
+    const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
+    auto load_tile = [&](int t, RowRegs &w) {
+        const bool ok = t < ntiles && kb0 < p.nb;
+        const uint32_t base = (uint32_t)(tb + t) * tile_bytes;
+        const uint32_t oh = ok ? base + lh : kOOB;
+        const uint32_t oq = ok ? base + lq : kOOB;
+        w.h = load16(rsw, oh);
+        w.q0 = load16(rsw, oq);
+        w.q1 = load16(rsw, oq + 16u);
+    };
+    int tk[S];
+    RowRegs w[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+        tk[k] = k;
+        load_tile(k, w[k]);
+    }
+
+    // 3. quantise every column's slice into the wave's LDS areas
+    uint8_t *area = lds + p.ring_off + wave * NC * ks_slice_bytes(SBW);
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        ks_stage_lds<SBW>(xv[c], lane, area + c * ks_slice_bytes(SBW),
+                          SUMS ? p.sq + (int64_t)c * (p.K / 32) : nullptr, SBW * slice * 8, p.K / 32);
+    // lanes read what other lanes of the wave wrote
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    Lane ln;
+    ln.lane = lane;
+    ln.g = kb0;
+    ln.j = j;
+    ln.sel = make_scale_sel(j);
+    // 4. the tiles, S in flight
+    int remaining = ntiles;
+    if (remaining > 0) {
+        for (;;) {
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                const RowScales sc = row_scales(w[k], ln);
+                const int rl = (tb + tk[k]) * TR + r;
+                float acc[NC];
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    acc[c] = 0.0f;
+                    const LaneAct a = ks_read_lds(area + c * ks_slice_bytes(SBW), SBW, s, j);
+                    int sa, sb;
+                    accumulate(w[k], sc, a, acc[c], sa, sb);
+                    if constexpr (SUMS) {
+                        if (tk[k] < ntiles && rl < n && kb0 < p.nb) {
+                            int32_t *o = p.sums + ((int64_t)c * p.M + wg_beg + rl) * (p.K / 32) + kb0 * 8 + 2 * j;
+                            o[0] = sa;
+                            o[1] = sb;
+                        }
+                    }
+                }
+                const bool wr = ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const float q = ks_reduce<SBW>(acc[c]);
+                    if (wr) part[(rl * NC + c) * KT + slice] = q;
+                }
+                tk[k] += S;
+                load_tile(tk[k], w[k]);
+            }
+            remaining -= S;
+            if (remaining <= 0) break;
+        }
+    }
+    __syncthreads();
+    // 5. each (row, column): the balanced tree over the 16/SBW slice sums
+    //    (+0 for the slices past the team)
+    for (int e = (int)threadIdx.x; e < n * NC; e += kWave * WAVES) {
+        const int row = e / NC, c = e - row * NC;
+        float q[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) q[k] = k < KT ? part[(row * NC + c) * KT + k] : 0.0f;
+#pragma unroll
+        for (int h = KW / 2; h >= 1; h /= 2)
+#pragma unroll
+            for (int t = 0; t < h; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+        p.dst[(int64_t)c * p.ld_dst + wg_beg + row] = q[0];
+    }
+}
+
+// The instantiated several-column short-team variants: two columns at 2 or
+// 4 super-blocks per wave for rows of 5 to 8 blocks (teams of 4 or 2) and
+// of 3 or 4 (teams of 2 or 1), three or four columns at 4 per wave for rows
+// of 3 or 4 blocks (teams of 1); 4, 8 or 16 waves; one or two tiles in
+// flight.
+constexpr bool ksplit_short_nc_exists(int nc, int sbw, int kt, int waves, int slots) {
+    const bool shape = nc == 2 ? ((sbw == 2 && (kt == 2 || kt == 4)) || (sbw == 4 && (kt == 1 || kt == 2)))
+                               : ((nc == 3 || nc == 4) && sbw == 4 && kt == 1);
+    return shape && (waves == 4 || waves == 8 || waves == 16) && waves % kt == 0 && (slots == 1 || slots == 2);
+}
+
 // LDS bytes of a long-row K-split launch: the partials, padded to 16 bytes,
 // then every wave's slice of every group (nw: 2 with a gate weight).
 // (kt: waves per team, 0 for 16/sbw).

@@ -87,6 +87,39 @@ const void *short_kernel(int sbw, int kt, int waves, int slots, bool sums, int e
 const void *q4k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
     return short_kernel<false>(sbw, kt, waves, slots, sums, epi, batch);
 }
+
+namespace {
+template <int NC, int SBW, int KT>
+const void *short_nc_sym(int waves, int slots, bool sums) {
+    auto by_s = [&](auto w_c) -> const void * {
+        constexpr int W = decltype(w_c)::value;
+        auto pick = [&](auto s_c) -> const void * {
+            constexpr int S = decltype(s_c)::value;
+            if constexpr (ksplit_short_nc_exists(NC, SBW, KT, W, S))
+                return sums ? reinterpret_cast<const void *>(&gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, true>)
+                            : reinterpret_cast<const void *>(&gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, false>);
+            return nullptr;
+        };
+        if (slots == 1) return pick(std::integral_constant<int, 1>{});
+        if (slots == 2) return pick(std::integral_constant<int, 2>{});
+        return nullptr;
+    };
+    if (waves == 4) return by_s(std::integral_constant<int, 4>{});
+    if (waves == 8) return by_s(std::integral_constant<int, 8>{});
+    if (waves == 16) return by_s(std::integral_constant<int, 16>{});
+    return nullptr;
+}
+}  // namespace
+
+const void *q4k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums) {
+    if (nc == 2 && sbw == 2 && kt == 2) return short_nc_sym<2, 2, 2>(waves, slots, sums);
+    if (nc == 2 && sbw == 2 && kt == 4) return short_nc_sym<2, 2, 4>(waves, slots, sums);
+    if (nc == 2 && sbw == 4 && kt == 1) return short_nc_sym<2, 4, 1>(waves, slots, sums);
+    if (nc == 2 && sbw == 4 && kt == 2) return short_nc_sym<2, 4, 2>(waves, slots, sums);
+    if (nc == 3 && sbw == 4 && kt == 1) return short_nc_sym<3, 4, 1>(waves, slots, sums);
+    if (nc == 4 && sbw == 4 && kt == 1) return short_nc_sym<4, 4, 1>(waves, slots, sums);
+    return nullptr;
+}
 #else
 const void *q6k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
     return short_kernel<true>(sbw, kt, waves, slots, sums, epi, batch);
