@@ -472,21 +472,25 @@ static bool short_nc_ok(int64_t K, int N, int tile_nc) {
 }
 
 // The several-column short-team kernel's automatic launch shape (aligned F32
-// columns whose rows short_nc_ok admits), one workgroup per CU; false where
-// the column split or the tile kernel measured faster.  Rows per CU rho:
-// two columns at 2 super-blocks per wave, 4 waves to rho 16, 8 to 24, then
-// two tiles in flight (16 waves at rho 41 to 48); three or four columns at
-// 4 per wave, 4 waves, from rho 13 (below: the column split), two tiles in
-// flight from rho 17.  Measured on MI355X, us, before -> after: two columns
-// 512 x 2048 3.09 -> 2.86, 2048 x 2048 4.14 -> 3.05, 1536 x 1536 4.04 ->
-// 3.03, 2048 x 1024 3.59 -> 2.98, 3072 x 1024 4.22 -> 3.05, 4096 x 768
-// 4.38 -> 3.04, 6144 x 2048 5.22 -> 4.09, 8192 x 2048 5.63 -> 4.53, 8960 x
-// 1536 5.75 -> 4.62, 11008 x 2048 6.42 -> 5.22, 12288 x 768 6.52 -> 4.11,
-// 14336 x 1024 6.80 -> 4.50, 16384 x 2048 7.88 -> 5.98; three columns 4096
-// x 768 4.87 -> 4.11, 5120 x 1024 5.25 -> 4.65, 6144 x 1024 5.51 -> 4.67,
-// 8192 x 768 6.39 -> 4.66; four columns 4096 x 768 5.18 -> 4.79, 5120 x
-// 1024 5.54 -> 5.47, 6144 x 1024 5.81 -> 5.48, 8192 x 768 6.95 -> 5.48.
-// Not measured past rho 64 (two columns) or 32 (three or four).
+// columns whose rows short_nc_ok admits), one workgroup per CU; false where the
+// column split or the tile kernel measured faster.  Rows per CU rho: two
+// columns at 2 super-blocks per wave, 4 waves to rho 16, 8 to 24, then two
+// tiles in flight (16 waves at rho 41 to 48); three or four columns at 4 per
+// wave, 4 waves, from rho 13 (below: the column split), two tiles in flight
+// from rho 17.  Up to rho 512 (two columns) or 64 (three or four).  Measured on
+// MI355X, us, before -> after: two columns 512 x 2048 3.09 -> 2.86, 2048 x 2048
+// 4.14 -> 3.05, 1536 x 1536 4.04 -> 3.03, 2048 x 1024 3.59 -> 2.98, 3072 x 1024
+// 4.22 -> 3.05, 4096 x 768 4.38 -> 3.04, 6144 x 2048 5.22 -> 4.09, 8192 x 2048
+// 5.63 -> 4.53, 8960 x 1536 5.75 -> 4.62, 11008 x 2048 6.42 -> 5.22, 12288 x
+// 768 6.52 -> 4.11, 14336 x 1024 6.80 -> 4.50, 16384 x 2048 7.88 -> 5.98; three
+// columns 4096 x 768 4.87 -> 4.11, 5120 x 1024 5.25 -> 4.65, 6144 x 1024 5.51
+// -> 4.67, 8192 x 768 6.39 -> 4.66; four columns 4096 x 768 5.18 -> 4.79, 5120
+// x 1024 5.54 -> 5.47, 6144 x 1024 5.81 -> 5.48, 8192 x 768 6.95 -> 5.48. Many
+// rows per CU: two columns 24576 x 2048 9.57 -> 7.59, 32768 x 2048 11.29 ->
+// 8.89, 65536 x 2048 19.01 -> 15.26, 128256 x 2048 32.49 -> 27.50, 32768 x 768
+// 10.71 -> 5.55; three columns 12288 x 1024 7.83 -> 5.70, 16384 x 768 8.08 ->
+// 5.72; four 12288 x 1024 8.51 -> 6.74, 16384 x 768 9.10 -> 6.80.  Not measured
+// past 501 rows per CU (two columns) or 64 (three or four).
 static bool short_nc_auto(int64_t M, int N, int cus, int &rows_per_step, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
@@ -494,12 +498,12 @@ static bool short_nc_auto(int64_t M, int N, int cus, int &rows_per_step, int &wa
         rows_per_step = 8;
         waves = rho <= 16 ? 4 : (rho > 40 && rho <= 48 ? 16 : 8);
         if (rho > 24 && waves == 8) slots = 2;
-        return rho <= 64;
+        return rho <= 512;
     }
     rows_per_step = 4;
     waves = 4;
     if (rho > 16) slots = 2;
-    return rho > 12 && rho <= 32;
+    return rho > 12 && rho <= 64;
 }
 
 // The K-split kernel's automatic launch shape for one aligned F32 column of
