@@ -96,8 +96,9 @@ const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense);
 // where ksplit_short_exists says it is not instantiated.
 const void *q4k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch);
 const void *q6k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch);
-// The several-column short-team kernel (q4k_short.hip; Q4_K), or null.
+// The several-column short-team kernels (q4k_short.hip, q6k_short.hip), or null.
 const void *q4k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums);
+const void *q6k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums);
 
 // Q6_K weight checks and launch (q6k_gemv.hip), for the type-dispatching
 // entry points of q4k_gemv.hip.

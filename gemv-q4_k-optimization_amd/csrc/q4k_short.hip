@@ -5,7 +5,9 @@
 // (ksplit_short_team).  Instantiated in translation units of
 // their own (this one with Q6 = false for Q4_K, q6k_short.hip for Q6_K), in
 // the shapes ksplit_short_exists lists: plain, parity (SUMS), fused (bias;
-// gate weight + GLU) and batched launches.
+// gate weight + GLU) and batched launches; with them the several-column
+// short-team kernels (two to four F32 columns, plain and parity) in the
+// shapes ksplit_short_nc_exists lists.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -83,21 +85,21 @@ const void *short_kernel(int sbw, int kt, int waves, int slots, bool sums, int e
 
 }  // namespace
 
-#ifndef Q4K_SHORT_Q6
-const void *q4k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
-    return short_kernel<false>(sbw, kt, waves, slots, sums, epi, batch);
-}
-
 namespace {
-template <int NC, int SBW, int KT>
+template <bool Q6, int NC, int SBW, int KT>
 const void *short_nc_sym(int waves, int slots, bool sums) {
     auto by_s = [&](auto w_c) -> const void * {
         constexpr int W = decltype(w_c)::value;
         auto pick = [&](auto s_c) -> const void * {
             constexpr int S = decltype(s_c)::value;
-            if constexpr (ksplit_short_nc_exists(NC, SBW, KT, W, S))
-                return sums ? reinterpret_cast<const void *>(&gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, true>)
-                            : reinterpret_cast<const void *>(&gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, false>);
+            if constexpr (ksplit_short_nc_exists(NC, SBW, KT, W, S)) {
+                if constexpr (Q6)
+                    return sums ? reinterpret_cast<const void *>(&gemv_q6k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, true>)
+                                : reinterpret_cast<const void *>(&gemv_q6k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, false>);
+                else
+                    return sums ? reinterpret_cast<const void *>(&gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, true>)
+                                : reinterpret_cast<const void *>(&gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, false>);
+            }
             return nullptr;
         };
         if (slots == 1) return pick(std::integral_constant<int, 1>{});
@@ -109,20 +111,32 @@ const void *short_nc_sym(int waves, int slots, bool sums) {
     if (waves == 16) return by_s(std::integral_constant<int, 16>{});
     return nullptr;
 }
+
+template <bool Q6>
+const void *short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums) {
+    if (nc == 2 && sbw == 2 && kt == 2) return short_nc_sym<Q6, 2, 2, 2>(waves, slots, sums);
+    if (nc == 2 && sbw == 2 && kt == 4) return short_nc_sym<Q6, 2, 2, 4>(waves, slots, sums);
+    if (nc == 2 && sbw == 4 && kt == 1) return short_nc_sym<Q6, 2, 4, 1>(waves, slots, sums);
+    if (nc == 2 && sbw == 4 && kt == 2) return short_nc_sym<Q6, 2, 4, 2>(waves, slots, sums);
+    if (nc == 3 && sbw == 4 && kt == 1) return short_nc_sym<Q6, 3, 4, 1>(waves, slots, sums);
+    if (nc == 4 && sbw == 4 && kt == 1) return short_nc_sym<Q6, 4, 4, 1>(waves, slots, sums);
+    return nullptr;
+}
 }  // namespace
 
+#ifndef Q4K_SHORT_Q6
+const void *q4k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
+    return short_kernel<false>(sbw, kt, waves, slots, sums, epi, batch);
+}
 const void *q4k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums) {
-    if (nc == 2 && sbw == 2 && kt == 2) return short_nc_sym<2, 2, 2>(waves, slots, sums);
-    if (nc == 2 && sbw == 2 && kt == 4) return short_nc_sym<2, 2, 4>(waves, slots, sums);
-    if (nc == 2 && sbw == 4 && kt == 1) return short_nc_sym<2, 4, 1>(waves, slots, sums);
-    if (nc == 2 && sbw == 4 && kt == 2) return short_nc_sym<2, 4, 2>(waves, slots, sums);
-    if (nc == 3 && sbw == 4 && kt == 1) return short_nc_sym<3, 4, 1>(waves, slots, sums);
-    if (nc == 4 && sbw == 4 && kt == 1) return short_nc_sym<4, 4, 1>(waves, slots, sums);
-    return nullptr;
+    return short_nc_kernel<false>(nc, sbw, kt, waves, slots, sums);
 }
 #else
 const void *q6k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
     return short_kernel<true>(sbw, kt, waves, slots, sums, epi, batch);
+}
+const void *q6k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums) {
+    return short_nc_kernel<true>(nc, sbw, kt, waves, slots, sums);
 }
 #endif
 

@@ -101,6 +101,7 @@ struct Q6Geometry {
     int ks_nc_p = 0; // several-column K-split kernel: columns of its reduction tree (2 or 4; 0: not it)
     int ks_kt = 0;   // long-row K-split kernel, rows shorter than one group: waves per team (0: 16/SBW)
     int colsplit = 0; // several columns as one launch over one-column channels (the columns; 0: not)
+    int ks_snc = 0;   // several columns of rows shorter than one group in short teams
 };
 
 // Columns per launch of the tile kernel for N columns of K values (halved
@@ -145,6 +146,39 @@ static Q6Geometry pick_geometry_q6_ksplit_nc(const DeviceInfo &di, int64_t K, in
             ksplit_nc_part_bytes(g.rows_base + (g.rows_extra ? 1 : 0), N, g.ksplit);
     g.lds_launch = g.lds;
     g.nc_chunk = N;
+    return g;
+}
+
+// The several-column short-team kernel (gemv_q6k_ksplit_short_nc_kernel)
+// for N columns of rows of K values: rows_per_step 8 or 4 (2 or 4
+// super-blocks per wave; three or four columns: 4), waves, workgroups
+// (default one per CU), tiles in flight; ksplit = 0 where the rows do not
+// qualify (3 to 8 blocks with two columns, 3 or 4 with three or four), the
+// variant is not instantiated or its LDS does not fit.
+static Q6Geometry pick_geometry_q6_short_nc(const DeviceInfo &di, int64_t K, int64_t M, int N, int rows_per_step,
+                                            int waves, int wgs, int slots) {
+    Q6Geometry g;
+    const int cus = di.cus > 0 ? di.cus : 1;
+    const int64_t nb = K / kQK;
+    if (K % kQK || nb < 3 || nb > (N == 2 ? 8 : 4) || N < 2 || N > 4) return g;
+    g.ksplit = rows_per_step == 4 || N > 2 ? 4 : 2;
+    g.ks_tr = 16 / g.ksplit;
+    g.ks_snc = ksplit_short_team((int)nb, g.ksplit);
+    g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 8;
+    g.slots = slots == 1 || slots == 2 ? slots : 1;
+    if (!g.ks_snc || !ksplit_short_nc_exists(N, g.ksplit, g.ks_snc, g.waves, g.slots)) {
+        g.ksplit = 0;
+        return g;
+    }
+    int64_t grid = wgs > 0 ? wgs : cus;
+    if (grid > M) grid = M;
+    g.grid = grid < 1 ? 1 : (int)grid;
+    g.rows_base = (int)(M / g.grid);
+    g.rows_extra = (int)(M % g.grid);
+    g.lds = q6_ksplit_short_nc_lds_bytes(g.rows_base + (g.rows_extra ? 1 : 0), N, g.ksplit, g.ks_snc, g.waves);
+    g.lds_launch = g.lds;
+    g.nc_chunk = N;
+    if (g.lds > (di.max_lds > 0 ? di.max_lds : 65536)) g.ksplit = 0;
     return g;
 }
 
@@ -365,12 +399,42 @@ static bool q6_ksplit_glu_auto(int64_t K, int64_t M, int cus, int &tr, int &wave
     return true;
 }
 
+// The several-column short-team kernel's automatic launch shape (aligned F32
+// columns of rows that pick_geometry_q6_short_nc admits), one workgroup per
+// CU; false where the column split or the tile kernel measured faster.  Rows
+// per CU rho: 4 waves, one tile in flight up to rho 16, two beyond; two
+// columns at 2 super-blocks per wave up to rho 512, three or four at 4 from
+// rho 13 (below: the column split) to 64.  Measured on MI355X, us, before ->
+// after: two columns 512 x 2048 3.46 -> 3.22, 2048 x 2048 4.50 -> 3.33,
+// 8192 x 2048 7.37 -> 5.21, 16384 x 768 10.38 -> 4.89, 128256 x 2048 62.59
+// -> 40.44; three columns 4096 x 768 5.07 -> 4.23; four 8192 x 768 7.96 ->
+// 5.74.
+static bool q6_short_nc_auto(int64_t M, int N, int cus, int &rows_per_step, int &waves, int &slots) {
+    const int64_t rho = (M + cus - 1) / cus;
+    rows_per_step = N == 2 ? 8 : 4;
+    waves = 4;
+    slots = rho > 16 ? 2 : 1;
+    return N == 2 ? rho <= 512 : rho > 12 && rho <= 64;
+}
+
 static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int64_t mats = 1,
                                    int fused = kFusedNone, bool f32_vec = true, bool q81 = false) {
     Q6Geometry g;
     const int max_lds = di.max_lds > 0 ? di.max_lds : 65536;
     const int cus = di.cus > 0 ? di.cus : 1;
     const int okern = g_ovr_kernel.load();
+    // several columns of rows shorter than one group: short teams (aligned
+    // F32 columns, the tile kernel launching all N at once; automatic only,
+    // before the column split, which these shapes measured slower)
+    if (fused == kFusedNone && mats == 1 && okern == 0 && g_ovr_rows.load() == 0 && g_ovr_waves.load() == 0 &&
+        g_ovr_wgs.load() == 0 && f32_vec && N >= 2 && N <= 4) {
+        bool dense = false;
+        int tr = 0, w = 0, sl = 0;
+        if (q6_tile_chunk(K, N, max_lds, dense) == N && !dense && q6_short_nc_auto(M, (int)N, cus, tr, w, sl)) {
+            const Q6Geometry gs = pick_geometry_q6_short_nc(di, K, M, (int)N, tr, w, 0, sl);
+            if (gs.ksplit) return gs;
+        }
+    }
     // several columns over few rows per CU: one launch of one-column channels
     // (split_columns; automatic only)
     if (fused == kFusedNone && mats == 1 && okern == 0 && g_ovr_rows.load() == 0 && g_ovr_waves.load() == 0 &&
@@ -407,6 +471,13 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
     const bool ksn_ok = N >= 2 && N <= 4 && mats == 1 && fused == kFusedNone && f32_vec && K <= 8 * 4096 &&
                         !tdense && (tchunk == N || (tchunk == 2 && N == 4));
     const int ksn_p = tchunk <= 2 ? 2 : 4;
+    // several columns of rows shorter than one group: short teams (the tile
+    // kernel launching all N columns at once)
+    if (ksn_ok && tchunk == N && okern == 5) {
+        const Q6Geometry gs = pick_geometry_q6_short_nc(di, K, M, (int)N, g_ovr_rows.load(), g_ovr_waves.load(),
+                                                        g_ovr_wgs.load(), g_ovr_slots.load());
+        if (gs.ksplit) return gs;
+    }
     if (ksn_ok && okern == 5)
         return pick_geometry_q6_ksplit_nc(di, K, M, g_ovr_rows.load(), g_ovr_waves.load(), g_ovr_wgs.load(),
                                           g_ovr_slots.load(), (int)N, ksn_p);
@@ -683,7 +754,8 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.glu_op = ep->glu_op;
         }
         const int epi = fused == kFusedGate ? kEpiGlu : (fused == kFusedBias ? kEpiBias : kEpiNone);
-        const void *fn = geo.ks_nc_p  ? q6_ksplit_nc_kernel<false>(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
+        const void *fn = geo.ks_snc ? q6k_ksplit_short_nc_kernel(nc, geo.ksplit, geo.ks_snc, geo.waves, geo.slots, false)
+                         : geo.ks_nc_p  ? q6_ksplit_nc_kernel<false>(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
                          : geo.ks_kt
                              ? q6k_ksplit_short_kernel(geo.ksplit, geo.ks_kt, geo.waves, geo.slots, false, epi, bl != nullptr)
                          : geo.ksplit && bl && fused == kFusedGate
@@ -702,9 +774,12 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
                          : geo.mfma ? q6_mfma_kernel_for(nc, geo.waves)
                          : bl       ? q6_kernel_for<true>(nc, geo.waves, geo.prologue, geo.slots, fused, dense)
                                     : q6_kernel_for<false>(nc, geo.waves, geo.prologue, geo.slots, fused, dense);
-        if (geo.ksplit && (nc != (geo.ks_nc_p ? geo.nc_chunk : 1) || ((fused || bl) && geo.ks_nc_p) || !p.x || !p.vec_ok))
+        const bool several = geo.ks_nc_p || geo.ks_snc;
+        if (geo.ksplit && (nc != (several ? geo.nc_chunk : 1) || ((fused || bl) && several) || !p.x || !p.vec_ok))
             return Q4K_EINVAL;
         if (geo.ks_nc_p) p.ring_off = q6_ksn_stage_bytes(p.K, nc);
+        if (geo.ks_snc)
+            p.ring_off = ksplit_short_nc_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), nc, geo.ks_snc);
         if (geo.mfma) {
             if (fused || bl) return Q4K_EINVAL;
             if (geo.mfma_ga && (p.x || !p.y)) return Q4K_EINVAL;  // GA reads the Q8_1 buffer
@@ -713,7 +788,8 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         }
         if (so) {  // parity variant: this chunk's columns of the group sums
             if (fused || bl) return Q4K_EINVAL;
-            fn = geo.ks_nc_p  ? q6k_ksplit_nc_sums_kernel(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
+            fn = geo.ks_snc ? q6k_ksplit_short_nc_kernel(nc, geo.ksplit, geo.ks_snc, geo.waves, geo.slots, true)
+                 : geo.ks_nc_p  ? q6k_ksplit_nc_sums_kernel(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
                  : geo.ks_kt    ? q6k_ksplit_short_kernel(geo.ksplit, geo.ks_kt, geo.waves, geo.slots, true, kEpiNone, false)
                  : geo.ks_long  ? q6k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)
                  : geo.ksplit ? q6k_ksplit_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)

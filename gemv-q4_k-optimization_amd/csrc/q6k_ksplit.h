@@ -450,6 +450,150 @@ __host__ __device__ constexpr int q6_ksplit_long_lds_bytes(int rows_per_wg, int 
     return ksplit_long_part_bytes(rows_per_wg, sbw, nw, kt) + waves * G * q6_ks_slice_bytes(sbw);
 }
 
+// Several Q6_K columns of rows shorter than one group in short teams (two
+// columns of rows of 3 to 8 blocks, three or four of 3 or 4): the Q6_K tile
+// kernel reduces several columns in the Q4_K tile kernel's order, so for
+// these rows its tree is the one-column tree (the reasoning of
+// gemv_q4k_ksplit_short_nc_kernel), and this is the one-column short-team
+// kernel with NC accumulators per lane.  p.ring_off: LDS offset of the wave
+// areas (after the rows x NC x KT partials).
+__host__ __device__ constexpr int q6_ksplit_short_nc_lds_bytes(int rows_per_wg, int nc, int sbw, int kt, int waves) {
+    return ksplit_short_nc_part_bytes(rows_per_wg, nc, kt) + waves * nc * q6_ks_slice_bytes(sbw);
+}
+
+template <int NC, int SBW, int WAVES, int S, int KT, bool SUMS = false>
+__global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_short_nc_kernel(Q4K_GEMV_KERNEL_ARGS) {
+    constexpr int KW = 16 / SBW;
+    constexpr int TR = 16 / SBW;
+    constexpr int TEAMS = WAVES / KT;
+    constexpr int V = 4 * SBW;
+    static_assert(NC >= 2 && NC <= 4 && TEAMS >= 1 && WAVES % KT == 0 && KT < KW, "short teams, 2-4 columns");
+    p = with_head(p, Q4K_GEMV_HEAD_VALUES);
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    float *part = reinterpret_cast<float *>(lds);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slice = wave % KT, team = wave / KT;
+    const int r = lane / (4 * SBW), s = (lane >> 2) & (SBW - 1);
+    const int h = (lane >> 1) & 1, jp = lane & 1;
+
+    const int b = (int)blockIdx.x;
+    const int wg_beg = b * p.rows_base + min(b, p.rows_extra);
+    const int n = p.rows_base + (b < p.rows_extra ? 1 : 0);
+    const int nt = (n + TR - 1) / TR;
+    const int tq = nt / TEAMS, trem = nt - tq * TEAMS;
+    const int tb = team * tq + min(team, trem);
+    const int ntiles = tq + (team < trem ? 1 : 0);
+
+    // 1. the slice of every column, issued first; past the row: zeros
+    float xv[NC][V];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x + (int64_t)c * p.ldx, (uint32_t)p.K * 4u);
+        const uint32_t off = (uint32_t)(((SBW * slice) * kQK + lane * V) * 4);
+#pragma unroll
+        for (int k = 0; k < V / 4; ++k) {
+            const f32x4 a = __builtin_bit_cast(f32x4, load16(rx, off + 16u * k));
+            xv[c][4 * k] = a[0];
+            xv[c][4 * k + 1] = a[1];
+            xv[c][4 * k + 2] = a[2];
+            xv[c][4 * k + 3] = a[3];
+        }
+    }
+
+    // 2. the first S tiles' weights (past the workgroup's rows or the row's
+    //    blocks: zeros)
+    const __amdgpu_buffer_rsrc_t rsw = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
+    Q6Lane ln;
+    ln.lane = lane;
+    ln.g = SBW * slice + s;
+    ln.h = h;
+    ln.jp = jp;
+    const uint32_t blk = (uint32_t)r * (uint32_t)p.row_stride + (uint32_t)ln.g * kQ6Bytes;
+    ln.o_lo = blk + 64u * (uint32_t)h + 16u * (uint32_t)jp;
+    ln.o_hi = blk + 128u + 32u * (uint32_t)h + 16u * (uint32_t)jp;
+    ln.o_sc = blk + 192u + 8u * (uint32_t)h;
+    ln.o_d = blk + 206u;
+    const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
+    auto load_tile = [&](int t, Q6Regs &w) {
+        const bool ok = t < ntiles && ln.g < p.nb;
+        q6_load(rsw, ln, (uint32_t)(tb + t) * tile_bytes, ok, w);
+    };
+    int tk[S];
+    Q6Regs w[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+        tk[k] = k;
+        load_tile(k, w[k]);
+    }
+
+    // 3. quantise every column's slice into the wave's LDS areas
+    uint8_t *area = lds + p.ring_off + wave * NC * q6_ks_slice_bytes(SBW);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) q6_ks_stage_lds<SBW>(xv[c], lane, area + c * q6_ks_slice_bytes(SBW));
+    // lanes read what other lanes of the wave wrote
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // 4. the tiles, S in flight
+    int remaining = ntiles;
+    if (remaining > 0) {
+        for (;;) {
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                uint32_t v[4][4];
+                int sc[4];
+                q6_values(w[k], v);
+                q6_scales(w[k], jp, sc);
+                const float d = half_bits_to_float(w[k].dw >> 16);
+                const int rl = (tb + tk[k]) * TR + r;
+                float acc[NC];
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    acc[c] = 0.0f;
+                    const Q6Act a = q6_ks_read_lds(area + c * q6_ks_slice_bytes(SBW), SBW, s, h, jp);
+                    int gs[4];
+                    q6_accumulate(v, sc, d, a, acc[c], gs);
+                    if constexpr (SUMS) {
+                        if (tk[k] < ntiles && rl < n && ln.g < p.nb) {
+                            int32_t *o =
+                                p.sums + ((int64_t)c * p.M + wg_beg + rl) * (p.K / 16) + ln.g * 16 + 8 * h + jp;
+#pragma unroll
+                            for (int m = 0; m < 4; ++m) o[2 * m] = gs[m];
+                        }
+                    }
+                }
+                const bool wr = ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const float q = ks_reduce<SBW>(acc[c]);
+                    if (wr) part[(rl * NC + c) * KT + slice] = q;
+                }
+                tk[k] += S;
+                load_tile(tk[k], w[k]);
+            }
+            remaining -= S;
+            if (remaining <= 0) break;
+        }
+    }
+    __syncthreads();
+    // 5. each (row, column): the balanced tree over the 16/SBW slice sums
+    //    (+0 for the slices past the team)
+    for (int e = (int)threadIdx.x; e < n * NC; e += kWave * WAVES) {
+        const int row = e / NC, c = e - row * NC;
+        float q[KW];
+#pragma unroll
+        for (int k = 0; k < KW; ++k) q[k] = k < KT ? part[(row * NC + c) * KT + k] : 0.0f;
+#pragma unroll
+        for (int hh = KW / 2; hh >= 1; hh /= 2)
+#pragma unroll
+            for (int t = 0; t < hh; ++t) q[t] = q[2 * t] + q[2 * t + 1];
+        p.dst[(int64_t)c * p.ld_dst + wg_beg + row] = q[0];
+    }
+}
+
 // The long-row variants: those of the Q4_K kernel (SBW 1 or 2 for rows of
 // up to 8 groups, 4 for rows of up to 4; three or four steps in flight in
 // workgroups of up to 8 waves).

@@ -152,3 +152,84 @@ def test_short_nc_not_elsewhere(Q, gpu):
     assert Q.geometry(1024, 3072, 3)["cols_per_launch"] == 1
     assert Q.geometry(2048, 8192, 3)["kernel"] == 1
     assert Q.geometry(768, 20000, 4)["kernel"] == 1
+
+
+Q6 = 14
+Q6_SHAPES = [(1000, 768, 2), (4096, 1024, 2), (300, 1280, 2), (37, 2048, 2), (1030, 2048, 2), (257, 1024, 3),
+             (4096, 768, 4), (5, 1024, 4)]
+
+
+@pytest.mark.parametrize("M,K,N", Q6_SHAPES)
+def test_q6k_short_nc_bits_equal_tile_kernel(Q, O, gpu, M, K, N):
+    """The Q6_K form: every instantiated launch shape at 1, 7 and 300
+    workgroups bit for bit against the Q6_K several-column tile kernel; the
+    tile kernel within the parity tolerance of the oracle."""
+    wq = Q.quantize_rows_q6_K(_common.weights(M, K, 110 + N), nthreads=16)
+    x = _common.activations(N, K, 111 + N)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    try:
+        Q.set_geometry_override(kernel=1)
+        assert Q.geometry(K, M, N, Q6)["cols_per_launch"] == N
+        y_tile = Q.mul_mat_vec_q(wd, K, xd, wtype=Q6).cpu().numpy()
+    finally:
+        release(Q)
+    ref = O.gemv_q6K_q8_1(wq, K, O.quantize_q8_1(x), want_sums=False)
+    _common.assert_within_tolerance(O, y_tile, ref, f"Q6_K tile {M}x{K} N={N}")
+    for tr, waves, slots in variants(N, K):
+        for wgs in (0, 7, 300):
+            try:
+                Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, workgroups=wgs, kernel=5)
+                Q.set_pipeline_override(slots=slots)
+                g = Q.geometry(K, M, N, Q6)  # (the Q6_K query reports rows per step as rows_per_tile)
+                assert g["kernel"] == 5 and g["rows_per_tile"] == tr and g["waves_per_wg"] == waves, g
+                assert g["cols_per_launch"] == N, g
+                y = Q.mul_mat_vec_q(wd, K, xd, wtype=Q6).cpu().numpy()
+            finally:
+                release(Q)
+            if not np.array_equal(y, y_tile):
+                bad = np.argwhere(y != y_tile)
+                raise AssertionError(f"Q6_K {M}x{K} N={N} rows/step {tr} waves {waves} slots {slots} wgs {wgs}: "
+                                     f"{len(bad)} outputs differ from the tile kernel, e.g. (col, row) "
+                                     f"{bad[:5].tolist()}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1000, 1024, 2), (300, 2048, 2), (129, 768, 4)])
+def test_q6k_short_nc_sums_exact(Q, O, gpu, M, K, N):
+    import torch
+    wq = Q.quantize_rows_q6_K(_common.weights(M, K, 120 + N), nthreads=16)
+    x = _common.activations(N, K, 121 + N)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    ref = O.gemv_q6K_q8_1(wq, K, O.quantize_q8_1(x))
+    for tr, waves, slots in variants(N, K):
+        try:
+            Q.set_geometry_override(rows_per_tile=tr, waves_per_wg=waves, kernel=5)
+            Q.set_pipeline_override(slots=slots)
+            assert Q.geometry(K, M, N, Q6)["kernel"] == 5
+            y, sums, _ = Q.mul_mat_vec_q_sums(wd, K, xd, wtype=Q6)
+            y_prod = Q.mul_mat_vec_q(wd, K, xd, wtype=Q6)
+        finally:
+            release(Q)
+        where = f"Q6_K {M}x{K} N={N} rows/step {tr} waves {waves} slots {slots}"
+        assert torch.equal(y, y_prod), where
+        assert np.array_equal(sums.cpu().numpy(), ref["s16"]), f"{where}: group sums differ"
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 2), (8192, 2048, 2), (16384, 768, 2), (4096, 768, 3),
+                                   (8192, 768, 4)])
+def test_q6k_short_nc_automatic_choice(Q, gpu, M, K, N):
+    """Q6_K: the same automatic range; the tile kernel's bits, also on the
+    pre-quantised route."""
+    g = Q.geometry(K, M, N, Q6)
+    assert g["kernel"] == 5 and g["cols_per_launch"] == N, g
+    wq = Q.quantize_rows_q6_K(_common.weights(M, K, 125), nthreads=16)
+    x = _common.activations(N, K, 126)
+    wd, xd = to_dev(wq, gpu), to_dev(x, gpu)
+    y = Q.mul_mat_vec_q(wd, K, xd, wtype=Q6).cpu().numpy()
+    try:
+        Q.set_geometry_override(kernel=1)
+        y_tile = Q.mul_mat_vec_q(wd, K, xd, wtype=Q6).cpu().numpy()
+    finally:
+        release(Q)
+    assert np.array_equal(y, y_tile)
+    q8d = Q.quantize_row_q8_1(xd)
+    assert np.array_equal(Q.op_mul_mat_vec_q(wd, K, q8d, N, wtype=Q6).cpu().numpy(), y)
