@@ -477,7 +477,7 @@ static bool short_nc_ok(int64_t K, int N, int tile_nc) {
 // columns at 2 super-blocks per wave, 4 waves to rho 16, 8 to 24, then two
 // tiles in flight (16 waves at rho 41 to 48); three or four columns at 4 per
 // wave, 4 waves, from rho 13 (below: the column split), two tiles in flight
-// from rho 17.  Up to rho 512 (two columns) or 64 (three or four).  Measured on
+// from rho 17, 8 waves beyond rho 64.  Measured on
 // MI355X, us, before -> after: two columns 512 x 2048 3.09 -> 2.86, 2048 x 2048
 // 4.14 -> 3.05, 1536 x 1536 4.04 -> 3.03, 2048 x 1024 3.59 -> 2.98, 3072 x 1024
 // 4.22 -> 3.05, 4096 x 768 4.38 -> 3.04, 6144 x 2048 5.22 -> 4.09, 8192 x 2048
@@ -489,8 +489,10 @@ static bool short_nc_ok(int64_t K, int N, int tile_nc) {
 // rows per CU: two columns 24576 x 2048 9.57 -> 7.59, 32768 x 2048 11.29 ->
 // 8.89, 65536 x 2048 19.01 -> 15.26, 128256 x 2048 32.49 -> 27.50, 32768 x 768
 // 10.71 -> 5.55; three columns 12288 x 1024 7.83 -> 5.70, 16384 x 768 8.08 ->
-// 5.72; four 12288 x 1024 8.51 -> 6.74, 16384 x 768 9.10 -> 6.80.  Not measured
-// past 501 rows per CU (two columns) or 64 (three or four).
+// 5.72; four 12288 x 1024 8.51 -> 6.74, 16384 x 768 9.10 -> 6.80; 151936 x 1024
+// two columns 35.79 -> 18.36, 65536 x 1024 three 22.05 -> 11.31 and four 25.29
+// -> 13.74 (8 waves beyond rho 64).  Measured up to rho 594; past it the LDS of
+// the partials bounds the rows per workgroup (pick_geometry_short_nc).
 static bool short_nc_auto(int64_t M, int N, int cus, int &rows_per_step, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
@@ -498,12 +500,12 @@ static bool short_nc_auto(int64_t M, int N, int cus, int &rows_per_step, int &wa
         rows_per_step = 8;
         waves = rho <= 16 ? 4 : (rho > 40 && rho <= 48 ? 16 : 8);
         if (rho > 24 && waves == 8) slots = 2;
-        return rho <= 512;
+        return true;
     }
     rows_per_step = 4;
-    waves = 4;
+    waves = rho > 64 ? 8 : 4;
     if (rho > 16) slots = 2;
-    return rho > 12 && rho <= 64;
+    return rho > 12;
 }
 
 // The K-split kernel's automatic launch shape for one aligned F32 column of
@@ -769,7 +771,14 @@ static bool ksplit_nc_auto(int64_t K, int64_t M, int64_t N, int cus, int &tr, in
 bool split_columns(int64_t K, int64_t M, int64_t N, int cus) {
     if (N < 2 || N > Q4K_MAX_BATCH || cus < 1) return false;
     const int64_t rho = (M + cus - 1) / cus;
-    return rho <= (N == 2 ? 8 : 12) && K <= 8 * 4096 && (K >= 4096 || ksplit_short_rows(K));
+    // rows shorter than one group of 5 or more blocks: up to 4 rows per CU
+    // (from 5 the tile kernel measured faster: 2048 x 2048 N=3 4.46 against
+    // 3.91 us, N=4 5.15 / 4.71, 1536 x 1536 N=3 4.37 / 3.89, 2048 x 3584 N=3
+    // 5.79 / 4.44, N=2 4.35 / 4.06, 2048 x 2304 N=2 4.08 / 3.86, Q6_K 2048 x
+    // 2048 N=3 4.81 / 4.26; at up to 4 the split: 512 x 2048 N=4 3.08 / 4.04,
+    // 1024 x 2560 N=4 4.18 / 4.53)
+    const int64_t lim = K < 4096 && K > 1024 ? 4 : (N == 2 ? 8 : 12);
+    return rho <= lim && K <= 8 * 4096 && (K >= 4096 || ksplit_short_rows(K));
 }
 
 // Launch geometry for an (M, K, N) product.

@@ -402,19 +402,21 @@ static bool q6_ksplit_glu_auto(int64_t K, int64_t M, int cus, int &tr, int &wave
 // The several-column short-team kernel's automatic launch shape (aligned F32
 // columns of rows that pick_geometry_q6_short_nc admits), one workgroup per
 // CU; false where the column split or the tile kernel measured faster.  Rows
-// per CU rho: 4 waves, one tile in flight up to rho 16, two beyond; two
-// columns at 2 super-blocks per wave up to rho 512, three or four at 4 from
-// rho 13 (below: the column split) to 64.  Measured on MI355X, us, before ->
-// after: two columns 512 x 2048 3.46 -> 3.22, 2048 x 2048 4.50 -> 3.33,
-// 8192 x 2048 7.37 -> 5.21, 16384 x 768 10.38 -> 4.89, 128256 x 2048 62.59
-// -> 40.44; three columns 4096 x 768 5.07 -> 4.23; four 8192 x 768 7.96 ->
-// 5.74.
+// per CU rho: one tile in flight up to rho 16, two beyond; two columns at 2
+// super-blocks per wave, 4 waves, three or four at 4 per wave from rho 13
+// (below: the column split), 4 waves up to rho 64, 8 beyond.  Measured on
+// MI355X, us, before -> after: two columns 512 x 2048 3.46 -> 3.22, 2048 x
+// 2048 4.50 -> 3.33, 8192 x 2048 7.37 -> 5.21, 16384 x 768 10.38 -> 4.89,
+// 128256 x 2048 62.59 -> 40.44, 151936 x 1024 68.59 -> 25.84; three columns
+// 4096 x 768 5.07 -> 4.23, 151936 x 1024 74.63 -> 28.49; four 8192 x 768 7.96
+// -> 5.74, 151936 x 1024 80.71 -> 33.98.  Measured up to rho 594; past it the
+// LDS of the partials bounds the rows per workgroup.
 static bool q6_short_nc_auto(int64_t M, int N, int cus, int &rows_per_step, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     rows_per_step = N == 2 ? 8 : 4;
-    waves = 4;
+    waves = N > 2 && rho > 64 ? 8 : 4;
     slots = rho > 16 ? 2 : 1;
-    return N == 2 ? rho <= 512 : rho > 12 && rho <= 64;
+    return N == 2 || rho > 12;
 }
 
 static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, int64_t N, int64_t mats = 1,

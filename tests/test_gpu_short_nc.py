@@ -121,11 +121,12 @@ def test_short_nc_sums_exact(Q, O, gpu, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(512, 2048, 2), (3072, 1024, 2), (8192, 2048, 2), (11008, 2048, 2),
-                                   (12288, 768, 2), (16384, 2048, 2), (32768, 768, 2), (4096, 768, 3),
-                                   (16384, 768, 3), (8192, 768, 4), (12288, 1024, 4)])
+                                   (12288, 768, 2), (16384, 2048, 2), (32768, 768, 2), (151936, 1024, 2),
+                                   (4096, 768, 3), (16384, 768, 3), (65536, 1024, 3), (8192, 768, 4),
+                                   (12288, 1024, 4)])
 def test_short_nc_automatic_choice(Q, gpu, M, K, N):
     """Aligned F32 columns of such rows take the kernel by themselves (two
-    columns to 512 rows per CU, three or four from 13 to 64), with the tile
+    columns at any rows per CU, three or four from 13), with the tile
     kernel's bits; the pre-quantised route (tile kernel or column split)
     gives the same bits."""
     g = Q.geometry(K, M, N)
@@ -145,13 +146,16 @@ def test_short_nc_automatic_choice(Q, gpu, M, K, N):
 
 
 def test_short_nc_not_elsewhere(Q, gpu):
-    """Past 512 rows per CU (two columns) or 64 (three or four), at up to 12
-    (three or four: the column split) and over rows of 5 or more blocks with
-    three or four columns the kernel is not chosen."""
-    assert Q.geometry(2048, 140000, 2)["kernel"] == 1
+    """At up to 12 rows per CU with three or four columns (the column split)
+    and over rows of 5 or more blocks with three or four columns the kernel
+    is not chosen; rows of 5 or more blocks keep the column split to 4 rows
+    per CU only."""
     assert Q.geometry(1024, 3072, 3)["cols_per_launch"] == 1
     assert Q.geometry(2048, 8192, 3)["kernel"] == 1
-    assert Q.geometry(768, 20000, 4)["kernel"] == 1
+    assert Q.geometry(2048, 2048, 3)["cols_per_launch"] == 3
+    assert Q.geometry(2048, 1024, 4)["cols_per_launch"] == 1
+    assert Q.geometry(3584, 2048, 2)["cols_per_launch"] == 2
+    assert Q.geometry(3584, 1024, 2)["cols_per_launch"] == 1
 
 
 Q6 = 14
@@ -214,8 +218,8 @@ def test_q6k_short_nc_sums_exact(Q, O, gpu, M, K, N):
         assert np.array_equal(sums.cpu().numpy(), ref["s16"]), f"{where}: group sums differ"
 
 
-@pytest.mark.parametrize("M,K,N", [(512, 2048, 2), (8192, 2048, 2), (16384, 768, 2), (4096, 768, 3),
-                                   (8192, 768, 4)])
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 2), (8192, 2048, 2), (16384, 768, 2), (151936, 1024, 2),
+                                   (4096, 768, 3), (8192, 768, 4), (40000, 1024, 4)])
 def test_q6k_short_nc_automatic_choice(Q, gpu, M, K, N):
     """Q6_K: the same automatic range; the tile kernel's bits, also on the
     pre-quantised route."""
