@@ -205,7 +205,7 @@ struct Geometry {
     int ks_p = 0;       // several-column K-split kernel: columns of its reduction tree (2 or 4)
     int ks_kt = 0;      // long-row K-split kernel, rows shorter than one group: waves per team (0: 16/SBW)
     int colsplit = 0;   // several columns as one launch over one-column channels (the columns; 0: not)
-    int ks_snc = 0;     // several columns of rows shorter than one group in short teams
+    int ks_snc = 0;     // several columns of rows shorter than one group in short teams: the tree's columns (2, 4)
 };
 
 // Tile kernel variants that are instantiated: those whose registers fit the
@@ -439,17 +439,19 @@ static Geometry pick_geometry_short_nc(const DeviceInfo &di, int64_t K, int64_t 
                                        int waves, int wgs, int slots) {
     Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
-    g.ksplit = rows_per_step == 4 || N > 2 ? 4 : 2;
+    const int nb = (int)(K / kQK);
+    const bool rc4 = N > 2 && nb > 4;  // the four-column tree: super-blocks w and w + 4 per wave
+    g.ksplit = rc4 ? 2 : (rows_per_step == 4 || N > 2 ? 4 : 2);
     g.R = 16 / g.ksplit;
-    g.ks_kt = ksplit_short_team((int)(K / kQK), g.ksplit);
+    g.ks_kt = rc4 ? 4 : ksplit_short_team(nb, g.ksplit);
     g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 8;
     g.slots = slots == 1 || slots == 2 ? slots : 1;
-    if (!g.ks_kt || !ksplit_short_nc_exists(N, g.ksplit, g.ks_kt, g.waves, g.slots)) {
+    if (!g.ks_kt || !ksplit_short_nc_exists(N, g.ksplit, g.ks_kt, g.waves, g.slots, rc4 ? 4 : 2)) {
         g.ksplit = 0;
         return g;
     }
     g.ks_long = 1;
-    g.ks_snc = 1;
+    g.ks_snc = rc4 ? 4 : 2;
     int64_t grid = wgs > 0 ? wgs : cus;
     if (grid > M) grid = M;
     g.grid = grid < 1 ? 1 : (int)grid;
@@ -463,12 +465,13 @@ static Geometry pick_geometry_short_nc(const DeviceInfo &di, int64_t K, int64_t 
 }
 
 // Whether N columns of rows of K values can take the several-column
-// short-team kernel: their tile-kernel tree reduces to the one-column tree
-// (rows of 3 to 8 blocks with two columns, 3 or 4 with three or four) and
-// the tile kernel launches all N at once.
+// short-team kernel: rows of 3 to 8 blocks (with two columns, or three or
+// four over 3 or 4 blocks, the tile kernel's tree reduces to the one-column
+// tree; three or four columns over 5 to 8 blocks pair super-blocks w and
+// w + 4 first) and the tile kernel launches all N at once.
 static bool short_nc_ok(int64_t K, int N, int tile_nc) {
     const int64_t nb = K / kQK;
-    return tile_nc == N && K % kQK == 0 && nb >= 3 && nb <= (N == 2 ? 8 : 4) && N >= 2 && N <= 4;
+    return tile_nc == N && K % kQK == 0 && nb >= 3 && nb <= 8 && N >= 2 && N <= 4;
 }
 
 // The several-column short-team kernel's automatic launch shape (aligned F32
@@ -491,11 +494,23 @@ static bool short_nc_ok(int64_t K, int N, int tile_nc) {
 // 10.71 -> 5.55; three columns 12288 x 1024 7.83 -> 5.70, 16384 x 768 8.08 ->
 // 5.72; four 12288 x 1024 8.51 -> 6.74, 16384 x 768 9.10 -> 6.80; 151936 x 1024
 // two columns 35.79 -> 18.36, 65536 x 1024 three 22.05 -> 11.31 and four 25.29
-// -> 13.74 (8 waves beyond rho 64).  Measured up to rho 594; past it the LDS of
-// the partials bounds the rows per workgroup (pick_geometry_short_nc).
-static bool short_nc_auto(int64_t M, int N, int cus, int &rows_per_step, int &waves, int &slots) {
+// -> 13.74 (8 waves beyond rho 64).  Three or four columns of rows of 5 to 8
+// blocks (super-blocks w and w + 4 per wave) from rho 5, 4 waves up to rho 32,
+// 8 beyond, two tiles in flight from rho 9: 2048 x 2048 three 3.93 -> 3.42,
+// four 4.75 -> 4.05, 3072 x 2048 three 4.83 -> 3.93, 8192 x 2048 three 6.48
+// -> 4.97, four 7.52 -> 5.59, 8960 x 1536 three 6.59 -> 5.38, 16384 x 2048
+// four 9.80 -> 7.72, 128256 x 2048 three 41.36 -> 29.06.  Measured up to rho
+// 594; past it the LDS of the partials bounds the rows per workgroup
+// (pick_geometry_short_nc).
+static bool short_nc_auto(int64_t M, int N, int nb, int cus, int &rows_per_step, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
     slots = 1;
+    if (N > 2 && nb > 4) {  // super-blocks w and w + 4 per wave: from 5 rows per CU (below: the column split)
+        rows_per_step = 8;
+        waves = rho > 32 ? 8 : 4;
+        slots = rho > 8 ? 2 : 1;
+        return rho > 4;
+    }
     if (N == 2) {
         rows_per_step = 8;
         waves = rho <= 16 ? 4 : (rho > 40 && rho <= 48 ? 16 : 8);
@@ -811,7 +826,7 @@ static Geometry pick_geometry(const DeviceInfo &di, int64_t K, int64_t M, int64_
     if (!fused && mats == 1 && okern == 0 && orows == 0 && owaves == 0 && owgs == 0 && f32_vec && N >= 2 &&
         N <= 4 && short_nc_ok(K, (int)N, nc)) {
         int tr = 0, w = 0, s = 0;
-        if (short_nc_auto(M, (int)N, cus, tr, w, s)) {
+        if (short_nc_auto(M, (int)N, (int)(K / kQK), cus, tr, w, s)) {
             const Geometry gs = pick_geometry_short_nc(di, K, M, (int)N, tr, w, 0, s);
             if (gs.ksplit) return gs;
         }
@@ -1201,7 +1216,8 @@ static int launch_gemv(DeviceInfo *di, const Geometry &geo, GemvParams p, int nc
         if (!p.x || !p.vec_ok) return Q4K_EINVAL;
         if (nc > 1 && geo.ks_snc) {
             if (nc != geo.nc_chunk) return Q4K_EINVAL;
-            fn = q4k_ksplit_short_nc_kernel(nc, geo.ksplit, geo.ks_kt, geo.waves, geo.slots, p.sums != nullptr);
+            fn = q4k_ksplit_short_nc_kernel(nc, geo.ksplit, geo.ks_kt, geo.waves, geo.slots, p.sums != nullptr,
+                                            geo.ks_snc);
             p.ring_off = ksplit_short_nc_part_bytes(geo.rows_base + (geo.rows_extra ? 1 : 0), nc, geo.ks_kt);
         } else if (nc > 1) {
             if (nc != geo.nc_chunk) return Q4K_EINVAL;

@@ -168,6 +168,17 @@ __device__ __forceinline__ float ks_reduce(float v) {
     return v;
 }
 
+// Two super-blocks per wave that lie 4 apart in the row (residue classes
+// mod 4): the pair first, then the chunks -- the several-column tile
+// kernel's order for a four-column tree (column_sums: g and g^4, then the
+// chunks).  The sum lands in the last lane of each 8-lane row group.
+__device__ __forceinline__ float ks_reduce_rc4(float v) {
+    v += dppf<kDppRor4>(v);
+    v += dppf<kDppXor1>(v);
+    v += dppf<kDppXor2>(v);
+    return v;
+}
+
 template <int SBW>
 __device__ __forceinline__ bool ks_writer(int lane) {
     return (lane & (4 * SBW - 1)) == 4 * SBW - 1;
@@ -386,10 +397,11 @@ __host__ __device__ constexpr int ks_slice_bytes(int sbw) { return 320 * sbw; }
 
 // The wave's slice of one group, quantised (lane L: values [L*V, +V)), into
 // its LDS area; sq (parity variants) gets the int32 sums of the blocks that
-// lie inside the row (blk0: the slice's first block in the row).
+// lie inside the row (blk0: the slice's first block in the row; blk_hi, two
+// super-blocks per wave: how many blocks further on the second one lies).
 template <int SBW>
 __device__ __forceinline__ void ks_stage_lds(const float (&v)[4 * SBW], int lane, uint8_t *area, int32_t *sq,
-                                             int blk0, int nblk) {
+                                             int blk0, int nblk, int blk_hi = 0) {
     constexpr int V = 4 * SBW;
     constexpr int LPB = 32 / V;
     uint32_t word[V / 4];
@@ -402,7 +414,8 @@ __device__ __forceinline__ void ks_stage_lds(const float (&v)[4 * SBW], int lane
     if ((lane & (LPB - 1)) == 0) {
         const int b = lane / LPB;
         reinterpret_cast<float2 *>(area + 256 * SBW)[b] = make_float2(d8, d8 * (float)qs);
-        if (sq && blk0 + b < nblk) sq[blk0 + b] = qs;
+        const int bi = blk0 + b + (b >> 3) * blk_hi;  // (blk_hi: the second super-block's blocks moved)
+        if (sq && bi < nblk) sq[bi] = qs;
     }
 }
 
@@ -631,13 +644,15 @@ __host__ __device__ constexpr int ksplit_short_nc_lds_bytes(int rows_per_wg, int
 // workgroup (whole teams of KT), S: row tiles in flight per wave.  SUMS: the
 // parity variant (every lane's int32 sub-block sums and the activation's
 // block sums, per column).  p.ring_off: LDS offset of the wave areas.
-template <int NC, int SBW, int WAVES, int S, int KT, bool SUMS = false>
+template <int NC, int SBW, int WAVES, int S, int KT, bool SUMS = false, int P = 2>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_short_nc_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
     constexpr int TR = 16 / SBW;
     constexpr int TEAMS = WAVES / KT;
     constexpr int V = 4 * SBW;
+    constexpr bool RC4 = P == 4;  // wave w: super-blocks w and w + 4
     static_assert(NC >= 2 && NC <= 4 && TEAMS >= 1 && WAVES % KT == 0 && KT < KW, "short teams, 2-4 columns");
+    static_assert(!RC4 || (SBW == 2 && KT == 4 && NC >= 3), "residue classes mod 4: rows of 5 to 8 blocks");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
@@ -660,7 +675,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_short_nc_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x + (int64_t)c * p.ldx, (uint32_t)p.K * 4u);
-        const uint32_t off = (uint32_t)(((SBW * slice) * kQK + lane * V) * 4);
+        const uint32_t off = RC4 ? (uint32_t)(((slice + 4 * (lane >> 5)) * kQK + (lane & 31) * V) * 4)
+                                 : (uint32_t)(((SBW * slice) * kQK + lane * V) * 4);
 #pragma unroll
         for (int k = 0; k < V / 4; ++k) {
             // the whole vector is cast (see the one-column long-row kernel)
@@ -674,7 +690,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_short_nc_kernel(
 
     // 2. the first S tiles' weights (rows past the workgroup's share: zeros)
     const __amdgpu_buffer_rsrc_t rsw = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
-    const int kb0 = SBW * slice + s;  // the lane's super-block
+    const int kb0 = RC4 ? slice + 4 * s : SBW * slice + s;  // the lane's super-block
     const uint32_t lh = (uint32_t)r * (uint32_t)p.row_stride + (uint32_t)(kb0 * kBlockBytes);
     const uint32_t lq = lh + 16u + 32u * (uint32_t)j;
     const uint32_t tile_bytes = (uint32_t)TR * (uint32_t)p.row_stride;
@@ -700,7 +716,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_short_nc_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c)
         ks_stage_lds<SBW>(xv[c], lane, area + c * ks_slice_bytes(SBW),
-                          SUMS ? p.sq + (int64_t)c * (p.K / 32) : nullptr, SBW * slice * 8, p.K / 32);
+                          SUMS ? p.sq + (int64_t)c * (p.K / 32) : nullptr, (RC4 ? slice : SBW * slice) * 8,
+                          p.K / 32, RC4 ? 24 : 0);
     // lanes read what other lanes of the wave wrote
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -737,7 +754,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_short_nc_kernel(
                 const bool wr = ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n;
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
-                    const float q = ks_reduce<SBW>(acc[c]);
+                    const float q = RC4 ? ks_reduce_rc4(acc[c]) : ks_reduce<SBW>(acc[c]);
                     if (wr) part[(rl * NC + c) * KT + slice] = q;
                 }
                 tk[k] += S;
@@ -768,9 +785,10 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q4k_ksplit_short_nc_kernel(
 // of 3 or 4 (teams of 2 or 1), three or four columns at 4 per wave for rows
 // of 3 or 4 blocks (teams of 1); 4, 8 or 16 waves; one or two tiles in
 // flight.
-constexpr bool ksplit_short_nc_exists(int nc, int sbw, int kt, int waves, int slots) {
-    const bool shape = nc == 2 ? ((sbw == 2 && (kt == 2 || kt == 4)) || (sbw == 4 && (kt == 1 || kt == 2)))
-                               : ((nc == 3 || nc == 4) && sbw == 4 && kt == 1);
+constexpr bool ksplit_short_nc_exists(int nc, int sbw, int kt, int waves, int slots, int p = 2) {
+    const bool shape = p == 4 ? (nc == 3 || nc == 4) && sbw == 2 && kt == 4
+                       : nc == 2 ? ((sbw == 2 && (kt == 2 || kt == 4)) || (sbw == 4 && (kt == 1 || kt == 2)))
+                                 : ((nc == 3 || nc == 4) && sbw == 4 && kt == 1);
     return shape && (waves == 4 || waves == 8 || waves == 16) && waves % kt == 0 && (slots == 1 || slots == 2);
 }
 

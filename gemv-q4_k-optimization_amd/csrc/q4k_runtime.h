@@ -97,8 +97,10 @@ const void *q6k_sums_kernel(int nc, int waves, int pro, int slots, bool dense);
 const void *q4k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch);
 const void *q6k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch);
 // The several-column short-team kernels (q4k_short.hip, q6k_short.hip), or null.
-const void *q4k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums);
-const void *q6k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums);
+// (p: columns of the tile kernel's reduction tree, 2, or 4 for rows of 5 to 8
+// blocks in three or four columns: super-blocks w and w + 4 per wave)
+const void *q4k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums, int p = 2);
+const void *q6k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums, int p = 2);
 
 // Q6_K weight checks and launch (q6k_gemv.hip), for the type-dispatching
 // entry points of q4k_gemv.hip.

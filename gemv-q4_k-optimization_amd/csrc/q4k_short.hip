@@ -86,19 +86,23 @@ const void *short_kernel(int sbw, int kt, int waves, int slots, bool sums, int e
 }  // namespace
 
 namespace {
-template <bool Q6, int NC, int SBW, int KT>
+template <bool Q6, int NC, int SBW, int KT, int P = 2>
 const void *short_nc_sym(int waves, int slots, bool sums) {
     auto by_s = [&](auto w_c) -> const void * {
         constexpr int W = decltype(w_c)::value;
         auto pick = [&](auto s_c) -> const void * {
             constexpr int S = decltype(s_c)::value;
-            if constexpr (ksplit_short_nc_exists(NC, SBW, KT, W, S)) {
+            if constexpr (ksplit_short_nc_exists(NC, SBW, KT, W, S, P)) {
                 if constexpr (Q6)
-                    return sums ? reinterpret_cast<const void *>(&gemv_q6k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, true>)
-                                : reinterpret_cast<const void *>(&gemv_q6k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, false>);
+                    return sums ? reinterpret_cast<const void *>(
+                                      &gemv_q6k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, true, P>)
+                                : reinterpret_cast<const void *>(
+                                      &gemv_q6k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, false, P>);
                 else
-                    return sums ? reinterpret_cast<const void *>(&gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, true>)
-                                : reinterpret_cast<const void *>(&gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, false>);
+                    return sums ? reinterpret_cast<const void *>(
+                                      &gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, true, P>)
+                                : reinterpret_cast<const void *>(
+                                      &gemv_q4k_ksplit_short_nc_kernel<NC, SBW, W, S, KT, false, P>);
             }
             return nullptr;
         };
@@ -113,7 +117,12 @@ const void *short_nc_sym(int waves, int slots, bool sums) {
 }
 
 template <bool Q6>
-const void *short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums) {
+const void *short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums, int p) {
+    if (p == 4) {  // residue classes mod 4 (three or four columns of rows of 5 to 8 blocks)
+        if (nc == 3 && sbw == 2 && kt == 4) return short_nc_sym<Q6, 3, 2, 4, 4>(waves, slots, sums);
+        if (nc == 4 && sbw == 2 && kt == 4) return short_nc_sym<Q6, 4, 2, 4, 4>(waves, slots, sums);
+        return nullptr;
+    }
     if (nc == 2 && sbw == 2 && kt == 2) return short_nc_sym<Q6, 2, 2, 2>(waves, slots, sums);
     if (nc == 2 && sbw == 2 && kt == 4) return short_nc_sym<Q6, 2, 2, 4>(waves, slots, sums);
     if (nc == 2 && sbw == 4 && kt == 1) return short_nc_sym<Q6, 2, 4, 1>(waves, slots, sums);
@@ -128,15 +137,15 @@ const void *short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool 
 const void *q4k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
     return short_kernel<false>(sbw, kt, waves, slots, sums, epi, batch);
 }
-const void *q4k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums) {
-    return short_nc_kernel<false>(nc, sbw, kt, waves, slots, sums);
+const void *q4k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums, int p) {
+    return short_nc_kernel<false>(nc, sbw, kt, waves, slots, sums, p);
 }
 #else
 const void *q6k_ksplit_short_kernel(int sbw, int kt, int waves, int slots, bool sums, int epi, bool batch) {
     return short_kernel<true>(sbw, kt, waves, slots, sums, epi, batch);
 }
-const void *q6k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums) {
-    return short_nc_kernel<true>(nc, sbw, kt, waves, slots, sums);
+const void *q6k_ksplit_short_nc_kernel(int nc, int sbw, int kt, int waves, int slots, bool sums, int p) {
+    return short_nc_kernel<true>(nc, sbw, kt, waves, slots, sums, p);
 }
 #endif
 

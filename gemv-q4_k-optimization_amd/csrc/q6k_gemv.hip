@@ -101,7 +101,8 @@ struct Q6Geometry {
     int ks_nc_p = 0; // several-column K-split kernel: columns of its reduction tree (2 or 4; 0: not it)
     int ks_kt = 0;   // long-row K-split kernel, rows shorter than one group: waves per team (0: 16/SBW)
     int colsplit = 0; // several columns as one launch over one-column channels (the columns; 0: not)
-    int ks_snc = 0;   // several columns of rows shorter than one group in short teams
+    int ks_snc = 0;   // several columns of rows shorter than one group in short teams: waves per team
+    int ks_snc_p = 2; // (and the tile kernel's tree columns, 2 or 4)
 };
 
 // Columns per launch of the tile kernel for N columns of K values (halved
@@ -153,20 +154,22 @@ static Q6Geometry pick_geometry_q6_ksplit_nc(const DeviceInfo &di, int64_t K, in
 // for N columns of rows of K values: rows_per_step 8 or 4 (2 or 4
 // super-blocks per wave; three or four columns: 4), waves, workgroups
 // (default one per CU), tiles in flight; ksplit = 0 where the rows do not
-// qualify (3 to 8 blocks with two columns, 3 or 4 with three or four), the
-// variant is not instantiated or its LDS does not fit.
+// qualify (3 to 8 blocks), the variant is not instantiated or its LDS does
+// not fit.
 static Q6Geometry pick_geometry_q6_short_nc(const DeviceInfo &di, int64_t K, int64_t M, int N, int rows_per_step,
                                             int waves, int wgs, int slots) {
     Q6Geometry g;
     const int cus = di.cus > 0 ? di.cus : 1;
     const int64_t nb = K / kQK;
-    if (K % kQK || nb < 3 || nb > (N == 2 ? 8 : 4) || N < 2 || N > 4) return g;
-    g.ksplit = rows_per_step == 4 || N > 2 ? 4 : 2;
+    if (K % kQK || nb < 3 || nb > 8 || N < 2 || N > 4) return g;
+    const bool rc4 = N > 2 && nb > 4;  // the four-column tree: super-blocks w and w + 4 per wave
+    g.ksplit = rc4 ? 2 : (rows_per_step == 4 || N > 2 ? 4 : 2);
     g.ks_tr = 16 / g.ksplit;
-    g.ks_snc = ksplit_short_team((int)nb, g.ksplit);
+    g.ks_snc = rc4 ? 4 : ksplit_short_team((int)nb, g.ksplit);
+    g.ks_snc_p = rc4 ? 4 : 2;
     g.waves = waves == 4 || waves == 8 || waves == 16 ? waves : 8;
     g.slots = slots == 1 || slots == 2 ? slots : 1;
-    if (!g.ks_snc || !ksplit_short_nc_exists(N, g.ksplit, g.ks_snc, g.waves, g.slots)) {
+    if (!g.ks_snc || !ksplit_short_nc_exists(N, g.ksplit, g.ks_snc, g.waves, g.slots, g.ks_snc_p)) {
         g.ksplit = 0;
         return g;
     }
@@ -411,8 +414,15 @@ static bool q6_ksplit_glu_auto(int64_t K, int64_t M, int cus, int &tr, int &wave
 // 4096 x 768 5.07 -> 4.23, 151936 x 1024 74.63 -> 28.49; four 8192 x 768 7.96
 // -> 5.74, 151936 x 1024 80.71 -> 33.98.  Measured up to rho 594; past it the
 // LDS of the partials bounds the rows per workgroup.
-static bool q6_short_nc_auto(int64_t M, int N, int cus, int &rows_per_step, int &waves, int &slots) {
+static bool q6_short_nc_auto(int64_t M, int N, int nb, int cus, int &rows_per_step, int &waves, int &slots) {
     const int64_t rho = (M + cus - 1) / cus;
+    if (N > 2 && nb > 4) {  // super-blocks w and w + 4 per wave (the Q4_K rule): 2048 x 1536 three 4.20 ->
+                            // 3.61 us, 8192 x 2048 four 8.75 -> 6.98, 128256 x 2048 four 73.16 -> 46.76
+        rows_per_step = 8;
+        waves = rho > 32 ? 8 : 4;
+        slots = rho > 8 ? 2 : 1;
+        return rho > 4;
+    }
     rows_per_step = N == 2 ? 8 : 4;
     waves = N > 2 && rho > 64 ? 8 : 4;
     slots = rho > 16 ? 2 : 1;
@@ -432,7 +442,7 @@ static Q6Geometry pick_geometry_q6(const DeviceInfo &di, int64_t K, int64_t M, i
         g_ovr_wgs.load() == 0 && f32_vec && N >= 2 && N <= 4) {
         bool dense = false;
         int tr = 0, w = 0, sl = 0;
-        if (q6_tile_chunk(K, N, max_lds, dense) == N && !dense && q6_short_nc_auto(M, (int)N, cus, tr, w, sl)) {
+        if (q6_tile_chunk(K, N, max_lds, dense) == N && !dense && q6_short_nc_auto(M, (int)N, (int)(K / kQK), cus, tr, w, sl)) {
             const Q6Geometry gs = pick_geometry_q6_short_nc(di, K, M, (int)N, tr, w, 0, sl);
             if (gs.ksplit) return gs;
         }
@@ -756,7 +766,7 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
             p.glu_op = ep->glu_op;
         }
         const int epi = fused == kFusedGate ? kEpiGlu : (fused == kFusedBias ? kEpiBias : kEpiNone);
-        const void *fn = geo.ks_snc ? q6k_ksplit_short_nc_kernel(nc, geo.ksplit, geo.ks_snc, geo.waves, geo.slots, false)
+        const void *fn = geo.ks_snc ? q6k_ksplit_short_nc_kernel(nc, geo.ksplit, geo.ks_snc, geo.waves, geo.slots, false, geo.ks_snc_p)
                          : geo.ks_nc_p  ? q6_ksplit_nc_kernel<false>(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
                          : geo.ks_kt
                              ? q6k_ksplit_short_kernel(geo.ksplit, geo.ks_kt, geo.waves, geo.slots, false, epi, bl != nullptr)
@@ -790,7 +800,7 @@ int run_gemv_q6(const void *src0, int64_t ne00, int64_t ne01, int64_t nb01, cons
         }
         if (so) {  // parity variant: this chunk's columns of the group sums
             if (fused || bl) return Q4K_EINVAL;
-            fn = geo.ks_snc ? q6k_ksplit_short_nc_kernel(nc, geo.ksplit, geo.ks_snc, geo.waves, geo.slots, true)
+            fn = geo.ks_snc ? q6k_ksplit_short_nc_kernel(nc, geo.ksplit, geo.ks_snc, geo.waves, geo.slots, true, geo.ks_snc_p)
                  : geo.ks_nc_p  ? q6k_ksplit_nc_sums_kernel(nc, geo.ks_nc_p, geo.ksplit, geo.waves, geo.slots)
                  : geo.ks_kt    ? q6k_ksplit_short_kernel(geo.ksplit, geo.ks_kt, geo.waves, geo.slots, true, kEpiNone, false)
                  : geo.ks_long  ? q6k_ksplit_long_sums_kernel(geo.ksplit, geo.waves, geo.slots, p.G)

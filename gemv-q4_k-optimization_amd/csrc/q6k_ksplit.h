@@ -461,13 +461,15 @@ __host__ __device__ constexpr int q6_ksplit_short_nc_lds_bytes(int rows_per_wg, 
     return ksplit_short_nc_part_bytes(rows_per_wg, nc, kt) + waves * nc * q6_ks_slice_bytes(sbw);
 }
 
-template <int NC, int SBW, int WAVES, int S, int KT, bool SUMS = false>
+template <int NC, int SBW, int WAVES, int S, int KT, bool SUMS = false, int P = 2>
 __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_short_nc_kernel(Q4K_GEMV_KERNEL_ARGS) {
     constexpr int KW = 16 / SBW;
     constexpr int TR = 16 / SBW;
     constexpr int TEAMS = WAVES / KT;
     constexpr int V = 4 * SBW;
+    constexpr bool RC4 = P == 4;  // wave w: super-blocks w and w + 4 (gemv_q4k_ksplit_short_nc_kernel)
     static_assert(NC >= 2 && NC <= 4 && TEAMS >= 1 && WAVES % KT == 0 && KT < KW, "short teams, 2-4 columns");
+    static_assert(!RC4 || (SBW == 2 && KT == 4 && NC >= 3), "residue classes mod 4: rows of 5 to 8 blocks");
     p = with_head(p, Q4K_GEMV_HEAD_VALUES);
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     float *part = reinterpret_cast<float *>(lds);
@@ -491,7 +493,8 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_short_nc_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x + (int64_t)c * p.ldx, (uint32_t)p.K * 4u);
-        const uint32_t off = (uint32_t)(((SBW * slice) * kQK + lane * V) * 4);
+        const uint32_t off = RC4 ? (uint32_t)(((slice + 4 * (lane >> 5)) * kQK + (lane & 31) * V) * 4)
+                                 : (uint32_t)(((SBW * slice) * kQK + lane * V) * 4);
 #pragma unroll
         for (int k = 0; k < V / 4; ++k) {
             const f32x4 a = __builtin_bit_cast(f32x4, load16(rx, off + 16u * k));
@@ -507,7 +510,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_short_nc_kernel(
     const __amdgpu_buffer_rsrc_t rsw = make_rsrc(p.w + (int64_t)wg_beg * p.row_stride, (uint32_t)(n * p.row_stride));
     Q6Lane ln;
     ln.lane = lane;
-    ln.g = SBW * slice + s;
+    ln.g = RC4 ? slice + 4 * s : SBW * slice + s;
     ln.h = h;
     ln.jp = jp;
     const uint32_t blk = (uint32_t)r * (uint32_t)p.row_stride + (uint32_t)ln.g * kQ6Bytes;
@@ -568,7 +571,7 @@ __global__ __launch_bounds__(kWave *WAVES) void gemv_q6k_ksplit_short_nc_kernel(
                 const bool wr = ks_writer<SBW>(lane) && tk[k] < ntiles && rl < n;
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
-                    const float q = ks_reduce<SBW>(acc[c]);
+                    const float q = RC4 ? ks_reduce_rc4(acc[c]) : ks_reduce<SBW>(acc[c]);
                     if (wr) part[(rl * NC + c) * KT + slice] = q;
                 }
                 tk[k] += S;

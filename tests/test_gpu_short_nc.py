@@ -1,6 +1,8 @@
-"""GPU parity of the several-column short-team kernel: two columns of rows of
-3 to 8 super-blocks, three or four columns of rows of 3 or 4 (768 .. 2048
-values), one team of as few waves as the row needs per row tile.
+"""GPU parity of the several-column short-team kernel: two to four columns of
+rows of 3 to 8 super-blocks (768 .. 2048 values), one team of as few waves as
+the row needs per row tile (three or four columns over 5 to 8 blocks: four
+waves, each with super-blocks w and w + 4, the tile kernel's four-column
+tree).
 
 Bar: every instantiated launch shape (super-blocks per wave, waves, tiles in
 flight) at one workgroup per CU, 7 and 300 workgroups, bit for bit against
@@ -40,6 +42,8 @@ def nc_exists(nc, sbw, kt, waves, slots):
 
 def variants(nc, K):
     nb = K // 256
+    if nc > 2 and nb > 4:  # super-blocks w and w + 4 per wave, teams of 4
+        return [(8, w, s) for w in (4, 8, 16) for s in (1, 2)]
     out = []
     for tr in (8, 4):
         sbw = 16 // tr
@@ -69,7 +73,8 @@ def release(Q):
 
 
 SHAPES = [(1000, 768, 2), (4096, 1024, 2), (300, 1280, 2), (2048, 1536, 2), (37, 1792, 2), (5, 2048, 2),
-          (1030, 2048, 2), (1000, 768, 3), (257, 1024, 3), (4096, 768, 4), (129, 1024, 4), (3, 1024, 4)]
+          (1030, 2048, 2), (1000, 768, 3), (257, 1024, 3), (4096, 768, 4), (129, 1024, 4), (3, 1024, 4),
+          (1000, 1280, 3), (300, 1536, 3), (4096, 1792, 3), (2048, 2048, 4), (37, 2048, 4), (1030, 2048, 3)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
@@ -100,7 +105,8 @@ def test_short_nc_bits_equal_tile_kernel(Q, O, gpu, M, K, N):
                                      f"{bad[:5].tolist()}")
 
 
-@pytest.mark.parametrize("M,K,N", [(1000, 1024, 2), (300, 2048, 2), (257, 768, 3), (129, 1024, 4)])
+@pytest.mark.parametrize("M,K,N", [(1000, 1024, 2), (300, 2048, 2), (257, 768, 3), (129, 1024, 4), (300, 2048, 3),
+                                   (129, 1536, 4)])
 def test_short_nc_sums_exact(Q, O, gpu, M, K, N):
     import torch
     wq = Q.quantize_rows_q4_K(_common.weights(M, K, 90 + N), nthreads=16)
@@ -123,7 +129,7 @@ def test_short_nc_sums_exact(Q, O, gpu, M, K, N):
 @pytest.mark.parametrize("M,K,N", [(512, 2048, 2), (3072, 1024, 2), (8192, 2048, 2), (11008, 2048, 2),
                                    (12288, 768, 2), (16384, 2048, 2), (32768, 768, 2), (151936, 1024, 2),
                                    (4096, 768, 3), (16384, 768, 3), (65536, 1024, 3), (8192, 768, 4),
-                                   (12288, 1024, 4)])
+                                   (12288, 1024, 4), (2048, 2048, 3), (8192, 2048, 4), (8960, 1536, 3)])
 def test_short_nc_automatic_choice(Q, gpu, M, K, N):
     """Aligned F32 columns of such rows take the kernel by themselves (two
     columns at any rows per CU, three or four from 13), with the tile
@@ -146,13 +152,12 @@ def test_short_nc_automatic_choice(Q, gpu, M, K, N):
 
 
 def test_short_nc_not_elsewhere(Q, gpu):
-    """At up to 12 rows per CU with three or four columns (the column split)
-    and over rows of 5 or more blocks with three or four columns the kernel
-    is not chosen; rows of 5 or more blocks keep the column split to 4 rows
-    per CU only."""
+    """At up to 12 rows per CU with three or four columns of rows of 3 or 4
+    blocks, at up to 4 over 5 to 8 (the column split) and over rows of 9 or
+    more blocks the kernel is not chosen; rows of 9 or more blocks keep the
+    column split to 4 rows per CU only."""
     assert Q.geometry(1024, 3072, 3)["cols_per_launch"] == 1
-    assert Q.geometry(2048, 8192, 3)["kernel"] == 1
-    assert Q.geometry(2048, 2048, 3)["cols_per_launch"] == 3
+    assert Q.geometry(2304, 8192, 3)["kernel"] == 1
     assert Q.geometry(2048, 1024, 4)["cols_per_launch"] == 1
     assert Q.geometry(3584, 2048, 2)["cols_per_launch"] == 2
     assert Q.geometry(3584, 1024, 2)["cols_per_launch"] == 1
@@ -160,7 +165,7 @@ def test_short_nc_not_elsewhere(Q, gpu):
 
 Q6 = 14
 Q6_SHAPES = [(1000, 768, 2), (4096, 1024, 2), (300, 1280, 2), (37, 2048, 2), (1030, 2048, 2), (257, 1024, 3),
-             (4096, 768, 4), (5, 1024, 4)]
+             (4096, 768, 4), (5, 1024, 4), (1000, 2048, 3), (257, 1280, 4)]
 
 
 @pytest.mark.parametrize("M,K,N", Q6_SHAPES)
@@ -197,7 +202,7 @@ def test_q6k_short_nc_bits_equal_tile_kernel(Q, O, gpu, M, K, N):
                                      f"{bad[:5].tolist()}")
 
 
-@pytest.mark.parametrize("M,K,N", [(1000, 1024, 2), (300, 2048, 2), (129, 768, 4)])
+@pytest.mark.parametrize("M,K,N", [(1000, 1024, 2), (300, 2048, 2), (129, 768, 4), (300, 2048, 4)])
 def test_q6k_short_nc_sums_exact(Q, O, gpu, M, K, N):
     import torch
     wq = Q.quantize_rows_q6_K(_common.weights(M, K, 120 + N), nthreads=16)
@@ -219,7 +224,8 @@ def test_q6k_short_nc_sums_exact(Q, O, gpu, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N", [(512, 2048, 2), (8192, 2048, 2), (16384, 768, 2), (151936, 1024, 2),
-                                   (4096, 768, 3), (8192, 768, 4), (40000, 1024, 4)])
+                                   (4096, 768, 3), (8192, 768, 4), (40000, 1024, 4), (2048, 1536, 3),
+                                   (8192, 2048, 4)])
 def test_q6k_short_nc_automatic_choice(Q, gpu, M, K, N):
     """Q6_K: the same automatic range; the tile kernel's bits, also on the
     pre-quantised route."""
